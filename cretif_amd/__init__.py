@@ -1,0 +1,213 @@
+"""cretif_amd -- MI355X (gfx950) fused dequant+matmul over GGUF block layouts.
+
+Python mirror of the reference's operator interface for this path.  Every
+function takes the reference's arguments in the reference's order
+(ref:include/cuinfer/kernels/matmul_quant.h:37-105,
+ref:include/cuinfer/quantization.h:145-174, ref:include/cuinfer/embedding.h:136,
+ref:include/cuinfer/attention.h:79-82) and calls the C ABI of libcretif.so
+(include/cri.h) directly.  Buffers are device tensors (torch, on the GPU) or
+raw device addresses (int); nothing is copied or allocated here.  Failures
+raise CretifError, as the reference's C++ entry points throw
+std::runtime_error.
+
+There is no CPU fallback: if libcretif.so is missing or no GPU is present,
+the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+__all__ = [
+    "CretifError",
+    "lib",
+    "library_path",
+    "matmul",
+    "matmul_q8_0",
+    "matmul_q4_0",
+    "matmul_q5_0",
+    "matmul_q4_k",
+    "matmul_q6_k",
+    "matmul_fp16",
+    "dequantize",
+    "dequantize_q8_0",
+    "dequantize_q4_0",
+    "dequantize_q5_0",
+    "dequantize_q6_k",
+    "dequantize_q4_k",
+    "matmul_transposed_b",
+    "batched_matmul_gqa",
+    "FORMAT_IDS",
+    "ABI_SYMBOLS",
+]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+library_path = os.path.join(_HERE, "libcretif.so")
+
+FORMAT_IDS = {"q8_0": 0, "q4_0": 1, "q5_0": 2, "q4_k": 3, "q6_k": 4, "fp16": 5}
+STATUS_NAMES = {
+    0: "CRI_OK",
+    -1: "CRI_ERR_INVALID_ARGUMENT",
+    -2: "CRI_ERR_SHAPE",
+    -3: "CRI_ERR_ALIGNMENT",
+    -4: "CRI_ERR_LAUNCH",
+    -5: "CRI_ERR_UNSUPPORTED",
+}
+
+_MATMUL = ["cri_matmul_" + f for f in ("q8_0", "q4_0", "q5_0", "q4_k", "q6_k", "fp16")]
+_DEQUANT = ["cri_dequantize_" + f for f in ("q8_0", "q4_0", "q5_0", "q6_k", "q4_k")]
+ABI_SYMBOLS = (
+    _MATMUL
+    + ["cri_matmul"]
+    + _DEQUANT
+    + [
+        "cri_matmul_transposed_b",
+        "cri_batched_matmul_gqa",
+        "cri_last_error_string",
+        "cri_block_bytes",
+        "cri_block_elems",
+        "cri_version",
+    ]
+)
+
+
+class CretifError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__("%s (%d): %s" % (STATUS_NAMES.get(status, "?"), status, message))
+        self.status = status
+
+
+_lib = None
+
+
+def lib():
+    """Load libcretif.so (after torch, so both share torch's HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(library_path):
+        raise RuntimeError("libcretif.so is not built; run `python -m cretif_amd.build` (or __graft_entry__.build())")
+    try:
+        import torch  # noqa: F401  -- load torch's libamdhip64 first so there is one HIP runtime
+    except ImportError:
+        pass
+    L = ctypes.CDLL(library_path)
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+    for name in _MATMUL:
+        f = getattr(L, name)
+        f.argtypes = [vp, vp, vp, i32, i32, i32, vp]
+        f.restype = i32
+    L.cri_matmul.argtypes = [i32, vp, vp, vp, i32, i32, i32, vp]
+    L.cri_matmul.restype = i32
+    for name in _DEQUANT:
+        f = getattr(L, name)
+        f.argtypes = [vp, vp, i32, vp]
+        f.restype = i32
+    L.cri_matmul_transposed_b.argtypes = [vp, vp, vp, i32, i32, i32, vp]
+    L.cri_matmul_transposed_b.restype = i32
+    L.cri_batched_matmul_gqa.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
+    L.cri_batched_matmul_gqa.restype = i32
+    L.cri_last_error_string.argtypes = []
+    L.cri_last_error_string.restype = ctypes.c_char_p
+    L.cri_block_bytes.argtypes = [i32]
+    L.cri_block_bytes.restype = i32
+    L.cri_block_elems.argtypes = [i32]
+    L.cri_block_elems.restype = i32
+    L.cri_version.restype = i32
+    _lib = L
+    return L
+
+
+def _ptr(t):
+    """Device address of a torch tensor (must live on the GPU) or a raw int."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    dev = getattr(t, "device", None)
+    if dev is None:
+        raise TypeError("expected a device tensor or an int address, got %r" % type(t))
+    if dev.type != "cuda":
+        raise ValueError("buffer is on %s; the HIP kernels need device (cuda) tensors" % dev)
+    if not t.is_contiguous():
+        raise ValueError("buffer must be contiguous")
+    return t.data_ptr()
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream  # torch.cuda.Stream
+
+
+def _check(status: int):
+    if status != 0:
+        msg = lib().cri_last_error_string().decode("utf-8", "replace")
+        raise CretifError(status, msg)
+
+
+def _mm(name):
+    def fn(A, B, C, M, N, K, stream=None):
+        _check(getattr(lib(), "cri_" + name)(_ptr(A), _ptr(B), _ptr(C), M, N, K, _stream(stream)))
+
+    fn.__name__ = name
+    fn.__doc__ = "C[M,N] = A[M,K] * dequant(B[N,K])^T (replaces cuinfer::%s)." % name
+    return fn
+
+
+matmul_q8_0 = _mm("matmul_q8_0")
+matmul_q4_0 = _mm("matmul_q4_0")
+matmul_q5_0 = _mm("matmul_q5_0")
+matmul_q4_k = _mm("matmul_q4_k")
+matmul_q6_k = _mm("matmul_q6_k")
+matmul_fp16 = _mm("matmul_fp16")
+
+
+def matmul(fmt, A, B, C, M, N, K, stream=None):
+    """Format-switched fused matmul (the switch of matmul_dispatch, ref:src/model.cu:797-825)."""
+    fid = FORMAT_IDS[fmt] if isinstance(fmt, str) else int(fmt)
+    _check(lib().cri_matmul(fid, _ptr(A), _ptr(B), _ptr(C), M, N, K, _stream(stream)))
+
+
+def _dq(name):
+    def fn(src, dst, n_blocks, stream=None):
+        _check(getattr(lib(), "cri_" + name)(_ptr(src), _ptr(dst), n_blocks, _stream(stream)))
+
+    fn.__name__ = name
+    fn.__doc__ = "dst[n_blocks * block] = dequant(src) (replaces cuinfer::%s)." % name
+    return fn
+
+
+dequantize_q8_0 = _dq("dequantize_q8_0")
+dequantize_q4_0 = _dq("dequantize_q4_0")
+dequantize_q5_0 = _dq("dequantize_q5_0")
+dequantize_q6_k = _dq("dequantize_q6_k")
+dequantize_q4_k = _dq("dequantize_q4_k")
+
+
+def dequantize(fmt, src, dst, n_blocks, stream=None):
+    {
+        "q8_0": dequantize_q8_0,
+        "q4_0": dequantize_q4_0,
+        "q5_0": dequantize_q5_0,
+        "q6_k": dequantize_q6_k,
+        "q4_k": dequantize_q4_k,
+    }[fmt](src, dst, n_blocks, stream)
+
+
+def matmul_transposed_b(A, B, C, M, N, K, stream=None):
+    """C[M,N] = A[M,K] * B[N,K]^T, fp32 (replaces cuinfer::matmul_transposed_b)."""
+    _check(lib().cri_matmul_transposed_b(_ptr(A), _ptr(B), _ptr(C), M, N, K, _stream(stream)))
+
+
+def batched_matmul_gqa(A, B, C, n_heads, n_kv_heads, M, N, K, stream=None):
+    """C[h] = A[h] * B[h / (n_heads/n_kv_heads)] (replaces cuinfer::batched_matmul_gqa)."""
+    _check(
+        lib().cri_batched_matmul_gqa(
+            _ptr(A), _ptr(B), _ptr(C), n_heads, n_kv_heads, M, N, K, _stream(stream)
+        )
+    )

@@ -1,0 +1,174 @@
+// abi.cpp -- the extern "C" boundary declared in include/cri.h.
+//
+// Validates every argument before anything is enqueued (the reference
+// launches unconditionally and truncates K/32 and K/256 silently,
+// ref:src/kernels/matmul_quant.cu:77-78, 322-323), picks a kernel, and turns
+// HIP launch failures into CRI_ERR_LAUNCH with a message.
+#include "../../include/cri.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "internal.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fn, const std::string& what) {
+    g_last_error = std::string(fn) + ": " + what;
+    return status;
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int check_launch(const char* fn) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(CRI_ERR_LAUNCH, fn, std::string("kernel launch failed: ") + hipGetErrorString(e));
+    return CRI_OK;
+}
+
+constexpr long kMaxElems = (1L << 40);
+
+int fill_zero(float* C, long n, hipStream_t stream, const char* fn);
+
+int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream,
+                const char* fn) {
+    if (M < 0 || N < 0 || K < 0)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn,
+                    "negative dimension (M=" + std::to_string(M) + ", N=" + std::to_string(N) +
+                        ", K=" + std::to_string(K) + ")");
+    const int be = cri::block_elems(fmt);
+    if (K % be != 0)
+        return fail(CRI_ERR_SHAPE, fn,
+                    "K=" + std::to_string(K) + " is not a multiple of the block size " + std::to_string(be));
+    if (M == 0 || N == 0) return CRI_OK;
+    if (!A || !B || !C) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(A, 4) || !aligned(C, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "A and C must be 4-byte aligned");
+    if (fmt == cri::kFmtF16 && !aligned(B, 2)) return fail(CRI_ERR_ALIGNMENT, fn, "FP16 B must be 2-byte aligned");
+    if (static_cast<long>(M) * K > kMaxElems || static_cast<long>(M) * N > kMaxElems)
+        return fail(CRI_ERR_SHAPE, fn, "problem too large");
+    if (K == 0) return fill_zero(C, static_cast<long>(M) * N, stream, fn);
+    int rc;
+    if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
+        rc = cri::detail::launch_gemv(fmt, A, B, C, N, K, stream);
+    else
+        rc = cri::detail::launch_generic_matmul(fmt, A, B, C, M, N, K, stream);
+    if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
+    return check_launch(fn);
+}
+
+int dequant_impl(int fmt, const void* src, float* dst, int n_blocks, hipStream_t stream, const char* fn) {
+    if (n_blocks < 0) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative n_blocks");
+    if (n_blocks == 0) return CRI_OK;
+    if (!src || !dst) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(dst, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "dst must be 4-byte aligned");
+    if (cri::detail::launch_dequant(fmt, src, dst, n_blocks, stream) != 0)
+        return fail(CRI_ERR_UNSUPPORTED, fn, "unknown format");
+    return check_launch(fn);
+}
+
+}  // namespace
+
+namespace {
+int fill_zero(float* C, long n, hipStream_t stream, const char* fn) {
+    cri::detail::launch_fill_zero(C, n, stream);
+    return check_launch(fn);
+}
+}  // namespace
+
+extern "C" {
+
+int cri_matmul_q8_0(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    return matmul_impl(cri::kFmtQ8_0, A, B, C, M, N, K, s, "cri_matmul_q8_0");
+}
+int cri_matmul_q4_0(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    return matmul_impl(cri::kFmtQ4_0, A, B, C, M, N, K, s, "cri_matmul_q4_0");
+}
+int cri_matmul_q5_0(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    return matmul_impl(cri::kFmtQ5_0, A, B, C, M, N, K, s, "cri_matmul_q5_0");
+}
+int cri_matmul_q4_k(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    return matmul_impl(cri::kFmtQ4_K, A, B, C, M, N, K, s, "cri_matmul_q4_k");
+}
+int cri_matmul_q6_k(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    return matmul_impl(cri::kFmtQ6_K, A, B, C, M, N, K, s, "cri_matmul_q6_k");
+}
+int cri_matmul_fp16(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    // The reference requires K % 32 == 0 for FP16 too (ref:include/cuinfer/kernels/matmul_quant.h:102).
+    if (K >= 0 && K % 32 != 0)
+        return fail(CRI_ERR_SHAPE, "cri_matmul_fp16", "K=" + std::to_string(K) + " is not a multiple of 32");
+    return matmul_impl(cri::kFmtF16, A, B, C, M, N, K, s, "cri_matmul_fp16");
+}
+int cri_matmul(int format, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    switch (format) {
+        case CRI_Q8_0: return cri_matmul_q8_0(A, B, C, M, N, K, s);
+        case CRI_Q4_0: return cri_matmul_q4_0(A, B, C, M, N, K, s);
+        case CRI_Q5_0: return cri_matmul_q5_0(A, B, C, M, N, K, s);
+        case CRI_Q4_K: return cri_matmul_q4_k(A, B, C, M, N, K, s);
+        case CRI_Q6_K: return cri_matmul_q6_k(A, B, C, M, N, K, s);
+        case CRI_FP16: return cri_matmul_fp16(A, B, C, M, N, K, s);
+    }
+    return fail(CRI_ERR_UNSUPPORTED, "cri_matmul", "unknown format id " + std::to_string(format));
+}
+
+int cri_dequantize_q8_0(const void* src, float* dst, int n_blocks, hipStream_t s) {
+    return dequant_impl(cri::kFmtQ8_0, src, dst, n_blocks, s, "cri_dequantize_q8_0");
+}
+int cri_dequantize_q4_0(const void* src, float* dst, int n_blocks, hipStream_t s) {
+    return dequant_impl(cri::kFmtQ4_0, src, dst, n_blocks, s, "cri_dequantize_q4_0");
+}
+int cri_dequantize_q5_0(const void* src, float* dst, int n_blocks, hipStream_t s) {
+    return dequant_impl(cri::kFmtQ5_0, src, dst, n_blocks, s, "cri_dequantize_q5_0");
+}
+int cri_dequantize_q6_k(const void* src, float* dst, int n_blocks, hipStream_t s) {
+    return dequant_impl(cri::kFmtQ6_K, src, dst, n_blocks, s, "cri_dequantize_q6_k");
+}
+int cri_dequantize_q4_k(const void* src, float* dst, int n_blocks, hipStream_t s) {
+    return dequant_impl(cri::kFmtQ4_K, src, dst, n_blocks, s, "cri_dequantize_q4_k");
+}
+
+int cri_matmul_transposed_b(const float* A, const float* B, float* C, int M, int N, int K, hipStream_t s) {
+    const char* fn = "cri_matmul_transposed_b";
+    if (M < 0 || N < 0 || K < 0) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative dimension");
+    if (M == 0 || N == 0) return CRI_OK;
+    if (!A || !B || !C) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(A, 4) || !aligned(B, 4) || !aligned(C, 4))
+        return fail(CRI_ERR_ALIGNMENT, fn, "A, B and C must be 4-byte aligned");
+    if (static_cast<long>(M) * K > kMaxElems || static_cast<long>(N) * K > kMaxElems)
+        return fail(CRI_ERR_SHAPE, fn, "problem too large");
+    if (K == 0) return fill_zero(C, static_cast<long>(M) * N, s, fn);
+    if (cri::detail::launch_transposed_b(A, B, C, M, N, K, s) != 0)
+        return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
+    return check_launch(fn);
+}
+
+int cri_batched_matmul_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_heads, int M, int N,
+                           int K, hipStream_t s) {
+    const char* fn = "cri_batched_matmul_gqa";
+    if (n_heads < 0 || n_kv_heads < 0 || M < 0 || N < 0 || K < 0)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative dimension");
+    if (n_heads == 0 || M == 0 || N == 0) return CRI_OK;
+    if (n_kv_heads == 0 || n_heads % n_kv_heads != 0)
+        return fail(CRI_ERR_SHAPE, fn,
+                    "n_heads=" + std::to_string(n_heads) + " is not a multiple of n_kv_heads=" +
+                        std::to_string(n_kv_heads));
+    if (!A || !B || !C) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(A, 4) || !aligned(B, 4) || !aligned(C, 4))
+        return fail(CRI_ERR_ALIGNMENT, fn, "A, B and C must be 4-byte aligned");
+    if (K == 0) return fill_zero(C, static_cast<long>(n_heads) * M * N, s, fn);
+    if (cri::detail::launch_gqa(A, B, C, n_heads, n_kv_heads, M, N, K, s) != 0)
+        return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
+    return check_launch(fn);
+}
+
+const char* cri_last_error_string(void) { return g_last_error.c_str(); }
+
+int cri_block_bytes(int format) { return format >= 0 && format <= 5 ? cri::block_bytes(format) : 0; }
+int cri_block_elems(int format) { return format >= 0 && format <= 5 ? cri::block_elems(format) : 0; }
+int cri_version(void) { return 100; }
+
+}  // extern "C"

@@ -1,0 +1,255 @@
+// cuinfer_api.cpp -- the reference's C++ entry points on top of the C ABI.
+//
+// Each wrapper forwards to its cri_* function and throws std::runtime_error
+// on a non-zero status, which is how the reference reports errors
+// (CUINFER_CHECK_CUDA, ref:include/cuinfer/cuda_utils.h:12-20).
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <stdexcept>
+#include <string>
+#include <utility>
+
+#include "../../include/cri.h"
+#include "../../include/cuinfer/attention.h"
+#include "../../include/cuinfer/dispatch.h"
+#include "../../include/cuinfer/embedding.h"
+#include "../../include/cuinfer/hip_utils.h"
+#include "../../include/cuinfer/kernels/matmul_quant.h"
+#include "../../include/cuinfer/quantization.h"
+#include "../../include/cuinfer/tensor.h"
+
+namespace cuinfer {
+
+void matmul_q8_0(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_matmul_q8_0(A, B, C, M, N, K, s));
+}
+void matmul_q4_0(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_matmul_q4_0(A, B, C, M, N, K, s));
+}
+void matmul_q5_0(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_matmul_q5_0(A, B, C, M, N, K, s));
+}
+void matmul_q4_k(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_matmul_q4_k(A, B, C, M, N, K, s));
+}
+void matmul_q6_k(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_matmul_q6_k(A, B, C, M, N, K, s));
+}
+void matmul_fp16(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_matmul_fp16(A, B, C, M, N, K, s));
+}
+
+void dequantize_q8_0(const void* src, float* dst, int n, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_dequantize_q8_0(src, dst, n, s));
+}
+void dequantize_q4_0(const void* src, float* dst, int n, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_dequantize_q4_0(src, dst, n, s));
+}
+void dequantize_q5_0(const void* src, float* dst, int n, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_dequantize_q5_0(src, dst, n, s));
+}
+void dequantize_q6_k(const void* src, float* dst, int n, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_dequantize_q6_k(src, dst, n, s));
+}
+void dequantize_q4_k(const void* src, float* dst, int n, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_dequantize_q4_k(src, dst, n, s));
+}
+
+void matmul_transposed_b(const float* A, const float* B, float* C, int M, int N, int K, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_matmul_transposed_b(A, B, C, M, N, K, s));
+}
+
+void batched_matmul_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_heads, int M, int N, int K,
+                        hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_batched_matmul_gqa(A, B, C, n_heads, n_kv_heads, M, N, K, s));
+}
+
+// ---------------------------------------------------------------- dispatch
+const char* weight_format_name(WeightFormat fmt) {
+    switch (fmt) {
+        case WeightFormat::FP32: return "FP32";
+        case WeightFormat::FP16: return "FP16";
+        case WeightFormat::Q8_0: return "Q8_0";
+        case WeightFormat::Q4_0: return "Q4_0";
+        case WeightFormat::Q5_0: return "Q5_0";
+        case WeightFormat::Q4_K: return "Q4_K";
+        case WeightFormat::Q6_K: return "Q6_K";
+    }
+    return "UNKNOWN";
+}
+
+WeightFormat weight_format_of(DType dtype) {
+    switch (dtype) {
+        case DType::FP16: return WeightFormat::FP16;
+        case DType::Q8_0: return WeightFormat::Q8_0;
+        case DType::Q4_0: return WeightFormat::Q4_0;
+        case DType::Q5_0: return WeightFormat::Q5_0;
+        case DType::Q4_K: return WeightFormat::Q4_K;
+        case DType::Q6_K: return WeightFormat::Q6_K;
+        default: return WeightFormat::FP32;
+    }
+}
+
+void matmul_dispatch(const float* A, const Tensor& weight, float* C, int M, int N, int K, WeightFormat format,
+                     hipStream_t s) {
+    int id;
+    switch (format) {
+        case WeightFormat::FP16: id = CRI_FP16; break;
+        case WeightFormat::Q8_0: id = CRI_Q8_0; break;
+        case WeightFormat::Q4_0: id = CRI_Q4_0; break;
+        case WeightFormat::Q5_0: id = CRI_Q5_0; break;
+        case WeightFormat::Q4_K: id = CRI_Q4_K; break;
+        case WeightFormat::Q6_K: id = CRI_Q6_K; break;
+        default:
+            throw std::invalid_argument("matmul_dispatch: FP32 weights ([K,N] pre-transposed) are not handled here");
+    }
+    CUINFER_CHECK_CRI(cri_matmul(id, A, weight.data(), C, M, N, K, s));
+}
+
+// ---------------------------------------------------------------- Tensor
+void Tensor::compute_shape_and_stride(const std::vector<int64_t>& shape, std::array<int64_t, 4>& out_shape,
+                                      std::array<int64_t, 4>& out_stride) {
+    out_shape.fill(1);
+    const int off = 4 - static_cast<int>(shape.size());
+    for (size_t i = 0; i < shape.size(); ++i) {
+        if (shape[i] <= 0) throw std::invalid_argument("Tensor: dimensions must be positive");
+        out_shape[off + i] = shape[i];
+    }
+    out_stride[3] = 1;
+    for (int i = 2; i >= 0; --i) out_stride[i] = out_stride[i + 1] * out_shape[i + 1];
+}
+
+Tensor::Tensor() = default;
+
+Tensor::Tensor(std::vector<int64_t> shape, DType dtype) : dtype_(dtype), owning_(true) {
+    if (shape.empty() || shape.size() > 4)
+        throw std::invalid_argument("Tensor shape must have 1-4 dimensions, got " + std::to_string(shape.size()));
+    compute_shape_and_stride(shape, shape_, stride_);
+    if (dtype_is_quantized(dtype) && shape_[3] % dtype_block_elements(dtype) != 0)
+        throw std::invalid_argument(std::string("Tensor: innermost dimension is not a multiple of the ") +
+                                    dtype_name(dtype) + " block size");
+    const size_t bytes = size_bytes();
+    if (bytes > 0) CUINFER_CHECK_HIP(hipMalloc(&data_, bytes));
+}
+
+Tensor::Tensor(void* data, std::array<int64_t, 4> shape, std::array<int64_t, 4> stride, DType dtype)
+    : data_(data), shape_(shape), stride_(stride), dtype_(dtype), owning_(false) {}
+
+Tensor::~Tensor() {
+    if (owning_ && data_) (void)hipFree(data_);
+    data_ = nullptr;
+}
+
+Tensor::Tensor(Tensor&& o) noexcept
+    : data_(o.data_), shape_(o.shape_), stride_(o.stride_), dtype_(o.dtype_), owning_(o.owning_) {
+    o.data_ = nullptr;
+    o.owning_ = false;
+}
+
+Tensor& Tensor::operator=(Tensor&& o) noexcept {
+    if (this != &o) {
+        if (owning_ && data_) (void)hipFree(data_);
+        data_ = o.data_;
+        shape_ = o.shape_;
+        stride_ = o.stride_;
+        dtype_ = o.dtype_;
+        owning_ = o.owning_;
+        o.data_ = nullptr;
+        o.owning_ = false;
+    }
+    return *this;
+}
+
+Tensor Tensor::from_host(const void* host, std::vector<int64_t> shape, DType dtype) {
+    Tensor t(std::move(shape), dtype);
+    t.copy_from_host(host, t.size_bytes());
+    return t;
+}
+
+Tensor Tensor::zeros(std::vector<int64_t> shape, DType dtype) {
+    Tensor t(std::move(shape), dtype);
+    if (t.size_bytes()) CUINFER_CHECK_HIP(hipMemset(t.data_, 0, t.size_bytes()));
+    return t;
+}
+
+Tensor Tensor::empty(std::vector<int64_t> shape, DType dtype) { return Tensor(std::move(shape), dtype); }
+
+Tensor Tensor::view(int64_t dim, int64_t start, int64_t end) const {
+    if (dim < 0 || dim >= 4) throw std::out_of_range("view(): dim must be in [0, 3]");
+    if (start < 0 || end > shape_[dim] || start >= end) throw std::out_of_range("view(): invalid range");
+    size_t byte_offset;
+    if (dtype_is_quantized(dtype_)) {
+        const int64_t elems = start * stride_[dim];
+        const int be = dtype_block_elements(dtype_);
+        if (elems % be != 0 || (dim == 3 && ((end - start) % be != 0)))
+            throw std::invalid_argument("view(): quantised slice must fall on block boundaries");
+        byte_offset = static_cast<size_t>(elems / be) * dtype_block_bytes(dtype_);
+    } else {
+        byte_offset = static_cast<size_t>(start * stride_[dim]) * dtype_size(dtype_);
+    }
+    auto ns = shape_;
+    ns[dim] = end - start;
+    return Tensor(static_cast<char*>(data_) + byte_offset, ns, stride_, dtype_);
+}
+
+Tensor Tensor::reshape(std::vector<int64_t> new_shape) const {
+    if (!is_contiguous()) throw std::runtime_error("reshape(): tensor must be contiguous");
+    std::array<int64_t, 4> s, st;
+    compute_shape_and_stride(new_shape, s, st);
+    if (s[0] * s[1] * s[2] * s[3] != numel()) throw std::invalid_argument("reshape(): element count mismatch");
+    return Tensor(data_, s, st, dtype_);
+}
+
+Tensor Tensor::clone() const {
+    if (!is_contiguous()) throw std::runtime_error("clone(): tensor must be contiguous");
+    std::vector<int64_t> s(shape_.begin(), shape_.end());
+    Tensor t(s, dtype_);
+    if (size_bytes()) CUINFER_CHECK_HIP(hipMemcpy(t.data_, data_, size_bytes(), hipMemcpyDeviceToDevice));
+    return t;
+}
+
+void Tensor::copy_from_host(const void* host, size_t bytes) {
+    if (bytes > size_bytes()) throw std::out_of_range("copy_from_host(): too many bytes");
+    if (bytes) CUINFER_CHECK_HIP(hipMemcpy(data_, host, bytes, hipMemcpyHostToDevice));
+}
+
+void Tensor::copy_to_host(void* host, size_t bytes) const {
+    if (bytes > size_bytes()) throw std::out_of_range("copy_to_host(): too many bytes");
+    if (bytes) CUINFER_CHECK_HIP(hipMemcpy(host, data_, bytes, hipMemcpyDeviceToHost));
+}
+
+int64_t Tensor::numel() const { return shape_[0] * shape_[1] * shape_[2] * shape_[3]; }
+
+size_t Tensor::size_bytes() const {
+    if (dtype_is_quantized(dtype_))
+        return static_cast<size_t>(numel() / dtype_block_elements(dtype_)) * dtype_block_bytes(dtype_);
+    return static_cast<size_t>(numel()) * dtype_size(dtype_);
+}
+
+int Tensor::ndim() const {
+    int lead = 0;
+    while (lead < 3 && shape_[lead] == 1) ++lead;
+    return 4 - lead;
+}
+
+bool Tensor::is_contiguous() const {
+    int64_t expect = 1;
+    for (int i = 3; i >= 0; --i) {
+        if (shape_[i] != 1 && stride_[i] != expect) return false;
+        expect *= shape_[i];
+    }
+    return true;
+}
+
+int64_t Tensor::shape(int dim) const {
+    if (dim < 0 || dim >= 4) throw std::out_of_range("shape(): dim out of range");
+    return shape_[dim];
+}
+
+int64_t Tensor::stride(int dim) const {
+    if (dim < 0 || dim >= 4) throw std::out_of_range("stride(): dim out of range");
+    return stride_[dim];
+}
+
+}  // namespace cuinfer

@@ -1,0 +1,62 @@
+// internal.hpp -- launchers shared between the kernel translation units and
+// the C ABI (abi.cpp).  Launchers assume the ABI has validated every shape,
+// pointer and alignment requirement; they only enqueue kernels.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+namespace cri {
+
+// Format ids; identical to cri_format in include/cri.h, plus fp32 weights for
+// the transposed-B GEMV.
+enum : int { kFmtQ8_0 = 0, kFmtQ4_0 = 1, kFmtQ5_0 = 2, kFmtQ4_K = 3, kFmtQ6_K = 4, kFmtF16 = 5, kFmtF32 = 6 };
+
+inline int block_elems(int fmt) {
+    switch (fmt) {
+        case kFmtQ8_0: case kFmtQ4_0: case kFmtQ5_0: return 32;
+        case kFmtQ4_K: case kFmtQ6_K: return 256;
+        case kFmtF16: case kFmtF32: return 1;
+    }
+    return 0;
+}
+inline int block_bytes(int fmt) {
+    switch (fmt) {
+        case kFmtQ8_0: return 34;
+        case kFmtQ4_0: return 18;
+        case kFmtQ5_0: return 22;
+        case kFmtQ4_K: return 144;
+        case kFmtQ6_K: return 210;
+        case kFmtF16: return 2;
+        case kFmtF32: return 4;
+    }
+    return 0;
+}
+inline long row_bytes(int fmt, int K) { return static_cast<long>(K / block_elems(fmt)) * block_bytes(fmt); }
+
+namespace detail {
+
+// Target number of resident waves for the GEMV grid (MI355X: 256 CUs).
+constexpr long kGemvTargetWaves = 2048;
+
+// batch-1 GEMV (gemv.hip)
+bool gemv_supported(int fmt, int K, const void* W);
+int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream);
+
+// any-M fused dequant matmul, element-wise decode (generic.hip)
+int launch_generic_matmul(int fmt, const float* A, const void* B, float* C, int M, int N, int K,
+                          hipStream_t stream);
+
+// standalone dequant (dequant.hip)
+int launch_dequant(int fmt, const void* src, float* dst, long n_blocks, hipStream_t stream);
+
+// C[0..n) = 0 with a kernel (no hipMemsetAsync, so the call can be captured in a graph)
+void launch_fill_zero(float* C, long n, hipStream_t stream);
+
+// fp32 neighbours (fp32ops.hip)
+int launch_transposed_b(const float* A, const float* B, float* C, int M, int N, int K, hipStream_t stream);
+int launch_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_heads, int M, int N, int K,
+               hipStream_t stream);
+
+}  // namespace detail
+}  // namespace cri

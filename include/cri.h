@@ -1,0 +1,109 @@
+/*
+ * cri.h -- C ABI of the MI355X (gfx950) fused dequant+matmul library.
+ *
+ * Every entry point takes device pointers owned by the caller, enqueues its
+ * kernels on `stream` (0 = the null stream) and returns without
+ * synchronising.  The library allocates no device memory and keeps no state
+ * between calls, so calls are re-entrant on any stream.
+ *
+ * Return value: CRI_OK (0) on success, otherwise a negative cri_status; the
+ * thread-local message from cri_last_error_string() says what was wrong.
+ * Unlike the reference (which silently truncates K/32 and K/256), shapes are
+ * validated before anything is launched.  Errors that happen while a kernel
+ * executes surface at the caller's next synchronisation, as in the reference.
+ *
+ * Conventions (ref:include/cuinfer/kernels/matmul_quant.h:1-22):
+ *   A : fp32 [M, K] row-major activations
+ *   B : [N, K] weights in GGUF row order: row n is K/bs consecutive blocks
+ *   C : fp32 [M, N] row-major output, fully overwritten (never accumulated)
+ *   A, B and C must not overlap.
+ */
+#ifndef CRI_H
+#define CRI_H
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum cri_status {
+    CRI_OK = 0,
+    CRI_ERR_INVALID_ARGUMENT = -1, /* null pointer or negative dimension       */
+    CRI_ERR_SHAPE = -2,            /* K not a multiple of the block size, etc. */
+    CRI_ERR_ALIGNMENT = -3,        /* pointer misaligned for its element type  */
+    CRI_ERR_LAUNCH = -4,           /* the HIP runtime rejected a launch        */
+    CRI_ERR_UNSUPPORTED = -5       /* format id unknown                        */
+} cri_status;
+
+/* Weight formats; the numbering is shared with cri_matmul()/cri_dequantize(). */
+typedef enum cri_format {
+    CRI_Q8_0 = 0,
+    CRI_Q4_0 = 1,
+    CRI_Q5_0 = 2,
+    CRI_Q4_K = 3,
+    CRI_Q6_K = 4,
+    CRI_FP16 = 5
+} cri_format;
+
+/* ---- fused dequant + matmul: C[M,N] = A[M,K] * dequant(B[N,K])^T ---------- */
+
+/* replaces cuinfer::matmul_q8_0, ref:include/cuinfer/kernels/matmul_quant.h:37 (K % 32 == 0) */
+int cri_matmul_q8_0(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+/* replaces cuinfer::matmul_q4_0, ref:include/cuinfer/kernels/matmul_quant.h:50 (K % 32 == 0) */
+int cri_matmul_q4_0(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+/* replaces cuinfer::matmul_q5_0, ref:include/cuinfer/kernels/matmul_quant.h:63 (K % 32 == 0) */
+int cri_matmul_q5_0(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+/* replaces cuinfer::matmul_q4_k, ref:include/cuinfer/kernels/matmul_quant.h:76 (K % 256 == 0) */
+int cri_matmul_q4_k(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+/* replaces cuinfer::matmul_q6_k, ref:include/cuinfer/kernels/matmul_quant.h:88 (K % 256 == 0) */
+int cri_matmul_q6_k(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+/* replaces cuinfer::matmul_fp16, ref:include/cuinfer/kernels/matmul_quant.h:104 (K % 32 == 0,
+ * as the reference requires; B must be 2-byte aligned) */
+int cri_matmul_fp16(const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+/* format-switched form of the six above; mirrors the switch of matmul_dispatch,
+ * ref:src/model.cu:797-825 (FP32 weights are not part of this library) */
+int cri_matmul(int format, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+
+/* ---- standalone dequant: dst[n_blocks * bs] = dequant(src) --------------- */
+
+/* replaces cuinfer::dequantize_q8_0, ref:include/cuinfer/quantization.h:145 */
+int cri_dequantize_q8_0(const void* src, float* dst, int n_blocks, hipStream_t stream);
+/* replaces cuinfer::dequantize_q4_0, ref:include/cuinfer/quantization.h:152 */
+int cri_dequantize_q4_0(const void* src, float* dst, int n_blocks, hipStream_t stream);
+/* replaces cuinfer::dequantize_q5_0, ref:include/cuinfer/quantization.h:159 */
+int cri_dequantize_q5_0(const void* src, float* dst, int n_blocks, hipStream_t stream);
+/* replaces cuinfer::dequantize_q6_k, ref:include/cuinfer/quantization.h:166 */
+int cri_dequantize_q6_k(const void* src, float* dst, int n_blocks, hipStream_t stream);
+/* replaces cuinfer::dequantize_q4_k, ref:include/cuinfer/quantization.h:173 */
+int cri_dequantize_q4_k(const void* src, float* dst, int n_blocks, hipStream_t stream);
+
+/* ---- fp32 neighbours of the path ----------------------------------------- */
+
+/* C[M,N] = A[M,K] * B[N,K]^T, all fp32; replaces cuinfer::matmul_transposed_b,
+ * ref:include/cuinfer/embedding.h:136-137 (any K >= 1) */
+int cri_matmul_transposed_b(const float* A, const float* B, float* C, int M, int N, int K,
+                            hipStream_t stream);
+
+/* C[h] = A[h] * B[h / (n_heads / n_kv_heads)] with A [n_heads, M, K],
+ * B [n_kv_heads, K, N], C [n_heads, M, N], all fp32; replaces
+ * cuinfer::batched_matmul_gqa, ref:include/cuinfer/attention.h:79-82
+ * (n_heads % n_kv_heads == 0 is checked here; the reference checks it only in
+ * AttentionBlock, ref:src/attention.cu:534-539) */
+int cri_batched_matmul_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_heads,
+                           int M, int N, int K, hipStream_t stream);
+
+/* ---- diagnostics ---------------------------------------------------------- */
+
+/* Message for the last non-zero status returned on this thread ("" if none). */
+const char* cri_last_error_string(void);
+/* Bytes per block / elements per block of a format (0 if unknown). */
+int cri_block_bytes(int format);
+int cri_block_elems(int format);
+/* Library ABI version (major * 10000 + minor * 100 + patch). */
+int cri_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CRI_H */

@@ -1,0 +1,112 @@
+"""The C ABI library loads, exports every function include/cri.h declares, and
+rejects bad arguments before touching the GPU (so this runs without one)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import cretif_amd as cri
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    names = []
+    for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if h.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", h)).read()
+            names += re.findall(r"^\s*(?:int|const char\*)\s+(cri_\w+)\s*\(", text, re.M)
+    return names
+
+
+def test_header_declares_abi():
+    names = header_functions()
+    assert len(names) >= 18
+    assert set(names) == set(cri.ABI_SYMBOLS)
+
+
+def test_library_exports_every_symbol():
+    L = ctypes.CDLL(cri.library_path)
+    for name in header_functions():
+        assert hasattr(L, name), name
+
+
+def test_block_tables():
+    L = cri.lib()
+    assert [L.cri_block_bytes(i) for i in range(6)] == [34, 18, 22, 144, 210, 2]
+    assert [L.cri_block_elems(i) for i in range(6)] == [32, 32, 32, 256, 256, 1]
+    assert L.cri_block_bytes(99) == 0
+    assert L.cri_version() >= 100
+
+
+FAKE = 1 << 20  # never dereferenced: every case below fails validation first
+
+
+@pytest.mark.parametrize(
+    "fn,K,status",
+    [
+        ("matmul_q8_0", 48, -2),
+        ("matmul_q4_0", 33, -2),
+        ("matmul_q5_0", 16, -2),
+        ("matmul_q4_k", 512 + 32, -2),
+        ("matmul_q6_k", 128, -2),
+        ("matmul_fp16", 40, -2),
+    ],
+)
+def test_bad_k_rejected(fn, K, status):
+    with pytest.raises(cri.CretifError) as e:
+        getattr(cri, fn)(FAKE, FAKE, FAKE, 1, 8, K, stream=0)
+    assert e.value.status == status
+    assert "multiple" in str(e.value)
+
+
+def test_negative_dims_and_nulls():
+    with pytest.raises(cri.CretifError) as e:
+        cri.matmul_q8_0(FAKE, FAKE, FAKE, -1, 8, 32, stream=0)
+    assert e.value.status == -1
+    with pytest.raises(cri.CretifError) as e:
+        cri.matmul_q4_k(0, FAKE, FAKE, 1, 8, 256, stream=0)
+    assert e.value.status == -1
+    with pytest.raises(cri.CretifError) as e:
+        cri.dequantize_q6_k(FAKE, FAKE, -3, stream=0)
+    assert e.value.status == -1
+
+
+def test_misaligned_rejected():
+    with pytest.raises(cri.CretifError) as e:
+        cri.matmul_q8_0(FAKE + 2, FAKE, FAKE, 1, 8, 32, stream=0)
+    assert e.value.status == -3
+    with pytest.raises(cri.CretifError) as e:
+        cri.matmul_fp16(FAKE, FAKE + 1, FAKE, 1, 8, 32, stream=0)
+    assert e.value.status == -3
+
+
+def test_empty_problems_are_noops():
+    # M == 0 or N == 0 or n_blocks == 0: nothing to launch, success
+    cri.matmul_q8_0(0, 0, 0, 0, 8, 32, stream=0)
+    cri.matmul_q4_k(0, 0, 0, 4, 0, 256, stream=0)
+    cri.dequantize_q4_k(0, 0, 0, stream=0)
+    cri.batched_matmul_gqa(0, 0, 0, 0, 8, 1, 64, 64, stream=0)
+
+
+def test_unknown_format():
+    with pytest.raises(cri.CretifError) as e:
+        cri.matmul(17, FAKE, FAKE, FAKE, 1, 8, 32, stream=0)
+    assert e.value.status == -5
+
+
+def test_gqa_head_ratio():
+    with pytest.raises(cri.CretifError) as e:
+        cri.batched_matmul_gqa(FAKE, FAKE, FAKE, 6, 4, 1, 64, 64, stream=0)
+    assert e.value.status == -2
+    with pytest.raises(cri.CretifError) as e:
+        cri.batched_matmul_gqa(FAKE, FAKE, FAKE, 4, 0, 1, 64, 64, stream=0)
+    assert e.value.status == -2
+
+
+def test_cpu_tensor_rejected():
+    torch = pytest.importorskip("torch")
+    A = torch.zeros(1, 32)
+    with pytest.raises(ValueError):
+        cri.matmul_q8_0(A, A, A, 1, 1, 32, stream=0)

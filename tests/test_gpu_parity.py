@@ -1,0 +1,243 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars (from the path's contract):
+  * dequantisation: bit-exact;
+  * fused matmul / GEMV in fp32 FMA: ||C - C_ref||_inf <= 1e-5 * ||C_ref||_inf;
+  * exact-integer inputs (every partial sum exact): bit-exact for every format
+    and every kernel variant, whatever the summation order.
+"""
+import numpy as np
+import pytest
+
+from conftest import bits_equal, normwise_rel_err
+
+torch = pytest.importorskip("torch")
+import cretif_amd as cri  # noqa: E402
+from cretif_amd import quant  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-5
+FMTS = ["q8_0", "q4_0", "q5_0", "q4_k", "q6_k", "fp16"]
+BE = {"q8_0": 32, "q4_0": 32, "q5_0": 32, "q4_k": 256, "q6_k": 256, "fp16": 1}
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def weights(fmt, N, K, seed):
+    return quant.synthetic_weights(fmt, N, K, seed=seed)
+
+
+def run_matmul(fmt, A, Bq, N, K):
+    M = A.shape[0]
+    dA, dB = dev(A), dev(Bq)
+    dC = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    cri.matmul(fmt, dA, dB, dC, M, N, K)
+    return host(dC)
+
+
+# ------------------------------------------------------------------ dequant
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q6_k", "q4_k"])
+def test_dequant_reference_blocks(orc, fmt):
+    nb = 64 if fmt in ("q8_0", "q4_0") else 8  # ref:tests/test_dequantize.cu:214-416
+    blocks = orc.make_blocks(fmt, nb)
+    n = nb * BE[fmt]
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    cri.dequantize(fmt, dev(blocks), out, nb)
+    assert bits_equal(host(out), orc.dequantize(fmt, blocks, n))
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q5_0", "q6_k", "q4_k"])
+@pytest.mark.parametrize("nb", [1, 3, 257, 20000])
+def test_dequant_random_bytes(orc, fmt, nb):
+    rng = np.random.default_rng(nb)
+    bb = quant.BLOCK_BYTES[fmt]
+    raw = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    specials = np.array([0.0, -0.0, 2.0**-24, 3 * 2.0**-20, 0.02, -1.5, 65504.0], np.float16)
+    d = rng.choice(specials, size=nb).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    if fmt == "q6_k":
+        raw[:, 208:210] = d
+    else:
+        raw[:, 0:2] = d
+        if fmt == "q4_k":
+            raw[:, 2:4] = rng.choice(specials, size=nb).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    n = nb * BE[fmt]
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    cri.dequantize(fmt, dev(raw.ravel()), out, nb)
+    assert bits_equal(host(out), orc.dequantize(fmt, raw.ravel(), n))
+
+
+def test_dequant_q5_0_reference_roundtrip(orc):
+    # ref:tests/test_matmul_quant.cu:569-603 (16 blocks from the LCG generator)
+    x = orc.random_matrix_lcg(1, 16 * 32, seed=42).ravel()
+    blocks = orc.quantize("q5_0", x)
+    out = torch.empty(512, dtype=torch.float32, device="cuda")
+    cri.dequantize_q5_0(dev(blocks), out, 16)
+    assert bits_equal(host(out), orc.dequantize("q5_0", blocks, 512))
+
+
+# ------------------------------------------------------------------ GEMV (M = 1)
+GEMV_SHAPES = [
+    ("q8_0", 1536, 576),     # BASELINE config 1 (SmolLM2-135M FFN up-proj)
+    ("q8_0", 8192, 2048),
+    ("q8_0", 2048, 8192),
+    ("q4_0", 8192, 2048),    # config 2
+    ("q4_0", 2048, 8192),
+    ("q5_0", 8192, 2048),
+    ("q5_0", 2048, 8192),
+    ("q4_k", 2048, 2048),    # config 3
+    ("q4_k", 512, 2048),
+    ("q4_k", 8192, 2048),
+    ("q4_k", 2048, 8192),
+    ("q6_k", 2048, 2048),
+    ("q6_k", 512, 2048),
+    ("q6_k", 128256, 2048),  # Llama-3.2-1B lm_head
+    ("fp16", 8192, 2048),
+    ("fp16", 2048, 8192),
+    ("fp16", 576, 576),
+]
+
+
+@pytest.mark.parametrize("fmt,N,K", GEMV_SHAPES)
+def test_gemv_baseline_shapes(orc, fmt, N, K):
+    A = quant.randn(K, seed=2000 + K).reshape(1, K)
+    Bq = weights(fmt, N, K, seed=1000 + N)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    err = normwise_rel_err(got, ref)
+    assert err <= GEMV_TOL, err
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("N", [1, 3, 17, 130, 1001])
+@pytest.mark.parametrize("K", [256, 768, 4096, 16384])
+def test_gemv_ragged(orc, fmt, N, K):
+    A = quant.randn(K, seed=K + N).reshape(1, K)
+    Bq = weights(fmt, N, K, seed=N * 7 + K)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q5_0", "fp16"])
+@pytest.mark.parametrize("K", [32, 96, 320, 576 + 32])
+def test_gemv_k_not_multiple_of_64(orc, fmt, K):
+    # odd block counts per row: rows not dword aligned -> element-wise path
+    N = 77
+    A = quant.randn(K, seed=K).reshape(1, K)
+    Bq = weights(fmt, N, K, seed=K + 1)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M", [1, 2, 5, 16])
+def test_exact_integer_bit_exact(orc, fmt, M):
+    from test_oracle_matmul import exact_case
+
+    N, K = 300, 1024
+    A, Bq = exact_case(fmt, M, N, K, seed=M)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert bits_equal(got, ref)
+
+
+def test_misaligned_weight_pointer(orc):
+    # B starting 2 bytes into an allocation: the ABI must route around the
+    # dword-aligned vector loads and still match
+    N, K = 64, 512
+    A = quant.randn(K, seed=1).reshape(1, K)
+    Bq = weights("q4_k", N, K, seed=2)
+    buf = torch.zeros(Bq.size + 2, dtype=torch.uint8, device="cuda")
+    buf[2:] = dev(Bq)
+    C = torch.empty(1, N, dtype=torch.float32, device="cuda")
+    cri.matmul_q4_k(dev(A), buf.data_ptr() + 2, C, 1, N, K)
+    ref = orc.matmul_quant("q4_k", A, Bq, N, K)
+    assert normwise_rel_err(host(C), ref) <= GEMV_TOL
+
+
+# ------------------------------------------------------------------ M > 1
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,N,K", [(4, 64, 256), (2, 200, 512), (16, 512, 2048), (33, 70, 768)])
+def test_matmul_small_m(orc, fmt, M, N, K):
+    A = quant.randn(M * K, seed=M * 31 + K).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=N + K)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= GEMV_TOL
+
+
+def test_reference_test_shapes(orc):
+    # shapes and LCG data of ref:tests/test_matmul_quant.cu (MatmulQ8_0/Q4_0/Q4_K/Q5_0/Q6_K/FP16)
+    cases = [
+        ("q8_0", 4, 64, 128, 1, 2), ("q8_0", 1, 576, 576, 10, 20), ("q4_0", 4, 64, 128, 3, 4),
+        ("q4_k", 4, 32, 256, 5, 6), ("q5_0", 4, 64, 128, 7, 8), ("q5_0", 1, 576, 576, 11, 12),
+        ("q6_k", 4, 32, 256, 10, 11), ("q6_k", 1, 576, 1536, 20, 21), ("q4_k", 1, 1536, 512, 30, 31),
+        ("fp16", 4, 256, 256, 100, 101), ("fp16", 1, 576, 576, 102, 103), ("fp16", 1, 576, 1536, 104, 105),
+        ("fp16", 4, 576, 576, 106, 107),
+    ]
+    for fmt, M, N, K, sa, sb in cases:
+        A = orc.random_matrix_lcg(M, K, seed=sa)
+        B = orc.random_matrix_lcg(N, K, seed=sb)
+        Bq = B.astype(np.float16).view(np.uint8).ravel() if fmt == "fp16" else orc.quantize(fmt, B)
+        got = run_matmul(fmt, A, Bq, N, K)
+        ref = orc.matmul_quant(fmt, A, Bq, N, K)
+        assert normwise_rel_err(got, ref) <= GEMV_TOL, (fmt, M, N, K)
+
+
+def test_k_zero_writes_zeros():
+    C = torch.full((3, 5), 7.0, device="cuda")
+    A = torch.zeros(3, 1, device="cuda")
+    B = torch.zeros(64, dtype=torch.uint8, device="cuda")
+    cri.matmul_q8_0(A, B, C, 3, 5, 0)
+    assert np.all(host(C) == 0.0)
+
+
+def test_nondefault_stream(orc):
+    N, K = 1024, 2048
+    A = quant.randn(K, seed=9).reshape(1, K)
+    Bq = weights("q4_k", N, K, seed=10)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        dA, dB = dev(A), dev(Bq)
+        C = torch.empty(1, N, device="cuda")
+        cri.matmul_q4_k(dA, dB, C, 1, N, K, stream=s)
+    s.synchronize()
+    assert normwise_rel_err(C.cpu().numpy(), orc.matmul_quant("q4_k", A, Bq, N, K)) <= GEMV_TOL
+
+
+# ------------------------------------------------------------------ fp32 neighbours
+@pytest.mark.parametrize("M,N,K", [(1, 4, 3), (2, 4, 3), (64, 64, 64), (1, 5000, 2048), (3, 1000, 2048),
+                                   (1, 333, 100), (16, 4096, 2048)])
+def test_transposed_b(orc, M, N, K):
+    A = quant.randn(M * K, seed=M + K).reshape(M, K)
+    B = quant.randn(N * K, seed=N + K).reshape(N, K)
+    C = torch.empty(M, N, device="cuda")
+    cri.matmul_transposed_b(dev(A), dev(B), C, M, N, K)
+    assert normwise_rel_err(host(C), orc.matmul_transposed_b(A, B)) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("H,Hkv,M,N,K", [
+    (4, 2, 2, 3, 4),          # ref:tests/test_attention.cu:389-423
+    (32, 8, 1, 2048, 64),     # decode Q K^T, kv = 2048
+    (32, 8, 1, 64, 2048),     # decode P V
+    (32, 8, 16, 2048, 64),
+    (32, 8, 16, 64, 2048),
+    (6, 3, 5, 37, 45),
+    (8, 8, 3, 10, 700),
+])
+def test_gqa(orc, H, Hkv, M, N, K):
+    A = quant.randn(H * M * K, seed=H + M).reshape(H, M, K)
+    B = quant.randn(Hkv * K * N, seed=N + K).reshape(Hkv, K, N)
+    C = torch.empty(H, M, N, device="cuda")
+    cri.batched_matmul_gqa(dev(A), dev(B), C, H, Hkv, M, N, K)
+    ref = orc.batched_matmul_gqa(A, B, H, Hkv, M, N, K)
+    assert normwise_rel_err(host(C), ref) <= GEMV_TOL
