@@ -108,6 +108,20 @@ class GemvRig:
         self.graph = None
 
 
+def measured_traffic(workload):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary of this
+    workload (profiles/<kernel>_<shape>.md, line `traffic_bytes_per_launch:`), or None."""
+    import glob
+    import re
+
+    fmt, N, K = GEMV_WORKLOADS[workload]
+    for path in glob.glob(os.path.join(ROOT, "profiles", "*%s*%dx%d*.md" % (fmt.replace("_", ""), N, K))):
+        m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", open(path).read(), re.M)
+        if m:
+            return int(m.group(1))
+    return None
+
+
 def cpu_baseline(fmt, N, K, budget_s=12.0):
     """The reference's CPU path (dequant + sequential fp32 matmul, restated in
     oracle/oracle.c) on this host, single-threaded, on a bounded sample."""
@@ -146,7 +160,20 @@ def main():
     ap.add_argument("--workload", default="q4_k_gemv", choices=sorted(GEMV_WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-details", action="store_true", help="skip the per-format side measurements")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run ten 64 MiB device copies (known bytes, for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
+
+    if args.copy_calibration:
+        import torch
+
+        a = torch.empty(64 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(10):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print("copied 10 x %d bytes" % a.numel())
+        return
 
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the kernels shard by "
@@ -196,7 +223,7 @@ def main():
                    "weight_copies": copies, "rotation_bytes": copies * (bpl - 4 * K - 4 * N),
                    "timing": "HIP graph of %d launches replayed; hipEvents on the replay stream" % copies},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload)},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(fmt, N, K)

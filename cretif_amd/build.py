@@ -36,7 +36,10 @@ COMMON = [
 ]
 # Device code: gfx950 only; packed-FP32 VALU ops disabled (the compiler would
 # otherwise pair independent fp32 FMAs into v_pk_fma_f32).
-DEVICE = ["--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Kernel arguments are preloaded into SGPRs (gfx950 feature), so a wave's first
+# loads do not wait on scalar-memory round trips for its arguments.
+DEVICE = ["--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-mllvm", "-amdgpu-kernarg-preload-count=16"]
 
 
 def _run(cmd):

@@ -23,10 +23,16 @@
 namespace cri {
 namespace dev {
 
-template <class F, int UPL>
+// PREF row-groups of weight bytes are kept in flight per wave: a wave issues
+// the loads of its first PREF row-groups before anything else, then stages
+// the activations, so the HBM latency of the weights overlaps the activation
+// fetch; afterwards every decoded row-group is immediately replaced by the
+// row-group PREF steps ahead.
+template <class F, int UPL, int PREF>
 __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, const uint8_t* __restrict__ W,
-                                                   float* __restrict__ y, int N, int units, long row_bytes,
+                                                   float* __restrict__ y, int N, int K, int units, long row_bytes,
                                                    int lpr_log2) {
+    extern __shared__ float xs[];  // K activations, staged once per workgroup
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
     const int u0 = lane & (lpr - 1);
@@ -34,9 +40,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
     const int rows_per_iter = 64 >> lpr_log2;
     const int gwave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
-    const int stride = nwaves * rows_per_iter;
+    const int stride = nwaves * rows_per_iter;  // rows between a wave's consecutive row-groups
 
-    typename F::Xr xr[UPL];
     int unit[UPL];
     bool valid[UPL];
 #pragma unroll
@@ -44,20 +49,42 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
         const int un = u0 + u * lpr;
         valid[u] = un < units;
         unit[u] = valid[u] ? un : 0;  // idle lanes decode a real unit and discard it
-        F::load_x(xr[u], x, unit[u]);
     }
 
-    int base = gwave * rows_per_iter;
-    if (base >= N) return;  // whole wave idle (uniform)
-
-    // Ping-pong register sets: decode one while the next rows' bytes arrive.
-    typename F::Data buf0[UPL], buf1[UPL];
+    // 1. activations: global -> registers (issued first, tiny), weights in flight behind them
+    f32x4 xv[4];
+    const int nx4 = K >> 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int j = threadIdx.x + 256 * i;
+        xv[i] = j < nx4 ? ld_f32x4(x + 4 * j) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    typename F::Data buf[PREF][UPL];
+    const int base0 = gwave * rows_per_iter;
     auto load_rows = [&](typename F::Data(&dst)[UPL], int b) {
         const int r = min(b + rsub, N - 1);
         const uint8_t* rp = W + static_cast<long>(r) * row_bytes;
 #pragma unroll
         for (int u = 0; u < UPL; ++u) F::load(dst[u], rp, unit[u]);
     };
+#pragma unroll
+    for (int p = 0; p < PREF; ++p)
+        if (base0 + p * stride < N) load_rows(buf[p], base0 + p * stride);
+
+    // 2. stage activations in LDS (K <= 4096 is covered by the four loads above)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int j = threadIdx.x + 256 * i;
+        if (j < nx4) *reinterpret_cast<f32x4*>(xs + 4 * j) = xv[i];
+    }
+    for (int j = threadIdx.x + 1024; j < nx4; j += 256)
+        *reinterpret_cast<f32x4*>(xs + 4 * j) = ld_f32x4(x + 4 * j);
+    __syncthreads();
+    typename F::Xr xr[UPL];
+#pragma unroll
+    for (int u = 0; u < UPL; ++u) F::load_x(xr[u], xs, unit[u]);
+
+    // 3. stream the wave's row-groups
     auto finish = [&](const typename F::Data(&src)[UPL], int b) {
         float acc = 0.0f;
 #pragma unroll
@@ -69,16 +96,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
         const int r = b + rsub;
         if (u0 == 0 && r < N) y[r] = acc;
     };
-    load_rows(buf0, base);
-    for (;;) {
-        if (base + stride < N) load_rows(buf1, base + stride);
-        finish(buf0, base);
-        base += stride;
-        if (base >= N) break;
-        if (base + stride < N) load_rows(buf0, base + stride);
-        finish(buf1, base);
-        base += stride;
-        if (base >= N) break;
+    for (int b = base0; b < N; b += PREF * stride) {
+#pragma unroll
+        for (int p = 0; p < PREF; ++p) {
+            const int bp = b + p * stride;
+            if (bp < N) {
+                finish(buf[p], bp);
+                const int bn = bp + PREF * stride;
+                if (bn < N) load_rows(buf[p], bn);
+            }
+        }
     }
 }
 
@@ -86,11 +113,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
 
 namespace detail {
 
-template <class F, int UPL>
-static void launch_gemv_t(const float* x, const void* W, float* y, int N, int units, long row_bytes, int lpr_log2,
-                          int blocks, hipStream_t stream) {
-    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL>), dim3(blocks), dim3(256), 0, stream, x,
-                       static_cast<const uint8_t*>(W), y, N, units, row_bytes, lpr_log2);
+template <class F, int UPL, int PREF>
+static void launch_gemv_t(const float* x, const void* W, float* y, int N, int K, int units, long row_bytes,
+                          int lpr_log2, hipStream_t stream) {
+    const int rows_per_iter = 64 >> lpr_log2;
+    const long groups = (static_cast<long>(N) + rows_per_iter - 1) / rows_per_iter;
+    // one wave per PREF row-groups (all of a small matrix is requested at once),
+    // capped at the resident-wave budget of the GPU for large N
+    long waves = (groups + PREF - 1) / PREF;
+    if (waves > kGemvTargetWaves) waves = kGemvTargetWaves;
+    const int blocks = static_cast<int>((waves + 3) / 4);
+    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF>), dim3(blocks), dim3(256), K * sizeof(float), stream, x,
+                       static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2);
 }
 
 template <class F>
@@ -101,18 +135,11 @@ static int launch_gemv_f(const float* x, const void* W, float* y, int N, int K, 
     while ((1 << lpr_log2) < units && lpr_log2 < 6) ++lpr_log2;
     const int lpr = 1 << lpr_log2;
     const int upl = (units + lpr - 1) / lpr;
-    const int rows_per_iter = 64 / lpr;
-    const long wave_iters = (static_cast<long>(N) + rows_per_iter - 1) / rows_per_iter;
-    // Enough waves to keep ~8 per CU in flight on a 256-CU part, but give each
-    // wave several rows so the activation load is amortised.
-    long waves = wave_iters < kGemvTargetWaves ? wave_iters : kGemvTargetWaves;
-    if (waves < 1) waves = 1;
-    const int blocks = static_cast<int>((waves + 3) / 4);
     switch (upl) {
-        case 1: launch_gemv_t<F, 1>(x, W, y, N, units, row_bytes, lpr_log2, blocks, stream); break;
-        case 2: launch_gemv_t<F, 2>(x, W, y, N, units, row_bytes, lpr_log2, blocks, stream); break;
+        case 1: launch_gemv_t<F, 1, F::kPref1>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
+        case 2: launch_gemv_t<F, 2, 2>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
         case 3:
-        case 4: launch_gemv_t<F, 4>(x, W, y, N, units, row_bytes, lpr_log2, blocks, stream); break;
+        case 4: launch_gemv_t<F, 4, 1>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
         default: return -1;
     }
     return 0;

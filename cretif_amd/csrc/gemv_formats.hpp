@@ -25,10 +25,11 @@ namespace dev {
 // ---------------------------------------------------------------------------
 // shared helpers
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void load_x64(float (&v)[64], const float* __restrict__ x, int k0) {
+// x points at the workgroup's LDS copy of the activations.
+__device__ __forceinline__ void load_x64(float (&v)[64], const float* x, int k0) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        f32x4 t = ld_f32x4(x + k0 + 4 * i);
+        f32x4 t = *reinterpret_cast<const f32x4*>(x + k0 + 4 * i);
         v[4 * i + 0] = t.x;
         v[4 * i + 1] = t.y;
         v[4 * i + 2] = t.z;
@@ -50,6 +51,7 @@ __device__ __forceinline__ float sum_range(const float (&v)[64], int b, int n) {
 // (ref:src/kernels/dequantize.cu:307-319).
 // ---------------------------------------------------------------------------
 struct GemvQ4K {
+    static constexpr int kPref1 = 4;  // row-groups in flight per wave at UPL = 1
     static constexpr int kBlockBytes = 144;
     struct Data {
         u32x4 h;       // d, dmin, scales[0..11]
@@ -59,7 +61,7 @@ struct GemvQ4K {
         float v[64];
         float xs_lo, xs_hi;
     };
-    static __device__ __forceinline__ void load_x(Xr& r, const float* __restrict__ x, int unit) {
+    static __device__ __forceinline__ void load_x(Xr& r, const float* x, int unit) {
         load_x64(r.v, x, unit * 64);
         r.xs_lo = sum_range(r.v, 0, 32);
         r.xs_hi = sum_range(r.v, 32, 32);
@@ -122,6 +124,7 @@ struct GemvQ4K {
 // qs @36..67 (ref:src/kernels/dequantize.cu:34-48).
 // ---------------------------------------------------------------------------
 struct GemvQ8_0 {
+    static constexpr int kPref1 = 2;  // row-groups in flight per wave at UPL = 1
     static constexpr int kPairBytes = 68;
     struct Data {
         u32x4 w0, w1, w2, w3;
@@ -130,7 +133,7 @@ struct GemvQ8_0 {
     struct Xr {
         float v[64];
     };
-    static __device__ __forceinline__ void load_x(Xr& r, const float* __restrict__ x, int unit) {
+    static __device__ __forceinline__ void load_x(Xr& r, const float* x, int unit) {
         load_x64(r.v, x, unit * 64);
     }
     static __device__ __forceinline__ void load(Data& d, const uint8_t* __restrict__ row, int unit) {
@@ -163,6 +166,7 @@ struct GemvQ8_0 {
 // Block A: d @0, qs @2..17; block B: d @18, qs @20..35.
 // ---------------------------------------------------------------------------
 struct GemvQ4_0 {
+    static constexpr int kPref1 = 4;  // row-groups in flight per wave at UPL = 1
     static constexpr int kPairBytes = 36;
     struct Data {
         u32x4 w0, w1;
@@ -172,7 +176,7 @@ struct GemvQ4_0 {
         float v[64];
         float xs_a, xs_b;
     };
-    static __device__ __forceinline__ void load_x(Xr& r, const float* __restrict__ x, int unit) {
+    static __device__ __forceinline__ void load_x(Xr& r, const float* x, int unit) {
         load_x64(r.v, x, unit * 64);
         r.xs_a = sum_range(r.v, 0, 32);
         r.xs_b = sum_range(r.v, 32, 32);
@@ -227,6 +231,7 @@ struct GemvQ4_0 {
 // nibble for i < 16), high bit = bit i of qh (ref:src/kernels/dequantize.cu:140-164).
 // ---------------------------------------------------------------------------
 struct GemvQ5_0 {
+    static constexpr int kPref1 = 4;  // row-groups in flight per wave at UPL = 1
     static constexpr int kPairBytes = 44;
     struct Data {
         u32x4 w0, w1;
@@ -236,7 +241,7 @@ struct GemvQ5_0 {
         float v[64];
         float xs_a, xs_b;
     };
-    static __device__ __forceinline__ void load_x(Xr& r, const float* __restrict__ x, int unit) {
+    static __device__ __forceinline__ void load_x(Xr& r, const float* x, int unit) {
         load_x64(r.v, x, unit * 64);
         r.xs_a = sum_range(r.v, 0, 32);
         r.xs_b = sum_range(r.v, 32, 32);
@@ -288,6 +293,7 @@ struct GemvQ5_0 {
 // read through dword-aligned windows and funnel-shifted into place.
 // ---------------------------------------------------------------------------
 struct GemvQ6K {
+    static constexpr int kPref1 = 3;  // row-groups in flight per wave at UPL = 1
     static constexpr int kBlockBytes = 210;
     struct Data {
         uint32_t a[5], b[5], h[5];  // aligned windows of ql lo-run, ql hi-run, qh
@@ -299,14 +305,14 @@ struct GemvQ6K {
         float v[64];  // v[16q + i] = x[256j + 128c + 32q + 16h + i]
         float xs[4];
     };
-    static __device__ __forceinline__ void load_x(Xr& r, const float* __restrict__ x, int unit) {
+    static __device__ __forceinline__ void load_x(Xr& r, const float* x, int unit) {
         const int j = unit >> 2, c = (unit >> 1) & 1, h = unit & 1;
         const int k0 = 256 * j + 128 * c + 16 * h;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                f32x4 t = ld_f32x4(x + k0 + 32 * q + 4 * i);
+                f32x4 t = *reinterpret_cast<const f32x4*>(x + k0 + 32 * q + 4 * i);
                 r.v[16 * q + 4 * i + 0] = t.x;
                 r.v[16 * q + 4 * i + 1] = t.y;
                 r.v[16 * q + 4 * i + 2] = t.z;
@@ -371,13 +377,14 @@ struct GemvQ6K {
 // FP16 weights: unit = 64 halves (128 bytes); fma(fpext(half), x, acc).
 // ---------------------------------------------------------------------------
 struct GemvF16 {
+    static constexpr int kPref1 = 2;  // row-groups in flight per wave at UPL = 1
     struct Data {
         u32x4 w[8];
     };
     struct Xr {
         float v[64];
     };
-    static __device__ __forceinline__ void load_x(Xr& r, const float* __restrict__ x, int unit) {
+    static __device__ __forceinline__ void load_x(Xr& r, const float* x, int unit) {
         load_x64(r.v, x, unit * 64);
     }
     static __device__ __forceinline__ void load(Data& d, const uint8_t* __restrict__ row, int unit) {
@@ -404,13 +411,14 @@ struct GemvF16 {
 // FP32 weights (transposed-B GEMV): unit = 64 floats (256 bytes).
 // ---------------------------------------------------------------------------
 struct GemvF32 {
+    static constexpr int kPref1 = 2;  // row-groups in flight per wave at UPL = 1
     struct Data {
         f32x4 w[16];
     };
     struct Xr {
         float v[64];
     };
-    static __device__ __forceinline__ void load_x(Xr& r, const float* __restrict__ x, int unit) {
+    static __device__ __forceinline__ void load_x(Xr& r, const float* x, int unit) {
         load_x64(r.v, x, unit * 64);
     }
     static __device__ __forceinline__ void load(Data& d, const uint8_t* __restrict__ row, int unit) {

@@ -43,6 +43,10 @@ constexpr long kGemvTargetWaves = 2048;
 bool gemv_supported(int fmt, int K, const void* W);
 int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream);
 
+// 1 <= M <= 16 fused dequant matmul on the matrix cores (mfma_skinny.hip)
+bool skinny_supported(int fmt, int M, int K, const void* B);
+int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+
 // any-M fused dequant matmul, element-wise decode (generic.hip)
 int launch_generic_matmul(int fmt, const float* A, const void* B, float* C, int M, int N, int K,
                           hipStream_t stream);

@@ -1,0 +1,348 @@
+// mfma_skinny.hip -- fused dequant GEMV / skinny GEMM on the matrix cores,
+// C[M,N] = A[M,K] * dequant(B[N,K])^T for 1 <= M <= 16 (decode batch sizes).
+//
+// Q4_K (ref:src/kernels/matmul_quant.cu:309-386 computes the same product on
+// fp32 FMA units).  gfx950 v_mfma_f32_16x16x32_f16 multiplies a 16(m) x 32(k)
+// activation tile by a 32(k) x 16(n) weight tile:
+//   * weights are the B operand as exact fp16 integers sc*q (6-bit scale times
+//     4-bit code <= 945), unpacked from the nibbles with one and-or (the
+//     1024 + q fp16 bit pattern) and one packed fma per two weights; the
+//     super-block scale d (and the row's activation scale) is applied to the
+//     fp32 accumulator once per 256 k;
+//   * activations are the A operand, split x = hi + lo into two fp16 parts
+//     (after a per-row power-of-two scaling that keeps hi < 2^15), so two
+//     MFMAs reproduce fp32-accurate products;
+//   * the -dmin * mn offsets become one 16x16x16 MFMA per super-block between
+//     the 6-bit mins and the per-sub-block activation sums (hi + lo, staged
+//     times 2^-6 so that 32 values below 2^15 cannot overflow fp16);
+// so the VALU only unpacks nibbles, and only the lanes that carry real rows
+// (m < M) read activations from LDS.  Each 16-row weight tile is split over
+// the waves of a workgroup by super-block and reduced through LDS at the end.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace cri {
+namespace dev {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kSkNW = 4;  // waves per workgroup
+
+// Order of the 8 k values of one k8 group inside an operand register set: the
+// nibble unpack produces (0,2), (1,3), (4,6), (5,7) pairs.
+__device__ constexpr int kPerm8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+
+// (v & m) | o as one v_and_or_b32: gfx950 VOP3 takes no literal constants, so
+// the mask comes from an SGPR and the or-constant from a VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(m), "v"(o));
+    return r;
+}
+
+__device__ __forceinline__ uint32_t pk_fma_f16(uint32_t a, uint32_t b, uint32_t c) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    h2 r = __builtin_elementwise_fma(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), __builtin_bit_cast(h2, c));
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ uint32_t f16x2_splat(float v) {
+    const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+    return static_cast<uint32_t>(h) | (static_cast<uint32_t>(h) << 16);
+}
+
+struct SkLds {
+    // byte offsets inside the dynamic LDS block
+    int xh, xl, xs, red, scl;
+    int bytes;
+};
+
+__device__ __host__ inline SkLds sk_layout(int M, int KC, int nw) {
+    SkLds L;
+    int o = 0;
+    L.xh = o; o += M * KC * 2;
+    L.xl = o; o += M * KC * 2;
+    L.xs = o; o += M * (KC / 64) * 8;  // per (m, sub-block pair): Xhi, Xhi, Xlo, Xlo
+    L.scl = o; o += 16 * 4 * 2;        // per m: max |x| bits, unscale
+    L.red = o; o += nw * 4 * 64 * 4;   // cross-wave reduction of k-split partials
+    L.bytes = o;
+    return L;
+}
+
+// Stage activations A[m][k0 .. k0+KC) (rows m < M) into LDS as fp16 hi/lo in
+// the operand order, after a per-row power-of-two scaling that puts max |x|
+// just under 2^15, plus per-sub-block sums (times 2^-6) for the mins.
+// Two barriers: one for the row maxima, one for the converted data.
+__device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int KC, char* lds, const SkLds& L) {
+    const int tid = threadIdx.x, nth = blockDim.x;
+    _Float16* xh = reinterpret_cast<_Float16*>(lds + L.xh);
+    _Float16* xl = reinterpret_cast<_Float16*>(lds + L.xl);
+    _Float16* xs = reinterpret_cast<_Float16*>(lds + L.xs);
+    uint32_t* mx = reinterpret_cast<uint32_t*>(lds + L.scl);
+    float* unscale = reinterpret_cast<float*>(lds + L.scl + 64);
+    const int groups = KC / 8;  // k8 groups per row; a multiple of 32
+    const int total = M * groups;
+    // 1. row maxima: wave-level DPP max of each k8 group's max, then one LDS atomic per row and wave
+    if (tid < 16) mx[tid] = 0u;
+    __syncthreads();
+    for (int e0 = 0; e0 < total; e0 += nth) {
+        const int e = e0 + tid;
+        float v = 0.0f;
+        int m = 0;
+        if (e < total) {
+            m = e / groups;
+            const float* src = A + static_cast<long>(m) * K + k0 + 8 * (e - m * groups);
+            const f32x4 a = ld_f32x4(src), b = ld_f32x4(src + 4);
+            v = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                      fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+            atomicMax(&mx[m], __builtin_bit_cast(uint32_t, v));
+        }
+    }
+    __syncthreads();
+    // 2. convert; four consecutive k8 groups (consecutive lanes) form a sub-block
+    for (int e0 = 0; e0 < total; e0 += nth) {
+        const int e = e0 + tid;
+        const bool live = e < total;
+        const int m = live ? e / groups : 0, g8 = live ? e - m * groups : 0;
+        const float mxv = __builtin_bit_cast(float, mx[m]);
+        int ex = 0;
+        if (mxv > 0.0f) {
+            frexpf(mxv, &ex);
+            ex -= 15;
+            ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
+        }
+        const float s = ldexpf(1.0f, -ex);
+        float sum = 0.0f;
+        if (live) {
+            const float* src = A + static_cast<long>(m) * K + k0 + 8 * g8;
+            const f32x4 a = ld_f32x4(src), b = ld_f32x4(src + 4);
+            const float v[8] = {a.x * s, a.y * s, a.z * s, a.w * s, b.x * s, b.y * s, b.z * s, b.w * s};
+            half8 hi, lo;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x = v[kPerm8[i]];
+                const _Float16 h = static_cast<_Float16>(x);
+                hi[i] = h;
+                lo[i] = static_cast<_Float16>(x - static_cast<float>(h));
+            }
+            *reinterpret_cast<half8*>(xh + m * KC + 8 * g8) = hi;
+            *reinterpret_cast<half8*>(xl + m * KC + 8 * g8) = lo;
+            sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+            if (g8 == 0) unscale[m] = ldexpf(1.0f, ex);
+        }
+        // sub-block sum over the quad (fixed order -> deterministic), pair via row_shl:4
+        sum = sum + dpp<kQuadPerm1032>(sum);
+        sum = sum + dpp<kQuadPerm2301>(sum);
+        const float next = dpp<0x104>(sum);  // row_shl:4: the quad above (sub-block 2p+1)
+        if (live && (g8 & 7) == 0) {
+            const float s0 = sum * 0.015625f, s1 = next * 0.015625f;  // 2^-6 keeps 32 * 2^15 in range
+            const _Float16 h0 = static_cast<_Float16>(s0), h1 = static_cast<_Float16>(s1);
+            half4 q;
+            q[0] = h0;
+            q[1] = h1;
+            q[2] = static_cast<_Float16>(s0 - static_cast<float>(h0));
+            q[3] = static_cast<_Float16>(s1 - static_cast<float>(h1));
+            *reinterpret_cast<half4*>(xs + 4 * (m * (KC / 64) + (g8 >> 3))) = q;
+        }
+    }
+    __syncthreads();
+}
+
+// One Q4_K super-block of a 16-row tile, computed by one wave.
+struct Q4KItem {
+    u32x4 h, q0, q1;
+};
+
+// acc contribution of one super-block: lane (g = k slice, n) holds the row's
+// 32 qs bytes of chunk g (sub-blocks 2g, 2g+1) and the 16-byte header; lanes
+// with m < M supply their row's activations from LDS (xa points at
+// row m, super-block start + 64 g).
+__device__ __forceinline__ f4 q4k_block(const Q4KItem& d, const _Float16* xha, const _Float16* xla,
+                                        const _Float16* xsa, bool has_row, int g, const float (&us)[4]) {
+    // 6-bit scale / min of sub-blocks 2g, 2g+1 (ref:src/kernels/dequantize.cu:298-305)
+    const bool low = g < 2;
+    const uint32_t o = (g & 1) * 16;
+    const uint32_t h1 = d.h.y, h2 = d.h.z, h3 = d.h.w;
+    const uint32_t a_sc = low ? h1 : h3, a_mn = low ? h2 : h3;
+    const uint32_t wa = low ? 6 : 4, wb = low ? 0 : 2, om = low ? 0 : 4;
+    const uint32_t sc_lo = ubfe(a_sc, o, wa) | (ubfe(h1, o + 6, wb) << 4);
+    const uint32_t mn_lo = ubfe(a_mn, o + om, wa) | (ubfe(h2, o + 6, wb) << 4);
+    const uint32_t sc_hi = ubfe(a_sc, o + 8, wa) | (ubfe(h1, o + 14, wb) << 4);
+    const uint32_t mn_hi = ubfe(a_mn, o + 8 + om, wa) | (ubfe(h2, o + 14, wb) << 4);
+    // (1024 + q) * sc - 1024 * sc = q * sc exactly (q * sc <= 945); high nibbles
+    // come out as 1024 + 16 q and use sc / 16
+    const float fsl = static_cast<float>(sc_lo), fsh = static_cast<float>(sc_hi);
+    const uint32_t mul_lo = f16x2_splat(fsl), add_lo = f16x2_splat(-1024.0f * fsl);
+    const uint32_t mul_hi = f16x2_splat(fsh * 0.0625f), add_hi = f16x2_splat(-64.0f * fsh);
+    const uint32_t q[8] = {d.q0.x, d.q0.y, d.q0.z, d.q0.w, d.q1.x, d.q1.y, d.q1.z, d.q1.w};
+    const half8 zero8 = half8{0, 0, 0, 0, 0, 0, 0, 0};
+    f4 P = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        half8 ah = zero8, al = zero8;
+        if (has_row) {  // only lanes carrying real activation rows read LDS
+            ah = *reinterpret_cast<const half8*>(xha + 8 * s);
+            al = *reinterpret_cast<const half8*>(xla + 8 * s);
+        }
+        const uint32_t w0 = q[2 * (s & 3)], w1 = q[2 * (s & 3) + 1];
+        const uint32_t m4 = s < 4 ? 0x000F000Fu : 0x00F000F0u;
+        const uint32_t mul = s < 4 ? mul_lo : mul_hi, add = s < 4 ? add_lo : add_hi;
+        typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+        const u4 b = u4{pk_fma_f16(and_or(w0, m4, 0x64006400u), mul, add),
+                        pk_fma_f16(and_or(w0 >> 8, m4, 0x64006400u), mul, add),
+                        pk_fma_f16(and_or(w1, m4, 0x64006400u), mul, add),
+                        pk_fma_f16(and_or(w1 >> 8, m4, 0x64006400u), mul, add)};
+        const half8 bw = __builtin_bit_cast(half8, b);
+        P = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, P, 0, 0, 0);
+        P = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, P, 0, 0, 0);
+    }
+    // mins: sum over sub-blocks of mn * X on a 16x16x16 MFMA, slots (Xhi, Xhi, Xlo, Xlo)
+    half4 as4 = half4{0, 0, 0, 0};
+    if (has_row) as4 = *reinterpret_cast<const half4*>(xsa);
+    const uint32_t mnp = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(mn_lo))) |
+                         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(mn_hi))) << 16);
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    const half4 bm = __builtin_bit_cast(half4, u2{mnp, mnp});
+    const f4 Pm = __builtin_amdgcn_mfma_f32_16x16x16f16(as4, bm, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    const float dd = h_lo(d.h.x), dmin = h_hi(d.h.x) * 64.0f;  // sums were staged times 2^-6
+    f4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = us[i] * (dd * P[i] - dmin * Pm[i]);
+    return r;
+}
+
+// Workgroup = NW waves = (NW / KS) tiles x KS k-splits.  The grid strides
+// over groups of NW / KS tiles; wave w works on tile w / KS of the group and
+// on super-blocks j = w % KS, + KS, ... of the current activation chunk.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void skinny_q4k_kernel(const float* __restrict__ A, const uint8_t* __restrict__ B,
+                                                             float* __restrict__ C, int M, int N, int K, int KC, int KS,
+                                                             long rbytes) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const SkLds L = sk_layout(M, KC, NW);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, nl = lane & 15;
+    const int m_a = lane & 15;  // row of the A operand this lane supplies
+    const bool has_row = m_a < M;
+    const int TW = NW / KS;     // tiles per group
+    const int my_tile = wave / KS, my_split = wave - (wave / KS) * KS;
+    const int ntiles = (N + 15) >> 4;
+    const int ngroups = (ntiles + TW - 1) / TW;
+    const _Float16* xh = reinterpret_cast<const _Float16*>(lds + L.xh);
+    const _Float16* xl = reinterpret_cast<const _Float16*>(lds + L.xl);
+    const _Float16* xs = reinterpret_cast<const _Float16*>(lds + L.xs);
+    const float* unscale = reinterpret_cast<const float*>(lds + L.scl + 64);
+    float* red = reinterpret_cast<float*>(lds + L.red);
+    const int sb_chunk = KC / 256;
+    const int nchunks = K / KC;
+    const int nitems = (sb_chunk - my_split + KS - 1) / KS;  // super-blocks per wave per chunk
+
+    for (int grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {
+        const int tile = grp * TW + my_tile;
+        int row = tile * 16 + nl;
+        row = row < N ? row : N - 1;
+        const uint8_t* rowp = B + static_cast<long>(row) * rbytes;
+        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < nchunks; ++c) {
+            const int k0 = c * KC;
+            const uint8_t* cp = rowp + static_cast<long>(k0 / 256 + my_split) * 144;
+            auto load_item = [&](Q4KItem& d, int it) {
+                const uint8_t* p = cp + static_cast<long>(it) * KS * 144;
+                d.h = ld_u32x4_a16(p);
+                d.q0 = ld_u32x4_a16(p + 16 + 32 * g);
+                d.q1 = ld_u32x4_a16(p + 32 + 32 * g);
+            };
+            // the first two super-blocks are requested before the activations are staged
+            Q4KItem b0, b1;
+            if (nitems > 0) load_item(b0, 0);
+            if (nitems > 1) load_item(b1, 1);
+            if (grp == static_cast<int>(blockIdx.x) || nchunks > 1) sk_stage(A, M, K, k0, KC, lds, L);
+            float us[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 4 * g + r;
+                us[r] = m < M ? unscale[m] : 0.0f;
+            }
+            auto run_item = [&](const Q4KItem& d, int it) {
+                const int jj = my_split + it * KS;
+                const int base = m_a * KC + jj * 256 + 64 * g;
+                acc += q4k_block(d, xh + base, xl + base, xs + 4 * (m_a * (KC / 64) + jj * 4 + g), has_row, g, us);
+            };
+            for (int it = 0; it < nitems; it += 2) {
+                run_item(b0, it);
+                if (it + 2 < nitems) load_item(b0, it + 2);
+                if (it + 1 >= nitems) break;
+                run_item(b1, it + 1);
+                if (it + 3 < nitems) load_item(b1, it + 3);
+            }
+            if (nchunks > 1) __syncthreads();  // the next chunk overwrites the staged activations
+        }
+        // reduce the KS k-split partials of each tile: red[w][r][lane]
+        if (KS == 1) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 4 * g + r, n = tile * 16 + nl;
+                if (m < M && n < N && tile < ntiles) C[static_cast<long>(m) * N + n] = acc[r];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[(wave * 4 + r) * 64 + lane] = acc[r];
+            __syncthreads();
+            // threads of wave w finish tile w / KS, register r = (w % KS) ... spread 4 regs x 64 lanes per tile
+            for (int e = threadIdx.x; e < TW * 256; e += 64 * NW) {
+                const int t = e >> 8, r = (e >> 6) & 3, ln = e & 63;
+                float sum = 0.0f;
+                for (int sp = 0; sp < KS; ++sp) sum += red[((t * KS + sp) * 4 + r) * 64 + ln];
+                const int tt = grp * TW + t;
+                const int m = 4 * (ln >> 4) + r, n = tt * 16 + (ln & 15);
+                if (m < M && n < N && tt < ntiles) C[static_cast<long>(m) * N + n] = sum;
+            }
+            __syncthreads();
+        }
+    }
+}
+
+}  // namespace dev
+
+namespace detail {
+
+bool skinny_supported(int fmt, int M, int K, const void* B) {
+    if (fmt != kFmtQ4_K) return false;
+    if (M < 1 || M > 16 || K % 256 != 0) return false;
+    return (reinterpret_cast<uintptr_t>(B) & 15u) == 0;  // 16-byte loads of 144-byte blocks
+}
+
+template <int NW>
+static void launch_sk(const float* A, const void* B, float* C, int M, int N, int K, int KC, int KS, hipStream_t stream) {
+    const int ntiles = (N + 15) / 16;
+    const int TW = NW / KS;
+    const int groups = (ntiles + TW - 1) / TW;
+    // enough workgroups for ~2048 waves; beyond that each workgroup strides over tile groups
+    int blocks = groups < 2048 / NW ? groups : 2048 / NW;
+    if (blocks < 1) blocks = 1;
+    const dev::SkLds L = dev::sk_layout(M, KC, NW);
+    hipLaunchKernelGGL(dev::skinny_q4k_kernel<NW>, dim3(blocks), dim3(64 * NW), L.bytes, stream, A,
+                       static_cast<const uint8_t*>(B), C, M, N, K, KC, KS, static_cast<long>(K / 256) * 144);
+}
+
+int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream) {
+    (void)fmt;
+    // activation chunk: the largest multiple of 256 dividing K whose fp16 hi/lo copy fits in 48 KB
+    int KC = (12288 / M) / 256 * 256;
+    if (KC > K) KC = K;
+    while (KC > 256 && K % KC != 0) KC -= 256;
+    if (KC < 256 || K % KC != 0) return -1;
+    const int ntiles = (N + 15) / 16;
+    const int sb = KC / 256;  // super-blocks per chunk
+    // split K over the waves of a workgroup when there are too few tiles for ~2048 waves
+    int KS = 1;
+    while (KS < 8 && KS * 2 <= sb && static_cast<long>(ntiles) * KS < 2048) KS *= 2;
+    if (KS >= 8) launch_sk<8>(A, B, C, M, N, K, KC, KS, stream);
+    else launch_sk<4>(A, B, C, M, N, K, KC, KS, stream);
+    return 0;
+}
+
+}  // namespace detail
+}  // namespace cri
