@@ -10,8 +10,8 @@
 //     super-block scale d (and the row's activation scale) is applied to the
 //     fp32 accumulator once per 256 k;
 //   * activations are the A operand, split x = hi + lo into two fp16 parts
-//     (after a per-row power-of-two scaling that keeps hi < 2^15), so two
-//     MFMAs reproduce fp32-accurate products;
+//     (after a power-of-two scaling per row and super-block that keeps
+//     hi < 2^15), so two MFMAs reproduce fp32-accurate products;
 //   * the -dmin * mn offsets become one 16x16x16 MFMA per super-block between
 //     the 6-bit mins and the per-sub-block activation sums (hi + lo, staged
 //     times 2^-6 so that 32 values below 2^15 cannot overflow fp16);
@@ -65,60 +65,56 @@ __device__ __host__ inline SkLds sk_layout(int M, int KC, int nw) {
     L.xh = o; o += M * KC * 2;
     L.xl = o; o += M * KC * 2;
     L.xs = o; o += M * (KC / 64) * 8;  // per (m, sub-block pair): Xhi, Xhi, Xlo, Xlo
-    L.scl = o; o += 16 * 4 * 2;        // per m: max |x| bits, unscale
+    L.scl = o; o += (KC / 256) * 16 * 4;  // unscale[super-block][m] (16 m slots, zero beyond M)
     L.red = o; o += nw * 4 * 64 * 4;   // cross-wave reduction of k-split partials
     L.bytes = o;
     return L;
 }
 
 // Stage activations A[m][k0 .. k0+KC) (rows m < M) into LDS as fp16 hi/lo in
-// the operand order, after a per-row power-of-two scaling that puts max |x|
-// just under 2^15, plus per-sub-block sums (times 2^-6) for the mins.
-// Two barriers: one for the row maxima, one for the converted data.
+// the operand order.  Each (row, super-block) of 256 activations gets its own
+// power-of-two scale that puts its max |x| just under 2^15 (the product of a
+// super-block is rescaled anyway); the 32 k8 groups of one super-block sit in
+// one half-wave, so the max is a DPP/swizzle reduction and needs no barrier.
+// Per-sub-block sums (times 2^-6) feed the mins MFMA.  One barrier.
 __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int KC, char* lds, const SkLds& L) {
     const int tid = threadIdx.x, nth = blockDim.x;
     _Float16* xh = reinterpret_cast<_Float16*>(lds + L.xh);
     _Float16* xl = reinterpret_cast<_Float16*>(lds + L.xl);
     _Float16* xs = reinterpret_cast<_Float16*>(lds + L.xs);
-    uint32_t* mx = reinterpret_cast<uint32_t*>(lds + L.scl);
-    float* unscale = reinterpret_cast<float*>(lds + L.scl + 64);
+    float* unscale = reinterpret_cast<float*>(lds + L.scl);
     const int groups = KC / 8;  // k8 groups per row; a multiple of 32
-    const int total = M * groups;
-    // 1. row maxima: wave-level DPP max of each k8 group's max, then one LDS atomic per row and wave
-    if (tid < 16) mx[tid] = 0u;
-    __syncthreads();
-    for (int e0 = 0; e0 < total; e0 += nth) {
-        const int e = e0 + tid;
-        float v = 0.0f;
-        int m = 0;
-        if (e < total) {
-            m = e / groups;
-            const float* src = A + static_cast<long>(m) * K + k0 + 8 * (e - m * groups);
-            const f32x4 a = ld_f32x4(src), b = ld_f32x4(src + 4);
-            v = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                      fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
-            atomicMax(&mx[m], __builtin_bit_cast(uint32_t, v));
+    const int nsb = KC / 256;
+    // slots of rows m >= M (never written below) read as 0
+    for (int e = tid; e < nsb * 16; e += nth)
+        if ((e & 15) >= M) unscale[e] = 0.0f;
+    for (int m = 0; m < M; ++m)
+    for (int g0 = 0; g0 < groups; g0 += nth) {  // nth is a multiple of 64: half-waves stay aligned
+        const int g8 = g0 + tid;
+        const bool live = g8 < groups;
+        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = a;
+        if (live) {
+            const float* src = A + static_cast<long>(m) * K + k0 + 8 * g8;
+            a = ld_f32x4(src);
+            b = ld_f32x4(src + 4);
         }
-    }
-    __syncthreads();
-    // 2. convert; four consecutive k8 groups (consecutive lanes) form a sub-block
-    for (int e0 = 0; e0 < total; e0 += nth) {
-        const int e = e0 + tid;
-        const bool live = e < total;
-        const int m = live ? e / groups : 0, g8 = live ? e - m * groups : 0;
-        const float mxv = __builtin_bit_cast(float, mx[m]);
+        float mx = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                         fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+        mx = fmaxf(mx, dpp<kQuadPerm1032>(mx));
+        mx = fmaxf(mx, dpp<kQuadPerm2301>(mx));
+        mx = fmaxf(mx, dpp<kRowHalfMirror>(mx));
+        mx = fmaxf(mx, dpp<kRowMirror>(mx));
+        mx = fmaxf(mx, swizzle_xor16(mx));  // max over the 32 lanes = one super-block
         int ex = 0;
-        if (mxv > 0.0f) {
-            frexpf(mxv, &ex);
+        if (mx > 0.0f) {
+            frexpf(mx, &ex);
             ex -= 15;
             ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
         }
         const float s = ldexpf(1.0f, -ex);
-        float sum = 0.0f;
+        const float v[8] = {a.x * s, a.y * s, a.z * s, a.w * s, b.x * s, b.y * s, b.z * s, b.w * s};
+        float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
         if (live) {
-            const float* src = A + static_cast<long>(m) * K + k0 + 8 * g8;
-            const f32x4 a = ld_f32x4(src), b = ld_f32x4(src + 4);
-            const float v[8] = {a.x * s, a.y * s, a.z * s, a.w * s, b.x * s, b.y * s, b.z * s, b.w * s};
             half8 hi, lo;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -129,8 +125,7 @@ __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int 
             }
             *reinterpret_cast<half8*>(xh + m * KC + 8 * g8) = hi;
             *reinterpret_cast<half8*>(xl + m * KC + 8 * g8) = lo;
-            sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-            if (g8 == 0) unscale[m] = ldexpf(1.0f, ex);
+            if ((g8 & 31) == 0) unscale[(g8 >> 5) * 16 + m] = ldexpf(1.0f, ex);
         }
         // sub-block sum over the quad (fixed order -> deterministic), pair via row_shl:4
         sum = sum + dpp<kQuadPerm1032>(sum);
@@ -178,14 +173,21 @@ __device__ __forceinline__ f4 q4k_block(const Q4KItem& d, const _Float16* xha, c
     const uint32_t mul_hi = f16x2_splat(fsh * 0.0625f), add_hi = f16x2_splat(-64.0f * fsh);
     const uint32_t q[8] = {d.q0.x, d.q0.y, d.q0.z, d.q0.w, d.q1.x, d.q1.y, d.q1.z, d.q1.w};
     const half8 zero8 = half8{0, 0, 0, 0, 0, 0, 0, 0};
-    f4 P = f4{0.f, 0.f, 0.f, 0.f};
+    half8 ah[8], al[8];
+    half4 as4 = half4{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) ah[s] = al[s] = zero8;
+    if (has_row) {  // only lanes carrying real activation rows read LDS; one batch per item
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            ah[s] = *reinterpret_cast<const half8*>(xha + 8 * s);
+            al[s] = *reinterpret_cast<const half8*>(xla + 8 * s);
+        }
+        as4 = *reinterpret_cast<const half4*>(xsa);
+    }
+    f4 Ph = f4{0.f, 0.f, 0.f, 0.f}, Pl = Ph;  // two independent MFMA chains
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        half8 ah = zero8, al = zero8;
-        if (has_row) {  // only lanes carrying real activation rows read LDS
-            ah = *reinterpret_cast<const half8*>(xha + 8 * s);
-            al = *reinterpret_cast<const half8*>(xla + 8 * s);
-        }
         const uint32_t w0 = q[2 * (s & 3)], w1 = q[2 * (s & 3) + 1];
         const uint32_t m4 = s < 4 ? 0x000F000Fu : 0x00F000F0u;
         const uint32_t mul = s < 4 ? mul_lo : mul_hi, add = s < 4 ? add_lo : add_hi;
@@ -195,12 +197,11 @@ __device__ __forceinline__ f4 q4k_block(const Q4KItem& d, const _Float16* xha, c
                         pk_fma_f16(and_or(w1, m4, 0x64006400u), mul, add),
                         pk_fma_f16(and_or(w1 >> 8, m4, 0x64006400u), mul, add)};
         const half8 bw = __builtin_bit_cast(half8, b);
-        P = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, P, 0, 0, 0);
-        P = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, P, 0, 0, 0);
+        Ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bw, Ph, 0, 0, 0);
+        Pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s], bw, Pl, 0, 0, 0);
     }
+    const f4 P = Ph + Pl;
     // mins: sum over sub-blocks of mn * X on a 16x16x16 MFMA, slots (Xhi, Xhi, Xlo, Xlo)
-    half4 as4 = half4{0, 0, 0, 0};
-    if (has_row) as4 = *reinterpret_cast<const half4*>(xsa);
     const uint32_t mnp = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(mn_lo))) |
                          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(mn_hi))) << 16);
     typedef uint32_t u2 __attribute__((ext_vector_type(2)));
@@ -218,26 +219,26 @@ __device__ __forceinline__ f4 q4k_block(const Q4KItem& d, const _Float16* xha, c
 // on super-blocks j = w % KS, + KS, ... of the current activation chunk.
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void skinny_q4k_kernel(const float* __restrict__ A, const uint8_t* __restrict__ B,
-                                                             float* __restrict__ C, int M, int N, int K, int KC, int KS,
-                                                             long rbytes) {
+                                                             float* __restrict__ C, int M, int N, int K, int KC,
+                                                             int ks_log2, int ngroups, int nchunks) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const SkLds L = sk_layout(M, KC, NW);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, nl = lane & 15;
     const int m_a = lane & 15;  // row of the A operand this lane supplies
     const bool has_row = m_a < M;
-    const int TW = NW / KS;     // tiles per group
-    const int my_tile = wave / KS, my_split = wave - (wave / KS) * KS;
+    const int KS = 1 << ks_log2;              // k-splits per tile (power of two)
+    const int TW = NW >> ks_log2;             // tiles per group
+    const int my_tile = wave >> ks_log2, my_split = wave & (KS - 1);
     const int ntiles = (N + 15) >> 4;
-    const int ngroups = (ntiles + TW - 1) / TW;
+    const long rbytes = static_cast<long>(K >> 8) * 144;
     const _Float16* xh = reinterpret_cast<const _Float16*>(lds + L.xh);
     const _Float16* xl = reinterpret_cast<const _Float16*>(lds + L.xl);
     const _Float16* xs = reinterpret_cast<const _Float16*>(lds + L.xs);
-    const float* unscale = reinterpret_cast<const float*>(lds + L.scl + 64);
+    const float* unscale = reinterpret_cast<const float*>(lds + L.scl);
     float* red = reinterpret_cast<float*>(lds + L.red);
     const int sb_chunk = KC / 256;
-    const int nchunks = K / KC;
-    const int nitems = (sb_chunk - my_split + KS - 1) / KS;  // super-blocks per wave per chunk
+    const int nitems = (sb_chunk - my_split + KS - 1) >> ks_log2;  // super-blocks per wave per chunk
 
     for (int grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {
         const int tile = grp * TW + my_tile;
@@ -247,9 +248,9 @@ __global__ __launch_bounds__(64 * NW) void skinny_q4k_kernel(const float* __rest
         f4 acc = f4{0.f, 0.f, 0.f, 0.f};
         for (int c = 0; c < nchunks; ++c) {
             const int k0 = c * KC;
-            const uint8_t* cp = rowp + static_cast<long>(k0 / 256 + my_split) * 144;
+            const uint8_t* cp = rowp + static_cast<long>((k0 >> 8) + my_split) * 144;
             auto load_item = [&](Q4KItem& d, int it) {
-                const uint8_t* p = cp + static_cast<long>(it) * KS * 144;
+                const uint8_t* p = cp + static_cast<long>(it << ks_log2) * 144;
                 d.h = ld_u32x4_a16(p);
                 d.q0 = ld_u32x4_a16(p + 16 + 32 * g);
                 d.q1 = ld_u32x4_a16(p + 32 + 32 * g);
@@ -259,15 +260,11 @@ __global__ __launch_bounds__(64 * NW) void skinny_q4k_kernel(const float* __rest
             if (nitems > 0) load_item(b0, 0);
             if (nitems > 1) load_item(b1, 1);
             if (grp == static_cast<int>(blockIdx.x) || nchunks > 1) sk_stage(A, M, K, k0, KC, lds, L);
-            float us[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = 4 * g + r;
-                us[r] = m < M ? unscale[m] : 0.0f;
-            }
             auto run_item = [&](const Q4KItem& d, int it) {
-                const int jj = my_split + it * KS;
+                const int jj = my_split + (it << ks_log2);
                 const int base = m_a * KC + jj * 256 + 64 * g;
+                const f32x4 u4 = *reinterpret_cast<const f32x4*>(unscale + jj * 16 + 4 * g);  // rows 4g .. 4g+3
+                const float us[4] = {u4.x, u4.y, u4.z, u4.w};
                 acc += q4k_block(d, xh + base, xl + base, xs + 4 * (m_a * (KC / 64) + jj * 4 + g), has_row, g, us);
             };
             for (int it = 0; it < nitems; it += 2) {
@@ -294,7 +291,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_q4k_kernel(const float* __rest
             for (int e = threadIdx.x; e < TW * 256; e += 64 * NW) {
                 const int t = e >> 8, r = (e >> 6) & 3, ln = e & 63;
                 float sum = 0.0f;
-                for (int sp = 0; sp < KS; ++sp) sum += red[((t * KS + sp) * 4 + r) * 64 + ln];
+                for (int sp = 0; sp < KS; ++sp) sum += red[(((t << ks_log2) + sp) * 4 + r) * 64 + ln];
                 const int tt = grp * TW + t;
                 const int m = 4 * (ln >> 4) + r, n = tt * 16 + (ln & 15);
                 if (m < M && n < N && tt < ntiles) C[static_cast<long>(m) * N + n] = sum;
@@ -319,12 +316,14 @@ static void launch_sk(const float* A, const void* B, float* C, int M, int N, int
     const int ntiles = (N + 15) / 16;
     const int TW = NW / KS;
     const int groups = (ntiles + TW - 1) / TW;
+    int ks_log2 = 0;
+    while ((1 << ks_log2) < KS) ++ks_log2;
     // enough workgroups for ~2048 waves; beyond that each workgroup strides over tile groups
     int blocks = groups < 2048 / NW ? groups : 2048 / NW;
     if (blocks < 1) blocks = 1;
     const dev::SkLds L = dev::sk_layout(M, KC, NW);
     hipLaunchKernelGGL(dev::skinny_q4k_kernel<NW>, dim3(blocks), dim3(64 * NW), L.bytes, stream, A,
-                       static_cast<const uint8_t*>(B), C, M, N, K, KC, KS, static_cast<long>(K / 256) * 144);
+                       static_cast<const uint8_t*>(B), C, M, N, K, KC, ks_log2, groups, K / KC);
 }
 
 int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream) {
