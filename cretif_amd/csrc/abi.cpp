@@ -33,6 +33,10 @@ int check_launch(const char* fn) {
 
 constexpr long kMaxElems = (1L << 40);
 
+// Batches above this many rows are prefill: they run on the fp16-operand MFMA
+// GEMM (stated tolerance 1e-3); smaller batches keep fp32-accurate kernels.
+constexpr int kPrefillMinM = 16;
+
 int fill_zero(float* C, long n, hipStream_t stream, const char* fn);
 
 int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream,
@@ -57,6 +61,8 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
         rc = cri::detail::launch_skinny(fmt, A, B, C, M, N, K, stream);
     else if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv(fmt, A, B, C, N, K, stream);
+    else if (M > kPrefillMinM && cri::detail::mfma_gemm_supported(fmt, M, N, K, A, B))
+        rc = cri::detail::launch_mfma_gemm(fmt, A, B, C, M, N, K, stream);
     else
         rc = cri::detail::launch_generic_matmul(fmt, A, B, C, M, N, K, stream);
     if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");

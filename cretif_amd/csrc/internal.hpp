@@ -47,6 +47,10 @@ int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, 
 bool skinny_supported(int fmt, int M, int K, const void* B);
 int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
 
+// multi-token fused dequant GEMM on the matrix cores, fp16 operands (mfma_gemm.hip)
+bool mfma_gemm_supported(int fmt, int M, int N, int K, const void* A, const void* B);
+int launch_mfma_gemm(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+
 // any-M fused dequant matmul, element-wise decode (generic.hip)
 int launch_generic_matmul(int fmt, const float* A, const void* B, float* C, int M, int N, int K,
                           hipStream_t stream);

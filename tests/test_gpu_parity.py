@@ -3,6 +3,7 @@
 Bars (from the path's contract):
   * dequantisation: bit-exact;
   * fused matmul / GEMV in fp32 FMA: ||C - C_ref||_inf <= 1e-5 * ||C_ref||_inf;
+  * prefill (M > 16) on the fp16-operand MFMA GEMM: the same norm, 1e-3;
   * exact-integer inputs (every partial sum exact): bit-exact for every format
     and every kernel variant, whatever the summation order.
 """
@@ -18,6 +19,12 @@ from cretif_amd import quant  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 GEMV_TOL = 1e-5
+PREFILL_TOL = 1e-3   # M > 16: fp16 operands, fp32 accumulation on the matrix cores
+PREFILL_MIN_M = 17
+
+
+def tol_for(M):
+    return GEMV_TOL if M < PREFILL_MIN_M else PREFILL_TOL
 FMTS = ["q8_0", "q4_0", "q5_0", "q4_k", "q6_k", "fp16"]
 BE = {"q8_0": 32, "q4_0": 32, "q5_0": 32, "q4_k": 256, "q6_k": 256, "fp16": 1}
 
@@ -172,7 +179,7 @@ def test_matmul_small_m(orc, fmt, M, N, K):
     Bq = weights(fmt, N, K, seed=N + K)
     got = run_matmul(fmt, A, Bq, N, K)
     ref = orc.matmul_quant(fmt, A, Bq, N, K)
-    assert normwise_rel_err(got, ref) <= GEMV_TOL
+    assert normwise_rel_err(got, ref) <= tol_for(M)
 
 
 def test_reference_test_shapes(orc):
@@ -191,6 +198,99 @@ def test_reference_test_shapes(orc):
         got = run_matmul(fmt, A, Bq, N, K)
         ref = orc.matmul_quant(fmt, A, Bq, N, K)
         assert normwise_rel_err(got, ref) <= GEMV_TOL, (fmt, M, N, K)
+
+
+# ------------------------------------------------------------------ prefill (M > 16): MFMA GEMM
+PREFILL_SHAPES = [(17, 64, 256), (64, 130, 512), (128, 128, 2048), (130, 300, 768), (200, 1000, 1024),
+                  (512, 256, 2048)]
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,N,K", PREFILL_SHAPES)
+def test_prefill_matches_oracle(orc, fmt, M, N, K):
+    A = quant.randn(M * K, seed=M * 13 + K).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=N * 3 + K)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    err = normwise_rel_err(got, ref)
+    assert err <= PREFILL_TOL, err
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_k"])
+@pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192)])
+def test_prefill_baseline_config(orc, fmt, N, K):
+    # 512 tokens x Llama-3.2-1B FFN gate/up and down; the oracle checks 3 bands of 128 output columns
+    M = 512
+    A = quant.randn(M * K, seed=K).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=N)
+    got = run_matmul(fmt, A, Bq, N, K)
+    assert np.all(np.isfinite(got))
+    for n0 in (0, N // 2 - 64, N - 128):
+        ref = orc.matmul_quant(fmt, A, Bq, N, K, rows=(n0, n0 + 128))[:, n0:n0 + 128]
+        err = normwise_rel_err(got[:, n0:n0 + 128], ref)
+        assert err <= PREFILL_TOL, (n0, err)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M", [17, 64, 130])
+def test_prefill_exact_integer_bit_exact(orc, fmt, M):
+    # integer activations and power-of-two-scaled integer weights are exact in
+    # fp16 and every fp32 partial sum is exact: the MFMA GEMM must be bit-exact
+    from test_oracle_matmul import exact_case
+
+    N, K = 300, 1024
+    A, Bq = exact_case(fmt, M, N, K, seed=M)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert bits_equal(got, ref)
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_k", "q6_k", "fp16"])
+@pytest.mark.parametrize("M,N,K", [(64, 128, 8192), (40, 100, 4096), (33, 64, 16384)])
+def test_prefill_split_k(orc, fmt, M, N, K):
+    # few output tiles: the k range is split over workgroups and added with atomics
+    A = quant.randn(M * K, seed=M + K).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=N + 5)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= PREFILL_TOL
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q5_0", "fp16"])
+@pytest.mark.parametrize("K", [576, 96, 32 * 35])
+def test_prefill_k_32_multiples(orc, fmt, K):
+    # K = 576 (SmolLM2, 9 steps of 64) takes the MFMA GEMM; K an odd multiple of
+    # 32 takes the element-wise kernel
+    M, N = 40, 1536
+    A = quant.randn(M * K, seed=K + 3).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=K + 4)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= PREFILL_TOL
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_k"])
+def test_prefill_unaligned_output(orc, fmt):
+    # C one float into an allocation (not 16-byte aligned) and N not a multiple
+    # of 4: scalar stores
+    M, N, K = 48, 257, 512
+    A = quant.randn(M * K, seed=9).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=10)
+    buf = torch.full((M * N + 1,), float("nan"), dtype=torch.float32, device="cuda")
+    cri.matmul(fmt, dev(A), dev(Bq), buf.data_ptr() + 4, M, N, K)
+    got = host(buf)[1:].reshape(M, N)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= PREFILL_TOL
+
+
+def test_prefill_large_activations(orc):
+    # activations up to ~3e3 (well inside fp16) keep the relative bound
+    M, N, K = 64, 256, 2048
+    A = quant.randn(M * K, seed=11).reshape(M, K) * 1000.0
+    Bq = weights("q8_0", N, K, seed=12)
+    got = run_matmul("q8_0", A, Bq, N, K)
+    ref = orc.matmul_quant("q8_0", A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= PREFILL_TOL
 
 
 def test_k_zero_writes_zeros():
