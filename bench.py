@@ -29,7 +29,16 @@ if ROOT not in sys.path:
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
 MALL_BYTES = 256 << 20
+
+# Multi-token prefill GEMMs: name -> (fmt, M, N, K); reported in TFLOP/s.
+PREFILL_WORKLOADS = {
+    "q8_0_prefill": ("q8_0", 512, 8192, 2048),
+    "q8_0_prefill_down": ("q8_0", 512, 2048, 8192),
+    "q4_k_prefill": ("q4_k", 512, 8192, 2048),
+    "q4_k_prefill_down": ("q4_k", 512, 2048, 8192),
+}
 
 GEMV_WORKLOADS = {
     # name: (fmt, N, K)
@@ -61,7 +70,7 @@ class GemvRig:
         from cretif_amd import quant
 
         self.fmt, self.N, self.K, self.M = fmt, N, K, M
-        w = quant.synthetic_weights(fmt, N, K, seed=seed)
+        w = tiled_weights(fmt, N, K, seed=seed)
         self.wbytes = w.size
         self.copies = int(max(1, min(max_copies, -(-min_bytes // w.size))))
         base = torch.from_numpy(w).cuda()
@@ -106,6 +115,106 @@ class GemvRig:
     def free(self):
         self.W = None
         self.graph = None
+
+
+def tiled_weights(fmt, N, K, seed, max_rows=8192):
+    """Synthetic weights of N rows built from at most `max_rows` quantized rows
+    repeated (rows are independent, so the bytes streamed per launch are the
+    same; the large Q6_K lm_head would otherwise take ~40 s of host
+    quantization)."""
+    from cretif_amd import quant
+
+    if N <= max_rows:
+        return quant.synthetic_weights(fmt, N, K, seed=seed)
+    rows = next(r for r in range(max_rows, 0, -1) if N % r == 0)
+    base = quant.synthetic_weights(fmt, rows, K, seed=seed).reshape(rows, -1)
+    return np.ascontiguousarray(np.tile(base, (N // rows, 1))).ravel()
+
+
+class DecodeStepRig:
+    """Synthetic Llama-3.2-1B-shaped decode step for M
+    tokens: 16 layers of Q4_K q (2048x2048), k and v (512x2048), o (2048x2048),
+    gate and up (8192x2048), down (2048x8192) plus the GQA QK^T and PV products
+    over an fp32 KV cache of T = 2048 positions (32 query heads over 8 KV heads,
+    head_dim 64), then the Q6_K lm_head (128256x2048).  The step is the path's
+    own kernels only (norms, RoPE, softmax and SiLU are not on the path); every
+    layer has its own weight and cache buffers, and the whole step is captured
+    as one HIP graph and replayed."""
+
+    LAYERS, D, H, HKV, HD, FF, VOCAB, T = 16, 2048, 32, 8, 64, 8192, 128256, 2048
+
+    def __init__(self, M, seed=1100):
+        import torch
+
+        import cretif_amd as cri
+
+        self.M = M
+        D, FF, T, H, HKV, HD = self.D, self.FF, self.T, self.H, self.HKV, self.HD
+        shapes = {"q": (D, D), "k": (HKV * HD, D), "v": (HKV * HD, D), "o": (D, D), "gate": (FF, D),
+                  "up": (FF, D), "down": (D, FF)}
+        base = {name: torch.from_numpy(tiled_weights("q4_k", n, k, seed + i)).cuda()
+                for i, (name, (n, k)) in enumerate(shapes.items())}
+        self.layers = [{name: base[name].clone() for name in shapes} for _ in range(self.LAYERS)]
+        del base
+        self.lm_head = torch.from_numpy(tiled_weights("q6_k", self.VOCAB, D, seed + 99)).cuda()
+        g = torch.Generator(device="cuda").manual_seed(3000)
+        self.kT = [torch.randn(HKV, HD, T, device="cuda", generator=g) for _ in range(self.LAYERS)]  # K^T per KV head
+        self.vc = [torch.randn(HKV, T, HD, device="cuda", generator=g) for _ in range(self.LAYERS)]
+        self.x = torch.randn(M, D, device="cuda", generator=g)
+        self.q = torch.empty(M, D, device="cuda")
+        self.kv = torch.empty(M, HKV * HD, device="cuda")
+        self.scores = torch.empty(H, M, T, device="cuda")
+        self.ctx = torch.empty(H, M, HD, device="cuda")
+        self.h = torch.empty(M, D, device="cuda")
+        self.ff = torch.empty(M, FF, device="cuda")
+        self.ff2 = torch.empty(M, FF, device="cuda")
+        self.logits = torch.empty(M, self.VOCAB, device="cuda")
+        self.weight_bytes = sum(t.numel() for L in self.layers for t in L.values()) + self.lm_head.numel()
+        self.kv_bytes = sum(t.numel() * 4 for t in self.kT) + sum(t.numel() * 4 for t in self.vc)
+        self.cri = cri
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):
+            self.step()
+        side.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=side):
+            self.step()
+        torch.cuda.synchronize()
+
+    def step(self):
+        cri, M, D, FF, H, HKV, HD, T = self.cri, self.M, self.D, self.FF, self.H, self.HKV, self.HD, self.T
+        x = self.x
+        for li, L in enumerate(self.layers):
+            cri.matmul("q4_k", x, L["q"], self.q, M, D, D)
+            cri.matmul("q4_k", x, L["k"], self.kv, M, HKV * HD, D)
+            cri.matmul("q4_k", x, L["v"], self.kv, M, HKV * HD, D)
+            # q [M, 32*64] read as [32, M, 64]: the shapes (not the token order) are what is timed
+            cri.batched_matmul_gqa(self.q, self.kT[li], self.scores, H, HKV, M, T, HD)
+            cri.batched_matmul_gqa(self.scores, self.vc[li], self.ctx, H, HKV, M, HD, T)
+            cri.matmul("q4_k", self.ctx, L["o"], self.h, M, D, D)
+            cri.matmul("q4_k", self.h, L["gate"], self.ff, M, FF, D)
+            cri.matmul("q4_k", self.h, L["up"], self.ff2, M, FF, D)
+            cri.matmul("q4_k", self.ff, L["down"], self.h, M, D, FF)
+            x = self.h
+        cri.matmul("q6_k", x, self.lm_head, self.logits, M, self.VOCAB, D)
+
+    def time(self, reps=20, warmup=3):
+        import torch
+
+        for _ in range(warmup):
+            self.graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            self.graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / reps
+
+    def free(self):
+        self.layers = self.lm_head = self.kT = self.vc = self.graph = None
 
 
 def measured_traffic(workload):
@@ -160,6 +269,10 @@ def main():
     ap.add_argument("--workload", default="q4_k_gemv", choices=sorted(GEMV_WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-details", action="store_true", help="skip the per-format side measurements")
+    ap.add_argument("--prefill", default=None, choices=sorted(PREFILL_WORKLOADS),
+                    help="only time one prefill GEMM workload (for profiling) and print its figures")
+    ap.add_argument("--decode-step", type=int, default=None, metavar="M",
+                    help="only time the synthetic decode step for M tokens (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run ten 64 MiB device copies (known bytes, for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -185,6 +298,19 @@ def main():
     import cretif_amd as cri
 
     cri.lib()
+    if args.decode_step:
+        r = DecodeStepRig(args.decode_step)
+        ms_step = r.time(reps=max(3, args.steps // 1000))
+        print(json.dumps({"workload": "decode_step", "M": args.decode_step, "ms_per_step": round(ms_step, 4),
+                          "tokens/s": round(args.decode_step / (ms_step * 1e-3), 1)}))
+        return
+    if args.prefill:
+        f, m_, n, k = PREFILL_WORKLOADS[args.prefill]
+        r = GemvRig(f, n, k, M=m_, max_copies=16)
+        m, launches = r.time(max(args.steps // 100, 2 * r.copies), 16)
+        print(json.dumps({"workload": args.prefill, "M": m_, "N": n, "K": k, "launches": launches,
+                          "us": round(m * 1e3, 3), "TFLOP/s": round(2.0 * m_ * n * k / (m * 1e-3) / 1e12, 1)}))
+        return
     fmt, N, K = GEMV_WORKLOADS[args.workload]
     rig = GemvRig(fmt, N, K)
     ms, launches = rig.time(args.steps, args.warmup)
@@ -203,6 +329,23 @@ def main():
             m, _ = r.time(max(640, 4 * r.copies), 64)
             details[name] = {"GB/s": round(r.bytes_per_launch() / (m * 1e-3) / 1e9, 1), "us": round(m * 1e3, 3),
                              "copies": r.copies}
+            r.free()
+            torch.cuda.empty_cache()
+        for name, (f, m_, n, k) in PREFILL_WORKLOADS.items():
+            r = GemvRig(f, n, k, M=m_, max_copies=16)
+            m, _ = r.time(max(64, 2 * r.copies), 16)
+            details[name] = {"TFLOP/s": round(2.0 * m_ * n * k / (m * 1e-3) / 1e12, 1), "us": round(m * 1e3, 3),
+                             "M": m_, "copies": r.copies, "fraction_of_fp16_mfma_peak": round(
+                                 2.0 * m_ * n * k / (m * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4)}
+            r.free()
+            torch.cuda.empty_cache()
+        for m_ in (1, 16):
+            r = DecodeStepRig(m_)
+            ms_step = r.time()
+            details["decode_step_m%d" % m_] = {
+                "tokens/s": round(m_ / (ms_step * 1e-3), 1), "ms_per_step": round(ms_step, 4),
+                "weight_GB/s": round(r.weight_bytes / (ms_step * 1e-3) / 1e9, 1),
+                "weight+kv_GB/s": round((r.weight_bytes + r.kv_bytes) / (ms_step * 1e-3) / 1e9, 1)}
             r.free()
             torch.cuda.empty_cache()
 

@@ -29,6 +29,8 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSkNW = 4;  // waves per workgroup
+// Staging items per thread: M * KC / 8 <= 1536 (KC <= 12288 / M) over >= 256 threads.
+constexpr int kSkMaxItems = 6;
 
 // Order of the 8 k values of one k8 group inside an operand register set: the
 // nibble unpack produces (0,2), (1,3), (4,6), (5,7) pairs.
@@ -59,12 +61,19 @@ struct SkLds {
     int bytes;
 };
 
+// Row strides (in halves) of the staged activations and sub-block sums: one
+// 16-byte (8-byte) pad per row puts the rows of a 16-lane operand fetch in
+// different LDS banks.
+__device__ __host__ inline int sk_xstride(int KC) { return KC + 8; }
+__device__ __host__ inline int sk_sstride(int KC) { return KC / 16 + 4; }
+
 __device__ __host__ inline SkLds sk_layout(int M, int KC, int nw) {
     SkLds L;
     int o = 0;
-    L.xh = o; o += M * KC * 2;
-    L.xl = o; o += M * KC * 2;
-    L.xs = o; o += M * (KC / 64) * 8;  // per (m, sub-block pair): Xhi, Xhi, Xlo, Xlo
+    L.xh = o; o += M * sk_xstride(KC) * 2;
+    L.xl = o; o += M * sk_xstride(KC) * 2;
+    L.xs = o; o += M * sk_sstride(KC) * 2;  // per (m, sub-block pair): Xhi, Xhi, Xlo, Xlo
+    o = (o + 15) & ~15;
     L.scl = o; o += (KC / 256) * 16 * 4;  // unscale[super-block][m] (16 m slots, zero beyond M)
     L.red = o; o += nw * 4 * 64 * 4;   // cross-wave reduction of k-split partials
     L.bytes = o;
@@ -88,16 +97,30 @@ __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int 
     // slots of rows m >= M (never written below) read as 0
     for (int e = tid; e < nsb * 16; e += nth)
         if ((e & 15) >= M) unscale[e] = 0.0f;
-    for (int m = 0; m < M; ++m)
-    for (int g0 = 0; g0 < groups; g0 += nth) {  // nth is a multiple of 64: half-waves stay aligned
-        const int g8 = g0 + tid;
-        const bool live = g8 < groups;
-        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = a;
-        if (live) {
+    // (row, k8 group) items e = m * groups + g8, strided over the threads; a
+    // 32-lane group always holds one (row, super-block), so its max is a lane
+    // reduction.  All loads are issued before any item is converted.
+    const int total = M * groups;  // <= 1536 (M * KC <= 12288), a multiple of 32
+    f32x4 va[kSkMaxItems], vb[kSkMaxItems];
+#pragma unroll
+    for (int it = 0; it < kSkMaxItems; ++it) {
+        const int e = it * nth + tid;
+        va[it] = vb[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (e < total) {
+            const int m = e / groups, g8 = e - m * groups;
             const float* src = A + static_cast<long>(m) * K + k0 + 8 * g8;
-            a = ld_f32x4(src);
-            b = ld_f32x4(src + 4);
+            va[it] = ld_f32x4(src);
+            vb[it] = ld_f32x4(src + 4);
         }
+    }
+#pragma unroll
+    for (int it = 0; it < kSkMaxItems; ++it) {
+        const int e0 = it * nth;
+        if (e0 >= total) break;  // uniform over the workgroup
+        const int e = e0 + tid;
+        const bool live = e < total;
+        const int m = live ? e / groups : 0, g8 = live ? e - m * groups : 0;
+        const f32x4 a = va[it], b = vb[it];
         float mx = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
                          fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
         mx = fmaxf(mx, dpp<kQuadPerm1032>(mx));
@@ -111,8 +134,8 @@ __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int 
             ex -= 15;
             ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
         }
-        const float s = ldexpf(1.0f, -ex);
-        const float v[8] = {a.x * s, a.y * s, a.z * s, a.w * s, b.x * s, b.y * s, b.z * s, b.w * s};
+        const float sc = ldexpf(1.0f, -ex);
+        const float v[8] = {a.x * sc, a.y * sc, a.z * sc, a.w * sc, b.x * sc, b.y * sc, b.z * sc, b.w * sc};
         float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
         if (live) {
             half8 hi, lo;
@@ -123,8 +146,8 @@ __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int 
                 hi[i] = h;
                 lo[i] = static_cast<_Float16>(x - static_cast<float>(h));
             }
-            *reinterpret_cast<half8*>(xh + m * KC + 8 * g8) = hi;
-            *reinterpret_cast<half8*>(xl + m * KC + 8 * g8) = lo;
+            *reinterpret_cast<half8*>(xh + m * sk_xstride(KC) + 8 * g8) = hi;
+            *reinterpret_cast<half8*>(xl + m * sk_xstride(KC) + 8 * g8) = lo;
             if ((g8 & 31) == 0) unscale[(g8 >> 5) * 16 + m] = ldexpf(1.0f, ex);
         }
         // sub-block sum over the quad (fixed order -> deterministic), pair via row_shl:4
@@ -139,7 +162,7 @@ __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int 
             q[1] = h1;
             q[2] = static_cast<_Float16>(s0 - static_cast<float>(h0));
             q[3] = static_cast<_Float16>(s1 - static_cast<float>(h1));
-            *reinterpret_cast<half4*>(xs + 4 * (m * (KC / 64) + (g8 >> 3))) = q;
+            *reinterpret_cast<half4*>(xs + m * sk_sstride(KC) + 4 * (g8 >> 3)) = q;
         }
     }
     __syncthreads();
@@ -262,10 +285,11 @@ __global__ __launch_bounds__(64 * NW) void skinny_q4k_kernel(const float* __rest
             if (grp == static_cast<int>(blockIdx.x) || nchunks > 1) sk_stage(A, M, K, k0, KC, lds, L);
             auto run_item = [&](const Q4KItem& d, int it) {
                 const int jj = my_split + (it << ks_log2);
-                const int base = m_a * KC + jj * 256 + 64 * g;
+                const int base = m_a * sk_xstride(KC) + jj * 256 + 64 * g;
                 const f32x4 u4 = *reinterpret_cast<const f32x4*>(unscale + jj * 16 + 4 * g);  // rows 4g .. 4g+3
                 const float us[4] = {u4.x, u4.y, u4.z, u4.w};
-                acc += q4k_block(d, xh + base, xl + base, xs + 4 * (m_a * (KC / 64) + jj * 4 + g), has_row, g, us);
+                acc += q4k_block(d, xh + base, xl + base, xs + m_a * sk_sstride(KC) + 4 * (jj * 4 + g), has_row, g,
+                                 us);
             };
             for (int it = 0; it < nitems; it += 2) {
                 run_item(b0, it);
@@ -333,6 +357,7 @@ int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N
     if (KC > K) KC = K;
     while (KC > 256 && K % KC != 0) KC -= 256;
     if (KC < 256 || K % KC != 0) return -1;
+    if (M * (KC / 8) > dev::kSkMaxItems * 256) return -1;  // staging items per thread (>= 256 threads)
     const int ntiles = (N + 15) / 16;
     const int sb = KC / 256;  // super-blocks per chunk
     // split K over the waves of a workgroup when there are too few tiles for ~2048 waves
