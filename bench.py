@@ -139,7 +139,11 @@ class DecodeStepRig:
     head_dim 64), then the Q6_K lm_head (128256x2048).  The step is the path's
     own kernels only (norms, RoPE, softmax and SiLU are not on the path); every
     layer has its own weight and cache buffers, and the whole step is captured
-    as one HIP graph and replayed."""
+    as one HIP graph and replayed.  As inference engines do, the q/k/v weights
+    of a layer are stored as one [3072, 2048] matrix and gate/up as one
+    [16384, 2048] matrix, so a layer is 4 weight launches (same bytes, fewer
+    launches).  Buffers are reused between layers: the timing covers the
+    products at their real shapes; the values are not chained semantically."""
 
     LAYERS, D, H, HKV, HD, FF, VOCAB, T = 16, 2048, 32, 8, 64, 8192, 128256, 2048
 
@@ -150,8 +154,7 @@ class DecodeStepRig:
 
         self.M = M
         D, FF, T, H, HKV, HD = self.D, self.FF, self.T, self.H, self.HKV, self.HD
-        shapes = {"q": (D, D), "k": (HKV * HD, D), "v": (HKV * HD, D), "o": (D, D), "gate": (FF, D),
-                  "up": (FF, D), "down": (D, FF)}
+        shapes = {"qkv": (D + 2 * HKV * HD, D), "o": (D, D), "gateup": (2 * FF, D), "down": (D, FF)}
         base = {name: torch.from_numpy(tiled_weights("q4_k", n, k, seed + i)).cuda()
                 for i, (name, (n, k)) in enumerate(shapes.items())}
         self.layers = [{name: base[name].clone() for name in shapes} for _ in range(self.LAYERS)]
@@ -161,13 +164,11 @@ class DecodeStepRig:
         self.kT = [torch.randn(HKV, HD, T, device="cuda", generator=g) for _ in range(self.LAYERS)]  # K^T per KV head
         self.vc = [torch.randn(HKV, T, HD, device="cuda", generator=g) for _ in range(self.LAYERS)]
         self.x = torch.randn(M, D, device="cuda", generator=g)
-        self.q = torch.empty(M, D, device="cuda")
-        self.kv = torch.empty(M, HKV * HD, device="cuda")
+        self.qkv = torch.empty(M, D + 2 * HKV * HD, device="cuda")
         self.scores = torch.empty(H, M, T, device="cuda")
         self.ctx = torch.empty(H, M, HD, device="cuda")
         self.h = torch.empty(M, D, device="cuda")
-        self.ff = torch.empty(M, FF, device="cuda")
-        self.ff2 = torch.empty(M, FF, device="cuda")
+        self.ff = torch.empty(M, 2 * FF, device="cuda")
         self.logits = torch.empty(M, self.VOCAB, device="cuda")
         self.weight_bytes = sum(t.numel() for L in self.layers for t in L.values()) + self.lm_head.numel()
         self.kv_bytes = sum(t.numel() * 4 for t in self.kT) + sum(t.numel() * 4 for t in self.vc)
@@ -185,15 +186,13 @@ class DecodeStepRig:
         cri, M, D, FF, H, HKV, HD, T = self.cri, self.M, self.D, self.FF, self.H, self.HKV, self.HD, self.T
         x = self.x
         for li, L in enumerate(self.layers):
-            cri.matmul("q4_k", x, L["q"], self.q, M, D, D)
-            cri.matmul("q4_k", x, L["k"], self.kv, M, HKV * HD, D)
-            cri.matmul("q4_k", x, L["v"], self.kv, M, HKV * HD, D)
-            # q [M, 32*64] read as [32, M, 64]: the shapes (not the token order) are what is timed
-            cri.batched_matmul_gqa(self.q, self.kT[li], self.scores, H, HKV, M, T, HD)
+            cri.matmul("q4_k", x, L["qkv"], self.qkv, M, D + 2 * HKV * HD, D)
+            # the first 32*M*64 values of the qkv output read as [32, M, 64] queries
+            cri.batched_matmul_gqa(self.qkv, self.kT[li], self.scores, H, HKV, M, T, HD)
             cri.batched_matmul_gqa(self.scores, self.vc[li], self.ctx, H, HKV, M, HD, T)
             cri.matmul("q4_k", self.ctx, L["o"], self.h, M, D, D)
-            cri.matmul("q4_k", self.h, L["gate"], self.ff, M, FF, D)
-            cri.matmul("q4_k", self.h, L["up"], self.ff2, M, FF, D)
+            cri.matmul("q4_k", self.h, L["gateup"], self.ff, M, 2 * FF, D)
+            # the first M*8192 values of the gate/up output read as the [M, 8192] down input
             cri.matmul("q4_k", self.ff, L["down"], self.h, M, D, FF)
             x = self.h
         cri.matmul("q6_k", x, self.lm_head, self.logits, M, self.VOCAB, D)

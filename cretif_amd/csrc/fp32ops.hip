@@ -5,11 +5,16 @@
 //   B with coalesced 16-byte loads, activations in VGPRs); other shapes use the
 //   LDS-tiled fallback.
 // batched_matmul_gqa: C[h] = A[h] * B[h / G] with A [H,M,K], B [Hkv,K,N]
-//   (ref:src/attention.cu:192-218).  One block serves all G query heads of a KV
-//   head, so each B tile is read once per group instead of once per head; when
-//   the (kv head, n tile) grid alone is too small to fill the GPU the K range is
-//   split across blocks and partial sums are combined with fp32 atomics into a
-//   zero-filled C.
+//   (ref:src/attention.cu:192-218).  The G query heads sharing a KV head are
+//   served together, so each B element is read once per KV head:
+//   a block owns 64 columns (one per lane) x 16 (head, m) rows of one KV
+//   group; its four waves take interleaved 16-column k slices of each 64-k
+//   stage (row values broadcast from LDS, B read once, coalesced along n) and
+//   add their partial sums through LDS in a fixed order.  Short K (QK^T over
+//   head_dim) has enough (column tile, row tile, KV head) blocks and stores
+//   plainly (deterministic); long K (PV over the cache length) is also split
+//   over blocks until the GPU is filled, and those partial tiles are added
+//   with fp32 atomics into a zero-filled C.
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -22,67 +27,70 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, l
     for (long j = i; j < n; j += stride) p[j] = 0.0f;
 }
 
-constexpr int kQTN = 64;  // n per tile
-constexpr int kQTR = 16;  // (head, m) rows per tile
-constexpr int kQTK = 32;  // k per LDS stage
+// ---- GQA kernel -----------------------------------------------------------------
+constexpr int kGsRT = 16;  // rows per block
+constexpr int kGsKC = 16;  // k per wave per LDS stage (a stage is 4 waves x 16 k)
 
-__global__ __launch_bounds__(256) void gqa_kernel(const float* __restrict__ A, const float* __restrict__ B,
-                                                  float* __restrict__ C, int G, int M, int N, int K,
-                                                  int k_split, int splits, int atomic) {
-    __shared__ float as[kQTR][kQTK + 1];
-    __shared__ float bs[kQTK][kQTN];
-    const int tid = threadIdx.x;
-    const int n0 = blockIdx.x * kQTN;
-    const int r0 = blockIdx.y * kQTR;
-    const int kv = blockIdx.z / splits;
-    const int split = blockIdx.z - kv * splits;
-    const int kb = split * k_split;
-    const int ke = min(K, kb + k_split);
-    const int R = G * M;  // rows of this KV group: (head in group, m)
-    const float* Bk = B + static_cast<long>(kv) * K * N;
-    const int tn = tid & 63, tr = (tid >> 6) * 4;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-
-    for (int k0 = kb; k0 < ke; k0 += kQTK) {
-        // A tile: 16 rows x 32 k, 2 floats per thread
+__global__ __launch_bounds__(256) void gqa_split_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                        float* __restrict__ C, int G, int M, int N, int K,
+                                                        int k_split, int atomic) {
+    __shared__ float qs[kGsRT][4 * kGsKC + 4];
+    __shared__ float red[3][kGsRT][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = blockIdx.x * 64 + lane;
+    const int kv = blockIdx.y;
+    const int rt = blockIdx.z % ((G * M + kGsRT - 1) / kGsRT);
+    const int split = blockIdx.z / ((G * M + kGsRT - 1) / kGsRT);
+    const int r0 = rt * kGsRT;
+    const int R = G * M;
+    const int kb = split * k_split, ke = min(K, kb + k_split);
+    const float* Bk = B + static_cast<long>(kv) * K * N + min(n, N - 1);
+    float acc[kGsRT];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int idx = tid + 256 * i;
-            const int rr = idx >> 5, kk = idx & 31;
-            const int r = r0 + rr, k = k0 + kk;
+    for (int r = 0; r < kGsRT; ++r) acc[r] = 0.0f;
+    // each stage: 4 waves x kGsKC k; wave w takes k [k0 + w * kGsKC, +kGsKC)
+    for (int k0 = kb; k0 < ke; k0 += 4 * kGsKC) {
+        for (int e = tid; e < kGsRT * 4 * kGsKC; e += 256) {
+            const int rr = e / (4 * kGsKC), kk = e - rr * (4 * kGsKC), r = r0 + rr, k = k0 + kk;
             float v = 0.0f;
             if (r < R && k < ke) {
                 const int head = kv * G + r / M, m = r - (r / M) * M;
                 v = A[(static_cast<long>(head) * M + m) * K + k];
             }
-            as[rr][kk] = v;
-        }
-        // B tile: 32 k x 64 n, coalesced along n
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int kk = (tid >> 6) + 4 * i, nn = tid & 63;
-            const int k = k0 + kk, n = n0 + nn;
-            bs[kk][nn] = (k < ke && n < N) ? Bk[static_cast<long>(k) * N + n] : 0.0f;
+            qs[rr][kk] = v;
         }
         __syncthreads();
-#pragma unroll 8
-        for (int kk = 0; kk < kQTK; ++kk) {
-            const float b = bs[kk][tn];
+        const int kw = k0 + wave * kGsKC;
+        float b[kGsKC];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(as[tr + i][kk], b, acc[i]);
-        }
+        for (int kk = 0; kk < kGsKC; ++kk) b[kk] = kw + kk < ke ? Bk[static_cast<long>(kw + kk) * N] : 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < kGsKC; kk += 4)
+#pragma unroll
+            for (int r = 0; r < kGsRT; ++r) {
+                const f32x4 q = *reinterpret_cast<const f32x4*>(&qs[r][wave * kGsKC + kk]);
+                acc[r] = __builtin_fmaf(q.x, b[kk], acc[r]);
+                acc[r] = __builtin_fmaf(q.y, b[kk + 1], acc[r]);
+                acc[r] = __builtin_fmaf(q.z, b[kk + 2], acc[r]);
+                acc[r] = __builtin_fmaf(q.w, b[kk + 3], acc[r]);
+            }
         __syncthreads();
     }
-    const int n = n0 + tn;
-    if (n >= N) return;
+    // add the four waves' partial sums (fixed order)
+    if (wave > 0)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = r0 + tr + i;
-        if (r >= R) continue;
+        for (int r = 0; r < kGsRT; ++r) red[wave - 1][r][lane] = acc[r];
+    __syncthreads();
+    if (wave != 0 || n >= N) return;
+#pragma unroll
+    for (int rr = 0; rr < kGsRT; ++rr) {
+        const int r = r0 + rr;
+        if (r >= R) break;
+        const float v = ((acc[rr] + red[0][rr][lane]) + red[1][rr][lane]) + red[2][rr][lane];
         const int head = kv * G + r / M, m = r - (r / M) * M;
         float* dst = C + (static_cast<long>(head) * M + m) * N + n;
-        if (atomic) atomicAdd(dst, acc[i]);
-        else *dst = acc[i];
+        if (atomic) atomicAdd(dst, v);
+        else *dst = v;
     }
 }
 
@@ -104,19 +112,21 @@ int launch_transposed_b(const float* A, const float* B, float* C, int M, int N, 
 int launch_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_heads, int M, int N, int K,
                hipStream_t stream) {
     const int G = n_heads / n_kv_heads;
-    const int R = G * M;
-    const int n_tiles = (N + dev::kQTN - 1) / dev::kQTN;
-    const int r_tiles = (R + dev::kQTR - 1) / dev::kQTR;
-    const long base = static_cast<long>(n_tiles) * r_tiles * n_kv_heads;
+    const long R = static_cast<long>(G) * M;
+    // split K over blocks only while (column tiles x row tiles x KV heads) leaves CUs idle
+    const long rtiles = (R + dev::kGsRT - 1) / dev::kGsRT;
+    const long base = static_cast<long>((N + 63) / 64) * rtiles * n_kv_heads;
+    const int stage = 4 * dev::kGsKC;
+    const int stages = (K + stage - 1) / stage;
     int splits = 1;
-    const int k_stages = (K + dev::kQTK - 1) / dev::kQTK;
-    while (base * splits < 512 && splits * 2 <= k_stages) splits *= 2;
-    const int k_split = ((k_stages + splits - 1) / splits) * dev::kQTK;
+    while (base * splits < 256 && splits * 2 <= stages) splits *= 2;
+    const int k_split = ((stages + splits - 1) / splits) * stage;
     splits = (K + k_split - 1) / k_split;
+    if (rtiles * splits > 65535) return -1;
     const int atomic = splits > 1;
     if (atomic) launch_fill_zero(C, static_cast<long>(n_heads) * M * N, stream);
-    const dim3 grid(n_tiles, r_tiles, n_kv_heads * splits);
-    hipLaunchKernelGGL(dev::gqa_kernel, grid, dim3(256), 0, stream, A, B, C, G, M, N, K, k_split, splits, atomic);
+    const dim3 grid((N + 63) / 64, n_kv_heads, static_cast<unsigned>(rtiles * splits));
+    hipLaunchKernelGGL(dev::gqa_split_kernel, grid, dim3(256), 0, stream, A, B, C, G, M, N, K, k_split, atomic);
     return 0;
 }
 

@@ -333,6 +333,9 @@ def test_transposed_b(orc, M, N, K):
     (32, 8, 16, 64, 2048),
     (6, 3, 5, 37, 45),
     (8, 8, 3, 10, 700),
+    (32, 8, 40, 1500, 300),   # columns kernel: 160 rows per KV head, several k stages, ragged n
+    (4, 1, 7, 90, 1030),      # split kernel: ragged k stage, 28 rows
+    (32, 8, 512, 64, 512),    # prefill-sized P V: many row tiles
 ])
 def test_gqa(orc, H, Hkv, M, N, K):
     A = quant.randn(H * M * K, seed=H + M).reshape(H, M, K)
