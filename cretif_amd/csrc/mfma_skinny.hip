@@ -18,6 +18,15 @@
 // so the VALU only unpacks nibbles, and only the lanes that carry real rows
 // (m < M) read activations from LDS.  Each 16-row weight tile is split over
 // the waves of a workgroup by super-block and reduced through LDS at the end.
+//
+// Q6_K (ref:src/kernels/matmul_quant.cu:408-494) for 2 <= M <= 16 uses the
+// same staging and tiling.  Its int8 sub-scale times the 6-bit code reaches
+// 4096, beyond fp16's exact integers, so each weight sc * (q6 - 32) goes in as
+// its fp16 rounding hi plus the exact remainder lo in {-1, 0, 1}: three MFMAs
+// (x_hi * hi, x_lo * hi, x_hi * lo) per 32 k, the dropped x_lo * lo being
+// 2^-11 of the smallest term; d is applied per super-block.
+#include <atomic>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -29,8 +38,10 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSkNW = 4;  // waves per workgroup
-// Staging items per thread: M * KC / 8 <= 1536 (KC <= 12288 / M) over >= 256 threads.
+// Staging items per thread per load batch.
 constexpr int kSkMaxItems = 6;
+// Activation chunk bound: M * KC <= kSkChunk (fp16 hi + lo copies: 4 * kSkChunk bytes of LDS).
+constexpr int kSkChunk = 32768;
 
 // Order of the 8 k values of one k8 group inside an operand register set: the
 // nibble unpack produces (0,2), (1,3), (4,6), (5,7) pairs.
@@ -99,12 +110,14 @@ __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int 
         if ((e & 15) >= M) unscale[e] = 0.0f;
     // (row, k8 group) items e = m * groups + g8, strided over the threads; a
     // 32-lane group always holds one (row, super-block), so its max is a lane
-    // reduction.  All loads are issued before any item is converted.
-    const int total = M * groups;  // <= 1536 (M * KC <= 12288), a multiple of 32
+    // reduction.  Items go in batches of kSkMaxItems per thread, each batch's
+    // loads issued before any of its items is converted.
+    const int total = M * groups;  // a multiple of 32
+    for (int e_batch = 0; e_batch < total; e_batch += kSkMaxItems * nth) {
     f32x4 va[kSkMaxItems], vb[kSkMaxItems];
 #pragma unroll
     for (int it = 0; it < kSkMaxItems; ++it) {
-        const int e = it * nth + tid;
+        const int e = e_batch + it * nth + tid;
         va[it] = vb[it] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (e < total) {
             const int m = e / groups, g8 = e - m * groups;
@@ -115,7 +128,7 @@ __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int 
     }
 #pragma unroll
     for (int it = 0; it < kSkMaxItems; ++it) {
-        const int e0 = it * nth;
+        const int e0 = e_batch + it * nth;
         if (e0 >= total) break;  // uniform over the workgroup
         const int e = e0 + tid;
         const bool live = e < total;
@@ -164,6 +177,7 @@ __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int 
             q[3] = static_cast<_Float16>(s1 - static_cast<float>(h1));
             *reinterpret_cast<half4*>(xs + m * sk_sstride(KC) + 4 * (g8 >> 3)) = q;
         }
+    }
     }
     __syncthreads();
 }
@@ -237,11 +251,126 @@ __device__ __forceinline__ f4 q4k_block(const Q4KItem& d, const _Float16* xha, c
     return r;
 }
 
+// Format policies of the skinny kernel: the bytes one lane (k slice g of a
+// 16-row tile, row nl) loads per super-block, and that super-block's
+// contribution to the lane's four outputs.
+struct SkQ4K {
+    static constexpr int kBlockBytes = 144;
+    typedef Q4KItem Item;
+    static __device__ __forceinline__ void load(Item& d, const uint8_t* sb, int g) {
+        d.h = ld_u32x4_a16(sb);
+        d.q0 = ld_u32x4_a16(sb + 16 + 32 * g);
+        d.q1 = ld_u32x4_a16(sb + 32 + 32 * g);
+    }
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
+                                               const _Float16* xsa, bool has_row, int g, const float (&us)[4]) {
+        return q4k_block(d, xha, xla, xsa, has_row, g, us);
+    }
+};
+
+// Q6_K super-block (ref:src/kernels/dequantize.cu:215-243): element 128 c + e
+// (e < 128) takes the low (e < 64) or high nibble of ql[64 c + (e % 64)] and
+// bits 2 (e / 32) .. +1 of qh[32 c + e % 32]; int8 scale scales[8 c + e / 16];
+// x = d * sc * (q6 - 32).  Lane slice g covers e in [64 (g & 1), +64) of chunk
+// c = g >> 1, so MFMA slice s (8 k) needs ql bytes [8 s, 8 s + 8) and qh bytes
+// [8 (s & 3), +8) of its chunk and one of four consecutive scales.  The
+// super-blocks are only 2-byte aligned: the loads round down to a dword and
+// funnel-shift.
+struct Q6KItem {
+    uint32_t ql[17], qh[9], sc[2];
+    uint32_t d;      // fp16 bits of d
+    uint32_t shift;  // byte offset of the super-block within its dword
+};
+struct SkQ6K {
+    static constexpr int kBlockBytes = 210;
+    typedef Q6KItem Item;
+    static __device__ __forceinline__ void load(Item& d, const uint8_t* sb, int g) {
+        const int c = g >> 1;
+        const uintptr_t sh = reinterpret_cast<uintptr_t>(sb) & 3;
+        const uint8_t* al = sb - sh + 64 * c;  // the runs below share sb's dword offset
+        const uint8_t* ah = sb - sh + 128 + 32 * c;
+        const uint8_t* as = sb - sh + 192 + 8 * c + 4 * (g & 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 v = ld_u32x4(al + 16 * i);
+            d.ql[4 * i] = v.x; d.ql[4 * i + 1] = v.y; d.ql[4 * i + 2] = v.z; d.ql[4 * i + 3] = v.w;
+        }
+        d.ql[16] = ld_u32(al + 64);  // <= sb + 132
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const u32x4 v = ld_u32x4(ah + 16 * i);
+            d.qh[4 * i] = v.x; d.qh[4 * i + 1] = v.y; d.qh[4 * i + 2] = v.z; d.qh[4 * i + 3] = v.w;
+        }
+        d.qh[8] = ld_u32(ah + 32);  // <= sb + 196
+        d.sc[0] = ld_u32(as);
+        d.sc[1] = ld_u32(as + (sh ? 4 : 0));  // second dword only when the scales straddle it (<= sb + 210)
+        d.d = *reinterpret_cast<const uint16_t*>(sb + 208);
+        d.shift = static_cast<uint32_t>(sh);
+    }
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
+                                               const _Float16*, bool has_row, int g, const float (&us)[4]) {
+        const uint32_t sh = d.shift;
+        const uint32_t scs = __builtin_amdgcn_alignbyte(d.sc[1], d.sc[0], sh);
+        uint32_t sc2[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc2[j] = f16x2_splat(static_cast<float>(static_cast<int8_t>(scs >> (8 * j))));
+        const uint32_t bias = f16x2_splat(-1056.0f);  // (1024 + q6) - 1056 = q6 - 32
+        const uint32_t lsh = 4 * (g & 1);
+        const half8 zero8 = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        half8 ah[8], al[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) ah[s] = al[s] = zero8;
+        if (has_row) {
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                ah[s] = *reinterpret_cast<const half8*>(xha + 8 * s);
+                al[s] = *reinterpret_cast<const half8*>(xla + 8 * s);
+            }
+        }
+        f4 Ph = f4{0.f, 0.f, 0.f, 0.f}, Pl = Ph, Pc = Ph;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint32_t hsh = 2 * (2 * (g & 1) + (s >> 2));
+            uint32_t w[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t ql = __builtin_amdgcn_alignbyte(d.ql[2 * s + j + 1], d.ql[2 * s + j], sh);
+                const uint32_t qh = __builtin_amdgcn_alignbyte(d.qh[2 * (s & 3) + j + 1], d.qh[2 * (s & 3) + j], sh);
+                w[j] = ((ql >> lsh) & 0x0F0F0F0Fu) | (((qh >> hsh) & 0x03030303u) << 4);  // q6 bytes
+            }
+            const uint32_t sc = sc2[2 * (s >> 2) + ((s & 3) >> 1)];
+            // register pairs (0,2), (1,3), (4,6), (5,7) of the slice, as the staged activations
+            const uint32_t t[4] = {and_or(w[0], 0x00FF00FFu, 0x64006400u), and_or(w[0] >> 8, 0x00FF00FFu, 0x64006400u),
+                                   and_or(w[1], 0x00FF00FFu, 0x64006400u), and_or(w[1] >> 8, 0x00FF00FFu, 0x64006400u)};
+            typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+            u4 hi, lo;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                // q6 - 32 exact; sc * (q6 - 32) = hi + lo with hi its fp16 rounding and
+                // lo in {-1, 0, 1} (|sc * (q6 - 32)| <= 4096), both exact
+                const uint32_t q = pk_fma_f16(t[r], 0x3C003C00u, bias);
+                hi[r] = pk_fma_f16(q, sc, 0u);
+                lo[r] = pk_fma_f16(q, sc, hi[r] ^ 0x80008000u);
+            }
+            const half8 bh = __builtin_bit_cast(half8, hi), bl = __builtin_bit_cast(half8, lo);
+            Ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bh, Ph, 0, 0, 0);
+            Pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s], bh, Pl, 0, 0, 0);
+            Pc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bl, Pc, 0, 0, 0);
+        }
+        const f4 P = (Ph + Pl) + Pc;
+        const float dd = h_lo(d.d);
+        f4 r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = us[i] * (dd * P[i]);
+        return r;
+    }
+};
+
 // Workgroup = NW waves = (NW / KS) tiles x KS k-splits.  The grid strides
 // over groups of NW / KS tiles; wave w works on tile w / KS of the group and
 // on super-blocks j = w % KS, + KS, ... of the current activation chunk.
-template <int NW>
-__global__ __launch_bounds__(64 * NW) void skinny_q4k_kernel(const float* __restrict__ A, const uint8_t* __restrict__ B,
+template <class F, int NW>
+__global__ __launch_bounds__(64 * NW) void skinny_kernel(const float* __restrict__ A, const uint8_t* __restrict__ B,
                                                              float* __restrict__ C, int M, int N, int K, int KC,
                                                              int ks_log2, int ngroups, int nchunks) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -254,7 +383,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_q4k_kernel(const float* __rest
     const int TW = NW >> ks_log2;             // tiles per group
     const int my_tile = wave >> ks_log2, my_split = wave & (KS - 1);
     const int ntiles = (N + 15) >> 4;
-    const long rbytes = static_cast<long>(K >> 8) * 144;
+    const long rbytes = static_cast<long>(K >> 8) * F::kBlockBytes;
     const _Float16* xh = reinterpret_cast<const _Float16*>(lds + L.xh);
     const _Float16* xl = reinterpret_cast<const _Float16*>(lds + L.xl);
     const _Float16* xs = reinterpret_cast<const _Float16*>(lds + L.xs);
@@ -271,25 +400,22 @@ __global__ __launch_bounds__(64 * NW) void skinny_q4k_kernel(const float* __rest
         f4 acc = f4{0.f, 0.f, 0.f, 0.f};
         for (int c = 0; c < nchunks; ++c) {
             const int k0 = c * KC;
-            const uint8_t* cp = rowp + static_cast<long>((k0 >> 8) + my_split) * 144;
-            auto load_item = [&](Q4KItem& d, int it) {
-                const uint8_t* p = cp + static_cast<long>(it << ks_log2) * 144;
-                d.h = ld_u32x4_a16(p);
-                d.q0 = ld_u32x4_a16(p + 16 + 32 * g);
-                d.q1 = ld_u32x4_a16(p + 32 + 32 * g);
+            const uint8_t* cp = rowp + static_cast<long>((k0 >> 8) + my_split) * F::kBlockBytes;
+            auto load_item = [&](typename F::Item& d, int it) {
+                F::load(d, cp + static_cast<long>(it << ks_log2) * F::kBlockBytes, g);
             };
             // the first two super-blocks are requested before the activations are staged
-            Q4KItem b0, b1;
+            typename F::Item b0, b1;
             if (nitems > 0) load_item(b0, 0);
             if (nitems > 1) load_item(b1, 1);
             if (grp == static_cast<int>(blockIdx.x) || nchunks > 1) sk_stage(A, M, K, k0, KC, lds, L);
-            auto run_item = [&](const Q4KItem& d, int it) {
+            auto run_item = [&](const typename F::Item& d, int it) {
                 const int jj = my_split + (it << ks_log2);
                 const int base = m_a * sk_xstride(KC) + jj * 256 + 64 * g;
                 const f32x4 u4 = *reinterpret_cast<const f32x4*>(unscale + jj * 16 + 4 * g);  // rows 4g .. 4g+3
                 const float us[4] = {u4.x, u4.y, u4.z, u4.w};
-                acc += q4k_block(d, xh + base, xl + base, xs + m_a * sk_sstride(KC) + 4 * (jj * 4 + g), has_row, g,
-                                 us);
+                acc += F::block(d, xh + base, xl + base, xs + m_a * sk_sstride(KC) + 4 * (jj * 4 + g), has_row, g,
+                                us);
             };
             for (int it = 0; it < nitems; it += 2) {
                 run_item(b0, it);
@@ -330,13 +456,26 @@ __global__ __launch_bounds__(64 * NW) void skinny_q4k_kernel(const float* __rest
 namespace detail {
 
 bool skinny_supported(int fmt, int M, int K, const void* B) {
-    if (fmt != kFmtQ4_K) return false;
     if (M < 1 || M > 16 || K % 256 != 0) return false;
-    return (reinterpret_cast<uintptr_t>(B) & 15u) == 0;  // 16-byte loads of 144-byte blocks
+    if (fmt == kFmtQ4_K) return (reinterpret_cast<uintptr_t>(B) & 15u) == 0;  // 16-byte loads of 144-byte blocks
+    // Q6_K: the batch-1 GEMV streams it at HBM rate; 2..16 rows share each decoded block here
+    if (fmt == kFmtQ6_K) return M >= 2 && (reinterpret_cast<uintptr_t>(B) & 1u) == 0;
+    return false;
 }
 
-template <int NW>
-static void launch_sk(const float* A, const void* B, float* C, int M, int N, int K, int KC, int KS, hipStream_t stream) {
+template <class F, int NW>
+static int launch_sk(const float* A, const void* B, float* C, int M, int N, int K, int KC, int KS, hipStream_t stream) {
+    // large chunks need more than the default 64 KB of dynamic LDS: raise the limit once per kernel and device
+    constexpr int kMaxDevices = 64;
+    static std::atomic<bool> ready[kMaxDevices];
+    int devid = 0;
+    if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return -1;
+    if (!ready[devid].load(std::memory_order_acquire)) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::skinny_kernel<F, NW>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+            return -1;
+        ready[devid].store(true, std::memory_order_release);
+    }
     const int ntiles = (N + 15) / 16;
     const int TW = NW / KS;
     const int groups = (ntiles + TW - 1) / TW;
@@ -346,26 +485,30 @@ static void launch_sk(const float* A, const void* B, float* C, int M, int N, int
     int blocks = groups < 2048 / NW ? groups : 2048 / NW;
     if (blocks < 1) blocks = 1;
     const dev::SkLds L = dev::sk_layout(M, KC, NW);
-    hipLaunchKernelGGL(dev::skinny_q4k_kernel<NW>, dim3(blocks), dim3(64 * NW), L.bytes, stream, A,
+    hipLaunchKernelGGL((dev::skinny_kernel<F, NW>), dim3(blocks), dim3(64 * NW), L.bytes, stream, A,
                        static_cast<const uint8_t*>(B), C, M, N, K, KC, ks_log2, groups, K / KC);
+    return 0;
 }
 
 int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream) {
-    (void)fmt;
-    // activation chunk: the largest multiple of 256 dividing K whose fp16 hi/lo copy fits in 48 KB
-    int KC = (12288 / M) / 256 * 256;
+    // activation chunk: the largest multiple of 256 dividing K with M * KC <= kSkChunk
+    // (few chunks: every chunk is staged once per workgroup); with 512+ tiles, half
+    // of that, so that two workgroups share a CU
+    const int ntiles = (N + 15) / 16;
+    const int chunk = ntiles >= 512 ? dev::kSkChunk / 2 : dev::kSkChunk;
+    int KC = (chunk / M) / 256 * 256;
     if (KC > K) KC = K;
     while (KC > 256 && K % KC != 0) KC -= 256;
     if (KC < 256 || K % KC != 0) return -1;
-    if (M * (KC / 8) > dev::kSkMaxItems * 256) return -1;  // staging items per thread (>= 256 threads)
-    const int ntiles = (N + 15) / 16;
     const int sb = KC / 256;  // super-blocks per chunk
     // split K over the waves of a workgroup when there are too few tiles for ~2048 waves
     int KS = 1;
     while (KS < 8 && KS * 2 <= sb && static_cast<long>(ntiles) * KS < 2048) KS *= 2;
-    if (KS >= 8) launch_sk<8>(A, B, C, M, N, K, KC, KS, stream);
-    else launch_sk<4>(A, B, C, M, N, K, KC, KS, stream);
-    return 0;
+    if (fmt == kFmtQ6_K)
+        return KS >= 8 ? launch_sk<dev::SkQ6K, 8>(A, B, C, M, N, K, KC, KS, stream)
+                       : launch_sk<dev::SkQ6K, 4>(A, B, C, M, N, K, KC, KS, stream);
+    return KS >= 8 ? launch_sk<dev::SkQ4K, 8>(A, B, C, M, N, K, KC, KS, stream)
+                   : launch_sk<dev::SkQ4K, 4>(A, B, C, M, N, K, KC, KS, stream);
 }
 
 }  // namespace detail

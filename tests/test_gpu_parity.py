@@ -182,6 +182,30 @@ def test_matmul_small_m(orc, fmt, M, N, K):
     assert normwise_rel_err(got, ref) <= tol_for(M)
 
 
+@pytest.mark.parametrize("M", [2, 7, 16])
+def test_q6_k_skinny_lm_head_rows(orc, M):
+    # decode batches against a slice of the lm_head shape (full-range int8 sub-scales)
+    N, K = 4096, 2048
+    A = quant.randn(M * K, seed=M + 77).reshape(M, K)
+    Bq = weights("q6_k", N, K, seed=78)
+    got = run_matmul("q6_k", A, Bq, N, K)
+    ref = orc.matmul_quant("q6_k", A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("off", [2, 4, 6])
+def test_q6_k_skinny_unaligned(orc, off):
+    # 210-byte super-blocks at 2-byte offsets; K/256 odd so rows alternate alignment
+    M, N, K = 5, 37, 768
+    A = quant.randn(M * K, seed=off).reshape(M, K)
+    Bq = weights("q6_k", N, K, seed=off + 1)
+    buf = torch.zeros(Bq.size + 8, dtype=torch.uint8, device="cuda")
+    buf[off:off + Bq.size] = dev(Bq)
+    C = torch.empty(M, N, dtype=torch.float32, device="cuda")
+    cri.matmul_q6_k(dev(A), buf.data_ptr() + off, C, M, N, K)
+    assert normwise_rel_err(host(C), orc.matmul_quant("q6_k", A, Bq, N, K)) <= GEMV_TOL
+
+
 def test_reference_test_shapes(orc):
     # shapes and LCG data of ref:tests/test_matmul_quant.cu (MatmulQ8_0/Q4_0/Q4_K/Q5_0/Q6_K/FP16)
     cases = [
