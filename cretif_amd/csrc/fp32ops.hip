@@ -28,7 +28,7 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, l
 }
 
 // ---- GQA kernel -----------------------------------------------------------------
-constexpr int kGsRT = 16;  // rows per block
+constexpr int kGsRT = 16;  // rows per block (32 measured slower: fewer blocks)
 constexpr int kGsKC = 16;  // k per wave per LDS stage (a stage is 4 waves x 16 k)
 
 __global__ __launch_bounds__(256) void gqa_split_kernel(const float* __restrict__ A, const float* __restrict__ B,
@@ -48,8 +48,14 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(const float* __restrict_
     float acc[kGsRT];
 #pragma unroll
     for (int r = 0; r < kGsRT; ++r) acc[r] = 0.0f;
-    // each stage: 4 waves x kGsKC k; wave w takes k [k0 + w * kGsKC, +kGsKC)
+    // each stage: 4 waves x kGsKC k; wave w takes k [k0 + w * kGsKC, +kGsKC).  The
+    // wave's B loads are issued before the row values are staged, so the two
+    // latencies overlap.
     for (int k0 = kb; k0 < ke; k0 += 4 * kGsKC) {
+        const int kw = k0 + wave * kGsKC;
+        float b[kGsKC];
+#pragma unroll
+        for (int kk = 0; kk < kGsKC; ++kk) b[kk] = kw + kk < ke ? Bk[static_cast<long>(kw + kk) * N] : 0.0f;
         for (int e = tid; e < kGsRT * 4 * kGsKC; e += 256) {
             const int rr = e / (4 * kGsKC), kk = e - rr * (4 * kGsKC), r = r0 + rr, k = k0 + kk;
             float v = 0.0f;
@@ -60,10 +66,6 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(const float* __restrict_
             qs[rr][kk] = v;
         }
         __syncthreads();
-        const int kw = k0 + wave * kGsKC;
-        float b[kGsKC];
-#pragma unroll
-        for (int kk = 0; kk < kGsKC; ++kk) b[kk] = kw + kk < ke ? Bk[static_cast<long>(kw + kk) * N] : 0.0f;
 #pragma unroll
         for (int kk = 0; kk < kGsKC; kk += 4)
 #pragma unroll
