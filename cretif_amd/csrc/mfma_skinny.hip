@@ -97,6 +97,71 @@ __device__ __host__ inline SkLds sk_layout(int M, int KC, int nw) {
 // super-block is rescaled anyway); the 32 k8 groups of one super-block sit in
 // one half-wave, so the max is a DPP/swizzle reduction and needs no barrier.
 // Per-sub-block sums (times 2^-6) feed the mins MFMA.  One barrier.
+// Convert one staging item (row m, k8 group g8; live = it exists) into LDS:
+// fp16 hi/lo in the operand order, the (row, super-block) unscale and the
+// sub-block sums.  All 64 lanes of the wave must call it together (lane
+// reductions); 32-lane groups hold one (row, super-block).
+__device__ __forceinline__ void sk_convert_item(const f32x4 a, const f32x4 b, bool live, int m, int g8, int KC,
+                                                _Float16* xh, _Float16* xl, _Float16* xs, float* unscale) {
+    float mx = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                     fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+    mx = fmaxf(mx, dpp<kQuadPerm1032>(mx));
+    mx = fmaxf(mx, dpp<kQuadPerm2301>(mx));
+    mx = fmaxf(mx, dpp<kRowHalfMirror>(mx));
+    mx = fmaxf(mx, dpp<kRowMirror>(mx));
+    mx = fmaxf(mx, swizzle_xor16(mx));  // max over the 32 lanes = one super-block
+    int ex = 0;
+    if (mx > 0.0f) {
+        frexpf(mx, &ex);
+        ex -= 15;
+        ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
+    }
+    const float sc = ldexpf(1.0f, -ex);
+    const float v[8] = {a.x * sc, a.y * sc, a.z * sc, a.w * sc, b.x * sc, b.y * sc, b.z * sc, b.w * sc};
+    float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    if (live) {
+        half8 hi, lo;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float x = v[kPerm8[i]];
+            const _Float16 h = static_cast<_Float16>(x);
+            hi[i] = h;
+            lo[i] = static_cast<_Float16>(x - static_cast<float>(h));
+        }
+        *reinterpret_cast<half8*>(xh + m * sk_xstride(KC) + 8 * g8) = hi;
+        *reinterpret_cast<half8*>(xl + m * sk_xstride(KC) + 8 * g8) = lo;
+        if ((g8 & 31) == 0) unscale[(g8 >> 5) * 16 + m] = ldexpf(1.0f, ex);
+    }
+    // sub-block sum over the quad (fixed order -> deterministic), pair via row_shl:4
+    sum = sum + dpp<kQuadPerm1032>(sum);
+    sum = sum + dpp<kQuadPerm2301>(sum);
+    const float next = dpp<0x104>(sum);  // row_shl:4: the quad above (sub-block 2p+1)
+    if (live && (g8 & 7) == 0) {
+        const float s0 = sum * 0.015625f, s1 = next * 0.015625f;  // 2^-6 keeps 32 * 2^15 in range
+        const _Float16 h0 = static_cast<_Float16>(s0), h1 = static_cast<_Float16>(s1);
+        half4 q;
+        q[0] = h0;
+        q[1] = h1;
+        q[2] = static_cast<_Float16>(s0 - static_cast<float>(h0));
+        q[3] = static_cast<_Float16>(s1 - static_cast<float>(h1));
+        *reinterpret_cast<half4*>(xs + m * sk_sstride(KC) + 4 * (g8 >> 3)) = q;
+    }
+}
+
+// Slots of unscale[] for rows m >= M (never written by the items) read as 0.
+__device__ __forceinline__ void sk_clear_unscale(int M, int KC, float* unscale) {
+    const int nsb = KC / 256;
+    for (int e = threadIdx.x; e < nsb * 16; e += blockDim.x)
+        if ((e & 15) >= M) unscale[e] = 0.0f;
+}
+
+// Stage activations A[m][k0 .. k0+KC) (rows m < M) into LDS as fp16 hi/lo in
+// the operand order.  Each (row, super-block) of 256 activations gets its own
+// power-of-two scale that puts its max |x| just under 2^15 (the product of a
+// super-block is rescaled anyway); (row, k8 group) items e = m * groups + g8
+// are strided over the threads in batches of kSkMaxItems per thread, each
+// batch's loads issued before any of its items is converted.  Per-sub-block
+// sums (times 2^-6) feed the mins MFMA.  One barrier.
 __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int KC, char* lds, const SkLds& L) {
     const int tid = threadIdx.x, nth = blockDim.x;
     _Float16* xh = reinterpret_cast<_Float16*>(lds + L.xh);
@@ -104,80 +169,60 @@ __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int 
     _Float16* xs = reinterpret_cast<_Float16*>(lds + L.xs);
     float* unscale = reinterpret_cast<float*>(lds + L.scl);
     const int groups = KC / 8;  // k8 groups per row; a multiple of 32
-    const int nsb = KC / 256;
-    // slots of rows m >= M (never written below) read as 0
-    for (int e = tid; e < nsb * 16; e += nth)
-        if ((e & 15) >= M) unscale[e] = 0.0f;
-    // (row, k8 group) items e = m * groups + g8, strided over the threads; a
-    // 32-lane group always holds one (row, super-block), so its max is a lane
-    // reduction.  Items go in batches of kSkMaxItems per thread, each batch's
-    // loads issued before any of its items is converted.
+    sk_clear_unscale(M, KC, unscale);
     const int total = M * groups;  // a multiple of 32
     for (int e_batch = 0; e_batch < total; e_batch += kSkMaxItems * nth) {
-    f32x4 va[kSkMaxItems], vb[kSkMaxItems];
+        f32x4 va[kSkMaxItems], vb[kSkMaxItems];
 #pragma unroll
-    for (int it = 0; it < kSkMaxItems; ++it) {
-        const int e = e_batch + it * nth + tid;
-        va[it] = vb[it] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (e < total) {
-            const int m = e / groups, g8 = e - m * groups;
-            const float* src = A + static_cast<long>(m) * K + k0 + 8 * g8;
-            va[it] = ld_f32x4(src);
-            vb[it] = ld_f32x4(src + 4);
+        for (int it = 0; it < kSkMaxItems; ++it) {
+            const int e = e_batch + it * nth + tid;
+            va[it] = vb[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (e < total) {
+                const int m = e / groups, g8 = e - m * groups;
+                const float* src = A + static_cast<long>(m) * K + k0 + 8 * g8;
+                va[it] = ld_f32x4(src);
+                vb[it] = ld_f32x4(src + 4);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kSkMaxItems; ++it) {
+            const int e0 = e_batch + it * nth;
+            if (e0 >= total) break;  // uniform over the workgroup
+            const int e = e0 + tid;
+            const bool live = e < total;
+            const int m = live ? e / groups : 0, g8 = live ? e - m * groups : 0;
+            sk_convert_item(va[it], vb[it], live, m, g8, KC, xh, xl, xs, unscale);
         }
     }
-#pragma unroll
-    for (int it = 0; it < kSkMaxItems; ++it) {
-        const int e0 = e_batch + it * nth;
-        if (e0 >= total) break;  // uniform over the workgroup
-        const int e = e0 + tid;
+    __syncthreads();
+}
+
+// When every thread has at most one item (M * KC / 8 <= threads), its two
+// loads are issued at kernel start, before the weight loads, and converted
+// here: waiting for them does not wait for the weights.
+__device__ __forceinline__ void sk_load_one(const float* __restrict__ A, int M, int K, int k0, int KC, f32x4& a,
+                                            f32x4& b) {
+    const int groups = KC / 8, e = threadIdx.x;
+    a = b = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (e < M * groups) {
+        const int m = e / groups, g8 = e - m * groups;
+        const float* src = A + static_cast<long>(m) * K + k0 + 8 * g8;
+        a = ld_f32x4(src);
+        b = ld_f32x4(src + 4);
+    }
+}
+__device__ __forceinline__ void sk_stage_one(const f32x4 a, const f32x4 b, int M, int KC, char* lds, const SkLds& L) {
+    _Float16* xh = reinterpret_cast<_Float16*>(lds + L.xh);
+    _Float16* xl = reinterpret_cast<_Float16*>(lds + L.xl);
+    _Float16* xs = reinterpret_cast<_Float16*>(lds + L.xs);
+    float* unscale = reinterpret_cast<float*>(lds + L.scl);
+    const int groups = KC / 8, e = threadIdx.x;
+    sk_clear_unscale(M, KC, unscale);
+    const int total = M * groups;
+    if ((e & ~63) < total) {  // whole waves past the items skip (lane reductions need all 64 lanes)
         const bool live = e < total;
         const int m = live ? e / groups : 0, g8 = live ? e - m * groups : 0;
-        const f32x4 a = va[it], b = vb[it];
-        float mx = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                         fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
-        mx = fmaxf(mx, dpp<kQuadPerm1032>(mx));
-        mx = fmaxf(mx, dpp<kQuadPerm2301>(mx));
-        mx = fmaxf(mx, dpp<kRowHalfMirror>(mx));
-        mx = fmaxf(mx, dpp<kRowMirror>(mx));
-        mx = fmaxf(mx, swizzle_xor16(mx));  // max over the 32 lanes = one super-block
-        int ex = 0;
-        if (mx > 0.0f) {
-            frexpf(mx, &ex);
-            ex -= 15;
-            ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
-        }
-        const float sc = ldexpf(1.0f, -ex);
-        const float v[8] = {a.x * sc, a.y * sc, a.z * sc, a.w * sc, b.x * sc, b.y * sc, b.z * sc, b.w * sc};
-        float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-        if (live) {
-            half8 hi, lo;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float x = v[kPerm8[i]];
-                const _Float16 h = static_cast<_Float16>(x);
-                hi[i] = h;
-                lo[i] = static_cast<_Float16>(x - static_cast<float>(h));
-            }
-            *reinterpret_cast<half8*>(xh + m * sk_xstride(KC) + 8 * g8) = hi;
-            *reinterpret_cast<half8*>(xl + m * sk_xstride(KC) + 8 * g8) = lo;
-            if ((g8 & 31) == 0) unscale[(g8 >> 5) * 16 + m] = ldexpf(1.0f, ex);
-        }
-        // sub-block sum over the quad (fixed order -> deterministic), pair via row_shl:4
-        sum = sum + dpp<kQuadPerm1032>(sum);
-        sum = sum + dpp<kQuadPerm2301>(sum);
-        const float next = dpp<0x104>(sum);  // row_shl:4: the quad above (sub-block 2p+1)
-        if (live && (g8 & 7) == 0) {
-            const float s0 = sum * 0.015625f, s1 = next * 0.015625f;  // 2^-6 keeps 32 * 2^15 in range
-            const _Float16 h0 = static_cast<_Float16>(s0), h1 = static_cast<_Float16>(s1);
-            half4 q;
-            q[0] = h0;
-            q[1] = h1;
-            q[2] = static_cast<_Float16>(s0 - static_cast<float>(h0));
-            q[3] = static_cast<_Float16>(s1 - static_cast<float>(h1));
-            *reinterpret_cast<half4*>(xs + m * sk_sstride(KC) + 4 * (g8 >> 3)) = q;
-        }
-    }
+        sk_convert_item(a, b, live, m, g8, KC, xh, xl, xs, unscale);
     }
     __syncthreads();
 }
@@ -404,11 +449,19 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const float* __restrict
             auto load_item = [&](typename F::Item& d, int it) {
                 F::load(d, cp + static_cast<long>(it << ks_log2) * F::kBlockBytes, g);
             };
-            // the first two super-blocks are requested before the activations are staged
+            // the first two super-blocks are requested before the activations are
+            // staged; single-item activation loads go first of all
+            const bool stage = grp == static_cast<int>(blockIdx.x) || nchunks > 1;
+            const bool one = M * (KC / 8) <= 64 * NW;
+            f32x4 xa, xb;
+            if (stage && one) sk_load_one(A, M, K, k0, KC, xa, xb);
             typename F::Item b0, b1;
             if (nitems > 0) load_item(b0, 0);
             if (nitems > 1) load_item(b1, 1);
-            if (grp == static_cast<int>(blockIdx.x) || nchunks > 1) sk_stage(A, M, K, k0, KC, lds, L);
+            if (stage) {
+                if (one) sk_stage_one(xa, xb, M, KC, lds, L);
+                else sk_stage(A, M, K, k0, KC, lds, L);
+            }
             auto run_item = [&](const typename F::Item& d, int it) {
                 const int jj = my_split + (it << ks_log2);
                 const int base = m_a * sk_xstride(KC) + jj * 256 + 64 * g;
