@@ -223,7 +223,7 @@ def measured_traffic(workload):
     import re
 
     fmt, N, K = GEMV_WORKLOADS[workload]
-    for path in glob.glob(os.path.join(ROOT, "profiles", "*%s*%dx%d*.md" % (fmt.replace("_", ""), N, K))):
+    for path in glob.glob(os.path.join(ROOT, "profiles", "*%s_gemv_%dx%d*.md" % (fmt.replace("_", ""), N, K))):
         m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", open(path).read(), re.M)
         if m:
             return int(m.group(1))
