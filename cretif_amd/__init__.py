@@ -37,6 +37,9 @@ __all__ = [
     "dequantize_q4_k",
     "matmul_transposed_b",
     "batched_matmul_gqa",
+    "fused_decode_attention",
+    "fused_decode_attention_ws",
+    "decode_attention_workspace_size",
     "FORMAT_IDS",
     "ABI_SYMBOLS",
 ]
@@ -63,6 +66,9 @@ ABI_SYMBOLS = (
     + [
         "cri_matmul_transposed_b",
         "cri_batched_matmul_gqa",
+        "cri_fused_decode_attention",
+        "cri_fused_decode_attention_ws",
+        "cri_fused_decode_attention_workspace_size",
         "cri_last_error_string",
         "cri_block_bytes",
         "cri_block_elems",
@@ -107,6 +113,13 @@ def lib():
     L.cri_matmul_transposed_b.restype = i32
     L.cri_batched_matmul_gqa.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
     L.cri_batched_matmul_gqa.restype = i32
+    L.cri_fused_decode_attention.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp]
+    L.cri_fused_decode_attention.restype = i32
+    L.cri_fused_decode_attention_ws.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp,
+                                                 ctypes.c_longlong, vp]
+    L.cri_fused_decode_attention_ws.restype = i32
+    L.cri_fused_decode_attention_workspace_size.argtypes = [i32, i32, i32, i32]
+    L.cri_fused_decode_attention_workspace_size.restype = ctypes.c_longlong
     L.cri_last_error_string.argtypes = []
     L.cri_last_error_string.restype = ctypes.c_char_p
     L.cri_block_bytes.argtypes = [i32]
@@ -209,5 +222,57 @@ def batched_matmul_gqa(A, B, C, n_heads, n_kv_heads, M, N, K, stream=None):
     _check(
         lib().cri_batched_matmul_gqa(
             _ptr(A), _ptr(B), _ptr(C), n_heads, n_kv_heads, M, N, K, _stream(stream)
+        )
+    )
+
+
+def fused_decode_attention(Q, K_cache, V_cache, output, n_heads, n_kv_heads, head_dim, kv_len, scale, stream=None):
+    """output[h] = softmax(scale * Q[h] . K[t, h/G]) V[t, h/G] over t < kv_len, one query token
+    (replaces cuinfer::fused_decode_attention, ref:include/cuinfer/attention.h:161-167)."""
+    _check(
+        lib().cri_fused_decode_attention(
+            _ptr(Q),
+            _ptr(K_cache),
+            _ptr(V_cache),
+            _ptr(output),
+            n_heads,
+            n_kv_heads,
+            head_dim,
+            kv_len,
+            float(scale),
+            _stream(stream),
+        )
+    )
+
+
+def decode_attention_workspace_size(n_heads, n_kv_heads, head_dim, kv_len):
+    """Bytes of device workspace fused_decode_attention_ws uses for this shape."""
+    n = lib().cri_fused_decode_attention_workspace_size(n_heads, n_kv_heads, head_dim, kv_len)
+    if n < 0:
+        _check(int(n))
+    return int(n)
+
+
+def fused_decode_attention_ws(Q, K_cache, V_cache, output, n_heads, n_kv_heads, head_dim, kv_len, scale,
+                              workspace, workspace_bytes=None, stream=None):
+    """Split form of fused_decode_attention with partial results in a caller
+    workspace (a device tensor, or an address plus workspace_bytes).  No
+    counterpart in the reference."""
+    if workspace_bytes is None:
+        workspace_bytes = workspace.numel() * workspace.element_size()
+    _check(
+        lib().cri_fused_decode_attention_ws(
+            _ptr(Q),
+            _ptr(K_cache),
+            _ptr(V_cache),
+            _ptr(output),
+            n_heads,
+            n_kv_heads,
+            head_dim,
+            kv_len,
+            float(scale),
+            _ptr(workspace),
+            int(workspace_bytes),
+            _stream(stream),
         )
     )

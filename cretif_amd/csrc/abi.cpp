@@ -173,6 +173,76 @@ int cri_batched_matmul_gqa(const float* A, const float* B, float* C, int n_heads
     return check_launch(fn);
 }
 
+int cri_fused_decode_attention(const float* Q, const float* K_cache, const float* V_cache, float* output,
+                               int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale, hipStream_t s) {
+    const char* fn = "cri_fused_decode_attention";
+    if (n_heads < 0 || n_kv_heads < 0 || head_dim < 0 || kv_len < 0)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative dimension");
+    if (n_heads == 0 || head_dim == 0) return CRI_OK;
+    if (n_kv_heads == 0 || n_heads % n_kv_heads != 0)
+        return fail(CRI_ERR_SHAPE, fn,
+                    "n_heads=" + std::to_string(n_heads) + " is not a multiple of n_kv_heads=" +
+                        std::to_string(n_kv_heads));
+    // the reference divides by an empty softmax sum (NaN output) for kv_len == 0
+    if (kv_len == 0) return fail(CRI_ERR_SHAPE, fn, "kv_len must be at least 1");
+    if (head_dim > cri::detail::kDecodeAttnMaxHeadDim)
+        return fail(CRI_ERR_SHAPE, fn,
+                    "head_dim=" + std::to_string(head_dim) + " exceeds " +
+                        std::to_string(cri::detail::kDecodeAttnMaxHeadDim));
+    if (!Q || !K_cache || !V_cache || !output) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(Q, 4) || !aligned(K_cache, 4) || !aligned(V_cache, 4) || !aligned(output, 4))
+        return fail(CRI_ERR_ALIGNMENT, fn, "Q, K_cache, V_cache and output must be 4-byte aligned");
+    if (static_cast<long>(kv_len) * n_kv_heads * head_dim > kMaxElems)
+        return fail(CRI_ERR_SHAPE, fn, "problem too large");
+    if (cri::detail::launch_decode_attention(Q, K_cache, V_cache, output, n_heads, n_kv_heads, head_dim, kv_len,
+                                             scale, s) != 0)
+        return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
+    return check_launch(fn);
+}
+
+long long cri_fused_decode_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, int kv_len) {
+    const char* fn = "cri_fused_decode_attention_workspace_size";
+    if (n_heads < 0 || n_kv_heads < 0 || head_dim < 0 || kv_len < 0)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative dimension");
+    if (n_heads == 0 || head_dim == 0 || kv_len == 0) return 0;
+    if (n_kv_heads == 0 || n_heads % n_kv_heads != 0)
+        return fail(CRI_ERR_SHAPE, fn, "n_heads is not a multiple of n_kv_heads");
+    return cri::detail::decode_attention_workspace_bytes(n_heads, n_kv_heads, head_dim, kv_len);
+}
+
+int cri_fused_decode_attention_ws(const float* Q, const float* K_cache, const float* V_cache, float* output,
+                                  int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale, void* workspace,
+                                  long long workspace_bytes, hipStream_t s) {
+    const char* fn = "cri_fused_decode_attention_ws";
+    if (workspace_bytes < 0) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative workspace size");
+    if (n_heads < 0 || n_kv_heads < 0 || head_dim < 0 || kv_len < 0 || n_heads == 0 || head_dim == 0 || kv_len == 0 ||
+        n_kv_heads == 0 || n_heads % n_kv_heads != 0 || head_dim > cri::detail::kDecodeAttnMaxHeadDim || !Q ||
+        !K_cache || !V_cache || !output ||
+        !cri::detail::decode_attention_split_supported(Q, K_cache, V_cache, head_dim)) {
+        // argument errors, or a shape the split kernel does not take: the workspace-free form
+        const int rc = cri_fused_decode_attention(Q, K_cache, V_cache, output, n_heads, n_kv_heads, head_dim, kv_len,
+                                                  scale, s);
+        if (rc != CRI_OK) {
+            const size_t colon = g_last_error.find(':');
+            g_last_error = std::string(fn) + (colon == std::string::npos ? ": " + g_last_error : g_last_error.substr(colon));
+        }
+        return rc;
+    }
+    if (!aligned(output, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "output must be 4-byte aligned");
+    if (!workspace) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null workspace");
+    if (!aligned(workspace, 16)) return fail(CRI_ERR_ALIGNMENT, fn, "workspace must be 16-byte aligned");
+    if (static_cast<long>(kv_len) * n_kv_heads * head_dim > kMaxElems) return fail(CRI_ERR_SHAPE, fn, "problem too large");
+    const int rc = cri::detail::launch_decode_attention_split(Q, K_cache, V_cache, output, n_heads, n_kv_heads,
+                                                              head_dim, kv_len, scale, static_cast<float*>(workspace),
+                                                              static_cast<long>(workspace_bytes), s);
+    if (rc == -2)
+        return fail(CRI_ERR_SHAPE, fn,
+                    "workspace of " + std::to_string(workspace_bytes) + " bytes holds less than one record per head (" +
+                        std::to_string(static_cast<long>(n_heads) * (head_dim + 4) * 4) + " bytes)");
+    if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
+    return check_launch(fn);
+}
+
 const char* cri_last_error_string(void) { return g_last_error.c_str(); }
 
 int cri_block_bytes(int format) { return format >= 0 && format <= 5 ? cri::block_bytes(format) : 0; }

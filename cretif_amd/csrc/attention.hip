@@ -1,0 +1,484 @@
+// attention.hip -- fused decode attention: one query token, grouped-query heads,
+// over the fp32 KV cache in its [kv_len, n_kv_heads, head_dim] layout
+// (ref:src/attention.cu:410-511 computes the same softmax(q K^T * scale) V with
+// one block per query head walking the positions one at a time).
+//
+// The call has no workspace (the reference's signature), so partial softmax
+// states cannot be merged across workgroups: a workgroup owns complete outputs.
+// It is one query head h and a slice of 8 output dims, and walks every
+// position of its KV head.  Launch shape for Llama-3.2-1B (32 heads, 8 KV heads,
+// head_dim 64): 8 slices of 8 dims -> 256 workgroups, and the 32 workgroups of
+// one KV head are mapped onto one XCD, so that head's K/V (1 MB at 2048
+// positions) comes from HBM once and the repeats hit that XCD's L2.
+//
+// Per wave and tile of 64 positions:
+//   * scores: 4 lanes per position, each lane holding 4-float slices of the
+//     query (dims 4r + 16i) and loading the same slices of the K row (16-byte
+//     loads, 64 contiguous bytes per lane quad); a 2-step quad reduction gives
+//     the dot products of 16 positions per load round, 4 rounds per tile; lane
+//     (quad q, r) keeps position 16 r + q, so the tile's 64 scores sit one per lane;
+//   * online softmax in base 2 (the query is pre-scaled by scale * log2 e): the
+//     tile max is a wave reduction, the rescale factor is wave-uniform and each
+//     lane updates its own running sum and its 8 accumulators with the V
+//     values of its own position;
+// and at the end the wave's lanes, then the workgroup's waves, are merged
+// (max, rescale, sum) in a fixed order.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace cri {
+namespace dev {
+
+constexpr int kAttWaves = 8;   // waves per workgroup; wave w takes tiles w, w + 8, ...
+constexpr int kAttTile = 64;   // positions per wave tile
+constexpr int kAttDs = 8;      // output dims per workgroup (one slice)
+
+// NQ: 4-float query slices per lane (head_dim <= 16 NQ).  VEC: head_dim % 4 == 0
+// and 16-byte aligned Q / K / V, so the slices load as 16-byte vectors.  One
+// workgroup per CU gives two waves per SIMD: registers go to loads in flight,
+// not to occupancy.
+template <int NQ, bool VEC>
+__global__ __launch_bounds__(64 * kAttWaves) __attribute__((amdgpu_waves_per_eu(1, 2))) void decode_attn_kernel(
+    const float* __restrict__ Q, const float* __restrict__ Kc, const float* __restrict__ Vc, float* __restrict__ out,
+    int G, int kvd, int D, int T, float qscale, int n_slices, int remap) {
+    constexpr int DS = kAttDs;
+    // position groups (16 positions each) whose K slices are loaded as one batch
+    constexpr int GB = NQ <= 4 ? 4 : (NQ == 8 ? 2 : 1);
+    // query slices per batch (scalar loads of head_dim > 128 in two halves)
+    constexpr int IB = (!VEC && NQ == 16) ? 8 : NQ;
+    __shared__ float red[kAttWaves][2 + DS];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int L = blockIdx.x;
+    if (remap) {  // gridDim.x % 8 == 0: logical index L runs on XCD L / (gridDim.x / 8)
+        const int per = gridDim.x >> 3;
+        L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    }
+    const int h = L / n_slices, sl = L - h * n_slices;
+    const int kvh = h / G;
+    const int d0 = sl * DS;
+    const int q4 = lane >> 2, r = lane & 3;
+    const float* Kh = Kc + static_cast<long>(kvh) * D;
+    const float* Vh = Vc + static_cast<long>(kvh) * D;
+
+    // Every load is unconditional, from an address clamped into the row (a
+    // guarded load becomes a branch with its own wait); values past head_dim
+    // are zeroed by a select or meet a zero query value.
+    f32x4 qv[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int d = 4 * r + 16 * i;
+        if constexpr (VEC) {
+            const f32x4 v = ld_f32x4(Q + static_cast<long>(h) * D + min(d, D - 4)) * qscale;
+            qv[i] = d < D ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float v = Q[static_cast<long>(h) * D + min(d + e, D - 1)] * qscale;
+                qv[i][e] = d + e < D ? v : 0.0f;
+            }
+        }
+    }
+
+    float m = -INFINITY, l = 0.0f;
+    float acc[DS];
+#pragma unroll
+    for (int e = 0; e < DS; ++e) acc[e] = 0.0f;
+    const int ntiles = (T + kAttTile - 1) / kAttTile;
+
+    // V slice of the lane's own position (its address does not depend on the scores)
+    auto load_v = [&](float (&vv)[DS], int base) {
+        const float* vp = Vh + static_cast<long>(min(base + 16 * r + q4, T - 1)) * kvd;
+        if constexpr (VEC) {
+#pragma unroll
+            for (int e = 0; e < DS; e += 4) {
+                const f32x4 v = ld_f32x4(vp + min(d0 + e, D - 4));  // 4 | D and 4 | d0
+                vv[e] = v.x; vv[e + 1] = v.y; vv[e + 2] = v.z; vv[e + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < DS; ++e) vv[e] = vp[min(d0 + e, D - 1)];
+        }
+    };
+    // K slices (query slices i0 .. i0+IB) of position group g of a tile
+    auto load_k = [&](f32x4 (&kv)[IB], int base, int g, int i0) {
+        const float* kp = Kh + static_cast<long>(min(base + 16 * g + q4, T - 1)) * kvd;
+#pragma unroll
+        for (int i = 0; i < IB; ++i) {
+            const int d = 4 * r + 16 * (i0 + i);
+            if constexpr (VEC) {
+                kv[i] = ld_f32x4(kp + min(d, D - 4));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) kv[i][e] = kp[min(d + e, D - 1)];
+            }
+        }
+    };
+    auto dot = [&](float part, const f32x4 (&kv)[IB], int i0) {
+#pragma unroll
+        for (int i = 0; i < IB; ++i) {
+            part = __builtin_fmaf(qv[i0 + i].x, kv[i].x, part);
+            part = __builtin_fmaf(qv[i0 + i].y, kv[i].y, part);
+            part = __builtin_fmaf(qv[i0 + i].z, kv[i].z, part);
+            part = __builtin_fmaf(qv[i0 + i].w, kv[i].w, part);
+        }
+        return part;
+    };
+    // lane (quad q, r) keeps the score of position 16 r + q of the tile
+    auto own_score = [&](float& s_own, float part, int base, int g, int limit) {
+        part += dpp<kQuadPerm1032>(part);
+        part += dpp<kQuadPerm2301>(part);
+        const int pos = base + 16 * g + q4;
+        if (g == r) s_own = pos < limit ? part : -INFINITY;
+    };
+    // online-softmax update with the tile's scores and the V slices of the lanes' positions
+    auto update = [&](float s_own, const float (&vraw)[DS]) {
+        // every processed tile has a valid position, so tmax and m_new are finite
+        const float tmax = wave_max(s_own);
+        const float m_new = fmaxf(m, tmax);
+        const float c = exp2f(m - m_new);  // 0 on the wave's first tile
+        const float p = exp2f(s_own - m_new);
+        l = __builtin_fmaf(l, c, p);
+#pragma unroll
+        for (int e = 0; e < DS; ++e) {
+            const float v = d0 + e < D ? vraw[e] : 0.0f;
+            acc[e] = __builtin_fmaf(p, v, acc[e] * c);
+        }
+        m = m_new;
+    };
+
+    if constexpr (NQ <= 4) {
+        // one tile at a time: its 18 loads (2 V + 16 K) are issued as one batch
+        // (a software pipeline over two tiles measured slower: the bound is the
+        // CU's vector-memory throughput, and the clamped prefetch past the end
+        // adds instructions)
+        for (int tile = wave; tile < ntiles; tile += kAttWaves) {
+            const int base = tile * kAttTile;
+            float vv[DS];
+            load_v(vv, base);
+            f32x4 kv[4][IB];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) load_k(kv[g], base, g, 0);
+            __builtin_amdgcn_sched_barrier(0);  // the batch above stays in flight together
+            float s_own = -INFINITY;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) own_score(s_own, dot(0.0f, kv[g], 0), base, g, T);
+            update(s_own, vv);
+        }
+    } else {
+        // head_dim > 64: one tile at a time, K in batches of GB position groups
+        for (int tile = wave; tile < ntiles; tile += kAttWaves) {
+            const int base = tile * kAttTile;
+            float vv[DS];
+            load_v(vv, base);
+            float s_own = -INFINITY;
+#pragma unroll
+            for (int g0 = 0; g0 < 4; g0 += GB) {
+                float part[GB];
+#pragma unroll
+                for (int gb = 0; gb < GB; ++gb) part[gb] = 0.0f;
+#pragma unroll
+                for (int i0 = 0; i0 < NQ; i0 += IB) {
+                    f32x4 kv[GB][IB];
+#pragma unroll
+                    for (int gb = 0; gb < GB; ++gb) load_k(kv[gb], base, g0 + gb, i0);
+                    __builtin_amdgcn_sched_barrier(0);  // the batch above stays in flight together
+#pragma unroll
+                    for (int gb = 0; gb < GB; ++gb) part[gb] = dot(part[gb], kv[gb], i0);
+                }
+#pragma unroll
+                for (int gb = 0; gb < GB; ++gb) own_score(s_own, part[gb], base, g0 + gb, T);
+            }
+            update(s_own, vv);
+        }
+    }
+
+    // merge: lanes of the wave (same m), then the waves (rescaled to the common max)
+    l = group_sum_t<6>(l);
+#pragma unroll
+    for (int e = 0; e < DS; ++e) acc[e] = group_sum_t<6>(acc[e]);
+    if (lane == 0) {
+        red[wave][0] = m;
+        red[wave][1] = l;
+#pragma unroll
+        for (int e = 0; e < DS; ++e) red[wave][2 + e] = acc[e];
+    }
+    __syncthreads();
+    const int e = threadIdx.x;
+    if (e < DS && d0 + e < D) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kAttWaves; ++w) M = fmaxf(M, red[w][0]);
+        float num = 0.0f, den = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttWaves; ++w) {
+            const float f = exp2f(red[w][0] - M);  // 0 for a wave without tiles (m = -inf)
+            num = __builtin_fmaf(f, red[w][2 + e], num);
+            den = __builtin_fmaf(f, red[w][1], den);
+        }
+        out[static_cast<long>(h) * D + d0 + e] = num / den;
+    }
+}
+
+// ---- split form (caller workspace) ---------------------------------------------
+//
+// A workgroup is KV head kvh, a quad of its query heads (one wave per head;
+// measured faster than two or four heads per wave, whose longer per-wave VALU
+// chains dominate a one-tile chunk) and a chunk of Tc positions in tiles of 32.
+// The waves read each tile's K and V rows 4 lanes per position (dims 4 r + 16 i,
+// 16-byte loads); the four waves of a quad hit the same lines, so the cache is
+// read from memory once in total.  Per head: the scores of the tile's 32
+// positions end on lanes r = 0, 1 (position 16 r + q), online softmax as above,
+// and P.V in the same lane layout as the loads (the weight of position 16 g + q
+// is broadcast from lane (q, g) inside its quad).  The chunk's (max, sum,
+// acc[D]) per head go to the workspace, and the combine kernel merges the
+// chunks of each head.  head_dim <= 64, a multiple of 4, and 16-byte aligned
+// Q, K, V.
+constexpr int kSplitTile = 32;
+
+template <int HQ>
+__global__ __launch_bounds__(256 / HQ) void decode_attn_split_kernel(const float* __restrict__ Q,
+                                                                     const float* __restrict__ Kc,
+                                                                     const float* __restrict__ Vc,
+                                                                     float* __restrict__ ws, int G, int kvd, int D,
+                                                                     int T, float qscale, int Tc, int nchunks,
+                                                                     int nhq) {
+    constexpr int NQ = 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = blockIdx.x % nchunks;
+    const int hq = (blockIdx.x / nchunks) % nhq;
+    const int kvh = blockIdx.x / (nchunks * nhq);
+    const int q4 = lane >> 2, r = lane & 3;
+    const int t0 = c * Tc, t1 = min(T, t0 + Tc);
+    const float* Kh = Kc + static_cast<long>(kvh) * D;
+    const float* Vh = Vc + static_cast<long>(kvh) * D;
+
+    f32x4 qv[HQ][NQ];
+#pragma unroll
+    for (int j = 0; j < HQ; ++j) {
+        const int hg = hq * 4 + wave * HQ + j;  // head index inside the KV group
+        const int h = kvh * G + min(hg, G - 1);
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) {
+            const int d = 4 * r + 16 * i;
+            const f32x4 v = ld_f32x4(Q + static_cast<long>(h) * D + min(d, D - 4)) * qscale;
+            qv[j][i] = d < D && hg < G ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    float m[HQ], l[HQ];
+    f32x4 acc[HQ][NQ];
+#pragma unroll
+    for (int j = 0; j < HQ; ++j) {
+        m[j] = -INFINITY;
+        l[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    for (int base = t0; base < t1; base += kSplitTile) {
+        f32x4 kv[2][NQ], vv[2][NQ];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const long row = static_cast<long>(min(base + 16 * g + q4, T - 1)) * kvd;
+#pragma unroll
+            for (int i = 0; i < NQ; ++i) {
+                const int d = min(4 * r + 16 * i, D - 4);
+                kv[g][i] = ld_f32x4(Kh + row + d);
+                vv[g][i] = ld_f32x4(Vh + row + d);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the tile's 16 loads stay in flight together
+#pragma unroll
+        for (int j = 0; j < HQ; ++j) {
+            float s_own = -INFINITY;  // lanes r = 2, 3 own no position of a 32-position tile
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                float part = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NQ; ++i) {
+                    part = __builtin_fmaf(qv[j][i].x, kv[g][i].x, part);
+                    part = __builtin_fmaf(qv[j][i].y, kv[g][i].y, part);
+                    part = __builtin_fmaf(qv[j][i].z, kv[g][i].z, part);
+                    part = __builtin_fmaf(qv[j][i].w, kv[g][i].w, part);
+                }
+                part += dpp<kQuadPerm1032>(part);
+                part += dpp<kQuadPerm2301>(part);
+                const int pos = base + 16 * g + q4;
+                if (g == r) s_own = pos < t1 ? part : -INFINITY;
+            }
+            // the tile has a valid position, so tmax and m_new are finite
+            const float tmax = wave_max(s_own);
+            const float m_new = fmaxf(m[j], tmax);
+            const float cf = exp2f(m[j] - m_new);
+            const float p = exp2f(s_own - m_new);
+            l[j] = __builtin_fmaf(l[j], cf, p);
+            m[j] = m_new;
+            const float p0 = dpp<0x00>(p);  // quad_perm [0,0,0,0]: weight of position 16 * 0 + q
+            const float p1 = dpp<0x55>(p);  // quad_perm [1,1,1,1]: weight of position 16 * 1 + q
+#pragma unroll
+            for (int i = 0; i < NQ; ++i) {
+                f32x4 a = acc[j][i] * cf;
+                a.x = __builtin_fmaf(p0, vv[0][i].x, a.x);
+                a.y = __builtin_fmaf(p0, vv[0][i].y, a.y);
+                a.z = __builtin_fmaf(p0, vv[0][i].z, a.z);
+                a.w = __builtin_fmaf(p0, vv[0][i].w, a.w);
+                a.x = __builtin_fmaf(p1, vv[1][i].x, a.x);
+                a.y = __builtin_fmaf(p1, vv[1][i].y, a.y);
+                a.z = __builtin_fmaf(p1, vv[1][i].z, a.z);
+                a.w = __builtin_fmaf(p1, vv[1][i].w, a.w);
+                acc[j][i] = a;
+            }
+        }
+    }
+
+    // sums over the 16 quads (lanes with the same r) and, for l, over all lanes
+    const int stride = D + 4;  // record: m, l, 2 pad, acc[D] (16-byte aligned)
+#pragma unroll
+    for (int j = 0; j < HQ; ++j) {
+        const int hg = hq * 4 + wave * HQ + j;
+        const float lsum = group_sum_t<6>(l[j]);
+        float* rec = ws + (static_cast<long>(kvh * G + min(hg, G - 1)) * nchunks + c) * stride;
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) {
+            f32x4 a = acc[j][i];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float v = a[e];
+                v += dpp<0x124>(v);  // row_ror:4
+                v += dpp<0x128>(v);  // row_ror:8
+                v += swizzle_xor16(v);
+                v += shfl_xor32(v);
+                a[e] = v;
+            }
+            const int d = 4 * r + 16 * i;
+            if (hg < G && q4 == 0 && d < D) *reinterpret_cast<f32x4*>(rec + 4 + d) = a;
+        }
+        if (hg < G && lane == 0) {
+            rec[0] = m[j];
+            rec[1] = lsum;
+        }
+    }
+}
+
+// out[h][d] = sum_c 2^(m_c - M) acc_c[d] / sum_c 2^(m_c - M) l_c, M = max_c m_c.
+// One wave per head: lanes take the chunks for the max and the sum (their loads
+// are independent), the factors go through LDS, and the accumulator loop over
+// the chunks is unrolled so its loads are in flight together.
+constexpr int kCombineMaxChunks = 4096;
+
+__global__ __launch_bounds__(64) void decode_attn_combine_kernel(const float* __restrict__ ws, float* __restrict__ out,
+                                                                 int D, int nchunks) {
+    __shared__ float fs[kCombineMaxChunks];
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const int stride = D + 4;
+    const float* P = ws + static_cast<long>(h) * nchunks * stride;
+    float mloc = -INFINITY;
+    for (int c = lane; c < nchunks; c += 64) mloc = fmaxf(mloc, P[static_cast<long>(c) * stride]);
+    const float M = wave_max(mloc);
+    float lloc = 0.0f;
+    for (int c = lane; c < nchunks; c += 64) {
+        const float f = exp2f(P[static_cast<long>(c) * stride] - M);
+        fs[c] = f;
+        lloc = __builtin_fmaf(f, P[static_cast<long>(c) * stride + 1], lloc);
+    }
+    const float den = group_sum_t<6>(lloc);
+    __syncthreads();
+    const int d = min(lane, D - 1);
+    float num = 0.0f;
+#pragma unroll 8
+    for (int c = 0; c < nchunks; ++c) num = __builtin_fmaf(fs[c], P[static_cast<long>(c) * stride + 4 + d], num);
+    if (lane < D) out[static_cast<long>(h) * D + lane] = num / den;
+}
+
+}  // namespace dev
+
+namespace detail {
+
+template <int NQ>
+static void launch_att(bool vec, dim3 grid, hipStream_t stream, const float* Q, const float* K, const float* V,
+                       float* out, int G, int kvd, int D, int T, float qscale, int n_slices, int remap) {
+    if (vec)
+        hipLaunchKernelGGL((dev::decode_attn_kernel<NQ, true>), grid, dim3(64 * dev::kAttWaves), 0, stream, Q, K, V,
+                           out, G, kvd, D, T, qscale, n_slices, remap);
+    else
+        hipLaunchKernelGGL((dev::decode_attn_kernel<NQ, false>), grid, dim3(64 * dev::kAttWaves), 0, stream, Q, K, V,
+                           out, G, kvd, D, T, qscale, n_slices, remap);
+}
+
+constexpr int kSplitHeadsPerWave = 1;  // 4 waves per workgroup, one query head each
+
+// Split form: chunk length (a multiple of 32 positions) that gives ~256 workgroups
+// (measured: 512 or 1024 smaller chunks are no faster at 2048 positions, slower
+// at 8192); fewer chunks when the workspace is smaller.
+static int split_chunks(int n_heads, int n_kv_heads, int D, int kv_len, long ws_floats, int* Tc_out) {
+    const int G = n_heads / n_kv_heads, nhq = (G + 3) / 4;
+    const long groups = static_cast<long>(n_kv_heads) * nhq;
+    long tiles = (kv_len + dev::kSplitTile - 1) / dev::kSplitTile;
+    long per = (tiles * groups + 255) / 256;  // tiles per chunk
+    if (per < 1) per = 1;
+    long nchunks = (tiles + per - 1) / per;
+    if (nchunks > dev::kCombineMaxChunks) {  // the combine kernel's factor array
+        per = (tiles + dev::kCombineMaxChunks - 1) / dev::kCombineMaxChunks;
+        nchunks = (tiles + per - 1) / per;
+    }
+    const long rec = static_cast<long>(n_heads) * (D + 4);
+    if (ws_floats >= 0 && nchunks * rec > ws_floats) {
+        nchunks = ws_floats / rec;
+        if (nchunks < 1) return 0;
+        per = (tiles + nchunks - 1) / nchunks;
+        nchunks = (tiles + per - 1) / per;
+    }
+    *Tc_out = static_cast<int>(per * dev::kSplitTile);
+    return static_cast<int>(nchunks);
+}
+
+bool decode_attention_split_supported(const float* Q, const float* K, const float* V, int head_dim) {
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    return head_dim >= 4 && head_dim <= 64 && head_dim % 4 == 0 && a16(Q) && a16(K) && a16(V);
+}
+
+long decode_attention_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int kv_len) {
+    int Tc = 0;
+    const int nchunks = split_chunks(n_heads, n_kv_heads, head_dim, kv_len, -1, &Tc);
+    return static_cast<long>(nchunks) * n_heads * (head_dim + 4) * 4;
+}
+
+int launch_decode_attention_split(const float* Q, const float* K, const float* V, float* out, int n_heads,
+                                  int n_kv_heads, int head_dim, int kv_len, float scale, float* ws, long ws_bytes,
+                                  hipStream_t stream) {
+    const int D = head_dim, G = n_heads / n_kv_heads, nhq = (G + 3) / 4;
+    int Tc = 0;
+    const int nchunks = split_chunks(n_heads, n_kv_heads, D, kv_len, ws_bytes / 4, &Tc);
+    if (nchunks < 1) return -2;  // workspace too small for one record per head
+    const long blocks = static_cast<long>(n_kv_heads) * nhq * nchunks;
+    if (blocks > 0x7FFFFFFFL) return -1;
+    const float qscale = scale * 1.44269504088896341f;
+    hipLaunchKernelGGL(dev::decode_attn_split_kernel<kSplitHeadsPerWave>, dim3(static_cast<unsigned>(blocks)),
+                       dim3(256 / kSplitHeadsPerWave), 0, stream, Q, K, V, ws, G, n_kv_heads * D, D, kv_len, qscale,
+                       Tc, nchunks, nhq);
+    hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads), dim3(64), 0, stream, ws, out, D, nchunks);
+    return 0;
+}
+
+int launch_decode_attention(const float* Q, const float* K, const float* V, float* out, int n_heads, int n_kv_heads,
+                            int head_dim, int kv_len, float scale, hipStream_t stream) {
+    const int D = head_dim;
+    if (D < 1 || D > kDecodeAttnMaxHeadDim || kv_len < 1) return -1;
+    const int G = n_heads / n_kv_heads, kvd = n_kv_heads * D;
+    const int n_slices = (D + dev::kAttDs - 1) / dev::kAttDs;
+    const long blocks = static_cast<long>(n_heads) * n_slices;
+    if (blocks > 0x7FFFFFFFL) return -1;
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    const bool vec = D % 4 == 0 && a16(Q) && a16(K) && a16(V);
+    const int remap = blocks % 8 == 0;
+    const float qscale = scale * 1.44269504088896341f;  // log2(e): the kernel works in base 2
+    const dim3 grid(static_cast<unsigned>(blocks));
+    if (D <= 16) launch_att<1>(vec, grid, stream, Q, K, V, out, G, kvd, D, kv_len, qscale, n_slices, remap);
+    else if (D <= 32) launch_att<2>(vec, grid, stream, Q, K, V, out, G, kvd, D, kv_len, qscale, n_slices, remap);
+    else if (D <= 64) launch_att<4>(vec, grid, stream, Q, K, V, out, G, kvd, D, kv_len, qscale, n_slices, remap);
+    else if (D <= 128) launch_att<8>(vec, grid, stream, Q, K, V, out, G, kvd, D, kv_len, qscale, n_slices, remap);
+    else launch_att<16>(vec, grid, stream, Q, K, V, out, G, kvd, D, kv_len, qscale, n_slices, remap);
+    return 0;
+}
+
+}  // namespace detail
+}  // namespace cri

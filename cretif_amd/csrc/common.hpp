@@ -99,6 +99,17 @@ __device__ __forceinline__ float group_sum(float v, int log2n) {
     return v;
 }
 
+// Maximum over the whole wave; every lane receives it.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp<kQuadPerm1032>(v));
+    v = fmaxf(v, dpp<kQuadPerm2301>(v));
+    v = fmaxf(v, dpp<kRowHalfMirror>(v));
+    v = fmaxf(v, dpp<kRowMirror>(v));
+    v = fmaxf(v, swizzle_xor16(v));
+    v = fmaxf(v, shfl_xor32(v));
+    return v;
+}
+
 template <int LOG2N>
 __device__ __forceinline__ float group_sum_t(float v) {
     if constexpr (LOG2N >= 1) v += dpp<kQuadPerm1032>(v);

@@ -65,6 +65,12 @@ void batched_matmul_gqa(const float* A, const float* B, float* C, int n_heads, i
     CUINFER_CHECK_CRI(cri_batched_matmul_gqa(A, B, C, n_heads, n_kv_heads, M, N, K, s));
 }
 
+void fused_decode_attention(const float* Q, const float* K_cache, const float* V_cache, float* output, int n_heads,
+                            int n_kv_heads, int head_dim, int kv_len, float scale, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_fused_decode_attention(Q, K_cache, V_cache, output, n_heads, n_kv_heads, head_dim, kv_len,
+                                                 scale, s));
+}
+
 // ---------------------------------------------------------------- dispatch
 const char* weight_format_name(WeightFormat fmt) {
     switch (fmt) {

@@ -66,5 +66,17 @@ int launch_transposed_b(const float* A, const float* B, float* C, int M, int N, 
 int launch_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_heads, int M, int N, int K,
                hipStream_t stream);
 
+// fused decode attention over the [kv_len, n_kv_heads, head_dim] cache (attention.hip)
+constexpr int kDecodeAttnMaxHeadDim = 256;
+int launch_decode_attention(const float* Q, const float* K, const float* V, float* out, int n_heads, int n_kv_heads,
+                            int head_dim, int kv_len, float scale, hipStream_t stream);
+// split over positions with partial results in a caller workspace (head_dim <= 64, 4 | head_dim,
+// 16-byte aligned Q/K/V); returns -2 when the workspace cannot hold one record per head
+bool decode_attention_split_supported(const float* Q, const float* K, const float* V, int head_dim);
+long decode_attention_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int kv_len);
+int launch_decode_attention_split(const float* Q, const float* K, const float* V, float* out, int n_heads,
+                                  int n_kv_heads, int head_dim, int kv_len, float scale, float* ws, long ws_bytes,
+                                  hipStream_t stream);
+
 }  // namespace detail
 }  // namespace cri

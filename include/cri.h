@@ -93,6 +93,38 @@ int cri_matmul_transposed_b(const float* A, const float* B, float* C, int M, int
 int cri_batched_matmul_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_heads,
                            int M, int N, int K, hipStream_t stream);
 
+/* out[h, :] = softmax(scale * Q[h, :] . K[t, h / G, :] over t < kv_len) V[t, h / G, :]
+ * for one query token, G = n_heads / n_kv_heads; Q [n_heads, head_dim],
+ * K_cache / V_cache [>= kv_len, n_kv_heads, head_dim] (position stride
+ * n_kv_heads * head_dim), out [n_heads, head_dim], all fp32; replaces
+ * cuinfer::fused_decode_attention, ref:include/cuinfer/attention.h:161-167
+ * (kernel ref:src/attention.cu:410-511).  Checked here: n_heads % n_kv_heads
+ * == 0, kv_len >= 1 (the reference returns NaN for an empty cache) and
+ * head_dim <= 256. */
+int cri_fused_decode_attention(const float* Q, const float* K_cache, const float* V_cache, float* output,
+                               int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale,
+                               hipStream_t stream);
+
+/* Split form of cri_fused_decode_attention, with no counterpart in the
+ * reference: for callers that can keep a device workspace (a decode loop or a
+ * captured graph).  The cache positions are split over workgroups that each
+ * read their K/V rows once for all the query heads of a KV head and write a
+ * partial softmax state (max, sum, accumulator) per head to `workspace`; a
+ * second kernel merges them.  The result equals cri_fused_decode_attention's
+ * to fp32 rounding.  `workspace`: device memory, 16-byte aligned; the call
+ * uses at most cri_fused_decode_attention_workspace_size() bytes of it (fewer
+ * chunks when workspace_bytes is smaller; CRI_ERR_SHAPE below one record per
+ * head).  Calls that share a workspace must be ordered on one stream.  Shapes
+ * the split kernel does not take (head_dim > 64, head_dim % 4 != 0, Q/K/V not
+ * 16-byte aligned) run cri_fused_decode_attention and leave the workspace
+ * untouched. */
+int cri_fused_decode_attention_ws(const float* Q, const float* K_cache, const float* V_cache, float* output,
+                                  int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale,
+                                  void* workspace, long long workspace_bytes, hipStream_t stream);
+/* Workspace bytes cri_fused_decode_attention_ws uses for this shape (0 for an
+ * empty problem; a negative cri_status for invalid arguments). */
+long long cri_fused_decode_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, int kv_len);
+
 /* ---- diagnostics ---------------------------------------------------------- */
 
 /* Message for the last non-zero status returned on this thread ("" if none). */

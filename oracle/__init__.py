@@ -53,6 +53,8 @@ def lib():
         L.orc_matmul_quant.argtypes = [i32, fp, vp, fp, i32, i32, i32]
         L.orc_matmul_transposed_b.argtypes = [fp, fp, fp, i32, i32, i32]
         L.orc_batched_matmul_gqa.argtypes = [fp, fp, fp, i32, i32, i32, i32, i32]
+        for name in ("orc_decode_attention", "orc_decode_attention_online"):
+            getattr(L, name).argtypes = [fp, fp, fp, fp, i32, i32, i32, i32, ctypes.c_float]
         for f in ("q8_0", "q4_0", "q5_0", "q6_k", "q4_k_simple", "q4_k_asym"):
             getattr(L, "orc_quantize_" + f).argtypes = [fp, vp, i64]
         for f in ("q8_0", "q4_0", "q6_k", "q4_k"):
@@ -134,6 +136,33 @@ def batched_matmul_gqa(A, B, n_heads, n_kv_heads, M, N, K):
     C = np.empty((n_heads, M, N), np.float32)
     lib().orc_batched_matmul_gqa(_p(A), _p(B), _p(C), n_heads, n_kv_heads, M, N, K)
     return C
+
+
+def decode_attention(Q, K, V, n_heads, n_kv_heads, head_dim, kv_len, scale, online=False):
+    """One-token attention over the [kv_len, n_kv_heads, head_dim] cache: the
+    reference CPU test's two-pass softmax, or (online=True) the reference kernel's
+    single-pass recurrence.  K and V may hold more positions than kv_len."""
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    assert Q.size >= n_heads * head_dim and K.size >= kv_len * n_kv_heads * head_dim
+    assert V.size >= kv_len * n_kv_heads * head_dim
+    out = np.empty(n_heads * head_dim, np.float32)
+    fn = lib().orc_decode_attention_online if online else lib().orc_decode_attention
+    fn(_p(Q), _p(K), _p(V), _p(out), n_heads, n_kv_heads, head_dim, kv_len, float(scale))
+    return out
+
+
+def np_decode_attention_f64(Q, K, V, n_heads, n_kv_heads, head_dim, kv_len, scale):
+    """fp64 brute force of the same attention (numpy, independent of the C code)."""
+    G = n_heads // n_kv_heads
+    q = np.asarray(Q, np.float64).reshape(n_heads, head_dim)
+    k = np.asarray(K, np.float64).reshape(-1, n_kv_heads, head_dim)[:kv_len]
+    v = np.asarray(V, np.float64).reshape(-1, n_kv_heads, head_dim)[:kv_len]
+    out = np.empty((n_heads, head_dim))
+    for h in range(n_heads):
+        s = k[:, h // G, :] @ q[h] * float(np.float32(scale))
+        w = np.exp(s - s.max())
+        out[h] = (w / w.sum()) @ v[:, h // G, :]
+    return out.ravel()
 
 
 # ---------------------------------------------------------------- quantizers

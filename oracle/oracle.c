@@ -290,6 +290,78 @@ void orc_batched_matmul_gqa(const float* A, const float* B, float* C,
     }
 }
 
+/* Decode attention of one query token over the [kv_len, n_kv_heads, head_dim]
+ * cache, as the reference's CPU test computes it: ref:tests/test_attention.cu:972-1008
+ * (cpu_fused_decode_attention) with cpu_softmax (:110-122).  Scores are
+ * sequential fp32 dot products times scale, the softmax subtracts the max
+ * (starting from -FLT_MAX) and divides each exp by the sum, and the V sum runs
+ * over positions in order. */
+void orc_decode_attention(const float* Q, const float* Kc, const float* Vc, float* out,
+                          int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale) {
+    const int groups = n_heads / n_kv_heads;
+    const int64_t kv_dim = (int64_t)n_kv_heads * head_dim;
+    float* scores = (float*)malloc(sizeof(float) * (size_t)(kv_len > 0 ? kv_len : 1));
+    float* w = (float*)malloc(sizeof(float) * (size_t)(kv_len > 0 ? kv_len : 1));
+    for (int h = 0; h < n_heads; ++h) {
+        const int kvh = h / groups;
+        const float* q = Q + (int64_t)h * head_dim;
+        for (int t = 0; t < kv_len; ++t) {
+            float dot = 0.0f;
+            for (int d = 0; d < head_dim; ++d) dot += q[d] * Kc[t * kv_dim + (int64_t)kvh * head_dim + d];
+            scores[t] = dot * scale;
+        }
+        float max_val = -3.40282347e+38f; /* -FLT_MAX */
+        for (int t = 0; t < kv_len; ++t)
+            if (scores[t] > max_val) max_val = scores[t];
+        float sum_exp = 0.0f;
+        for (int t = 0; t < kv_len; ++t) sum_exp += expf(scores[t] - max_val);
+        for (int t = 0; t < kv_len; ++t) w[t] = expf(scores[t] - max_val) / sum_exp;
+        for (int d = 0; d < head_dim; ++d) {
+            float val = 0.0f;
+            for (int t = 0; t < kv_len; ++t) val += w[t] * Vc[t * kv_dim + (int64_t)kvh * head_dim + d];
+            out[(int64_t)h * head_dim + d] = val;
+        }
+    }
+    free(scores);
+    free(w);
+}
+
+/* The same attention by the reference kernel's single-pass recurrence,
+ * ref:src/attention.cu:446-493: per position, score = dot * scale, running max
+ * m, correction = exp(m_old - m_new), p = exp(score - m_new),
+ * sum = sum * correction + p, acc[d] = acc[d] * correction + p * V[d]; finally
+ * acc[d] * (1 / sum).  The dot is sequential here (the kernel's block
+ * reduction order is not portable). */
+void orc_decode_attention_online(const float* Q, const float* Kc, const float* Vc, float* out,
+                                 int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale) {
+    const int groups = n_heads / n_kv_heads;
+    const int64_t kv_dim = (int64_t)n_kv_heads * head_dim;
+    float* acc = (float*)malloc(sizeof(float) * (size_t)(head_dim > 0 ? head_dim : 1));
+    for (int h = 0; h < n_heads; ++h) {
+        const int kvh = h / groups;
+        const float* q = Q + (int64_t)h * head_dim;
+        float max_score = -INFINITY, sum_exp = 0.0f;
+        for (int d = 0; d < head_dim; ++d) acc[d] = 0.0f;
+        for (int t = 0; t < kv_len; ++t) {
+            const float* k = Kc + t * kv_dim + (int64_t)kvh * head_dim;
+            const float* v = Vc + t * kv_dim + (int64_t)kvh * head_dim;
+            float dot = 0.0f;
+            for (int d = 0; d < head_dim; ++d) dot += q[d] * k[d];
+            const float score = dot * scale;
+            const float old_max = max_score;
+            const float new_max = fmaxf(old_max, score);
+            const float correction = expf(old_max - new_max);
+            const float exp_score = expf(score - new_max);
+            max_score = new_max;
+            sum_exp = sum_exp * correction + exp_score;
+            for (int d = 0; d < head_dim; ++d) acc[d] = acc[d] * correction + exp_score * v[d];
+        }
+        const float inv_sum = 1.0f / sum_exp;
+        for (int d = 0; d < head_dim; ++d) out[(int64_t)h * head_dim + d] = acc[d] * inv_sum;
+    }
+    free(acc);
+}
+
 /* ---------------------------------------------------------------------------
  * Host quantizers (ref:tests/test_matmul_quant.cu).  std::round is roundf
  * (half away from zero); __float2half is round-to-nearest-even.

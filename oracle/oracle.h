@@ -20,6 +20,11 @@
  *                         2^k codes per field.
  *   orc_matmul_*        : fp64 brute force with an error bound, exact-integer
  *                         KATs (every partial sum exact), linearity, one-hot.
+ *   orc_decode_attention*: the two reference formulations against each other,
+ *                         an fp64 brute force with an error bound, and closed
+ *                         forms (kv_len 1 -> V[0]; equal scores -> mean of V;
+ *                         one dominant score -> its V row; a position
+ *                         permutation leaves the output unchanged).
  *   orc_quantize_*      : bit-exact vs the numpy quantizers in cretif_amd/quant.py
  *                         (written separately) and round-trip error bounds.
  */
@@ -64,6 +69,14 @@ void orc_matmul_transposed_b(const float* A, const float* B, float* C, int M, in
 /* ref:tests/test_attention.cu:76-85 (cpu_matmul) + :399-407 (GQA mapping) */
 void orc_batched_matmul_gqa(const float* A, const float* B, float* C,
                             int n_heads, int n_kv_heads, int M, int N, int K);
+
+/* one-token decode attention, cache layout [kv_len, n_kv_heads, head_dim]:
+ * two-pass softmax of ref:tests/test_attention.cu:972-1008 (+ cpu_softmax :110-122) */
+void orc_decode_attention(const float* Q, const float* Kc, const float* Vc, float* out,
+                          int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale);
+/* the reference kernel's online recurrence, ref:src/attention.cu:446-493 */
+void orc_decode_attention_online(const float* Q, const float* Kc, const float* Vc, float* out,
+                                 int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale);
 
 /* host quantizers restated from ref:tests/test_matmul_quant.cu */
 void orc_quantize_q8_0(const float* x, void* dst, int64_t n);        /* :46-71   */

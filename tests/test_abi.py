@@ -16,7 +16,7 @@ def header_functions():
     for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
         if h.endswith(".h"):
             text = open(os.path.join(ROOT, "include", h)).read()
-            names += re.findall(r"^\s*(?:int|const char\*)\s+(cri_\w+)\s*\(", text, re.M)
+            names += re.findall(r"^\s*(?:int|long long|const char\*)\s+(cri_\w+)\s*\(", text, re.M)
     return names
 
 
@@ -110,3 +110,46 @@ def test_cpu_tensor_rejected():
     A = torch.zeros(1, 32)
     with pytest.raises(ValueError):
         cri.matmul_q8_0(A, A, A, 1, 1, 32, stream=0)
+
+
+def test_decode_attention_validation():
+    f = cri.fused_decode_attention
+    for args, status in [
+        ((32, 8, 64, 0), -2),      # empty cache (the reference would return NaN)
+        ((6, 4, 64, 10), -2),      # n_heads not a multiple of n_kv_heads
+        ((4, 0, 64, 10), -2),
+        ((4, 4, 257, 10), -2),     # head_dim above the kernel's limit
+        ((4, 4, -1, 10), -1),
+        ((4, 4, 64, -5), -1),
+    ]:
+        with pytest.raises(cri.CretifError) as e:
+            f(FAKE, FAKE, FAKE, FAKE, *args, 0.125, stream=0)
+        assert e.value.status == status, args
+    with pytest.raises(cri.CretifError) as e:
+        f(0, FAKE, FAKE, FAKE, 4, 4, 64, 10, 0.125, stream=0)
+    assert e.value.status == -1
+    with pytest.raises(cri.CretifError) as e:
+        f(FAKE, FAKE + 2, FAKE, FAKE, 4, 4, 64, 10, 0.125, stream=0)
+    assert e.value.status == -3
+    f(0, 0, 0, 0, 0, 8, 64, 10, 0.125, stream=0)  # no heads: nothing to do
+
+
+def test_decode_attention_ws_validation():
+    assert cri.decode_attention_workspace_size(32, 8, 64, 2048) > 0
+    assert cri.decode_attention_workspace_size(0, 8, 64, 2048) == 0
+    with pytest.raises(cri.CretifError) as e:
+        cri.decode_attention_workspace_size(6, 4, 64, 10)
+    assert e.value.status == -2
+    f = cri.fused_decode_attention_ws
+    with pytest.raises(cri.CretifError) as e:   # argument errors are reported as in the workspace-free form
+        f(FAKE, FAKE, FAKE, FAKE, 32, 8, 64, 0, 0.125, FAKE, 1 << 20, stream=0)
+    assert e.value.status == -2 and "cri_fused_decode_attention_ws" in str(e.value)
+    with pytest.raises(cri.CretifError) as e:
+        f(FAKE, FAKE, FAKE, FAKE, 32, 8, 64, 100, 0.125, 0, 1 << 20, stream=0)
+    assert e.value.status == -1
+    with pytest.raises(cri.CretifError) as e:
+        f(FAKE, FAKE, FAKE, FAKE, 32, 8, 64, 100, 0.125, FAKE + 4, 1 << 20, stream=0)
+    assert e.value.status == -3
+    with pytest.raises(cri.CretifError) as e:   # not even one record per head
+        f(FAKE, FAKE, FAKE, FAKE, 32, 8, 64, 100, 0.125, FAKE, 100, stream=0)
+    assert e.value.status == -2
