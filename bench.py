@@ -143,16 +143,22 @@ class DecodeStepRig:
     of a layer are stored as one [3072, 2048] matrix and gate/up as one
     [16384, 2048] matrix, so a layer is 4 weight launches (same bytes, fewer
     launches).  Buffers are reused between layers: the timing covers the
-    products at their real shapes; the values are not chained semantically."""
+    products at their real shapes; the values are not chained semantically.
+    attention='fused' (M = 1) replaces the two GQA products by the fused decode
+    attention (softmax included) over a [T, 8, 64] cache, in its split form
+    with a preallocated workspace, as the reference's decode path calls
+    fused_decode_attention (ref:src/model.cu:928-943)."""
 
     LAYERS, D, H, HKV, HD, FF, VOCAB, T = 16, 2048, 32, 8, 64, 8192, 128256, 2048
 
-    def __init__(self, M, seed=1100):
+    def __init__(self, M, seed=1100, attention="gqa"):
         import torch
 
         import cretif_amd as cri
 
-        self.M = M
+        if attention not in ("gqa", "fused") or (attention == "fused" and M != 1):
+            raise ValueError("attention is 'gqa', or 'fused' for M = 1 (one query token)")
+        self.M, self.attention = M, attention
         D, FF, T, H, HKV, HD = self.D, self.FF, self.T, self.H, self.HKV, self.HD
         shapes = {"qkv": (D + 2 * HKV * HD, D), "o": (D, D), "gateup": (2 * FF, D), "down": (D, FF)}
         base = {name: torch.from_numpy(tiled_weights("q4_k", n, k, seed + i)).cuda()
@@ -161,8 +167,15 @@ class DecodeStepRig:
         del base
         self.lm_head = torch.from_numpy(tiled_weights("q6_k", self.VOCAB, D, seed + 99)).cuda()
         g = torch.Generator(device="cuda").manual_seed(3000)
-        self.kT = [torch.randn(HKV, HD, T, device="cuda", generator=g) for _ in range(self.LAYERS)]  # K^T per KV head
-        self.vc = [torch.randn(HKV, T, HD, device="cuda", generator=g) for _ in range(self.LAYERS)]
+        if attention == "gqa":
+            # batched_matmul_gqa operands: K^T [Hkv, HD, T] and V [Hkv, T, HD] per layer
+            self.kT = [torch.randn(HKV, HD, T, device="cuda", generator=g) for _ in range(self.LAYERS)]
+            self.vc = [torch.randn(HKV, T, HD, device="cuda", generator=g) for _ in range(self.LAYERS)]
+        else:
+            # fused decode attention reads the cache layout [T, Hkv, HD] directly
+            self.kT = [torch.randn(T, HKV, HD, device="cuda", generator=g) for _ in range(self.LAYERS)]
+            self.vc = [torch.randn(T, HKV, HD, device="cuda", generator=g) for _ in range(self.LAYERS)]
+            self.ws = torch.empty(cri.decode_attention_workspace_size(H, HKV, HD, T) // 4, device="cuda")
         self.x = torch.randn(M, D, device="cuda", generator=g)
         self.qkv = torch.empty(M, D + 2 * HKV * HD, device="cuda")
         self.scores = torch.empty(H, M, T, device="cuda")
@@ -187,9 +200,15 @@ class DecodeStepRig:
         x = self.x
         for li, L in enumerate(self.layers):
             cri.matmul("q4_k", x, L["qkv"], self.qkv, M, D + 2 * HKV * HD, D)
-            # the first 32*M*64 values of the qkv output read as [32, M, 64] queries
-            cri.batched_matmul_gqa(self.qkv, self.kT[li], self.scores, H, HKV, M, T, HD)
-            cri.batched_matmul_gqa(self.scores, self.vc[li], self.ctx, H, HKV, M, HD, T)
+            if self.attention == "gqa":
+                # the first 32*M*64 values of the qkv output read as [32, M, 64] queries
+                cri.batched_matmul_gqa(self.qkv, self.kT[li], self.scores, H, HKV, M, T, HD)
+                cri.batched_matmul_gqa(self.scores, self.vc[li], self.ctx, H, HKV, M, HD, T)
+            else:
+                # softmax(q K^T / 8) V in one fused call (its split form; the q rows are the
+                # first 32 * 64 values of the qkv output)
+                cri.fused_decode_attention_ws(self.qkv, self.kT[li], self.vc[li], self.ctx, H, HKV, HD, T, 0.125,
+                                              self.ws)
             cri.matmul("q4_k", self.ctx, L["o"], self.h, M, D, D)
             cri.matmul("q4_k", self.h, L["gateup"], self.ff, M, 2 * FF, D)
             # the first M*8192 values of the gate/up output read as the [M, 8192] down input
@@ -214,6 +233,70 @@ class DecodeStepRig:
 
     def free(self):
         self.layers = self.lm_head = self.kT = self.vc = self.graph = None
+
+
+class AttentionRig:
+    """Fused decode attention of one token (32 query heads over 8 KV heads,
+    head_dim 64) over an fp32 cache of T positions in the [T, 8, 64] layout, for
+    `copies` distinct caches (>= 2 x the MALL) captured in one graph and replayed.
+    form 'plain' is cri_fused_decode_attention (reference signature), 'ws' its
+    split form with a workspace."""
+
+    H, HKV, HD = 32, 8, 64
+
+    def __init__(self, form, T=2048, min_bytes=2 * MALL_BYTES):
+        import torch
+
+        import cretif_amd as cri
+
+        H, HKV, HD = self.H, self.HKV, self.HD
+        self.T, self.form = T, form
+        cache = T * HKV * HD * 4
+        self.copies = int(max(2, -(-min_bytes // (2 * cache))))
+        g = torch.Generator(device="cuda").manual_seed(3000)
+        self.K = [torch.randn(T, HKV, HD, device="cuda", generator=g) for _ in range(self.copies)]
+        self.V = [torch.randn(T, HKV, HD, device="cuda", generator=g) for _ in range(self.copies)]
+        self.q = torch.randn(H * HD, device="cuda", generator=g)
+        self.out = torch.empty(H * HD, device="cuda")
+        self.ws = torch.empty(max(4, cri.decode_attention_workspace_size(H, HKV, HD, T) // 4), device="cuda")
+
+        def run():
+            for k, v in zip(self.K, self.V):
+                if form == "plain":
+                    cri.fused_decode_attention(self.q, k, v, self.out, H, HKV, HD, T, 0.125)
+                else:
+                    cri.fused_decode_attention_ws(self.q, k, v, self.out, H, HKV, HD, T, 0.125, self.ws)
+
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):
+            run()
+        side.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=side):
+            run()
+        torch.cuda.synchronize()
+
+    def bytes_per_call(self):
+        # algorithmic: q, out and every K and V value of the T positions, once
+        return 4 * (2 * self.H * self.HD + 2 * self.T * self.HKV * self.HD)
+
+    def time(self, reps=20):
+        """ms per call."""
+        import torch
+
+        self.graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            self.graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / (reps * self.copies)
+
+    def free(self):
+        self.K = self.V = self.graph = None
 
 
 def measured_traffic(workload):
@@ -272,6 +355,10 @@ def main():
                     help="only time one prefill GEMM workload (for profiling) and print its figures")
     ap.add_argument("--decode-step", type=int, default=None, metavar="M",
                     help="only time the synthetic decode step for M tokens (for profiling)")
+    ap.add_argument("--step-attention", default="gqa", choices=["gqa", "fused"],
+                    help="attention of --decode-step: the two GQA products (default) or the fused kernel (M = 1)")
+    ap.add_argument("--attention", default=None, choices=["plain", "ws"],
+                    help="only time the fused decode attention at 2048 positions (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run ten 64 MiB device copies (known bytes, for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -297,10 +384,18 @@ def main():
     import cretif_amd as cri
 
     cri.lib()
+    if args.attention:
+        r = AttentionRig(args.attention)
+        ms_call = r.time(reps=max(3, args.steps // r.copies))
+        print(json.dumps({"workload": "decode_attention_" + args.attention, "T": r.T, "calls": r.copies,
+                          "us": round(ms_call * 1e3, 3),
+                          "GB/s": round(r.bytes_per_call() / (ms_call * 1e-3) / 1e9, 1)}))
+        return
     if args.decode_step:
-        r = DecodeStepRig(args.decode_step)
+        r = DecodeStepRig(args.decode_step, attention=args.step_attention)
         ms_step = r.time(reps=max(3, args.steps // 1000))
-        print(json.dumps({"workload": "decode_step", "M": args.decode_step, "ms_per_step": round(ms_step, 4),
+        print(json.dumps({"workload": "decode_step", "M": args.decode_step, "attention": args.step_attention,
+                          "ms_per_step": round(ms_step, 4),
                           "tokens/s": round(args.decode_step / (ms_step * 1e-3), 1)}))
         return
     if args.prefill:
@@ -338,10 +433,19 @@ def main():
                                  2.0 * m_ * n * k / (m * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4)}
             r.free()
             torch.cuda.empty_cache()
-        for m_ in (1, 16):
-            r = DecodeStepRig(m_)
+        for form in ("plain", "ws"):
+            r = AttentionRig(form)
+            ms_call = r.time()
+            details["decode_attention_%s_T2048" % form] = {
+                "us": round(ms_call * 1e3, 3), "GB/s": round(r.bytes_per_call() / (ms_call * 1e-3) / 1e9, 1),
+                "copies": r.copies}
+            r.free()
+            torch.cuda.empty_cache()
+        for m_, attn in ((1, "gqa"), (16, "gqa"), (1, "fused")):
+            r = DecodeStepRig(m_, attention=attn)
             ms_step = r.time()
-            details["decode_step_m%d" % m_] = {
+            key = "decode_step_m%d" % m_ + ("_fused_attention" if attn == "fused" else "")
+            details[key] = {
                 "tokens/s": round(m_ / (ms_step * 1e-3), 1), "ms_per_step": round(ms_step, 4),
                 "weight_GB/s": round(r.weight_bytes / (ms_step * 1e-3) / 1e9, 1),
                 "weight+kv_GB/s": round((r.weight_bytes + r.kv_bytes) / (ms_step * 1e-3) / 1e9, 1)}
