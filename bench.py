@@ -151,14 +151,16 @@ class DecodeStepRig:
 
     LAYERS, D, H, HKV, HD, FF, VOCAB, T = 16, 2048, 32, 8, 64, 8192, 128256, 2048
 
-    def __init__(self, M, seed=1100, attention="gqa"):
+    def __init__(self, M, seed=1100, attention="gqa", elementwise="none"):
         import torch
 
         import cretif_amd as cri
 
         if attention not in ("gqa", "fused") or (attention == "fused" and M != 1):
             raise ValueError("attention is 'gqa', or 'fused' for M = 1 (one query token)")
-        self.M, self.attention = M, attention
+        if elementwise not in ("none", "separate", "fused") or (elementwise == "separate" and M != 1):
+            raise ValueError("elementwise is 'none', 'fused', or 'separate' for M = 1")
+        self.M, self.attention, self.elementwise = M, attention, elementwise
         D, FF, T, H, HKV, HD = self.D, self.FF, self.T, self.H, self.HKV, self.HD
         shapes = {"qkv": (D + 2 * HKV * HD, D), "o": (D, D), "gateup": (2 * FF, D), "down": (D, FF)}
         base = {name: torch.from_numpy(tiled_weights("q4_k", n, k, seed + i)).cuda()
@@ -182,6 +184,14 @@ class DecodeStepRig:
         self.ctx = torch.empty(H, M, HD, device="cuda")
         self.h = torch.empty(M, D, device="cuda")
         self.ff = torch.empty(M, 2 * FF, device="cuda")
+        # residual stream and norms (elementwise != "none"): two hidden buffers (the fused
+        # form writes hidden + residual to the other one), RMSNorm weights ~ 1 + N(0, 0.1)
+        self.hid = [torch.randn(M, D, device="cuda", generator=g) for _ in range(2)]
+        self.attn_out = torch.empty(M, D, device="cuda")
+        self.ffn_out = torch.empty(M, D, device="cuda")
+        self.normed = torch.empty(M, D, device="cuda")
+        self.act = torch.empty(M, FF, device="cuda")
+        self.norm_w = [1.0 + 0.1 * torch.randn(D, device="cuda", generator=g) for _ in range(2 * self.LAYERS + 1)]
         self.logits = torch.empty(M, self.VOCAB, device="cuda")
         self.weight_bytes = sum(t.numel() for L in self.layers for t in L.values()) + self.lm_head.numel()
         self.kv_bytes = sum(t.numel() * 4 for t in self.kT) + sum(t.numel() * 4 for t in self.vc)
@@ -196,25 +206,68 @@ class DecodeStepRig:
         torch.cuda.synchronize()
 
     def step(self):
-        cri, M, D, FF, H, HKV, HD, T = self.cri, self.M, self.D, self.FF, self.H, self.HKV, self.HD, self.T
+        if self.elementwise != "none":
+            return self.step_with_norms()
+        cri, M, D, FF, HKV, HD = self.cri, self.M, self.D, self.FF, self.HKV, self.HD
         x = self.x
         for li, L in enumerate(self.layers):
             cri.matmul("q4_k", x, L["qkv"], self.qkv, M, D + 2 * HKV * HD, D)
-            if self.attention == "gqa":
-                # the first 32*M*64 values of the qkv output read as [32, M, 64] queries
-                cri.batched_matmul_gqa(self.qkv, self.kT[li], self.scores, H, HKV, M, T, HD)
-                cri.batched_matmul_gqa(self.scores, self.vc[li], self.ctx, H, HKV, M, HD, T)
-            else:
-                # softmax(q K^T / 8) V in one fused call (its split form; the q rows are the
-                # first 32 * 64 values of the qkv output)
-                cri.fused_decode_attention_ws(self.qkv, self.kT[li], self.vc[li], self.ctx, H, HKV, HD, T, 0.125,
-                                              self.ws)
+            # the first 32*M*64 values of the qkv output read as [32, M, 64] queries; 'fused' is
+            # softmax(q K^T / 8) V in one call (its split form)
+            self.attend(li)
             cri.matmul("q4_k", self.ctx, L["o"], self.h, M, D, D)
             cri.matmul("q4_k", self.h, L["gateup"], self.ff, M, 2 * FF, D)
             # the first M*8192 values of the gate/up output read as the [M, 8192] down input
             cri.matmul("q4_k", self.ff, L["down"], self.h, M, D, FF)
             x = self.h
         cri.matmul("q6_k", x, self.lm_head, self.logits, M, self.VOCAB, D)
+
+    def attend(self, li):
+        cri, M, H, HKV, HD, T = self.cri, self.M, self.H, self.HKV, self.HD, self.T
+        if self.attention == "gqa":
+            cri.batched_matmul_gqa(self.qkv, self.kT[li], self.scores, H, HKV, M, T, HD)
+            cri.batched_matmul_gqa(self.scores, self.vc[li], self.ctx, H, HKV, M, HD, T)
+        else:
+            cri.fused_decode_attention_ws(self.qkv, self.kT[li], self.vc[li], self.ctx, H, HKV, HD, T, 0.125, self.ws)
+
+    def step_with_norms(self):
+        """The layer with its elementwise neighbours, as the reference's decode loop runs it
+        (ref:src/model.cu:894-1018): h += ffn_out; n = RMSNorm(h); q/k/v; attention; o;
+        h += attn_out; n = RMSNorm(h); gate/up; silu(gate) * up; down; and after the last
+        layer h += ffn_out; n = RMSNorm(h); lm_head.  'separate' launches rmsnorm_residual
+        and silu_mul; 'fused' folds them into the next matmul's activation staging."""
+        cri, M, D, FF, HKV, HD = self.cri, self.M, self.D, self.FF, self.HKV, self.HD
+        fused = self.elementwise == "fused"
+        cur, res = 0, None  # hidden buffer in use; residual still to be added (none before layer 0)
+        eps = 1e-5
+
+        def norm_then(w, Wq, out, N, fmt="q4_k"):
+            nonlocal cur
+            if fused:
+                cri.matmul_rmsnorm(fmt, self.hid[cur], res, w, self.hid[1 - cur], Wq, out, M, N, D, eps)
+                cur = 1 - cur
+            else:
+                cri.rmsnorm_residual(self.hid[cur], res, w, self.hid[cur], self.normed, M, D, eps)
+                cri.matmul(fmt, self.normed, Wq, out, M, N, D)
+
+        for li, L in enumerate(self.layers):
+            norm_then(self.norm_w[2 * li], L["qkv"], self.qkv, D + 2 * HKV * HD)
+            self.attend(li)
+            cri.matmul("q4_k", self.ctx, L["o"], self.attn_out, M, D, D)
+            res = self.attn_out
+            norm_then(self.norm_w[2 * li + 1], L["gateup"], self.ff, 2 * FF)
+            if fused:
+                cri.matmul_swiglu("q4_k", self.ff, self.ff.data_ptr() + 4 * FF, 2 * FF, L["down"], self.ffn_out, M,
+                                  D, FF)
+            else:
+                cri.silu_mul(self.ff, self.ff.data_ptr() + 4 * FF, self.act, M * FF)  # M = 1
+                cri.matmul("q4_k", self.act, L["down"], self.ffn_out, M, D, FF)
+            res = self.ffn_out
+        if fused:
+            cri.matmul_rmsnorm("q6_k", self.hid[cur], res, self.norm_w[-1], None, self.lm_head, self.logits, M,
+                               self.VOCAB, D, eps)
+        else:
+            norm_then(self.norm_w[-1], self.lm_head, self.logits, self.VOCAB, fmt="q6_k")
 
     def time(self, reps=20, warmup=3):
         import torch
@@ -357,6 +410,8 @@ def main():
                     help="only time the synthetic decode step for M tokens (for profiling)")
     ap.add_argument("--step-attention", default="gqa", choices=["gqa", "fused"],
                     help="attention of --decode-step: the two GQA products (default) or the fused kernel (M = 1)")
+    ap.add_argument("--step-elementwise", default="none", choices=["none", "separate", "fused"],
+                    help="--decode-step with the layer's RMSNorm / SiLU work: separate launches or fused prologues")
     ap.add_argument("--attention", default=None, choices=["plain", "ws"],
                     help="only time the fused decode attention at 2048 positions (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -392,9 +447,10 @@ def main():
                           "GB/s": round(r.bytes_per_call() / (ms_call * 1e-3) / 1e9, 1)}))
         return
     if args.decode_step:
-        r = DecodeStepRig(args.decode_step, attention=args.step_attention)
+        r = DecodeStepRig(args.decode_step, attention=args.step_attention, elementwise=args.step_elementwise)
         ms_step = r.time(reps=max(3, args.steps // 1000))
         print(json.dumps({"workload": "decode_step", "M": args.decode_step, "attention": args.step_attention,
+                          "elementwise": args.step_elementwise,
                           "ms_per_step": round(ms_step, 4),
                           "tokens/s": round(args.decode_step / (ms_step * 1e-3), 1)}))
         return
@@ -441,10 +497,12 @@ def main():
                 "copies": r.copies}
             r.free()
             torch.cuda.empty_cache()
-        for m_, attn in ((1, "gqa"), (16, "gqa"), (1, "fused")):
-            r = DecodeStepRig(m_, attention=attn)
+        for m_, attn, ew in ((1, "gqa", "none"), (16, "gqa", "none"), (1, "fused", "none"), (1, "fused", "separate"),
+                             (1, "fused", "fused"), (16, "gqa", "fused")):
+            r = DecodeStepRig(m_, attention=attn, elementwise=ew)
             ms_step = r.time()
-            key = "decode_step_m%d" % m_ + ("_fused_attention" if attn == "fused" else "")
+            key = "decode_step_m%d" % m_ + ("_fused_attention" if attn == "fused" else "") + (
+                "" if ew == "none" else "_norms_" + ew)
             details[key] = {
                 "tokens/s": round(m_ / (ms_step * 1e-3), 1), "ms_per_step": round(ms_step, 4),
                 "weight_GB/s": round(r.weight_bytes / (ms_step * 1e-3) / 1e9, 1),

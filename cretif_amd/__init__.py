@@ -40,6 +40,10 @@ __all__ = [
     "fused_decode_attention",
     "fused_decode_attention_ws",
     "decode_attention_workspace_size",
+    "matmul_rmsnorm",
+    "matmul_swiglu",
+    "rmsnorm_residual",
+    "silu_mul",
     "FORMAT_IDS",
     "ABI_SYMBOLS",
 ]
@@ -69,6 +73,10 @@ ABI_SYMBOLS = (
         "cri_fused_decode_attention",
         "cri_fused_decode_attention_ws",
         "cri_fused_decode_attention_workspace_size",
+        "cri_matmul_rmsnorm",
+        "cri_matmul_swiglu",
+        "cri_rmsnorm_residual",
+        "cri_silu_mul",
         "cri_last_error_string",
         "cri_block_bytes",
         "cri_block_elems",
@@ -120,6 +128,14 @@ def lib():
     L.cri_fused_decode_attention_ws.restype = i32
     L.cri_fused_decode_attention_workspace_size.argtypes = [i32, i32, i32, i32]
     L.cri_fused_decode_attention_workspace_size.restype = ctypes.c_longlong
+    L.cri_matmul_rmsnorm.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i32, i32, ctypes.c_float, vp]
+    L.cri_matmul_rmsnorm.restype = i32
+    L.cri_matmul_swiglu.argtypes = [i32, vp, vp, i32, vp, vp, i32, i32, i32, vp]
+    L.cri_matmul_swiglu.restype = i32
+    L.cri_rmsnorm_residual.argtypes = [vp, vp, vp, vp, vp, i32, i32, ctypes.c_float, vp]
+    L.cri_rmsnorm_residual.restype = i32
+    L.cri_silu_mul.argtypes = [vp, vp, vp, ctypes.c_longlong, vp]
+    L.cri_silu_mul.restype = i32
     L.cri_last_error_string.argtypes = []
     L.cri_last_error_string.restype = ctypes.c_char_p
     L.cri_block_bytes.argtypes = [i32]
@@ -276,3 +292,38 @@ def fused_decode_attention_ws(Q, K_cache, V_cache, output, n_heads, n_kv_heads, 
             _stream(stream),
         )
     )
+
+
+def _fid(fmt):
+    return FORMAT_IDS[fmt] if isinstance(fmt, str) else int(fmt)
+
+
+def matmul_rmsnorm(fmt, hidden, residual, norm_weight, hidden_out, B, C, M, N, K, eps=1e-5, stream=None):
+    """C = RMSNorm(hidden + residual) * dequant(B)^T with hidden + residual written to
+    hidden_out (either of residual / hidden_out may be None); decode batches M <= 16."""
+    _check(
+        lib().cri_matmul_rmsnorm(
+            _fid(fmt), _ptr(hidden), _ptr(residual), _ptr(norm_weight), _ptr(hidden_out), _ptr(B), _ptr(C),
+            M, N, K, float(eps), _stream(stream),
+        )
+    )
+
+
+def matmul_swiglu(fmt, gate, up, ld, B, C, M, N, K, stream=None):
+    """C = (silu(gate) * up) * dequant(B)^T, gate/up rows ld floats apart; decode batches M <= 16."""
+    _check(lib().cri_matmul_swiglu(_fid(fmt), _ptr(gate), _ptr(up), ld, _ptr(B), _ptr(C), M, N, K, _stream(stream)))
+
+
+def rmsnorm_residual(input, residual, weight, output, normed, rows, n, eps=1e-5, stream=None):
+    """output = input + residual; normed = RMSNorm(output) * weight (replaces cuinfer::rmsnorm_residual)."""
+    _check(
+        lib().cri_rmsnorm_residual(
+            _ptr(input), _ptr(residual), _ptr(weight), _ptr(output), _ptr(normed), rows, n, float(eps),
+            _stream(stream),
+        )
+    )
+
+
+def silu_mul(gate, up, out, n, stream=None):
+    """out = silu(gate) * up (cuinfer::silu then cuinfer::multiply, as one launch)."""
+    _check(lib().cri_silu_mul(_ptr(gate), _ptr(up), _ptr(out), int(n), _stream(stream)))

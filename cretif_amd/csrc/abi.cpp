@@ -200,6 +200,98 @@ int cri_fused_decode_attention(const float* Q, const float* K_cache, const float
     return check_launch(fn);
 }
 
+namespace {
+
+bool overlaps(const void* a, long abytes, const void* b, long bbytes) {
+    if (!a || !b || abytes <= 0 || bbytes <= 0) return false;
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + static_cast<uintptr_t>(bbytes) && y < x + static_cast<uintptr_t>(abytes);
+}
+
+// Batches up to this many rows take the fused activation prologues (decode).
+constexpr int kFusedMaxM = 16;
+
+int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float* C, int M, int N, int K,
+                 hipStream_t stream, const char* fn) {
+    if (fmt < cri::kFmtQ8_0 || fmt > cri::kFmtF16) return fail(CRI_ERR_UNSUPPORTED, fn, "unknown format id");
+    if (M < 0 || N < 0 || K < 0) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative dimension");
+    const int be = cri::block_elems(fmt);
+    if (K % be != 0 || (fmt == cri::kFmtF16 && K % 32 != 0))
+        return fail(CRI_ERR_SHAPE, fn, "K=" + std::to_string(K) + " is not a multiple of the block size");
+    if (M == 0 || N == 0) return CRI_OK;
+    if (M > kFusedMaxM)
+        return fail(CRI_ERR_UNSUPPORTED, fn,
+                    "the fused prologue serves decode batches (M <= 16); for M=" + std::to_string(M) +
+                        " run cri_rmsnorm_residual / cri_silu_mul, then cri_matmul");
+    if (!B || !C) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(C, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "C must be 4-byte aligned");
+    if (fmt == cri::kFmtF16 && !aligned(B, 2)) return fail(CRI_ERR_ALIGNMENT, fn, "FP16 B must be 2-byte aligned");
+    int rc = -1;
+    if (cri::detail::skinny_supported(fmt, M, K, B))
+        rc = cri::detail::launch_skinny_act(mode, fmt, act, B, C, M, N, K, stream);
+    if (rc != 0 && M == 1 && cri::detail::gemv_supported(fmt, K, B))
+        rc = cri::detail::launch_gemv_act(mode, fmt, act, B, C, N, K, stream);
+    if (rc != 0) rc = cri::detail::launch_generic_matmul_act(mode, fmt, act, B, C, M, N, K, stream);
+    if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
+    return check_launch(fn);
+}
+
+}  // namespace
+
+int cri_matmul_rmsnorm(int format, const float* hidden, const float* residual, const float* norm_weight,
+                       float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, hipStream_t s) {
+    const char* fn = "cri_matmul_rmsnorm";
+    if (M > 0 && N > 0 && K == 0) return fail(CRI_ERR_SHAPE, fn, "K=0: the RMS of an empty row is undefined");
+    if (M > 0 && N > 0 && K > 0) {
+        if (!hidden || !norm_weight) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null hidden or norm_weight");
+        if (!aligned(hidden, 4) || !aligned(residual, 4) || !aligned(norm_weight, 4) || !aligned(hidden_out, 4))
+            return fail(CRI_ERR_ALIGNMENT, fn, "hidden, residual, norm_weight and hidden_out must be 4-byte aligned");
+        const long bytes = static_cast<long>(M) * K * 4;
+        if (overlaps(hidden_out, bytes, hidden, bytes) || overlaps(hidden_out, bytes, residual, bytes))
+            return fail(CRI_ERR_INVALID_ARGUMENT, fn,
+                        "hidden_out overlaps hidden or residual (other workgroups still read them)");
+    }
+    const cri::ActIn act{hidden, residual, norm_weight, hidden_out, K, eps};
+    return fused_matmul(cri::kActRMSNorm, format, act, B, C, M, N, K, s, fn);
+}
+
+int cri_matmul_swiglu(int format, const float* gate, const float* up, int ld, const void* B, float* C, int M, int N,
+                      int K, hipStream_t s) {
+    const char* fn = "cri_matmul_swiglu";
+    if (M > 0 && N > 0 && K > 0) {
+        if (!gate || !up) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null gate or up");
+        if (ld < K) return fail(CRI_ERR_SHAPE, fn, "ld=" + std::to_string(ld) + " is below K=" + std::to_string(K));
+        if (!aligned(gate, 4) || !aligned(up, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "gate and up must be 4-byte aligned");
+    }
+    const cri::ActIn act{gate, up, nullptr, nullptr, ld, 0.0f};
+    return fused_matmul(cri::kActSwiGLU, format, act, B, C, M, N, K, s, fn);
+}
+
+int cri_rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output,
+                         float* normed, int rows, int n, float eps, hipStream_t s) {
+    const char* fn = "cri_rmsnorm_residual";
+    if (rows < 0 || n < 0) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative dimension");
+    if (rows == 0) return CRI_OK;
+    if (n == 0) return fail(CRI_ERR_SHAPE, fn, "n=0: the RMS of an empty row is undefined");
+    if (!input || !weight || !output || !normed) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(input, 4) || !aligned(residual, 4) || !aligned(weight, 4) || !aligned(output, 4) ||
+        !aligned(normed, 4))
+        return fail(CRI_ERR_ALIGNMENT, fn, "all buffers must be 4-byte aligned");
+    cri::detail::launch_rmsnorm_residual(input, residual, weight, output, normed, rows, n, eps, s);
+    return check_launch(fn);
+}
+
+int cri_silu_mul(const float* gate, const float* up, float* out, long long n, hipStream_t s) {
+    const char* fn = "cri_silu_mul";
+    if (n < 0) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative n");
+    if (n == 0) return CRI_OK;
+    if (!gate || !up || !out) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(gate, 4) || !aligned(up, 4) || !aligned(out, 4))
+        return fail(CRI_ERR_ALIGNMENT, fn, "all buffers must be 4-byte aligned");
+    cri::detail::launch_silu_mul(gate, up, out, static_cast<long>(n), s);
+    return check_launch(fn);
+}
+
 long long cri_fused_decode_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, int kv_len) {
     const char* fn = "cri_fused_decode_attention_workspace_size";
     if (n_heads < 0 || n_kv_heads < 0 || head_dim < 0 || kv_len < 0)

@@ -15,6 +15,7 @@
 #include "../../include/cuinfer/dispatch.h"
 #include "../../include/cuinfer/embedding.h"
 #include "../../include/cuinfer/hip_utils.h"
+#include "../../include/cuinfer/kernels/elementwise.h"
 #include "../../include/cuinfer/kernels/matmul_quant.h"
 #include "../../include/cuinfer/quantization.h"
 #include "../../include/cuinfer/tensor.h"
@@ -97,20 +98,44 @@ WeightFormat weight_format_of(DType dtype) {
     }
 }
 
+static int format_id(WeightFormat format, const char* fn) {
+    switch (format) {
+        case WeightFormat::FP16: return CRI_FP16;
+        case WeightFormat::Q8_0: return CRI_Q8_0;
+        case WeightFormat::Q4_0: return CRI_Q4_0;
+        case WeightFormat::Q5_0: return CRI_Q5_0;
+        case WeightFormat::Q4_K: return CRI_Q4_K;
+        case WeightFormat::Q6_K: return CRI_Q6_K;
+        default: break;
+    }
+    throw std::invalid_argument(std::string(fn) + ": FP32 weights ([K,N] pre-transposed) are not handled here");
+}
+
 void matmul_dispatch(const float* A, const Tensor& weight, float* C, int M, int N, int K, WeightFormat format,
                      hipStream_t s) {
-    int id;
-    switch (format) {
-        case WeightFormat::FP16: id = CRI_FP16; break;
-        case WeightFormat::Q8_0: id = CRI_Q8_0; break;
-        case WeightFormat::Q4_0: id = CRI_Q4_0; break;
-        case WeightFormat::Q5_0: id = CRI_Q5_0; break;
-        case WeightFormat::Q4_K: id = CRI_Q4_K; break;
-        case WeightFormat::Q6_K: id = CRI_Q6_K; break;
-        default:
-            throw std::invalid_argument("matmul_dispatch: FP32 weights ([K,N] pre-transposed) are not handled here");
-    }
-    CUINFER_CHECK_CRI(cri_matmul(id, A, weight.data(), C, M, N, K, s));
+    CUINFER_CHECK_CRI(cri_matmul(format_id(format, "matmul_dispatch"), A, weight.data(), C, M, N, K, s));
+}
+
+void matmul_dispatch_rmsnorm(const float* hidden, const float* residual, const float* norm_weight, float* hidden_out,
+                             const Tensor& weight, float* C, int M, int N, int K, WeightFormat format, float eps,
+                             hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_matmul_rmsnorm(format_id(format, "matmul_dispatch_rmsnorm"), hidden, residual, norm_weight,
+                                         hidden_out, weight.data(), C, M, N, K, eps, s));
+}
+
+void matmul_dispatch_swiglu(const float* gate, const float* up, int ld, const Tensor& weight, float* C, int M, int N,
+                            int K, WeightFormat format, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_matmul_swiglu(format_id(format, "matmul_dispatch_swiglu"), gate, up, ld, weight.data(), C,
+                                        M, N, K, s));
+}
+
+void rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output, float* normed,
+                      int rows, int n, float eps, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_rmsnorm_residual(input, residual, weight, output, normed, rows, n, eps, s));
+}
+
+void silu_mul(const float* gate, const float* up, float* out, long long n, hipStream_t s) {
+    CUINFER_CHECK_CRI(cri_silu_mul(gate, up, out, n, s));
 }
 
 // ---------------------------------------------------------------- Tensor

@@ -1,0 +1,66 @@
+// elementwise.hip -- the path's two elementwise neighbours as standalone
+// kernels, for callers that do not fuse them into the next matmul (prefill
+// batches, or any other consumer).
+//
+// rmsnorm_residual (ref:src/kernels/elementwise.cu:463-513): per row,
+//   v = input + residual; output = v; normed = v * weight * rsqrt(mean(v^2) + eps).
+//   One workgroup per row; output may alias input (each element is read
+//   before it is written, by the same thread).  residual may be null.
+// silu_mul (ref:src/kernels/elementwise.cu:93-99 then :300-305, the pair the
+//   quantized FFN calls at ref:src/model.cu:996-997): out = silu(gate) * up.
+#include "act.hpp"
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace cri {
+namespace dev {
+
+__global__ __launch_bounds__(256) void rmsnorm_residual_kernel(const float* input, const float* residual,
+                                                               const float* __restrict__ weight, float* output,
+                                                               float* __restrict__ normed, int n, float eps) {
+    __shared__ float part[4];
+    const long row = blockIdx.x;
+    const float* in = input + row * n;
+    const float* res = residual ? residual + row * n : nullptr;
+    float* out = output + row * n;
+    float* nrm = normed + row * n;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = in[i] + (res ? res[i] : 0.0f);
+        out[i] = v;
+        ss = __builtin_fmaf(v, v, ss);
+    }
+    ss = group_sum_t<6>(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float f = rms_factor(((part[0] + part[1]) + part[2]) + part[3], n, eps);
+    for (int i = threadIdx.x; i < n; i += 256) nrm[i] = out[i] * weight[i] * f;
+}
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* gate, const float* up, float* out, long n) {
+    const long stride = static_cast<long>(gridDim.x) * 256;
+    for (long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
+        out[i] = silu_f(gate[i]) * up[i];
+}
+
+}  // namespace dev
+
+namespace detail {
+
+int launch_rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output,
+                            float* normed, int rows, int n, float eps, hipStream_t stream) {
+    hipLaunchKernelGGL(dev::rmsnorm_residual_kernel, dim3(rows), dim3(256), 0, stream, input, residual, weight, output,
+                       normed, n, eps);
+    return 0;
+}
+
+int launch_silu_mul(const float* gate, const float* up, float* out, long n, hipStream_t stream) {
+    long blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(dev::silu_mul_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, gate, up, out,
+                       n);
+    return 0;
+}
+
+}  // namespace detail
+}  // namespace cri

@@ -16,6 +16,11 @@
 //     first lane of the row writes y.
 // Weights are read once from HBM with dword-aligned 16-byte loads; the lanes of
 // a row read adjacent bytes, so a wave's loads of one row cover whole cache lines.
+//
+// MODE (see ActIn): the activations are computed while staged -- SwiGLU of the
+// gate/up outputs, or RMSNorm of hidden + residual (the row factor multiplies
+// y, the workgroup-wide sum of squares is reduced through LDS).
+#include "act.hpp"
 #include "common.hpp"
 #include "gemv_formats.hpp"
 #include "internal.hpp"
@@ -28,11 +33,11 @@ namespace dev {
 // the activations, so the HBM latency of the weights overlaps the activation
 // fetch; afterwards every decoded row-group is immediately replaced by the
 // row-group PREF steps ahead.
-template <class F, int UPL, int PREF>
-__global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, const uint8_t* __restrict__ W,
+template <class F, int UPL, int PREF, int MODE>
+__global__ __launch_bounds__(256) void gemv_kernel(const ActIn P, const uint8_t* __restrict__ W,
                                                    float* __restrict__ y, int N, int K, int units, long row_bytes,
                                                    int lpr_log2) {
-    extern __shared__ float xs[];  // K activations, staged once per workgroup
+    extern __shared__ float xs[];  // K activations, staged once per workgroup (+4 partial sums)
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
     const int u0 = lane & (lpr - 1);
@@ -52,12 +57,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
     }
 
     // 1. activations: global -> registers (issued first, tiny), weights in flight behind them
-    f32x4 xv[4];
+    ActRaw<MODE> xv[4];
     const int nx4 = K >> 2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int j = threadIdx.x + 256 * i;
-        xv[i] = j < nx4 ? ld_f32x4(x + 4 * j) : f32x4{0.f, 0.f, 0.f, 0.f};
+        if (j < nx4) act_load<MODE>(xv[i], P, 0, 4 * j);
     }
     typename F::Data buf[PREF][UPL];
     const int base0 = gwave * rows_per_iter;
@@ -72,14 +77,25 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
         if (base0 + p * stride < N) load_rows(buf[p], base0 + p * stride);
 
     // 2. stage activations in LDS (K <= 4096 is covered by the four loads above)
+    float ss = 0.0f;
+    const bool write_h = blockIdx.x == 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int j = threadIdx.x + 256 * i;
-        if (j < nx4) *reinterpret_cast<f32x4*>(xs + 4 * j) = xv[i];
+        if (j < nx4) *reinterpret_cast<f32x4*>(xs + 4 * j) = act_finish<MODE>(xv[i], P, 0, 4 * j, K, ss, write_h);
     }
-    for (int j = threadIdx.x + 1024; j < nx4; j += 256)
-        *reinterpret_cast<f32x4*>(xs + 4 * j) = ld_f32x4(x + 4 * j);
+    for (int j = threadIdx.x + 1024; j < nx4; j += 256) {
+        ActRaw<MODE> raw;
+        act_load<MODE>(raw, P, 0, 4 * j);
+        *reinterpret_cast<f32x4*>(xs + 4 * j) = act_finish<MODE>(raw, P, 0, 4 * j, K, ss, write_h);
+    }
+    if constexpr (MODE == kActRMSNorm) {
+        ss = group_sum_t<6>(ss);
+        if (lane == 0) xs[K + (threadIdx.x >> 6)] = ss;
+    }
     __syncthreads();
+    float rs = 1.0f;
+    if constexpr (MODE == kActRMSNorm) rs = rms_factor(((xs[K] + xs[K + 1]) + xs[K + 2]) + xs[K + 3], K, P.eps);
     typename F::Xr xr[UPL];
 #pragma unroll
     for (int u = 0; u < UPL; ++u) F::load_x(xr[u], xs, unit[u]);
@@ -94,7 +110,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
         }
         acc = group_sum(acc, lpr_log2);
         const int r = b + rsub;
-        if (u0 == 0 && r < N) y[r] = acc;
+        if (u0 == 0 && r < N) y[r] = MODE == kActRMSNorm ? acc * rs : acc;
     };
     for (int b = base0; b < N; b += PREF * stride) {
 #pragma unroll
@@ -113,8 +129,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
 
 namespace detail {
 
-template <class F, int UPL, int PREF>
-static void launch_gemv_t(const float* x, const void* W, float* y, int N, int K, int units, long row_bytes,
+template <class F, int UPL, int PREF, int MODE>
+static void launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K, int units, long row_bytes,
                           int lpr_log2, hipStream_t stream) {
     const int rows_per_iter = 64 >> lpr_log2;
     const long groups = (static_cast<long>(N) + rows_per_iter - 1) / rows_per_iter;
@@ -123,12 +139,13 @@ static void launch_gemv_t(const float* x, const void* W, float* y, int N, int K,
     long waves = (groups + PREF - 1) / PREF;
     if (waves > kGemvTargetWaves) waves = kGemvTargetWaves;
     const int blocks = static_cast<int>((waves + 3) / 4);
-    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF>), dim3(blocks), dim3(256), K * sizeof(float), stream, x,
+    const int lds = (K + (MODE == kActRMSNorm ? 4 : 0)) * static_cast<int>(sizeof(float));
+    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE>), dim3(blocks), dim3(256), lds, stream, act,
                        static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2);
 }
 
-template <class F>
-static int launch_gemv_f(const float* x, const void* W, float* y, int N, int K, long row_bytes,
+template <class F, int MODE>
+static int launch_gemv_f(const ActIn& x, const void* W, float* y, int N, int K, long row_bytes,
                          hipStream_t stream) {
     const int units = K / 64;
     int lpr_log2 = 0;
@@ -136,10 +153,10 @@ static int launch_gemv_f(const float* x, const void* W, float* y, int N, int K, 
     const int lpr = 1 << lpr_log2;
     const int upl = (units + lpr - 1) / lpr;
     switch (upl) {
-        case 1: launch_gemv_t<F, 1, F::kPref1>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
-        case 2: launch_gemv_t<F, 2, 2>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
+        case 1: launch_gemv_t<F, 1, F::kPref1, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
+        case 2: launch_gemv_t<F, 2, 2, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
         case 3:
-        case 4: launch_gemv_t<F, 4, 1>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
+        case 4: launch_gemv_t<F, 4, 1, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
         default: return -1;
     }
     return 0;
@@ -151,15 +168,33 @@ bool gemv_supported(int fmt, int K, const void* W) {
     return (reinterpret_cast<uintptr_t>(W) & 3u) == 0;  // dword-aligned vector loads
 }
 
-int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream) {
+template <int MODE>
+static int launch_gemv_m(int fmt, const ActIn& x, const void* W, float* y, int N, int K, hipStream_t stream) {
     switch (fmt) {
-        case kFmtQ8_0: return launch_gemv_f<dev::GemvQ8_0>(x, W, y, N, K, (K / 32) * 34L, stream);
-        case kFmtQ4_0: return launch_gemv_f<dev::GemvQ4_0>(x, W, y, N, K, (K / 32) * 18L, stream);
-        case kFmtQ5_0: return launch_gemv_f<dev::GemvQ5_0>(x, W, y, N, K, (K / 32) * 22L, stream);
-        case kFmtQ4_K: return launch_gemv_f<dev::GemvQ4K>(x, W, y, N, K, (K / 256) * 144L, stream);
-        case kFmtQ6_K: return launch_gemv_f<dev::GemvQ6K>(x, W, y, N, K, (K / 256) * 210L, stream);
-        case kFmtF16: return launch_gemv_f<dev::GemvF16>(x, W, y, N, K, K * 2L, stream);
-        case kFmtF32: return launch_gemv_f<dev::GemvF32>(x, W, y, N, K, K * 4L, stream);
+        case kFmtQ8_0: return launch_gemv_f<dev::GemvQ8_0, MODE>(x, W, y, N, K, (K / 32) * 34L, stream);
+        case kFmtQ4_0: return launch_gemv_f<dev::GemvQ4_0, MODE>(x, W, y, N, K, (K / 32) * 18L, stream);
+        case kFmtQ5_0: return launch_gemv_f<dev::GemvQ5_0, MODE>(x, W, y, N, K, (K / 32) * 22L, stream);
+        case kFmtQ4_K: return launch_gemv_f<dev::GemvQ4K, MODE>(x, W, y, N, K, (K / 256) * 144L, stream);
+        case kFmtQ6_K: return launch_gemv_f<dev::GemvQ6K, MODE>(x, W, y, N, K, (K / 256) * 210L, stream);
+        case kFmtF16: return launch_gemv_f<dev::GemvF16, MODE>(x, W, y, N, K, K * 2L, stream);
+        case kFmtF32:
+            if constexpr (MODE == kActPlain) return launch_gemv_f<dev::GemvF32, MODE>(x, W, y, N, K, K * 4L, stream);
+            break;
+    }
+    return -1;
+}
+
+int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream) {
+    const ActIn act{x, nullptr, nullptr, nullptr, K, 0.0f};
+    return launch_gemv_m<kActPlain>(fmt, act, W, y, N, K, stream);
+}
+
+int launch_gemv_act(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t stream) {
+    if (mode == kActRMSNorm && (K + 4) * 4 > 65536) return -1;  // the 4 partial sums must fit beside x in 64 KB
+    switch (mode) {
+        case kActPlain: return launch_gemv_m<kActPlain>(fmt, act, W, y, N, K, stream);
+        case kActSwiGLU: return launch_gemv_m<kActSwiGLU>(fmt, act, W, y, N, K, stream);
+        case kActRMSNorm: return launch_gemv_m<kActRMSNorm>(fmt, act, W, y, N, K, stream);
     }
     return -1;
 }

@@ -34,18 +34,40 @@ inline int block_bytes(int fmt) {
 }
 inline long row_bytes(int fmt, int K) { return static_cast<long>(K / block_elems(fmt)) * block_bytes(fmt); }
 
+// Activation prologue of the fused decode matmuls: the A operand is computed
+// from its neighbours' outputs while it is staged, instead of by separate
+// elementwise launches (ref:src/model.cu:960-1010 runs rmsnorm_residual, silu
+// and multiply between the GEMVs).
+//   kActPlain   : x[m][k] = a[m*lda + k]
+//   kActSwiGLU  : x[m][k] = silu(a[m*lda + k]) * b[m*lda + k]            (gate, up)
+//   kActRMSNorm : v = a[m*lda + k] + b[m*lda + k] (b may be null), x = v * w[k],
+//                 the output row m scaled by 1/sqrt(mean_k v^2 + eps), and v
+//                 written to h_out[m*K + k] when h_out is not null
+enum : int { kActPlain = 0, kActSwiGLU = 1, kActRMSNorm = 2 };
+struct ActIn {
+    const float* a;
+    const float* b;
+    const float* w;
+    float* h_out;
+    long lda;
+    float eps;
+};
+
 namespace detail {
 
 // Target number of resident waves for the GEMV grid (MI355X: 256 CUs).
 constexpr long kGemvTargetWaves = 2048;
 
-// batch-1 GEMV (gemv.hip)
+// batch-1 GEMV (gemv.hip); the _act form takes an activation prologue
 bool gemv_supported(int fmt, int K, const void* W);
 int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream);
+int launch_gemv_act(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t stream);
 
 // 1 <= M <= 16 fused dequant matmul on the matrix cores (mfma_skinny.hip)
 bool skinny_supported(int fmt, int M, int K, const void* B);
 int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+int launch_skinny_act(int mode, int fmt, const ActIn& act, const void* B, float* C, int M, int N, int K,
+                      hipStream_t stream);
 
 // multi-token fused dequant GEMM on the matrix cores, fp16 operands (mfma_gemm.hip)
 bool mfma_gemm_supported(int fmt, int M, int N, int K, const void* A, const void* B);
@@ -54,6 +76,13 @@ int launch_mfma_gemm(int fmt, const float* A, const void* B, float* C, int M, in
 // any-M fused dequant matmul, element-wise decode (generic.hip)
 int launch_generic_matmul(int fmt, const float* A, const void* B, float* C, int M, int N, int K,
                           hipStream_t stream);
+int launch_generic_matmul_act(int mode, int fmt, const ActIn& act, const void* B, float* C, int M, int N, int K,
+                              hipStream_t stream);
+
+// standalone neighbours (elementwise.hip): the reference's rmsnorm_residual and silu + multiply
+int launch_rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output,
+                            float* normed, int rows, int n, float eps, hipStream_t stream);
+int launch_silu_mul(const float* gate, const float* up, float* out, long n, hipStream_t stream);
 
 // standalone dequant (dequant.hip)
 int launch_dequant(int fmt, const void* src, float* dst, long n_blocks, hipStream_t stream);

@@ -25,8 +25,14 @@
 // its fp16 rounding hi plus the exact remainder lo in {-1, 0, 1}: three MFMAs
 // (x_hi * hi, x_lo * hi, x_hi * lo) per 32 k, the dropped x_lo * lo being
 // 2^-11 of the smallest term; d is applied per super-block.
+//
+// MODE (see ActIn): the activations are computed while staged -- SwiGLU of the
+// gate/up outputs, or RMSNorm of hidden + residual: per (row, super-block)
+// sums of squares go to LDS next to the unscale factors, and the epilogue
+// multiplies each output row by 1/sqrt(mean + eps).
 #include <atomic>
 
+#include "act.hpp"
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -37,7 +43,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kSkNW = 4;  // waves per workgroup
 // Staging items per thread per load batch.
 constexpr int kSkMaxItems = 6;
 // Activation chunk bound: M * KC <= kSkChunk (fp16 hi + lo copies: 4 * kSkChunk bytes of LDS).
@@ -68,7 +73,7 @@ __device__ __forceinline__ uint32_t f16x2_splat(float v) {
 
 struct SkLds {
     // byte offsets inside the dynamic LDS block
-    int xh, xl, xs, red, scl;
+    int xh, xl, xs, red, scl, ssq;
     int bytes;
 };
 
@@ -78,7 +83,7 @@ struct SkLds {
 __device__ __host__ inline int sk_xstride(int KC) { return KC + 8; }
 __device__ __host__ inline int sk_sstride(int KC) { return KC / 16 + 4; }
 
-__device__ __host__ inline SkLds sk_layout(int M, int KC, int nw) {
+__device__ __host__ inline SkLds sk_layout(int M, int KC, int nw, int K = 0, bool rms = false) {
     SkLds L;
     int o = 0;
     L.xh = o; o += M * sk_xstride(KC) * 2;
@@ -87,6 +92,7 @@ __device__ __host__ inline SkLds sk_layout(int M, int KC, int nw) {
     o = (o + 15) & ~15;
     L.scl = o; o += (KC / 256) * 16 * 4;  // unscale[super-block][m] (16 m slots, zero beyond M)
     L.red = o; o += nw * 4 * 64 * 4;   // cross-wave reduction of k-split partials
+    L.ssq = o; o += rms ? (K / 256) * 16 * 4 : 0;  // RMSNorm: sum of v^2 per [super-block of K][m]
     L.bytes = o;
     return L;
 }
@@ -102,7 +108,12 @@ __device__ __host__ inline SkLds sk_layout(int M, int KC, int nw) {
 // sub-block sums.  All 64 lanes of the wave must call it together (lane
 // reductions); 32-lane groups hold one (row, super-block).
 __device__ __forceinline__ void sk_convert_item(const f32x4 a, const f32x4 b, bool live, int m, int g8, int KC,
-                                                _Float16* xh, _Float16* xl, _Float16* xs, float* unscale) {
+                                                _Float16* xh, _Float16* xl, _Float16* xs, float* unscale,
+                                                float ss = 0.0f, float* ssq = nullptr) {
+    if (ssq) {  // RMSNorm: the (row, super-block) sum of v^2 over the 32 lanes holding it, fixed order
+        ss = group_sum_t<5>(ss);
+        if (live && (g8 & 31) == 0) ssq[(g8 >> 5) * 16 + m] = ss;
+    }
     float mx = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
                      fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
     mx = fmaxf(mx, dpp<kQuadPerm1032>(mx));
@@ -162,8 +173,11 @@ __device__ __forceinline__ void sk_clear_unscale(int M, int KC, float* unscale) 
 // are strided over the threads in batches of kSkMaxItems per thread, each
 // batch's loads issued before any of its items is converted.  Per-sub-block
 // sums (times 2^-6) feed the mins MFMA.  One barrier.
-__device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int KC, char* lds, const SkLds& L) {
+template <int MODE>
+__device__ void sk_stage(const ActIn& P, int M, int K, int k0, int KC, char* lds, const SkLds& L) {
     const int tid = threadIdx.x, nth = blockDim.x;
+    const bool write_h = blockIdx.x == 0;
+    float* ssq = MODE == kActRMSNorm ? reinterpret_cast<float*>(lds + L.ssq) + (k0 >> 8) * 16 : nullptr;
     _Float16* xh = reinterpret_cast<_Float16*>(lds + L.xh);
     _Float16* xl = reinterpret_cast<_Float16*>(lds + L.xl);
     _Float16* xs = reinterpret_cast<_Float16*>(lds + L.xs);
@@ -171,27 +185,33 @@ __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int 
     const int groups = KC / 8;  // k8 groups per row; a multiple of 32
     sk_clear_unscale(M, KC, unscale);
     const int total = M * groups;  // a multiple of 32
-    for (int e_batch = 0; e_batch < total; e_batch += kSkMaxItems * nth) {
-        f32x4 va[kSkMaxItems], vb[kSkMaxItems];
+    // items per load batch: the prologues hold 2x (SwiGLU) or 3x (RMSNorm) the raw values per item
+    constexpr int kItems = MODE == kActPlain ? kSkMaxItems : (MODE == kActSwiGLU ? 4 : 3);
+    for (int e_batch = 0; e_batch < total; e_batch += kItems * nth) {
+        ActRaw<MODE> ra[kItems], rb[kItems];
 #pragma unroll
-        for (int it = 0; it < kSkMaxItems; ++it) {
+        for (int it = 0; it < kItems; ++it) {
             const int e = e_batch + it * nth + tid;
-            va[it] = vb[it] = f32x4{0.f, 0.f, 0.f, 0.f};
             if (e < total) {
                 const int m = e / groups, g8 = e - m * groups;
-                const float* src = A + static_cast<long>(m) * K + k0 + 8 * g8;
-                va[it] = ld_f32x4(src);
-                vb[it] = ld_f32x4(src + 4);
+                act_load<MODE>(ra[it], P, m, k0 + 8 * g8);
+                act_load<MODE>(rb[it], P, m, k0 + 8 * g8 + 4);
             }
         }
 #pragma unroll
-        for (int it = 0; it < kSkMaxItems; ++it) {
+        for (int it = 0; it < kItems; ++it) {
             const int e0 = e_batch + it * nth;
             if (e0 >= total) break;  // uniform over the workgroup
             const int e = e0 + tid;
             const bool live = e < total;
             const int m = live ? e / groups : 0, g8 = live ? e - m * groups : 0;
-            sk_convert_item(va[it], vb[it], live, m, g8, KC, xh, xl, xs, unscale);
+            float ss = 0.0f;
+            f32x4 va = f32x4{0.f, 0.f, 0.f, 0.f}, vb = va;
+            if (live) {
+                va = act_finish<MODE>(ra[it], P, m, k0 + 8 * g8, K, ss, write_h);
+                vb = act_finish<MODE>(rb[it], P, m, k0 + 8 * g8 + 4, K, ss, write_h);
+            }
+            sk_convert_item(va, vb, live, m, g8, KC, xh, xl, xs, unscale, ss, ssq);
         }
     }
     __syncthreads();
@@ -200,18 +220,19 @@ __device__ void sk_stage(const float* __restrict__ A, int M, int K, int k0, int 
 // When every thread has at most one item (M * KC / 8 <= threads), its two
 // loads are issued at kernel start, before the weight loads, and converted
 // here: waiting for them does not wait for the weights.
-__device__ __forceinline__ void sk_load_one(const float* __restrict__ A, int M, int K, int k0, int KC, f32x4& a,
-                                            f32x4& b) {
+template <int MODE>
+__device__ __forceinline__ void sk_load_one(const ActIn& P, int M, int k0, int KC, ActRaw<MODE>& a,
+                                            ActRaw<MODE>& b) {
     const int groups = KC / 8, e = threadIdx.x;
-    a = b = f32x4{0.f, 0.f, 0.f, 0.f};
     if (e < M * groups) {
         const int m = e / groups, g8 = e - m * groups;
-        const float* src = A + static_cast<long>(m) * K + k0 + 8 * g8;
-        a = ld_f32x4(src);
-        b = ld_f32x4(src + 4);
+        act_load<MODE>(a, P, m, k0 + 8 * g8);
+        act_load<MODE>(b, P, m, k0 + 8 * g8 + 4);
     }
 }
-__device__ __forceinline__ void sk_stage_one(const f32x4 a, const f32x4 b, int M, int KC, char* lds, const SkLds& L) {
+template <int MODE>
+__device__ __forceinline__ void sk_stage_one(const ActRaw<MODE>& ra, const ActRaw<MODE>& rb, const ActIn& P, int M,
+                                             int K, int k0, int KC, char* lds, const SkLds& L) {
     _Float16* xh = reinterpret_cast<_Float16*>(lds + L.xh);
     _Float16* xl = reinterpret_cast<_Float16*>(lds + L.xl);
     _Float16* xs = reinterpret_cast<_Float16*>(lds + L.xs);
@@ -222,7 +243,14 @@ __device__ __forceinline__ void sk_stage_one(const f32x4 a, const f32x4 b, int M
     if ((e & ~63) < total) {  // whole waves past the items skip (lane reductions need all 64 lanes)
         const bool live = e < total;
         const int m = live ? e / groups : 0, g8 = live ? e - m * groups : 0;
-        sk_convert_item(a, b, live, m, g8, KC, xh, xl, xs, unscale);
+        float ss = 0.0f;
+        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = a;
+        if (live) {
+            a = act_finish<MODE>(ra, P, m, k0 + 8 * g8, K, ss, blockIdx.x == 0);
+            b = act_finish<MODE>(rb, P, m, k0 + 8 * g8 + 4, K, ss, blockIdx.x == 0);
+        }
+        float* ssq = MODE == kActRMSNorm ? reinterpret_cast<float*>(lds + L.ssq) + (k0 >> 8) * 16 : nullptr;
+        sk_convert_item(a, b, live, m, g8, KC, xh, xl, xs, unscale, ss, ssq);
     }
     __syncthreads();
 }
@@ -414,12 +442,12 @@ struct SkQ6K {
 // Workgroup = NW waves = (NW / KS) tiles x KS k-splits.  The grid strides
 // over groups of NW / KS tiles; wave w works on tile w / KS of the group and
 // on super-blocks j = w % KS, + KS, ... of the current activation chunk.
-template <class F, int NW>
-__global__ __launch_bounds__(64 * NW) void skinny_kernel(const float* __restrict__ A, const uint8_t* __restrict__ B,
+template <class F, int NW, int MODE>
+__global__ __launch_bounds__(64 * NW) void skinny_kernel(const ActIn P, const uint8_t* __restrict__ B,
                                                              float* __restrict__ C, int M, int N, int K, int KC,
                                                              int ks_log2, int ngroups, int nchunks) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const SkLds L = sk_layout(M, KC, NW);
+    const SkLds L = sk_layout(M, KC, NW, K, MODE == kActRMSNorm);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, nl = lane & 15;
     const int m_a = lane & 15;  // row of the A operand this lane supplies
@@ -453,14 +481,14 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const float* __restrict
             // staged; single-item activation loads go first of all
             const bool stage = grp == static_cast<int>(blockIdx.x) || nchunks > 1;
             const bool one = M * (KC / 8) <= 64 * NW;
-            f32x4 xa, xb;
-            if (stage && one) sk_load_one(A, M, K, k0, KC, xa, xb);
+            ActRaw<MODE> xa, xb;
+            if (stage && one) sk_load_one<MODE>(P, M, k0, KC, xa, xb);
             typename F::Item b0, b1;
             if (nitems > 0) load_item(b0, 0);
             if (nitems > 1) load_item(b1, 1);
             if (stage) {
-                if (one) sk_stage_one(xa, xb, M, KC, lds, L);
-                else sk_stage(A, M, K, k0, KC, lds, L);
+                if (one) sk_stage_one<MODE>(xa, xb, P, M, K, k0, KC, lds, L);
+                else sk_stage<MODE>(P, M, K, k0, KC, lds, L);
             }
             auto run_item = [&](const typename F::Item& d, int it) {
                 const int jj = my_split + (it << ks_log2);
@@ -479,12 +507,24 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const float* __restrict
             }
             if (nchunks > 1) __syncthreads();  // the next chunk overwrites the staged activations
         }
+        // RMSNorm: the row factor of output row m (the sums of every chunk stay in LDS)
+        auto row_factor = [&](int m) {
+            if constexpr (MODE == kActRMSNorm) {
+                const float* ssq = reinterpret_cast<const float*>(lds + L.ssq);
+                float ss = 0.0f;
+                for (int sb = 0; sb < (K >> 8); ++sb) ss += ssq[sb * 16 + min(m, M - 1)];
+                return rms_factor(ss, K, P.eps);
+            } else {
+                (void)m;
+                return 1.0f;
+            }
+        };
         // reduce the KS k-split partials of each tile: red[w][r][lane]
         if (KS == 1) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = 4 * g + r, n = tile * 16 + nl;
-                if (m < M && n < N && tile < ntiles) C[static_cast<long>(m) * N + n] = acc[r];
+                if (m < M && n < N && tile < ntiles) C[static_cast<long>(m) * N + n] = acc[r] * row_factor(m);
             }
         } else {
 #pragma unroll
@@ -497,7 +537,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const float* __restrict
                 for (int sp = 0; sp < KS; ++sp) sum += red[(((t << ks_log2) + sp) * 4 + r) * 64 + ln];
                 const int tt = grp * TW + t;
                 const int m = 4 * (ln >> 4) + r, n = tt * 16 + (ln & 15);
-                if (m < M && n < N && tt < ntiles) C[static_cast<long>(m) * N + n] = sum;
+                if (m < M && n < N && tt < ntiles) C[static_cast<long>(m) * N + n] = sum * row_factor(m);
             }
             __syncthreads();
         }
@@ -516,15 +556,16 @@ bool skinny_supported(int fmt, int M, int K, const void* B) {
     return false;
 }
 
-template <class F, int NW>
-static int launch_sk(const float* A, const void* B, float* C, int M, int N, int K, int KC, int KS, hipStream_t stream) {
+template <class F, int NW, int MODE>
+static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int K, int KC, int KS,
+                     hipStream_t stream) {
     // large chunks need more than the default 64 KB of dynamic LDS: raise the limit once per kernel and device
     constexpr int kMaxDevices = 64;
     static std::atomic<bool> ready[kMaxDevices];
     int devid = 0;
     if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return -1;
     if (!ready[devid].load(std::memory_order_acquire)) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::skinny_kernel<F, NW>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::skinny_kernel<F, NW, MODE>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
             return -1;
         ready[devid].store(true, std::memory_order_release);
@@ -537,13 +578,16 @@ static int launch_sk(const float* A, const void* B, float* C, int M, int N, int 
     // enough workgroups for ~2048 waves; beyond that each workgroup strides over tile groups
     int blocks = groups < 2048 / NW ? groups : 2048 / NW;
     if (blocks < 1) blocks = 1;
-    const dev::SkLds L = dev::sk_layout(M, KC, NW);
-    hipLaunchKernelGGL((dev::skinny_kernel<F, NW>), dim3(blocks), dim3(64 * NW), L.bytes, stream, A,
+    const dev::SkLds L = dev::sk_layout(M, KC, NW, K, MODE == kActRMSNorm);
+    if (L.bytes > 160 * 1024) return -1;
+    hipLaunchKernelGGL((dev::skinny_kernel<F, NW, MODE>), dim3(blocks), dim3(64 * NW), L.bytes, stream, A,
                        static_cast<const uint8_t*>(B), C, M, N, K, KC, ks_log2, groups, K / KC);
     return 0;
 }
 
-int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream) {
+template <int MODE>
+static int launch_skinny_m(int fmt, const ActIn& A, const void* B, float* C, int M, int N, int K,
+                           hipStream_t stream) {
     // activation chunk: the largest multiple of 256 dividing K with M * KC <= kSkChunk
     // (few chunks: every chunk is staged once per workgroup)
     const int ntiles = (N + 15) / 16;
@@ -557,8 +601,23 @@ int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N
     while (KS < 8 && KS * 2 <= sb && static_cast<long>(ntiles) * KS < 2048) KS *= 2;
     // eight waves per workgroup (8 / KS tiles each): measured faster than four for
     // every decode shape, from 512 x 2048 to the 128256 x 2048 lm_head
-    if (fmt == kFmtQ6_K) return launch_sk<dev::SkQ6K, 8>(A, B, C, M, N, K, KC, KS, stream);
-    return launch_sk<dev::SkQ4K, 8>(A, B, C, M, N, K, KC, KS, stream);
+    if (fmt == kFmtQ6_K) return launch_sk<dev::SkQ6K, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
+    return launch_sk<dev::SkQ4K, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
+}
+
+int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream) {
+    const ActIn act{A, nullptr, nullptr, nullptr, K, 0.0f};
+    return launch_skinny_m<kActPlain>(fmt, act, B, C, M, N, K, stream);
+}
+
+int launch_skinny_act(int mode, int fmt, const ActIn& act, const void* B, float* C, int M, int N, int K,
+                      hipStream_t stream) {
+    switch (mode) {
+        case kActPlain: return launch_skinny_m<kActPlain>(fmt, act, B, C, M, N, K, stream);
+        case kActSwiGLU: return launch_skinny_m<kActSwiGLU>(fmt, act, B, C, M, N, K, stream);
+        case kActRMSNorm: return launch_skinny_m<kActRMSNorm>(fmt, act, B, C, M, N, K, stream);
+    }
+    return -1;
 }
 
 }  // namespace detail

@@ -125,6 +125,37 @@ int cri_fused_decode_attention_ws(const float* Q, const float* K_cache, const fl
  * empty problem; a negative cri_status for invalid arguments). */
 long long cri_fused_decode_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, int kv_len);
 
+/* ---- neighbour fusions: the activation computed while the matmul stages it -- */
+
+/* C[M,N] = normed[M,K] * dequant(B[N,K])^T with v = hidden + residual and
+ * normed = v * norm_weight * rsqrt(mean_k(v^2) + eps), the RMSNorm that feeds
+ * q/k/v and gate/up (ref:src/kernels/elementwise.cu:463-513, called at
+ * ref:src/model.cu:961-967 and :1012-1018 before matmul_dispatch).  v is also
+ * written to hidden_out [M, K] when it is not null; hidden_out must not overlap
+ * hidden or residual (checked).  residual may be null (plain RMSNorm).  No
+ * counterpart in the reference: it replaces a rmsnorm_residual launch and the
+ * normed buffer.  Decode batches only (1 <= M <= 16; CRI_ERR_UNSUPPORTED
+ * above), every format; fp32 accuracy as cri_matmul at M <= 16. */
+int cri_matmul_rmsnorm(int format, const float* hidden, const float* residual, const float* norm_weight,
+                       float* hidden_out, const void* B, float* C, int M, int N, int K, float eps,
+                       hipStream_t stream);
+/* C[M,N] = (silu(gate) * up)[M,K] * dequant(B[N,K])^T, silu(x) = x / (1 + exp(-x)):
+ * the FFN down projection of ref:src/model.cu:996-1002 with its silu and
+ * multiply launches folded in.  gate and up rows are `ld` floats apart (ld >= K;
+ * gate = buf, up = buf + inter, ld = 2 * inter reads a fused gate/up output).
+ * No counterpart in the reference.  Decode batches only (1 <= M <= 16). */
+int cri_matmul_swiglu(int format, const float* gate, const float* up, int ld, const void* B, float* C, int M,
+                      int N, int K, hipStream_t stream);
+
+/* Standalone forms, for batches the fused prologues do not take.
+ * replaces cuinfer::rmsnorm_residual, ref:include/cuinfer/kernels/elementwise.h:107
+ * (output may alias input; residual may be null) */
+int cri_rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output,
+                         float* normed, int rows, int n, float eps, hipStream_t stream);
+/* out = silu(gate) * up over n elements: cuinfer::silu then cuinfer::multiply,
+ * ref:include/cuinfer/kernels/elementwise.h:23 and :75 (out may alias gate or up) */
+int cri_silu_mul(const float* gate, const float* up, float* out, long long n, hipStream_t stream);
+
 /* ---- diagnostics ---------------------------------------------------------- */
 
 /* Message for the last non-zero status returned on this thread ("" if none). */

@@ -23,4 +23,16 @@ WeightFormat weight_format_of(DType dtype);
 void matmul_dispatch(const float* A, const Tensor& weight, float* C, int M, int N, int K, WeightFormat format,
                      hipStream_t stream = 0);
 
+// Decode-batch (M <= 16) forms with the neighbouring elementwise work folded into the
+// matmul's activation staging (no counterpart in the reference; see cri_matmul_rmsnorm /
+// cri_matmul_swiglu in cri.h):
+//   C = RMSNorm(hidden + residual) * weight^T, hidden + residual also written to hidden_out
+//   (not null, not overlapping hidden/residual) -- replaces rmsnorm_residual + matmul_dispatch;
+//   C = (silu(gate) * up) * weight^T, gate/up rows ld floats apart -- replaces silu + multiply + matmul_dispatch.
+void matmul_dispatch_rmsnorm(const float* hidden, const float* residual, const float* norm_weight, float* hidden_out,
+                             const Tensor& weight, float* C, int M, int N, int K, WeightFormat format, float eps,
+                             hipStream_t stream = 0);
+void matmul_dispatch_swiglu(const float* gate, const float* up, int ld, const Tensor& weight, float* C, int M, int N,
+                            int K, WeightFormat format, hipStream_t stream = 0);
+
 }  // namespace cuinfer

@@ -53,6 +53,8 @@ def lib():
         L.orc_matmul_quant.argtypes = [i32, fp, vp, fp, i32, i32, i32]
         L.orc_matmul_transposed_b.argtypes = [fp, fp, fp, i32, i32, i32]
         L.orc_batched_matmul_gqa.argtypes = [fp, fp, fp, i32, i32, i32, i32, i32]
+        L.orc_rmsnorm_residual.argtypes = [fp, fp, fp, fp, fp, i32, i32, ctypes.c_float]
+        L.orc_silu_mul.argtypes = [fp, fp, fp, i64]
         for name in ("orc_decode_attention", "orc_decode_attention_online"):
             getattr(L, name).argtypes = [fp, fp, fp, fp, i32, i32, i32, i32, ctypes.c_float]
         for f in ("q8_0", "q4_0", "q5_0", "q6_k", "q4_k_simple", "q4_k_asym"):
@@ -163,6 +165,26 @@ def np_decode_attention_f64(Q, K, V, n_heads, n_kv_heads, head_dim, kv_len, scal
         w = np.exp(s - s.max())
         out[h] = (w / w.sum()) @ v[:, h // G, :]
     return out.ravel()
+
+
+def rmsnorm_residual(x, residual, weight, eps=1e-5):
+    """(output, normed) of the reference's rmsnorm_residual over rows of x [rows, n]."""
+    x = _f32(x)
+    rows, n = x.shape
+    res = None if residual is None else _f32(residual).reshape(rows, n)
+    w = _f32(weight)
+    out = np.empty_like(x)
+    normed = np.empty_like(x)
+    lib().orc_rmsnorm_residual(_p(x), None if res is None else _p(res), _p(w), _p(out), _p(normed), rows, n,
+                               float(eps))
+    return out, normed
+
+
+def silu_mul(gate, up):
+    g, u = _f32(gate), _f32(up)
+    out = np.empty_like(g)
+    lib().orc_silu_mul(_p(g), _p(u), _p(out), g.size)
+    return out
 
 
 # ---------------------------------------------------------------- quantizers

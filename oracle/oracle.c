@@ -362,6 +362,38 @@ void orc_decode_attention_online(const float* Q, const float* Kc, const float* V
     free(acc);
 }
 
+/* RMSNorm with a residual, ref:src/kernels/elementwise.cu:463-504 per row:
+ * v = input + residual (residual may be NULL), output = v, sum of v^2 (here in
+ * index order; the kernel's tree order is not portable), factor =
+ * 1 / sqrt(sum / n + eps) (the kernel's rsqrtf), normed = output * weight * factor. */
+void orc_rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output,
+                          float* normed, int rows, int n, float eps) {
+    for (int r = 0; r < rows; ++r) {
+        const float* in = input + (int64_t)r * n;
+        const float* res = residual ? residual + (int64_t)r * n : NULL;
+        float* out = output + (int64_t)r * n;
+        float* nrm = normed + (int64_t)r * n;
+        float ss = 0.0f;
+        for (int i = 0; i < n; ++i) {
+            const float v = in[i] + (res ? res[i] : 0.0f);
+            out[i] = v;
+            ss += v * v;
+        }
+        const float mean_sq = ss / (float)n;
+        const float f = 1.0f / sqrtf(mean_sq + eps);
+        for (int i = 0; i < n; ++i) nrm[i] = out[i] * weight[i] * f;
+    }
+}
+
+/* silu then multiply, ref:src/kernels/elementwise.cu:93-99 and :300-305 */
+void orc_silu_mul(const float* gate, const float* up, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float x = gate[i];
+        const float s = x / (1.0f + expf(-x));
+        out[i] = s * up[i];
+    }
+}
+
 /* ---------------------------------------------------------------------------
  * Host quantizers (ref:tests/test_matmul_quant.cu).  std::round is roundf
  * (half away from zero); __float2half is round-to-nearest-even.

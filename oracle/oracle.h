@@ -25,6 +25,10 @@
  *                         forms (kv_len 1 -> V[0]; equal scores -> mean of V;
  *                         one dominant score -> its V row; a position
  *                         permutation leaves the output unchanged).
+ *   orc_rmsnorm_residual, orc_silu_mul: fp64 numpy, closed forms (a constant
+ *                         row normalises to c / sqrt(c^2 + eps); silu(0) = 0,
+ *                         silu(x) -> x and -> 0 at the ends), the residual sum
+ *                         exact, scale invariance of the normed row.
  *   orc_quantize_*      : bit-exact vs the numpy quantizers in cretif_amd/quant.py
  *                         (written separately) and round-trip error bounds.
  */
@@ -77,6 +81,11 @@ void orc_decode_attention(const float* Q, const float* Kc, const float* Vc, floa
 /* the reference kernel's online recurrence, ref:src/attention.cu:446-493 */
 void orc_decode_attention_online(const float* Q, const float* Kc, const float* Vc, float* out,
                                  int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale);
+
+/* the matmuls' elementwise neighbours: ref:src/kernels/elementwise.cu:463-504, :93-99 + :300-305 */
+void orc_rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output,
+                          float* normed, int rows, int n, float eps);
+void orc_silu_mul(const float* gate, const float* up, float* out, int64_t n);
 
 /* host quantizers restated from ref:tests/test_matmul_quant.cu */
 void orc_quantize_q8_0(const float* x, void* dst, int64_t n);        /* :46-71   */

@@ -153,3 +153,32 @@ def test_decode_attention_ws_validation():
     with pytest.raises(cri.CretifError) as e:   # not even one record per head
         f(FAKE, FAKE, FAKE, FAKE, 32, 8, 64, 100, 0.125, FAKE, 100, stream=0)
     assert e.value.status == -2
+
+
+def test_fused_prologue_validation():
+    with pytest.raises(cri.CretifError) as e:
+        cri.matmul_rmsnorm("q4_k", FAKE, None, FAKE, None, FAKE, FAKE, 1, 8, 0, stream=0)
+    assert e.value.status == -2
+    with pytest.raises(cri.CretifError) as e:
+        cri.matmul_rmsnorm("q4_k", FAKE, None, 0, None, FAKE, FAKE, 1, 8, 256, stream=0)
+    assert e.value.status == -1
+    with pytest.raises(cri.CretifError) as e:   # hidden_out overlapping hidden
+        cri.matmul_rmsnorm("q4_k", FAKE, None, FAKE, FAKE + 64, FAKE, FAKE, 1, 8, 256, stream=0)
+    assert e.value.status == -1
+    with pytest.raises(cri.CretifError) as e:
+        cri.matmul_rmsnorm("q4_k", FAKE, None, FAKE, None, FAKE, FAKE, 17, 8, 256, stream=0)
+    assert e.value.status == -5
+    with pytest.raises(cri.CretifError) as e:
+        cri.matmul_swiglu("q4_k", FAKE, FAKE, 128, FAKE, FAKE, 1, 8, 256, stream=0)
+    assert e.value.status == -2
+    with pytest.raises(cri.CretifError) as e:
+        cri.matmul_swiglu("q8_0", FAKE, FAKE, 64, FAKE, FAKE, 1, 8, 48, stream=0)
+    assert e.value.status == -2
+    with pytest.raises(cri.CretifError) as e:
+        cri.rmsnorm_residual(FAKE, None, FAKE, FAKE, FAKE, 2, 0, stream=0)
+    assert e.value.status == -2
+    with pytest.raises(cri.CretifError) as e:
+        cri.silu_mul(FAKE, FAKE, FAKE + 2, 10, stream=0)
+    assert e.value.status == -3
+    cri.silu_mul(0, 0, 0, 0, stream=0)
+    cri.matmul_swiglu("q4_k", 0, 0, 0, 0, 0, 0, 8, 256, stream=0)
