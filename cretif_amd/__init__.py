@@ -44,6 +44,8 @@ __all__ = [
     "matmul_swiglu",
     "rmsnorm_residual",
     "silu_mul",
+    "embedding_rows",
+    "GGUFFile",
     "FORMAT_IDS",
     "ABI_SYMBOLS",
 ]
@@ -59,6 +61,7 @@ STATUS_NAMES = {
     -3: "CRI_ERR_ALIGNMENT",
     -4: "CRI_ERR_LAUNCH",
     -5: "CRI_ERR_UNSUPPORTED",
+    -6: "CRI_ERR_FILE",
 }
 
 _MATMUL = ["cri_matmul_" + f for f in ("q8_0", "q4_0", "q5_0", "q4_k", "q6_k", "fp16")]
@@ -77,6 +80,24 @@ ABI_SYMBOLS = (
         "cri_matmul_swiglu",
         "cri_rmsnorm_residual",
         "cri_silu_mul",
+        "cri_gguf_open",
+        "cri_gguf_close",
+        "cri_gguf_version",
+        "cri_gguf_tensor_count",
+        "cri_gguf_metadata_count",
+        "cri_gguf_find_tensor",
+        "cri_gguf_tensor_info",
+        "cri_gguf_tensor_data",
+        "cri_gguf_metadata_type",
+        "cri_gguf_get_u32",
+        "cri_gguf_get_i32",
+        "cri_gguf_get_u64",
+        "cri_gguf_get_f32",
+        "cri_gguf_get_string",
+        "cri_gguf_get_array_length",
+        "cri_gguf_model_params",
+        "cri_gguf_upload",
+        "cri_embedding_rows",
         "cri_last_error_string",
         "cri_block_bytes",
         "cri_block_elems",
@@ -92,6 +113,32 @@ class CretifError(RuntimeError):
 
 
 _lib = None
+
+
+class _GGUFTensor(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("ggml_type", ctypes.c_int),
+        ("format", ctypes.c_int),
+        ("n_dims", ctypes.c_int),
+        ("dims", ctypes.c_longlong * 8),
+        ("n_elements", ctypes.c_longlong),
+        ("byte_size", ctypes.c_longlong),
+        ("data_offset", ctypes.c_longlong),
+    ]
+
+
+class _GGUFModel(ctypes.Structure):
+    _fields_ = [("architecture", ctypes.c_char * 64)] + [
+        (n, ctypes.c_uint)
+        for n in ("context_length", "embedding_length", "block_count", "head_count", "head_count_kv",
+                  "feed_forward_length", "rope_dimension_count", "vocab_size")
+    ] + [
+        ("rope_freq_base", ctypes.c_float),
+        ("rms_norm_eps", ctypes.c_float),
+        ("tie_word_embeddings", ctypes.c_int),
+        ("missing", ctypes.c_uint),
+    ]
 
 
 def lib():
@@ -136,6 +183,37 @@ def lib():
     L.cri_rmsnorm_residual.restype = i32
     L.cri_silu_mul.argtypes = [vp, vp, vp, ctypes.c_longlong, vp]
     L.cri_silu_mul.restype = i32
+    L.cri_embedding_rows.argtypes = [i32, vp, vp, vp, i32, i32, i32, vp]
+    L.cri_embedding_rows.restype = i32
+    ll = ctypes.c_longlong
+    L.cri_gguf_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(vp)]
+    L.cri_gguf_open.restype = i32
+    L.cri_gguf_close.argtypes = [vp]
+    L.cri_gguf_close.restype = None
+    L.cri_gguf_version.argtypes = [vp]
+    L.cri_gguf_version.restype = i32
+    for n in ("cri_gguf_tensor_count", "cri_gguf_metadata_count"):
+        getattr(L, n).argtypes = [vp]
+        getattr(L, n).restype = ll
+    L.cri_gguf_find_tensor.argtypes = [vp, ctypes.c_char_p]
+    L.cri_gguf_find_tensor.restype = i32
+    L.cri_gguf_tensor_info.argtypes = [vp, i32, ctypes.POINTER(_GGUFTensor)]
+    L.cri_gguf_tensor_info.restype = i32
+    L.cri_gguf_tensor_data.argtypes = [vp, i32]
+    L.cri_gguf_tensor_data.restype = vp
+    L.cri_gguf_metadata_type.argtypes = [vp, ctypes.c_char_p]
+    L.cri_gguf_metadata_type.restype = i32
+    for n, t in (("u32", ctypes.c_uint), ("i32", ctypes.c_int), ("u64", ctypes.c_ulonglong), ("f32", ctypes.c_float),
+                 ("string", ctypes.c_char_p)):
+        f = getattr(L, "cri_gguf_get_" + n)
+        f.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(t)]
+        f.restype = i32
+    L.cri_gguf_get_array_length.argtypes = [vp, ctypes.c_char_p]
+    L.cri_gguf_get_array_length.restype = ll
+    L.cri_gguf_model_params.argtypes = [vp, ctypes.POINTER(_GGUFModel)]
+    L.cri_gguf_model_params.restype = i32
+    L.cri_gguf_upload.argtypes = [vp, i32, vp, ll, vp]
+    L.cri_gguf_upload.restype = i32
     L.cri_last_error_string.argtypes = []
     L.cri_last_error_string.restype = ctypes.c_char_p
     L.cri_block_bytes.argtypes = [i32]
@@ -327,3 +405,124 @@ def rmsnorm_residual(input, residual, weight, output, normed, rows, n, eps=1e-5,
 def silu_mul(gate, up, out, n, stream=None):
     """out = silu(gate) * up (cuinfer::silu then cuinfer::multiply, as one launch)."""
     _check(lib().cri_silu_mul(_ptr(gate), _ptr(up), _ptr(out), int(n), _stream(stream)))
+
+
+def embedding_rows(fmt, table, ids, out, n_ids, dim, vocab, stream=None):
+    """out[i] = dequant(table row ids[i]) (zero rows for ids outside [0, vocab)); fmt may be 'fp32'."""
+    fid = 6 if fmt == "fp32" else _fid(fmt)
+    _check(lib().cri_embedding_rows(fid, _ptr(table), _ptr(ids), _ptr(out), n_ids, dim, vocab, _stream(stream)))
+
+
+_MODEL_FIELDS = ("context_length", "embedding_length", "block_count", "head_count", "head_count_kv",
+                 "feed_forward_length", "rope_dimension_count", "vocab_size")
+
+
+class GGUFFile:
+    """A GGUF file opened through cri_gguf_* (the reader of cuinfer::GGUFParser).
+    Metadata getters raise CretifError on a missing key or a type mismatch."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        _check(lib().cri_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().cri_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def version(self):
+        return lib().cri_gguf_version(self._h)
+
+    @property
+    def tensor_count(self):
+        return lib().cri_gguf_tensor_count(self._h)
+
+    @property
+    def metadata_count(self):
+        return lib().cri_gguf_metadata_count(self._h)
+
+    def tensor(self, index):
+        t = _GGUFTensor()
+        _check(lib().cri_gguf_tensor_info(self._h, index, ctypes.byref(t)))
+        return {
+            "name": t.name.decode(),
+            "ggml_type": t.ggml_type,
+            "format": t.format,
+            "dims": [t.dims[i] for i in range(t.n_dims)],
+            "n_elements": t.n_elements,
+            "byte_size": t.byte_size,
+            "data_offset": t.data_offset,
+        }
+
+    def tensors(self):
+        return [self.tensor(i) for i in range(self.tensor_count)]
+
+    def find_tensor(self, name):
+        i = lib().cri_gguf_find_tensor(self._h, name.encode())
+        return None if i < 0 else i
+
+    def tensor_bytes(self, index):
+        """A copy of the tensor's raw bytes (host)."""
+        import numpy as np
+
+        info = self.tensor(index)
+        p = lib().cri_gguf_tensor_data(self._h, index)
+        return np.frombuffer(ctypes.string_at(p, info["byte_size"]), dtype=np.uint8).copy()
+
+    def metadata_type(self, key):
+        return lib().cri_gguf_metadata_type(self._h, key.encode())
+
+    def _get(self, kind, ctype, key):
+        v = ctype()
+        _check(getattr(lib(), "cri_gguf_get_" + kind)(self._h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def get_u32(self, key):
+        return self._get("u32", ctypes.c_uint, key)
+
+    def get_i32(self, key):
+        return self._get("i32", ctypes.c_int, key)
+
+    def get_u64(self, key):
+        return self._get("u64", ctypes.c_ulonglong, key)
+
+    def get_f32(self, key):
+        return self._get("f32", ctypes.c_float, key)
+
+    def get_string(self, key):
+        return self._get("string", ctypes.c_char_p, key).decode()
+
+    def array_length(self, key):
+        n = lib().cri_gguf_get_array_length(self._h, key.encode())
+        if n < 0:
+            _check(int(n))
+        return n
+
+    def model_params(self):
+        m = _GGUFModel()
+        _check(lib().cri_gguf_model_params(self._h, ctypes.byref(m)))
+        out = {"architecture": m.architecture.decode(), "rope_freq_base": m.rope_freq_base,
+               "rms_norm_eps": m.rms_norm_eps, "tie_word_embeddings": bool(m.tie_word_embeddings)}
+        for i, f in enumerate(_MODEL_FIELDS):
+            out[f] = None if m.missing >> i & 1 else getattr(m, f)
+        return out
+
+    def upload(self, index, dst, dst_bytes=None, stream=None):
+        """Copy the tensor's raw bytes to a device buffer (returns when done)."""
+        if dst_bytes is None:
+            dst_bytes = dst.numel() * dst.element_size()
+        _check(lib().cri_gguf_upload(self._h, index, _ptr(dst), int(dst_bytes), _stream(stream)))

@@ -81,6 +81,8 @@ int dequant_impl(int fmt, const void* src, float* dst, int n_blocks, hipStream_t
 
 }  // namespace
 
+void cri_internal_set_error(const char* msg) { g_last_error = msg; }
+
 namespace {
 int fill_zero(float* C, long n, hipStream_t stream, const char* fn) {
     cri::detail::launch_fill_zero(C, n, stream);
@@ -332,6 +334,22 @@ int cri_fused_decode_attention_ws(const float* Q, const float* K_cache, const fl
                     "workspace of " + std::to_string(workspace_bytes) + " bytes holds less than one record per head (" +
                         std::to_string(static_cast<long>(n_heads) * (head_dim + 4) * 4) + " bytes)");
     if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
+    return check_launch(fn);
+}
+
+int cri_embedding_rows(int format, const void* table, const int* ids, float* out, int n_ids, int dim, int vocab,
+                       hipStream_t s) {
+    const char* fn = "cri_embedding_rows";
+    if (format < CRI_Q8_0 || format > CRI_FP32) return fail(CRI_ERR_UNSUPPORTED, fn, "unknown format id");
+    if (n_ids < 0 || dim < 0 || vocab < 0) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative dimension");
+    if (n_ids == 0 || dim == 0) return CRI_OK;
+    if (dim % cri::block_elems(format) != 0)
+        return fail(CRI_ERR_SHAPE, fn, "dim=" + std::to_string(dim) + " is not a multiple of the block size");
+    if (!table || !ids || !out) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(ids, 4) || !aligned(out, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "ids and out must be 4-byte aligned");
+    if ((format == CRI_FP16 && !aligned(table, 2)) || (format == CRI_FP32 && !aligned(table, 4)))
+        return fail(CRI_ERR_ALIGNMENT, fn, "table misaligned for its element type");
+    cri::detail::launch_embedding_rows(format, table, ids, out, n_ids, dim, vocab, s);
     return check_launch(fn);
 }
 

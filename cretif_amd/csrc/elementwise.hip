@@ -64,3 +64,36 @@ int launch_silu_mul(const float* gate, const float* up, float* out, long n, hipS
 
 }  // namespace detail
 }  // namespace cri
+
+// ---- embedding rows from a (quantized) table -------------------------------------
+#include "decode.hpp"
+
+namespace cri {
+namespace dev {
+
+// One workgroup per token: out[i][k] = decode(table row ids[i], k), the
+// reference's per-element dequant (so bit-identical to dequantize + gather).
+__global__ __launch_bounds__(256) void embedding_rows_kernel(int fmt, const uint8_t* __restrict__ table,
+                                                             const int* __restrict__ ids, float* __restrict__ out,
+                                                             int dim, int vocab, long rbytes) {
+    const long i = blockIdx.x;
+    const int id = ids[i];
+    const bool ok = id >= 0 && id < vocab;
+    const uint8_t* row = table + (ok ? static_cast<long>(id) : 0) * rbytes;
+    float* o = out + i * dim;
+    for (int k = threadIdx.x; k < dim; k += 256) o[k] = ok ? decode_row_elem(fmt, row, k) : 0.0f;
+}
+
+}  // namespace dev
+
+namespace detail {
+
+int launch_embedding_rows(int fmt, const void* table, const int* ids, float* out, int n_ids, int dim, int vocab,
+                          hipStream_t stream) {
+    hipLaunchKernelGGL(dev::embedding_rows_kernel, dim3(n_ids), dim3(256), 0, stream, fmt,
+                       static_cast<const uint8_t*>(table), ids, out, dim, vocab, row_bytes(fmt, dim));
+    return 0;
+}
+
+}  // namespace detail
+}  // namespace cri

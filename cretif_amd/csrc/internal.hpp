@@ -83,6 +83,9 @@ int launch_generic_matmul_act(int mode, int fmt, const ActIn& act, const void* B
 int launch_rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output,
                             float* normed, int rows, int n, float eps, hipStream_t stream);
 int launch_silu_mul(const float* gate, const float* up, float* out, long n, hipStream_t stream);
+// token rows of a (quantized) embedding table, dequantized (elementwise.hip)
+int launch_embedding_rows(int fmt, const void* table, const int* ids, float* out, int n_ids, int dim, int vocab,
+                          hipStream_t stream);
 
 // standalone dequant (dequant.hip)
 int launch_dequant(int fmt, const void* src, float* dst, long n_blocks, hipStream_t stream);

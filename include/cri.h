@@ -33,7 +33,8 @@ typedef enum cri_status {
     CRI_ERR_SHAPE = -2,            /* K not a multiple of the block size, etc. */
     CRI_ERR_ALIGNMENT = -3,        /* pointer misaligned for its element type  */
     CRI_ERR_LAUNCH = -4,           /* the HIP runtime rejected a launch        */
-    CRI_ERR_UNSUPPORTED = -5       /* format id unknown                        */
+    CRI_ERR_UNSUPPORTED = -5,      /* format id unknown                        */
+    CRI_ERR_FILE = -6              /* GGUF file missing, unreadable, malformed */
 } cri_status;
 
 /* Weight formats; the numbering is shared with cri_matmul()/cri_dequantize(). */
@@ -43,7 +44,8 @@ typedef enum cri_format {
     CRI_Q5_0 = 2,
     CRI_Q4_K = 3,
     CRI_Q6_K = 4,
-    CRI_FP16 = 5
+    CRI_FP16 = 5,
+    CRI_FP32 = 6 /* only for cri_embedding_rows and cri_gguf_tensor.format */
 } cri_format;
 
 /* ---- fused dequant + matmul: C[M,N] = A[M,K] * dequant(B[N,K])^T ---------- */
@@ -155,6 +157,66 @@ int cri_rmsnorm_residual(const float* input, const float* residual, const float*
 /* out = silu(gate) * up over n elements: cuinfer::silu then cuinfer::multiply,
  * ref:include/cuinfer/kernels/elementwise.h:23 and :75 (out may alias gate or up) */
 int cri_silu_mul(const float* gate, const float* up, float* out, long long n, hipStream_t stream);
+
+/* ---- GGUF files: the weights' on-disk format -------------------------------
+ * A reader with the reference's parsing rules (ref:src/gguf_parser.cpp; the C++
+ * class is cuinfer::GGUFParser in cuinfer/gguf_parser.h), for hosts that bind C.
+ * The file is memory-mapped; names and strings returned stay valid until
+ * cri_gguf_close.  A tensor's data lying past the end of the file is rejected at
+ * open (CRI_ERR_FILE). */
+typedef struct cri_gguf cri_gguf;
+typedef struct cri_gguf_tensor {
+    const char* name;
+    int ggml_type;         /* GGML type tag (0 F32, 1 F16, 2 Q4_0, 6 Q5_0, 8 Q8_0, 12 Q4_K, 14 Q6_K, ...) */
+    int format;            /* cri_format of the data, CRI_FP32, or -1 for types the matmuls do not take */
+    int n_dims;
+    long long dims[8];     /* dims[0] innermost: a [N, K] weight is {K, N} */
+    long long n_elements;
+    long long byte_size;   /* -1 for a GGML type this reader does not know */
+    long long data_offset; /* bytes from the start of the file */
+} cri_gguf_tensor;
+typedef struct cri_gguf_model {
+    char architecture[64]; /* general.architecture */
+    unsigned context_length, embedding_length, block_count, head_count, head_count_kv, feed_forward_length,
+        rope_dimension_count, vocab_size; /* bit i of `missing` set: field i (in this order) absent */
+    float rope_freq_base;  /* default 10000 */
+    float rms_norm_eps;    /* default 1e-5 */
+    int tie_word_embeddings; /* 1 when there is no output.weight */
+    unsigned missing;
+} cri_gguf_model;
+/* replaces cuinfer::GGUFParser::GGUFParser, ref:include/cuinfer/gguf_parser.h:165 */
+int cri_gguf_open(const char* path, cri_gguf** out);
+void cri_gguf_close(cri_gguf* file);
+int cri_gguf_version(const cri_gguf* file);
+long long cri_gguf_tensor_count(const cri_gguf* file);
+long long cri_gguf_metadata_count(const cri_gguf* file);
+/* index of the named tensor, or -1 (find_tensor, ref:include/cuinfer/gguf_parser.h:236) */
+int cri_gguf_find_tensor(const cri_gguf* file, const char* name);
+int cri_gguf_tensor_info(const cri_gguf* file, int index, cri_gguf_tensor* out);
+/* host pointer into the mapping (tensor_data, ref:include/cuinfer/gguf_parser.h:240) */
+const void* cri_gguf_tensor_data(const cri_gguf* file, int index);
+/* GGUF value type tag of a metadata key, or -1 */
+int cri_gguf_metadata_type(const cri_gguf* file, const char* key);
+/* typed getters: CRI_ERR_SHAPE for a missing key or another type (get_*, ref:include/cuinfer/gguf_parser.h:197-201) */
+int cri_gguf_get_u32(const cri_gguf* file, const char* key, unsigned* out);
+int cri_gguf_get_i32(const cri_gguf* file, const char* key, int* out);
+int cri_gguf_get_u64(const cri_gguf* file, const char* key, unsigned long long* out);
+int cri_gguf_get_f32(const cri_gguf* file, const char* key, float* out);
+int cri_gguf_get_string(const cri_gguf* file, const char* key, const char** out);
+long long cri_gguf_get_array_length(const cri_gguf* file, const char* key);
+/* the model helpers, ref:include/cuinfer/gguf_parser.h:208-230 */
+int cri_gguf_model_params(const cri_gguf* file, cri_gguf_model* out);
+/* the tensor's raw bytes to device memory; returns when the copy is done
+ * (the upload of load_weight_quantized, ref:src/model.cu:406-411) */
+int cri_gguf_upload(const cri_gguf* file, int index, void* device_dst, long long dst_bytes, hipStream_t stream);
+
+/* out[i, :] = dequant(row ids[i] of table [vocab, dim]) in fp32, bit-identical to
+ * dequantize + gather; ids outside [0, vocab) give zero rows.  format: a
+ * cri_format or CRI_FP32.  Lets the token embedding stay in its file format
+ * when the LM head reuses it (the reference dequantizes the tied table to
+ * FP32, ref:src/model.cu:603); no counterpart in the reference. */
+int cri_embedding_rows(int format, const void* table, const int* ids, float* out, int n_ids, int dim, int vocab,
+                       hipStream_t stream);
 
 /* ---- diagnostics ---------------------------------------------------------- */
 

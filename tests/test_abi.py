@@ -16,7 +16,7 @@ def header_functions():
     for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
         if h.endswith(".h"):
             text = open(os.path.join(ROOT, "include", h)).read()
-            names += re.findall(r"^\s*(?:int|long long|const char\*)\s+(cri_\w+)\s*\(", text, re.M)
+            names += re.findall(r"^\s*(?:int|long long|void|const void\*|const char\*)\s+(cri_\w+)\s*\(", text, re.M)
     return names
 
 
