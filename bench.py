@@ -51,6 +51,11 @@ GEMV_WORKLOADS = {
     "q4_k_gemv_down": ("q4_k", 2048, 8192),
     "q8_0_gemv_down": ("q8_0", 2048, 8192),
     "q6_k_lm_head": ("q6_k", 128256, 2048),
+    # the reference's tied LM head: the token table dequantized to fp32 and multiplied by
+    # matmul_transposed_b (ref:src/model.cu:1027-1029); against q6_k_lm_head / q8_0_lm_head it
+    # shows what keeping the tied table quantized saves
+    "fp32_tied_lm_head": ("fp32", 128256, 2048),
+    "q8_0_lm_head": ("q8_0", 128256, 2048),
 }
 
 
@@ -70,7 +75,8 @@ class GemvRig:
         from cretif_amd import quant
 
         self.fmt, self.N, self.K, self.M = fmt, N, K, M
-        w = tiled_weights(fmt, N, K, seed=seed)
+        w = tiled_weights(fmt, N, K, seed=seed) if fmt != "fp32" else \
+            quant.randn(N * K, seed=seed).astype(np.float32).view(np.uint8)
         self.wbytes = w.size
         self.copies = int(max(1, min(max_copies, -(-min_bytes // w.size))))
         base = torch.from_numpy(w).cuda()
@@ -81,13 +87,19 @@ class GemvRig:
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
+        def run(Wi):
+            if fmt == "fp32":
+                cri.matmul_transposed_b(self.x, Wi, self.y, M, N, K)
+            else:
+                cri.matmul(fmt, self.x, Wi, self.y, M, N, K)
+
         with torch.cuda.stream(side):
             for Wi in self.W:  # eager warm-up on the side stream
-                cri.matmul(fmt, self.x, Wi, self.y, M, N, K)
+                run(Wi)
         side.synchronize()
         with torch.cuda.graph(self.graph, stream=side):
             for Wi in self.W:
-                cri.matmul(fmt, self.x, Wi, self.y, M, N, K)
+                run(Wi)
         torch.cuda.synchronize()
 
     def bytes_per_launch(self):

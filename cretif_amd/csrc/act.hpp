@@ -31,10 +31,11 @@ struct ActRaw<kActRMSNorm> {
     f32x4 h, r, w;
 };
 
-// Loads of x[m][k .. k+4) (k % 4 == 0, all four in range).
+// Loads of x[m][k .. k+4) (k % 4 == 0, all four in range); rows lda floats apart
+// (the kernels pass K in plain mode, so P.lda is not read there).
 template <int MODE>
-__device__ __forceinline__ void act_load(ActRaw<MODE>& raw, const ActIn& P, int m, int k) {
-    const long off = static_cast<long>(m) * P.lda + k;
+__device__ __forceinline__ void act_load(ActRaw<MODE>& raw, const ActIn& P, int m, int k, long lda) {
+    const long off = static_cast<long>(m) * lda + k;
     if constexpr (MODE == kActPlain) {
         raw.a = ld_f32x4(P.a + off);
     } else if constexpr (MODE == kActSwiGLU) {

@@ -33,10 +33,11 @@ namespace dev {
 // the activations, so the HBM latency of the weights overlaps the activation
 // fetch; afterwards every decoded row-group is immediately replaced by the
 // row-group PREF steps ahead.
+// The activation prologue comes last in the arguments (the first 16 argument
+// dwords are preloaded into SGPRs; P.a still falls inside them).
 template <class F, int UPL, int PREF, int MODE>
-__global__ __launch_bounds__(256) void gemv_kernel(const ActIn P, const uint8_t* __restrict__ W,
-                                                   float* __restrict__ y, int N, int K, int units, long row_bytes,
-                                                   int lpr_log2) {
+__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W, float* __restrict__ y, int N, int K,
+                                                   int units, long row_bytes, int lpr_log2, const ActIn P) {
     extern __shared__ float xs[];  // K activations, staged once per workgroup (+4 partial sums)
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
@@ -62,7 +63,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const ActIn P, const uint8_t*
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int j = threadIdx.x + 256 * i;
-        if (j < nx4) act_load<MODE>(xv[i], P, 0, 4 * j);
+        if (j < nx4) act_load<MODE>(xv[i], P, 0, 4 * j, 0);
     }
     typename F::Data buf[PREF][UPL];
     const int base0 = gwave * rows_per_iter;
@@ -86,7 +87,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const ActIn P, const uint8_t*
     }
     for (int j = threadIdx.x + 1024; j < nx4; j += 256) {
         ActRaw<MODE> raw;
-        act_load<MODE>(raw, P, 0, 4 * j);
+        act_load<MODE>(raw, P, 0, 4 * j, 0);
         *reinterpret_cast<f32x4*>(xs + 4 * j) = act_finish<MODE>(raw, P, 0, 4 * j, K, ss, write_h);
     }
     if constexpr (MODE == kActRMSNorm) {
@@ -140,8 +141,8 @@ static void launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int 
     if (waves > kGemvTargetWaves) waves = kGemvTargetWaves;
     const int blocks = static_cast<int>((waves + 3) / 4);
     const int lds = (K + (MODE == kActRMSNorm ? 4 : 0)) * static_cast<int>(sizeof(float));
-    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE>), dim3(blocks), dim3(256), lds, stream, act,
-                       static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2);
+    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE>), dim3(blocks), dim3(256), lds, stream,
+                       static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act);
 }
 
 template <class F, int MODE>

@@ -53,14 +53,14 @@ __global__ __launch_bounds__(256) void generic_matmul_kernel(int fmt, const ActI
             f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
             if (m < M && k + 4 <= K) {
                 ActRaw<MODE> raw;
-                act_load<MODE>(raw, P, m, k);
+                act_load<MODE>(raw, P, m, k, MODE == kActPlain ? K : P.lda);
                 v = act_finish<MODE>(raw, P, m, k, K, ss, blockIdx.x == 0);
             } else if (m < M) {
                 // ragged K: one element at a time (the four-wide form needs k + 4 <= K)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     if (k + i >= K) break;
-                    const long off = static_cast<long>(m) * P.lda + k + i;
+                    const long off = static_cast<long>(m) * (MODE == kActPlain ? K : P.lda) + k + i;
                     float x;
                     if constexpr (MODE == kActPlain) {
                         x = P.a[off];

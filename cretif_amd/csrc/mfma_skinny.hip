@@ -176,6 +176,7 @@ __device__ __forceinline__ void sk_clear_unscale(int M, int KC, float* unscale) 
 template <int MODE>
 __device__ void sk_stage(const ActIn& P, int M, int K, int k0, int KC, char* lds, const SkLds& L) {
     const int tid = threadIdx.x, nth = blockDim.x;
+    const long lda = MODE == kActPlain ? K : P.lda;
     const bool write_h = blockIdx.x == 0;
     float* ssq = MODE == kActRMSNorm ? reinterpret_cast<float*>(lds + L.ssq) + (k0 >> 8) * 16 : nullptr;
     _Float16* xh = reinterpret_cast<_Float16*>(lds + L.xh);
@@ -192,10 +193,11 @@ __device__ void sk_stage(const ActIn& P, int M, int K, int k0, int KC, char* lds
 #pragma unroll
         for (int it = 0; it < kItems; ++it) {
             const int e = e_batch + it * nth + tid;
+            if constexpr (MODE == kActPlain) ra[it].a = rb[it].a = f32x4{0.f, 0.f, 0.f, 0.f};
             if (e < total) {
                 const int m = e / groups, g8 = e - m * groups;
-                act_load<MODE>(ra[it], P, m, k0 + 8 * g8);
-                act_load<MODE>(rb[it], P, m, k0 + 8 * g8 + 4);
+                act_load<MODE>(ra[it], P, m, k0 + 8 * g8, lda);
+                act_load<MODE>(rb[it], P, m, k0 + 8 * g8 + 4, lda);
             }
         }
 #pragma unroll
@@ -205,13 +207,17 @@ __device__ void sk_stage(const ActIn& P, int M, int K, int k0, int KC, char* lds
             const int e = e0 + tid;
             const bool live = e < total;
             const int m = live ? e / groups : 0, g8 = live ? e - m * groups : 0;
-            float ss = 0.0f;
-            f32x4 va = f32x4{0.f, 0.f, 0.f, 0.f}, vb = va;
-            if (live) {
-                va = act_finish<MODE>(ra[it], P, m, k0 + 8 * g8, K, ss, write_h);
-                vb = act_finish<MODE>(rb[it], P, m, k0 + 8 * g8 + 4, K, ss, write_h);
+            if constexpr (MODE == kActPlain) {
+                sk_convert_item(ra[it].a, rb[it].a, live, m, g8, KC, xh, xl, xs, unscale);
+            } else {
+                float ss = 0.0f;
+                f32x4 va = f32x4{0.f, 0.f, 0.f, 0.f}, vb = va;
+                if (live) {
+                    va = act_finish<MODE>(ra[it], P, m, k0 + 8 * g8, K, ss, write_h);
+                    vb = act_finish<MODE>(rb[it], P, m, k0 + 8 * g8 + 4, K, ss, write_h);
+                }
+                sk_convert_item(va, vb, live, m, g8, KC, xh, xl, xs, unscale, ss, ssq);
             }
-            sk_convert_item(va, vb, live, m, g8, KC, xh, xl, xs, unscale, ss, ssq);
         }
     }
     __syncthreads();
@@ -221,13 +227,15 @@ __device__ void sk_stage(const ActIn& P, int M, int K, int k0, int KC, char* lds
 // loads are issued at kernel start, before the weight loads, and converted
 // here: waiting for them does not wait for the weights.
 template <int MODE>
-__device__ __forceinline__ void sk_load_one(const ActIn& P, int M, int k0, int KC, ActRaw<MODE>& a,
+__device__ __forceinline__ void sk_load_one(const ActIn& P, int M, int K, int k0, int KC, ActRaw<MODE>& a,
                                             ActRaw<MODE>& b) {
     const int groups = KC / 8, e = threadIdx.x;
+    const long lda = MODE == kActPlain ? K : P.lda;
+    if constexpr (MODE == kActPlain) a.a = b.a = f32x4{0.f, 0.f, 0.f, 0.f};  // dead lanes convert zeros
     if (e < M * groups) {
         const int m = e / groups, g8 = e - m * groups;
-        act_load<MODE>(a, P, m, k0 + 8 * g8);
-        act_load<MODE>(b, P, m, k0 + 8 * g8 + 4);
+        act_load<MODE>(a, P, m, k0 + 8 * g8, lda);
+        act_load<MODE>(b, P, m, k0 + 8 * g8 + 4, lda);
     }
 }
 template <int MODE>
@@ -243,14 +251,18 @@ __device__ __forceinline__ void sk_stage_one(const ActRaw<MODE>& ra, const ActRa
     if ((e & ~63) < total) {  // whole waves past the items skip (lane reductions need all 64 lanes)
         const bool live = e < total;
         const int m = live ? e / groups : 0, g8 = live ? e - m * groups : 0;
-        float ss = 0.0f;
-        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = a;
-        if (live) {
-            a = act_finish<MODE>(ra, P, m, k0 + 8 * g8, K, ss, blockIdx.x == 0);
-            b = act_finish<MODE>(rb, P, m, k0 + 8 * g8 + 4, K, ss, blockIdx.x == 0);
+        if constexpr (MODE == kActPlain) {
+            sk_convert_item(ra.a, rb.a, live, m, g8, KC, xh, xl, xs, unscale);
+        } else {
+            float ss = 0.0f;
+            f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = a;
+            if (live) {
+                a = act_finish<MODE>(ra, P, m, k0 + 8 * g8, K, ss, blockIdx.x == 0);
+                b = act_finish<MODE>(rb, P, m, k0 + 8 * g8 + 4, K, ss, blockIdx.x == 0);
+            }
+            float* ssq = MODE == kActRMSNorm ? reinterpret_cast<float*>(lds + L.ssq) + (k0 >> 8) * 16 : nullptr;
+            sk_convert_item(a, b, live, m, g8, KC, xh, xl, xs, unscale, ss, ssq);
         }
-        float* ssq = MODE == kActRMSNorm ? reinterpret_cast<float*>(lds + L.ssq) + (k0 >> 8) * 16 : nullptr;
-        sk_convert_item(a, b, live, m, g8, KC, xh, xl, xs, unscale, ss, ssq);
     }
     __syncthreads();
 }
@@ -442,10 +454,13 @@ struct SkQ6K {
 // Workgroup = NW waves = (NW / KS) tiles x KS k-splits.  The grid strides
 // over groups of NW / KS tiles; wave w works on tile w / KS of the group and
 // on super-blocks j = w % KS, + KS, ... of the current activation chunk.
+// The activation prologue comes last in the arguments: the first 16 argument
+// dwords are preloaded into SGPRs, and the shape integers are needed first
+// (the plain path reads only P.a, which still falls inside them).
 template <class F, int NW, int MODE>
-__global__ __launch_bounds__(64 * NW) void skinny_kernel(const ActIn P, const uint8_t* __restrict__ B,
-                                                             float* __restrict__ C, int M, int N, int K, int KC,
-                                                             int ks_log2, int ngroups, int nchunks) {
+__global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restrict__ B, float* __restrict__ C, int M,
+                                                             int N, int K, int KC, int ks_log2, int ngroups,
+                                                             int nchunks, const ActIn P) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const SkLds L = sk_layout(M, KC, NW, K, MODE == kActRMSNorm);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -482,7 +497,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const ActIn P, const ui
             const bool stage = grp == static_cast<int>(blockIdx.x) || nchunks > 1;
             const bool one = M * (KC / 8) <= 64 * NW;
             ActRaw<MODE> xa, xb;
-            if (stage && one) sk_load_one<MODE>(P, M, k0, KC, xa, xb);
+            if (stage && one) sk_load_one<MODE>(P, M, K, k0, KC, xa, xb);
             typename F::Item b0, b1;
             if (nitems > 0) load_item(b0, 0);
             if (nitems > 1) load_item(b1, 1);
@@ -580,8 +595,8 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
     if (blocks < 1) blocks = 1;
     const dev::SkLds L = dev::sk_layout(M, KC, NW, K, MODE == kActRMSNorm);
     if (L.bytes > 160 * 1024) return -1;
-    hipLaunchKernelGGL((dev::skinny_kernel<F, NW, MODE>), dim3(blocks), dim3(64 * NW), L.bytes, stream, A,
-                       static_cast<const uint8_t*>(B), C, M, N, K, KC, ks_log2, groups, K / KC);
+    hipLaunchKernelGGL((dev::skinny_kernel<F, NW, MODE>), dim3(blocks), dim3(64 * NW), L.bytes, stream,
+                       static_cast<const uint8_t*>(B), C, M, N, K, KC, ks_log2, groups, K / KC, A);
     return 0;
 }
 
