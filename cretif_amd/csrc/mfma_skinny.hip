@@ -341,6 +341,7 @@ __device__ __forceinline__ f4 q4k_block(const Q4KItem& d, const _Float16* xha, c
 // contribution to the lane's four outputs.
 struct SkQ4K {
     static constexpr int kBlockBytes = 144;
+    static constexpr int kSliceStride = 64;  // lane group g holds k [64 g, 64 g + 64) of a super-block
     typedef Q4KItem Item;
     static __device__ __forceinline__ void load(Item& d, const uint8_t* sb, int g) {
         d.h = ld_u32x4_a16(sb);
@@ -368,6 +369,7 @@ struct Q6KItem {
 };
 struct SkQ6K {
     static constexpr int kBlockBytes = 210;
+    static constexpr int kSliceStride = 64;
     typedef Q6KItem Item;
     static __device__ __forceinline__ void load(Item& d, const uint8_t* sb, int g) {
         const int c = g >> 1;
@@ -451,6 +453,229 @@ struct SkQ6K {
     }
 };
 
+// ---- 32-element block formats (Q8_0, Q4_0, Q5_0) and FP16 --------------------------
+//
+// An item is 8 consecutive 32-element blocks of a row (256 k, the same unit as a
+// K-quant super-block, so the activation chunks and k splits are shared).  MFMA s
+// of an item covers block s alone: lane group g supplies its elements
+// [8 g, 8 g + 8), so each block's product (x_hi.q + x_lo.q, q an exact fp16
+// integer) is finished in one output register set and scaled by that block's d
+// -- the output lane's column is the weight row it loaded.  The staged
+// activations hold k in groups of 8 with the (0,2),(1,3),(4,6),(5,7) pair order,
+// which each format's unpack produces.  Blocks start at any 2-byte offset: the
+// loads round down to a dword and funnel-shift, and read only dwords that lie
+// inside the item (the parity of s, a compile-time constant, says which).
+
+// One block: P = x_hi . w + x_lo . w on the matrix cores, r += d * P.
+__device__ __forceinline__ void blk_accumulate(const half8 ah, const half8 al, const half8 bw, float d, f4& r) {
+    f4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    P = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, P, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = __builtin_fmaf(d, P[i], r[i]);
+}
+
+__device__ __forceinline__ void blk_load_x(const _Float16* xha, const _Float16* xla, bool has_row, half8 (&ah)[8],
+                                           half8 (&al)[8]) {
+    const half8 zero8 = half8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) ah[s] = al[s] = zero8;
+    if (has_row) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            ah[s] = *reinterpret_cast<const half8*>(xha + 32 * s);
+            al[s] = *reinterpret_cast<const half8*>(xla + 32 * s);
+        }
+    }
+}
+
+__device__ __forceinline__ float half_bits(uint32_t h) { return h_lo(h); }
+
+// Q8_0 (ref:src/kernels/dequantize.cu:34-47): 34-byte blocks, int8 quants at
+// byte 2.  Lane slice = 8 quants at 34 s + 2 + 8 g: dword offset 2 for even s
+// (3 dwords, shifted), 0 for odd s (2 dwords).  q + 128 (sign bit flipped) is
+// placed in the 1024 + b pattern and 1152 subtracted: q exactly.
+struct Q8Item {
+    uint32_t q[8][3];
+    uint32_t d[8];
+};
+struct SkQ8_0 {
+    static constexpr int kBlockBytes = 272;  // 8 blocks
+    static constexpr int kSliceStride = 8;
+    typedef Q8Item Item;
+    static __device__ __forceinline__ void load(Item& d, const uint8_t* it, int g) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint8_t* p = it + 34 * s + 8 * g + (s & 1 ? 2 : 0);  // dword-aligned
+            d.q[s][0] = ld_u32(p);
+            d.q[s][1] = ld_u32(p + 4);
+            d.q[s][2] = (s & 1) ? 0u : ld_u32(p + 8);
+            d.d[s] = *reinterpret_cast<const uint16_t*>(it + 34 * s);
+        }
+    }
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
+                                               const _Float16*, bool has_row, int, const float (&us)[4]) {
+        half8 ah[8], al[8];
+        blk_load_x(xha, xla, has_row, ah, al);
+        const uint32_t off = f16x2_splat(-1152.0f);
+        f4 r = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint32_t w0 = ((s & 1) ? d.q[s][0] : __builtin_amdgcn_alignbyte(d.q[s][1], d.q[s][0], 2)) ^ 0x80808080u;
+            const uint32_t w1 = ((s & 1) ? d.q[s][1] : __builtin_amdgcn_alignbyte(d.q[s][2], d.q[s][1], 2)) ^ 0x80808080u;
+            typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+            const u4 b = u4{pk_fma_f16(and_or(w0, 0x00FF00FFu, 0x64006400u), 0x3C003C00u, off),
+                            pk_fma_f16(and_or(w0 >> 8, 0x00FF00FFu, 0x64006400u), 0x3C003C00u, off),
+                            pk_fma_f16(and_or(w1, 0x00FF00FFu, 0x64006400u), 0x3C003C00u, off),
+                            pk_fma_f16(and_or(w1 >> 8, 0x00FF00FFu, 0x64006400u), 0x3C003C00u, off)};
+            blk_accumulate(ah[s], al[s], __builtin_bit_cast(half8, b), half_bits(d.d[s]), r);
+        }
+        f4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = us[i] * r[i];
+        return o;
+    }
+};
+
+// Q4_0 in the reference's element order (element e <- qs[e / 2], low nibble for
+// even e; ref:src/kernels/dequantize.cu:84-100): 18-byte blocks, the lane's 8
+// elements are the 4 bytes at 18 s + 2 + 4 g.  Bytes (b0 b1 b2 b3) are permuted
+// to (b0 b2 b1 b3), so nibble fields at shifts 0, 4, 8, 12 give the element
+// pairs (0,2), (1,3), (4,6), (5,7); 1032 is subtracted from 1024 + nib.
+struct Q4Item {
+    uint32_t q[8][2];
+    uint32_t d[8];
+};
+struct SkQ4_0 {
+    static constexpr int kBlockBytes = 144;
+    static constexpr int kSliceStride = 8;
+    typedef Q4Item Item;
+    static __device__ __forceinline__ void load(Item& d, const uint8_t* it, int g) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint8_t* p = it + 18 * s + 4 * g + (s & 1 ? 2 : 0);  // dword-aligned
+            d.q[s][0] = ld_u32(p);
+            d.q[s][1] = (s & 1) ? 0u : ld_u32(p + 4);
+            d.d[s] = *reinterpret_cast<const uint16_t*>(it + 18 * s);
+        }
+    }
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
+                                               const _Float16*, bool has_row, int, const float (&us)[4]) {
+        half8 ah[8], al[8];
+        blk_load_x(xha, xla, has_row, ah, al);
+        const uint32_t off = f16x2_splat(-1032.0f);
+        f4 r = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint32_t w = (s & 1) ? d.q[s][0] : __builtin_amdgcn_alignbyte(d.q[s][1], d.q[s][0], 2);
+            const uint32_t wp = __builtin_amdgcn_perm(w, w, 0x03010200u);  // bytes (b0, b2, b1, b3)
+            typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+            const u4 b = u4{pk_fma_f16(and_or(wp, 0x000F000Fu, 0x64006400u), 0x3C003C00u, off),
+                            pk_fma_f16(and_or(wp >> 4, 0x000F000Fu, 0x64006400u), 0x3C003C00u, off),
+                            pk_fma_f16(and_or(wp >> 8, 0x000F000Fu, 0x64006400u), 0x3C003C00u, off),
+                            pk_fma_f16(and_or(wp >> 12, 0x000F000Fu, 0x64006400u), 0x3C003C00u, off)};
+            blk_accumulate(ah[s], al[s], __builtin_bit_cast(half8, b), half_bits(d.d[s]), r);
+        }
+        f4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = us[i] * r[i];
+        return o;
+    }
+};
+
+// Q5_0 (ref:src/kernels/dequantize.cu:137-164): 22-byte blocks, d, qh (u32 LE)
+// at 2, qs at 6; element e: low nibble of qs[e % 16] for e < 16 else the high
+// one, high bit = bit e of qh.  Lane group g takes qs bytes [8 (g & 1), +8)
+// (nibble shift 4 (g >> 1)) and qh byte g; each bit pair moves to bits 4 and 20
+// of its fp16 pair, OR-ed into the 1024 pattern; 1040 is subtracted.
+struct Q5Item {
+    uint32_t q[8][3];
+    uint32_t h[8];
+    uint32_t d[8];
+};
+struct SkQ5_0 {
+    static constexpr int kBlockBytes = 176;
+    static constexpr int kSliceStride = 8;
+    typedef Q5Item Item;
+    static __device__ __forceinline__ void load(Item& d, const uint8_t* it, int g) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint8_t* blk = it + 22 * s;
+            const uint8_t* p = blk + 6 + 8 * (g & 1) - (s & 1 ? 0 : 2);  // dword-aligned
+            d.q[s][0] = ld_u32(p);
+            d.q[s][1] = ld_u32(p + 4);
+            d.q[s][2] = (s & 1) ? 0u : ld_u32(p + 8);
+            const uintptr_t hb = reinterpret_cast<uintptr_t>(blk + 2 + g);
+            d.h[s] = (ld_u32(reinterpret_cast<const uint8_t*>(hb & ~static_cast<uintptr_t>(3))) >> (8 * (hb & 3))) & 0xFFu;
+            d.d[s] = *reinterpret_cast<const uint16_t*>(blk);
+        }
+    }
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
+                                               const _Float16*, bool has_row, int g, const float (&us)[4]) {
+        half8 ah[8], al[8];
+        blk_load_x(xha, xla, has_row, ah, al);
+        const uint32_t off = f16x2_splat(-1040.0f);
+        const uint32_t sh = 4 * (g >> 1);
+        f4 r = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint32_t w0 = ((s & 1) ? d.q[s][0] : __builtin_amdgcn_alignbyte(d.q[s][1], d.q[s][0], 2)) >> sh;
+            const uint32_t w1 = ((s & 1) ? d.q[s][1] : __builtin_amdgcn_alignbyte(d.q[s][2], d.q[s][1], 2)) >> sh;
+            const uint32_t t = d.h[s];  // qh byte g in the low 8 bits
+            const uint32_t h02 = ((t << 4) | (t << 18)) & 0x00100010u;
+            const uint32_t h13 = ((t << 3) | (t << 17)) & 0x00100010u;
+            const uint32_t h46 = (t | (t << 14)) & 0x00100010u;
+            const uint32_t h57 = ((t >> 1) | (t << 13)) & 0x00100010u;
+            typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+            const u4 b = u4{pk_fma_f16(and_or(w0, 0x000F000Fu, 0x64006400u | h02), 0x3C003C00u, off),
+                            pk_fma_f16(and_or(w0 >> 8, 0x000F000Fu, 0x64006400u | h13), 0x3C003C00u, off),
+                            pk_fma_f16(and_or(w1, 0x000F000Fu, 0x64006400u | h46), 0x3C003C00u, off),
+                            pk_fma_f16(and_or(w1 >> 8, 0x000F000Fu, 0x64006400u | h57), 0x3C003C00u, off)};
+            blk_accumulate(ah[s], al[s], __builtin_bit_cast(half8, b), half_bits(d.d[s]), r);
+        }
+        f4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = us[i] * r[i];
+        return o;
+    }
+};
+
+// FP16 weights (ref:src/kernels/matmul_quant.cu:510-558): the lane's 8 halves
+// at 64 s + 16 g are the B operand after a half swap into the (0,2),(1,3),(4,6),
+// (5,7) order; products fp16 x fp16 are exact in fp32, two MFMA chains.
+struct F16Item {
+    u32x4 v[8];
+};
+struct SkF16 {
+    static constexpr int kBlockBytes = 512;
+    static constexpr int kSliceStride = 8;
+    typedef F16Item Item;
+    static __device__ __forceinline__ void load(Item& d, const uint8_t* it, int g) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) d.v[s] = ld_u32x4(it + 64 * s + 16 * g);
+    }
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
+                                               const _Float16*, bool has_row, int, const float (&us)[4]) {
+        half8 ah[8], al[8];
+        blk_load_x(xha, xla, has_row, ah, al);
+        f4 Ph = f4{0.f, 0.f, 0.f, 0.f}, Pl = Ph;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const u32x4 v = d.v[s];
+            typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+            const u4 b = u4{__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.y, v.x, 0x07060302u),
+                            __builtin_amdgcn_perm(v.w, v.z, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
+            const half8 bw = __builtin_bit_cast(half8, b);
+            Ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bw, Ph, 0, 0, 0);
+            Pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s], bw, Pl, 0, 0, 0);
+        }
+        const f4 P = Ph + Pl;
+        f4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = us[i] * P[i];
+        return o;
+    }
+};
+
 // Workgroup = NW waves = (NW / KS) tiles x KS k-splits.  The grid strides
 // over groups of NW / KS tiles; wave w works on tile w / KS of the group and
 // on super-blocks j = w % KS, + KS, ... of the current activation chunk.
@@ -507,7 +732,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
             }
             auto run_item = [&](const typename F::Item& d, int it) {
                 const int jj = my_split + (it << ks_log2);
-                const int base = m_a * sk_xstride(KC) + jj * 256 + 64 * g;
+                const int base = m_a * sk_xstride(KC) + jj * 256 + F::kSliceStride * g;
                 const f32x4 u4 = *reinterpret_cast<const f32x4*>(unscale + jj * 16 + 4 * g);  // rows 4g .. 4g+3
                 const float us[4] = {u4.x, u4.y, u4.z, u4.w};
                 acc += F::block(d, xh + base, xl + base, xs + m_a * sk_sstride(KC) + 4 * (jj * 4 + g), has_row, g,
@@ -568,6 +793,9 @@ bool skinny_supported(int fmt, int M, int K, const void* B) {
     if (fmt == kFmtQ4_K) return (reinterpret_cast<uintptr_t>(B) & 15u) == 0;  // 16-byte loads of 144-byte blocks
     // Q6_K: the batch-1 GEMV streams it at HBM rate; 2..16 rows share each decoded block here
     if (fmt == kFmtQ6_K) return M >= 2 && (reinterpret_cast<uintptr_t>(B) & 1u) == 0;
+    // the 32-element formats and FP16 likewise from 2 rows; rows of 8-block items stay dword-aligned
+    if (fmt == kFmtQ8_0 || fmt == kFmtQ4_0 || fmt == kFmtQ5_0 || fmt == kFmtF16)
+        return M >= 2 && (reinterpret_cast<uintptr_t>(B) & 3u) == 0;
     return false;
 }
 
@@ -616,8 +844,15 @@ static int launch_skinny_m(int fmt, const ActIn& A, const void* B, float* C, int
     while (KS < 8 && KS * 2 <= sb && static_cast<long>(ntiles) * KS < 2048) KS *= 2;
     // eight waves per workgroup (8 / KS tiles each): measured faster than four for
     // every decode shape, from 512 x 2048 to the 128256 x 2048 lm_head
-    if (fmt == kFmtQ6_K) return launch_sk<dev::SkQ6K, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
-    return launch_sk<dev::SkQ4K, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
+    switch (fmt) {
+        case kFmtQ6_K: return launch_sk<dev::SkQ6K, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtQ4_K: return launch_sk<dev::SkQ4K, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtQ8_0: return launch_sk<dev::SkQ8_0, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtQ4_0: return launch_sk<dev::SkQ4_0, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtQ5_0: return launch_sk<dev::SkQ5_0, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtF16: return launch_sk<dev::SkF16, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
+    }
+    return -1;
 }
 
 int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream) {

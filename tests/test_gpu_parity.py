@@ -368,3 +368,32 @@ def test_gqa(orc, H, Hkv, M, N, K):
     cri.batched_matmul_gqa(dev(A), dev(B), C, H, Hkv, M, N, K)
     ref = orc.batched_matmul_gqa(A, B, H, Hkv, M, N, K)
     assert normwise_rel_err(host(C), ref) <= GEMV_TOL
+
+
+# ---- the 32-element formats and FP16 on the skinny MFMA kernel (2 <= M <= 16) ----
+def random_code_weights(fmt, N, K, seed):
+    """Raw random bytes for every quant field (all codes, Q8_0 -128 included, all Q5_0
+    high bits), with each block's fp16 scale replaced by a finite value in
+    [2^-10, 2^3]; FP16 weights as random finite halves."""
+    rng = np.random.default_rng(seed)
+    if fmt == "fp16":
+        return rng.uniform(-2, 2, size=N * K).astype(np.float16).view(np.uint8)
+    bb = quant.BLOCK_BYTES[fmt]
+    raw = rng.integers(0, 256, size=(N * K // 32, bb), dtype=np.uint8)
+    d = (rng.choice([-1.0, 1.0], size=raw.shape[0]) * 2.0 ** rng.uniform(-10, 3, size=raw.shape[0])).astype(np.float16)
+    raw[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    return raw.ravel()
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q5_0", "fp16"])
+@pytest.mark.parametrize("M,N,K,off", [(2, 37, 256, 0), (3, 200, 768, 4), (9, 64, 2048, 8), (16, 50, 8192, 12),
+                                       (16, 1024, 4096, 0)])
+def test_skinny_block_formats_random_codes(orc, fmt, M, N, K, off):
+    A = quant.randn(M * K, seed=M * 7 + K).reshape(M, K)
+    Bq = random_code_weights(fmt, N, K, seed=N + off)
+    buf = torch.zeros(Bq.size + 16, dtype=torch.uint8, device="cuda")
+    buf[off:off + Bq.size] = dev(Bq)
+    C = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    cri.matmul(fmt, dev(A), buf.data_ptr() + off, C, M, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert normwise_rel_err(host(C), ref) <= GEMV_TOL
