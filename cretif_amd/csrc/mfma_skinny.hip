@@ -160,9 +160,10 @@ __device__ __forceinline__ void sk_convert_item(const f32x4 a, const f32x4 b, bo
 }
 
 // Slots of unscale[] for rows m >= M (never written by the items) read as 0.
+template <int NT>
 __device__ __forceinline__ void sk_clear_unscale(int M, int KC, float* unscale) {
     const int nsb = KC / 256;
-    for (int e = threadIdx.x; e < nsb * 16; e += blockDim.x)
+    for (int e = threadIdx.x; e < nsb * 16; e += NT)
         if ((e & 15) >= M) unscale[e] = 0.0f;
 }
 
@@ -173,9 +174,10 @@ __device__ __forceinline__ void sk_clear_unscale(int M, int KC, float* unscale) 
 // are strided over the threads in batches of kSkMaxItems per thread, each
 // batch's loads issued before any of its items is converted.  Per-sub-block
 // sums (times 2^-6) feed the mins MFMA.  One barrier.
-template <int MODE>
+template <int MODE, int NT>
 __device__ void sk_stage(const ActIn& P, int M, int K, int k0, int KC, char* lds, const SkLds& L) {
-    const int tid = threadIdx.x, nth = blockDim.x;
+    const int tid = threadIdx.x;
+    constexpr int nth = NT;
     const long lda = MODE == kActPlain ? K : P.lda;
     const bool write_h = blockIdx.x == 0;
     float* ssq = MODE == kActRMSNorm ? reinterpret_cast<float*>(lds + L.ssq) + (k0 >> 8) * 16 : nullptr;
@@ -184,7 +186,7 @@ __device__ void sk_stage(const ActIn& P, int M, int K, int k0, int KC, char* lds
     _Float16* xs = reinterpret_cast<_Float16*>(lds + L.xs);
     float* unscale = reinterpret_cast<float*>(lds + L.scl);
     const int groups = KC / 8;  // k8 groups per row; a multiple of 32
-    sk_clear_unscale(M, KC, unscale);
+    sk_clear_unscale<NT>(M, KC, unscale);
     const int total = M * groups;  // a multiple of 32
     // items per load batch: the prologues hold 2x (SwiGLU) or 3x (RMSNorm) the raw values per item
     constexpr int kItems = MODE == kActPlain ? kSkMaxItems : (MODE == kActSwiGLU ? 4 : 3);
@@ -238,7 +240,7 @@ __device__ __forceinline__ void sk_load_one(const ActIn& P, int M, int K, int k0
         act_load<MODE>(b, P, m, k0 + 8 * g8 + 4, lda);
     }
 }
-template <int MODE>
+template <int MODE, int NT>
 __device__ __forceinline__ void sk_stage_one(const ActRaw<MODE>& ra, const ActRaw<MODE>& rb, const ActIn& P, int M,
                                              int K, int k0, int KC, char* lds, const SkLds& L) {
     _Float16* xh = reinterpret_cast<_Float16*>(lds + L.xh);
@@ -246,7 +248,7 @@ __device__ __forceinline__ void sk_stage_one(const ActRaw<MODE>& ra, const ActRa
     _Float16* xs = reinterpret_cast<_Float16*>(lds + L.xs);
     float* unscale = reinterpret_cast<float*>(lds + L.scl);
     const int groups = KC / 8, e = threadIdx.x;
-    sk_clear_unscale(M, KC, unscale);
+    sk_clear_unscale<NT>(M, KC, unscale);
     const int total = M * groups;
     if ((e & ~63) < total) {  // whole waves past the items skip (lane reductions need all 64 lanes)
         const bool live = e < total;
@@ -267,17 +269,29 @@ __device__ __forceinline__ void sk_stage_one(const ActRaw<MODE>& ra, const ActRa
     __syncthreads();
 }
 
+// The A operand of the skinny MFMAs.  Activation rows are staged as fp16 x_hi
+// and x_lo (x_hi + x_lo = x to ~22 bits).  Two lane-row layouts:
+//  - plain (M > 8): lane row m supplies x_hi of activation row m to one MFMA
+//    chain and x_lo to a second one; output row m is the sum of both;
+//  - paired (PAIR, M <= 8): lane row 2 i supplies x_hi and lane row 2 i + 1
+//    x_lo of activation row i to the same MFMA, so one MFMA does the work of
+//    two, and output rows 2 i and 2 i + 1 are added in the epilogue.
+// Lane rows past the real ones read the last real row: an A row only feeds
+// its own output row, and those are never stored (their unscale factor is 0).
+// x0 / x1 point at the lane's hi / lo row (plain) or its one row (paired; x1
+// unused); odd marks the lo rows of the paired layout.
+
 // One Q4_K super-block of a 16-row tile, computed by one wave.
 struct Q4KItem {
     u32x4 h, q0, q1;
 };
 
 // acc contribution of one super-block: lane (g = k slice, n) holds the row's
-// 32 qs bytes of chunk g (sub-blocks 2g, 2g+1) and the 16-byte header; lanes
-// with m < M supply their row's activations from LDS (xa points at
-// row m, super-block start + 64 g).
-__device__ __forceinline__ f4 q4k_block(const Q4KItem& d, const _Float16* xha, const _Float16* xla,
-                                        const _Float16* xsa, bool has_row, int g, const float (&us)[4]) {
+// 32 qs bytes of chunk g (sub-blocks 2g, 2g+1) and the 16-byte header; x0 / x1
+// point at the lane's activation row(s) in LDS, super-block start + 64 g.
+template <bool PAIR>
+__device__ __forceinline__ f4 q4k_block(const Q4KItem& d, const _Float16* x0, const _Float16* x1,
+                                        const _Float16* xsa, bool odd, int g, const float (&us)[4]) {
     // 6-bit scale / min of sub-blocks 2g, 2g+1 (ref:src/kernels/dequantize.cu:298-305)
     const bool low = g < 2;
     const uint32_t o = (g & 1) * 16;
@@ -294,20 +308,16 @@ __device__ __forceinline__ f4 q4k_block(const Q4KItem& d, const _Float16* xha, c
     const uint32_t mul_lo = f16x2_splat(fsl), add_lo = f16x2_splat(-1024.0f * fsl);
     const uint32_t mul_hi = f16x2_splat(fsh * 0.0625f), add_hi = f16x2_splat(-64.0f * fsh);
     const uint32_t q[8] = {d.q0.x, d.q0.y, d.q0.z, d.q0.w, d.q1.x, d.q1.y, d.q1.z, d.q1.w};
-    const half8 zero8 = half8{0, 0, 0, 0, 0, 0, 0, 0};
-    half8 ah[8], al[8];
-    half4 as4 = half4{0, 0, 0, 0};
+    half8 a0[8], a1[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) ah[s] = al[s] = zero8;
-    if (has_row) {  // only lanes carrying real activation rows read LDS; one batch per item
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            ah[s] = *reinterpret_cast<const half8*>(xha + 8 * s);
-            al[s] = *reinterpret_cast<const half8*>(xla + 8 * s);
-        }
-        as4 = *reinterpret_cast<const half4*>(xsa);
+    for (int s = 0; s < 8; ++s) {  // one batch of LDS reads per item
+        a0[s] = *reinterpret_cast<const half8*>(x0 + 8 * s);
+        if constexpr (!PAIR) a1[s] = *reinterpret_cast<const half8*>(x1 + 8 * s);
     }
-    f4 Ph = f4{0.f, 0.f, 0.f, 0.f}, Pl = Ph;  // two independent MFMA chains
+    // sub-block sums (hi and lo parts); paired: they enter once, on the even row
+    half4 as4 = *reinterpret_cast<const half4*>(xsa);
+    if constexpr (PAIR) as4 = odd ? half4{0, 0, 0, 0} : as4;
+    f4 P0 = f4{0.f, 0.f, 0.f, 0.f}, P1 = P0;  // two independent MFMA chains
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
         const uint32_t w0 = q[2 * (s & 3)], w1 = q[2 * (s & 3) + 1];
@@ -319,10 +329,15 @@ __device__ __forceinline__ f4 q4k_block(const Q4KItem& d, const _Float16* xha, c
                         pk_fma_f16(and_or(w1, m4, 0x64006400u), mul, add),
                         pk_fma_f16(and_or(w1 >> 8, m4, 0x64006400u), mul, add)};
         const half8 bw = __builtin_bit_cast(half8, b);
-        Ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bw, Ph, 0, 0, 0);
-        Pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s], bw, Pl, 0, 0, 0);
+        if constexpr (PAIR) {
+            if (s & 1) P1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[s], bw, P1, 0, 0, 0);
+            else P0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[s], bw, P0, 0, 0, 0);
+        } else {
+            P0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[s], bw, P0, 0, 0, 0);
+            P1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[s], bw, P1, 0, 0, 0);
+        }
     }
-    const f4 P = Ph + Pl;
+    const f4 P = P0 + P1;
     // mins: sum over sub-blocks of mn * X on a 16x16x16 MFMA, slots (Xhi, Xhi, Xlo, Xlo)
     const uint32_t mnp = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(mn_lo))) |
                          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(mn_hi))) << 16);
@@ -348,9 +363,10 @@ struct SkQ4K {
         d.q0 = ld_u32x4_a16(sb + 16 + 32 * g);
         d.q1 = ld_u32x4_a16(sb + 32 + 32 * g);
     }
-    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
-                                               const _Float16* xsa, bool has_row, int g, const float (&us)[4]) {
-        return q4k_block(d, xha, xla, xsa, has_row, g, us);
+    template <bool PAIR>
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* x0, const _Float16* x1,
+                                               const _Float16* xsa, bool odd, int g, const float (&us)[4]) {
+        return q4k_block<PAIR>(d, x0, x1, xsa, odd, g, us);
     }
 };
 
@@ -394,8 +410,9 @@ struct SkQ6K {
         d.d = *reinterpret_cast<const uint16_t*>(sb + 208);
         d.shift = static_cast<uint32_t>(sh);
     }
-    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
-                                               const _Float16*, bool has_row, int g, const float (&us)[4]) {
+    template <bool PAIR>
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* x0, const _Float16* x1,
+                                               const _Float16*, bool, int g, const float (&us)[4]) {
         const uint32_t sh = d.shift;
         const uint32_t scs = __builtin_amdgcn_alignbyte(d.sc[1], d.sc[0], sh);
         uint32_t sc2[4];
@@ -403,17 +420,15 @@ struct SkQ6K {
         for (int j = 0; j < 4; ++j) sc2[j] = f16x2_splat(static_cast<float>(static_cast<int8_t>(scs >> (8 * j))));
         const uint32_t bias = f16x2_splat(-1056.0f);  // (1024 + q6) - 1056 = q6 - 32
         const uint32_t lsh = 4 * (g & 1);
-        const half8 zero8 = half8{0, 0, 0, 0, 0, 0, 0, 0};
-        half8 ah[8], al[8];
+        half8 a0[8], a1[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) ah[s] = al[s] = zero8;
-        if (has_row) {
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                ah[s] = *reinterpret_cast<const half8*>(xha + 8 * s);
-                al[s] = *reinterpret_cast<const half8*>(xla + 8 * s);
-            }
+        for (int s = 0; s < 8; ++s) {
+            a0[s] = *reinterpret_cast<const half8*>(x0 + 8 * s);
+            if constexpr (!PAIR) a1[s] = *reinterpret_cast<const half8*>(x1 + 8 * s);
         }
+        // Ph: x_hi (paired: x_hi or x_lo) times the weights' hi part, Pc: times the
+        // lo part (paired: for both rows, adding the tiny x_lo * lo term), Pl: x_lo
+        // times the hi part (plain only)
         f4 Ph = f4{0.f, 0.f, 0.f, 0.f}, Pl = Ph, Pc = Ph;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
@@ -440,9 +455,9 @@ struct SkQ6K {
                 lo[r] = pk_fma_f16(q, sc, hi[r] ^ 0x80008000u);
             }
             const half8 bh = __builtin_bit_cast(half8, hi), bl = __builtin_bit_cast(half8, lo);
-            Ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bh, Ph, 0, 0, 0);
-            Pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s], bh, Pl, 0, 0, 0);
-            Pc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bl, Pc, 0, 0, 0);
+            Ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[s], bh, Ph, 0, 0, 0);
+            if constexpr (!PAIR) Pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[s], bh, Pl, 0, 0, 0);
+            Pc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[s], bl, Pc, 0, 0, 0);
         }
         const f4 P = (Ph + Pl) + Pc;
         const float dd = h_lo(d.d);
@@ -466,25 +481,22 @@ struct SkQ6K {
 // loads round down to a dword and funnel-shift, and read only dwords that lie
 // inside the item (the parity of s, a compile-time constant, says which).
 
-// One block: P = x_hi . w + x_lo . w on the matrix cores, r += d * P.
-__device__ __forceinline__ void blk_accumulate(const half8 ah, const half8 al, const half8 bw, float d, f4& r) {
-    f4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    P = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, P, 0, 0, 0);
+// One block: P = x_hi . w + x_lo . w on the matrix cores (one MFMA when the
+// rows are paired), r += d * P.
+template <bool PAIR>
+__device__ __forceinline__ void blk_accumulate(const half8 a0, const half8 a1, const half8 bw, float d, f4& r) {
+    f4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bw, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    if constexpr (!PAIR) P = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bw, P, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[i] = __builtin_fmaf(d, P[i], r[i]);
 }
 
-__device__ __forceinline__ void blk_load_x(const _Float16* xha, const _Float16* xla, bool has_row, half8 (&ah)[8],
-                                           half8 (&al)[8]) {
-    const half8 zero8 = half8{0, 0, 0, 0, 0, 0, 0, 0};
+template <bool PAIR>
+__device__ __forceinline__ void blk_load_x(const _Float16* x0, const _Float16* x1, half8 (&a0)[8], half8 (&a1)[8]) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) ah[s] = al[s] = zero8;
-    if (has_row) {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            ah[s] = *reinterpret_cast<const half8*>(xha + 32 * s);
-            al[s] = *reinterpret_cast<const half8*>(xla + 32 * s);
-        }
+    for (int s = 0; s < 8; ++s) {
+        a0[s] = *reinterpret_cast<const half8*>(x0 + 32 * s);
+        if constexpr (!PAIR) a1[s] = *reinterpret_cast<const half8*>(x1 + 32 * s);
     }
 }
 
@@ -512,10 +524,11 @@ struct SkQ8_0 {
             d.d[s] = *reinterpret_cast<const uint16_t*>(it + 34 * s);
         }
     }
-    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
-                                               const _Float16*, bool has_row, int, const float (&us)[4]) {
-        half8 ah[8], al[8];
-        blk_load_x(xha, xla, has_row, ah, al);
+    template <bool PAIR>
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* x0, const _Float16* x1,
+                                               const _Float16*, bool, int, const float (&us)[4]) {
+        half8 a0[8], a1[8];
+        blk_load_x<PAIR>(x0, x1, a0, a1);
         const uint32_t off = f16x2_splat(-1152.0f);
         f4 r = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -527,7 +540,7 @@ struct SkQ8_0 {
                             pk_fma_f16(and_or(w0 >> 8, 0x00FF00FFu, 0x64006400u), 0x3C003C00u, off),
                             pk_fma_f16(and_or(w1, 0x00FF00FFu, 0x64006400u), 0x3C003C00u, off),
                             pk_fma_f16(and_or(w1 >> 8, 0x00FF00FFu, 0x64006400u), 0x3C003C00u, off)};
-            blk_accumulate(ah[s], al[s], __builtin_bit_cast(half8, b), half_bits(d.d[s]), r);
+            blk_accumulate<PAIR>(a0[s], a1[s], __builtin_bit_cast(half8, b), half_bits(d.d[s]), r);
         }
         f4 o;
 #pragma unroll
@@ -558,10 +571,11 @@ struct SkQ4_0 {
             d.d[s] = *reinterpret_cast<const uint16_t*>(it + 18 * s);
         }
     }
-    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
-                                               const _Float16*, bool has_row, int, const float (&us)[4]) {
-        half8 ah[8], al[8];
-        blk_load_x(xha, xla, has_row, ah, al);
+    template <bool PAIR>
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* x0, const _Float16* x1,
+                                               const _Float16*, bool, int, const float (&us)[4]) {
+        half8 a0[8], a1[8];
+        blk_load_x<PAIR>(x0, x1, a0, a1);
         const uint32_t off = f16x2_splat(-1032.0f);
         f4 r = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -573,7 +587,7 @@ struct SkQ4_0 {
                             pk_fma_f16(and_or(wp >> 4, 0x000F000Fu, 0x64006400u), 0x3C003C00u, off),
                             pk_fma_f16(and_or(wp >> 8, 0x000F000Fu, 0x64006400u), 0x3C003C00u, off),
                             pk_fma_f16(and_or(wp >> 12, 0x000F000Fu, 0x64006400u), 0x3C003C00u, off)};
-            blk_accumulate(ah[s], al[s], __builtin_bit_cast(half8, b), half_bits(d.d[s]), r);
+            blk_accumulate<PAIR>(a0[s], a1[s], __builtin_bit_cast(half8, b), half_bits(d.d[s]), r);
         }
         f4 o;
 #pragma unroll
@@ -609,10 +623,11 @@ struct SkQ5_0 {
             d.d[s] = *reinterpret_cast<const uint16_t*>(blk);
         }
     }
-    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
-                                               const _Float16*, bool has_row, int g, const float (&us)[4]) {
-        half8 ah[8], al[8];
-        blk_load_x(xha, xla, has_row, ah, al);
+    template <bool PAIR>
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* x0, const _Float16* x1,
+                                               const _Float16*, bool, int g, const float (&us)[4]) {
+        half8 a0[8], a1[8];
+        blk_load_x<PAIR>(x0, x1, a0, a1);
         const uint32_t off = f16x2_splat(-1040.0f);
         const uint32_t sh = 4 * (g >> 1);
         f4 r = f4{0.f, 0.f, 0.f, 0.f};
@@ -630,7 +645,7 @@ struct SkQ5_0 {
                             pk_fma_f16(and_or(w0 >> 8, 0x000F000Fu, 0x64006400u | h13), 0x3C003C00u, off),
                             pk_fma_f16(and_or(w1, 0x000F000Fu, 0x64006400u | h46), 0x3C003C00u, off),
                             pk_fma_f16(and_or(w1 >> 8, 0x000F000Fu, 0x64006400u | h57), 0x3C003C00u, off)};
-            blk_accumulate(ah[s], al[s], __builtin_bit_cast(half8, b), half_bits(d.d[s]), r);
+            blk_accumulate<PAIR>(a0[s], a1[s], __builtin_bit_cast(half8, b), half_bits(d.d[s]), r);
         }
         f4 o;
 #pragma unroll
@@ -653,10 +668,11 @@ struct SkF16 {
 #pragma unroll
         for (int s = 0; s < 8; ++s) d.v[s] = ld_u32x4(it + 64 * s + 16 * g);
     }
-    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* xha, const _Float16* xla,
-                                               const _Float16*, bool has_row, int, const float (&us)[4]) {
-        half8 ah[8], al[8];
-        blk_load_x(xha, xla, has_row, ah, al);
+    template <bool PAIR>
+    static __device__ __forceinline__ f4 block(const Item& d, const _Float16* x0, const _Float16* x1,
+                                               const _Float16*, bool, int, const float (&us)[4]) {
+        half8 a0[8], a1[8];
+        blk_load_x<PAIR>(x0, x1, a0, a1);
         f4 Ph = f4{0.f, 0.f, 0.f, 0.f}, Pl = Ph;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
@@ -665,8 +681,13 @@ struct SkF16 {
             const u4 b = u4{__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.y, v.x, 0x07060302u),
                             __builtin_amdgcn_perm(v.w, v.z, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
             const half8 bw = __builtin_bit_cast(half8, b);
-            Ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bw, Ph, 0, 0, 0);
-            Pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s], bw, Pl, 0, 0, 0);
+            if constexpr (PAIR) {  // two chains over alternate slices
+                if (s & 1) Pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[s], bw, Pl, 0, 0, 0);
+                else Ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[s], bw, Ph, 0, 0, 0);
+            } else {
+                Ph = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[s], bw, Ph, 0, 0, 0);
+                Pl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[s], bw, Pl, 0, 0, 0);
+            }
         }
         const f4 P = Ph + Pl;
         f4 o;
@@ -679,71 +700,105 @@ struct SkF16 {
 // Workgroup = NW waves = (NW / KS) tiles x KS k-splits.  The grid strides
 // over groups of NW / KS tiles; wave w works on tile w / KS of the group and
 // on super-blocks j = w % KS, + KS, ... of the current activation chunk.
-// The activation prologue comes last in the arguments: the first 16 argument
-// dwords are preloaded into SGPRs, and the shape integers are needed first
-// (the plain path reads only P.a, which still falls inside them).
-template <class F, int NW, int MODE>
-__global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restrict__ B, float* __restrict__ C, int M,
-                                                             int N, int K, int KC, int ks_log2, int ngroups,
-                                                             int nchunks, const ActIn P) {
+// Argument order: the 14 dwords of B, C, A and the eight integers are
+// preloaded into SGPRs at wave launch (an aggregate argument and the hidden
+// grid sizes are not), so the plain path issues its first loads without
+// waiting on a scalar load of the argument block.  The activation pointer is
+// passed on its own (A == P.a); the rest of the prologue comes last.
+template <class F, int NW, int MODE, bool PAIR>
+__global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restrict__ B, float* __restrict__ C,
+                                                             const float* __restrict__ A, int M, int N, int K, int KC,
+                                                             int ks_log2, int ngroups, int nchunks, int nblocks,
+                                                             const ActIn Pin) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const SkLds L = sk_layout(M, KC, NW, K, MODE == kActRMSNorm);
+    const ActIn P{A, Pin.b, Pin.w, Pin.h_out, Pin.lda, Pin.eps};
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, nl = lane & 15;
-    const int m_a = lane & 15;  // row of the A operand this lane supplies
-    const bool has_row = m_a < M;
     const int KS = 1 << ks_log2;              // k-splits per tile (power of two)
     const int TW = NW >> ks_log2;             // tiles per group
     const int my_tile = wave >> ks_log2, my_split = wave & (KS - 1);
-    const int ntiles = (N + 15) >> 4;
     const long rbytes = static_cast<long>(K >> 8) * F::kBlockBytes;
+    const int sb_chunk = KC / 256;
+    const int nitems = (sb_chunk - my_split + KS - 1) >> ks_log2;  // super-blocks per wave per chunk
+    const bool one = M * (KC / 8) <= 64 * NW;  // at most one activation item per thread
+    // weight row of this lane in group grp (clamped: the last tile may be partial)
+    auto row_ptr = [&](int grp) {
+        const int row = min((grp * TW + my_tile) * 16 + nl, N - 1);
+        return B + static_cast<long>(row) * rbytes;
+    };
+    auto load_item = [&](typename F::Item& d, const uint8_t* cp, int it) {
+        F::load(d, cp + static_cast<long>(it << ks_log2) * F::kBlockBytes, g);
+    };
+    // The first chunk of the first group is requested before anything else is
+    // computed: the single-item activation loads, then the first two
+    // super-blocks of this wave.  Everything after waits on them anyway.
+    typename F::Item b0, b1;
+    ActRaw<MODE> xa, xb;
+    {
+        const uint8_t* cp = row_ptr(blockIdx.x) + static_cast<long>(my_split) * F::kBlockBytes;
+        if (one) sk_load_one<MODE>(P, M, K, 0, KC, xa, xb);
+        if (nitems > 0) load_item(b0, cp, 0);
+        if (nitems > 1) load_item(b1, cp, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    const SkLds L = sk_layout(M, KC, NW, K, MODE == kActRMSNorm);
+    // A operand of this lane (lane row m_a): activation row xrow, its hi and lo
+    // parts (plain) or one of them (paired: lo on odd lane rows)
+    const int m_a = lane & 15;
+    const int xrow = min(PAIR ? m_a >> 1 : m_a, M - 1);
+    const bool odd = PAIR && (m_a & 1);
+    const int ntiles = (N + 15) >> 4;
     const _Float16* xh = reinterpret_cast<const _Float16*>(lds + L.xh);
     const _Float16* xl = reinterpret_cast<const _Float16*>(lds + L.xl);
     const _Float16* xs = reinterpret_cast<const _Float16*>(lds + L.xs);
+    const _Float16* x0 = (odd ? xl : xh) + xrow * sk_xstride(KC) + F::kSliceStride * g;
+    const _Float16* x1 = xl + xrow * sk_xstride(KC) + F::kSliceStride * g;
+    const _Float16* xsr = xs + xrow * sk_sstride(KC) + 4 * g;
     const float* unscale = reinterpret_cast<const float*>(lds + L.scl);
     float* red = reinterpret_cast<float*>(lds + L.red);
-    const int sb_chunk = KC / 256;
-    const int nitems = (sb_chunk - my_split + KS - 1) >> ks_log2;  // super-blocks per wave per chunk
 
-    for (int grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {
+    for (int grp = blockIdx.x; grp < ngroups; grp += nblocks) {
         const int tile = grp * TW + my_tile;
-        int row = tile * 16 + nl;
-        row = row < N ? row : N - 1;
-        const uint8_t* rowp = B + static_cast<long>(row) * rbytes;
+        const uint8_t* rowp = row_ptr(grp);
         f4 acc = f4{0.f, 0.f, 0.f, 0.f};
         for (int c = 0; c < nchunks; ++c) {
             const int k0 = c * KC;
             const uint8_t* cp = rowp + static_cast<long>((k0 >> 8) + my_split) * F::kBlockBytes;
-            auto load_item = [&](typename F::Item& d, int it) {
-                F::load(d, cp + static_cast<long>(it << ks_log2) * F::kBlockBytes, g);
-            };
-            // the first two super-blocks are requested before the activations are
-            // staged; single-item activation loads go first of all
-            const bool stage = grp == static_cast<int>(blockIdx.x) || nchunks > 1;
-            const bool one = M * (KC / 8) <= 64 * NW;
-            ActRaw<MODE> xa, xb;
-            if (stage && one) sk_load_one<MODE>(P, M, K, k0, KC, xa, xb);
-            typename F::Item b0, b1;
-            if (nitems > 0) load_item(b0, 0);
-            if (nitems > 1) load_item(b1, 1);
+            // activations are staged for every chunk of the first group, and for
+            // every group when there are several chunks
+            const bool first = grp == static_cast<int>(blockIdx.x);
+            const bool stage = first || nchunks > 1;
+            if (!first || c > 0) {  // chunk 0 of the first group was requested at entry
+                if (stage && one) sk_load_one<MODE>(P, M, K, k0, KC, xa, xb);
+                if (nitems > 0) load_item(b0, cp, 0);
+                if (nitems > 1) load_item(b1, cp, 1);
+            }
             if (stage) {
-                if (one) sk_stage_one<MODE>(xa, xb, P, M, K, k0, KC, lds, L);
-                else sk_stage<MODE>(P, M, K, k0, KC, lds, L);
+                if (one) sk_stage_one<MODE, 64 * NW>(xa, xb, P, M, K, k0, KC, lds, L);
+                else sk_stage<MODE, 64 * NW>(P, M, K, k0, KC, lds, L);
             }
             auto run_item = [&](const typename F::Item& d, int it) {
                 const int jj = my_split + (it << ks_log2);
-                const int base = m_a * sk_xstride(KC) + jj * 256 + F::kSliceStride * g;
-                const f32x4 u4 = *reinterpret_cast<const f32x4*>(unscale + jj * 16 + 4 * g);  // rows 4g .. 4g+3
-                const float us[4] = {u4.x, u4.y, u4.z, u4.w};
-                acc += F::block(d, xh + base, xl + base, xs + m_a * sk_sstride(KC) + 4 * (jj * 4 + g), has_row, g,
-                                us);
+                // unscale of this lane's four output rows: activation rows 4g .. 4g+3,
+                // paired 2g, 2g, 2g+1, 2g+1
+                float us[4];
+                if constexpr (PAIR) {
+                    const f32x2 u2 = *reinterpret_cast<const f32x2*>(unscale + jj * 16 + 2 * g);
+                    us[0] = us[1] = u2.x;
+                    us[2] = us[3] = u2.y;
+                } else {
+                    const f32x4 u4 = *reinterpret_cast<const f32x4*>(unscale + jj * 16 + 4 * g);
+                    us[0] = u4.x, us[1] = u4.y, us[2] = u4.z, us[3] = u4.w;
+                }
+                acc += F::template block<PAIR>(d, x0 + jj * 256, x1 + jj * 256, xsr + 16 * jj, odd, g, us);
             };
             for (int it = 0; it < nitems; it += 2) {
                 run_item(b0, it);
-                if (it + 2 < nitems) load_item(b0, it + 2);
+                if (it + 2 < nitems) load_item(b0, cp, it + 2);
                 if (it + 1 >= nitems) break;
                 run_item(b1, it + 1);
-                if (it + 3 < nitems) load_item(b1, it + 3);
+                if (it + 3 < nitems) load_item(b1, cp, it + 3);
             }
             if (nchunks > 1) __syncthreads();  // the next chunk overwrites the staged activations
         }
@@ -759,27 +814,33 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
                 return 1.0f;
             }
         };
+        // output values of this lane: rows 4g + r (r < 4), paired rows 2g + r (r < 2)
+        // as the sum of the hi and lo lane rows
+        constexpr int kRows = PAIR ? 2 : 4;
+        f4 out = acc;
+        if constexpr (PAIR) out = f4{acc[0] + acc[1], acc[2] + acc[3], 0.f, 0.f};
         // reduce the KS k-split partials of each tile: red[w][r][lane]
         if (KS == 1) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = 4 * g + r, n = tile * 16 + nl;
-                if (m < M && n < N && tile < ntiles) C[static_cast<long>(m) * N + n] = acc[r] * row_factor(m);
+            for (int r = 0; r < kRows; ++r) {
+                const int m = kRows * g + r, n = tile * 16 + nl;
+                if (m < M && n < N && tile < ntiles) C[static_cast<long>(m) * N + n] = out[r] * row_factor(m);
             }
         } else {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) red[(wave * 4 + r) * 64 + lane] = acc[r];
+            for (int r = 0; r < kRows; ++r) red[(wave * 4 + r) * 64 + lane] = out[r];
             __syncthreads();
             // threads of wave w finish tile w / KS, register r = (w % KS) ... spread 4 regs x 64 lanes per tile
             for (int e = threadIdx.x; e < TW * 256; e += 64 * NW) {
                 const int t = e >> 8, r = (e >> 6) & 3, ln = e & 63;
+                if (r >= kRows) continue;
                 float sum = 0.0f;
                 for (int sp = 0; sp < KS; ++sp) sum += red[(((t << ks_log2) + sp) * 4 + r) * 64 + ln];
                 const int tt = grp * TW + t;
-                const int m = 4 * (ln >> 4) + r, n = tt * 16 + (ln & 15);
+                const int m = kRows * (ln >> 4) + r, n = tt * 16 + (ln & 15);
                 if (m < M && n < N && tt < ntiles) C[static_cast<long>(m) * N + n] = sum * row_factor(m);
             }
-            __syncthreads();
+            if (grp + nblocks < ngroups) __syncthreads();  // the next group reuses red[]
         }
     }
 }
@@ -799,7 +860,7 @@ bool skinny_supported(int fmt, int M, int K, const void* B) {
     return false;
 }
 
-template <class F, int NW, int MODE>
+template <class F, int NW, int MODE, bool PAIR>
 static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int K, int KC, int KS,
                      hipStream_t stream) {
     // large chunks need more than the default 64 KB of dynamic LDS: raise the limit once per kernel and device
@@ -808,7 +869,7 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
     int devid = 0;
     if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return -1;
     if (!ready[devid].load(std::memory_order_acquire)) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::skinny_kernel<F, NW, MODE>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::skinny_kernel<F, NW, MODE, PAIR>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
             return -1;
         ready[devid].store(true, std::memory_order_release);
@@ -823,9 +884,17 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
     if (blocks < 1) blocks = 1;
     const dev::SkLds L = dev::sk_layout(M, KC, NW, K, MODE == kActRMSNorm);
     if (L.bytes > 160 * 1024) return -1;
-    hipLaunchKernelGGL((dev::skinny_kernel<F, NW, MODE>), dim3(blocks), dim3(64 * NW), L.bytes, stream,
-                       static_cast<const uint8_t*>(B), C, M, N, K, KC, ks_log2, groups, K / KC, A);
+    hipLaunchKernelGGL((dev::skinny_kernel<F, NW, MODE, PAIR>), dim3(blocks), dim3(64 * NW), L.bytes, stream,
+                       static_cast<const uint8_t*>(B), C, A.a, M, N, K, KC, ks_log2, groups, K / KC, blocks, A);
     return 0;
+}
+
+// up to 8 activation rows: hi and lo parts share each MFMA (paired lane rows)
+template <class F, int MODE>
+static int launch_sk_rows(const ActIn& A, const void* B, float* C, int M, int N, int K, int KC, int KS,
+                          hipStream_t stream) {
+    if (M <= 8) return launch_sk<F, 8, MODE, true>(A, B, C, M, N, K, KC, KS, stream);
+    return launch_sk<F, 8, MODE, false>(A, B, C, M, N, K, KC, KS, stream);
 }
 
 template <int MODE>
@@ -845,12 +914,12 @@ static int launch_skinny_m(int fmt, const ActIn& A, const void* B, float* C, int
     // eight waves per workgroup (8 / KS tiles each): measured faster than four for
     // every decode shape, from 512 x 2048 to the 128256 x 2048 lm_head
     switch (fmt) {
-        case kFmtQ6_K: return launch_sk<dev::SkQ6K, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
-        case kFmtQ4_K: return launch_sk<dev::SkQ4K, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
-        case kFmtQ8_0: return launch_sk<dev::SkQ8_0, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
-        case kFmtQ4_0: return launch_sk<dev::SkQ4_0, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
-        case kFmtQ5_0: return launch_sk<dev::SkQ5_0, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
-        case kFmtF16: return launch_sk<dev::SkF16, 8, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtQ6_K: return launch_sk_rows<dev::SkQ6K, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtQ4_K: return launch_sk_rows<dev::SkQ4K, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtQ8_0: return launch_sk_rows<dev::SkQ8_0, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtQ4_0: return launch_sk_rows<dev::SkQ4_0, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtQ5_0: return launch_sk_rows<dev::SkQ5_0, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtF16: return launch_sk_rows<dev::SkF16, MODE>(A, B, C, M, N, K, KC, KS, stream);
     }
     return -1;
 }
