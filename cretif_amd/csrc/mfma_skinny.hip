@@ -697,6 +697,18 @@ struct SkF16 {
     }
 };
 
+// p[0] + p[256] + ... + p[256 (KS - 1)], in that order, all reads issued first.
+template <int KS>
+__device__ __forceinline__ float sum_splits(const float* p) {
+    float v[KS];
+#pragma unroll
+    for (int i = 0; i < KS; ++i) v[i] = p[256 * i];
+    float s = v[0];
+#pragma unroll
+    for (int i = 1; i < KS; ++i) s += v[i];
+    return s;
+}
+
 // Workgroup = NW waves = (NW / KS) tiles x KS k-splits.  The grid strides
 // over groups of NW / KS tiles; wave w works on tile w / KS of the group and
 // on super-blocks j = w % KS, + KS, ... of the current activation chunk.
@@ -736,7 +748,14 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
     ActRaw<MODE> xa, xb;
     {
         const uint8_t* cp = row_ptr(blockIdx.x) + static_cast<long>(my_split) * F::kBlockBytes;
-        if (one) sk_load_one<MODE>(P, M, K, 0, KC, xa, xb);
+        if (one) {
+            sk_load_one<MODE>(P, M, K, 0, KC, xa, xb);
+            // every wave's activation loads enter the vector-memory queue before any
+            // weight load: the L1 returns data in request order, and the weights
+            // miss to HBM while the activations are L2 hits (no wait here)
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+        }
         if (nitems > 0) load_item(b0, cp, 0);
         if (nitems > 1) load_item(b1, cp, 1);
     }
@@ -834,8 +853,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
             for (int e = threadIdx.x; e < TW * 256; e += 64 * NW) {
                 const int t = e >> 8, r = (e >> 6) & 3, ln = e & 63;
                 if (r >= kRows) continue;
-                float sum = 0.0f;
-                for (int sp = 0; sp < KS; ++sp) sum += red[(((t << ks_log2) + sp) * 4 + r) * 64 + ln];
+                const float* rp = red + ((t << ks_log2) * 4 + r) * 64 + ln;  // split sp at rp[256 sp]
+                const float sum = ks_log2 == 1 ? sum_splits<2>(rp) : ks_log2 == 2 ? sum_splits<4>(rp) : sum_splits<8>(rp);
                 const int tt = grp * TW + t;
                 const int m = kRows * (ln >> 4) + r, n = tt * 16 + (ln & 15);
                 if (m < M && n < N && tt < ntiles) C[static_cast<long>(m) * N + n] = sum * row_factor(m);
