@@ -73,9 +73,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 #pragma unroll
         for (int u = 0; u < UPL; ++u) F::load(dst[u], rp, unit[u]);
     };
+    // Every prefetch is issued unconditionally (rows past the end are clamped to
+    // row N - 1, cached after its first read): a load under a condition leaves
+    // the compiler unsure how many loads are in flight, and it then waits for
+    // all of them before decoding the oldest row-group.
 #pragma unroll
-    for (int p = 0; p < PREF; ++p)
-        if (base0 + p * stride < N) load_rows(buf[p], base0 + p * stride);
+    for (int p = 0; p < PREF; ++p) load_rows(buf[p], base0 + p * stride);
 
     // 2. stage activations in LDS (K <= 4096 is covered by the four loads above)
     float ss = 0.0f;
@@ -117,11 +120,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 #pragma unroll
         for (int p = 0; p < PREF; ++p) {
             const int bp = b + p * stride;
-            if (bp < N) {
-                finish(buf[p], bp);
-                const int bn = bp + PREF * stride;
-                if (bn < N) load_rows(buf[p], bn);
-            }
+            if (bp < N) finish(buf[p], bp);
+            load_rows(buf[p], bp + PREF * stride);
         }
     }
 }

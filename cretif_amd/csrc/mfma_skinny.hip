@@ -741,9 +741,19 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
     auto load_item = [&](typename F::Item& d, const uint8_t* cp, int it) {
         F::load(d, cp + static_cast<long>(it << ks_log2) * F::kBlockBytes, g);
     };
+    // item it if it exists, else a placeholder read that every lane takes from the
+    // same address (one cache line per instruction; the registers go unused)
+    auto load_item_or_none = [&](typename F::Item& d, const uint8_t* cp, int it) {
+        const bool real = it < nitems;
+        F::load(d, real ? cp + static_cast<long>(it << ks_log2) * F::kBlockBytes : B, real ? g : 0);
+    };
     // The first chunk of the first group is requested before anything else is
     // computed: the single-item activation loads, then the first two
     // super-blocks of this wave.  Everything after waits on them anyway.
+    // Weight loads are never under a condition: the compiler then knows how many
+    // are in flight and waits only for the ones a computation needs (a guarded
+    // load makes it wait for all of them).  A wave with one item fills b1 with a
+    // placeholder read instead.
     typename F::Item b0, b1;
     ActRaw<MODE> xa, xb;
     {
@@ -756,8 +766,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_barrier();
         }
-        if (nitems > 0) load_item(b0, cp, 0);
-        if (nitems > 1) load_item(b1, cp, 1);
+        load_item(b0, cp, 0);
+        load_item_or_none(b1, cp, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -777,68 +787,42 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
     const float* unscale = reinterpret_cast<const float*>(lds + L.scl);
     float* red = reinterpret_cast<float*>(lds + L.red);
 
-    for (int grp = blockIdx.x; grp < ngroups; grp += nblocks) {
-        const int tile = grp * TW + my_tile;
-        const uint8_t* rowp = row_ptr(grp);
-        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-        for (int c = 0; c < nchunks; ++c) {
-            const int k0 = c * KC;
-            const uint8_t* cp = rowp + static_cast<long>((k0 >> 8) + my_split) * F::kBlockBytes;
-            // activations are staged for every chunk of the first group, and for
-            // every group when there are several chunks
-            const bool first = grp == static_cast<int>(blockIdx.x);
-            const bool stage = first || nchunks > 1;
-            if (!first || c > 0) {  // chunk 0 of the first group was requested at entry
-                if (stage && one) sk_load_one<MODE>(P, M, K, k0, KC, xa, xb);
-                if (nitems > 0) load_item(b0, cp, 0);
-                if (nitems > 1) load_item(b1, cp, 1);
-            }
-            if (stage) {
-                if (one) sk_stage_one<MODE, 64 * NW>(xa, xb, P, M, K, k0, KC, lds, L);
-                else sk_stage<MODE, 64 * NW>(P, M, K, k0, KC, lds, L);
-            }
-            auto run_item = [&](const typename F::Item& d, int it) {
-                const int jj = my_split + (it << ks_log2);
-                // unscale of this lane's four output rows: activation rows 4g .. 4g+3,
-                // paired 2g, 2g, 2g+1, 2g+1
-                float us[4];
-                if constexpr (PAIR) {
-                    const f32x2 u2 = *reinterpret_cast<const f32x2*>(unscale + jj * 16 + 2 * g);
-                    us[0] = us[1] = u2.x;
-                    us[2] = us[3] = u2.y;
-                } else {
-                    const f32x4 u4 = *reinterpret_cast<const f32x4*>(unscale + jj * 16 + 4 * g);
-                    us[0] = u4.x, us[1] = u4.y, us[2] = u4.z, us[3] = u4.w;
-                }
-                acc += F::template block<PAIR>(d, x0 + jj * 256, x1 + jj * 256, xsr + 16 * jj, odd, g, us);
-            };
-            for (int it = 0; it < nitems; it += 2) {
-                run_item(b0, it);
-                if (it + 2 < nitems) load_item(b0, cp, it + 2);
-                if (it + 1 >= nitems) break;
-                run_item(b1, it + 1);
-                if (it + 3 < nitems) load_item(b1, cp, it + 3);
-            }
-            if (nchunks > 1) __syncthreads();  // the next chunk overwrites the staged activations
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+    auto run_item = [&](const typename F::Item& d, int it) {
+        const int jj = my_split + (it << ks_log2);
+        // unscale of this lane's four output rows: activation rows 4g .. 4g+3,
+        // paired 2g, 2g, 2g+1, 2g+1
+        float us[4];
+        if constexpr (PAIR) {
+            const f32x2 u2 = *reinterpret_cast<const f32x2*>(unscale + jj * 16 + 2 * g);
+            us[0] = us[1] = u2.x;
+            us[2] = us[3] = u2.y;
+        } else {
+            const f32x4 u4 = *reinterpret_cast<const f32x4*>(unscale + jj * 16 + 4 * g);
+            us[0] = u4.x, us[1] = u4.y, us[2] = u4.z, us[3] = u4.w;
         }
-        // RMSNorm: the row factor of output row m (the sums of every chunk stay in LDS)
-        auto row_factor = [&](int m) {
-            if constexpr (MODE == kActRMSNorm) {
-                const float* ssq = reinterpret_cast<const float*>(lds + L.ssq);
-                float ss = 0.0f;
-                for (int sb = 0; sb < (K >> 8); ++sb) ss += ssq[sb * 16 + min(m, M - 1)];
-                return rms_factor(ss, K, P.eps);
-            } else {
-                (void)m;
-                return 1.0f;
-            }
-        };
-        // output values of this lane: rows 4g + r (r < 4), paired rows 2g + r (r < 2)
-        // as the sum of the hi and lo lane rows
+        acc += F::template block<PAIR>(d, x0 + jj * 256, x1 + jj * 256, xsr + 16 * jj, odd, g, us);
+    };
+    // RMSNorm: the row factor of output row m (the sums of every chunk stay in LDS)
+    auto row_factor = [&](int m) {
+        if constexpr (MODE == kActRMSNorm) {
+            const float* ssq = reinterpret_cast<const float*>(lds + L.ssq);
+            float ss = 0.0f;
+            for (int sb = 0; sb < (K >> 8); ++sb) ss += ssq[sb * 16 + min(m, M - 1)];
+            return rms_factor(ss, K, P.eps);
+        } else {
+            (void)m;
+            return 1.0f;
+        }
+    };
+    // C of group grp: this lane's outputs are rows 4g + r (r < 4), paired rows
+    // 2g + r (r < 2) as the sum of the hi and lo lane rows; the KS k-split
+    // partials of each tile are reduced through LDS, red[w][r][lane]
+    auto finish_group = [&](int grp) {
+        const int tile = grp * TW + my_tile;
         constexpr int kRows = PAIR ? 2 : 4;
         f4 out = acc;
         if constexpr (PAIR) out = f4{acc[0] + acc[1], acc[2] + acc[3], 0.f, 0.f};
-        // reduce the KS k-split partials of each tile: red[w][r][lane]
         if (KS == 1) {
 #pragma unroll
             for (int r = 0; r < kRows; ++r) {
@@ -861,6 +845,52 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
             }
             if (grp + nblocks < ngroups) __syncthreads();  // the next group reuses red[]
         }
+    };
+
+    // chunks c = 0 .. nchunks - 1 of groups blockIdx.x, + nblocks, ...; the
+    // weights of each chunk were requested before the previous one finished
+    int grp = blockIdx.x, c = 0;
+    while (true) {
+        const int k0 = c * KC;
+        const uint8_t* cp = row_ptr(grp) + static_cast<long>((k0 >> 8) + my_split) * F::kBlockBytes;
+        // activations are staged for every chunk of the first group, and for
+        // every group when there are several chunks
+        if (grp == static_cast<int>(blockIdx.x) || nchunks > 1) {
+            if (one) sk_stage_one<MODE, 64 * NW>(xa, xb, P, M, K, k0, KC, lds, L);
+            else sk_stage<MODE, 64 * NW>(P, M, K, k0, KC, lds, L);
+        }
+        // two super-blocks in flight: each item's registers are refilled with the
+        // item two ahead right after it is used; the last two drain without loads
+        int it = 0;
+        for (; it + 2 < nitems; it += 2) {
+            run_item(b0, it);
+            load_item(b0, cp, it + 2);
+            run_item(b1, it + 1);
+            load_item_or_none(b1, cp, it + 3);
+        }
+        run_item(b0, it);
+        if (it + 1 < nitems) run_item(b1, it + 1);
+
+        const bool last_chunk = c + 1 == nchunks;
+        const int ngrp = last_chunk ? grp + nblocks : grp, nc = last_chunk ? 0 : c + 1;
+        if (ngrp >= ngroups) {  // nothing left to request
+            finish_group(grp);
+            break;
+        }
+        // the next chunk is requested before the chunk barrier and this group's reduction
+        {
+            const uint8_t* np = row_ptr(ngrp) + static_cast<long>(((nc * KC) >> 8) + my_split) * F::kBlockBytes;
+            if (one && nchunks > 1) sk_load_one<MODE>(P, M, K, nc * KC, KC, xa, xb);
+            load_item(b0, np, 0);
+            load_item_or_none(b1, np, 1);
+        }
+        if (nchunks > 1) __syncthreads();  // the next chunk overwrites the staged activations
+        if (last_chunk) {
+            finish_group(grp);
+            acc = f4{0.f, 0.f, 0.f, 0.f};
+        }
+        grp = ngrp;
+        c = nc;
     }
 }
 
