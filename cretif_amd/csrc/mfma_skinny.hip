@@ -231,14 +231,15 @@ __device__ void sk_stage(const ActIn& P, int M, int K, int k0, int KC, char* lds
 // here: waiting for them does not wait for the weights.
 template <int MODE, int NT, int NPT>
 __device__ __forceinline__ void sk_load_few(const ActIn& P, int M, int K, int k0, int KC, ActRaw<MODE> (&a)[NPT],
-                                            ActRaw<MODE> (&b)[NPT]) {
+                                            ActRaw<MODE> (&b)[NPT], bool none = false) {
     const int groups = KC / 8, total = M * groups;
     const long lda = MODE == kActPlain ? K : P.lda;
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
         // an item past the end reads item 0 (every such lane the same address):
         // whole 32-lane groups are past the end, and they are not converted
-        const int e0 = threadIdx.x + i * NT, e = e0 < total ? e0 : 0;
+        // none: a placeholder read (every lane item 0), whose registers go unused
+        const int e0 = threadIdx.x + i * NT, e = e0 < total && !none ? e0 : 0;
         const int m = e / groups, g8 = e - m * groups;
         act_load<MODE>(a[i], P, m, k0 + 8 * g8, lda);
         act_load<MODE>(b[i], P, m, k0 + 8 * g8 + 4, lda);
@@ -725,7 +726,7 @@ __device__ __forceinline__ float sum_splits(const float* p) {
 // grid sizes are not), so the plain path issues its first loads without
 // waiting on a scalar load of the argument block.  The activation pointer is
 // passed on its own (A == P.a); the rest of the prologue comes last.
-template <class F, int NW, int MODE, bool PAIR, int NPT>
+template <class F, int NW, int MODE, bool PAIR, int NPT, bool XPF>
 __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restrict__ B, float* __restrict__ C,
                                                              const float* __restrict__ A, int M, int N, int K, int KC,
                                                              int ks_log2, int ngroups, int nchunks, int nblocks,
@@ -740,7 +741,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
     const long rbytes = static_cast<long>(K >> 8) * F::kBlockBytes;
     const int sb_chunk = KC / 256;
     const int nitems = (sb_chunk - my_split + KS - 1) >> ks_log2;  // super-blocks per wave per chunk
-    const bool few = M * (KC / 8) <= NPT * 64 * NW;  // at most NPT activation items per thread
+    // at most NPT activation items per thread (the launcher guarantees it for NPT > 1)
+    const bool few = NPT > 1 || M * (KC / 8) <= 64 * NW;
     // weight row of this lane in group grp (clamped: the last tile may be partial)
     auto row_ptr = [&](int grp) {
         const int row = min((grp * TW + my_tile) * 16 + nl, N - 1);
@@ -867,6 +869,14 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
             if (few) sk_stage_few<MODE, 64 * NW, NPT>(xa, xb, P, M, K, k0, KC, lds, L);
             else sk_stage<MODE, 64 * NW>(P, M, K, k0, KC, lds, L);
         }
+        // XPF (several chunks, register staging): the next chunk's activations are
+        // requested now, so their latency hides behind this chunk's items; always
+        // issued (a placeholder read when no chunk follows) to keep the compiler's
+        // wait counts exact
+        if constexpr (XPF) {
+            const bool none = c + 1 == nchunks && grp + nblocks >= ngroups;
+            sk_load_few<MODE, 64 * NW, NPT>(P, M, K, c + 1 == nchunks ? 0 : k0 + KC, KC, xa, xb, none);
+        }
         // two super-blocks in flight: each item's registers are refilled with the
         // item two ahead right after it is used; the last two drain without loads
         int it = 0;
@@ -888,7 +898,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
         // the next chunk is requested before the chunk barrier and this group's reduction
         {
             const uint8_t* np = row_ptr(ngrp) + static_cast<long>(((nc * KC) >> 8) + my_split) * F::kBlockBytes;
-            if (few && nchunks > 1) sk_load_few<MODE, 64 * NW, NPT>(P, M, K, nc * KC, KC, xa, xb);
+            if constexpr (!XPF)
+                if (few && nchunks > 1) sk_load_few<MODE, 64 * NW, NPT>(P, M, K, nc * KC, KC, xa, xb);
             load_item(b0, np, 0);
             load_item_or_none(b1, np, 1);
         }
@@ -917,7 +928,7 @@ bool skinny_supported(int fmt, int M, int K, const void* B) {
     return false;
 }
 
-template <class F, int NW, int MODE, bool PAIR, int NPT>
+template <class F, int NW, int MODE, bool PAIR, int NPT, bool XPF = false>
 static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int K, int KC, int KS,
                      hipStream_t stream) {
     // large chunks need more than the default 64 KB of dynamic LDS: raise the limit once per kernel and device
@@ -926,7 +937,7 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
     int devid = 0;
     if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return -1;
     if (!ready[devid].load(std::memory_order_acquire)) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::skinny_kernel<F, NW, MODE, PAIR, NPT>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::skinny_kernel<F, NW, MODE, PAIR, NPT, XPF>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
             return -1;
         ready[devid].store(true, std::memory_order_release);
@@ -941,7 +952,7 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
     if (blocks < 1) blocks = 1;
     const dev::SkLds L = dev::sk_layout(M, KC, NW, K, MODE == kActRMSNorm);
     if (L.bytes > 160 * 1024) return -1;
-    hipLaunchKernelGGL((dev::skinny_kernel<F, NW, MODE, PAIR, NPT>), dim3(blocks), dim3(64 * NW), L.bytes, stream,
+    hipLaunchKernelGGL((dev::skinny_kernel<F, NW, MODE, PAIR, NPT, XPF>), dim3(blocks), dim3(64 * NW), L.bytes, stream,
                        static_cast<const uint8_t*>(B), C, A.a, M, N, K, KC, ks_log2, groups, K / KC, blocks, A);
     return 0;
 }
@@ -959,6 +970,16 @@ static int launch_sk_rows(const ActIn& A, const void* B, float* C, int M, int N,
                 return launch_sk<F, 8, MODE, true, 2>(A, B, C, M, N, K, KC, KS, stream);
         return launch_sk<F, 8, MODE, true, 1>(A, B, C, M, N, K, KC, KS, stream);
     }
+    // Q4_K, more than 8 rows, plain activations, up to eight items per thread:
+    // all of a chunk's activation loads are in registers ahead of time, and with
+    // several chunks (M = 16 at the FFN down shape: 4 of 2048) the next chunk's
+    // are requested while this one computes (29.5 -> 26.4 us there; a single
+    // chunk is faster without that request: 2048 x 2048 8.3 against 9.1 us)
+    if constexpr (std::is_same<F, dev::SkQ4K>::value && MODE == kActPlain)
+        if (M * (KC / 8) > 512 && M * (KC / 8) <= 4096) {
+            if (K > KC) return launch_sk<F, 8, MODE, false, 8, true>(A, B, C, M, N, K, KC, KS, stream);
+            return launch_sk<F, 8, MODE, false, 8, false>(A, B, C, M, N, K, KC, KS, stream);
+        }
     return launch_sk<F, 8, MODE, false, 1>(A, B, C, M, N, K, KC, KS, stream);
 }
 
