@@ -182,6 +182,32 @@ def test_matmul_small_m(orc, fmt, M, N, K):
     assert normwise_rel_err(got, ref) <= tol_for(M)
 
 
+# Shapes chosen for the skinny kernel's activation-staging and row-layout paths
+# (K % 256 == 0, 1 <= M <= 16): activation chunk KC = largest multiple of 256
+# dividing K with M * KC <= 32768; items = M * KC / 8 against 512 threads.
+SKINNY_PATH_SHAPES = [
+    (1, 300, 8192),    # paired rows, two activation items per thread (1024)
+    (2, 300, 4096),    # paired rows, two items per thread (1024)
+    (3, 300, 4096),    # paired rows, general staging loop (1536 items)
+    (8, 300, 4096),    # largest paired M, general staging (4096 items)
+    (9, 300, 4096),    # smallest unpaired M: KC 2048, 2 chunks, eight items per thread
+    (12, 300, 2048),   # unpaired, one chunk of eight items per thread
+    (16, 300, 8192),   # FFN-down-like: 4 chunks of eight items per thread
+    (16, 300, 16384),  # 8 chunks
+    (16, 40000, 4096),  # 2 chunks and more row groups than workgroups (grid stride)
+]
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q6_k", "q8_0"])
+@pytest.mark.parametrize("M,N,K", SKINNY_PATH_SHAPES)
+def test_skinny_staging_paths(orc, fmt, M, N, K):
+    A = quant.randn(M * K, seed=M * 131 + K + N).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=N + 3 * K + M)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= GEMV_TOL
+
+
 @pytest.mark.parametrize("M", [2, 7, 16])
 def test_q6_k_skinny_lm_head_rows(orc, M):
     # decode batches against a slice of the lm_head shape (full-range int8 sub-scales)
