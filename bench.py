@@ -426,6 +426,9 @@ def main():
                     help="--decode-step with the layer's RMSNorm / SiLU work: separate launches or fused prologues")
     ap.add_argument("--attention", default=None, choices=["plain", "ws"],
                     help="only time the fused decode attention at 2048 positions (for profiling)")
+    ap.add_argument("--launch-floor", action="store_true",
+                    help="only time the headline kernel on a one-tile problem (Q4_K, 16 x 256) in the same graph "
+                         "rig: the per-launch cost with no data to stream, with and without a profiler")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run ten 64 MiB device copies (known bytes, for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -451,6 +454,12 @@ def main():
     import cretif_amd as cri
 
     cri.lib()
+    if args.launch_floor:
+        r = GemvRig("q4_k", 16, 256, M=1, max_copies=57)
+        ms, n = r.time(args.steps, args.warmup)
+        print(json.dumps({"workload": "launch_floor q4_k 16x256 M=1", "launches": n, "copies": r.copies,
+                          "us_per_launch": round(ms * 1e3, 3)}))
+        return
     if args.attention:
         r = AttentionRig(args.attention)
         ms_call = r.time(reps=max(3, args.steps // r.copies))
