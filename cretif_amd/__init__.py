@@ -45,6 +45,7 @@ __all__ = [
     "rmsnorm_residual",
     "silu_mul",
     "embedding_rows",
+    "stream_read",
     "GGUFFile",
     "FORMAT_IDS",
     "ABI_SYMBOLS",
@@ -98,6 +99,7 @@ ABI_SYMBOLS = (
         "cri_gguf_model_params",
         "cri_gguf_upload",
         "cri_embedding_rows",
+        "cri_stream_read",
         "cri_last_error_string",
         "cri_block_bytes",
         "cri_block_elems",
@@ -184,6 +186,7 @@ def lib():
     L.cri_silu_mul.argtypes = [vp, vp, vp, ctypes.c_longlong, vp]
     L.cri_silu_mul.restype = i32
     L.cri_embedding_rows.argtypes = [i32, vp, vp, vp, i32, i32, i32, vp]
+    L.cri_stream_read.argtypes = [vp, ctypes.c_longlong, vp, vp]
     L.cri_embedding_rows.restype = i32
     ll = ctypes.c_longlong
     L.cri_gguf_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(vp)]
@@ -411,6 +414,13 @@ def embedding_rows(fmt, table, ids, out, n_ids, dim, vocab, stream=None):
     """out[i] = dequant(table row ids[i]) (zero rows for ids outside [0, vocab)); fmt may be 'fp32'."""
     fid = 6 if fmt == "fp32" else _fid(fmt)
     _check(lib().cri_embedding_rows(fid, _ptr(table), _ptr(ids), _ptr(out), n_ids, dim, vocab, _stream(stream)))
+
+
+def stream_read(src, n_bytes, sink, stream=None):
+    """Read n_bytes (a multiple of 16) at src once with 16-byte loads: the achievable streaming-read
+    bandwidth (a measurement aid).  sink is one device word, written only if the XOR of the words one
+    thread reads (four 16-byte chunks, 4096 bytes apart) equals 0x9E3779B9."""
+    _check(lib().cri_stream_read(_ptr(src), n_bytes, _ptr(sink), _stream(stream)))
 
 
 _MODEL_FIELDS = ("context_length", "embedding_length", "block_count", "head_count", "head_count_kv",

@@ -294,6 +294,17 @@ int cri_silu_mul(const float* gate, const float* up, float* out, long long n, hi
     return check_launch(fn);
 }
 
+int cri_stream_read(const void* src, long long n_bytes, unsigned* sink, hipStream_t s) {
+    const char* fn = "cri_stream_read";
+    if (n_bytes < 0 || n_bytes % 16 != 0)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "n_bytes must be a non-negative multiple of 16");
+    if (n_bytes == 0) return CRI_OK;
+    if (!src || !sink) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(src, 16) || !aligned(sink, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "src must be 16-byte aligned");
+    if (cri::detail::launch_stream_read(src, n_bytes, sink, s) != 0) return fail(CRI_ERR_SHAPE, fn, "too large");
+    return check_launch(fn);
+}
+
 long long cri_fused_decode_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, int kv_len) {
     const char* fn = "cri_fused_decode_attention_workspace_size";
     if (n_heads < 0 || n_kv_heads < 0 || head_dim < 0 || kv_len < 0)

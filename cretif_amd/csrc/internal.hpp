@@ -84,6 +84,7 @@ int launch_rmsnorm_residual(const float* input, const float* residual, const flo
                             float* normed, int rows, int n, float eps, hipStream_t stream);
 int launch_silu_mul(const float* gate, const float* up, float* out, long n, hipStream_t stream);
 // token rows of a (quantized) embedding table, dequantized (elementwise.hip)
+int launch_stream_read(const void* src, long n_bytes, uint32_t* sink, hipStream_t stream);
 int launch_embedding_rows(int fmt, const void* table, const int* ids, float* out, int n_ids, int dim, int vocab,
                           hipStream_t stream);
 

@@ -220,6 +220,13 @@ int cri_embedding_rows(int format, const void* table, const int* ids, float* out
 
 /* ---- diagnostics ---------------------------------------------------------- */
 
+/* Reads n_bytes (a multiple of 16) at src (16-byte aligned) once with 16-byte
+ * loads and nothing else: the achievable streaming-read bandwidth that the
+ * GEMV rooflines are read against.  sink (one device word) is written only if
+ * the XOR of the words one thread reads (four 16-byte chunks, 4096 bytes apart)
+ * equals 0x9E3779B9.  A measurement aid with no counterpart in the reference. */
+int cri_stream_read(const void* src, long long n_bytes, unsigned* sink, hipStream_t stream);
+
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* cri_last_error_string(void);
 /* Bytes per block / elements per block of a format (0 if unknown). */

@@ -182,3 +182,16 @@ def test_fused_prologue_validation():
     assert e.value.status == -3
     cri.silu_mul(0, 0, 0, 0, stream=0)
     cri.matmul_swiglu("q4_k", 0, 0, 0, 0, 0, 0, 8, 256, stream=0)
+
+
+def test_stream_read_validation():
+    with pytest.raises(cri.CretifError) as e:
+        cri.stream_read(FAKE, 24, FAKE, stream=0)  # not a multiple of 16
+    assert e.value.status == -1
+    with pytest.raises(cri.CretifError) as e:
+        cri.stream_read(FAKE + 8, 64, FAKE, stream=0)
+    assert e.value.status == -3
+    with pytest.raises(cri.CretifError) as e:
+        cri.stream_read(0, 64, FAKE, stream=0)
+    assert e.value.status == -1
+    cri.stream_read(0, 0, 0, stream=0)

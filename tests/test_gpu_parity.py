@@ -423,3 +423,18 @@ def test_skinny_block_formats_random_codes(orc, fmt, M, N, K, off):
     cri.matmul(fmt, dev(A), buf.data_ptr() + off, C, M, N, K)
     ref = orc.matmul_quant(fmt, A, Bq, N, K)
     assert normwise_rel_err(host(C), ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("n_bytes", [16, 4096 * 16 + 16, 9437184])
+def test_stream_read_probe(n_bytes):
+    # the bandwidth probe writes nothing but the sink: a zero buffer leaves it untouched; a
+    # buffer whose first word is the probe's constant (the rest zero) sets it, since the
+    # thread that reads word 0 reads three other, zero, chunks with it (n_bytes >= 16 KB)
+    src = torch.zeros(n_bytes, dtype=torch.uint8, device="cuda")
+    sink = torch.full((1,), 7, dtype=torch.int32, device="cuda")
+    cri.stream_read(src, n_bytes, sink)
+    assert int(host(sink)[0]) == 7
+    if n_bytes >= 16 * 1024:
+        src.view(torch.int32)[0] = int(np.uint32(0x9E3779B9).view(np.int32))
+        cri.stream_read(src, n_bytes, sink)
+        assert np.uint32(host(sink)[0]) == np.uint32(0x9E3779B9)
