@@ -421,23 +421,37 @@ def cpu_baseline(fmt, N, K, budget_s=12.0):
     x = quant.randn(K, seed=8).reshape(1, K)
     orc.matmul_quant(fmt, x, w, rows, K)  # warm
     t0 = time.perf_counter()
-    n = 0
+    calls = []
     while True:
+        t = time.perf_counter()
         orc.matmul_quant(fmt, x, w, rows, K)
-        n += 1
+        calls.append(time.perf_counter() - t)
         el = time.perf_counter() - t0
-        if el >= budget_s:
+        if el >= budget_s and len(calls) >= 5:
             break
-    per_call = el / n
+    per_call = float(np.median(calls))  # median of the calls, as the reference's benchmarks report
     gbs = algo_bytes(fmt, 1, rows, K) / per_call / 1e9
     return {
         "value": round(gbs, 3),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": "%s GEMV M=1, %d of %d rows x K=%d, %d calls in %.1f s (oracle/oracle.c, gcc -O2 "
-        "-ffp-contract=off, 1 thread, %s)" % (fmt, rows, N, K, n, el, platform.processor() or platform.machine()),
+        "sample": "%s GEMV M=1, %d of %d rows x K=%d, median of %d calls over %.1f s (oracle/oracle.c, gcc -O2 "
+        "-ffp-contract=off, 1 thread; host %s, %d logical CPUs visible)" % (
+            fmt, rows, N, K, len(calls), el, cpu_model(), os.cpu_count() or 0),
     }
+
+
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), else the platform's machine string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def main():
