@@ -67,16 +67,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
     }
     typename F::Data buf[PREF][UPL];
     const int base0 = gwave * rows_per_iter;
+    // Row-group b past the end is a placeholder read: every lane takes unit 0 of row 0, so the
+    // unconditional prefetch after a wave's last row-group costs one cache line per instruction.
     auto load_rows = [&](typename F::Data(&dst)[UPL], int b) {
+        const bool real = b < N;
         const int r = min(b + rsub, N - 1);
-        const uint8_t* rp = W + static_cast<long>(r) * row_bytes;
+        const uint8_t* rp = real ? W + static_cast<long>(r) * row_bytes : W;
 #pragma unroll
-        for (int u = 0; u < UPL; ++u) F::load(dst[u], rp, unit[u]);
+        for (int u = 0; u < UPL; ++u) F::load(dst[u], rp, real ? unit[u] : 0);
     };
-    // Every prefetch is issued unconditionally (rows past the end are clamped to
-    // row N - 1, cached after its first read): a load under a condition leaves
-    // the compiler unsure how many loads are in flight, and it then waits for
-    // all of them before decoding the oldest row-group.
+    // Every prefetch is issued unconditionally (row-groups past the end are
+    // placeholder reads): a load under a condition leaves the compiler unsure how
+    // many loads are in flight, and it then waits for all of them before decoding
+    // the oldest row-group.
 #pragma unroll
     for (int p = 0; p < PREF; ++p) load_rows(buf[p], base0 + p * stride);
 
