@@ -20,6 +20,8 @@
 // MODE (see ActIn): the activations are computed while staged -- SwiGLU of the
 // gate/up outputs, or RMSNorm of hidden + residual (the row factor multiplies
 // y, the workgroup-wide sum of squares is reduced through LDS).
+#include <atomic>
+
 #include "act.hpp"
 #include "common.hpp"
 #include "gemv_formats.hpp"
@@ -38,7 +40,7 @@ namespace dev {
 template <class F, int UPL, int PREF, int MODE>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W, float* __restrict__ y, int N, int K,
                                                    int units, long row_bytes, int lpr_log2, const ActIn P) {
-    extern __shared__ float xs[];  // K activations, staged once per workgroup (+4 partial sums)
+    extern __shared__ float xs[];  // K activations (padded, xpad), staged once per workgroup (+4 partial sums)
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
     const int u0 = lane & (lpr - 1);
@@ -89,20 +91,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int j = threadIdx.x + 256 * i;
-        if (j < nx4) *reinterpret_cast<f32x4*>(xs + 4 * j) = act_finish<MODE>(xv[i], P, 0, 4 * j, K, ss, write_h);
+        if (j < nx4) *reinterpret_cast<f32x4*>(xs + xpad(4 * j)) = act_finish<MODE>(xv[i], P, 0, 4 * j, K, ss, write_h);
     }
     for (int j = threadIdx.x + 1024; j < nx4; j += 256) {
         ActRaw<MODE> raw;
         act_load<MODE>(raw, P, 0, 4 * j, 0);
-        *reinterpret_cast<f32x4*>(xs + 4 * j) = act_finish<MODE>(raw, P, 0, 4 * j, K, ss, write_h);
+        *reinterpret_cast<f32x4*>(xs + xpad(4 * j)) = act_finish<MODE>(raw, P, 0, 4 * j, K, ss, write_h);
     }
     if constexpr (MODE == kActRMSNorm) {
         ss = group_sum_t<6>(ss);
-        if (lane == 0) xs[K + (threadIdx.x >> 6)] = ss;
+        if (lane == 0) xs[xpad(K) + (threadIdx.x >> 6)] = ss;
     }
     __syncthreads();
     float rs = 1.0f;
-    if constexpr (MODE == kActRMSNorm) rs = rms_factor(((xs[K] + xs[K + 1]) + xs[K + 2]) + xs[K + 3], K, P.eps);
+    if constexpr (MODE == kActRMSNorm) {
+        const float* part = xs + xpad(K);
+        rs = rms_factor(((part[0] + part[1]) + part[2]) + part[3], K, P.eps);
+    }
     typename F::Xr xr[UPL];
 #pragma unroll
     for (int u = 0; u < UPL; ++u) F::load_x(xr[u], xs, unit[u]);
@@ -134,7 +139,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 namespace detail {
 
 template <class F, int UPL, int PREF, int MODE>
-static void launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K, int units, long row_bytes,
+static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K, int units, long row_bytes,
                           int lpr_log2, hipStream_t stream) {
     const int rows_per_iter = 64 >> lpr_log2;
     const long groups = (static_cast<long>(N) + rows_per_iter - 1) / rows_per_iter;
@@ -143,9 +148,22 @@ static void launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int 
     long waves = (groups + PREF - 1) / PREF;
     if (waves > kGemvTargetWaves) waves = kGemvTargetWaves;
     const int blocks = static_cast<int>((waves + 3) / 4);
-    const int lds = (K + (MODE == kActRMSNorm ? 4 : 0)) * static_cast<int>(sizeof(float));
+    const int lds = (dev::xpad(K) + (MODE == kActRMSNorm ? 4 : 0)) * static_cast<int>(sizeof(float));
+    if (lds > 65536) {  // beyond the default dynamic-LDS limit: raise it once per kernel and device
+        constexpr int kMaxDevices = 64;
+        static std::atomic<bool> ready[kMaxDevices];
+        int devid = 0;
+        if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return -1;
+        if (!ready[devid].load(std::memory_order_acquire)) {
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::gemv_kernel<F, UPL, PREF, MODE>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+                return -1;
+            ready[devid].store(true, std::memory_order_release);
+        }
+    }
     hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE>), dim3(blocks), dim3(256), lds, stream,
                        static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act);
+    return 0;
 }
 
 template <class F, int MODE>
@@ -157,10 +175,10 @@ static int launch_gemv_f(const ActIn& x, const void* W, float* y, int N, int K, 
     const int lpr = 1 << lpr_log2;
     const int upl = (units + lpr - 1) / lpr;
     switch (upl) {
-        case 1: launch_gemv_t<F, 1, F::kPref1, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
-        case 2: launch_gemv_t<F, 2, 2, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
+        case 1: return launch_gemv_t<F, 1, F::kPref1, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
+        case 2: return launch_gemv_t<F, 2, 2, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
         case 3:
-        case 4: launch_gemv_t<F, 4, 1, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream); break;
+        case 4: return launch_gemv_t<F, 4, 1, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
         default: return -1;
     }
     return 0;
@@ -194,7 +212,7 @@ int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, 
 }
 
 int launch_gemv_act(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t stream) {
-    if (mode == kActRMSNorm && (K + 4) * 4 > 65536) return -1;  // the 4 partial sums must fit beside x in 64 KB
+    if ((dev::xpad(K) + 4) * 4 > 160 * 1024) return -1;  // the staged activations (+ 4 partial sums) fit in LDS
     switch (mode) {
         case kActPlain: return launch_gemv_m<kActPlain>(fmt, act, W, y, N, K, stream);
         case kActSwiGLU: return launch_gemv_m<kActSwiGLU>(fmt, act, W, y, N, K, stream);

@@ -25,11 +25,18 @@ namespace dev {
 // ---------------------------------------------------------------------------
 // shared helpers
 // ---------------------------------------------------------------------------
-// x points at the workgroup's LDS copy of the activations.
-__device__ __forceinline__ void load_x64(float (&v)[64], const float* x, int k0) {
+// x points at the workgroup's LDS copy of the activations, stored padded: element
+// k at k + 4 (k / 64).  A lane reads the 64 activations of its unit, and the lanes
+// of a row hold consecutive units, 64 floats apart; padded, their 16-byte reads
+// start 68 floats apart and fall in different banks (unpadded, a read instruction
+// sent all of its lanes to the same banks).
+__host__ __device__ __forceinline__ int xpad(int k) { return k + ((k >> 6) << 2); }
+
+__device__ __forceinline__ void load_x64(float (&v)[64], const float* x, int k0) {  // k0 % 64 == 0
+    const float* xu = x + xpad(k0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        f32x4 t = *reinterpret_cast<const f32x4*>(x + k0 + 4 * i);
+        f32x4 t = *reinterpret_cast<const f32x4*>(xu + 4 * i);
         v[4 * i + 0] = t.x;
         v[4 * i + 1] = t.y;
         v[4 * i + 2] = t.z;
@@ -312,7 +319,7 @@ struct GemvQ6K {
         for (int q = 0; q < 4; ++q)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                f32x4 t = *reinterpret_cast<const f32x4*>(x + k0 + 32 * q + 4 * i);
+                f32x4 t = *reinterpret_cast<const f32x4*>(x + xpad(k0 + 32 * q + 4 * i));
                 r.v[16 * q + 4 * i + 0] = t.x;
                 r.v[16 * q + 4 * i + 1] = t.y;
                 r.v[16 * q + 4 * i + 2] = t.z;
