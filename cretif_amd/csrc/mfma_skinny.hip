@@ -730,7 +730,7 @@ template <class F, int NW, int MODE, bool PAIR, int NPT, bool XPF>
 __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restrict__ B, float* __restrict__ C,
                                                              const float* __restrict__ A, int M, int N, int K, int KC,
                                                              int ks_log2, int ngroups, int nchunks, int nblocks,
-                                                             const ActIn Pin) {
+                                                             int cs_log2, const ActIn Pin) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const ActIn P{A, Pin.b, Pin.w, Pin.h_out, Pin.lda, Pin.eps};
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -741,6 +741,12 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
     const long rbytes = static_cast<long>(K >> 8) * F::kBlockBytes;
     const int sb_chunk = KC / 256;
     const int nitems = (sb_chunk - my_split + KS - 1) >> ks_log2;  // super-blocks per wave per chunk
+    // chunk split across workgroups (cs_log2 > 0): workgroup b takes chunks
+    // [c_begin, c_begin + cps) of groups b >> cs_log2, + gstride, ..., and adds
+    // its partial sums into C (zero-filled by the launcher)
+    const int cps = nchunks >> cs_log2;
+    const int c_begin = (static_cast<int>(blockIdx.x) & ((1 << cs_log2) - 1)) * cps;
+    const int grp0 = static_cast<int>(blockIdx.x) >> cs_log2, gstride = nblocks >> cs_log2;
     // at most NPT activation items per thread (the launcher guarantees it for NPT > 1)
     const bool few = NPT > 1 || M * (KC / 8) <= 64 * NW;
     // weight row of this lane in group grp (clamped: the last tile may be partial)
@@ -767,9 +773,9 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
     typename F::Item b0, b1;
     ActRaw<MODE> xa[NPT], xb[NPT];
     {
-        const uint8_t* cp = row_ptr(blockIdx.x) + static_cast<long>(my_split) * F::kBlockBytes;
+        const uint8_t* cp = row_ptr(grp0) + static_cast<long>(((c_begin * KC) >> 8) + my_split) * F::kBlockBytes;
         if (few) {
-            sk_load_few<MODE, 64 * NW, NPT>(P, M, K, 0, KC, xa, xb);
+            sk_load_few<MODE, 64 * NW, NPT>(P, M, K, c_begin * KC, KC, xa, xb);
             // every wave's activation loads enter the vector-memory queue before any
             // weight load: the L1 returns data in request order, and the weights
             // miss to HBM while the activations are L2 hits (no wait here)
@@ -837,7 +843,11 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
 #pragma unroll
             for (int r = 0; r < kRows; ++r) {
                 const int m = kRows * g + r, n = tile * 16 + nl;
-                if (m < M && n < N && tile < ntiles) C[static_cast<long>(m) * N + n] = out[r] * row_factor(m);
+                if (m < M && n < N && tile < ntiles) {
+                    float* dst = C + static_cast<long>(m) * N + n;
+                    if (cs_log2) atomicAdd(dst, out[r] * row_factor(m));
+                    else *dst = out[r] * row_factor(m);
+                }
             }
         } else {
 #pragma unroll
@@ -851,21 +861,25 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
                 const float sum = ks_log2 == 1 ? sum_splits<2>(rp) : ks_log2 == 2 ? sum_splits<4>(rp) : sum_splits<8>(rp);
                 const int tt = grp * TW + t;
                 const int m = kRows * (ln >> 4) + r, n = tt * 16 + (ln & 15);
-                if (m < M && n < N && tt < ntiles) C[static_cast<long>(m) * N + n] = sum * row_factor(m);
+                if (m < M && n < N && tt < ntiles) {
+                    float* dst = C + static_cast<long>(m) * N + n;
+                    if (cs_log2) atomicAdd(dst, sum * row_factor(m));
+                    else *dst = sum * row_factor(m);
+                }
             }
-            if (grp + nblocks < ngroups) __syncthreads();  // the next group reuses red[]
+            if (grp + gstride < ngroups) __syncthreads();  // the next group reuses red[]
         }
     };
 
-    // chunks c = 0 .. nchunks - 1 of groups blockIdx.x, + nblocks, ...; the
-    // weights of each chunk were requested before the previous one finished
-    int grp = blockIdx.x, c = 0;
+    // chunks c = c_begin .. c_begin + cps - 1 of groups grp0, + gstride, ...;
+    // the weights of each chunk were requested before the previous one finished
+    int grp = grp0, c = c_begin;
     while (true) {
         const int k0 = c * KC;
         const uint8_t* cp = row_ptr(grp) + static_cast<long>((k0 >> 8) + my_split) * F::kBlockBytes;
         // activations are staged for every chunk of the first group, and for
-        // every group when there are several chunks
-        if (grp == static_cast<int>(blockIdx.x) || nchunks > 1) {
+        // every group when the workgroup has several chunks
+        if (grp == grp0 || cps > 1) {
             if (few) sk_stage_few<MODE, 64 * NW, NPT>(xa, xb, P, M, K, k0, KC, lds, L);
             else sk_stage<MODE, 64 * NW>(P, M, K, k0, KC, lds, L);
         }
@@ -874,8 +888,9 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
         // issued (a placeholder read when no chunk follows) to keep the compiler's
         // wait counts exact
         if constexpr (XPF) {
-            const bool none = c + 1 == nchunks && grp + nblocks >= ngroups;
-            sk_load_few<MODE, 64 * NW, NPT>(P, M, K, c + 1 == nchunks ? 0 : k0 + KC, KC, xa, xb, none);
+            const bool lastc = c + 1 == c_begin + cps;
+            const bool none = lastc && grp + gstride >= ngroups;
+            sk_load_few<MODE, 64 * NW, NPT>(P, M, K, lastc ? c_begin * KC : k0 + KC, KC, xa, xb, none);
         }
         // two super-blocks in flight: each item's registers are refilled with the
         // item two ahead right after it is used; the last two drain without loads
@@ -889,8 +904,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
         run_item(b0, it);
         if (it + 1 < nitems) run_item(b1, it + 1);
 
-        const bool last_chunk = c + 1 == nchunks;
-        const int ngrp = last_chunk ? grp + nblocks : grp, nc = last_chunk ? 0 : c + 1;
+        const bool last_chunk = c + 1 == c_begin + cps;
+        const int ngrp = last_chunk ? grp + gstride : grp, nc = last_chunk ? c_begin : c + 1;
         if (ngrp >= ngroups) {  // nothing left to request
             finish_group(grp);
             break;
@@ -899,11 +914,11 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
         {
             const uint8_t* np = row_ptr(ngrp) + static_cast<long>(((nc * KC) >> 8) + my_split) * F::kBlockBytes;
             if constexpr (!XPF)
-                if (few && nchunks > 1) sk_load_few<MODE, 64 * NW, NPT>(P, M, K, nc * KC, KC, xa, xb);
+                if (few && cps > 1) sk_load_few<MODE, 64 * NW, NPT>(P, M, K, nc * KC, KC, xa, xb);
             load_item(b0, np, 0);
             load_item_or_none(b1, np, 1);
         }
-        if (nchunks > 1) __syncthreads();  // the next chunk overwrites the staged activations
+        if (cps > 1) __syncthreads();  // the next chunk overwrites the staged activations
         if (last_chunk) {
             finish_group(grp);
             acc = f4{0.f, 0.f, 0.f, 0.f};
@@ -952,8 +967,22 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
     if (blocks < 1) blocks = 1;
     const dev::SkLds L = dev::sk_layout(M, KC, NW, K, MODE == kActRMSNorm);
     if (L.bytes > 160 * 1024) return -1;
+    // Few tile groups and several activation chunks (the FFN down projection at
+    // M = 5..16: 128 groups, 2 or 4 chunks): every workgroup would stage all of
+    // K on half the CUs, so the chunks are split over 2 workgroups per group
+    // that add into a zero-filled C (0 + a + b equals 0 + b + a exactly, so the
+    // result does not depend on their order).  The RMSNorm prologue needs every
+    // chunk's sum of squares in one workgroup and is not split.
+    const int nchunks = K / KC;
+    int cs_log2 = 0;
+    if (MODE != kActRMSNorm && 2 * groups <= 2048 / NW && nchunks % 2 == 0) cs_log2 = 1;
+    if (cs_log2 > 0) {
+        blocks = groups << cs_log2;
+        launch_fill_zero(C, static_cast<long>(M) * N, stream);
+    }
     hipLaunchKernelGGL((dev::skinny_kernel<F, NW, MODE, PAIR, NPT, XPF>), dim3(blocks), dim3(64 * NW), L.bytes, stream,
-                       static_cast<const uint8_t*>(B), C, A.a, M, N, K, KC, ks_log2, groups, K / KC, blocks, A);
+                       static_cast<const uint8_t*>(B), C, A.a, M, N, K, KC, ks_log2, groups, nchunks, blocks, cs_log2,
+                       A);
     return 0;
 }
 

@@ -37,9 +37,10 @@ def rnd(shape, seed, scale=1.0):
 
 # (M, N, K): M = 1 runs the GEMV (skinny for Q4_K), 2..16 the skinny kernel (Q4_K, Q6_K) or the
 # element-wise kernel, K = 4096 / 8192 at M = 16 gives the skinny kernel 2 / 4 activation chunks
-# (1, 300, 8192) and (2, 256, 4096): two activation items per thread in the skinny kernel
+# (1, 300, 8192) and (2, 256, 4096): two activation items per thread in the skinny kernel;
+# (8, 256, 8192), (16, 128, 8192): the SwiGLU path splits the chunks over two workgroups
 SHAPES = [(1, 512, 2048), (2, 300, 2048), (7, 256, 1024), (16, 512, 2048), (16, 256, 4096), (16, 128, 8192),
-          (1, 300, 8192), (2, 256, 4096)]
+          (1, 300, 8192), (2, 256, 4096), (8, 256, 8192)]
 
 
 @pytest.mark.parametrize("fmt", FMTS)

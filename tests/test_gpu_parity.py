@@ -195,6 +195,11 @@ SKINNY_PATH_SHAPES = [
     (16, 300, 8192),   # FFN-down-like: 4 chunks of eight items per thread
     (16, 300, 16384),  # 8 chunks
     (16, 40000, 4096),  # 2 chunks and more row groups than workgroups (grid stride)
+    # chunks split over two workgroups adding into a zero-filled C (few row groups, even chunk count)
+    (5, 300, 8192),    # paired rows, KC 4096: one chunk per workgroup
+    (8, 300, 8192),    # largest paired M, one chunk per workgroup
+    (16, 2048, 8192),  # the FFN down shape: 128 row groups, two chunks per workgroup
+    (16, 4096, 8192),  # 256 row groups: not split
 ]
 
 
@@ -206,6 +211,17 @@ def test_skinny_staging_paths(orc, fmt, M, N, K):
     got = run_matmul(fmt, A, Bq, N, K)
     ref = orc.matmul_quant(fmt, A, Bq, N, K)
     assert normwise_rel_err(got, ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+def test_skinny_chunk_split_is_deterministic(fmt):
+    # two partial sums per output added atomically in either order: the same bits every call
+    M, N, K = 16, 2048, 8192
+    A = quant.randn(M * K, seed=91).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=92)
+    first = run_matmul(fmt, A, Bq, N, K)
+    for _ in range(3):
+        assert np.array_equal(run_matmul(fmt, A, Bq, N, K), first)
 
 
 @pytest.mark.parametrize("M", [2, 7, 16])
