@@ -93,15 +93,17 @@ def test_matmul_swiglu_separate_buffers(orc, fmt):
     assert normwise_rel_err(host(C), orc.matmul_quant(fmt, orc.silu_mul(g, u), W, N, K)) <= TOL
 
 
-@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
-def test_misaligned_weights_take_the_elementwise_kernel(orc, fmt):
+@pytest.mark.parametrize("fmt,offset", [("q4_k", 2), ("q8_0", 2), ("q4_k", 4)])
+def test_misaligned_weights(orc, fmt, offset):
+    # 2 bytes off: the element-wise kernel; Q4_K 4 bytes off (dword but not 16-byte
+    # aligned): the batch-1 GEMV with the RMSNorm prologue
     M, N, K = 1, 64, 512
     W = quant.synthetic_weights(fmt, N, K, seed=41)
     buf = torch.zeros(W.size + 8, dtype=torch.uint8, device="cuda")
-    buf[2:2 + W.size] = dev(W)
+    buf[offset:offset + W.size] = dev(W)
     h, w = rnd((M, K), 42), rnd(K, 43)
     C = torch.empty(M, N, device="cuda")
-    cri.matmul_rmsnorm(fmt, dev(h), None, dev(w), None, buf.data_ptr() + 2, C, M, N, K, 1e-5)
+    cri.matmul_rmsnorm(fmt, dev(h), None, dev(w), None, buf.data_ptr() + offset, C, M, N, K, 1e-5)
     _, normed = orc.rmsnorm_residual(h, None, w, 1e-5)
     assert normwise_rel_err(host(C), orc.matmul_quant(fmt, normed, W, N, K)) <= TOL
 

@@ -157,16 +157,18 @@ def test_exact_integer_bit_exact(orc, fmt, M):
     assert bits_equal(got, ref)
 
 
-def test_misaligned_weight_pointer(orc):
-    # B starting 2 bytes into an allocation: the ABI must route around the
-    # dword-aligned vector loads and still match
-    N, K = 64, 512
+@pytest.mark.parametrize("offset,N,K", [(2, 64, 512), (4, 300, 2048), (8, 1001, 4096)])
+def test_misaligned_weight_pointer(orc, offset, N, K):
+    # B starting `offset` bytes into an allocation: 2 bytes routes around the
+    # dword-aligned vector loads (element-wise kernel); 4 or 8 bytes is dword
+    # aligned but not 16-byte aligned, which the skinny kernel needs, so Q4_K at
+    # M = 1 runs the batch-1 GEMV
     A = quant.randn(K, seed=1).reshape(1, K)
     Bq = weights("q4_k", N, K, seed=2)
-    buf = torch.zeros(Bq.size + 2, dtype=torch.uint8, device="cuda")
-    buf[2:] = dev(Bq)
+    buf = torch.zeros(Bq.size + offset, dtype=torch.uint8, device="cuda")
+    buf[offset:] = dev(Bq)
     C = torch.empty(1, N, dtype=torch.float32, device="cuda")
-    cri.matmul_q4_k(dev(A), buf.data_ptr() + 2, C, 1, N, K)
+    cri.matmul_q4_k(dev(A), buf.data_ptr() + offset, C, 1, N, K)
     ref = orc.matmul_quant("q4_k", A, Bq, N, K)
     assert normwise_rel_err(host(C), ref) <= GEMV_TOL
 
