@@ -396,6 +396,52 @@ class AttentionRig:
         self.K = self.V = self.graph = None
 
 
+class GqaRig:
+    """batched_matmul_gqa (32 query heads over 8 KV heads, head_dim 64, T = 2048):
+    'qk' is Q K^T (A [32, M, 64], B [8, 64, T]), 'pv' is P V (A [32, M, T],
+    B [8, T, 64]).  Both operands rotate over `copies` distinct buffers (>= 2 x
+    the MALL) in one captured graph.  Algorithmic bytes: 4 (H M K + Hkv K N + H M N)."""
+
+    H, HKV, HD, T = 32, 8, 64, 2048
+
+    def __init__(self, product, M, min_bytes=2 * MALL_BYTES):
+        import torch
+
+        import cretif_amd as cri
+
+        H, HKV = self.H, self.HKV
+        self.M = M
+        self.K, self.N = (self.HD, self.T) if product == "qk" else (self.T, self.HD)
+        K, N = self.K, self.N
+        per = 4 * (H * M * K + HKV * K * N)
+        self.copies = int(max(2, min(256, -(-min_bytes // per))))
+        g = torch.Generator(device="cuda").manual_seed(3000 + M)
+        self.A = [torch.randn(H, M, K, device="cuda", generator=g) for _ in range(self.copies)]
+        self.B = [torch.randn(HKV, K, N, device="cuda", generator=g) for _ in range(self.copies)]
+        self.C = torch.empty(H, M, N, device="cuda")
+
+        def run():
+            for a_, b_ in zip(self.A, self.B):
+                cri.batched_matmul_gqa(a_, b_, self.C, H, HKV, M, N, K)
+
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):
+            run()
+        side.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=side):
+            run()
+        torch.cuda.synchronize()
+
+    def bytes_per_call(self):
+        return 4 * (self.H * self.M * self.K + self.HKV * self.K * self.N + self.H * self.M * self.N)
+
+    time = AttentionRig.time
+
+    def free(self):
+        self.A = self.B = self.graph = None
+
+
 def measured_traffic(workload):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary of this
     workload (profiles/<kernel>_<shape>.md, line `traffic_bytes_per_launch:`), or None."""
@@ -556,6 +602,16 @@ def main():
                              "copies": r.copies}
             r.free()
             torch.cuda.empty_cache()
+        # batched decode (BASELINE config 5 at M = 16): reported against the HBM and the fp16 MFMA roofs
+        for name, (f, m_, n, k) in (("q4_k_gemv_m16", ("q4_k", 16, 8192, 2048)),
+                                    ("q4_k_gemv_down_m16", ("q4_k", 16, 2048, 8192))):
+            r = GemvRig(f, n, k, M=m_, max_copies=64)
+            m, _ = r.time(max(640, 4 * r.copies), 64)
+            details[name] = {"GB/s": round(r.bytes_per_launch() / (m * 1e-3) / 1e9, 1),
+                             "TFLOP/s": round(2.0 * m_ * n * k / (m * 1e-3) / 1e12, 2), "us": round(m * 1e3, 3),
+                             "M": m_, "copies": r.copies}
+            r.free()
+            torch.cuda.empty_cache()
         for name, (f, m_, n, k) in PREFILL_WORKLOADS.items():
             r = GemvRig(f, n, k, M=m_, max_copies=16)
             m, _ = r.time(max(64, 2 * r.copies), 16)
@@ -572,6 +628,15 @@ def main():
                 "copies": r.copies}
             r.free()
             torch.cuda.empty_cache()
+        for product in ("qk", "pv"):
+            for m_ in (1, 16):
+                r = GqaRig(product, m_)
+                ms_call = r.time()
+                details["gqa_%s_m%d_T2048" % (product, m_)] = {
+                    "us": round(ms_call * 1e3, 3), "GB/s": round(r.bytes_per_call() / (ms_call * 1e-3) / 1e9, 1),
+                    "copies": r.copies}
+                r.free()
+                torch.cuda.empty_cache()
         for m_, attn, ew in ((1, "gqa", "none"), (16, "gqa", "none"), (1, "fused", "none"), (1, "fused", "separate"),
                              (1, "fused", "fused"), (16, "gqa", "fused")):
             r = DecodeStepRig(m_, attention=attn, elementwise=ew)
