@@ -144,8 +144,12 @@ static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K
     const int rows_per_iter = 64 >> lpr_log2;
     const long groups = (static_cast<long>(N) + rows_per_iter - 1) / rows_per_iter;
     // one wave per PREF row-groups (all of a small matrix is requested at once),
-    // capped at the resident-wave budget of the GPU for large N
-    long waves = (groups + PREF - 1) / PREF;
+    // capped at the resident-wave budget of the GPU for large N.  With one unit
+    // per lane and no more row groups than that budget, one wave per row group
+    // instead: the short matrices of a decode step (Q6_K 2048 x 2048 5.23 ->
+    // 4.08 us, 512 x 2048 5.14 -> 3.90, Q8_0 1536 x 576 3.11 -> 2.81) are bound
+    // by each wave's serial chain, not by bytes in flight
+    long waves = (UPL == 1 && groups <= kGemvTargetWaves) ? groups : (groups + PREF - 1) / PREF;
     if (waves > kGemvTargetWaves) waves = kGemvTargetWaves;
     const int blocks = static_cast<int>((waves + 3) / 4);
     const int lds = (dev::xpad(K) + (MODE == kActRMSNorm ? 4 : 0)) * static_cast<int>(sizeof(float));
