@@ -149,7 +149,7 @@ static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K
     // instead: the short matrices of a decode step (Q6_K 2048 x 2048 5.23 ->
     // 4.08 us, 512 x 2048 5.14 -> 3.90, Q8_0 1536 x 576 3.11 -> 2.81) are bound
     // by each wave's serial chain, not by bytes in flight
-    long waves = (UPL == 1 && groups <= kGemvTargetWaves) ? groups : (groups + PREF - 1) / PREF;
+    long waves = (UPL == 1 && (F::kSpread || groups <= kGemvTargetWaves)) ? groups : (groups + PREF - 1) / PREF;
     if (waves > kGemvTargetWaves) waves = kGemvTargetWaves;
     const int blocks = static_cast<int>((waves + 3) / 4);
     const int lds = (dev::xpad(K) + (MODE == kActRMSNorm ? 4 : 0)) * static_cast<int>(sizeof(float));

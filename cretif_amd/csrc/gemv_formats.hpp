@@ -59,6 +59,7 @@ __device__ __forceinline__ float sum_range(const float (&v)[64], int b, int n) {
 // ---------------------------------------------------------------------------
 struct GemvQ4K {
     static constexpr int kPref1 = 4;  // row-groups in flight per wave at UPL = 1
+    static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
     static constexpr int kBlockBytes = 144;
     struct Data {
         u32x4 h;       // d, dmin, scales[0..11]
@@ -132,6 +133,7 @@ struct GemvQ4K {
 // ---------------------------------------------------------------------------
 struct GemvQ8_0 {
     static constexpr int kPref1 = 2;  // row-groups in flight per wave at UPL = 1
+    static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
     static constexpr int kPairBytes = 68;
     struct Data {
         u32x4 w0, w1, w2, w3;
@@ -174,6 +176,7 @@ struct GemvQ8_0 {
 // ---------------------------------------------------------------------------
 struct GemvQ4_0 {
     static constexpr int kPref1 = 4;  // row-groups in flight per wave at UPL = 1
+    static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
     static constexpr int kPairBytes = 36;
     struct Data {
         u32x4 w0, w1;
@@ -239,6 +242,7 @@ struct GemvQ4_0 {
 // ---------------------------------------------------------------------------
 struct GemvQ5_0 {
     static constexpr int kPref1 = 4;  // row-groups in flight per wave at UPL = 1
+    static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
     static constexpr int kPairBytes = 44;
     struct Data {
         u32x4 w0, w1;
@@ -301,6 +305,9 @@ struct GemvQ5_0 {
 // ---------------------------------------------------------------------------
 struct GemvQ6K {
     static constexpr int kPref1 = 3;  // row-groups in flight per wave at UPL = 1
+    // one row group per wave up to the wave budget at UPL = 1, whatever N: the
+    // decode is long enough that more, shorter waves win (8192 x 2048: 8.20 -> 6.94 us)
+    static constexpr bool kSpread = true;
     static constexpr int kBlockBytes = 210;
     struct Data {
         uint32_t a[5], b[5], h[5];  // aligned windows of ql lo-run, ql hi-run, qh
@@ -385,6 +392,7 @@ struct GemvQ6K {
 // ---------------------------------------------------------------------------
 struct GemvF16 {
     static constexpr int kPref1 = 2;  // row-groups in flight per wave at UPL = 1
+    static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
     struct Data {
         u32x4 w[8];
     };
@@ -419,6 +427,7 @@ struct GemvF16 {
 // ---------------------------------------------------------------------------
 struct GemvF32 {
     static constexpr int kPref1 = 2;  // row-groups in flight per wave at UPL = 1
+    static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
     struct Data {
         f32x4 w[16];
     };
