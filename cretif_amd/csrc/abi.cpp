@@ -57,7 +57,10 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
         return fail(CRI_ERR_SHAPE, fn, "problem too large");
     if (K == 0) return fill_zero(C, static_cast<long>(M) * N, stream, fn);
     int rc;
-    if (cri::detail::skinny_supported(fmt, M, K, B))
+    if (M == 2 && (fmt == cri::kFmtQ8_0 || fmt == cri::kFmtQ4_0 || fmt == cri::kFmtQ5_0) && K <= 4096 &&
+        cri::detail::gemv_supported(fmt, K, B))
+        rc = cri::detail::launch_gemv2(fmt, A, B, C, N, K, stream);
+    else if (cri::detail::skinny_supported(fmt, M, K, B))
         rc = cri::detail::launch_skinny(fmt, A, B, C, M, N, K, stream);
     else if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv(fmt, A, B, C, N, K, stream);

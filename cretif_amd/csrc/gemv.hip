@@ -37,10 +37,13 @@ namespace dev {
 // row-group PREF steps ahead.
 // The activation prologue comes last in the arguments (the first 16 argument
 // dwords are preloaded into SGPRs; P.a still falls inside them).
-template <class F, int UPL, int PREF, int MODE>
+// MR activation rows (1, or 2 for plain activations): each decoded unit of
+// weights is multiplied with both rows, so a batch of two streams the weights once.
+template <class F, int UPL, int PREF, int MODE, int MR = 1>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W, float* __restrict__ y, int N, int K,
                                                    int units, long row_bytes, int lpr_log2, const ActIn P) {
-    extern __shared__ float xs[];  // K activations (padded, xpad), staged once per workgroup (+4 partial sums)
+    static_assert(MR == 1 || MODE == kActPlain, "two activation rows: plain activations only");
+    extern __shared__ float xs[];  // MR x K activations (padded, xpad), staged once per workgroup (+4 partial sums)
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
     const int u0 = lane & (lpr - 1);
@@ -60,13 +63,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
     }
 
     // 1. activations: global -> registers (issued first, tiny), weights in flight behind them
-    ActRaw<MODE> xv[4];
+    ActRaw<MODE> xv[MR][4];
     const int nx4 = K >> 2;
+    const int xrow = xpad(K);  // LDS floats per staged activation row
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int j = threadIdx.x + 256 * i;
-        if (j < nx4) act_load<MODE>(xv[i], P, 0, 4 * j, 0);
-    }
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = threadIdx.x + 256 * i;
+            if (j < nx4) act_load<MODE>(xv[m][i], P, m, 4 * j, P.lda);
+        }
     typename F::Data buf[PREF][UPL];
     const int base0 = gwave * rows_per_iter;
     // Row-group b past the end is a placeholder read: every lane takes unit 0 of row 0, so the
@@ -89,15 +95,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
     float ss = 0.0f;
     const bool write_h = blockIdx.x == 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int j = threadIdx.x + 256 * i;
-        if (j < nx4) *reinterpret_cast<f32x4*>(xs + xpad(4 * j)) = act_finish<MODE>(xv[i], P, 0, 4 * j, K, ss, write_h);
-    }
-    for (int j = threadIdx.x + 1024; j < nx4; j += 256) {
-        ActRaw<MODE> raw;
-        act_load<MODE>(raw, P, 0, 4 * j, 0);
-        *reinterpret_cast<f32x4*>(xs + xpad(4 * j)) = act_finish<MODE>(raw, P, 0, 4 * j, K, ss, write_h);
-    }
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = threadIdx.x + 256 * i;
+            if (j < nx4)
+                *reinterpret_cast<f32x4*>(xs + m * xrow + xpad(4 * j)) =
+                    act_finish<MODE>(xv[m][i], P, m, 4 * j, K, ss, write_h);
+        }
+    for (int j = threadIdx.x + 1024; j < nx4; j += 256)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            ActRaw<MODE> raw;
+            act_load<MODE>(raw, P, m, 4 * j, P.lda);
+            *reinterpret_cast<f32x4*>(xs + m * xrow + xpad(4 * j)) = act_finish<MODE>(raw, P, m, 4 * j, K, ss, write_h);
+        }
     if constexpr (MODE == kActRMSNorm) {
         ss = group_sum_t<6>(ss);
         if (lane == 0) xs[xpad(K) + (threadIdx.x >> 6)] = ss;
@@ -108,21 +120,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
         const float* part = xs + xpad(K);
         rs = rms_factor(((part[0] + part[1]) + part[2]) + part[3], K, P.eps);
     }
-    typename F::Xr xr[UPL];
+    typename F::Xr xr[MR][UPL];
 #pragma unroll
-    for (int u = 0; u < UPL; ++u) F::load_x(xr[u], xs, unit[u]);
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int u = 0; u < UPL; ++u) F::load_x(xr[m][u], xs + m * xrow, unit[u]);
 
     // 3. stream the wave's row-groups
     auto finish = [&](const typename F::Data(&src)[UPL], int b) {
-        float acc = 0.0f;
 #pragma unroll
-        for (int u = 0; u < UPL; ++u) {
-            const float p = F::dot(src[u], xr[u], unit[u]);
-            acc += valid[u] ? p : 0.0f;
+        for (int m = 0; m < MR; ++m) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int u = 0; u < UPL; ++u) {
+                const float p = F::dot(src[u], xr[m][u], unit[u]);
+                acc += valid[u] ? p : 0.0f;
+            }
+            acc = group_sum(acc, lpr_log2);
+            const int r = b + rsub;
+            if (u0 == 0 && r < N) y[static_cast<long>(m) * N + r] = MODE == kActRMSNorm ? acc * rs : acc;
         }
-        acc = group_sum(acc, lpr_log2);
-        const int r = b + rsub;
-        if (u0 == 0 && r < N) y[r] = MODE == kActRMSNorm ? acc * rs : acc;
     };
     for (int b = base0; b < N; b += PREF * stride) {
 #pragma unroll
@@ -138,7 +155,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 
 namespace detail {
 
-template <class F, int UPL, int PREF, int MODE>
+template <class F, int UPL, int PREF, int MODE, int MR = 1>
 static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K, int units, long row_bytes,
                           int lpr_log2, hipStream_t stream) {
     const int rows_per_iter = 64 >> lpr_log2;
@@ -152,25 +169,25 @@ static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K
     long waves = (UPL == 1 && (F::kSpread || groups <= kGemvTargetWaves)) ? groups : (groups + PREF - 1) / PREF;
     if (waves > kGemvTargetWaves) waves = kGemvTargetWaves;
     const int blocks = static_cast<int>((waves + 3) / 4);
-    const int lds = (dev::xpad(K) + (MODE == kActRMSNorm ? 4 : 0)) * static_cast<int>(sizeof(float));
+    const int lds = (MR * dev::xpad(K) + (MODE == kActRMSNorm ? 4 : 0)) * static_cast<int>(sizeof(float));
     if (lds > 65536) {  // beyond the default dynamic-LDS limit: raise it once per kernel and device
         constexpr int kMaxDevices = 64;
         static std::atomic<bool> ready[kMaxDevices];
         int devid = 0;
         if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return -1;
         if (!ready[devid].load(std::memory_order_acquire)) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::gemv_kernel<F, UPL, PREF, MODE>),
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::gemv_kernel<F, UPL, PREF, MODE, MR>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
                 return -1;
             ready[devid].store(true, std::memory_order_release);
         }
     }
-    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE>), dim3(blocks), dim3(256), lds, stream,
+    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE, MR>), dim3(blocks), dim3(256), lds, stream,
                        static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act);
     return 0;
 }
 
-template <class F, int MODE>
+template <class F, int MODE, int MR = 1>
 static int launch_gemv_f(const ActIn& x, const void* W, float* y, int N, int K, long row_bytes,
                          hipStream_t stream) {
     const int units = K / 64;
@@ -179,10 +196,14 @@ static int launch_gemv_f(const ActIn& x, const void* W, float* y, int N, int K, 
     const int lpr = 1 << lpr_log2;
     const int upl = (units + lpr - 1) / lpr;
     switch (upl) {
-        case 1: return launch_gemv_t<F, 1, F::kPref1, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
-        case 2: return launch_gemv_t<F, 2, 2, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
+        case 1: return launch_gemv_t<F, 1, F::kPref1, MODE, MR>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
+        case 2:
+            if constexpr (MR > 1) return -1;  // two activation rows: one unit per lane (K <= 4096)
+            return launch_gemv_t<F, 2, 2, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
         case 3:
-        case 4: return launch_gemv_t<F, 4, 1, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
+        case 4:
+            if constexpr (MR > 1) return -1;
+            return launch_gemv_t<F, 4, 1, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
         default: return -1;
     }
     return 0;
@@ -206,6 +227,19 @@ static int launch_gemv_m(int fmt, const ActIn& x, const void* W, float* y, int N
         case kFmtF32:
             if constexpr (MODE == kActPlain) return launch_gemv_f<dev::GemvF32, MODE>(x, W, y, N, K, K * 4L, stream);
             break;
+    }
+    return -1;
+}
+
+// Two activation rows (a batch of two decode tokens) for the 32-element formats: the
+// weights are decoded once and streamed once for both rows.  K <= 4096.
+int launch_gemv2(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream) {
+    const ActIn act{x, nullptr, nullptr, nullptr, K, 0.0f};
+    if (K / 64 > 64) return -1;
+    switch (fmt) {
+        case kFmtQ8_0: return launch_gemv_f<dev::GemvQ8_0, kActPlain, 2>(act, W, y, N, K, (K / 32) * 34L, stream);
+        case kFmtQ4_0: return launch_gemv_f<dev::GemvQ4_0, kActPlain, 2>(act, W, y, N, K, (K / 32) * 18L, stream);
+        case kFmtQ5_0: return launch_gemv_f<dev::GemvQ5_0, kActPlain, 2>(act, W, y, N, K, (K / 32) * 22L, stream);
     }
     return -1;
 }

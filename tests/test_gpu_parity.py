@@ -215,6 +215,21 @@ def test_skinny_staging_paths(orc, fmt, M, N, K):
     assert normwise_rel_err(got, ref) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q5_0"])
+@pytest.mark.parametrize("N,K", [(1536, 576), (300, 2048), (17, 4096), (1001, 64), (8192, 2048)])
+def test_two_row_gemv(orc, fmt, N, K):
+    # M = 2 of the 32-element formats with K <= 4096 (K % 64 == 0): one GEMV launch
+    # multiplies each decoded weight unit with both activation rows
+    A = quant.randn(2 * K, seed=N + K).reshape(2, K)
+    Bq = weights(fmt, N, K, seed=N * 3 + K)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= GEMV_TOL
+    # each row alone through the batch-1 GEMV gives the same bits
+    for m in range(2):
+        assert np.array_equal(run_matmul(fmt, A[m:m + 1], Bq, N, K), got[m:m + 1])
+
+
 @pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
 def test_skinny_chunk_split_is_deterministic(fmt):
     # two partial sums per output added atomically in either order: the same bits every call
