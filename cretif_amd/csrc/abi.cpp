@@ -57,7 +57,10 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
         return fail(CRI_ERR_SHAPE, fn, "problem too large");
     if (K == 0) return fill_zero(C, static_cast<long>(M) * N, stream, fn);
     int rc;
-    if (M == 2 && (fmt == cri::kFmtQ8_0 || fmt == cri::kFmtQ4_0 || fmt == cri::kFmtQ5_0) && K <= 4096 &&
+    // a batch of two on the two-row GEMV (Q8_0, Q4_0, Q5_0, Q6_K; measured faster than the
+    // skinny MFMA kernel there)
+    if (M == 2 && (fmt == cri::kFmtQ8_0 || fmt == cri::kFmtQ4_0 || fmt == cri::kFmtQ5_0 || fmt == cri::kFmtQ6_K) &&
+        K <= 4096 &&
         cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv2(fmt, A, B, C, N, K, stream);
     else if (cri::detail::skinny_supported(fmt, M, K, B))

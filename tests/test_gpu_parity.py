@@ -215,10 +215,11 @@ def test_skinny_staging_paths(orc, fmt, M, N, K):
     assert normwise_rel_err(got, ref) <= GEMV_TOL
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q5_0"])
-@pytest.mark.parametrize("N,K", [(1536, 576), (300, 2048), (17, 4096), (1001, 64), (8192, 2048)])
+@pytest.mark.parametrize("fmt,N,K", [(f, n, k) for f in ("q8_0", "q4_0", "q5_0")
+                                     for n, k in ((1536, 576), (300, 2048), (17, 4096), (1001, 64), (8192, 2048))]
+                         + [("q6_k", 2048, 2048), ("q6_k", 300, 4096), ("q6_k", 17, 256)])
 def test_two_row_gemv(orc, fmt, N, K):
-    # M = 2 of the 32-element formats with K <= 4096 (K % 64 == 0): one GEMV launch
+    # M = 2 of Q8_0 / Q4_0 / Q5_0 / Q6_K with K <= 4096 (K % 64 == 0): one GEMV launch
     # multiplies each decoded weight unit with both activation rows
     A = quant.randn(2 * K, seed=N + K).reshape(2, K)
     Bq = weights(fmt, N, K, seed=N * 3 + K)
