@@ -62,15 +62,20 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
     if (M == 2 && (fmt == cri::kFmtQ8_0 || fmt == cri::kFmtQ4_0 || fmt == cri::kFmtQ5_0 || fmt == cri::kFmtQ6_K) &&
         K <= 4096 &&
         cri::detail::gemv_supported(fmt, K, B))
-        rc = cri::detail::launch_gemv2(fmt, A, B, C, N, K, stream);
+        rc = cri::detail::launch_gemv2(fmt, A, B, C, M, N, K, stream);
     else if (cri::detail::skinny_supported(fmt, M, K, B))
         rc = cri::detail::launch_skinny(fmt, A, B, C, M, N, K, stream);
     else if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv(fmt, A, B, C, N, K, stream);
     else if (M > kPrefillMinM && cri::detail::mfma_gemm_supported(fmt, M, N, K, A, B))
         rc = cri::detail::launch_mfma_gemm(fmt, A, B, C, M, N, K, stream);
+    else if (M <= 16 && (fmt == cri::kFmtQ8_0 || fmt == cri::kFmtQ4_0 || fmt == cri::kFmtQ5_0) && K <= 4096 &&
+             cri::detail::gemv_supported(fmt, K, B))
+        // small batches whose K is not a multiple of 256 (no skinny kernel): row pairs on the two-row GEMV
+        rc = cri::detail::launch_gemv2(fmt, A, B, C, M, N, K, stream);
     else
-        rc = cri::detail::launch_generic_matmul(fmt, A, B, C, M, N, K, stream);
+        rc = -1;
+    if (rc != 0) rc = cri::detail::launch_generic_matmul(fmt, A, B, C, M, N, K, stream);
     if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
     return check_launch(fn);
 }

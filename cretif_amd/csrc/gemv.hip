@@ -39,9 +39,11 @@ namespace dev {
 // dwords are preloaded into SGPRs; P.a still falls inside them).
 // MR activation rows (1, or 2 for plain activations): each decoded unit of
 // weights is multiplied with both rows, so a batch of two streams the weights once.
+// Workgroup row blockIdx.y takes activation rows MR y .. MR y + MR - 1 of mrows
+// (past the last row: the last row again, not stored).
 template <class F, int UPL, int PREF, int MODE, int MR = 1>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W, float* __restrict__ y, int N, int K,
-                                                   int units, long row_bytes, int lpr_log2, const ActIn P) {
+                                                   int units, long row_bytes, int lpr_log2, const ActIn P, int mrows) {
     static_assert(MR == 1 || MODE == kActPlain, "two activation rows: plain activations only");
     extern __shared__ float xs[];  // MR x K activations (padded, xpad), staged once per workgroup (+4 partial sums)
     const int lane = threadIdx.x & 63;
@@ -71,7 +73,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int j = threadIdx.x + 256 * i;
-            if (j < nx4) act_load<MODE>(xv[m][i], P, m, 4 * j, P.lda);
+            if (j < nx4) act_load<MODE>(xv[m][i], P, min(MR * static_cast<int>(blockIdx.y) + m, mrows - 1), 4 * j, P.lda);
         }
     typename F::Data buf[PREF][UPL];
     const int base0 = gwave * rows_per_iter;
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             ActRaw<MODE> raw;
-            act_load<MODE>(raw, P, m, 4 * j, P.lda);
+            act_load<MODE>(raw, P, min(MR * static_cast<int>(blockIdx.y) + m, mrows - 1), 4 * j, P.lda);
             *reinterpret_cast<f32x4*>(xs + m * xrow + xpad(4 * j)) = act_finish<MODE>(raw, P, m, 4 * j, K, ss, write_h);
         }
     if constexpr (MODE == kActRMSNorm) {
@@ -138,7 +140,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
             }
             acc = group_sum(acc, lpr_log2);
             const int r = b + rsub;
-            if (u0 == 0 && r < N) y[static_cast<long>(m) * N + r] = MODE == kActRMSNorm ? acc * rs : acc;
+            const int orow = MR * static_cast<int>(blockIdx.y) + m;
+            if (u0 == 0 && r < N && orow < mrows) y[static_cast<long>(orow) * N + r] = MODE == kActRMSNorm ? acc * rs : acc;
         }
     };
     for (int b = base0; b < N; b += PREF * stride) {
@@ -157,7 +160,7 @@ namespace detail {
 
 template <class F, int UPL, int PREF, int MODE, int MR = 1>
 static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K, int units, long row_bytes,
-                          int lpr_log2, hipStream_t stream) {
+                          int lpr_log2, hipStream_t stream, int mrows = 1) {
     const int rows_per_iter = 64 >> lpr_log2;
     const long groups = (static_cast<long>(N) + rows_per_iter - 1) / rows_per_iter;
     // one wave per PREF row-groups (all of a small matrix is requested at once),
@@ -182,21 +185,22 @@ static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K
             ready[devid].store(true, std::memory_order_release);
         }
     }
-    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE, MR>), dim3(blocks), dim3(256), lds, stream,
-                       static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act);
+    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE, MR>), dim3(blocks, (mrows + MR - 1) / MR), dim3(256), lds,
+                       stream, static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act, mrows);
     return 0;
 }
 
 template <class F, int MODE, int MR = 1>
 static int launch_gemv_f(const ActIn& x, const void* W, float* y, int N, int K, long row_bytes,
-                         hipStream_t stream) {
+                         hipStream_t stream, int mrows = 1) {
     const int units = K / 64;
     int lpr_log2 = 0;
     while ((1 << lpr_log2) < units && lpr_log2 < 6) ++lpr_log2;
     const int lpr = 1 << lpr_log2;
     const int upl = (units + lpr - 1) / lpr;
     switch (upl) {
-        case 1: return launch_gemv_t<F, 1, F::kPref1, MODE, MR>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
+        case 1:
+            return launch_gemv_t<F, 1, F::kPref1, MODE, MR>(x, W, y, N, K, units, row_bytes, lpr_log2, stream, mrows);
         case 2:
             if constexpr (MR > 1) return -1;  // two activation rows: one unit per lane (K <= 4096)
             return launch_gemv_t<F, 2, 2, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
@@ -233,16 +237,17 @@ static int launch_gemv_m(int fmt, const ActIn& x, const void* W, float* y, int N
 
 // Two activation rows (a batch of two decode tokens) for the 32-element formats and
 // Q6_K: the weights are decoded once and streamed once for both rows.  K <= 4096.
+// M rows (up to 16) run as ceil(M / 2) row pairs, one per grid row.
 // (Q4_K and FP16 at M = 2 measured faster on the skinny MFMA kernel: 5.1 against
 // 6.9 us and 8.9 against 9.7 us at 8192 x 2048.)
-int launch_gemv2(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream) {
+int launch_gemv2(int fmt, const float* x, const void* W, float* y, int M, int N, int K, hipStream_t stream) {
     const ActIn act{x, nullptr, nullptr, nullptr, K, 0.0f};
-    if (K / 64 > 64) return -1;
+    if (K / 64 > 64 || M < 1 || M > 16) return -1;
     switch (fmt) {
-        case kFmtQ8_0: return launch_gemv_f<dev::GemvQ8_0, kActPlain, 2>(act, W, y, N, K, (K / 32) * 34L, stream);
-        case kFmtQ4_0: return launch_gemv_f<dev::GemvQ4_0, kActPlain, 2>(act, W, y, N, K, (K / 32) * 18L, stream);
-        case kFmtQ5_0: return launch_gemv_f<dev::GemvQ5_0, kActPlain, 2>(act, W, y, N, K, (K / 32) * 22L, stream);
-        case kFmtQ6_K: return launch_gemv_f<dev::GemvQ6K, kActPlain, 2>(act, W, y, N, K, (K / 256) * 210L, stream);
+        case kFmtQ8_0: return launch_gemv_f<dev::GemvQ8_0, kActPlain, 2>(act, W, y, N, K, (K / 32) * 34L, stream, M);
+        case kFmtQ4_0: return launch_gemv_f<dev::GemvQ4_0, kActPlain, 2>(act, W, y, N, K, (K / 32) * 18L, stream, M);
+        case kFmtQ5_0: return launch_gemv_f<dev::GemvQ5_0, kActPlain, 2>(act, W, y, N, K, (K / 32) * 22L, stream, M);
+        case kFmtQ6_K: return launch_gemv_f<dev::GemvQ6K, kActPlain, 2>(act, W, y, N, K, (K / 256) * 210L, stream, M);
     }
     return -1;
 }

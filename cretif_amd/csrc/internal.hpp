@@ -61,7 +61,7 @@ constexpr long kGemvTargetWaves = 2048;
 // batch-1 GEMV (gemv.hip); the _act form takes an activation prologue
 bool gemv_supported(int fmt, int K, const void* W);
 int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream);
-int launch_gemv2(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream);
+int launch_gemv2(int fmt, const float* x, const void* W, float* y, int M, int N, int K, hipStream_t stream);
 int launch_gemv_act(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t stream);
 
 // 1 <= M <= 16 fused dequant matmul on the matrix cores (mfma_skinny.hip)

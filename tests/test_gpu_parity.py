@@ -231,6 +231,19 @@ def test_two_row_gemv(orc, fmt, N, K):
         assert np.array_equal(run_matmul(fmt, A[m:m + 1], Bq, N, K), got[m:m + 1])
 
 
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q5_0"])
+@pytest.mark.parametrize("M,N,K", [(3, 1536, 576), (5, 300, 320), (16, 77, 4032), (7, 1001, 64)])
+def test_row_pair_gemv(orc, fmt, M, N, K):
+    # 3 <= M <= 16 with K % 256 != 0 (no skinny kernel): row pairs of the two-row GEMV,
+    # one per grid row (an odd M repeats its last row in the last pair, unstored)
+    A = quant.randn(M * K, seed=M * 7 + K).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=N + M + K)
+    got = run_matmul(fmt, A, Bq, N, K)
+    assert normwise_rel_err(got, orc.matmul_quant(fmt, A, Bq, N, K)) <= GEMV_TOL
+    for m in (0, M - 1):
+        assert np.array_equal(run_matmul(fmt, A[m:m + 1], Bq, N, K), got[m:m + 1])
+
+
 @pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
 def test_skinny_chunk_split_is_deterministic(fmt):
     # two partial sums per output added atomically in either order: the same bits every call
