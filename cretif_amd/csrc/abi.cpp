@@ -57,10 +57,12 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
         return fail(CRI_ERR_SHAPE, fn, "problem too large");
     if (K == 0) return fill_zero(C, static_cast<long>(M) * N, stream, fn);
     int rc;
-    // a batch of two on the two-row GEMV (Q8_0, Q4_0, Q5_0, Q6_K; measured faster than the
-    // skinny MFMA kernel there)
-    if (M == 2 && (fmt == cri::kFmtQ8_0 || fmt == cri::kFmtQ4_0 || fmt == cri::kFmtQ5_0 || fmt == cri::kFmtQ6_K) &&
-        K <= 4096 &&
+    // batches of two (Q8_0, Q4_0, Q5_0, Q6_K) or up to four (the 32-element formats) as row
+    // pairs on the two-row GEMV: measured faster than the skinny MFMA kernel there
+    // (8192 x 2048 at M = 4: Q4_0 11.7 -> 9.3 us, Q5_0 16.7 -> 9.5, Q8_0 12.0 -> 10.4); from
+    // M = 8, and for Q6_K from M = 4, the skinny kernel is faster
+    const bool fmt32 = fmt == cri::kFmtQ8_0 || fmt == cri::kFmtQ4_0 || fmt == cri::kFmtQ5_0;
+    if (((M >= 2 && M <= 4 && fmt32) || (M == 2 && fmt == cri::kFmtQ6_K)) && K <= 4096 &&
         cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv2(fmt, A, B, C, M, N, K, stream);
     else if (cri::detail::skinny_supported(fmt, M, K, B))
@@ -69,8 +71,7 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
         rc = cri::detail::launch_gemv(fmt, A, B, C, N, K, stream);
     else if (M > kPrefillMinM && cri::detail::mfma_gemm_supported(fmt, M, N, K, A, B))
         rc = cri::detail::launch_mfma_gemm(fmt, A, B, C, M, N, K, stream);
-    else if (M <= 16 && (fmt == cri::kFmtQ8_0 || fmt == cri::kFmtQ4_0 || fmt == cri::kFmtQ5_0) && K <= 4096 &&
-             cri::detail::gemv_supported(fmt, K, B))
+    else if (M <= 16 && fmt32 && K <= 4096 && cri::detail::gemv_supported(fmt, K, B))
         // small batches whose K is not a multiple of 256 (no skinny kernel): row pairs on the two-row GEMV
         rc = cri::detail::launch_gemv2(fmt, A, B, C, M, N, K, stream);
     else

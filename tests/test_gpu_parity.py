@@ -232,10 +232,11 @@ def test_two_row_gemv(orc, fmt, N, K):
 
 
 @pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q5_0"])
-@pytest.mark.parametrize("M,N,K", [(3, 1536, 576), (5, 300, 320), (16, 77, 4032), (7, 1001, 64)])
+@pytest.mark.parametrize("M,N,K", [(3, 1536, 576), (5, 300, 320), (16, 77, 4032), (7, 1001, 64),
+                                   (3, 300, 2048), (4, 8192, 2048)])
 def test_row_pair_gemv(orc, fmt, M, N, K):
-    # 3 <= M <= 16 with K % 256 != 0 (no skinny kernel): row pairs of the two-row GEMV,
-    # one per grid row (an odd M repeats its last row in the last pair, unstored)
+    # row pairs of the two-row GEMV, one per grid row (an odd M repeats its last row in the
+    # last pair, unstored): 3 <= M <= 4, and up to 16 when K % 256 != 0 (no skinny kernel)
     A = quant.randn(M * K, seed=M * 7 + K).reshape(M, K)
     Bq = weights(fmt, N, K, seed=N + M + K)
     got = run_matmul(fmt, A, Bq, N, K)
