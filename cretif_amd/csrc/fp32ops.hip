@@ -7,7 +7,7 @@
 // batched_matmul_gqa: C[h] = A[h] * B[h / G] with A [H,M,K], B [Hkv,K,N]
 //   (ref:src/attention.cu:192-218).  The G query heads sharing a KV head are
 //   served together, so each B element is read once per KV head:
-//   a block owns 64 columns (one per lane) x 16 (head, m) rows of one KV
+//   a block owns 64 columns (one per lane) x RT (4 or 8) (head, m) rows of one KV
 //   group; its four waves take interleaved 16-column k slices of each 64-k
 //   stage (row values broadcast from LDS, B read once, coalesced along n) and
 //   add their partial sums through LDS in a fixed order.  Short K (QK^T over
@@ -28,26 +28,30 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, l
 }
 
 // ---- GQA kernel -----------------------------------------------------------------
-constexpr int kGsRT = 16;  // rows per block (32 measured slower: fewer blocks)
+// RT rows per block: 4 when a KV group has at most 4 (head, m) rows (one query
+// token), else 8.  Fewer rows per block mean more blocks in flight, which these
+// latency-bound products need (T = 2048, 32/8 heads: Q K^T 4.7 -> 3.4 us at M = 1,
+// 8.8 -> 7.4 at M = 16 against 16 rows; 32 rows was slower still).
 constexpr int kGsKC = 16;  // k per wave per LDS stage (a stage is 4 waves x 16 k)
 
+template <int RT>
 __global__ __launch_bounds__(256) void gqa_split_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                         float* __restrict__ C, int G, int M, int N, int K,
                                                         int k_split, int atomic) {
-    __shared__ float qs[kGsRT][4 * kGsKC + 4];
-    __shared__ float red[3][kGsRT][64];
+    __shared__ float qs[RT][4 * kGsKC + 4];
+    __shared__ float red[3][RT][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = blockIdx.x * 64 + lane;
     const int kv = blockIdx.y;
-    const int rt = blockIdx.z % ((G * M + kGsRT - 1) / kGsRT);
-    const int split = blockIdx.z / ((G * M + kGsRT - 1) / kGsRT);
-    const int r0 = rt * kGsRT;
+    const int rt = blockIdx.z % ((G * M + RT - 1) / RT);
+    const int split = blockIdx.z / ((G * M + RT - 1) / RT);
+    const int r0 = rt * RT;
     const int R = G * M;
     const int kb = split * k_split, ke = min(K, kb + k_split);
     const float* Bk = B + static_cast<long>(kv) * K * N + min(n, N - 1);
-    float acc[kGsRT];
+    float acc[RT];
 #pragma unroll
-    for (int r = 0; r < kGsRT; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < RT; ++r) acc[r] = 0.0f;
     // each stage: 4 waves x kGsKC k; wave w takes k [k0 + w * kGsKC, +kGsKC).  The
     // wave's B loads are issued before the row values are staged, so the two
     // latencies overlap.
@@ -56,7 +60,7 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(const float* __restrict_
         float b[kGsKC];
 #pragma unroll
         for (int kk = 0; kk < kGsKC; ++kk) b[kk] = kw + kk < ke ? Bk[static_cast<long>(kw + kk) * N] : 0.0f;
-        for (int e = tid; e < kGsRT * 4 * kGsKC; e += 256) {
+        for (int e = tid; e < RT * 4 * kGsKC; e += 256) {
             const int rr = e / (4 * kGsKC), kk = e - rr * (4 * kGsKC), r = r0 + rr, k = k0 + kk;
             float v = 0.0f;
             if (r < R && k < ke) {
@@ -69,7 +73,7 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(const float* __restrict_
 #pragma unroll
         for (int kk = 0; kk < kGsKC; kk += 4)
 #pragma unroll
-            for (int r = 0; r < kGsRT; ++r) {
+            for (int r = 0; r < RT; ++r) {
                 const f32x4 q = *reinterpret_cast<const f32x4*>(&qs[r][wave * kGsKC + kk]);
                 acc[r] = __builtin_fmaf(q.x, b[kk], acc[r]);
                 acc[r] = __builtin_fmaf(q.y, b[kk + 1], acc[r]);
@@ -81,11 +85,11 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(const float* __restrict_
     // add the four waves' partial sums (fixed order)
     if (wave > 0)
 #pragma unroll
-        for (int r = 0; r < kGsRT; ++r) red[wave - 1][r][lane] = acc[r];
+        for (int r = 0; r < RT; ++r) red[wave - 1][r][lane] = acc[r];
     __syncthreads();
     if (wave != 0 || n >= N) return;
 #pragma unroll
-    for (int rr = 0; rr < kGsRT; ++rr) {
+    for (int rr = 0; rr < RT; ++rr) {
         const int r = r0 + rr;
         if (r >= R) break;
         const float v = ((acc[rr] + red[0][rr][lane]) + red[1][rr][lane]) + red[2][rr][lane];
@@ -119,7 +123,8 @@ int launch_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_h
     // blocks per CU: a block's stages run one after another, so several resident blocks
     // per CU hide each other's load latency (P V at M = 16: 21.2 us with ~1 block per CU,
     // 14.2 with 2, 12.5 with 4, despite 4x the atomic adds)
-    const long rtiles = (R + dev::kGsRT - 1) / dev::kGsRT;
+    const int RT = R <= 4 ? 4 : 8;
+    const long rtiles = (R + RT - 1) / RT;
     const long base = static_cast<long>((N + 63) / 64) * rtiles * n_kv_heads;
     const int stage = 4 * dev::kGsKC;
     const int stages = (K + stage - 1) / stage;
@@ -131,7 +136,10 @@ int launch_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_h
     const int atomic = splits > 1;
     if (atomic) launch_fill_zero(C, static_cast<long>(n_heads) * M * N, stream);
     const dim3 grid((N + 63) / 64, n_kv_heads, static_cast<unsigned>(rtiles * splits));
-    hipLaunchKernelGGL(dev::gqa_split_kernel, grid, dim3(256), 0, stream, A, B, C, G, M, N, K, k_split, atomic);
+    if (RT == 4)
+        hipLaunchKernelGGL(dev::gqa_split_kernel<4>, grid, dim3(256), 0, stream, A, B, C, G, M, N, K, k_split, atomic);
+    else
+        hipLaunchKernelGGL(dev::gqa_split_kernel<8>, grid, dim3(256), 0, stream, A, B, C, G, M, N, K, k_split, atomic);
     return 0;
 }
 
