@@ -37,6 +37,54 @@ __global__ __launch_bounds__(256) void rmsnorm_residual_kernel(const float* inpu
     for (int i = threadIdx.x; i < n; i += 256) nrm[i] = out[i] * weight[i] * f;
 }
 
+// Rows of up to 4096 floats, 16-byte aligned: every load of the row (input,
+// residual and weight, 16 bytes each) is issued before the reduction and the
+// values stay in registers, so the row takes one memory round trip (the loop
+// form above re-reads `output` after the barrier).  `output` is the same; the
+// sum of squares is accumulated in another order, so `normed` can differ from
+// the loop form in the last bits.
+__global__ __launch_bounds__(256) void rmsnorm_residual_vec_kernel(const float* input, const float* residual,
+                                                                   const float* __restrict__ weight, float* output,
+                                                                   float* __restrict__ normed, int n, float eps) {
+    __shared__ float part[4];
+    const long row = blockIdx.x;
+    const float* in = input + row * n;
+    const float* res = residual ? residual + row * n : nullptr;
+    float* out = output + row * n;
+    float* nrm = normed + row * n;
+    f32x4 v[4], w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = 4 * (threadIdx.x + 256 * j);
+        if (i < n) {
+            v[j] = *reinterpret_cast<const f32x4*>(in + i);
+            if (res) v[j] += *reinterpret_cast<const f32x4*>(res + i);
+            w[j] = *reinterpret_cast<const f32x4*>(weight + i);
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = 4 * (threadIdx.x + 256 * j);
+        if (i < n) {
+            *reinterpret_cast<f32x4*>(out + i) = v[j];
+            ss = __builtin_fmaf(v[j].x, v[j].x, ss);
+            ss = __builtin_fmaf(v[j].y, v[j].y, ss);
+            ss = __builtin_fmaf(v[j].z, v[j].z, ss);
+            ss = __builtin_fmaf(v[j].w, v[j].w, ss);
+        }
+    }
+    ss = group_sum_t<6>(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float f = rms_factor(((part[0] + part[1]) + part[2]) + part[3], n, eps);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = 4 * (threadIdx.x + 256 * j);
+        if (i < n) *reinterpret_cast<f32x4*>(nrm + i) = v[j] * w[j] * f;
+    }
+}
+
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float* gate, const float* up, float* out, long n) {
     const long stride = static_cast<long>(gridDim.x) * 256;
     for (long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
@@ -49,8 +97,13 @@ namespace detail {
 
 int launch_rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output,
                             float* normed, int rows, int n, float eps, hipStream_t stream) {
-    hipLaunchKernelGGL(dev::rmsnorm_residual_kernel, dim3(rows), dim3(256), 0, stream, input, residual, weight, output,
-                       normed, n, eps);
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (n <= 4096 && n % 4 == 0 && a16(input) && a16(residual) && a16(weight) && a16(output) && a16(normed))
+        hipLaunchKernelGGL(dev::rmsnorm_residual_vec_kernel, dim3(rows), dim3(256), 0, stream, input, residual, weight,
+                           output, normed, n, eps);
+    else
+        hipLaunchKernelGGL(dev::rmsnorm_residual_kernel, dim3(rows), dim3(256), 0, stream, input, residual, weight,
+                           output, normed, n, eps);
     return 0;
 }
 
