@@ -538,7 +538,7 @@ def main():
 
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the kernels shard by "
-              "output rows without communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "output rows without communication). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
