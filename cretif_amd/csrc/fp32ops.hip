@@ -13,7 +13,7 @@
 //   add their partial sums through LDS in a fixed order.  Short K (QK^T over
 //   head_dim) has enough (column tile, row tile, KV head) blocks and stores
 //   plainly (deterministic); long K (PV over the cache length) is also split
-//   over blocks until ~4 blocks per CU run, and those partial tiles are added
+//   over blocks until ~8 blocks per CU run, and those partial tiles are added
 //   with fp32 atomics into a zero-filled C.
 #include "common.hpp"
 #include "internal.hpp"
@@ -119,17 +119,18 @@ int launch_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_h
                hipStream_t stream) {
     const int G = n_heads / n_kv_heads;
     const long R = static_cast<long>(G) * M;
-    // split K over blocks while (column tiles x row tiles x KV heads) gives fewer than ~4
+    // split K over blocks while (column tiles x row tiles x KV heads) gives fewer than ~8
     // blocks per CU: a block's stages run one after another, so several resident blocks
-    // per CU hide each other's load latency (P V at M = 16: 21.2 us with ~1 block per CU,
-    // 14.2 with 2, 12.5 with 4, despite 4x the atomic adds)
+    // per CU hide each other's load latency (P V at M = 16 with 16-row blocks: 21.2 us
+    // with ~1 block per CU, 14.2 with 2, 12.5 with 4, despite 4x the atomic adds; with
+    // 8-row blocks 10.6 us at 4 and 10.2 at 8)
     const int RT = R <= 4 ? 4 : 8;
     const long rtiles = (R + RT - 1) / RT;
     const long base = static_cast<long>((N + 63) / 64) * rtiles * n_kv_heads;
     const int stage = 4 * dev::kGsKC;
     const int stages = (K + stage - 1) / stage;
     int splits = 1;
-    while (base * splits < 1024 && splits * 2 <= stages) splits *= 2;
+    while (base * splits < 2048 && splits * 2 <= stages) splits *= 2;
     const int k_split = ((stages + splits - 1) / splits) * stage;
     splits = (K + k_split - 1) / k_split;
     if (rtiles * splits > 65535) return -1;
