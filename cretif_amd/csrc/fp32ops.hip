@@ -6,7 +6,8 @@
 //   LDS-tiled fallback.
 // batched_matmul_gqa: C[h] = A[h] * B[h / G] with A [H,M,K], B [Hkv,K,N]
 //   (ref:src/attention.cu:192-218).  The G query heads sharing a KV head are
-//   served together, so each B element is read once per KV head:
+//   served together, so each B element is read once per row tile of its KV
+//   group (the repeats hit the caches):
 //   a block owns 64 columns (one per lane) x RT (4 or 8) (head, m) rows of one KV
 //   group; its four waves take interleaved 16-column k slices of each 64-k
 //   stage (row values broadcast from LDS, B read once, coalesced along n) and
