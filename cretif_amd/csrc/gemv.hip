@@ -203,7 +203,9 @@ static int launch_gemv_f(const ActIn& x, const void* W, float* y, int N, int K, 
             return launch_gemv_t<F, 1, F::kPref1, MODE, MR>(x, W, y, N, K, units, row_bytes, lpr_log2, stream, mrows);
         case 2:
             if constexpr (MR > 1) return -1;  // two activation rows: one unit per lane (K <= 4096)
-            return launch_gemv_t<F, 2, 2, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
+            // one row group in flight: fewer registers, twice the waves (2048 x 8192: Q8_0 7.68 ->
+            // 7.36 us, Q4_0 6.27 -> 6.09, Q5_0 7.24 -> 6.93, FP16 11.13 -> 10.25 against two)
+            return launch_gemv_t<F, 2, 1, MODE>(x, W, y, N, K, units, row_bytes, lpr_log2, stream);
         case 3:
         case 4:
             if constexpr (MR > 1) return -1;
