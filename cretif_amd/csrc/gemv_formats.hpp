@@ -132,7 +132,7 @@ struct GemvQ4K {
 // qs @36..67 (ref:src/kernels/dequantize.cu:34-48).
 // ---------------------------------------------------------------------------
 struct GemvQ8_0 {
-    static constexpr int kPref1 = 2;  // row-groups in flight per wave at UPL = 1
+    static constexpr int kPref1 = 1;  // row-groups in flight per wave at UPL = 1 (8192 x 2048: 5.67 us at 2, 5.29 at 1)
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
     static constexpr int kPairBytes = 68;
     struct Data {
@@ -175,7 +175,7 @@ struct GemvQ8_0 {
 // Block A: d @0, qs @2..17; block B: d @18, qs @20..35.
 // ---------------------------------------------------------------------------
 struct GemvQ4_0 {
-    static constexpr int kPref1 = 4;  // row-groups in flight per wave at UPL = 1
+    static constexpr int kPref1 = 1;  // row-groups in flight per wave at UPL = 1 (8192 x 2048: 4.63 us at 4, 4.41 at 1)
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
     static constexpr int kPairBytes = 36;
     struct Data {
@@ -241,7 +241,7 @@ struct GemvQ4_0 {
 // nibble for i < 16), high bit = bit i of qh (ref:src/kernels/dequantize.cu:140-164).
 // ---------------------------------------------------------------------------
 struct GemvQ5_0 {
-    static constexpr int kPref1 = 4;  // row-groups in flight per wave at UPL = 1
+    static constexpr int kPref1 = 1;  // row-groups in flight per wave at UPL = 1 (8192 x 2048: 5.52 us at 4, 5.14 at 1)
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
     static constexpr int kPairBytes = 44;
     struct Data {
@@ -304,7 +304,7 @@ struct GemvQ5_0 {
 // read through dword-aligned windows and funnel-shifted into place.
 // ---------------------------------------------------------------------------
 struct GemvQ6K {
-    static constexpr int kPref1 = 3;  // row-groups in flight per wave at UPL = 1
+    static constexpr int kPref1 = 2;  // row-groups in flight per wave at UPL = 1 (lm_head: 46.0 us at 3, 45.3 at 2, 49.8 at 1)
     // one row group per wave up to the wave budget at UPL = 1, whatever N: the
     // decode is long enough that more, shorter waves win (8192 x 2048: 8.20 -> 6.94 us)
     static constexpr bool kSpread = true;
@@ -391,7 +391,7 @@ struct GemvQ6K {
 // FP16 weights: unit = 64 halves (128 bytes); fma(fpext(half), x, acc).
 // ---------------------------------------------------------------------------
 struct GemvF16 {
-    static constexpr int kPref1 = 2;  // row-groups in flight per wave at UPL = 1
+    static constexpr int kPref1 = 1;  // row-groups in flight per wave at UPL = 1 (8192 x 2048: 9.08 us at 2, 8.38 at 1)
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
     struct Data {
         u32x4 w[8];
