@@ -58,7 +58,7 @@ __device__ __forceinline__ float sum_range(const float (&v)[64], int b, int n) {
 // (ref:src/kernels/dequantize.cu:307-319).
 // ---------------------------------------------------------------------------
 struct GemvQ4K {
-    static constexpr int kPref1 = 4;  // row-groups in flight per wave at UPL = 1
+    static constexpr int kPref1 = 1;  // row-groups in flight per wave at UPL = 1 (8192 x 2048: 4.84 us at 4, 4.55 at 1)
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
     static constexpr int kBlockBytes = 144;
     struct Data {

@@ -1,5 +1,7 @@
 // mfma_skinny.hip -- fused dequant GEMV / skinny GEMM on the matrix cores,
 // C[M,N] = A[M,K] * dequant(B[N,K])^T for 1 <= M <= 16 (decode batch sizes).
+// The ABI sends it 2 <= M <= 16 (the batch-1 GEMV of gemv.hip measured faster at
+// M = 1 for every format, Q4_K included); M = 1 stays supported by the kernel.
 //
 // Q4_K (ref:src/kernels/matmul_quant.cu:309-386 computes the same product on
 // fp32 FMA units).  gfx950 v_mfma_f32_16x16x32_f16 multiplies a 16(m) x 32(k)
@@ -934,7 +936,9 @@ namespace detail {
 
 bool skinny_supported(int fmt, int M, int K, const void* B) {
     if (M < 1 || M > 16 || K % 256 != 0) return false;
-    if (fmt == kFmtQ4_K) return (reinterpret_cast<uintptr_t>(B) & 15u) == 0;  // 16-byte loads of 144-byte blocks
+    // Q4_K from 2 rows (16-byte loads of 144-byte blocks); the batch-1 GEMV measured faster at M = 1
+    // (8192 x 2048 4.79 -> 4.55 us, 2048 x 2048 3.43 -> 2.87, 512 x 2048 3.33 -> 2.72)
+    if (fmt == kFmtQ4_K) return M >= 2 && (reinterpret_cast<uintptr_t>(B) & 15u) == 0;
     // Q6_K: the batch-1 GEMV streams it at HBM rate; 2..16 rows share each decoded block here
     if (fmt == kFmtQ6_K) return M >= 2 && (reinterpret_cast<uintptr_t>(B) & 1u) == 0;
     // the 32-element formats and FP16 likewise from 2 rows; rows of 8-block items stay dword-aligned
