@@ -60,6 +60,7 @@ __device__ __forceinline__ float sum_range(const float (&v)[64], int b, int n) {
 struct GemvQ4K {
     static constexpr int kPref1 = 1;  // row-groups in flight per wave at UPL = 1 (8192 x 2048: 4.84 us at 4, 4.55 at 1)
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
+    static constexpr bool kPairUnits = true;  // two units per lane at K = 2048 for N >= 8192 (8192 x 2048: Q4_K 4.53 -> 4.37 us, Q4_0 4.43 -> 4.23; 16384 x 2048 Q4_K 6.94 -> 6.09)
     static constexpr int kBlockBytes = 144;
     struct Data {
         u32x4 h;       // d, dmin, scales[0..11]
@@ -134,6 +135,7 @@ struct GemvQ4K {
 struct GemvQ8_0 {
     static constexpr int kPref1 = 1;  // row-groups in flight per wave at UPL = 1 (8192 x 2048: 5.67 us at 2, 5.29 at 1)
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
+    static constexpr bool kPairUnits = false;
     static constexpr int kPairBytes = 68;
     struct Data {
         u32x4 w0, w1, w2, w3;
@@ -177,6 +179,7 @@ struct GemvQ8_0 {
 struct GemvQ4_0 {
     static constexpr int kPref1 = 1;  // row-groups in flight per wave at UPL = 1 (8192 x 2048: 4.63 us at 4, 4.41 at 1)
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
+    static constexpr bool kPairUnits = true;  // two units per lane at K = 2048 for N >= 8192 (8192 x 2048: Q4_K 4.53 -> 4.37 us, Q4_0 4.43 -> 4.23; 16384 x 2048 Q4_K 6.94 -> 6.09)
     static constexpr int kPairBytes = 36;
     struct Data {
         u32x4 w0, w1;
@@ -243,6 +246,7 @@ struct GemvQ4_0 {
 struct GemvQ5_0 {
     static constexpr int kPref1 = 1;  // row-groups in flight per wave at UPL = 1 (8192 x 2048: 5.52 us at 4, 5.14 at 1)
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
+    static constexpr bool kPairUnits = false;
     static constexpr int kPairBytes = 44;
     struct Data {
         u32x4 w0, w1;
@@ -308,6 +312,7 @@ struct GemvQ6K {
     // one row group per wave up to the wave budget at UPL = 1, whatever N: the
     // decode is long enough that more, shorter waves win (8192 x 2048: 8.20 -> 6.94 us)
     static constexpr bool kSpread = true;
+    static constexpr bool kPairUnits = false;
     static constexpr int kBlockBytes = 210;
     struct Data {
         uint32_t a[5], b[5], h[5];  // aligned windows of ql lo-run, ql hi-run, qh
@@ -393,6 +398,7 @@ struct GemvQ6K {
 struct GemvF16 {
     static constexpr int kPref1 = 1;  // row-groups in flight per wave at UPL = 1 (8192 x 2048: 9.08 us at 2, 8.38 at 1)
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
+    static constexpr bool kPairUnits = false;
     struct Data {
         u32x4 w[8];
     };
@@ -428,6 +434,7 @@ struct GemvF16 {
 struct GemvF32 {
     static constexpr int kPref1 = 2;  // row-groups in flight per wave at UPL = 1
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
+    static constexpr bool kPairUnits = false;
     struct Data {
         f32x4 w[16];
     };
