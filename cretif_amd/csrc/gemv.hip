@@ -196,7 +196,7 @@ static int launch_gemv_f(const ActIn& x, const void* W, float* y, int N, int K, 
     const int units = K / 64;
     int lpr_log2 = 0;
     while ((1 << lpr_log2) < units && lpr_log2 < 6) ++lpr_log2;
-    // the 4-bit formats on long matrices: 16 lanes per row, two units each (fewer lanes to reduce
+    // Q4_K, Q4_0, Q5_0 on long matrices: 16 lanes per row, two units each (fewer lanes to reduce
     // over, twice the rows per wave iteration)
     if (F::kPairUnits && MR == 1 && units == 32 && N >= 8192) lpr_log2 = 4;
     const int lpr = 1 << lpr_log2;

@@ -246,7 +246,7 @@ struct GemvQ4_0 {
 struct GemvQ5_0 {
     static constexpr int kPref1 = 1;  // row-groups in flight per wave at UPL = 1 (8192 x 2048: 5.52 us at 4, 5.14 at 1)
     static constexpr bool kSpread = false;  // one wave per kPref1 row groups above 2048 groups
-    static constexpr bool kPairUnits = false;
+    static constexpr bool kPairUnits = true;  // 8192 x 2048 5.05 -> 4.99 us, 16384 x 2048 8.14 -> 7.52
     static constexpr int kPairBytes = 44;
     struct Data {
         u32x4 w0, w1;

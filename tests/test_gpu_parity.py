@@ -227,8 +227,8 @@ def test_two_row_gemv(orc, fmt, N, K):
     ref = orc.matmul_quant(fmt, A, Bq, N, K)
     assert normwise_rel_err(got, ref) <= GEMV_TOL
     # each row alone through the batch-1 GEMV gives the same bits, unless the batch-1 GEMV
-    # takes two units per lane there (the 4-bit formats at K = 2048 from 8192 rows)
-    if not (fmt in ("q4_0", "q4_k") and K == 2048 and N >= 8192):
+    # takes two units per lane there (Q4_0, Q5_0, Q4_K at K = 2048 from 8192 rows)
+    if not (fmt in ("q4_0", "q5_0", "q4_k") and K == 2048 and N >= 8192):
         for m in range(2):
             assert np.array_equal(run_matmul(fmt, A[m:m + 1], Bq, N, K), got[m:m + 1])
 
@@ -243,7 +243,7 @@ def test_row_pair_gemv(orc, fmt, M, N, K):
     Bq = weights(fmt, N, K, seed=N + M + K)
     got = run_matmul(fmt, A, Bq, N, K)
     assert normwise_rel_err(got, orc.matmul_quant(fmt, A, Bq, N, K)) <= GEMV_TOL
-    if not (fmt in ("q4_0", "q4_k") and K == 2048 and N >= 8192):
+    if not (fmt in ("q4_0", "q5_0", "q4_k") and K == 2048 and N >= 8192):
         for m in (0, M - 1):
             assert np.array_equal(run_matmul(fmt, A[m:m + 1], Bq, N, K), got[m:m + 1])
 
