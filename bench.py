@@ -11,7 +11,10 @@ replay stream plus device synchronisation.
 
 GB/s counts algorithmic bytes only: N*(K/bs)*block_bytes + 4*M*K + 4*M*N.
 
-    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu] [--no-details]
+    python bench.py [--steps K] [--warmup W] [--samples S] [--workload NAME] [--no-cpu] [--no-details]
+
+A timed sample is exactly K launches (--steps); S samples (>= 5) are taken back to
+back and the median sample gives `value` and `ms_per_step`.
 """
 from __future__ import annotations
 
@@ -40,6 +43,12 @@ PREFILL_WORKLOADS = {
     "q4_k_prefill_down": ("q4_k", 512, 2048, 8192),
 }
 
+# batched decode GEMVs (BASELINE config 5 at M = 16): name -> (fmt, M, N, K)
+SKINNY_WORKLOADS = {
+    "q4_k_gemv_m16": ("q4_k", 16, 8192, 2048),
+    "q4_k_gemv_down_m16": ("q4_k", 16, 2048, 8192),
+}
+
 GEMV_WORKLOADS = {
     # name: (fmt, N, K)
     "q4_k_gemv": ("q4_k", 8192, 2048),
@@ -65,10 +74,54 @@ def algo_bytes(fmt, M, N, K):
     return N * quant.row_bytes(fmt, K) + 4 * M * K + 4 * M * N
 
 
-class GemvRig:
-    """Weights replicated over `copies` device buffers, launches captured in a graph."""
+def rotation_plan(steps, need, max_nodes=20000):
+    """(copies, graphs, continuous): `graphs` graphs of exactly `steps` launches each, graph
+    r using weight copies (r * steps + i) % copies, so that replaying them in turn walks one
+    continuous rotation over >= `need` copies and no launch finds its weights in the
+    Infinity Cache.  Falls back to one graph whose rotation restarts every sample when a
+    continuous plan would need more than max_nodes launches."""
+    import math
 
-    def __init__(self, fmt, N, K, M=1, seed=1, min_bytes=2 * MALL_BYTES, max_copies=64):
+    if steps <= need:
+        copies = -(-need // steps) * steps
+        return copies, copies // steps, True
+    for c in range(need, 2 * need + 1):
+        if steps % c == 0:
+            return c, 1, True
+    graphs = need // math.gcd(need, steps)
+    if graphs * steps <= max_nodes:
+        return need, graphs, True
+    return need, 1, False
+
+
+def time_graphs(graphs, samples, warmup_steps, steps, stream):
+    """ms of each of `samples` consecutive graph replays (graphs taken in turn), after
+    ceil(warmup_steps / steps) untimed replays; HIP events on the replay stream between
+    the replays, which are all enqueued before the one synchronisation."""
+    import torch
+
+    torch.cuda.synchronize()
+    gi = 0
+    for _ in range(max(1, -(-warmup_steps // steps))):
+        graphs[gi % len(graphs)].replay()
+        gi += 1
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(samples + 1)]
+    with torch.cuda.stream(stream):
+        ev[0].record(stream)
+        for i in range(samples):
+            graphs[gi % len(graphs)].replay()
+            gi += 1
+            ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    return [ev[i].elapsed_time(ev[i + 1]) for i in range(samples)]
+
+
+class GemvRig:
+    """Weights replicated over enough device copies that each launch streams from HBM;
+    `steps` launches per captured graph (see rotation_plan)."""
+
+    def __init__(self, fmt, N, K, M=1, seed=1, min_bytes=2 * MALL_BYTES, max_copies=64, steps=None):
         import torch
 
         import cretif_amd as cri
@@ -78,60 +131,55 @@ class GemvRig:
         w = tiled_weights(fmt, N, K, seed=seed) if fmt != "fp32" else \
             quant.randn(N * K, seed=seed).astype(np.float32).view(np.uint8)
         self.wbytes = w.size
-        self.copies = int(max(1, min(max_copies, -(-min_bytes // w.size))))
+        need = int(max(1, min(max_copies, -(-min_bytes // w.size))))
+        self.steps = steps or need
+        self.copies, ngraphs, self.continuous = rotation_plan(self.steps, need)
         base = torch.from_numpy(w).cuda()
         self.W = [base] + [base.clone() for _ in range(self.copies - 1)]
         self.x = torch.from_numpy(quant.randn(M * K, seed=seed + 1).reshape(M, K)).cuda()
         self.y = torch.empty(M, N, device="cuda")
         self.cri = cri
         torch.cuda.synchronize()
-        self.graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
+        self.stream = torch.cuda.Stream()
+
         def run(Wi):
             if fmt == "fp32":
                 cri.matmul_transposed_b(self.x, Wi, self.y, M, N, K)
             else:
                 cri.matmul(fmt, self.x, Wi, self.y, M, N, K)
 
-        with torch.cuda.stream(side):
+        with torch.cuda.stream(self.stream):
             for Wi in self.W:  # eager warm-up on the side stream
                 run(Wi)
-        side.synchronize()
-        with torch.cuda.graph(self.graph, stream=side):
-            for Wi in self.W:
-                run(Wi)
+        self.stream.synchronize()
+        self.graphs = []
+        for r in range(ngraphs):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=self.stream):
+                for i in range(self.steps):
+                    run(self.W[(r * self.steps + i) % self.copies])
+            self.graphs.append(g)
         torch.cuda.synchronize()
 
     def bytes_per_launch(self):
         return algo_bytes(self.fmt, self.M, self.N, self.K)
 
-    def time(self, steps, warmup):
-        """Returns (ms per launch, launches timed)."""
-        import torch
+    def samples(self, samples, warmup):
+        """ms per launch of each sample (one replay = `steps` launches)."""
+        return [t / self.steps for t in time_graphs(self.graphs, samples, warmup, self.steps, self.stream)]
 
-        reps = max(1, -(-steps // self.copies))
-        wreps = max(1, -(-warmup // self.copies))
-        for _ in range(wreps):
-            self.graph.replay()
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(reps):
-            self.graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        launches = reps * self.copies
-        return start.elapsed_time(end) / launches, launches
+    def time(self, samples=9, warmup=64):
+        """Median ms per launch over `samples` samples."""
+        return float(np.median(self.samples(samples, warmup)))
 
     def free(self):
         self.W = None
-        self.graph = None
+        self.graphs = None
 
 
 class StreamRig:
     """The achievable streaming-read line: cri_stream_read over `copies` buffers of n_bytes (rotated
-    over >= 2x the Infinity Cache, as the GEMVs), launches captured in a graph, timed as GemvRig."""
+    over >= 2x the Infinity Cache, as the GEMVs), one rotation per captured graph."""
 
     def __init__(self, n_bytes, min_bytes=2 * MALL_BYTES, max_copies=64):
         import torch
@@ -139,26 +187,28 @@ class StreamRig:
         import cretif_amd as cri
 
         self.n_bytes = n_bytes
-        self.copies = int(max(1, min(max_copies, -(-min_bytes // n_bytes))))
+        self.copies = self.steps = int(max(1, min(max_copies, -(-min_bytes // n_bytes))))
         base = torch.zeros(n_bytes, dtype=torch.uint8, device="cuda")
         self.W = [base] + [base.clone() for _ in range(self.copies - 1)]
         self.sink = torch.zeros(1, dtype=torch.int32, device="cuda")
-        side = torch.cuda.Stream()
-        with torch.cuda.stream(side):
+        self.stream = torch.cuda.Stream()
+        with torch.cuda.stream(self.stream):
             for Wi in self.W:
                 cri.stream_read(Wi, n_bytes, self.sink)
-        side.synchronize()
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph, stream=side):
+        self.stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
             for Wi in self.W:
                 cri.stream_read(Wi, n_bytes, self.sink)
+        self.graphs = [g]
         torch.cuda.synchronize()
 
+    samples = GemvRig.samples
     time = GemvRig.time
 
     def free(self):
         self.W = None
-        self.graph = None
+        self.graphs = None
 
 
 def tiled_weights(fmt, N, K, seed, max_rows=8192):
@@ -175,161 +225,93 @@ def tiled_weights(fmt, N, K, seed, max_rows=8192):
     return np.ascontiguousarray(np.tile(base, (N // rows, 1))).ravel()
 
 
+def hip_memcpy(dst, src, nbytes, kind):
+    """hipMemcpy through the HIP runtime torch loaded (kind 1: host to device, 3: device to device)."""
+    import ctypes
+
+    path = next(ln.split()[-1] for ln in open("/proc/self/maps") if "libamdhip64" in ln)
+    h = ctypes.CDLL(path)
+    h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    if h.hipMemcpy(dst, src, nbytes, kind) != 0:
+        raise RuntimeError("hipMemcpy failed")
+
+
 class DecodeStepRig:
-    """Synthetic Llama-3.2-1B-shaped decode step for M
-    tokens: 16 layers of Q4_K q (2048x2048), k and v (512x2048), o (2048x2048),
-    gate and up (8192x2048), down (2048x8192) plus the GQA QK^T and PV products
-    over an fp32 KV cache of T = 2048 positions (32 query heads over 8 KV heads,
-    head_dim 64), then the Q6_K lm_head (128256x2048).  The step is the path's
-    own kernels only (norms, RoPE, softmax and SiLU are not on the path); every
-    layer has its own weight and cache buffers, and the whole step is captured
-    as one HIP graph and replayed.  As inference engines do, the q/k/v weights
-    of a layer are stored as one [3072, 2048] matrix and gate/up as one
-    [16384, 2048] matrix, so a layer is 4 weight launches (same bytes, fewer
-    launches).  Buffers are reused between layers: the timing covers the
-    products at their real shapes; the values are not chained semantically.
-    attention='fused' (M = 1) replaces the two GQA products by the fused decode
-    attention (softmax included) over a [T, 8, 64] cache, in its split form
-    with a preallocated workspace, as the reference's decode path calls
-    fused_decode_attention (ref:src/model.cu:928-943)."""
+    """BASELINE config 5 through the product decode step (cri_decoder_*, C++
+    cuinfer::DecodeStep): a synthetic Llama-3.2-1B -- 16 layers of Q4_K q (2048x2048),
+    k and v (512x2048), o (2048x2048), gate and up (8192x2048), down (2048x8192), RMSNorm
+    weights ~ 1 + N(0, 0.1), a Q8_0 token table and a Q6_K 128256x2048 LM head --
+    with an fp32 KV cache ~ N(0, 1) filled to 2048 positions.  One step is M tokens:
+    embedding, per layer RMSNorm + q/k/v (one stacked matrix), RoPE + cache append,
+    attention over the cache (32 query heads over 8 KV heads, head_dim 64), o,
+    residual + RMSNorm + gate/up (one stacked matrix), SiLU * up + down, then the final
+    RMSNorm, the LM head and the greedy token of each row, values chained throughout;
+    captured once as a HIP graph.  Each timed replay runs at position 2048 - M (the last
+    row sees all 2048 positions); the position is reset by a kernel outside the timed
+    events.  Every layer has its own weight copy (the same bytes: weights are N(0, 0.02)
+    rows quantized once and tiled)."""
 
     LAYERS, D, H, HKV, HD, FF, VOCAB, T = 16, 2048, 32, 8, 64, 8192, 128256, 2048
 
-    def __init__(self, M, seed=1100, attention="gqa", elementwise="none"):
+    def __init__(self, M, seed=1100):
         import torch
 
         import cretif_amd as cri
 
-        if attention not in ("gqa", "fused") or (attention == "fused" and M != 1):
-            raise ValueError("attention is 'gqa', or 'fused' for M = 1 (one query token)")
-        if elementwise not in ("none", "separate", "fused") or (elementwise == "separate" and M != 1):
-            raise ValueError("elementwise is 'none', 'fused', or 'separate' for M = 1")
-        self.M, self.attention, self.elementwise = M, attention, elementwise
-        D, FF, T, H, HKV, HD = self.D, self.FF, self.T, self.H, self.HKV, self.HD
-        shapes = {"qkv": (D + 2 * HKV * HD, D), "o": (D, D), "gateup": (2 * FF, D), "down": (D, FF)}
-        base = {name: torch.from_numpy(tiled_weights("q4_k", n, k, seed + i)).cuda()
-                for i, (name, (n, k)) in enumerate(shapes.items())}
-        self.layers = [{name: base[name].clone() for name in shapes} for _ in range(self.LAYERS)]
-        del base
-        self.lm_head = torch.from_numpy(tiled_weights("q6_k", self.VOCAB, D, seed + 99)).cuda()
+        D, FF, H, HKV, HD, V, T = self.D, self.FF, self.H, self.HKV, self.HD, self.VOCAB, self.T
+        self.M = M
+        shapes = {"q": (H * HD, D), "k": (HKV * HD, D), "v": (HKV * HD, D), "o": (D, H * HD), "gate": (FF, D),
+                  "up": (FF, D), "down": (D, FF)}
+        w = {n: ("q4_k", tiled_weights("q4_k", r, c, seed + i)) for i, (n, (r, c)) in enumerate(shapes.items())}
+        rng = np.random.default_rng(seed)
+        self.dec = dec = cri.Decoder(self.LAYERS, D, H, HKV, HD, FF, V, T, max_batch=16, rope_theta=500000.0)
+        for li in range(self.LAYERS):
+            dec.set_layer(li, (1 + 0.1 * rng.standard_normal(D)).astype(np.float32),
+                          (1 + 0.1 * rng.standard_normal(D)).astype(np.float32), **w)
+        dec.set_embedding("q8_0", tiled_weights("q8_0", V, D, seed + 98))
+        dec.set_output((1 + 0.1 * rng.standard_normal(D)).astype(np.float32),
+                       ("q6_k", tiled_weights("q6_k", V, D, seed + 99)))
         g = torch.Generator(device="cuda").manual_seed(3000)
-        if attention == "gqa":
-            # batched_matmul_gqa operands: K^T [Hkv, HD, T] and V [Hkv, T, HD] per layer
-            self.kT = [torch.randn(HKV, HD, T, device="cuda", generator=g) for _ in range(self.LAYERS)]
-            self.vc = [torch.randn(HKV, T, HD, device="cuda", generator=g) for _ in range(self.LAYERS)]
-        else:
-            # fused decode attention reads the cache layout [T, Hkv, HD] directly
-            self.kT = [torch.randn(T, HKV, HD, device="cuda", generator=g) for _ in range(self.LAYERS)]
-            self.vc = [torch.randn(T, HKV, HD, device="cuda", generator=g) for _ in range(self.LAYERS)]
-            self.ws = torch.empty(cri.decode_attention_workspace_size(H, HKV, HD, T) // 4, device="cuda")
-        self.x = torch.randn(M, D, device="cuda", generator=g)
-        self.qkv = torch.empty(M, D + 2 * HKV * HD, device="cuda")
-        self.scores = torch.empty(H, M, T, device="cuda")
-        self.ctx = torch.empty(H, M, HD, device="cuda")
-        self.h = torch.empty(M, D, device="cuda")
-        self.ff = torch.empty(M, 2 * FF, device="cuda")
-        # residual stream and norms (elementwise != "none"): two hidden buffers (the fused
-        # form writes hidden + residual to the other one), RMSNorm weights ~ 1 + N(0, 0.1)
-        self.hid = [torch.randn(M, D, device="cuda", generator=g) for _ in range(2)]
-        self.attn_out = torch.empty(M, D, device="cuda")
-        self.ffn_out = torch.empty(M, D, device="cuda")
-        self.normed = torch.empty(M, D, device="cuda")
-        self.act = torch.empty(M, FF, device="cuda")
-        self.norm_w = [1.0 + 0.1 * torch.randn(D, device="cuda", generator=g) for _ in range(2 * self.LAYERS + 1)]
-        self.logits = torch.empty(M, self.VOCAB, device="cuda")
-        self.weight_bytes = sum(t.numel() for L in self.layers for t in L.values()) + self.lm_head.numel()
-        self.kv_bytes = sum(t.numel() * 4 for t in self.kT) + sum(t.numel() * 4 for t in self.vc)
-        self.cri = cri
-        side = torch.cuda.Stream()
-        with torch.cuda.stream(side):
-            self.step()
-        side.synchronize()
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph, stream=side):
-            self.step()
+        for li in range(self.LAYERS):
+            ka, va = dec.kv_cache(li)
+            for addr in (ka, va):
+                t = torch.randn(T * HKV * HD, device="cuda", generator=g)
+                torch.cuda.synchronize()
+                hip_memcpy(addr, t.data_ptr(), t.numel() * 4, 3)
+        self.weight_bytes = dec.weight_bytes
+        self.kv_bytes = 2 * self.LAYERS * T * HKV * HD * 4
+        self.ids = torch.from_numpy(rng.integers(0, V, M).astype(np.int32)).cuda()
+        self.logits = torch.empty(M, V, device="cuda")
+        self.next_ids = torch.empty(M, dtype=torch.int32, device="cuda")
+        self.stream = torch.cuda.Stream()
+        self.pos0 = T - M
         torch.cuda.synchronize()
+        dec.capture(self.ids, M, self.logits, self.next_ids, stream=self.stream)
 
-    def step(self):
-        if self.elementwise != "none":
-            return self.step_with_norms()
-        cri, M, D, FF, HKV, HD = self.cri, self.M, self.D, self.FF, self.HKV, self.HD
-        x = self.x
-        for li, L in enumerate(self.layers):
-            cri.matmul("q4_k", x, L["qkv"], self.qkv, M, D + 2 * HKV * HD, D)
-            # the first 32*M*64 values of the qkv output read as [32, M, 64] queries; 'fused' is
-            # softmax(q K^T / 8) V in one call (its split form)
-            self.attend(li)
-            cri.matmul("q4_k", self.ctx, L["o"], self.h, M, D, D)
-            cri.matmul("q4_k", self.h, L["gateup"], self.ff, M, 2 * FF, D)
-            # the first M*8192 values of the gate/up output read as the [M, 8192] down input
-            cri.matmul("q4_k", self.ff, L["down"], self.h, M, D, FF)
-            x = self.h
-        cri.matmul("q6_k", x, self.lm_head, self.logits, M, self.VOCAB, D)
-
-    def attend(self, li):
-        cri, M, H, HKV, HD, T = self.cri, self.M, self.H, self.HKV, self.HD, self.T
-        if self.attention == "gqa":
-            cri.batched_matmul_gqa(self.qkv, self.kT[li], self.scores, H, HKV, M, T, HD)
-            cri.batched_matmul_gqa(self.scores, self.vc[li], self.ctx, H, HKV, M, HD, T)
-        else:
-            cri.fused_decode_attention_ws(self.qkv, self.kT[li], self.vc[li], self.ctx, H, HKV, HD, T, 0.125, self.ws)
-
-    def step_with_norms(self):
-        """The layer with its elementwise neighbours, as the reference's decode loop runs it
-        (ref:src/model.cu:894-1018): h += ffn_out; n = RMSNorm(h); q/k/v; attention; o;
-        h += attn_out; n = RMSNorm(h); gate/up; silu(gate) * up; down; and after the last
-        layer h += ffn_out; n = RMSNorm(h); lm_head.  'separate' launches rmsnorm_residual
-        and silu_mul; 'fused' folds them into the next matmul's activation staging."""
-        cri, M, D, FF, HKV, HD = self.cri, self.M, self.D, self.FF, self.HKV, self.HD
-        fused = self.elementwise == "fused"
-        cur, res = 0, None  # hidden buffer in use; residual still to be added (none before layer 0)
-        eps = 1e-5
-
-        def norm_then(w, Wq, out, N, fmt="q4_k"):
-            nonlocal cur
-            if fused:
-                cri.matmul_rmsnorm(fmt, self.hid[cur], res, w, self.hid[1 - cur], Wq, out, M, N, D, eps)
-                cur = 1 - cur
-            else:
-                cri.rmsnorm_residual(self.hid[cur], res, w, self.hid[cur], self.normed, M, D, eps)
-                cri.matmul(fmt, self.normed, Wq, out, M, N, D)
-
-        for li, L in enumerate(self.layers):
-            norm_then(self.norm_w[2 * li], L["qkv"], self.qkv, D + 2 * HKV * HD)
-            self.attend(li)
-            cri.matmul("q4_k", self.ctx, L["o"], self.attn_out, M, D, D)
-            res = self.attn_out
-            norm_then(self.norm_w[2 * li + 1], L["gateup"], self.ff, 2 * FF)
-            if fused:
-                cri.matmul_swiglu("q4_k", self.ff, self.ff.data_ptr() + 4 * FF, 2 * FF, L["down"], self.ffn_out, M,
-                                  D, FF)
-            else:
-                cri.silu_mul(self.ff, self.ff.data_ptr() + 4 * FF, self.act, M * FF)  # M = 1
-                cri.matmul("q4_k", self.act, L["down"], self.ffn_out, M, D, FF)
-            res = self.ffn_out
-        if fused:
-            cri.matmul_rmsnorm("q6_k", self.hid[cur], res, self.norm_w[-1], None, self.lm_head, self.logits, M,
-                               self.VOCAB, D, eps)
-        else:
-            norm_then(self.norm_w[-1], self.lm_head, self.logits, self.VOCAB, fmt="q6_k")
-
-    def time(self, reps=20, warmup=3):
+    def samples(self, samples=9, warmup=3):
+        """ms of each of `samples` replays at position 2048 - M."""
         import torch
 
+        s = self.stream
         for _ in range(warmup):
-            self.graph.replay()
+            self.dec.set_position(self.pos0, stream=s)
+            self.dec.replay(stream=s)
         torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(reps):
-            self.graph.replay()
-        end.record()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(samples)]
+        for a, b in ev:
+            self.dec.set_position(self.pos0, stream=s)
+            a.record(s)
+            self.dec.replay(stream=s)
+            b.record(s)
         torch.cuda.synchronize()
-        return start.elapsed_time(end) / reps
+        return [a.elapsed_time(b) for a, b in ev]
+
+    def time(self, samples=9, warmup=3):
+        return float(np.median(self.samples(samples, warmup)))
 
     def free(self):
-        self.layers = self.lm_head = self.kT = self.vc = self.graph = None
+        self.dec.close()
+        self.dec = None
 
 
 class AttentionRig:
@@ -364,36 +346,25 @@ class AttentionRig:
                 else:
                     cri.fused_decode_attention_ws(self.q, k, v, self.out, H, HKV, HD, T, 0.125, self.ws)
 
-        side = torch.cuda.Stream()
-        with torch.cuda.stream(side):
+        self.stream = torch.cuda.Stream()
+        with torch.cuda.stream(self.stream):
             run()
-        side.synchronize()
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph, stream=side):
+        self.stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
             run()
+        self.graphs, self.steps = [g], self.copies
         torch.cuda.synchronize()
 
     def bytes_per_call(self):
         # algorithmic: q, out and every K and V value of the T positions, once
         return 4 * (2 * self.H * self.HD + 2 * self.T * self.HKV * self.HD)
 
-    def time(self, reps=20):
-        """ms per call."""
-        import torch
-
-        self.graph.replay()
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(reps):
-            self.graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / (reps * self.copies)
+    samples = GemvRig.samples
+    time = GemvRig.time
 
     def free(self):
-        self.K = self.V = self.graph = None
+        self.K = self.V = self.graphs = None
 
 
 class GqaRig:
@@ -424,22 +395,24 @@ class GqaRig:
             for a_, b_ in zip(self.A, self.B):
                 cri.batched_matmul_gqa(a_, b_, self.C, H, HKV, M, N, K)
 
-        side = torch.cuda.Stream()
-        with torch.cuda.stream(side):
+        self.stream = torch.cuda.Stream()
+        with torch.cuda.stream(self.stream):
             run()
-        side.synchronize()
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph, stream=side):
+        self.stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
             run()
+        self.graphs, self.steps = [g], self.copies
         torch.cuda.synchronize()
 
     def bytes_per_call(self):
         return 4 * (self.H * self.M * self.K + self.HKV * self.K * self.N + self.H * self.M * self.N)
 
-    time = AttentionRig.time
+    samples = GemvRig.samples
+    time = GemvRig.time
 
     def free(self):
-        self.A = self.B = self.graph = None
+        self.A = self.B = self.graphs = None
 
 
 def measured_traffic(workload):
@@ -503,19 +476,18 @@ def cpu_model():
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=12800)
-    ap.add_argument("--warmup", type=int, default=640)
+    ap.add_argument("--steps", type=int, default=400, help="launches per timed sample of the headline GEMV")
+    ap.add_argument("--warmup", type=int, default=400, help="untimed launches before the samples")
+    ap.add_argument("--samples", type=int, default=25, help="timed samples (>= 5); the median is reported")
     ap.add_argument("--workload", default="q4_k_gemv", choices=sorted(GEMV_WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-details", action="store_true", help="skip the per-format side measurements")
     ap.add_argument("--prefill", default=None, choices=sorted(PREFILL_WORKLOADS),
                     help="only time one prefill GEMM workload (for profiling) and print its figures")
+    ap.add_argument("--gemv", default=None, choices=sorted(GEMV_WORKLOADS) + sorted(SKINNY_WORKLOADS),
+                    help="only time one GEMV workload (for profiling) and print its figures")
     ap.add_argument("--decode-step", type=int, default=None, metavar="M",
-                    help="only time the synthetic decode step for M tokens (for profiling)")
-    ap.add_argument("--step-attention", default="gqa", choices=["gqa", "fused"],
-                    help="attention of --decode-step: the two GQA products (default) or the fused kernel (M = 1)")
-    ap.add_argument("--step-elementwise", default="none", choices=["none", "separate", "fused"],
-                    help="--decode-step with the layer's RMSNorm / SiLU work: separate launches or fused prologues")
+                    help="only time the synthetic Llama-3.2-1B decode step for M tokens (for profiling)")
     ap.add_argument("--attention", default=None, choices=["plain", "ws"],
                     help="only time the fused decode attention at 2048 positions (for profiling)")
     ap.add_argument("--launch-floor", action="store_true",
@@ -524,6 +496,7 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run ten 64 MiB device copies (known bytes, for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
+    samples = max(5, args.samples)
 
     if args.copy_calibration:
         import torch
@@ -548,81 +521,89 @@ def main():
     cri.lib()
     if args.launch_floor:
         r = GemvRig("q4_k", 16, 256, M=1, max_copies=57)
-        ms, n = r.time(args.steps, args.warmup)
-        print(json.dumps({"workload": "launch_floor q4_k 16x256 M=1", "launches": n, "copies": r.copies,
-                          "us_per_launch": round(ms * 1e3, 3)}))
+        ms = r.time(samples, args.warmup)
+        print(json.dumps({"workload": "launch_floor q4_k 16x256 M=1", "launches_per_sample": r.steps,
+                          "samples": samples, "us_per_launch": round(ms * 1e3, 3)}))
         return
     if args.attention:
         r = AttentionRig(args.attention)
-        ms_call = r.time(reps=max(3, args.steps // r.copies))
-        print(json.dumps({"workload": "decode_attention_" + args.attention, "T": r.T, "calls": r.copies,
+        ms_call = r.time(samples)
+        print(json.dumps({"workload": "decode_attention_" + args.attention, "T": r.T, "calls_per_sample": r.copies,
                           "us": round(ms_call * 1e3, 3),
                           "GB/s": round(r.bytes_per_call() / (ms_call * 1e-3) / 1e9, 1)}))
         return
     if args.decode_step:
-        r = DecodeStepRig(args.decode_step, attention=args.step_attention, elementwise=args.step_elementwise)
-        ms_step = r.time(reps=max(3, args.steps // 1000))
-        print(json.dumps({"workload": "decode_step", "M": args.decode_step, "attention": args.step_attention,
-                          "elementwise": args.step_elementwise,
-                          "ms_per_step": round(ms_step, 4),
+        r = DecodeStepRig(args.decode_step)
+        ms_step = r.time(samples)
+        print(json.dumps({"workload": "decode_step", "M": args.decode_step, "ms_per_step": round(ms_step, 4),
                           "tokens/s": round(args.decode_step / (ms_step * 1e-3), 1)}))
         return
     if args.prefill:
         f, m_, n, k = PREFILL_WORKLOADS[args.prefill]
         r = GemvRig(f, n, k, M=m_, max_copies=16)
-        m, launches = r.time(max(args.steps // 100, 2 * r.copies), 16)
-        print(json.dumps({"workload": args.prefill, "M": m_, "N": n, "K": k, "launches": launches,
+        m = r.time(samples, 16)
+        print(json.dumps({"workload": args.prefill, "M": m_, "N": n, "K": k, "launches_per_sample": r.steps,
                           "us": round(m * 1e3, 3), "TFLOP/s": round(2.0 * m_ * n * k / (m * 1e-3) / 1e12, 1)}))
         return
+    if args.gemv:
+        if args.gemv in SKINNY_WORKLOADS:
+            f, m_, n, k = SKINNY_WORKLOADS[args.gemv]
+        else:
+            (f, n, k), m_ = GEMV_WORKLOADS[args.gemv], 1
+        r = GemvRig(f, n, k, M=m_)
+        m = r.time(samples, 64)
+        print(json.dumps({"workload": args.gemv, "M": m_, "N": n, "K": k, "launches_per_sample": r.steps,
+                          "us": round(m * 1e3, 3), "GB/s": round(r.bytes_per_launch() / (m * 1e-3) / 1e9, 1)}))
+        return
     fmt, N, K = GEMV_WORKLOADS[args.workload]
-    rig = GemvRig(fmt, N, K)
-    ms, launches = rig.time(args.steps, args.warmup)
+    rig = GemvRig(fmt, N, K, steps=max(1, args.steps))
+    per_launch = rig.samples(samples, args.warmup)
+    ms = float(np.median(per_launch))
     bpl = rig.bytes_per_launch()
     gbs = bpl / (ms * 1e-3) / 1e9
-    copies = rig.copies
+    copies, graphs, continuous = rig.copies, len(rig.graphs), rig.continuous
     rig.free()
     torch.cuda.empty_cache()
 
     details = {}
     if not args.no_details:
+        def gemv_line(r, m):
+            return {"GB/s": round(r.bytes_per_launch() / (m * 1e-3) / 1e9, 1), "us": round(m * 1e3, 3),
+                    "copies": r.copies}
+
         # achievable line: a bare 16-byte streaming read of the headline's weight bytes and of the
         # Q6_K lm_head's (one launch each, same rig)
         for name, nb in (("stream_read_9.4MB", 9437184), ("stream_read_215MB", 215470080)):
             r = StreamRig(nb)
-            m, _ = r.time(max(640, 4 * r.copies), 64)
+            m = r.time(9, 64)
             details[name] = {"GB/s": round(nb / (m * 1e-3) / 1e9, 1), "us": round(m * 1e3, 3), "copies": r.copies}
             r.free()
             torch.cuda.empty_cache()
         for name, (f, n, k) in GEMV_WORKLOADS.items():
             if name == args.workload:
                 continue
-            r = GemvRig(f, n, k, max_copies=64)
-            m, _ = r.time(max(640, 4 * r.copies), 64)
-            details[name] = {"GB/s": round(r.bytes_per_launch() / (m * 1e-3) / 1e9, 1), "us": round(m * 1e3, 3),
-                             "copies": r.copies}
+            r = GemvRig(f, n, k)
+            details[name] = gemv_line(r, r.time(9, 64))
             r.free()
             torch.cuda.empty_cache()
         # batched decode (BASELINE config 5 at M = 16): reported against the HBM and the fp16 MFMA roofs
-        for name, (f, m_, n, k) in (("q4_k_gemv_m16", ("q4_k", 16, 8192, 2048)),
-                                    ("q4_k_gemv_down_m16", ("q4_k", 16, 2048, 8192))):
-            r = GemvRig(f, n, k, M=m_, max_copies=64)
-            m, _ = r.time(max(640, 4 * r.copies), 64)
-            details[name] = {"GB/s": round(r.bytes_per_launch() / (m * 1e-3) / 1e9, 1),
-                             "TFLOP/s": round(2.0 * m_ * n * k / (m * 1e-3) / 1e12, 2), "us": round(m * 1e3, 3),
-                             "M": m_, "copies": r.copies}
+        for name, (f, m_, n, k) in SKINNY_WORKLOADS.items():
+            r = GemvRig(f, n, k, M=m_)
+            m = r.time(9, 64)
+            details[name] = dict(gemv_line(r, m), M=m_, **{"TFLOP/s": round(2.0 * m_ * n * k / (m * 1e-3) / 1e12, 2)})
             r.free()
             torch.cuda.empty_cache()
         for name, (f, m_, n, k) in PREFILL_WORKLOADS.items():
             r = GemvRig(f, n, k, M=m_, max_copies=16)
-            m, _ = r.time(max(64, 2 * r.copies), 16)
-            details[name] = {"TFLOP/s": round(2.0 * m_ * n * k / (m * 1e-3) / 1e12, 1), "us": round(m * 1e3, 3),
-                             "M": m_, "copies": r.copies, "fraction_of_fp16_mfma_peak": round(
-                                 2.0 * m_ * n * k / (m * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4)}
+            m = r.time(9, 16)
+            tf = 2.0 * m_ * n * k / (m * 1e-3) / 1e12
+            details[name] = {"TFLOP/s": round(tf, 1), "us": round(m * 1e3, 3), "M": m_, "copies": r.copies,
+                             "fraction_of_fp16_mfma_peak": round(tf / FP16_MFMA_PEAK_TFLOPS, 4)}
             r.free()
             torch.cuda.empty_cache()
         for form in ("plain", "ws"):
             r = AttentionRig(form)
-            ms_call = r.time()
+            ms_call = r.time(9)
             details["decode_attention_%s_T2048" % form] = {
                 "us": round(ms_call * 1e3, 3), "GB/s": round(r.bytes_per_call() / (ms_call * 1e-3) / 1e9, 1),
                 "copies": r.copies}
@@ -631,22 +612,20 @@ def main():
         for product in ("qk", "pv"):
             for m_ in (1, 16):
                 r = GqaRig(product, m_)
-                ms_call = r.time()
+                ms_call = r.time(9)
                 details["gqa_%s_m%d_T2048" % (product, m_)] = {
                     "us": round(ms_call * 1e3, 3), "GB/s": round(r.bytes_per_call() / (ms_call * 1e-3) / 1e9, 1),
                     "copies": r.copies}
                 r.free()
                 torch.cuda.empty_cache()
-        for m_, attn, ew in ((1, "gqa", "none"), (16, "gqa", "none"), (1, "fused", "none"), (1, "fused", "separate"),
-                             (1, "fused", "fused"), (16, "gqa", "fused")):
-            r = DecodeStepRig(m_, attention=attn, elementwise=ew)
-            ms_step = r.time()
-            key = "decode_step_m%d" % m_ + ("_fused_attention" if attn == "fused" else "") + (
-                "" if ew == "none" else "_norms_" + ew)
-            details[key] = {
+        for m_ in (1, 16):
+            r = DecodeStepRig(m_)
+            ms_step = r.time(9)
+            details["decode_step_m%d" % m_] = {
                 "tokens/s": round(m_ / (ms_step * 1e-3), 1), "ms_per_step": round(ms_step, 4),
                 "weight_GB/s": round(r.weight_bytes / (ms_step * 1e-3) / 1e9, 1),
-                "weight+kv_GB/s": round((r.weight_bytes + r.kv_bytes) / (ms_step * 1e-3) / 1e9, 1)}
+                "weight+kv_GB/s": round((r.weight_bytes + r.kv_bytes) / (ms_step * 1e-3) / 1e9, 1),
+                "timing": "median of 9 replays of the captured cri_decoder step at position %d" % r.pos0}
             r.free()
             torch.cuda.empty_cache()
 
@@ -655,7 +634,7 @@ def main():
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": launches,
+        "steps": rig.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 6),
         "higher_is_better": True,
@@ -665,7 +644,13 @@ def main():
         "data": "synthetic: w ~ N(0, 0.02) quantised to %s, x ~ N(0, 1)" % fmt,
         "config": {"workload": "%s decode GEMV M=1" % fmt.upper(), "N": N, "K": K, "M": 1,
                    "weight_copies": copies, "rotation_bytes": copies * (bpl - 4 * K - 4 * N),
-                   "timing": "HIP graph of %d launches replayed; hipEvents on the replay stream" % copies},
+                   "samples": samples,
+                   "us_per_launch_min_median_max": [round(min(per_launch) * 1e3, 3), round(ms * 1e3, 3),
+                                                    round(max(per_launch) * 1e3, 3)],
+                   "timing": "%d samples of %d launches (%d captured graph%s replayed in turn%s); hipEvents on the "
+                             "replay stream between the samples; value from the median sample" % (
+                                 samples, rig.steps, graphs, "s" if graphs > 1 else "",
+                                 "" if continuous else "; the rotation restarts every sample")},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload)},
     }

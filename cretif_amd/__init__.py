@@ -47,6 +47,7 @@ __all__ = [
     "embedding_rows",
     "stream_read",
     "GGUFFile",
+    "Decoder",
     "FORMAT_IDS",
     "ABI_SYMBOLS",
 ]
@@ -99,6 +100,18 @@ ABI_SYMBOLS = (
         "cri_gguf_model_params",
         "cri_gguf_upload",
         "cri_embedding_rows",
+        "cri_decoder_create",
+        "cri_decoder_destroy",
+        "cri_decoder_set_layer",
+        "cri_decoder_set_embedding",
+        "cri_decoder_set_output",
+        "cri_decoder_forward",
+        "cri_decoder_capture",
+        "cri_decoder_replay",
+        "cri_decoder_set_position",
+        "cri_decoder_position",
+        "cri_decoder_kv_cache",
+        "cri_decoder_weight_bytes",
         "cri_stream_read",
         "cri_last_error_string",
         "cri_block_bytes",
@@ -141,6 +154,20 @@ class _GGUFModel(ctypes.Structure):
         ("tie_word_embeddings", ctypes.c_int),
         ("missing", ctypes.c_uint),
     ]
+
+
+class _DecoderConfig(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_int) for f in ("n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "ffn_dim",
+                                            "vocab_size", "max_seq_len", "max_batch")] + [
+        ("rms_norm_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+
+_LAYER_MATS = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+class _DecoderLayer(ctypes.Structure):
+    _fields_ = [("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p)] + [
+        (n + "_format", ctypes.c_int) for n in _LAYER_MATS] + [(n, ctypes.c_void_p) for n in _LAYER_MATS]
 
 
 def lib():
@@ -217,6 +244,29 @@ def lib():
     L.cri_gguf_model_params.restype = i32
     L.cri_gguf_upload.argtypes = [vp, i32, vp, ll, vp]
     L.cri_gguf_upload.restype = i32
+    L.cri_decoder_create.argtypes = [ctypes.POINTER(_DecoderConfig), ctypes.POINTER(vp)]
+    L.cri_decoder_create.restype = i32
+    L.cri_decoder_destroy.argtypes = [vp]
+    L.cri_decoder_destroy.restype = None
+    L.cri_decoder_set_layer.argtypes = [vp, i32, ctypes.POINTER(_DecoderLayer)]
+    L.cri_decoder_set_layer.restype = i32
+    L.cri_decoder_set_embedding.argtypes = [vp, i32, vp]
+    L.cri_decoder_set_embedding.restype = i32
+    L.cri_decoder_set_output.argtypes = [vp, vp, i32, vp]
+    L.cri_decoder_set_output.restype = i32
+    for n in ("cri_decoder_forward", "cri_decoder_capture"):
+        getattr(L, n).argtypes = [vp, vp, i32, vp, vp, vp]
+        getattr(L, n).restype = i32
+    L.cri_decoder_replay.argtypes = [vp, vp]
+    L.cri_decoder_replay.restype = i32
+    L.cri_decoder_set_position.argtypes = [vp, i32, vp]
+    L.cri_decoder_set_position.restype = i32
+    L.cri_decoder_position.argtypes = [vp]
+    L.cri_decoder_position.restype = i32
+    L.cri_decoder_kv_cache.argtypes = [vp, i32, ctypes.POINTER(vp), ctypes.POINTER(vp)]
+    L.cri_decoder_kv_cache.restype = i32
+    L.cri_decoder_weight_bytes.argtypes = [vp]
+    L.cri_decoder_weight_bytes.restype = ll
     L.cri_last_error_string.argtypes = []
     L.cri_last_error_string.restype = ctypes.c_char_p
     L.cri_block_bytes.argtypes = [i32]
@@ -536,3 +586,94 @@ class GGUFFile:
         if dst_bytes is None:
             dst_bytes = dst.numel() * dst.element_size()
         _check(lib().cri_gguf_upload(self._h, index, _ptr(dst), int(dst_bytes), _stream(stream)))
+
+
+def _host_or_device_ptr(x):
+    """Address of a host numpy array (C-contiguous) or of a device tensor / int address."""
+    try:
+        import numpy as np
+    except ImportError:  # pragma: no cover
+        np = None
+    if np is not None and isinstance(x, np.ndarray):
+        if not x.flags["C_CONTIGUOUS"]:
+            raise ValueError("host arrays must be C-contiguous")
+        return x.ctypes.data
+    return _ptr(x)
+
+
+_FMT_OR_FP32 = dict(FORMAT_IDS, fp32=6)
+
+
+class Decoder:
+    """The decode step (cri_decoder_*, C++ cuinfer::DecodeStep): the reference's quantized
+    forward pass (ref:src/model.cu:831-1039) over buffers allocated at construction.
+    Weights are copied in from host numpy arrays or device tensors; forward / replay run
+    M tokens at the current position and advance it."""
+
+    def __init__(self, n_layers, dim, n_heads, n_kv_heads, head_dim, ffn_dim, vocab_size, max_seq_len,
+                 max_batch=16, rms_norm_eps=1e-5, rope_theta=10000.0):
+        c = _DecoderConfig(n_layers, dim, n_heads, n_kv_heads, head_dim, ffn_dim, vocab_size, max_seq_len, max_batch,
+                           rms_norm_eps, rope_theta)
+        h = ctypes.c_void_p()
+        _check(lib().cri_decoder_create(ctypes.byref(c), ctypes.byref(h)))
+        self._h = h
+        self.config = {f: getattr(c, f) for f, _ in _DecoderConfig._fields_}
+        self._keep = []  # host arrays stay alive until their copies are done (copies are synchronous)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().cri_decoder_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_layer(self, layer, attn_norm, ffn_norm, **mats):
+        """mats: q, k, v, o, gate, up, down, each (fmt, data) with data [N, K] GGUF blocks."""
+        w = _DecoderLayer()
+        w.attn_norm = _host_or_device_ptr(attn_norm)
+        w.ffn_norm = _host_or_device_ptr(ffn_norm)
+        for n in _LAYER_MATS:
+            fmt, data = mats[n]
+            setattr(w, n + "_format", FORMAT_IDS[fmt])
+            setattr(w, n, _host_or_device_ptr(data))
+        _check(lib().cri_decoder_set_layer(self._h, layer, ctypes.byref(w)))
+
+    def set_embedding(self, fmt, table):
+        _check(lib().cri_decoder_set_embedding(self._h, _FMT_OR_FP32[fmt], _host_or_device_ptr(table)))
+
+    def set_output(self, output_norm, lm_head=None):
+        """lm_head: (fmt, data), or None to tie the head to the token table."""
+        fmt, data = (-1, None) if lm_head is None else (_FMT_OR_FP32[lm_head[0]], _host_or_device_ptr(lm_head[1]))
+        _check(lib().cri_decoder_set_output(self._h, _host_or_device_ptr(output_norm), fmt, data))
+
+    def forward(self, token_ids, M, logits, next_ids=None, stream=None):
+        _check(lib().cri_decoder_forward(self._h, _ptr(token_ids), M, _ptr(logits), _ptr(next_ids),
+                                         _stream(stream)))
+
+    def capture(self, token_ids, M, logits, next_ids=None, stream=None):
+        _check(lib().cri_decoder_capture(self._h, _ptr(token_ids), M, _ptr(logits), _ptr(next_ids),
+                                         _stream(stream)))
+
+    def replay(self, stream=None):
+        _check(lib().cri_decoder_replay(self._h, _stream(stream)))
+
+    @property
+    def position(self):
+        return lib().cri_decoder_position(self._h)
+
+    def set_position(self, pos, stream=None):
+        _check(lib().cri_decoder_set_position(self._h, pos, _stream(stream)))
+
+    def kv_cache(self, layer):
+        """(k, v) device addresses of the layer's [max_seq_len, n_kv_heads, head_dim] caches."""
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        _check(lib().cri_decoder_kv_cache(self._h, layer, ctypes.byref(k), ctypes.byref(v)))
+        return k.value, v.value
+
+    @property
+    def weight_bytes(self):
+        return int(lib().cri_decoder_weight_bytes(self._h))

@@ -31,6 +31,24 @@ int check_launch(const char* fn) {
     return CRI_OK;
 }
 
+// Clears an error an earlier, unrelated HIP call left pending, so that check_launch
+// reports only the status of this call's own launches.
+void clear_pending_error() { (void)hipGetLastError(); }
+
+// A specialised launcher either enqueued its kernels (0), declined the shape
+// (kDeclined: the element-wise kernel takes it) or hit a runtime failure
+// (kFailed: reported, never retried on another kernel).
+int finish_matmul(int rc, const char* fn) {
+    if (rc == cri::detail::kFailed) {
+        const hipError_t e = hipGetLastError();
+        return fail(CRI_ERR_LAUNCH, fn,
+                    std::string("kernel set-up or launch failed: ") +
+                        (e != hipSuccess ? hipGetErrorString(e) : "hipFuncSetAttribute/hipGetDevice refused"));
+    }
+    if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
+    return check_launch(fn);
+}
+
 constexpr long kMaxElems = (1L << 40);
 
 // Batches above this many rows are prefill: they run on the fp16-operand MFMA
@@ -55,6 +73,7 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
     if (fmt == cri::kFmtF16 && !aligned(B, 2)) return fail(CRI_ERR_ALIGNMENT, fn, "FP16 B must be 2-byte aligned");
     if (static_cast<long>(M) * K > kMaxElems || static_cast<long>(M) * N > kMaxElems)
         return fail(CRI_ERR_SHAPE, fn, "problem too large");
+    clear_pending_error();
     if (K == 0) return fill_zero(C, static_cast<long>(M) * N, stream, fn);
     int rc;
     // batches of two (Q8_0, Q4_0, Q5_0, Q6_K) or up to four (the 32-element formats) as row
@@ -75,10 +94,9 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
         // small batches whose K is not a multiple of 256 (no skinny kernel): row pairs on the two-row GEMV
         rc = cri::detail::launch_gemv2(fmt, A, B, C, M, N, K, stream);
     else
-        rc = -1;
-    if (rc != 0) rc = cri::detail::launch_generic_matmul(fmt, A, B, C, M, N, K, stream);
-    if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
-    return check_launch(fn);
+        rc = cri::detail::kDeclined;
+    if (rc == cri::detail::kDeclined) rc = cri::detail::launch_generic_matmul(fmt, A, B, C, M, N, K, stream);
+    return finish_matmul(rc, fn);
 }
 
 int dequant_impl(int fmt, const void* src, float* dst, int n_blocks, hipStream_t stream, const char* fn) {
@@ -86,6 +104,7 @@ int dequant_impl(int fmt, const void* src, float* dst, int n_blocks, hipStream_t
     if (n_blocks == 0) return CRI_OK;
     if (!src || !dst) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
     if (!aligned(dst, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "dst must be 4-byte aligned");
+    clear_pending_error();
     if (cri::detail::launch_dequant(fmt, src, dst, n_blocks, stream) != 0)
         return fail(CRI_ERR_UNSUPPORTED, fn, "unknown format");
     return check_launch(fn);
@@ -97,6 +116,7 @@ void cri_internal_set_error(const char* msg) { g_last_error = msg; }
 
 namespace {
 int fill_zero(float* C, long n, hipStream_t stream, const char* fn) {
+    clear_pending_error();
     cri::detail::launch_fill_zero(C, n, stream);
     return check_launch(fn);
 }
@@ -163,6 +183,7 @@ int cri_matmul_transposed_b(const float* A, const float* B, float* C, int M, int
     if (static_cast<long>(M) * K > kMaxElems || static_cast<long>(N) * K > kMaxElems)
         return fail(CRI_ERR_SHAPE, fn, "problem too large");
     if (K == 0) return fill_zero(C, static_cast<long>(M) * N, s, fn);
+    clear_pending_error();
     if (cri::detail::launch_transposed_b(A, B, C, M, N, K, s) != 0)
         return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
     return check_launch(fn);
@@ -182,6 +203,7 @@ int cri_batched_matmul_gqa(const float* A, const float* B, float* C, int n_heads
     if (!aligned(A, 4) || !aligned(B, 4) || !aligned(C, 4))
         return fail(CRI_ERR_ALIGNMENT, fn, "A, B and C must be 4-byte aligned");
     if (K == 0) return fill_zero(C, static_cast<long>(n_heads) * M * N, s, fn);
+    clear_pending_error();
     if (cri::detail::launch_gqa(A, B, C, n_heads, n_kv_heads, M, N, K, s) != 0)
         return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
     return check_launch(fn);
@@ -208,6 +230,7 @@ int cri_fused_decode_attention(const float* Q, const float* K_cache, const float
         return fail(CRI_ERR_ALIGNMENT, fn, "Q, K_cache, V_cache and output must be 4-byte aligned");
     if (static_cast<long>(kv_len) * n_kv_heads * head_dim > kMaxElems)
         return fail(CRI_ERR_SHAPE, fn, "problem too large");
+    clear_pending_error();
     if (cri::detail::launch_decode_attention(Q, K_cache, V_cache, output, n_heads, n_kv_heads, head_dim, kv_len,
                                              scale, s) != 0)
         return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
@@ -240,14 +263,14 @@ int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float*
     if (!B || !C) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
     if (!aligned(C, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "C must be 4-byte aligned");
     if (fmt == cri::kFmtF16 && !aligned(B, 2)) return fail(CRI_ERR_ALIGNMENT, fn, "FP16 B must be 2-byte aligned");
-    int rc = -1;
+    clear_pending_error();
+    int rc = cri::detail::kDeclined;
     if (cri::detail::skinny_supported(fmt, M, K, B))
         rc = cri::detail::launch_skinny_act(mode, fmt, act, B, C, M, N, K, stream);
-    if (rc != 0 && M == 1 && cri::detail::gemv_supported(fmt, K, B))
+    if (rc == cri::detail::kDeclined && M == 1 && cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv_act(mode, fmt, act, B, C, N, K, stream);
-    if (rc != 0) rc = cri::detail::launch_generic_matmul_act(mode, fmt, act, B, C, M, N, K, stream);
-    if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
-    return check_launch(fn);
+    if (rc == cri::detail::kDeclined) rc = cri::detail::launch_generic_matmul_act(mode, fmt, act, B, C, M, N, K, stream);
+    return finish_matmul(rc, fn);
 }
 
 }  // namespace
@@ -291,6 +314,7 @@ int cri_rmsnorm_residual(const float* input, const float* residual, const float*
     if (!aligned(input, 4) || !aligned(residual, 4) || !aligned(weight, 4) || !aligned(output, 4) ||
         !aligned(normed, 4))
         return fail(CRI_ERR_ALIGNMENT, fn, "all buffers must be 4-byte aligned");
+    clear_pending_error();
     cri::detail::launch_rmsnorm_residual(input, residual, weight, output, normed, rows, n, eps, s);
     return check_launch(fn);
 }
@@ -302,6 +326,7 @@ int cri_silu_mul(const float* gate, const float* up, float* out, long long n, hi
     if (!gate || !up || !out) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
     if (!aligned(gate, 4) || !aligned(up, 4) || !aligned(out, 4))
         return fail(CRI_ERR_ALIGNMENT, fn, "all buffers must be 4-byte aligned");
+    clear_pending_error();
     cri::detail::launch_silu_mul(gate, up, out, static_cast<long>(n), s);
     return check_launch(fn);
 }
@@ -313,6 +338,7 @@ int cri_stream_read(const void* src, long long n_bytes, unsigned* sink, hipStrea
     if (n_bytes == 0) return CRI_OK;
     if (!src || !sink) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
     if (!aligned(src, 16) || !aligned(sink, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "src must be 16-byte aligned");
+    clear_pending_error();
     if (cri::detail::launch_stream_read(src, n_bytes, sink, s) != 0) return fail(CRI_ERR_SHAPE, fn, "too large");
     return check_launch(fn);
 }
@@ -349,6 +375,7 @@ int cri_fused_decode_attention_ws(const float* Q, const float* K_cache, const fl
     if (!workspace) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null workspace");
     if (!aligned(workspace, 16)) return fail(CRI_ERR_ALIGNMENT, fn, "workspace must be 16-byte aligned");
     if (static_cast<long>(kv_len) * n_kv_heads * head_dim > kMaxElems) return fail(CRI_ERR_SHAPE, fn, "problem too large");
+    clear_pending_error();
     const int rc = cri::detail::launch_decode_attention_split(Q, K_cache, V_cache, output, n_heads, n_kv_heads,
                                                               head_dim, kv_len, scale, static_cast<float*>(workspace),
                                                               static_cast<long>(workspace_bytes), s);
@@ -372,6 +399,7 @@ int cri_embedding_rows(int format, const void* table, const int* ids, float* out
     if (!aligned(ids, 4) || !aligned(out, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "ids and out must be 4-byte aligned");
     if ((format == CRI_FP16 && !aligned(table, 2)) || (format == CRI_FP32 && !aligned(table, 4)))
         return fail(CRI_ERR_ALIGNMENT, fn, "table misaligned for its element type");
+    clear_pending_error();
     cri::detail::launch_embedding_rows(format, table, ids, out, n_ids, dim, vocab, s);
     return check_launch(fn);
 }

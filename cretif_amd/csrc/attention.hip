@@ -223,34 +223,47 @@ __global__ __launch_bounds__(64 * kAttWaves) __attribute__((amdgpu_waves_per_eu(
 //
 // A workgroup is KV head kvh, a quad of its query heads (one wave per head;
 // measured faster than two or four heads per wave, whose longer per-wave VALU
-// chains dominate a one-tile chunk) and a chunk of Tc positions in tiles of 32.
-// The waves read each tile's K and V rows 4 lanes per position (dims 4 r + 16 i,
-// 16-byte loads); the four waves of a quad hit the same lines, so the cache is
-// read from memory once in total.  Per head: the scores of the tile's 32
-// positions end on lanes r = 0, 1 (position 16 r + q), online softmax as above,
-// and P.V in the same lane layout as the loads (the weight of position 16 g + q
-// is broadcast from lane (q, g) inside its quad).  The chunk's (max, sum,
-// acc[D]) per head go to the workspace, and the combine kernel merges the
-// chunks of each head.  head_dim <= 64, a multiple of 4, and 16-byte aligned
-// Q, K, V.
+// chains dominate a one-tile chunk), a chunk of the positions in tiles of 32,
+// and one query row m (blockIdx.y).  The waves read each tile's K and V rows 4
+// lanes per position (dims 4 r + 16 i, 16-byte loads); the four waves of a quad
+// hit the same lines, so the cache is read from memory once per query row (the
+// rows of one call re-read it from the caches).  Per head: the scores of the
+// tile's 32 positions end on lanes r = 0, 1 (position 16 r + q), online softmax
+// as above, and P.V in the same lane layout as the loads (the weight of position
+// 16 g + q is broadcast from lane (q, g) inside its quad).  The chunk's (max,
+// sum, acc[D]) per (row, head) go to the workspace, and the combine kernel
+// merges the chunks of each (row, head).
+//
+// Query row m sees the first kv0 + m positions, plus *kv_dev when kv_dev is
+// not null (causal: the rows are consecutive tokens whose keys are already in
+// the cache; a position counter read from device memory keeps a captured graph
+// of the call valid as the sequence grows).  The
+// positions of a row are cut into nchunks chunks of whole tiles, the chunk
+// length computed from the row's length (a chunk past the end writes an empty
+// record: max -inf, sum 0).  head_dim <= 16 NQ, a multiple of 4, and 16-byte
+// aligned Q, K, V.
 constexpr int kSplitTile = 32;
 
-template <int HQ>
+template <int HQ, int NQ>
 __global__ __launch_bounds__(256 / HQ) void decode_attn_split_kernel(const float* __restrict__ Q,
                                                                      const float* __restrict__ Kc,
                                                                      const float* __restrict__ Vc,
                                                                      float* __restrict__ ws, int G, int kvd, int D,
-                                                                     int T, float qscale, int Tc, int nchunks,
-                                                                     int nhq) {
-    constexpr int NQ = 4;
+                                                                     const int* __restrict__ kv_dev, int kv0,
+                                                                     float qscale, int nchunks, int nhq, long ldq) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = blockIdx.x % nchunks;
     const int hq = (blockIdx.x / nchunks) % nhq;
     const int kvh = blockIdx.x / (nchunks * nhq);
+    const int mrow = blockIdx.y;
+    const int H = G * (gridDim.x / (nchunks * nhq));
+    const int T = (kv_dev ? *kv_dev : 0) + kv0 + mrow;  // positions this row attends to
+    const int Tc = kSplitTile * ((((T + kSplitTile - 1) / kSplitTile) + nchunks - 1) / nchunks);
     const int q4 = lane >> 2, r = lane & 3;
     const int t0 = c * Tc, t1 = min(T, t0 + Tc);
     const float* Kh = Kc + static_cast<long>(kvh) * D;
     const float* Vh = Vc + static_cast<long>(kvh) * D;
+    const float* Qm = Q + mrow * ldq;
 
     f32x4 qv[HQ][NQ];
 #pragma unroll
@@ -260,7 +273,7 @@ __global__ __launch_bounds__(256 / HQ) void decode_attn_split_kernel(const float
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
             const int d = 4 * r + 16 * i;
-            const f32x4 v = ld_f32x4(Q + static_cast<long>(h) * D + min(d, D - 4)) * qscale;
+            const f32x4 v = ld_f32x4(Qm + static_cast<long>(h) * D + min(d, D - 4)) * qscale;
             qv[j][i] = d < D && hg < G ? v : f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
@@ -286,7 +299,7 @@ __global__ __launch_bounds__(256 / HQ) void decode_attn_split_kernel(const float
                 vv[g][i] = ld_f32x4(Vh + row + d);
             }
         }
-        __builtin_amdgcn_sched_barrier(0);  // the tile's 16 loads stay in flight together
+        __builtin_amdgcn_sched_barrier(0);  // the tile's loads stay in flight together
 #pragma unroll
         for (int j = 0; j < HQ; ++j) {
             float s_own = -INFINITY;  // lanes r = 2, 3 own no position of a 32-position tile
@@ -336,7 +349,7 @@ __global__ __launch_bounds__(256 / HQ) void decode_attn_split_kernel(const float
     for (int j = 0; j < HQ; ++j) {
         const int hg = hq * 4 + wave * HQ + j;
         const float lsum = group_sum_t<6>(l[j]);
-        float* rec = ws + (static_cast<long>(kvh * G + min(hg, G - 1)) * nchunks + c) * stride;
+        float* rec = ws + ((static_cast<long>(mrow) * H + kvh * G + min(hg, G - 1)) * nchunks + c) * stride;
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
             f32x4 a = acc[j][i];
@@ -359,18 +372,20 @@ __global__ __launch_bounds__(256 / HQ) void decode_attn_split_kernel(const float
     }
 }
 
-// out[h][d] = sum_c 2^(m_c - M) acc_c[d] / sum_c 2^(m_c - M) l_c, M = max_c m_c.
-// One wave per head: lanes take the chunks for the max and the sum (their loads
-// are independent), the factors go through LDS, and the accumulator loop over
-// the chunks is unrolled so its loads are in flight together.
+// out[m][h][d] = sum_c 2^(m_c - M) acc_c[d] / sum_c 2^(m_c - M) l_c, M = max_c m_c,
+// for query row m = blockIdx.y (output rows ldo floats apart).  One wave per
+// (row, head): lanes take the chunks for the max and the sum (their loads are
+// independent), the factors go through LDS, and the accumulator loop over the
+// chunks is unrolled so its loads are in flight together.  Empty chunks (max
+// -inf) get the factor 0; chunk 0 always holds a position.
 constexpr int kCombineMaxChunks = 4096;
 
 __global__ __launch_bounds__(64) void decode_attn_combine_kernel(const float* __restrict__ ws, float* __restrict__ out,
-                                                                 int D, int nchunks) {
+                                                                 int D, int nchunks, long ldo) {
     __shared__ float fs[kCombineMaxChunks];
-    const int h = blockIdx.x, lane = threadIdx.x;
+    const int h = blockIdx.x, mrow = blockIdx.y, lane = threadIdx.x;
     const int stride = D + 4;
-    const float* P = ws + static_cast<long>(h) * nchunks * stride;
+    const float* P = ws + (static_cast<long>(mrow) * gridDim.x + h) * nchunks * stride;
     float mloc = -INFINITY;
     for (int c = lane; c < nchunks; c += 64) mloc = fmaxf(mloc, P[static_cast<long>(c) * stride]);
     const float M = wave_max(mloc);
@@ -382,11 +397,14 @@ __global__ __launch_bounds__(64) void decode_attn_combine_kernel(const float* __
     }
     const float den = group_sum_t<6>(lloc);
     __syncthreads();
-    const int d = min(lane, D - 1);
-    float num = 0.0f;
+    float* o = out + mrow * ldo + static_cast<long>(h) * D;
+    for (int d0 = 0; d0 < D; d0 += 64) {
+        const int d = min(d0 + lane, D - 1);
+        float num = 0.0f;
 #pragma unroll 8
-    for (int c = 0; c < nchunks; ++c) num = __builtin_fmaf(fs[c], P[static_cast<long>(c) * stride + 4 + d], num);
-    if (lane < D) out[static_cast<long>(h) * D + lane] = num / den;
+        for (int c = 0; c < nchunks; ++c) num = __builtin_fmaf(fs[c], P[static_cast<long>(c) * stride + 4 + d], num);
+        if (d0 + lane < D) o[d0 + lane] = num / den;
+    }
 }
 
 }  // namespace dev
@@ -406,57 +424,66 @@ static void launch_att(bool vec, dim3 grid, hipStream_t stream, const float* Q, 
 
 constexpr int kSplitHeadsPerWave = 1;  // 4 waves per workgroup, one query head each
 
-// Split form: chunk length (a multiple of 32 positions) that gives ~256 workgroups
-// (measured: 512 or 1024 smaller chunks are no faster at 2048 positions, slower
-// at 8192); fewer chunks when the workspace is smaller.
-static int split_chunks(int n_heads, int n_kv_heads, int D, int kv_len, long ws_floats, int* Tc_out) {
+// Split form: number of chunks (of whole 32-position tiles) that gives ~256
+// workgroups per query row at kv_len positions (measured: 512 or 1024 smaller
+// chunks are no faster at 2048 positions, slower at 8192); fewer chunks when the
+// workspace (ws_floats >= 0) is smaller.  The kernel recomputes the chunk
+// length from the row's own length.
+static int split_chunks(int n_heads, int n_kv_heads, int D, int kv_len, int rows, long ws_floats) {
     const int G = n_heads / n_kv_heads, nhq = (G + 3) / 4;
     const long groups = static_cast<long>(n_kv_heads) * nhq;
-    long tiles = (kv_len + dev::kSplitTile - 1) / dev::kSplitTile;
+    const long tiles = (kv_len + dev::kSplitTile - 1) / dev::kSplitTile;
     long per = (tiles * groups + 255) / 256;  // tiles per chunk
     if (per < 1) per = 1;
     long nchunks = (tiles + per - 1) / per;
-    if (nchunks > dev::kCombineMaxChunks) {  // the combine kernel's factor array
-        per = (tiles + dev::kCombineMaxChunks - 1) / dev::kCombineMaxChunks;
-        nchunks = (tiles + per - 1) / per;
-    }
-    const long rec = static_cast<long>(n_heads) * (D + 4);
-    if (ws_floats >= 0 && nchunks * rec > ws_floats) {
-        nchunks = ws_floats / rec;
-        if (nchunks < 1) return 0;
-        per = (tiles + nchunks - 1) / nchunks;
-        nchunks = (tiles + per - 1) / per;
-    }
-    *Tc_out = static_cast<int>(per * dev::kSplitTile);
+    if (nchunks > dev::kCombineMaxChunks) nchunks = dev::kCombineMaxChunks;  // the combine kernel's factor array
+    const long rec = static_cast<long>(rows) * n_heads * (D + 4);
+    if (ws_floats >= 0 && nchunks * rec > ws_floats) nchunks = ws_floats / rec;
     return static_cast<int>(nchunks);
 }
 
 bool decode_attention_split_supported(const float* Q, const float* K, const float* V, int head_dim) {
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    return head_dim >= 4 && head_dim <= 64 && head_dim % 4 == 0 && a16(Q) && a16(K) && a16(V);
+    return head_dim >= 4 && head_dim <= kDecodeAttnSplitMaxHeadDim && head_dim % 4 == 0 && a16(Q) && a16(K) &&
+           a16(V);
 }
 
 long decode_attention_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int kv_len) {
-    int Tc = 0;
-    const int nchunks = split_chunks(n_heads, n_kv_heads, head_dim, kv_len, -1, &Tc);
+    const int nchunks = split_chunks(n_heads, n_kv_heads, head_dim, kv_len, 1, -1);
     return static_cast<long>(nchunks) * n_heads * (head_dim + 4) * 4;
+}
+
+int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const float* V, float* out, long ldo,
+                                 int rows, int n_heads, int n_kv_heads, int head_dim, const int* kv_dev, int kv0,
+                                 int nchunks, float scale, float* ws, hipStream_t stream) {
+    const int D = head_dim, G = n_heads / n_kv_heads, nhq = (G + 3) / 4;
+    if (nchunks < 1 || nchunks > dev::kCombineMaxChunks || rows < 1 || rows > 65535) return kDeclined;
+    const long blocks = static_cast<long>(n_kv_heads) * nhq * nchunks;
+    if (blocks > 0x7FFFFFFFL) return kDeclined;
+    const float qscale = scale * 1.44269504088896341f;
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(rows));
+    if (D <= 64)
+        hipLaunchKernelGGL((dev::decode_attn_split_kernel<kSplitHeadsPerWave, 4>), grid, dim3(256 / kSplitHeadsPerWave),
+                           0, stream, Q, K, V, ws, G, n_kv_heads * D, D, kv_dev, kv0, qscale, nchunks, nhq, ldq);
+    else
+        hipLaunchKernelGGL((dev::decode_attn_split_kernel<kSplitHeadsPerWave, 8>), grid, dim3(256 / kSplitHeadsPerWave),
+                           0, stream, Q, K, V, ws, G, n_kv_heads * D, D, kv_dev, kv0, qscale, nchunks, nhq, ldq);
+    hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads, static_cast<unsigned>(rows)), dim3(64), 0, stream,
+                       ws, out, D, nchunks, ldo);
+    return 0;
+}
+
+int decode_attention_rows_chunks(int n_heads, int n_kv_heads, int head_dim, int max_kv_len) {
+    return split_chunks(n_heads, n_kv_heads, head_dim, max_kv_len, 1, -1);
 }
 
 int launch_decode_attention_split(const float* Q, const float* K, const float* V, float* out, int n_heads,
                                   int n_kv_heads, int head_dim, int kv_len, float scale, float* ws, long ws_bytes,
                                   hipStream_t stream) {
-    const int D = head_dim, G = n_heads / n_kv_heads, nhq = (G + 3) / 4;
-    int Tc = 0;
-    const int nchunks = split_chunks(n_heads, n_kv_heads, D, kv_len, ws_bytes / 4, &Tc);
+    const int nchunks = split_chunks(n_heads, n_kv_heads, head_dim, kv_len, 1, ws_bytes / 4);
     if (nchunks < 1) return -2;  // workspace too small for one record per head
-    const long blocks = static_cast<long>(n_kv_heads) * nhq * nchunks;
-    if (blocks > 0x7FFFFFFFL) return -1;
-    const float qscale = scale * 1.44269504088896341f;
-    hipLaunchKernelGGL(dev::decode_attn_split_kernel<kSplitHeadsPerWave>, dim3(static_cast<unsigned>(blocks)),
-                       dim3(256 / kSplitHeadsPerWave), 0, stream, Q, K, V, ws, G, n_kv_heads * D, D, kv_len, qscale,
-                       Tc, nchunks, nhq);
-    hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads), dim3(64), 0, stream, ws, out, D, nchunks);
-    return 0;
+    return launch_decode_attention_rows(Q, 0, K, V, out, 0, 1, n_heads, n_kv_heads, head_dim, nullptr, kv_len,
+                                        nchunks, scale, ws, stream);
 }
 
 int launch_decode_attention(const float* Q, const float* K, const float* V, float* out, int n_heads, int n_kv_heads,

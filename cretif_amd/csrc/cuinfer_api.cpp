@@ -111,20 +111,37 @@ static int format_id(WeightFormat format, const char* fn) {
     throw std::invalid_argument(std::string(fn) + ": FP32 weights ([K,N] pre-transposed) are not handled here");
 }
 
+// The matmuls read the weight as N rows of K/bs consecutive blocks from weight.data(): a strided
+// view (for example a column slice of a quantized tensor) or a tensor holding fewer than N*K
+// elements would be read wrongly or past its end, so both are rejected before anything runs.
+static void check_weight(const Tensor& weight, int N, int K, const char* fn) {
+    if (!weight.is_contiguous())
+        throw std::invalid_argument(std::string(fn) + ": the weight tensor is a strided view; the matmul reads "
+                                    "N x K contiguous elements");
+    if (weight.dtype() != DType::FP32 && N > 0 && K > 0 &&
+        weight.numel() < static_cast<int64_t>(N) * static_cast<int64_t>(K))
+        throw std::invalid_argument(std::string(fn) + ": the weight tensor holds " + std::to_string(weight.numel()) +
+                                    " elements, fewer than N x K = " +
+                                    std::to_string(static_cast<int64_t>(N) * K));
+}
+
 void matmul_dispatch(const float* A, const Tensor& weight, float* C, int M, int N, int K, WeightFormat format,
                      hipStream_t s) {
+    check_weight(weight, N, K, "matmul_dispatch");
     CUINFER_CHECK_CRI(cri_matmul(format_id(format, "matmul_dispatch"), A, weight.data(), C, M, N, K, s));
 }
 
 void matmul_dispatch_rmsnorm(const float* hidden, const float* residual, const float* norm_weight, float* hidden_out,
                              const Tensor& weight, float* C, int M, int N, int K, WeightFormat format, float eps,
                              hipStream_t s) {
+    check_weight(weight, N, K, "matmul_dispatch_rmsnorm");
     CUINFER_CHECK_CRI(cri_matmul_rmsnorm(format_id(format, "matmul_dispatch_rmsnorm"), hidden, residual, norm_weight,
                                          hidden_out, weight.data(), C, M, N, K, eps, s));
 }
 
 void matmul_dispatch_swiglu(const float* gate, const float* up, int ld, const Tensor& weight, float* C, int M, int N,
                             int K, WeightFormat format, hipStream_t s) {
+    check_weight(weight, N, K, "matmul_dispatch_swiglu");
     CUINFER_CHECK_CRI(cri_matmul_swiglu(format_id(format, "matmul_dispatch_swiglu"), gate, up, ld, weight.data(), C,
                                         M, N, K, s));
 }
@@ -141,12 +158,17 @@ void silu_mul(const float* gate, const float* up, float* out, long long n, hipSt
 // ---------------------------------------------------------------- Tensor
 void Tensor::compute_shape_and_stride(const std::vector<int64_t>& shape, std::array<int64_t, 4>& out_shape,
                                       std::array<int64_t, 4>& out_stride) {
+    if (shape.empty() || shape.size() > 4)
+        throw std::invalid_argument("Tensor shape must have 1-4 dimensions, got " + std::to_string(shape.size()));
     out_shape.fill(1);
     const int off = 4 - static_cast<int>(shape.size());
     for (size_t i = 0; i < shape.size(); ++i) {
         if (shape[i] <= 0) throw std::invalid_argument("Tensor: dimensions must be positive");
         out_shape[off + i] = shape[i];
     }
+    int64_t n = 1;
+    for (int64_t d : out_shape)
+        if (__builtin_mul_overflow(n, d, &n)) throw std::invalid_argument("Tensor: element count overflows int64");
     out_stride[3] = 1;
     for (int i = 2; i >= 0; --i) out_stride[i] = out_stride[i + 1] * out_shape[i + 1];
 }
@@ -154,8 +176,6 @@ void Tensor::compute_shape_and_stride(const std::vector<int64_t>& shape, std::ar
 Tensor::Tensor() = default;
 
 Tensor::Tensor(std::vector<int64_t> shape, DType dtype) : dtype_(dtype), owning_(true) {
-    if (shape.empty() || shape.size() > 4)
-        throw std::invalid_argument("Tensor shape must have 1-4 dimensions, got " + std::to_string(shape.size()));
     compute_shape_and_stride(shape, shape_, stride_);
     if (dtype_is_quantized(dtype) && shape_[3] % dtype_block_elements(dtype) != 0)
         throw std::invalid_argument(std::string("Tensor: innermost dimension is not a multiple of the ") +
@@ -174,7 +194,10 @@ Tensor::~Tensor() {
 
 Tensor::Tensor(Tensor&& o) noexcept
     : data_(o.data_), shape_(o.shape_), stride_(o.stride_), dtype_(o.dtype_), owning_(o.owning_) {
+    // the moved-from tensor is empty: no data, every dimension 1 (ref:src/tensor.cu:69-100)
     o.data_ = nullptr;
+    o.shape_.fill(1);
+    o.stride_.fill(1);
     o.owning_ = false;
 }
 
@@ -187,6 +210,8 @@ Tensor& Tensor::operator=(Tensor&& o) noexcept {
         dtype_ = o.dtype_;
         owning_ = o.owning_;
         o.data_ = nullptr;
+        o.shape_.fill(1);
+        o.stride_.fill(1);
         o.owning_ = false;
     }
     return *this;
@@ -226,6 +251,9 @@ Tensor Tensor::view(int64_t dim, int64_t start, int64_t end) const {
 
 Tensor Tensor::reshape(std::vector<int64_t> new_shape) const {
     if (!is_contiguous()) throw std::runtime_error("reshape(): tensor must be contiguous");
+    if (new_shape.empty() || new_shape.size() > 4)
+        throw std::invalid_argument("reshape(): shape must have 1-4 dimensions, got " +
+                                    std::to_string(new_shape.size()));
     std::array<int64_t, 4> s, st;
     compute_shape_and_stride(new_shape, s, st);
     if (s[0] * s[1] * s[2] * s[3] != numel()) throw std::invalid_argument("reshape(): element count mismatch");
@@ -241,12 +269,12 @@ Tensor Tensor::clone() const {
 }
 
 void Tensor::copy_from_host(const void* host, size_t bytes) {
-    if (bytes > size_bytes()) throw std::out_of_range("copy_from_host(): too many bytes");
+    if (bytes > size_bytes()) throw std::invalid_argument("copy_from_host(): more bytes than the tensor holds");
     if (bytes) CUINFER_CHECK_HIP(hipMemcpy(data_, host, bytes, hipMemcpyHostToDevice));
 }
 
 void Tensor::copy_to_host(void* host, size_t bytes) const {
-    if (bytes > size_bytes()) throw std::out_of_range("copy_to_host(): too many bytes");
+    if (bytes > size_bytes()) throw std::invalid_argument("copy_to_host(): more bytes than the tensor holds");
     if (bytes) CUINFER_CHECK_HIP(hipMemcpy(host, data_, bytes, hipMemcpyDeviceToHost));
 }
 

@@ -1,0 +1,614 @@
+// decode_step.cpp -- cuinfer::DecodeStep and its C ABI (cri_decoder_*).
+//
+// The layer loop of TransformerModel::forward's quantized path
+// (ref:src/model.cu:831-1039) over buffers allocated once, with every
+// projection going through matmul_dispatch (or its fused-prologue forms for
+// batches of up to 16 tokens) and the position kept in device memory so that
+// one captured graph serves every following token.
+#include "../../include/cuinfer/decode_step.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/cri.h"
+#include "../../include/cuinfer/embedding.h"
+#include "../../include/cuinfer/hip_utils.h"
+#include "../../include/cuinfer/kernels/elementwise.h"
+#include "internal.hpp"
+
+namespace cuinfer {
+
+namespace {
+
+// Batches up to this many tokens take the fused RMSNorm / SwiGLU prologues.
+constexpr int kFusedMaxBatch = 16;
+
+DType dtype_of(WeightFormat f) {
+    switch (f) {
+        case WeightFormat::FP32: return DType::FP32;
+        case WeightFormat::FP16: return DType::FP16;
+        case WeightFormat::Q8_0: return DType::Q8_0;
+        case WeightFormat::Q4_0: return DType::Q4_0;
+        case WeightFormat::Q5_0: return DType::Q5_0;
+        case WeightFormat::Q4_K: return DType::Q4_K;
+        case WeightFormat::Q6_K: return DType::Q6_K;
+    }
+    return DType::FP32;
+}
+
+size_t row_bytes(WeightFormat f, int64_t K) {
+    const DType d = dtype_of(f);
+    return static_cast<size_t>(K / dtype_block_elements(d)) * dtype_block_bytes(d);
+}
+
+void check_k(WeightFormat f, int64_t K, const char* what) {
+    if (f == WeightFormat::FP32)
+        throw std::invalid_argument(std::string("DecodeStep: ") + what +
+                                    " is FP32; projections take FP16 or a block format ([N, K] rows)");
+    const int be = dtype_block_elements(dtype_of(f));
+    if (K % be != 0)
+        throw std::invalid_argument(std::string("DecodeStep: ") + what + " has K = " + std::to_string(K) +
+                                    ", not a multiple of its " + weight_format_name(f) + " block size " +
+                                    std::to_string(be));
+}
+
+void copy_in(void* dst, const void* src, size_t bytes, const char* what) {
+    if (!src) throw std::invalid_argument(std::string("DecodeStep: null ") + what);
+    CUINFER_CHECK_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDefault));
+}
+
+void check_status(int rc, const char* what) {
+    if (rc == cri::detail::kFailed || rc == CRI_ERR_LAUNCH)
+        throw std::runtime_error(std::string("DecodeStep: ") + what + " launch failed");
+    if (rc != 0) throw std::runtime_error(std::string("DecodeStep: ") + what + " declined the shape");
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        throw std::runtime_error(std::string("DecodeStep: ") + what + " launch failed: " + hipGetErrorString(e));
+}
+
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+int cri_id(WeightFormat f) {
+    switch (f) {
+        case WeightFormat::FP32: return CRI_FP32;
+        case WeightFormat::FP16: return CRI_FP16;
+        case WeightFormat::Q8_0: return CRI_Q8_0;
+        case WeightFormat::Q4_0: return CRI_Q4_0;
+        case WeightFormat::Q5_0: return CRI_Q5_0;
+        case WeightFormat::Q4_K: return CRI_Q4_K;
+        case WeightFormat::Q6_K: return CRI_Q6_K;
+    }
+    return -1;
+}
+
+}  // namespace
+
+struct DecodeStep::Layer {
+    bool set = false;
+    Tensor attn_norm, ffn_norm;
+    // q/k/v: one [q_dim + 2 kv_dim, dim] matrix when the three share a format, else three
+    bool qkv_fused = false;
+    Tensor qkv, q, k, v;
+    WeightFormat qkv_fmt = WeightFormat::Q4_K, q_fmt = WeightFormat::Q4_K, k_fmt = WeightFormat::Q4_K,
+                 v_fmt = WeightFormat::Q4_K;
+    Tensor o;
+    WeightFormat o_fmt = WeightFormat::Q4_K;
+    // gate/up: one [2 ffn, dim] matrix when they share a format (rows [0, ffn) gate, [ffn, 2 ffn) up)
+    bool gu_fused = false;
+    Tensor gu, gate, up;
+    WeightFormat gu_fmt = WeightFormat::Q4_K, gate_fmt = WeightFormat::Q4_K, up_fmt = WeightFormat::Q4_K;
+    Tensor down;
+    WeightFormat down_fmt = WeightFormat::Q4_K;
+};
+
+DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
+    auto bad = [](const std::string& m) { throw std::invalid_argument("DecodeStep: " + m); };
+    if (c.n_layers < 1 || c.dim < 1 || c.n_heads < 1 || c.n_kv_heads < 1 || c.head_dim < 1 ||
+        c.intermediate_size < 1 || c.vocab_size < 1 || c.max_seq_len < 1)
+        bad("every dimension of the configuration must be positive");
+    if (c.max_batch < 1 || c.max_batch > 65535) bad("max_batch must be in [1, 65535]");
+    if (c.n_heads % c.n_kv_heads != 0) bad("n_heads is not a multiple of n_kv_heads");
+    if (c.head_dim % 4 != 0 || c.head_dim > cri::detail::kDecodeAttnSplitMaxHeadDim)
+        bad("head_dim must be a multiple of 4 and at most " +
+            std::to_string(cri::detail::kDecodeAttnSplitMaxHeadDim) + " (the attention kernel's layout)");
+    if (c.dim % 4 != 0 || c.intermediate_size % 4 != 0) bad("dim and intermediate_size must be multiples of 4");
+    q_dim_ = c.n_heads * c.head_dim;
+    kv_dim_ = c.n_kv_heads * c.head_dim;
+    const int64_t MB = c.max_batch;
+    layers_.resize(c.n_layers);
+    for (auto& L : layers_) L = std::make_unique<Layer>();
+    const int64_t cache = static_cast<int64_t>(c.n_layers) * c.max_seq_len * kv_dim_;
+    k_cache_ = Tensor::zeros({cache});
+    v_cache_ = Tensor::zeros({cache});
+    pos_dev_ = Tensor::zeros({4}, DType::INT8);
+    for (auto& h : hid_) h = Tensor::empty({MB, static_cast<int64_t>(c.dim)});
+    normed_ = Tensor::empty({MB, static_cast<int64_t>(c.dim)});
+    qkv_ = Tensor::empty({MB, static_cast<int64_t>(q_dim_ + 2 * kv_dim_)});
+    ctx_ = Tensor::empty({MB, static_cast<int64_t>(q_dim_)});
+    attn_out_ = Tensor::empty({MB, static_cast<int64_t>(c.dim)});
+    ff_ = Tensor::empty({MB, 2 * static_cast<int64_t>(c.intermediate_size)});
+    act_ = Tensor::empty({MB, static_cast<int64_t>(c.intermediate_size)});
+    ffn_out_ = Tensor::empty({MB, static_cast<int64_t>(c.dim)});
+    nchunks_ = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len);
+    attn_ws_ = Tensor::empty({MB * c.n_heads * nchunks_ * (c.head_dim + 4)});
+}
+
+DecodeStep::~DecodeStep() {
+    if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+    if (graph_) (void)hipGraphDestroy(graph_);
+}
+
+void DecodeStep::set_layer(int li, const LayerWeightsRef& w) {
+    if (li < 0 || li >= cfg_.n_layers) throw std::out_of_range("DecodeStep::set_layer: layer out of range");
+    Layer& L = *layers_[li];
+    const int64_t D = cfg_.dim, F = cfg_.intermediate_size, QD = q_dim_, KVD = kv_dim_;
+    check_k(w.q.format, D, "q");
+    check_k(w.k.format, D, "k");
+    check_k(w.v.format, D, "v");
+    check_k(w.o.format, QD, "o");
+    check_k(w.gate.format, D, "gate");
+    check_k(w.up.format, D, "up");
+    check_k(w.down.format, F, "down");
+    L.attn_norm = Tensor::empty({D});
+    L.ffn_norm = Tensor::empty({D});
+    copy_in(L.attn_norm.data(), w.attn_norm, D * 4, "attn_norm");
+    copy_in(L.ffn_norm.data(), w.ffn_norm, D * 4, "ffn_norm");
+
+    L.qkv_fused = w.q.format == w.k.format && w.q.format == w.v.format;
+    L.q = Tensor();
+    L.k = Tensor();
+    L.v = Tensor();
+    L.qkv = Tensor();
+    if (L.qkv_fused) {
+        L.qkv_fmt = w.q.format;
+        const size_t rb = row_bytes(L.qkv_fmt, D);
+        L.qkv = Tensor::empty({QD + 2 * KVD, D}, dtype_of(L.qkv_fmt));
+        char* base = static_cast<char*>(L.qkv.data());
+        copy_in(base, w.q.data, QD * rb, "q");
+        copy_in(base + QD * rb, w.k.data, KVD * rb, "k");
+        copy_in(base + (QD + KVD) * rb, w.v.data, KVD * rb, "v");
+    } else {
+        L.q_fmt = w.q.format;
+        L.k_fmt = w.k.format;
+        L.v_fmt = w.v.format;
+        L.q = Tensor::empty({QD, D}, dtype_of(L.q_fmt));
+        L.k = Tensor::empty({KVD, D}, dtype_of(L.k_fmt));
+        L.v = Tensor::empty({KVD, D}, dtype_of(L.v_fmt));
+        copy_in(L.q.data(), w.q.data, L.q.size_bytes(), "q");
+        copy_in(L.k.data(), w.k.data, L.k.size_bytes(), "k");
+        copy_in(L.v.data(), w.v.data, L.v.size_bytes(), "v");
+    }
+    L.o_fmt = w.o.format;
+    L.o = Tensor::empty({D, QD}, dtype_of(L.o_fmt));
+    copy_in(L.o.data(), w.o.data, L.o.size_bytes(), "o");
+
+    L.gu_fused = w.gate.format == w.up.format;
+    L.gu = Tensor();
+    L.gate = Tensor();
+    L.up = Tensor();
+    if (L.gu_fused) {
+        L.gu_fmt = w.gate.format;
+        const size_t rb = row_bytes(L.gu_fmt, D);
+        L.gu = Tensor::empty({2 * F, D}, dtype_of(L.gu_fmt));
+        char* base = static_cast<char*>(L.gu.data());
+        copy_in(base, w.gate.data, F * rb, "gate");
+        copy_in(base + F * rb, w.up.data, F * rb, "up");
+    } else {
+        L.gate_fmt = w.gate.format;
+        L.up_fmt = w.up.format;
+        L.gate = Tensor::empty({F, D}, dtype_of(L.gate_fmt));
+        L.up = Tensor::empty({F, D}, dtype_of(L.up_fmt));
+        copy_in(L.gate.data(), w.gate.data, L.gate.size_bytes(), "gate");
+        copy_in(L.up.data(), w.up.data, L.up.size_bytes(), "up");
+    }
+    L.down_fmt = w.down.format;
+    L.down = Tensor::empty({D, F}, dtype_of(L.down_fmt));
+    copy_in(L.down.data(), w.down.data, L.down.size_bytes(), "down");
+    L.set = true;
+}
+
+void DecodeStep::set_token_embedding(const WeightRef& table) {
+    if (table.format != WeightFormat::FP32) check_k(table.format, cfg_.dim, "token embedding");
+    tok_fmt_ = table.format;
+    tok_table_ = Tensor::empty({static_cast<int64_t>(cfg_.vocab_size), static_cast<int64_t>(cfg_.dim)},
+                               dtype_of(tok_fmt_));
+    copy_in(tok_table_.data(), table.data, tok_table_.size_bytes(), "token embedding");
+    tok_set_ = true;
+}
+
+void DecodeStep::set_output(const float* output_norm, const WeightRef* lm_head) {
+    out_norm_ = Tensor::empty({static_cast<int64_t>(cfg_.dim)});
+    copy_in(out_norm_.data(), output_norm, static_cast<size_t>(cfg_.dim) * 4, "output_norm");
+    lm_tied_ = lm_head == nullptr;
+    lm_head_ = Tensor();
+    if (!lm_tied_) {
+        if (lm_head->format != WeightFormat::FP32) check_k(lm_head->format, cfg_.dim, "lm_head");
+        lm_fmt_ = lm_head->format;
+        lm_head_ = Tensor::empty({static_cast<int64_t>(cfg_.vocab_size), static_cast<int64_t>(cfg_.dim)},
+                                 dtype_of(lm_fmt_));
+        copy_in(lm_head_.data(), lm_head->data, lm_head_.size_bytes(), "lm_head");
+    }
+    out_set_ = true;
+}
+
+void DecodeStep::check_ready() const {
+    for (size_t i = 0; i < layers_.size(); ++i)
+        if (!layers_[i]->set) throw std::logic_error("DecodeStep: layer " + std::to_string(i) + " has no weights");
+    if (!tok_set_) throw std::logic_error("DecodeStep: no token embedding table");
+    if (!out_set_) throw std::logic_error("DecodeStep: no output norm / LM head");
+    if (lm_tied_ && !tok_set_) throw std::logic_error("DecodeStep: tied LM head without a token table");
+}
+
+float* DecodeStep::k_cache(int layer) {
+    if (layer < 0 || layer >= cfg_.n_layers) throw std::out_of_range("DecodeStep::k_cache: layer out of range");
+    return k_cache_.data_as<float>() + static_cast<int64_t>(layer) * cfg_.max_seq_len * kv_dim_;
+}
+float* DecodeStep::v_cache(int layer) {
+    if (layer < 0 || layer >= cfg_.n_layers) throw std::out_of_range("DecodeStep::v_cache: layer out of range");
+    return v_cache_.data_as<float>() + static_cast<int64_t>(layer) * cfg_.max_seq_len * kv_dim_;
+}
+
+size_t DecodeStep::weight_bytes() const {
+    size_t n = tok_table_.size_bytes() + out_norm_.size_bytes() + lm_head_.size_bytes();
+    for (const auto& L : layers_)
+        for (const Tensor* t : {&L->attn_norm, &L->ffn_norm, &L->qkv, &L->q, &L->k, &L->v, &L->o, &L->gu, &L->gate,
+                                &L->up, &L->down})
+            n += t->size_bytes();
+    return n;
+}
+
+void DecodeStep::set_position(int pos, hipStream_t s) {
+    if (pos < 0 || pos > cfg_.max_seq_len)
+        throw std::out_of_range("DecodeStep::set_position: " + std::to_string(pos) + " outside [0, max_seq_len]");
+    check_status(cri::detail::launch_pos_set(static_cast<int*>(pos_dev_.data()), pos, s), "position update");
+    pos_host_ = pos;
+}
+
+// hidden[cur] (+ res) -> RMSNorm -> q/k/v -> RoPE + cache append -> attention -> o: attn_out
+void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res, hipStream_t s) {
+    const int D = cfg_.dim, QD = q_dim_, KVD = kv_dim_, MB = cfg_.max_batch;
+    const float eps = cfg_.rms_norm_eps;
+    float* h = hid_[cur].data_as<float>();
+    float* h_next = hid_[1 - cur].data_as<float>();
+    float* base = qkv_.data_as<float>();
+    float *q, *k, *v;
+    long ldq, ldk, ldv;
+    if (L.qkv_fused) {
+        q = base;
+        k = base + QD;
+        v = base + QD + KVD;
+        ldq = ldk = ldv = QD + 2 * KVD;
+    } else {
+        q = base;
+        k = base + static_cast<long>(MB) * QD;
+        v = k + static_cast<long>(MB) * KVD;
+        ldq = QD;
+        ldk = ldv = KVD;
+    }
+    if (M <= kFusedMaxBatch) {
+        // h_next = h + res; projections of RMSNorm(h_next) (the first writes h_next)
+        if (L.qkv_fused) {
+            matmul_dispatch_rmsnorm(h, res, L.attn_norm.data_as<float>(), h_next, L.qkv, q, M, QD + 2 * KVD, D,
+                                    L.qkv_fmt, eps, s);
+        } else {
+            matmul_dispatch_rmsnorm(h, res, L.attn_norm.data_as<float>(), h_next, L.q, q, M, QD, D, L.q_fmt, eps, s);
+            matmul_dispatch_rmsnorm(h, res, L.attn_norm.data_as<float>(), nullptr, L.k, k, M, KVD, D, L.k_fmt, eps, s);
+            matmul_dispatch_rmsnorm(h, res, L.attn_norm.data_as<float>(), nullptr, L.v, v, M, KVD, D, L.v_fmt, eps, s);
+        }
+        cur = 1 - cur;
+    } else {
+        // hidden += res; normed = RMSNorm(hidden)  (ref:src/model.cu:963-967 for the residual form)
+        rmsnorm_residual(h, res, L.attn_norm.data_as<float>(), h, normed_.data_as<float>(), M, D, eps, s);
+        const float* n = normed_.data_as<float>();
+        if (L.qkv_fused) {
+            matmul_dispatch(n, L.qkv, q, M, QD + 2 * KVD, D, L.qkv_fmt, s);
+        } else {
+            matmul_dispatch(n, L.q, q, M, QD, D, L.q_fmt, s);
+            matmul_dispatch(n, L.k, k, M, KVD, D, L.k_fmt, s);
+            matmul_dispatch(n, L.v, v, M, KVD, D, L.v_fmt, s);
+        }
+    }
+    const int* pos = static_cast<const int*>(pos_dev_.data());
+    check_status(cri::detail::launch_rope_append(q, ldq, k, ldk, v, ldv, M, cfg_.n_heads, cfg_.n_kv_heads,
+                                                 cfg_.head_dim, cfg_.rope_theta, pos, k_cache(li), v_cache(li), s),
+                 "rope/append");
+    // row m attends to positions [0, pos + m] (ref:src/attention.cu:60-75; one token: :410-511)
+    const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
+    check_status(cri::detail::launch_decode_attention_rows(q, ldq, k_cache(li), v_cache(li), ctx_.data_as<float>(), QD,
+                                                           M, cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim, pos, 1,
+                                                           nchunks_, scale, attn_ws_.data_as<float>(), s),
+                 "attention");
+    matmul_dispatch(ctx_.data_as<float>(), L.o, attn_out_.data_as<float>(), M, D, QD, L.o_fmt, s);
+    res = attn_out_.data_as<float>();
+}
+
+// hidden[cur] (+ attn_out) -> RMSNorm -> gate/up -> SiLU(gate) * up -> down: ffn_out
+void DecodeStep::ffn_block(Layer& L, int M, int& cur, const float*& res, hipStream_t s) {
+    const int D = cfg_.dim, F = cfg_.intermediate_size, MB = cfg_.max_batch;
+    const float eps = cfg_.rms_norm_eps;
+    float* h = hid_[cur].data_as<float>();
+    float* h_next = hid_[1 - cur].data_as<float>();
+    float* ff = ff_.data_as<float>();
+    float* ffn_out = ffn_out_.data_as<float>();
+    if (M <= kFusedMaxBatch) {
+        if (L.gu_fused) {
+            // ff rows: [gate (F) | up (F)]
+            matmul_dispatch_rmsnorm(h, res, L.ffn_norm.data_as<float>(), h_next, L.gu, ff, M, 2 * F, D, L.gu_fmt, eps,
+                                    s);
+            matmul_dispatch_swiglu(ff, ff + F, 2 * F, L.down, ffn_out, M, D, F, L.down_fmt, s);
+        } else {
+            float* up = ff + static_cast<long>(MB) * F;
+            matmul_dispatch_rmsnorm(h, res, L.ffn_norm.data_as<float>(), h_next, L.gate, ff, M, F, D, L.gate_fmt, eps,
+                                    s);
+            matmul_dispatch_rmsnorm(h, res, L.ffn_norm.data_as<float>(), nullptr, L.up, up, M, F, D, L.up_fmt, eps, s);
+            matmul_dispatch_swiglu(ff, up, F, L.down, ffn_out, M, D, F, L.down_fmt, s);
+        }
+        cur = 1 - cur;
+    } else {
+        rmsnorm_residual(h, res, L.ffn_norm.data_as<float>(), h, normed_.data_as<float>(), M, D, eps, s);
+        const float* n = normed_.data_as<float>();
+        float* gate = ff;
+        float* up = ff + static_cast<long>(MB) * F;
+        if (L.gu_fused) {
+            // the stacked matrix read as its two halves ([0, F) gate, [F, 2F) up)
+            const Tensor g = L.gu.view(2, 0, F), u = L.gu.view(2, F, 2 * F);
+            matmul_dispatch(n, g, gate, M, F, D, L.gu_fmt, s);
+            matmul_dispatch(n, u, up, M, F, D, L.gu_fmt, s);
+        } else {
+            matmul_dispatch(n, L.gate, gate, M, F, D, L.gate_fmt, s);
+            matmul_dispatch(n, L.up, up, M, F, D, L.up_fmt, s);
+        }
+        silu_mul(gate, up, act_.data_as<float>(), static_cast<long long>(M) * F, s);  // ref:src/model.cu:996-997
+        matmul_dispatch(act_.data_as<float>(), L.down, ffn_out, M, D, F, L.down_fmt, s);
+    }
+    res = ffn_out;
+}
+
+void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s) {
+    const int D = cfg_.dim, V = cfg_.vocab_size;
+    const float eps = cfg_.rms_norm_eps;
+    // token rows straight from the table in its own format (the reference's Embedding::forward
+    // reads an FP32 table, ref:src/embedding.cu:237-263)
+    CUINFER_CHECK_CRI(
+        cri_embedding_rows(cri_id(tok_fmt_), tok_table_.data(), ids, hid_[0].data_as<float>(), M, D, V, s));
+    int cur = 0;
+    const float* res = nullptr;  // residual still to be added to hidden[cur]
+    for (int li = 0; li < cfg_.n_layers; ++li) {
+        Layer& L = *layers_[li];
+        attn_block(L, li, M, cur, res, s);
+        ffn_block(L, M, cur, res, s);
+    }
+    // final RMSNorm(hidden + ffn_out) and the LM head
+    const Tensor& W = lm_tied_ ? tok_table_ : lm_head_;
+    const WeightFormat wf = lm_tied_ ? tok_fmt_ : lm_fmt_;
+    float* h = hid_[cur].data_as<float>();
+    if (wf != WeightFormat::FP32 && M <= kFusedMaxBatch) {
+        matmul_dispatch_rmsnorm(h, res, out_norm_.data_as<float>(), hid_[1 - cur].data_as<float>(), W, logits, M, V,
+                                D, wf, eps, s);
+    } else {
+        rmsnorm_residual(h, res, out_norm_.data_as<float>(), h, normed_.data_as<float>(), M, D, eps, s);
+        if (wf == WeightFormat::FP32)  // tied FP32 table (ref:src/model.cu:1027-1029)
+            matmul_transposed_b(normed_.data_as<float>(), W.data_as<float>(), logits, M, V, D, s);
+        else
+            matmul_dispatch(normed_.data_as<float>(), W, logits, M, V, D, wf, s);
+    }
+    if (next_ids) check_status(cri::detail::launch_argmax_rows(logits, V, M, V, next_ids, s), "argmax");
+    check_status(cri::detail::launch_pos_add(static_cast<int*>(pos_dev_.data()), M, s), "position update");
+}
+
+void DecodeStep::forward(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s) {
+    check_ready();
+    if (M < 1 || M > cfg_.max_batch)
+        throw std::invalid_argument("DecodeStep::forward: M = " + std::to_string(M) + " outside [1, max_batch = " +
+                                    std::to_string(cfg_.max_batch) + "]");
+    if (!ids || !logits) throw std::invalid_argument("DecodeStep::forward: null token_ids or logits");
+    if (!aligned4(ids) || !aligned4(logits) || !aligned4(next_ids))
+        throw std::invalid_argument("DecodeStep::forward: token_ids, logits and next_ids must be 4-byte aligned");
+    if (pos_host_ + M > cfg_.max_seq_len)  // ref:src/model.cu:845-851
+        throw std::overflow_error("DecodeStep::forward: would exceed max sequence length (" +
+                                  std::to_string(pos_host_ + M) + " > " + std::to_string(cfg_.max_seq_len) + ")");
+    enqueue(ids, M, logits, next_ids, s);
+    pos_host_ += M;
+}
+
+void DecodeStep::capture(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s) {
+    check_ready();
+    if (!s) throw std::invalid_argument("DecodeStep::capture: the null stream cannot be captured");
+    if (M < 1 || M > cfg_.max_batch) throw std::invalid_argument("DecodeStep::capture: M outside [1, max_batch]");
+    if (!ids || !logits) throw std::invalid_argument("DecodeStep::capture: null token_ids or logits");
+    if (!aligned4(ids) || !aligned4(logits) || !aligned4(next_ids))
+        throw std::invalid_argument("DecodeStep::capture: token_ids, logits and next_ids must be 4-byte aligned");
+    if (graph_exec_) {
+        (void)hipGraphExecDestroy(graph_exec_);
+        graph_exec_ = nullptr;
+    }
+    if (graph_) {
+        (void)hipGraphDestroy(graph_);
+        graph_ = nullptr;
+    }
+    graph_m_ = 0;
+    CUINFER_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    try {
+        enqueue(ids, M, logits, next_ids, s);
+    } catch (...) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(s, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+    }
+    CUINFER_CHECK_HIP(hipStreamEndCapture(s, &graph_));
+    CUINFER_CHECK_HIP(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+    graph_m_ = M;
+}
+
+void DecodeStep::replay(hipStream_t s) {
+    if (!graph_exec_) throw std::logic_error("DecodeStep::replay: nothing captured");
+    if (pos_host_ + graph_m_ > cfg_.max_seq_len)
+        throw std::overflow_error("DecodeStep::replay: would exceed max sequence length (" +
+                                  std::to_string(pos_host_ + graph_m_) + " > " + std::to_string(cfg_.max_seq_len) +
+                                  ")");
+    CUINFER_CHECK_HIP(hipGraphLaunch(graph_exec_, s));
+    pos_host_ += graph_m_;
+}
+
+}  // namespace cuinfer
+
+// ---------------------------------------------------------------- C ABI
+void cri_internal_set_error(const char* msg);  // abi.cpp
+
+struct cri_decoder {
+    cuinfer::DecodeStep step;
+    explicit cri_decoder(const cuinfer::DecodeStepConfig& c) : step(c) {}
+};
+
+namespace {
+
+int dec_fail(int status, const char* fn, const std::string& what) {
+    cri_internal_set_error((std::string(fn) + ": " + what).c_str());
+    return status;
+}
+
+// exceptions of the C++ layer -> status codes
+template <class F>
+int guarded(const char* fn, F&& f) {
+    try {
+        f();
+        return CRI_OK;
+    } catch (const std::overflow_error& e) {
+        return dec_fail(CRI_ERR_SHAPE, fn, e.what());
+    } catch (const std::out_of_range& e) {
+        return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, e.what());
+    } catch (const std::invalid_argument& e) {
+        return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, e.what());
+    } catch (const std::logic_error& e) {
+        return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, e.what());
+    } catch (const std::exception& e) {
+        return dec_fail(CRI_ERR_LAUNCH, fn, e.what());
+    }
+}
+
+bool weight_format(int f, cuinfer::WeightFormat* out, bool allow_fp32) {
+    using cuinfer::WeightFormat;
+    switch (f) {
+        case CRI_Q8_0: *out = WeightFormat::Q8_0; return true;
+        case CRI_Q4_0: *out = WeightFormat::Q4_0; return true;
+        case CRI_Q5_0: *out = WeightFormat::Q5_0; return true;
+        case CRI_Q4_K: *out = WeightFormat::Q4_K; return true;
+        case CRI_Q6_K: *out = WeightFormat::Q6_K; return true;
+        case CRI_FP16: *out = WeightFormat::FP16; return true;
+        case CRI_FP32: *out = WeightFormat::FP32; return allow_fp32;
+    }
+    return false;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cri_decoder_create(const cri_decoder_config* c, cri_decoder** out) {
+    const char* fn = "cri_decoder_create";
+    if (!c || !out) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null argument");
+    *out = nullptr;
+    cuinfer::DecodeStepConfig cfg;
+    cfg.n_layers = c->n_layers;
+    cfg.dim = c->dim;
+    cfg.n_heads = c->n_heads;
+    cfg.n_kv_heads = c->n_kv_heads;
+    cfg.head_dim = c->head_dim;
+    cfg.intermediate_size = c->ffn_dim;
+    cfg.vocab_size = c->vocab_size;
+    cfg.max_seq_len = c->max_seq_len;
+    cfg.rms_norm_eps = c->rms_norm_eps;
+    cfg.rope_theta = c->rope_theta;
+    cfg.max_batch = c->max_batch;
+    return guarded(fn, [&] { *out = new cri_decoder(cfg); });
+}
+
+void cri_decoder_destroy(cri_decoder* d) { delete d; }
+
+int cri_decoder_set_layer(cri_decoder* d, int layer, const cri_decoder_layer* w) {
+    const char* fn = "cri_decoder_set_layer";
+    if (!d || !w) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null argument");
+    cuinfer::LayerWeightsRef r;
+    r.attn_norm = w->attn_norm;
+    r.ffn_norm = w->ffn_norm;
+    const struct {
+        int f;
+        const void* p;
+        cuinfer::WeightRef* dst;
+        const char* name;
+    } ws[] = {{w->q_format, w->q, &r.q, "q"},          {w->k_format, w->k, &r.k, "k"},
+              {w->v_format, w->v, &r.v, "v"},          {w->o_format, w->o, &r.o, "o"},
+              {w->gate_format, w->gate, &r.gate, "gate"}, {w->up_format, w->up, &r.up, "up"},
+              {w->down_format, w->down, &r.down, "down"}};
+    for (const auto& x : ws) {
+        if (!weight_format(x.f, &x.dst->format, false))
+            return dec_fail(CRI_ERR_UNSUPPORTED, fn, std::string("unsupported format id for ") + x.name);
+        x.dst->data = x.p;
+    }
+    return guarded(fn, [&] { d->step.set_layer(layer, r); });
+}
+
+int cri_decoder_set_embedding(cri_decoder* d, int format, const void* table) {
+    const char* fn = "cri_decoder_set_embedding";
+    if (!d) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null decoder");
+    cuinfer::WeightRef r;
+    if (!weight_format(format, &r.format, true)) return dec_fail(CRI_ERR_UNSUPPORTED, fn, "unsupported format id");
+    r.data = table;
+    return guarded(fn, [&] { d->step.set_token_embedding(r); });
+}
+
+int cri_decoder_set_output(cri_decoder* d, const float* output_norm, int format, const void* lm_head) {
+    const char* fn = "cri_decoder_set_output";
+    if (!d) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null decoder");
+    cuinfer::WeightRef r;
+    if (format >= 0 && !weight_format(format, &r.format, true))
+        return dec_fail(CRI_ERR_UNSUPPORTED, fn, "unsupported format id");
+    r.data = lm_head;
+    return guarded(fn, [&] { d->step.set_output(output_norm, format < 0 ? nullptr : &r); });
+}
+
+int cri_decoder_forward(cri_decoder* d, const int* token_ids, int M, float* logits, int* next_ids, hipStream_t s) {
+    const char* fn = "cri_decoder_forward";
+    if (!d) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null decoder");
+    return guarded(fn, [&] { d->step.forward(token_ids, M, logits, next_ids, s); });
+}
+
+int cri_decoder_capture(cri_decoder* d, const int* token_ids, int M, float* logits, int* next_ids, hipStream_t s) {
+    const char* fn = "cri_decoder_capture";
+    if (!d) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null decoder");
+    return guarded(fn, [&] { d->step.capture(token_ids, M, logits, next_ids, s); });
+}
+
+int cri_decoder_replay(cri_decoder* d, hipStream_t s) {
+    const char* fn = "cri_decoder_replay";
+    if (!d) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null decoder");
+    return guarded(fn, [&] { d->step.replay(s); });
+}
+
+int cri_decoder_set_position(cri_decoder* d, int pos, hipStream_t s) {
+    const char* fn = "cri_decoder_set_position";
+    if (!d) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null decoder");
+    return guarded(fn, [&] { d->step.set_position(pos, s); });
+}
+
+int cri_decoder_position(const cri_decoder* d) { return d ? d->step.position() : CRI_ERR_INVALID_ARGUMENT; }
+
+int cri_decoder_kv_cache(cri_decoder* d, int layer, float** k, float** v) {
+    const char* fn = "cri_decoder_kv_cache";
+    if (!d || !k || !v) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null argument");
+    return guarded(fn, [&] {
+        *k = d->step.k_cache(layer);
+        *v = d->step.v_cache(layer);
+    });
+}
+
+long long cri_decoder_weight_bytes(const cri_decoder* d) {
+    return d ? static_cast<long long>(d->step.weight_bytes()) : CRI_ERR_INVALID_ARGUMENT;
+}
+
+}  // extern "C"

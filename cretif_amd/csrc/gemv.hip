@@ -177,11 +177,11 @@ static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K
         constexpr int kMaxDevices = 64;
         static std::atomic<bool> ready[kMaxDevices];
         int devid = 0;
-        if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return -1;
+        if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return kFailed;
         if (!ready[devid].load(std::memory_order_acquire)) {
             if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::gemv_kernel<F, UPL, PREF, MODE, MR>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-                return -1;
+                return kFailed;
             ready[devid].store(true, std::memory_order_release);
         }
     }

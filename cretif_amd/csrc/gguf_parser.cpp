@@ -100,7 +100,9 @@ double GGUFValue::as_float64() const { return value_as<double>(*this, GGUFValueT
 uint64_t GGUFTensorInfo::element_count() const {
     if (dimensions.empty()) return 0;
     uint64_t n = 1;
-    for (uint64_t d : dimensions) n *= d;
+    for (uint64_t d : dimensions)
+        if (__builtin_mul_overflow(n, d, &n))
+            throw std::runtime_error("Tensor '" + name + "': the product of its dimensions overflows 64 bits");
     return n;
 }
 
@@ -110,7 +112,10 @@ size_t GGUFTensorInfo::byte_size() const {
     if (n % be != 0)
         throw std::runtime_error("Tensor '" + name + "' has " + std::to_string(n) +
                                  " elements, not a multiple of its block size " + std::to_string(be));
-    return static_cast<size_t>(n / be * bb);
+    uint64_t bytes;
+    if (__builtin_mul_overflow(n / be, static_cast<uint64_t>(bb), &bytes))
+        throw std::runtime_error("Tensor '" + name + "': its byte size overflows 64 bits");
+    return static_cast<size_t>(bytes);
 }
 
 // ---------------------------------------------------------------- reader

@@ -55,6 +55,12 @@ struct ActIn {
 
 namespace detail {
 
+// Launcher status: 0 = enqueued; kDeclined = this kernel does not take the shape
+// (the caller may try another); kFailed = the HIP runtime refused a set-up call
+// or the launch (the caller reports CRI_ERR_LAUNCH and tries nothing else).
+constexpr int kDeclined = -1;
+constexpr int kFailed = -4;
+
 // Target number of resident waves for the GEMV grid (MI355X: 256 CUs).
 constexpr long kGemvTargetWaves = 2048;
 
@@ -104,13 +110,36 @@ int launch_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_h
 constexpr int kDecodeAttnMaxHeadDim = 256;
 int launch_decode_attention(const float* Q, const float* K, const float* V, float* out, int n_heads, int n_kv_heads,
                             int head_dim, int kv_len, float scale, hipStream_t stream);
-// split over positions with partial results in a caller workspace (head_dim <= 64, 4 | head_dim,
+// split over positions with partial results in a caller workspace (head_dim <= 128, 4 | head_dim,
 // 16-byte aligned Q/K/V); returns -2 when the workspace cannot hold one record per head
+constexpr int kDecodeAttnSplitMaxHeadDim = 128;
 bool decode_attention_split_supported(const float* Q, const float* K, const float* V, int head_dim);
 long decode_attention_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int kv_len);
 int launch_decode_attention_split(const float* Q, const float* K, const float* V, float* out, int n_heads,
                                   int n_kv_heads, int head_dim, int kv_len, float scale, float* ws, long ws_bytes,
                                   hipStream_t stream);
+// the split form for `rows` consecutive query tokens (row m at Q + m*ldq, output at out + m*ldo):
+// row m attends to the first kv0 + m positions (+ *kv_dev when kv_dev is not null);
+// nchunks chunks per row (decode_attention_rows_chunks gives ~256 workgroups per row at
+// max_kv_len); ws holds rows * n_heads * nchunks records of head_dim + 4 floats
+int decode_attention_rows_chunks(int n_heads, int n_kv_heads, int head_dim, int max_kv_len);
+int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const float* V, float* out, long ldo,
+                                 int rows, int n_heads, int n_kv_heads, int head_dim, const int* kv_dev, int kv0,
+                                 int nchunks, float scale, float* ws, hipStream_t stream);
+
+// decode step neighbours (step_kernels.hip)
+// RoPE of the rows' q and k at positions *pos + m (ref:src/kernels/elementwise.cu:232-266),
+// q rotated in place, rotated k and v written to the caches' rows *pos + m
+// (KVCache::append, ref:src/kv_cache.cu:157-211); caches [max_seq, n_kv_heads, head_dim]
+int launch_rope_append(float* q, long ldq, const float* k, long ldk, const float* v, long ldv, int rows, int n_heads,
+                       int n_kv_heads, int head_dim, float theta, const int* pos, float* k_cache, float* v_cache,
+                       hipStream_t stream);
+// out[m] = index of the largest logits[m][i], the smallest index among equal maxima, NaN ignored
+// (kernel_argmax, ref:src/embedding.cu:155-200)
+int launch_argmax_rows(const float* logits, long ld, int rows, int n, int* out, hipStream_t stream);
+// *pos += delta / *pos = value
+int launch_pos_add(int* pos, int delta, hipStream_t stream);
+int launch_pos_set(int* pos, int value, hipStream_t stream);
 
 }  // namespace detail
 }  // namespace cri

@@ -616,16 +616,16 @@ int launch_w(dim3 grid, hipStream_t stream, const float* A, const uint8_t* B, fl
     constexpr int kMaxDevices = 64;
     static std::atomic<bool> ready[kMaxDevices];
     int devid = 0;
-    if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return -4;
+    if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return kFailed;
     if (!ready[devid].load(std::memory_order_acquire)) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::mfma_gemm_kernel<W>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, dev::kLdsBytes) != hipSuccess)
-            return -4;
+            return kFailed;
         ready[devid].store(true, std::memory_order_release);
     }
     hipLaunchKernelGGL(dev::mfma_gemm_kernel<W>, grid, dim3(dev::kThreads), dev::kLdsBytes, stream, A, B, C, M, N, K,
                        rb, MT, NT, sps, remap, atomic, vec);
-    return hipGetLastError() == hipSuccess ? 0 : -4;
+    return 0;  // the launch's own status is read by the caller (hipGetLastError)
 }
 
 }  // namespace

@@ -954,11 +954,11 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
     constexpr int kMaxDevices = 64;
     static std::atomic<bool> ready[kMaxDevices];
     int devid = 0;
-    if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return -1;
+    if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return kFailed;
     if (!ready[devid].load(std::memory_order_acquire)) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::skinny_kernel<F, NW, MODE, PAIR, NPT, XPF>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-            return -1;
+            return kFailed;
         ready[devid].store(true, std::memory_order_release);
     }
     const int ntiles = (N + 15) / 16;

@@ -45,6 +45,13 @@ static Tensor upload_2d(const GGUFParser& parser, const GGUFTensorInfo& info, We
         throw std::runtime_error("load_weight_quantized: expected a 2-D tensor for '" + info.name + "', got " +
                                  std::to_string(info.dimensions.size()) + "-D");
     out_format = ggml_type_to_weight_format(info.type);
+    // the matmuls take N and K as int: larger dimensions cannot be multiplied, only misread
+    constexpr uint64_t kMaxDim = 0x7fffffffu;
+    if (info.dimensions[0] == 0 || info.dimensions[1] == 0 || info.dimensions[0] > kMaxDim ||
+        info.dimensions[1] > kMaxDim)
+        throw std::runtime_error("load_weight_quantized: '" + info.name + "' has dimensions {" +
+                                 std::to_string(info.dimensions[0]) + ", " + std::to_string(info.dimensions[1]) +
+                                 "}, outside [1, 2^31 - 1]");
     const int64_t K = static_cast<int64_t>(info.dimensions[0]), N = static_cast<int64_t>(info.dimensions[1]);
     Tensor t({N, K}, dtype_of(out_format));
     const size_t bytes = info.byte_size();
@@ -171,7 +178,11 @@ int cri_gguf_tensor_info(const cri_gguf* g, int index, cri_gguf_tensor* out) {
     out->format = ggml_to_format(t.type);
     out->n_dims = static_cast<int>(t.dimensions.size());
     for (size_t d = 0; d < t.dimensions.size() && d < 8; ++d) out->dims[d] = static_cast<long long>(t.dimensions[d]);
-    out->n_elements = static_cast<long long>(t.element_count());
+    try {
+        out->n_elements = static_cast<long long>(t.element_count());
+    } catch (const std::exception&) {
+        out->n_elements = -1;  // the dimensions' product overflows (a tensor of a type not checked at open)
+    }
     try {
         out->byte_size = static_cast<long long>(t.byte_size());
     } catch (const std::exception&) {

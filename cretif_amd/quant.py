@@ -188,3 +188,38 @@ def synthetic_weights(fmt: str, N: int, K: int, seed: int, sigma: float = 0.02, 
         w = (rng.standard_normal((r1 - r0) * K, dtype=np.float32) * F32(sigma)).astype(F32)
         out[r0 * rb:r1 * rb] = quantize(fmt, w)
     return out
+
+
+# fp16 scale fields of random_blocks: weights of standard deviation ~0.02, as N(0, 0.02) weights
+RANDOM_BLOCK_SCALE = {"q8_0": 2.6e-4, "q4_0": 4.3e-3, "q5_0": 2.2e-3, "q4_k": 1e-4, "q6_k": 1.5e-5, "fp16": 3.5e-4}
+
+
+def random_blocks(fmt: str, N: int, K: int, seed: int, scale: float | None = None) -> np.ndarray:
+    """[N, K] weights as uniformly random block bytes with every fp16 scale field set to
+    `scale` times a factor in [0.5, 1.5): valid blocks of every code, ~100x faster to make
+    than quantized Gaussians.  For parity tests at full model size (both sides read the
+    same bytes), not for measurements."""
+    scale = RANDOM_BLOCK_SCALE[fmt] if scale is None else scale
+    rb = row_bytes(fmt, K)
+    rng = np.random.default_rng(seed)
+    out = rng.integers(0, 256, size=N * rb, dtype=np.uint8)
+    if fmt == "fp16":
+        v = (rng.random(N * K, dtype=np.float32) - F32(0.5)) * F32(200.0 * scale)
+        return v.astype(np.float16).view(np.uint8)
+    blk = out.reshape(-1, BLOCK_BYTES[fmt])
+
+    def f16(n):
+        return (F32(scale) * (F32(0.5) + rng.random(n, dtype=np.float32))).astype(np.float16).view(np.uint8).reshape(
+            n, 2)
+
+    nb = blk.shape[0]
+    if fmt in ("q8_0", "q4_0", "q5_0"):
+        blk[:, 0:2] = f16(nb)
+    elif fmt == "q4_k":  # d, dmin
+        blk[:, 0:2] = f16(nb)
+        blk[:, 2:4] = f16(nb)
+    elif fmt == "q6_k":  # d is the last field
+        blk[:, 208:210] = f16(nb)
+    else:
+        raise ValueError(fmt)
+    return out

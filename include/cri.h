@@ -117,7 +117,7 @@ int cri_fused_decode_attention(const float* Q, const float* K_cache, const float
  * uses at most cri_fused_decode_attention_workspace_size() bytes of it (fewer
  * chunks when workspace_bytes is smaller; CRI_ERR_SHAPE below one record per
  * head).  Calls that share a workspace must be ordered on one stream.  Shapes
- * the split kernel does not take (head_dim > 64, head_dim % 4 != 0, Q/K/V not
+ * the split kernel does not take (head_dim > 128, head_dim % 4 != 0, Q/K/V not
  * 16-byte aligned) run cri_fused_decode_attention and leave the workspace
  * untouched. */
 int cri_fused_decode_attention_ws(const float* Q, const float* K_cache, const float* V_cache, float* output,
@@ -217,6 +217,56 @@ int cri_gguf_upload(const cri_gguf* file, int index, void* device_dst, long long
  * FP32, ref:src/model.cu:603); no counterpart in the reference. */
 int cri_embedding_rows(int format, const void* table, const int* ids, float* out, int n_ids, int dim, int vocab,
                        hipStream_t stream);
+
+/* ---- the decode step: TransformerModel::forward's layer loop ---------------
+ * A decoder owns its weights (copied in), activation buffers, KV cache
+ * [n_layers][max_seq_len, n_kv_heads, head_dim] and workspace, all allocated at
+ * create; forward and replay allocate nothing.  The C++ class is
+ * cuinfer::DecodeStep (cuinfer/decode_step.h).  It replaces the quantized path
+ * of TransformerModel::forward, ref:src/model.cu:831-1039 (embedding, per layer
+ * RMSNorm, q/k/v, RoPE, KV append, attention, o, residual + RMSNorm, gate/up,
+ * SiLU * up, down, residual; final RMSNorm, LM head) and the greedy
+ * argmax_sample, ref:src/embedding.cu:305-326.  Batch row m of a call at
+ * position p attends to cache positions [0, p + m] (the reference's causal
+ * mask; one token: its fused decode attention).  The position is kept in
+ * device memory, so a captured step replays correctly token after token. */
+typedef struct cri_decoder cri_decoder;
+typedef struct cri_decoder_config {
+    int n_layers, dim, n_heads, n_kv_heads, head_dim, ffn_dim, vocab_size, max_seq_len;
+    int max_batch; /* tokens per call, 1..65535 (up to 16 use the fused norm prologues) */
+    float rms_norm_eps, rope_theta;
+} cri_decoder_config;
+/* one layer's tensors; weights [N, K] in GGUF row order, in host or device memory
+ * (copied at set time); norms fp32 [dim]; formats: cri_format, not CRI_FP32 */
+typedef struct cri_decoder_layer {
+    const float* attn_norm;
+    const float* ffn_norm;
+    int q_format, k_format, v_format, o_format, gate_format, up_format, down_format;
+    const void *q, *k, *v, *o, *gate, *up, *down;
+} cri_decoder_layer;
+int cri_decoder_create(const cri_decoder_config* config, cri_decoder** out);
+void cri_decoder_destroy(cri_decoder* dec);
+int cri_decoder_set_layer(cri_decoder* dec, int layer, const cri_decoder_layer* weights);
+/* token table [vocab, dim]: a cri_format or CRI_FP32 */
+int cri_decoder_set_embedding(cri_decoder* dec, int format, const void* table);
+/* final norm fp32 [dim] and LM head [vocab, dim]; format -1 ties the head to the token table */
+int cri_decoder_set_output(cri_decoder* dec, const float* output_norm, int format, const void* lm_head);
+/* M tokens (device int32 [M]) at positions position() .. +M-1 -> logits (device fp32 [M, vocab]);
+ * next_ids (device int32 [M] or NULL) <- argmax of each logits row (ties: the smallest index).
+ * CRI_ERR_SHAPE when position() + M would exceed max_seq_len. */
+int cri_decoder_forward(cri_decoder* dec, const int* token_ids, int M, float* logits, int* next_ids,
+                        hipStream_t stream);
+/* capture the same call as one HIP graph on a non-null stream (nothing runs), and replay it:
+ * each replay is one more step of M tokens; next_ids == token_ids generates greedily */
+int cri_decoder_capture(cri_decoder* dec, const int* token_ids, int M, float* logits, int* next_ids,
+                        hipStream_t stream);
+int cri_decoder_replay(cri_decoder* dec, hipStream_t stream);
+/* the sequence position (0 = empty cache); set with a kernel on `stream` */
+int cri_decoder_set_position(cri_decoder* dec, int pos, hipStream_t stream);
+int cri_decoder_position(const cri_decoder* dec);
+/* the layer's K and V cache, [max_seq_len, n_kv_heads, head_dim] fp32 device memory */
+int cri_decoder_kv_cache(cri_decoder* dec, int layer, float** k_cache, float** v_cache);
+long long cri_decoder_weight_bytes(const cri_decoder* dec);
 
 /* ---- diagnostics ---------------------------------------------------------- */
 

@@ -1,0 +1,136 @@
+// decode_step.h -- one transformer step over M tokens with preallocated
+// buffers, built on matmul_dispatch and captured as one HIP graph.
+//
+// The step is the layer loop of TransformerModel::forward's quantized path
+// (ref:src/model.cu:831-1039): token embedding; per layer RMSNorm, the q/k/v
+// projections, RoPE on q and k (ref:src/kernels/elementwise.cu:232-266), the
+// KV-cache append (ref:src/kv_cache.cu:157-211), attention over the cache,
+// the o projection, residual + RMSNorm, gate/up, SiLU * up, down, residual;
+// then the final RMSNorm, the LM head and (optionally) the greedy token
+// (argmax_sample, ref:src/embedding.cu:305-326).  Differences, each deliberate:
+//   * every buffer is allocated once, at construction (the reference allocates
+//     q/k/v, attn_concat and attn_out with Tensor::zeros inside the layer loop,
+//     ref:src/model.cu:906-908, 937, 946, and two device words per argmax);
+//   * q/k/v weights of one format are stored as one [q_dim + 2 kv_dim, dim]
+//     matrix and gate/up as one [2 ffn, dim] matrix (GGUF rows are
+//     independent, so stacking them is a byte concatenation): one launch each;
+//   * for batches of up to 16 tokens the RMSNorm (with the residual add) and
+//     SiLU * up are computed inside the next matmul's activation staging
+//     (matmul_dispatch_rmsnorm / matmul_dispatch_swiglu);
+//   * attention is one split online-softmax kernel for every batch size: row m
+//     of the batch sees the first position() + m + 1 cache positions, which is
+//     the reference's causal mask (ref:src/attention.cu:60-75) for a
+//     multi-token call and its fused decode attention for one token;
+//   * the sequence position lives in device memory and the step's own last
+//     kernel advances it, so a captured step can be replayed for every
+//     following token without being captured again.
+//
+// Weights are copied into the step's own device buffers from host or device
+// memory (hipMemcpyDefault) in their GGUF [N, K] block layout.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <vector>
+
+#include "dispatch.h"
+#include "tensor.h"
+
+namespace cuinfer {
+
+// The ModelConfig fields a step needs (ref:include/cuinfer/model.h:62-76),
+// plus the largest batch (tokens per call) the buffers are sized for.
+struct DecodeStepConfig {
+    int n_layers = 0;
+    int dim = 0;
+    int n_heads = 0;
+    int n_kv_heads = 0;
+    int head_dim = 0;
+    int intermediate_size = 0;
+    int vocab_size = 0;
+    int max_seq_len = 0;
+    float rms_norm_eps = 1e-5f;
+    float rope_theta = 10000.0f;
+    int max_batch = 16;
+};
+
+// A weight matrix [N, K] in GGUF row order, in host or device memory.
+struct WeightRef {
+    WeightFormat format = WeightFormat::Q4_K;
+    const void* data = nullptr;
+};
+
+// One layer's tensors (blk.N.* in a GGUF file); the norms are fp32 [dim].
+struct LayerWeightsRef {
+    const float* attn_norm = nullptr;
+    const float* ffn_norm = nullptr;
+    WeightRef q, k, v, o, gate, up, down;
+};
+
+class DecodeStep {
+public:
+    // Allocates the weights' and activations' buffers and the KV cache
+    // (2 * n_layers * max_seq_len * n_kv_heads * head_dim floats).  Throws
+    // std::invalid_argument for an inconsistent configuration.
+    explicit DecodeStep(const DecodeStepConfig& cfg);
+    ~DecodeStep();
+    DecodeStep(const DecodeStep&) = delete;
+    DecodeStep& operator=(const DecodeStep&) = delete;
+
+    void set_layer(int layer, const LayerWeightsRef& w);
+    // token embedding table [vocab, dim]: FP32 or any matmul format
+    void set_token_embedding(const WeightRef& table);
+    // final norm and LM head [vocab, dim]; lm_head == nullptr ties it to the
+    // token table, kept in that table's format (an FP32 table multiplies
+    // through matmul_transposed_b, as the reference's tied head does)
+    void set_output(const float* output_norm, const WeightRef* lm_head);
+
+    // Runs M tokens (1 <= M <= max_batch) at positions position() ..
+    // position() + M - 1: token ids (device int32 [M]) -> logits (device fp32
+    // [M, vocab]); next_ids (device int32 [M], may be null) receives the
+    // argmax of each logits row.  Enqueued on `stream`; advances position().
+    void forward(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, hipStream_t stream = 0);
+
+    // Captures forward(token_ids, M, logits, next_ids) on `stream` (not the
+    // null stream) as one HIP graph, replacing any earlier capture; nothing
+    // runs and position() is unchanged.  replay() launches it on `stream`:
+    // each replay is one more step of M tokens (next_ids may be token_ids, so
+    // replays generate greedily).
+    void capture(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, hipStream_t stream);
+    void replay(hipStream_t stream);
+
+    int position() const { return pos_host_; }
+    // sets the device position counter (reset = 0) with a kernel on `stream`
+    void set_position(int pos, hipStream_t stream = 0);
+
+    float* k_cache(int layer);  // [max_seq_len, n_kv_heads, head_dim]
+    float* v_cache(int layer);
+    const DecodeStepConfig& config() const { return cfg_; }
+    size_t weight_bytes() const;
+    int captured_batch() const { return graph_m_; }
+
+private:
+    struct Layer;
+    void enqueue(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, hipStream_t stream);
+    void check_ready() const;
+    void attn_block(Layer& L, int li, int M, int& cur, const float*& res, hipStream_t s);
+    void ffn_block(Layer& L, int M, int& cur, const float*& res, hipStream_t s);
+
+    DecodeStepConfig cfg_;
+    int q_dim_ = 0, kv_dim_ = 0, nchunks_ = 0;
+    std::vector<std::unique_ptr<Layer>> layers_;
+    Tensor tok_table_, out_norm_, lm_head_;
+    WeightFormat tok_fmt_ = WeightFormat::FP32, lm_fmt_ = WeightFormat::FP32;
+    bool tok_set_ = false, out_set_ = false, lm_tied_ = false;
+    Tensor k_cache_, v_cache_, pos_dev_;
+    Tensor hid_[2], normed_, qkv_, ctx_, attn_out_, ff_, act_, ffn_out_, attn_ws_;
+    int pos_host_ = 0;
+    hipGraph_t graph_ = nullptr;
+    hipGraphExec_t graph_exec_ = nullptr;
+    int graph_m_ = 0;
+};
+
+}  // namespace cuinfer

@@ -61,6 +61,9 @@ def lib():
             getattr(L, "orc_quantize_" + f).argtypes = [fp, vp, i64]
         for f in ("q8_0", "q4_0", "q6_k", "q4_k"):
             getattr(L, "orc_make_%s_blocks" % f).argtypes = [vp, i32]
+        L.orc_rope.argtypes = [fp, i32, i32, i32, ctypes.c_float]
+        L.orc_argmax.argtypes = [fp, i32]
+        L.orc_argmax.restype = ctypes.c_int32
         L.orc_random_matrix_lcg.argtypes = [fp, i64, ctypes.c_uint32]
         L.orc_randn.argtypes = [fp, i64, ctypes.c_uint64, ctypes.c_float]
         _lib = L
@@ -121,6 +124,26 @@ def matmul_quant(fmt: str, A, Bq, N: int, K: int, rows=None):
     C = np.zeros((M, N), np.float32)
     n0, n1 = (0, N) if rows is None else rows
     lib().orc_matmul_quant_rows(FORMATS[fmt], _p(A), _p(Bq), _p(C), M, N, K, n0, n1)
+    return C
+
+
+def matmul_quant_mt(fmt: str, A, Bq, N: int, K: int, threads=None):
+    """matmul_quant with the output columns split over threads (each thread runs the same
+    sequential per-element arithmetic on its own columns, so the result is bit-identical)."""
+    import concurrent.futures as cf
+
+    A, Bq = _f32(A), _u8(Bq)
+    M = A.shape[0]
+    C = np.zeros((M, N), np.float32)
+    threads = threads or min(16, os.cpu_count() or 4)
+    step = max(1, -(-N // threads))
+    L = lib()
+
+    def run(n0):
+        L.orc_matmul_quant_rows(FORMATS[fmt], _p(A), _p(Bq), _p(C), M, N, K, n0, min(N, n0 + step))
+
+    with cf.ThreadPoolExecutor(threads) as ex:
+        list(ex.map(run, range(0, N, step)))
     return C
 
 
@@ -185,6 +208,76 @@ def silu_mul(gate, up):
     out = np.empty_like(g)
     lib().orc_silu_mul(_p(g), _p(u), _p(out), g.size)
     return out
+
+
+def rope(x, pos, head_dim, n_heads, theta):
+    """RoPE of one token's heads (ref:src/kernels/elementwise.cu:232-257); returns a copy."""
+    out = _f32(x).copy()
+    lib().orc_rope(_p(out), int(pos), head_dim, n_heads, float(theta))
+    return out
+
+
+def argmax(x):
+    """The reference kernel's argmax (ref:src/embedding.cu:155-200)."""
+    x = _f32(x)
+    return int(lib().orc_argmax(_p(x), x.size))
+
+
+def decode_step(model, ids, pos, k_cache, v_cache):
+    """One forward of the tokens `ids` at positions pos .. pos + M - 1, composed from
+    the oracle's functions in the order of the reference's quantized forward pass
+    (ref:src/model.cu:876-1039).  `model`: dict with n_heads, n_kv_heads, head_dim,
+    dim, ffn, vocab, eps, theta, 'tok' (fmt, table bytes or fp32 [vocab, dim]),
+    'layers' (list of dicts: attn_norm, ffn_norm and (fmt, bytes) for q, k, v, o,
+    gate, up, down), 'out_norm' and 'lm' ((fmt, bytes), or None for a head tied to
+    the token table).  k_cache / v_cache: one [max_seq, n_kv_heads, head_dim] fp32
+    array per layer, appended to in place.  Returns (logits [M, vocab], argmax ids)."""
+    H, Hkv, D = model["n_heads"], model["n_kv_heads"], model["head_dim"]
+    dim, F, V = model["dim"], model["ffn"], model["vocab"]
+    eps, theta = model["eps"], model["theta"]
+    M = len(ids)
+    qd, kvd = H * D, Hkv * D
+
+    def mm(w, x, N, K):
+        fmt, data = w
+        return matmul_quant_mt(fmt, x, data, N, K)
+
+    tfmt, table = model["tok"]
+    if tfmt == "fp32":
+        hidden = _f32(np.asarray(table, np.float32).reshape(V, dim)[list(ids)])
+    else:  # the row's blocks dequantized: dequantize + gather
+        rb = dim // BLOCK_ELEMS[tfmt] * BLOCK_BYTES[tfmt]
+        t = _u8(table)
+        hidden = np.stack([dequantize(tfmt, t[i * rb:(i + 1) * rb], dim) for i in ids])
+    layers = model["layers"]
+    # first layer's standalone RMSNorm (ref:src/model.cu:882-885)
+    hidden, normed = rmsnorm_residual(hidden, None, layers[0]["attn_norm"], eps)
+    scale = np.float32(1.0) / np.float32(np.sqrt(np.float32(D)))
+    for i, L in enumerate(layers):
+        q = mm(L["q"], normed, qd, dim)  # ref:src/model.cu:910-918
+        k = mm(L["k"], normed, kvd, dim)
+        v = mm(L["v"], normed, kvd, dim)
+        for t in range(M):  # ref:src/model.cu:921-926
+            q[t] = rope(q[t], pos + t, D, H, theta)
+            k[t] = rope(k[t], pos + t, D, Hkv, theta)
+        k_cache[i][pos:pos + M] = k.reshape(M, Hkv, D)  # KVCache::append, ref:src/kv_cache.cu:157-211
+        v_cache[i][pos:pos + M] = v.reshape(M, Hkv, D)
+        ctx = np.stack([decode_attention(q[t], k_cache[i], v_cache[i], H, Hkv, D, pos + t + 1, scale)
+                        for t in range(M)])  # row t sees positions <= pos + t (ref:src/attention.cu:60-75)
+        attn_out = mm(L["o"], ctx, dim, qd)
+        hidden, normed = rmsnorm_residual(hidden, attn_out, L["ffn_norm"], eps)  # ref:src/model.cu:963-967
+        gate = mm(L["gate"], normed, F, dim)  # ref:src/model.cu:986-994
+        up = mm(L["up"], normed, F, dim)
+        act = silu_mul(gate, up)  # ref:src/model.cu:996-997
+        ffn_out = mm(L["down"], act, dim, F)
+        nxt = layers[i + 1]["attn_norm"] if i + 1 < len(layers) else model["out_norm"]
+        hidden, normed = rmsnorm_residual(hidden, ffn_out, nxt, eps)  # ref:src/model.cu:1008-1018
+    lm = model["lm"] if model["lm"] is not None else model["tok"]
+    if lm[0] == "fp32":  # tied FP32 table, ref:src/model.cu:1027-1029
+        logits = matmul_transposed_b(normed, np.asarray(lm[1], np.float32).reshape(V, dim))
+    else:
+        logits = mm(lm, normed, V, dim)
+    return logits, np.array([argmax(r) for r in logits], np.int32)
 
 
 # ---------------------------------------------------------------- quantizers

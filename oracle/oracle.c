@@ -394,6 +394,39 @@ void orc_silu_mul(const float* gate, const float* up, float* out, int64_t n) {
     }
 }
 
+/* RoPE of one token's heads in place, ref:src/kernels/elementwise.cu:232-257:
+ * pair i of a head (elements 2i, 2i+1) turns by pos / theta^(2i / head_dim),
+ * with the reference's fp32 expressions for the frequency and the angle. */
+void orc_rope(float* qk, int pos, int head_dim, int n_heads, float theta) {
+    const int half = head_dim / 2;
+    for (int h = 0; h < n_heads; ++h) {
+        for (int i = 0; i < half; ++i) {
+            const float freq = 1.0f / powf(theta, (2.0f * (float)i) / (float)head_dim);
+            const float ang = (float)pos * freq;
+            const float c = cosf(ang), s = sinf(ang);
+            float* p = qk + (int64_t)h * head_dim + 2 * i;
+            const float x0 = p[0], x1 = p[1];
+            p[0] = x0 * c - x1 * s;
+            p[1] = x0 * s + x1 * c;
+        }
+    }
+}
+
+/* Greedy token, ref:src/embedding.cu:155-200 (kernel_argmax): the largest value
+ * (NaN never compares larger), the smallest index among equal maxima, starting
+ * from (-FLT_MAX, 0) -- so a row of -inf / NaN gives 0. */
+int32_t orc_argmax(const float* x, int n) {
+    float best = -3.402823466e38f;
+    int32_t bi = 0;
+    for (int i = 0; i < n; ++i) {
+        if (x[i] > best) {
+            best = x[i];
+            bi = i;
+        }
+    }
+    return bi;
+}
+
 /* ---------------------------------------------------------------------------
  * Host quantizers (ref:tests/test_matmul_quant.cu).  std::round is roundf
  * (half away from zero); __float2half is round-to-nearest-even.

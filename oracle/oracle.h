@@ -29,6 +29,12 @@
  *                         row normalises to c / sqrt(c^2 + eps); silu(0) = 0,
  *                         silu(x) -> x and -> 0 at the ends), the residual sum
  *                         exact, scale invariance of the normed row.
+ *   orc_rope            : pos 0 is the identity (bit-exact), each pair keeps its
+ *                         norm, pair 0 turns by exactly pos radians, a turn by
+ *                         p then q equals a turn by p + q (fp64 numpy), and the
+ *                         whole map against an fp64 numpy rotation.
+ *   orc_argmax          : numpy argmax on rows without NaN, ties to the first
+ *                         index, NaN skipped, all -inf / NaN -> 0.
  *   orc_quantize_*      : bit-exact vs the numpy quantizers in cretif_amd/quant.py
  *                         (written separately) and round-trip error bounds.
  */
@@ -86,6 +92,11 @@ void orc_decode_attention_online(const float* Q, const float* Kc, const float* V
 void orc_rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output,
                           float* normed, int rows, int n, float eps);
 void orc_silu_mul(const float* gate, const float* up, float* out, int64_t n);
+
+/* RoPE of n_heads heads of one token in place, ref:src/kernels/elementwise.cu:232-257 */
+void orc_rope(float* qk, int pos, int head_dim, int n_heads, float theta);
+/* argmax with the reference kernel's tie and NaN rules, ref:src/embedding.cu:155-200 */
+int32_t orc_argmax(const float* x, int n);
 
 /* host quantizers restated from ref:tests/test_matmul_quant.cu */
 void orc_quantize_q8_0(const float* x, void* dst, int64_t n);        /* :46-71   */

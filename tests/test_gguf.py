@@ -142,6 +142,23 @@ def test_tensor_past_end_of_file_rejected(tmp_path):
     opens_with_error(str(p), "past the end")
 
 
+def test_overflowing_dimensions_rejected(tmp_path):
+    # {2^62 + 1, 4}: the element count wraps to 4 in 64 bits and the byte size to 16, which would
+    # pass the end-of-file check; the reader must refuse the product instead
+    w = GGUFWriter().add_tensor("w", [(1 << 62) + 1, 4], "f32", b"\0" * 16)
+    opens_with_error(write(tmp_path, w), "overflows")
+    # a Q8_0 tensor whose element count (31 * 2^59) fits but whose byte size (n / 32 * 34) does not
+    w = GGUFWriter().add_tensor("w", [32, 31 << 54], "q8_0", b"\0" * 34)
+    opens_with_error(write(tmp_path, w, "b.gguf"), "overflows")
+
+
+def test_unknown_type_with_overflowing_dims_is_listed(tmp_path):
+    w = GGUFWriter().add_tensor("odd", [1 << 40, 1 << 40], 99, b"\0" * 16)
+    with cri.GGUFFile(write(tmp_path, w)) as f:
+        info = f.tensor(0)
+        assert info["n_elements"] == -1 and info["byte_size"] == -1
+
+
 def test_partial_block_rejected(tmp_path):
     w = GGUFWriter().add_tensor("w", [100], "q8_0", b"\0" * 136)
     opens_with_error(write(tmp_path, w), "not a multiple")

@@ -196,12 +196,20 @@ def test_ws_small_workspace(orc, records):
     assert normwise_rel_err(got, ref) <= ATTN_TOL
 
 
-@pytest.mark.parametrize("H,Hkv,D,T", [(32, 8, 128, 500), (6, 3, 6, 77), (8, 2, 256, 90)])
+@pytest.mark.parametrize("H,Hkv,D,T", [(6, 3, 6, 77), (8, 2, 256, 90), (4, 2, 132, 50)])
 def test_ws_other_shapes_use_workspace_free_kernel(H, Hkv, D, T):
     Q, K, V = make(H, Hkv, D, T, seed=D + T)
     a = run_ws(Q, K, V, H, Hkv, D, T, 0.2)
     b = run(Q, K, V, H, Hkv, D, T, 0.2)
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("H,Hkv,D,T", [(32, 8, 128, 500), (8, 8, 96, 3000), (16, 4, 128, 1)])
+def test_ws_head_dim_up_to_128(orc, H, Hkv, D, T):
+    # head_dim 68..128 takes the split kernel's 8-slice layout
+    Q, K, V = make(H, Hkv, D, T, seed=D + T)
+    got = run_ws(Q, K, V, H, Hkv, D, T, 0.2)
+    assert normwise_rel_err(got, orc.decode_attention(Q, K, V, H, Hkv, D, T, 0.2)) <= ATTN_TOL
 
 
 def test_ws_dominant_position_is_exact():

@@ -1,0 +1,279 @@
+"""GPU parity of the decode step (cri_decoder_*, C++ cuinfer::DecodeStep): the
+BASELINE config-5 step at Llama-3.2-1B shapes -- Q4_K q/k/v/o/gate/up/down
+(2048x2048, 512x2048, 8192x2048, 2048x8192), a Q6_K 128256x2048 LM head, an fp32
+KV cache of 2048 positions ~ N(0, 1), 32 query heads over 8 KV heads -- with the
+values chained through the layers, against the oracle's composition of the
+reference's forward pass (oracle.decode_step: orc_rmsnorm_residual, the
+reference's dequant + sequential matmul, orc_rope, orc_decode_attention per
+causal row, orc_silu_mul, orc_argmax; ref:src/model.cu:876-1039).
+
+Two full-size layers are run (the oracle composes 16 in about 8x the CPU time;
+every layer is the same code).  Weights are random valid blocks
+(quant.random_blocks: std ~0.02) so that the host can make 2 x 61M weights in
+seconds; both sides read the same bytes.
+
+Bars (normwise, ||x - ref||_inf / ||ref||_inf): logits and the appended KV rows
+<= 1e-5 for batches of up to 16 tokens (the fp32-accurate matmul bar; the step
+chains 2 layers of them); 2e-3 for a 17-token batch, which runs the prefill GEMM
+on fp16 operands (its stated bar is 1e-3 per product).  Greedy ids: the GPU's
+argmax of its own logits exactly, and the oracle's wherever the oracle's top two
+logits are further apart than the logits' error bound.  A replayed graph equals
+the eager step bit for bit (the M <= 16 kernels are deterministic)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import normwise_rel_err
+
+torch = pytest.importorskip("torch")
+import cretif_amd as cri  # noqa: E402
+from cretif_amd import quant  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+PREFILL_TOL = 2e-3
+LLAMA = dict(dim=2048, n_heads=32, n_kv_heads=8, head_dim=64, ffn=8192, vocab=128256)
+
+
+def _hip():
+    path = next(ln.split()[-1] for ln in open("/proc/self/maps") if "libamdhip64" in ln)
+    h = ctypes.CDLL(path)
+    h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    return h
+
+
+def to_device(addr, a):
+    a = np.ascontiguousarray(a, np.float32)
+    torch.cuda.synchronize()
+    assert _hip().hipMemcpy(addr, a.ctypes.data, a.nbytes, 1) == 0  # hipMemcpyHostToDevice
+
+
+def from_device(addr, shape):
+    out = np.empty(shape, np.float32)
+    torch.cuda.synchronize()
+    assert _hip().hipMemcpy(out.ctypes.data, addr, out.nbytes, 2) == 0  # hipMemcpyDeviceToHost
+    return out
+
+
+def tiled(fmt, N, K, seed, rows=4096):
+    """N rows from `rows` random rows repeated (the large tables; the row pattern still
+    differs from one tile to the next in position)."""
+    base = quant.random_blocks(fmt, rows, K, seed).reshape(rows, -1)
+    return np.ascontiguousarray(np.tile(base, (-(-N // rows), 1))[:N]).ravel()
+
+
+def make_model(n_layers, dim, n_heads, n_kv_heads, head_dim, ffn, vocab, seed=1100, fmts=None, tok="q8_0",
+               lm="q6_k", big_tables=True):
+    fmts = fmts or {}
+    rng = np.random.default_rng(seed)
+    layers = []
+    for i in range(n_layers):
+        b = seed + 10 * i
+
+        def w(name, n, k, s):
+            f = fmts.get(name, "q4_k")
+            return f, quant.random_blocks(f, n, k, b + s)
+
+        layers.append({
+            "attn_norm": (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32),
+            "ffn_norm": (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32),
+            "q": w("q", n_heads * head_dim, dim, 0), "k": w("k", n_kv_heads * head_dim, dim, 1),
+            "v": w("v", n_kv_heads * head_dim, dim, 2), "o": w("o", dim, n_heads * head_dim, 3),
+            "gate": w("gate", ffn, dim, 4), "up": w("up", ffn, dim, 5), "down": w("down", dim, ffn, 6)})
+    make = tiled if big_tables else (lambda f, n, k, s: quant.random_blocks(f, n, k, s))
+    if tok == "fp32":
+        table = (rng.standard_normal(vocab * dim) * 0.02).astype(np.float32)
+    else:
+        table = make(tok, vocab, dim, seed + 500)
+    return {"n_heads": n_heads, "n_kv_heads": n_kv_heads, "head_dim": head_dim, "dim": dim, "ffn": ffn,
+            "vocab": vocab, "eps": 1e-5, "theta": 500000.0, "tok": (tok, table), "layers": layers,
+            "out_norm": (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32),
+            "lm": None if lm is None else (lm, make(lm, vocab, dim, seed + 501))}
+
+
+def make_decoder(m, max_seq, max_batch=16):
+    d = cri.Decoder(len(m["layers"]), m["dim"], m["n_heads"], m["n_kv_heads"], m["head_dim"], m["ffn"], m["vocab"],
+                    max_seq, max_batch=max_batch, rms_norm_eps=m["eps"], rope_theta=m["theta"])
+    for i, L in enumerate(m["layers"]):
+        d.set_layer(i, L["attn_norm"], L["ffn_norm"], **{k: L[k] for k in ("q", "k", "v", "o", "gate", "up", "down")})
+    d.set_embedding(*m["tok"])
+    d.set_output(m["out_norm"], m["lm"])
+    return d
+
+
+def random_cache(m, T, seed):
+    rng = np.random.default_rng(seed)
+    shape = (T, m["n_kv_heads"], m["head_dim"])
+    return ([rng.standard_normal(shape).astype(np.float32) for _ in m["layers"]],
+            [rng.standard_normal(shape).astype(np.float32) for _ in m["layers"]])
+
+
+def load_cache(dec, kc, vc):
+    for i, (k, v) in enumerate(zip(kc, vc)):
+        ka, va = dec.kv_cache(i)
+        to_device(ka, k)
+        to_device(va, v)
+
+
+def check_ids(got_ids, logits, ref_logits, ref_ids, tol):
+    # the GPU's ids are the argmax (first index of the maximum) of its own logits
+    assert np.array_equal(got_ids, np.argmax(logits, axis=1))
+    bound = 2 * tol * np.max(np.abs(ref_logits))
+    for r in range(ref_logits.shape[0]):
+        top2 = np.sort(ref_logits[r])[-2:]
+        if top2[1] - top2[0] > bound:
+            assert got_ids[r] == ref_ids[r]
+
+
+@pytest.fixture(scope="module")
+def llama2():
+    """Two full-size Llama-3.2-1B layers, Q6_K LM head, Q8_0 token table; cache of 2048."""
+    m = make_model(2, **LLAMA)
+    dec = make_decoder(m, max_seq=2048)
+    return m, dec
+
+
+@pytest.mark.parametrize("M,pos", [(1, 2047), (16, 2032), (1, 0), (5, 700)])
+def test_step_llama_shapes(orc, llama2, M, pos):
+    m, dec = llama2
+    kc, vc = random_cache(m, 2048, 3000 + pos)
+    load_cache(dec, kc, vc)
+    ids = np.random.default_rng(M + pos).integers(0, m["vocab"], M).astype(np.int32)
+    dids = torch.from_numpy(ids).cuda()
+    logits = torch.full((M, m["vocab"]), float("nan"), device="cuda")
+    nxt = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    dec.set_position(pos)
+    dec.forward(dids, M, logits, nxt)
+    assert dec.position == pos + M
+    got = logits.cpu().numpy()
+    ref, ref_ids = orc.decode_step(m, list(ids), pos, kc, vc)
+    err = normwise_rel_err(got, ref)
+    print("decode step M=%d pos=%d: logits normwise err %.2e" % (M, pos, err))
+    assert err <= TOL
+    check_ids(nxt.cpu().numpy(), got, ref, ref_ids, TOL)
+    # the rows appended to every layer's cache: rotated k and plain v.  The rotation angle
+    # pos * freq turns a one-ulp difference in the frequency (fp32 powf here and there) into
+    # pos ulps of the angle, so the k bar adds (pos + M) * 2^-23 to the matmul bar
+    k_tol = TOL + (pos + M) * 2.0 ** -23
+    for i in range(len(m["layers"])):
+        ka, va = dec.kv_cache(i)
+        shape = (2048, m["n_kv_heads"], m["head_dim"])
+        gk, gv = from_device(ka, shape), from_device(va, shape)
+        assert normwise_rel_err(gk[pos:pos + M], kc[i][pos:pos + M]) <= k_tol
+        assert normwise_rel_err(gv[pos:pos + M], vc[i][pos:pos + M]) <= TOL
+        assert np.array_equal(gk[:pos], kc[i][:pos]) and np.array_equal(gk[pos + M:], kc[i][pos + M:])
+
+
+def test_graph_replay_equals_eager_and_generates(orc, llama2):
+    m, dec = llama2
+    kc, vc = random_cache(m, 2048, 77)
+    load_cache(dec, kc, vc)
+    pos0, steps = 1000, 4
+    s = torch.cuda.Stream()
+    ids = torch.tensor([123], dtype=torch.int32, device="cuda")
+    logits = torch.empty(1, m["vocab"], device="cuda")
+    # eager greedy loop
+    eager_ids, eager_logits = [], []
+    dec.set_position(pos0)
+    cur = ids.clone()
+    for _ in range(steps):
+        nxt = torch.empty(1, dtype=torch.int32, device="cuda")
+        dec.forward(cur, 1, logits, nxt)
+        eager_logits.append(logits.cpu().numpy().copy())
+        eager_ids.append(int(nxt.cpu()[0]))
+        cur = nxt
+    # the same loop as replays of one captured step whose next_ids is its token_ids
+    load_cache(dec, kc, vc)
+    buf = ids.clone()
+    with torch.cuda.stream(s):
+        dec.capture(buf, 1, logits, buf, stream=s)
+        dec.set_position(pos0, stream=s)
+        for t in range(steps):
+            dec.replay(stream=s)
+            s.synchronize()
+            assert np.array_equal(logits.cpu().numpy().view(np.uint32), eager_logits[t].view(np.uint32))
+            assert int(buf.cpu()[0]) == eager_ids[t]
+    assert dec.position == pos0 + steps
+    # and the first step against the oracle
+    ref, ref_ids = orc.decode_step(m, [123], pos0, *random_cache(m, 2048, 77))
+    assert normwise_rel_err(eager_logits[0], ref) <= TOL
+
+
+def test_batch16_replay_equals_eager(llama2):
+    m, dec = llama2
+    kc, vc = random_cache(m, 2048, 5)
+    load_cache(dec, kc, vc)
+    M, pos = 16, 100
+    ids = torch.from_numpy(np.arange(M, dtype=np.int32) * 7919).cuda()
+    a = torch.empty(M, m["vocab"], device="cuda")
+    dec.set_position(pos)
+    dec.forward(ids, M, a)
+    eager = a.cpu().numpy().copy()
+    load_cache(dec, kc, vc)
+    s = torch.cuda.Stream()
+    b = torch.empty(M, m["vocab"], device="cuda")
+    with torch.cuda.stream(s):
+        dec.capture(ids, M, b, None, stream=s)
+        dec.set_position(pos, stream=s)
+        dec.replay(stream=s)
+    s.synchronize()
+    assert np.array_equal(b.cpu().numpy().view(np.uint32), eager.view(np.uint32))
+
+
+@pytest.mark.parametrize("M", [17, 3])
+def test_step_mixed_formats_tied_fp32_head(orc, M):
+    # q/k/v and gate/up of different formats (three / two separate matrices), an FP32 token
+    # table tied to the LM head (matmul_transposed_b), head_dim 128 (the 8-slice attention
+    # layout), and for M = 17 the unfused path (rmsnorm_residual, prefill GEMM, silu_mul)
+    m = make_model(2, dim=512, n_heads=4, n_kv_heads=2, head_dim=128, ffn=1024, vocab=1000, seed=7,
+                   fmts={"q": "q8_0", "k": "q4_0", "v": "q5_0", "o": "fp16", "gate": "q6_k", "up": "q4_k",
+                         "down": "q8_0"}, tok="fp32", lm=None, big_tables=False)
+    dec = make_decoder(m, max_seq=256, max_batch=32)
+    kc, vc = random_cache(m, 256, 9)
+    load_cache(dec, kc, vc)
+    pos = 40
+    ids = np.random.default_rng(M).integers(0, m["vocab"], M).astype(np.int32)
+    logits = torch.empty(M, m["vocab"], device="cuda")
+    nxt = torch.empty(M, dtype=torch.int32, device="cuda")
+    dec.set_position(pos)
+    dec.forward(torch.from_numpy(ids).cuda(), M, logits, nxt)
+    got = logits.cpu().numpy()
+    ref, ref_ids = orc.decode_step(m, list(ids), pos, kc, vc)
+    tol = PREFILL_TOL if M > 16 else TOL
+    err = normwise_rel_err(got, ref)
+    print("mixed-format step M=%d: normwise err %.2e" % (M, err))
+    assert err <= tol
+    check_ids(nxt.cpu().numpy(), got, ref, ref_ids, tol)
+
+
+def test_decoder_errors():
+    m = make_model(1, dim=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=100, big_tables=False)
+    with pytest.raises(cri.CretifError):  # n_heads not a multiple of n_kv_heads
+        cri.Decoder(1, 256, 4, 3, 64, 512, 100, 64)
+    with pytest.raises(cri.CretifError):  # head_dim past the attention layout
+        cri.Decoder(1, 256, 1, 1, 256, 512, 100, 64)
+    d = cri.Decoder(1, 256, 4, 2, 64, 512, 100, 8, max_batch=4)
+    ids = torch.zeros(8, dtype=torch.int32, device="cuda")
+    out = torch.empty(8, 100, device="cuda")
+    with pytest.raises(cri.CretifError):  # no weights yet
+        d.forward(ids, 1, out)
+    L = m["layers"][0]
+    d.set_layer(0, L["attn_norm"], L["ffn_norm"], **{k: L[k] for k in ("q", "k", "v", "o", "gate", "up", "down")})
+    d.set_embedding(*m["tok"])
+    d.set_output(m["out_norm"], m["lm"])
+    with pytest.raises(cri.CretifError):  # M above max_batch
+        d.forward(ids, 5, out)
+    d.forward(ids, 4, out)
+    d.forward(ids, 4, out)
+    assert d.position == 8
+    with pytest.raises(cri.CretifError) as e:  # past max_seq_len
+        d.forward(ids, 1, out)
+    assert e.value.status == -2
+    with pytest.raises(cri.CretifError):
+        d.replay()  # nothing captured
+    with pytest.raises(cri.CretifError):
+        d.set_position(9)
+    d.set_position(0)
+    torch.cuda.synchronize()
