@@ -148,6 +148,7 @@ class GemvRig:
             else:
                 cri.matmul(fmt, self.x, Wi, self.y, M, N, K)
 
+        self._run = run
         with torch.cuda.stream(self.stream):
             for Wi in self.W:  # eager warm-up on the side stream
                 run(Wi)
@@ -163,6 +164,39 @@ class GemvRig:
 
     def bytes_per_launch(self):
         return algo_bytes(self.fmt, self.M, self.N, self.K)
+
+    def chain_samples(self, samples):
+        """ms per launch of `samples` consecutive samples of exactly `steps` launches, all in
+        one captured graph with a device timestamp kernel (cri_timestamp, 100 MHz clock)
+        between the samples, so no graph boundary falls inside the timed region (each
+        boundary costs ~13 us on this box).  The graph runs once untimed, once timed; the
+        rotation over the weight copies continues through it.  Also returns the hipEvent
+        time of the whole timed replay (ms), which brackets the samples."""
+        import torch
+
+        K, cri = self.steps, self.cri
+        ts = torch.zeros(samples + 1, dtype=torch.int64, device="cuda")
+        g = torch.cuda.CUDAGraph()
+        n = 0
+        with torch.cuda.graph(g, stream=self.stream):
+            for i in range(samples):
+                cri.timestamp(ts.data_ptr() + 8 * i)
+                for _ in range(K):
+                    self._run(self.W[n % self.copies])
+                    n += 1
+            cri.timestamp(ts.data_ptr() + 8 * samples)
+        torch.cuda.synchronize()
+        g.replay()  # warm-up pass
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(self.stream):
+            e0.record(self.stream)
+            g.replay()
+            e1.record(self.stream)
+        torch.cuda.synchronize()
+        t = ts.cpu().numpy().astype(np.int64)
+        per = [(t[i + 1] - t[i]) * 1e-5 / K for i in range(samples)]  # 100 MHz ticks -> ms per launch
+        return per, e0.elapsed_time(e1)
 
     def samples(self, samples, warmup):
         """ms per launch of each sample (one replay = `steps` launches)."""
@@ -496,7 +530,8 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run ten 64 MiB device copies (known bytes, for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
-    samples = max(5, args.samples)
+    # a sample is exactly --steps launches; the timed graph holds samples x steps of them
+    samples = max(5, min(args.samples, 40000 // max(1, args.steps)))
 
     if args.copy_calibration:
         import torch
@@ -557,11 +592,12 @@ def main():
         return
     fmt, N, K = GEMV_WORKLOADS[args.workload]
     rig = GemvRig(fmt, N, K, steps=max(1, args.steps))
-    per_launch = rig.samples(samples, args.warmup)
+    rig.samples(1, args.warmup)  # W untimed warm-up launches
+    per_launch, event_ms = rig.chain_samples(samples)
     ms = float(np.median(per_launch))
     bpl = rig.bytes_per_launch()
     gbs = bpl / (ms * 1e-3) / 1e9
-    copies, graphs, continuous = rig.copies, len(rig.graphs), rig.continuous
+    copies = rig.copies
     rig.free()
     torch.cuda.empty_cache()
 
@@ -647,10 +683,10 @@ def main():
                    "samples": samples,
                    "us_per_launch_min_median_max": [round(min(per_launch) * 1e3, 3), round(ms * 1e3, 3),
                                                     round(max(per_launch) * 1e3, 3)],
-                   "timing": "%d samples of %d launches (%d captured graph%s replayed in turn%s); hipEvents on the "
-                             "replay stream between the samples; value from the median sample" % (
-                                 samples, rig.steps, graphs, "s" if graphs > 1 else "",
-                                 "" if continuous else "; the rotation restarts every sample")},
+                   "event_ms_all_samples": round(event_ms, 4),
+                   "timing": "%d back-to-back samples of exactly %d launches in one captured graph, a device "
+                             "timestamp (100 MHz clock) between samples; value from the median sample; the "
+                             "hipEvents around the whole replay give event_ms_all_samples" % (samples, rig.steps)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload)},
     }

@@ -113,6 +113,8 @@ ABI_SYMBOLS = (
         "cri_decoder_kv_cache",
         "cri_decoder_weight_bytes",
         "cri_stream_read",
+        "cri_stream_read_ex",
+        "cri_timestamp",
         "cri_last_error_string",
         "cri_block_bytes",
         "cri_block_elems",
@@ -214,6 +216,10 @@ def lib():
     L.cri_silu_mul.restype = i32
     L.cri_embedding_rows.argtypes = [i32, vp, vp, vp, i32, i32, i32, vp]
     L.cri_stream_read.argtypes = [vp, ctypes.c_longlong, vp, vp]
+    L.cri_stream_read_ex.argtypes = [vp, ctypes.c_longlong, vp, i32, i32, vp]
+    L.cri_stream_read_ex.restype = i32
+    L.cri_timestamp.argtypes = [vp, vp]
+    L.cri_timestamp.restype = i32
     L.cri_embedding_rows.restype = i32
     ll = ctypes.c_longlong
     L.cri_gguf_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(vp)]
@@ -471,6 +477,17 @@ def stream_read(src, n_bytes, sink, stream=None):
     bandwidth (a measurement aid).  sink is one device word, written only if the XOR of the words one
     thread reads (four 16-byte chunks, 4096 bytes apart) equals 0x9E3779B9."""
     _check(lib().cri_stream_read(_ptr(src), n_bytes, _ptr(sink), _stream(stream)))
+
+
+def timestamp(dst, stream=None):
+    """cri_timestamp: the GPU's 100 MHz clock into dst (a device int64 tensor element or address)."""
+    _check(lib().cri_timestamp(_ptr(dst), _stream(stream)))
+
+
+def stream_read_ex(src, n_bytes, sink, loads_per_thread=4, grid_blocks=0, stream=None):
+    """cri_stream_read_ex: the streaming-read probe with its launch shape as parameters."""
+    _check(lib().cri_stream_read_ex(_ptr(src), int(n_bytes), _ptr(sink), loads_per_thread, grid_blocks,
+                                    _stream(stream)))
 
 
 _MODEL_FIELDS = ("context_length", "embedding_length", "block_count", "head_count", "head_count_kv",

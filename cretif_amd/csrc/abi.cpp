@@ -343,6 +343,30 @@ int cri_stream_read(const void* src, long long n_bytes, unsigned* sink, hipStrea
     return check_launch(fn);
 }
 
+int cri_timestamp(unsigned long long* dst, hipStream_t s) {
+    const char* fn = "cri_timestamp";
+    if (!dst) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(dst, 8)) return fail(CRI_ERR_ALIGNMENT, fn, "dst must be 8-byte aligned");
+    clear_pending_error();
+    cri::detail::launch_timestamp(dst, s);
+    return check_launch(fn);
+}
+
+int cri_stream_read_ex(const void* src, long long n_bytes, unsigned* sink, int loads_per_thread, int grid_blocks,
+                       hipStream_t s) {
+    const char* fn = "cri_stream_read_ex";
+    if (n_bytes < 0 || n_bytes % 16 != 0)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "n_bytes must be a non-negative multiple of 16");
+    if (grid_blocks < 0) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative grid_blocks");
+    if (n_bytes == 0) return CRI_OK;
+    if (!src || !sink) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(src, 16) || !aligned(sink, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "src must be 16-byte aligned");
+    clear_pending_error();
+    if (cri::detail::launch_stream_read_ex(src, n_bytes, sink, loads_per_thread, grid_blocks, s) != 0)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "loads_per_thread must be 1, 2, 4, 8 or 16");
+    return check_launch(fn);
+}
+
 long long cri_fused_decode_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, int kv_len) {
     const char* fn = "cri_fused_decode_attention_workspace_size";
     if (n_heads < 0 || n_kv_heads < 0 || head_dim < 0 || kv_len < 0)

@@ -92,6 +92,12 @@ int launch_rmsnorm_residual(const float* input, const float* residual, const flo
 int launch_silu_mul(const float* gate, const float* up, float* out, long n, hipStream_t stream);
 // token rows of a (quantized) embedding table, dequantized (elementwise.hip)
 int launch_stream_read(const void* src, long n_bytes, uint32_t* sink, hipStream_t stream);
+// the device's 100 MHz wall clock written to *dst (probe.hip)
+int launch_timestamp(unsigned long long* dst, hipStream_t stream);
+// per 16-byte loads per thread in flight (1, 2, 4, 8, 16); grid_blocks 0: one pass of a grid
+// covering the buffer, else that many blocks of 256 threads striding over it
+int launch_stream_read_ex(const void* src, long n_bytes, uint32_t* sink, int per, long grid_blocks,
+                          hipStream_t stream);
 int launch_embedding_rows(int fmt, const void* table, const int* ids, float* out, int n_ids, int dim, int vocab,
                           hipStream_t stream);
 

@@ -277,6 +277,20 @@ long long cri_decoder_weight_bytes(const cri_decoder* dec);
  * equals 0x9E3779B9.  A measurement aid with no counterpart in the reference. */
 int cri_stream_read(const void* src, long long n_bytes, unsigned* sink, hipStream_t stream);
 
+/* cri_stream_read with the launch shape as parameters, for sweeping it:
+ * loads_per_thread (1, 2, 4, 8 or 16) 16-byte loads in flight per thread;
+ * grid_blocks 0 covers the buffer once with one pass per thread, otherwise
+ * that many workgroups of 256 threads stride over it.  cri_stream_read is
+ * (4, 0).  A measurement aid with no counterpart in the reference. */
+int cri_stream_read_ex(const void* src, long long n_bytes, unsigned* sink, int loads_per_thread, int grid_blocks,
+                       hipStream_t stream);
+
+/* Writes the GPU's constant 100 MHz clock (wall_clock64) to *dst (device, 8-byte
+ * aligned) from a one-wave kernel on `stream`: timestamps between the kernels of
+ * a captured graph, where events cannot be recorded.  A measurement aid with no
+ * counterpart in the reference. */
+int cri_timestamp(unsigned long long* dst, hipStream_t stream);
+
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* cri_last_error_string(void);
 /* Bytes per block / elements per block of a format (0 if unknown). */
