@@ -39,6 +39,7 @@ __all__ = [
     "batched_matmul_gqa",
     "fused_decode_attention",
     "fused_decode_attention_ws",
+    "fused_decode_attention_noalloc",
     "decode_attention_workspace_size",
     "matmul_rmsnorm",
     "matmul_swiglu",
@@ -77,6 +78,7 @@ ABI_SYMBOLS = (
         "cri_batched_matmul_gqa",
         "cri_fused_decode_attention",
         "cri_fused_decode_attention_ws",
+        "cri_fused_decode_attention_noalloc",
         "cri_fused_decode_attention_workspace_size",
         "cri_matmul_rmsnorm",
         "cri_matmul_swiglu",
@@ -204,6 +206,8 @@ def lib():
     L.cri_fused_decode_attention_ws.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp,
                                                  ctypes.c_longlong, vp]
     L.cri_fused_decode_attention_ws.restype = i32
+    L.cri_fused_decode_attention_noalloc.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp]
+    L.cri_fused_decode_attention_noalloc.restype = i32
     L.cri_fused_decode_attention_workspace_size.argtypes = [i32, i32, i32, i32]
     L.cri_fused_decode_attention_workspace_size.restype = ctypes.c_longlong
     L.cri_matmul_rmsnorm.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i32, i32, ctypes.c_float, vp]
@@ -429,6 +433,14 @@ def fused_decode_attention_ws(Q, K_cache, V_cache, output, n_heads, n_kv_heads, 
             _stream(stream),
         )
     )
+
+
+def fused_decode_attention_noalloc(Q, K_cache, V_cache, output, n_heads, n_kv_heads, head_dim, kv_len, scale,
+                                   stream=None):
+    """cri_fused_decode_attention_noalloc: the split form with its records in the library's
+    static per-GPU scratch (no workspace, no allocation; calls on one GPU must not overlap)."""
+    _check(lib().cri_fused_decode_attention_noalloc(_ptr(Q), _ptr(K_cache), _ptr(V_cache), _ptr(output), n_heads,
+                                                    n_kv_heads, head_dim, kv_len, float(scale), _stream(stream)))
 
 
 def _fid(fmt):

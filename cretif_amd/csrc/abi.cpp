@@ -411,6 +411,39 @@ int cri_fused_decode_attention_ws(const float* Q, const float* K_cache, const fl
     return check_launch(fn);
 }
 
+int cri_fused_decode_attention_noalloc(const float* Q, const float* K_cache, const float* V_cache, float* output,
+                                       int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale,
+                                       hipStream_t s) {
+    const char* fn = "cri_fused_decode_attention_noalloc";
+    if (n_heads < 0 || n_kv_heads < 0 || head_dim < 0 || kv_len < 0)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative dimension");
+    if (n_heads == 0 || head_dim == 0) return CRI_OK;
+    if (n_kv_heads == 0 || n_heads % n_kv_heads != 0)
+        return fail(CRI_ERR_SHAPE, fn, "n_heads is not a multiple of n_kv_heads");
+    if (kv_len == 0) return fail(CRI_ERR_SHAPE, fn, "kv_len must be at least 1");
+    if (!Q || !K_cache || !V_cache || !output) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!cri::detail::decode_attention_split_supported(Q, K_cache, V_cache, head_dim))
+        return fail(CRI_ERR_UNSUPPORTED, fn,
+                    "needs 4 | head_dim <= " + std::to_string(cri::detail::kDecodeAttnSplitMaxHeadDim) +
+                        " and 16-byte aligned Q, K_cache, V_cache");
+    if (!aligned(output, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "output must be 4-byte aligned");
+    if (static_cast<long>(kv_len) * n_kv_heads * head_dim > kMaxElems) return fail(CRI_ERR_SHAPE, fn, "problem too large");
+    const long rec = static_cast<long>(n_heads) * (head_dim + 4) * 4;
+    if (rec > cri::detail::kNoallocScratchBytes)
+        return fail(CRI_ERR_SHAPE, fn,
+                    "one partial record per head needs " + std::to_string(rec) + " bytes, more than the " +
+                        std::to_string(cri::detail::kNoallocScratchBytes) + "-byte static scratch");
+    clear_pending_error();
+    float* ws = nullptr;
+    if (cri::detail::noalloc_scratch(&ws) != 0)
+        return fail(CRI_ERR_LAUNCH, fn, "hipGetSymbolAddress of the static scratch failed");
+    const int rc = cri::detail::launch_decode_attention_split(Q, K_cache, V_cache, output, n_heads, n_kv_heads,
+                                                              head_dim, kv_len, scale, ws,
+                                                              cri::detail::kNoallocScratchBytes, s);
+    if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
+    return check_launch(fn);
+}
+
 int cri_embedding_rows(int format, const void* table, const int* ids, float* out, int n_ids, int dim, int vocab,
                        hipStream_t s) {
     const char* fn = "cri_embedding_rows";

@@ -23,8 +23,16 @@
 //     values of its own position;
 // and at the end the wave's lanes, then the workgroup's waves, are merged
 // (max, rescale, sum) in a fixed order.
+#include <atomic>
+
 #include "common.hpp"
 #include "internal.hpp"
+
+// Partial softmax records of cri_fused_decode_attention_noalloc: one array per
+// GPU, held until the process ends.  Host code never uses this name as an
+// address (in host code it is a stand-in, not device memory): the device
+// address comes from hipGetSymbolAddress, once per device (noalloc_scratch).
+static __device__ __align__(256) float scratch[cri::detail::kNoallocScratchBytes / sizeof(float)];
 
 namespace cri {
 namespace dev {
@@ -484,6 +492,23 @@ int launch_decode_attention_split(const float* Q, const float* K, const float* V
     if (nchunks < 1) return -2;  // workspace too small for one record per head
     return launch_decode_attention_rows(Q, 0, K, V, out, 0, 1, n_heads, n_kv_heads, head_dim, nullptr, kv_len,
                                         nchunks, scale, ws, stream);
+}
+
+int noalloc_scratch(float** out) {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<float*> ptrs[kMaxDevices];
+    int devid = 0;
+    if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return kFailed;
+    float* p = ptrs[devid].load(std::memory_order_acquire);
+    if (!p) {
+        void* addr = nullptr;
+        // with this device current: its own copy of the array
+        if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr) return kFailed;
+        p = static_cast<float*>(addr);
+        ptrs[devid].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return 0;
 }
 
 int launch_decode_attention(const float* Q, const float* K, const float* V, float* out, int n_heads, int n_kv_heads,

@@ -133,6 +133,11 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
                                  int rows, int n_heads, int n_kv_heads, int head_dim, const int* kv_dev, int kv0,
                                  int nchunks, float scale, float* ws, hipStream_t stream);
 
+// cri_fused_decode_attention_noalloc: its records live in a file-scope device array of this
+// many bytes (attention.hip); noalloc_scratch gives the current device's address of it
+constexpr long kNoallocScratchBytes = 1L << 20;
+int noalloc_scratch(float** out);
+
 // decode step neighbours (step_kernels.hip)
 // RoPE of the rows' q and k at positions *pos + m (ref:src/kernels/elementwise.cu:232-266),
 // q rotated in place, rotated k and v written to the caches' rows *pos + m

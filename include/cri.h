@@ -123,6 +123,21 @@ int cri_fused_decode_attention(const float* Q, const float* K_cache, const float
 int cri_fused_decode_attention_ws(const float* Q, const float* K_cache, const float* V_cache, float* output,
                                   int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale,
                                   void* workspace, long long workspace_bytes, hipStream_t stream);
+/* No counterpart in the reference: cri_fused_decode_attention_ws without a
+ * workspace argument and without any allocation, for callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid it).  The partial records live in a static device array of 1 MiB per
+ * GPU (held until the process ends; every record is written before it is read,
+ * so nothing needs clearing): fewer position chunks are used when a shape's
+ * records would not fit, and CRI_ERR_SHAPE is returned when one record per head,
+ * n_heads * (head_dim + 4) * 4 bytes, exceeds 1 MiB.  Needs 4 | head_dim <= 128
+ * and 16-byte aligned Q, K_cache, V_cache (CRI_ERR_UNSUPPORTED otherwise).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams, or host threads) race and must be ordered by the caller.
+ * The result equals cri_fused_decode_attention_ws's for the same shape. */
+int cri_fused_decode_attention_noalloc(const float* Q, const float* K_cache, const float* V_cache, float* output,
+                                       int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale,
+                                       hipStream_t stream);
 /* Workspace bytes cri_fused_decode_attention_ws uses for this shape (0 for an
  * empty problem; a negative cri_status for invalid arguments). */
 long long cri_fused_decode_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, int kv_len);
