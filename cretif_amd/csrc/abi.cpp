@@ -88,6 +88,8 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
         rc = cri::detail::launch_skinny(fmt, A, B, C, M, N, K, stream);
     else if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv(fmt, A, B, C, N, K, stream);
+    else if (M > kPrefillMinM && cri::detail::prefill_supported(fmt, M, N, K, A, B))
+        rc = cri::detail::launch_prefill(fmt, A, B, C, M, N, K, stream);
     else if (M > kPrefillMinM && cri::detail::mfma_gemm_supported(fmt, M, N, K, A, B))
         rc = cri::detail::launch_mfma_gemm(fmt, A, B, C, M, N, K, stream);
     else if (M <= 16 && fmt32 && K <= 4096 && cri::detail::gemv_supported(fmt, K, B))

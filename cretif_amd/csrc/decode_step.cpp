@@ -135,6 +135,24 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     ffn_out_ = Tensor::empty({MB, static_cast<int64_t>(c.dim)});
     nchunks_ = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len);
     attn_ws_ = Tensor::empty({MB * c.n_heads * nchunks_ * (c.head_dim + 4)});
+    // zeroed once; the argmax kernel that counts in them leaves them zero again
+    argmax_part_ = Tensor::empty({MB * cri::detail::argmax_slices(c.vocab_size) * 2});
+    argmax_count_ = Tensor::zeros({MB});
+    // RoPE (cos, sin) per (position, pair), ref:src/kernels/elementwise.cu:241-248: the frequency
+    // 1 / theta^(2i / head_dim) and the angle pos * freq with the reference's fp32 operations,
+    // theta^e, cos and sin in double rounded once to fp32
+    const int half = c.head_dim / 2;
+    std::vector<float> rot(static_cast<size_t>(c.max_seq_len) * half * 2);
+    for (int i = 0; i < half; ++i) {
+        const float e = (2.0f * static_cast<float>(i)) / static_cast<float>(c.head_dim);
+        const float freq = 1.0f / static_cast<float>(std::pow(static_cast<double>(c.rope_theta), static_cast<double>(e)));
+        for (int p = 0; p < c.max_seq_len; ++p) {
+            const float ang = static_cast<float>(p) * freq;
+            rot[(static_cast<size_t>(p) * half + i) * 2] = static_cast<float>(std::cos(static_cast<double>(ang)));
+            rot[(static_cast<size_t>(p) * half + i) * 2 + 1] = static_cast<float>(std::sin(static_cast<double>(ang)));
+        }
+    }
+    rope_ = Tensor::from_host(rot.data(), {static_cast<int64_t>(rot.size())});
 }
 
 DecodeStep::~DecodeStep() {
@@ -314,7 +332,8 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
     }
     const int* pos = static_cast<const int*>(pos_dev_.data());
     check_status(cri::detail::launch_rope_append(q, ldq, k, ldk, v, ldv, M, cfg_.n_heads, cfg_.n_kv_heads,
-                                                 cfg_.head_dim, cfg_.rope_theta, pos, k_cache(li), v_cache(li), s),
+                                                 cfg_.head_dim, rope_.data_as<float>(), pos, k_cache(li),
+                                                 v_cache(li), s),
                  "rope/append");
     // row m attends to positions [0, pos + m] (ref:src/attention.cu:60-75; one token: :410-511)
     const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
@@ -396,8 +415,13 @@ void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next
         else
             matmul_dispatch(normed_.data_as<float>(), W, logits, M, V, D, wf, s);
     }
-    if (next_ids) check_status(cri::detail::launch_argmax_rows(logits, V, M, V, next_ids, s), "argmax");
-    check_status(cri::detail::launch_pos_add(static_cast<int*>(pos_dev_.data()), M, s), "position update");
+    int* pos = static_cast<int*>(pos_dev_.data());
+    if (next_ids)  // the argmax's last workgroup also advances the position
+        check_status(cri::detail::launch_argmax_rows(logits, V, M, V, next_ids, argmax_part_.data_as<float>(),
+                                                     static_cast<unsigned*>(argmax_count_.data()), pos, M, s),
+                     "argmax");
+    else
+        check_status(cri::detail::launch_pos_add(pos, M, s), "position update");
 }
 
 void DecodeStep::forward(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s) {

@@ -80,6 +80,10 @@ int launch_skinny_act(int mode, int fmt, const ActIn& act, const void* B, float*
 bool mfma_gemm_supported(int fmt, int M, int N, int K, const void* A, const void* B);
 int launch_mfma_gemm(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
 
+// multi-token GEMM with weights decoded straight into MFMA operands, Q4_K and Q8_0 (prefill.hip)
+bool prefill_supported(int fmt, int M, int N, int K, const void* A, const void* B);
+int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+
 // any-M fused dequant matmul, element-wise decode (generic.hip)
 int launch_generic_matmul(int fmt, const float* A, const void* B, float* C, int M, int N, int K,
                           hipStream_t stream);
@@ -141,13 +145,18 @@ int noalloc_scratch(float** out);
 // decode step neighbours (step_kernels.hip)
 // RoPE of the rows' q and k at positions *pos + m (ref:src/kernels/elementwise.cu:232-266),
 // q rotated in place, rotated k and v written to the caches' rows *pos + m
-// (KVCache::append, ref:src/kv_cache.cu:157-211); caches [max_seq, n_kv_heads, head_dim]
+// (KVCache::append, ref:src/kv_cache.cu:157-211); caches [max_seq, n_kv_heads, head_dim];
+// rot: the (cos, sin) table [max_seq, head_dim / 2] of fp32 pairs
 int launch_rope_append(float* q, long ldq, const float* k, long ldk, const float* v, long ldv, int rows, int n_heads,
-                       int n_kv_heads, int head_dim, float theta, const int* pos, float* k_cache, float* v_cache,
+                       int n_kv_heads, int head_dim, const float* rot, const int* pos, float* k_cache, float* v_cache,
                        hipStream_t stream);
 // out[m] = index of the largest logits[m][i], the smallest index among equal maxima, NaN ignored
-// (kernel_argmax, ref:src/embedding.cu:155-200)
-int launch_argmax_rows(const float* logits, long ld, int rows, int n, int* out, hipStream_t stream);
+// (kernel_argmax, ref:src/embedding.cu:155-200); rows are cut into argmax_slices(n) slices whose
+// (value, index) go to part (2 floats each, rows * slices); counters: rows zeroed words (re-zeroed
+// by the kernel); *pos += pos_add at the end when pos is not null
+int argmax_slices(int n);
+int launch_argmax_rows(const float* logits, long ld, int rows, int n, int* out, float* part, unsigned* counters,
+                       int* pos, int pos_add, hipStream_t stream);
 // *pos += delta / *pos = value
 int launch_pos_add(int* pos, int delta, hipStream_t stream);
 int launch_pos_set(int* pos, int value, hipStream_t stream);

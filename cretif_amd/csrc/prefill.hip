@@ -1,0 +1,538 @@
+// prefill.hip -- fused dequant GEMM for multi-token (prefill) batches on the
+// matrix cores, C[M,N] = A[M,K] * dequant(B[N,K])^T, for the Q4_K and Q8_0
+// weights of BASELINE's prefill configuration (the other formats keep the
+// LDS-staged kernel of mfma_gemm.hip).
+//
+// The reference computes the product with one fp32 FMA chain per output
+// (ref:src/kernels/matmul_quant.cu:64-130 Q8_0, :309-386 Q4_K).  Here:
+//   * a workgroup of eight waves (two per SIMD, so one wave's dependency
+//     stalls are filled by the other's work) owns a 64(m) x 256(n) output
+//     tile; wave w owns the 32 weight rows [32 w, 32 w + 32) and all 64 m, as
+//     two v_mfma_f32_32x32x16_f16 tiles (32 fp32 accumulators per lane);
+//   * activations are the MFMA A operand: each k step (64 columns) every
+//     thread converts 8 fp32 values of two rows to fp16 and writes them to a
+//     double-buffered LDS tile of 64 rows x 64 halves, which all eight waves
+//     read (8 ds_read_b128 per wave and step);
+//   * weights are the B operand and never touch LDS: each lane decodes the
+//     bytes of its own weight row (its output column) in registers, to the
+//     reference's dequantized value rounded once to fp16 (Q8_0: d * q; Q4_K:
+//     d * (sc * q) - dmin * mn, sc * q exact), two weights per packed op;
+//   * a lane's bytes of one step are one contiguous run (Q4_K: 16 quant bytes
+//     of the super-block chunk; Q8_0: one whole 34-byte block), so the 8 k of
+//     each MFMA sub-step are not consecutive k; the activation fragment of
+//     every sub-step is fetched from the LDS columns of the same k, so the
+//     products and sums are the same as in k order;
+//   * a lane's outputs are C[m][n] for its column n and 16 rows m, so the 32
+//     lanes of a half-wave store 128 contiguous bytes of one row;
+//   * the eight m blocks that share a weight block are consecutive workgroups
+//     on one XCD (each XCD has its own L2), so the weights come from HBM once;
+//     when the tiles cannot fill 256 CUs the k range is split over workgroups
+//     that add into a zeroed C with fp32 atomics.
+// Activations outside fp16's comfortable range would lose the 1e-3 bound (a
+// value >= 65504 becomes inf; a row whose largest magnitude is below 2^-10
+// keeps only subnormal precision), so each thread tracks the largest
+// magnitude of its rows; the rows flagged that way are recomputed in fp32 from
+// the reference's per-element decode at the end of the tile (the fp16 MFMA
+// results of those rows are not stored).  Dequantized weights must fit fp16
+// (|x| < 65504), as every GGUF model's do.
+#include <atomic>
+#include <type_traits>
+
+#include "common.hpp"
+#include "decode.hpp"
+#include "internal.hpp"
+
+namespace cri {
+namespace dev {
+namespace {
+
+typedef _Float16 ph8 __attribute__((ext_vector_type(8)));
+typedef _Float16 ph2 __attribute__((ext_vector_type(2)));
+typedef float pf16v __attribute__((ext_vector_type(16)));
+typedef float pf2 __attribute__((ext_vector_type(2)));
+typedef uint32_t pu2 __attribute__((ext_vector_type(2)));
+typedef uint32_t pu4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+constexpr int kPTM = 64, kPTN = 256, kPKS = 64, kPThreads = 512;
+constexpr int kPStage = kPTM * kPKS * 2;  // one fp16 activation tile, bytes
+constexpr uint32_t kPMagic = 0x64646464u;
+constexpr float kPRowMax = 65504.0f;      // at or above: fp16 infinity
+constexpr float kPRowMin = 0x1p-10f;      // below (and nonzero): subnormal precision only
+
+__device__ __forceinline__ uint32_t p_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+// bytes b0, b1 (lo) or b2, b3 (hi) of w as the fp16 pair (1024 + b, 1024 + b')
+__device__ __forceinline__ uint32_t p_mlo(uint32_t w) { return p_perm(kPMagic, w, 0x04010400u); }
+__device__ __forceinline__ uint32_t p_mhi(uint32_t w) { return p_perm(kPMagic, w, 0x04030402u); }
+// byte P of w as the fp16 pair (1024 + b, 1024 + b)
+template <int P>
+__device__ __forceinline__ uint32_t p_msplat(uint32_t w) {
+    return p_perm(kPMagic, w, 0x04000400u | (P << 16) | P);
+}
+__device__ __forceinline__ constexpr uint32_t p_const(float lo, float hi) {
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))) << 16);
+}
+__device__ __forceinline__ uint32_t p_fma(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(ph2, a), __builtin_bit_cast(ph2, b),
+                                                                  __builtin_bit_cast(ph2, c)));
+}
+__device__ __forceinline__ uint32_t p_add(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(ph2, a) + __builtin_bit_cast(ph2, b));
+}
+__device__ __forceinline__ uint32_t p_mul(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(ph2, a) * __builtin_bit_cast(ph2, b));
+}
+
+// ---------------------------------------------------------------------------
+// B-operand formats.  A wave's weight bytes of one group (four k steps) are
+// kRowBytes consecutive bytes of each of its 32 rows; they are copied into a
+// per-wave LDS area row after row with coalesced 16-byte loads (kRowBytes / 16
+// lanes per row), so each cache line is requested once.  read<J>(): one
+// lane's bytes of step J of the group from that area.  prep<J>(): the step's
+// scale constants.  sub<S>(): the 8 fp16 weights (4 dwords) of MFMA sub-step
+// S.  chunk(S, h): which 8-column chunk of the 64-column step those 8 weights
+// are, so the activation fragment is fetched from the same k.  Splits start
+// on a multiple of four steps, so J = step mod 4 is a compile-time position.
+
+// ref:src/kernels/dequantize.cu:289-324.  Step j of a super-block is its
+// 64-element chunk j: elements 64j + e (e < 32) are the low nibbles of
+// qs[32j + e] in sub-block 2j, elements 64j + 32 + e the high nibbles in
+// sub-block 2j + 1; x = d * sc * q - dmin * mn.  Lane half h takes qs[32j +
+// 16h .. + 16): sub-steps 0, 1 are the low nibbles of its bytes 0..7, 8..15
+// (k = 64j + 16h + 0..15), sub-steps 2, 3 their high nibbles (k + 32).  A
+// group is one super-block (144 bytes per row).
+struct PQ4K {
+    static constexpr int kBlockK = 256;
+    static constexpr int kRowBytes = 144;
+    static __device__ __forceinline__ long group_offset(int first_step) { return (first_step >> 2) * 144L; }
+    struct Frag {
+        u32x4 hdr;  // d, dmin (fp16), scales[12]
+        u32x4 qs;   // qs[32j + 16h .. + 16)
+    };
+    template <int J>
+    static __device__ __forceinline__ void read(Frag& f, const char* row, int h) {
+        f.hdr = *reinterpret_cast<const u32x4*>(row);
+        f.qs = *reinterpret_cast<const u32x4*>(row + 16 + 32 * J + 16 * h);
+    }
+    static __device__ __forceinline__ constexpr int chunk(int s, int h) { return 4 * (s >> 1) + 2 * h + (s & 1); }
+    struct Consts {
+        uint32_t a[2], c[2], m[2], d2;  // fp16 pairs; [0]: low nibbles, [1]: high nibbles
+    };
+    // 6-bit (sc, mn) of sub-blocks 2J and 2J + 1 (ref:src/kernels/dequantize.cu:298-305),
+    // as bytes of a dword: J < 2 takes scales[0..3] / [4..7] & 63, J >= 2 the
+    // split encoding (scales[8..11] nibbles + top bits of scales[0..3] / [4..7])
+    template <int J>
+    static __device__ __forceinline__ void prep(const Frag& f, Consts& k) {
+        uint32_t scd, mnd;
+        if constexpr (J < 2) {
+            scd = f.hdr.y & 0x3F3F3F3Fu;
+            mnd = f.hdr.z & 0x3F3F3F3Fu;
+        } else {
+            scd = (f.hdr.w & 0x0F0F0F0Fu) | ((f.hdr.y >> 2) & 0x30303030u);
+            mnd = ((f.hdr.w >> 4) & 0x0F0F0F0Fu) | ((f.hdr.z >> 2) & 0x30303030u);
+        }
+        constexpr int b0 = 2 * (J & 1);
+        const uint32_t m1024 = p_const(-1024.0f, -1024.0f);
+        const uint32_t sc0 = p_add(p_msplat<b0>(scd), m1024), sc1 = p_add(p_msplat<b0 + 1>(scd), m1024);
+        const uint32_t mn0 = p_add(p_msplat<b0>(mnd), m1024), mn1 = p_add(p_msplat<b0 + 1>(mnd), m1024);
+        const uint32_t nd = p_perm(f.hdr.x, f.hdr.x, 0x03020302u) ^ 0x80008000u;  // (-dmin, -dmin)
+        k.d2 = p_perm(f.hdr.x, f.hdr.x, 0x01000100u);
+        // low nibbles: (1024 + q) sc - 1024 sc = sc q exactly (<= 945);
+        // high nibbles masked in place are 16 q: (1024 + 16 q) sc/16 - 64 sc
+        k.a[0] = sc0;
+        k.c[0] = p_mul(sc0, p_const(-1024.0f, -1024.0f));
+        k.a[1] = p_mul(sc1, p_const(0.0625f, 0.0625f));
+        k.c[1] = p_mul(sc1, p_const(-64.0f, -64.0f));
+        k.m[0] = p_mul(mn0, nd);
+        k.m[1] = p_mul(mn1, nd);
+    }
+    // B fragment of sub-step S: d (sc q) - dmin mn, one rounding to fp16
+    template <int S>
+    static __device__ __forceinline__ void sub(const Frag& f, const Consts& k, uint32_t (&b)[4]) {
+        constexpr int hi = S >= 2 ? 1 : 0;
+        constexpr uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+        const uint32_t src[2] = {(S & 1) ? f.qs.z : f.qs.x, (S & 1) ? f.qs.w : f.qs.y};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t u = src[i] & mask;
+            b[2 * i] = p_fma(p_fma(p_mlo(u), k.a[hi], k.c[hi]), k.d2, k.m[hi]);
+            b[2 * i + 1] = p_fma(p_fma(p_mhi(u), k.a[hi], k.c[hi]), k.d2, k.m[hi]);
+        }
+    }
+};
+
+// ref:src/kernels/dequantize.cu:45-47, x = d * q.  Step j covers the 34-byte
+// blocks 2j and 2j + 1; lane half h decodes block 2j + h whole (sub-step S:
+// its elements 8S .. 8S + 7, k = 64j + 32h + 8S ..).  K % 64 == 0 makes a
+// row an even number of blocks, so a group (four steps, 272 bytes per row)
+// starts dword-aligned; block 2j + h starts at byte 68j + 34h of it, its
+// quants at 68j + 34h + 2.  A lane reads the 9 dwords from byte 68j + 32h
+// and funnel-shifts its quants by 2 (h = 0) or 4 (h = 1) bytes.
+struct PQ8_0 {
+    static constexpr int kBlockK = 32;
+    static constexpr int kRowBytes = 272;
+    static __device__ __forceinline__ long group_offset(int first_step) { return first_step * 68L; }
+    struct Frag {
+        uint32_t dw[9];
+    };
+    template <int J>
+    static __device__ __forceinline__ void read(Frag& f, const char* row, int h) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 68 * J + 32 * h);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) f.dw[i] = p[i];
+    }
+    static __device__ __forceinline__ constexpr int chunk(int s, int h) { return 4 * h + s; }
+    struct Consts {
+        uint32_t d2, sel;
+    };
+    template <int J>
+    static __device__ __forceinline__ void prep(const Frag& f, Consts& k) {
+        const bool h1 = (__lane_id() >> 5) != 0;
+        k.d2 = p_perm(f.dw[0], f.dw[0], h1 ? 0x03020302u : 0x01000100u);
+        k.sel = h1 ? 0x07060504u : 0x05040302u;  // dword pair -> quants shifted by 4 or 2 bytes
+    }
+    // B fragment of sub-step S: d * q, one rounding to fp16
+    template <int S>
+    static __device__ __forceinline__ void sub(const Frag& f, const Consts& k, uint32_t (&b)[4]) {
+        const uint32_t bias = p_const(-1152.0f, -1152.0f);  // 1024 + 128
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t q = p_perm(f.dw[2 * S + i + 1], f.dw[2 * S + i], k.sel);
+            const uint32_t x = q ^ 0x80808080u;  // int8 -> q + 128
+            b[2 * i] = p_mul(p_add(p_mlo(x), bias), k.d2);
+            b[2 * i + 1] = p_mul(p_add(p_mhi(x), bias), k.d2);
+        }
+    }
+};
+
+// LDS activation tile: row r (128 bytes) holds 8 chunks of 8 halves; chunk c is
+// stored in slot c ^ (r & 7) ^ ((r >> 3) & 1) (conflict-free for 32-row
+// operand fetches, one chunk per half-wave).
+__device__ __forceinline__ int p_off(int r, int c) { return (r << 7) + ((c ^ (r & 7) ^ ((r >> 3) & 1)) << 4); }
+
+template <int J>
+using pos_t = std::integral_constant<int, J>;
+
+// dynamic LDS: two activation buffers of four step tiles, then one weight area per wave
+template <class W>
+constexpr int prefill_lds_bytes() {
+    return 8 * kPStage + (kPThreads / 64) * 32 * W::kRowBytes;
+}
+
+template <class W>
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_gemm_kernel(
+    const float* __restrict__ A, const uint8_t* __restrict__ B, float* __restrict__ C, int M, int N, int K,
+    long row_bytes, int MT, int NT, int steps_per_split, int remap, int atomic) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    int* const rowflag = reinterpret_cast<int*>(lds);  // after the k loop
+    int bid = blockIdx.x;
+    if (remap) {  // XCD x (= bid % 8) runs a contiguous run of logical tiles
+        const int per_xcd = gridDim.x >> 3;
+        bid = (bid & 7) * per_xcd + (bid >> 3);
+    }
+    const int mt = bid % MT;  // the m blocks of one weight block are consecutive
+    const int rest = bid / MT;
+    const int nt = rest % NT;
+    const int ksplit = rest / NT;
+    const int s_begin = ksplit * steps_per_split;
+    const int s_end = min(K / kPKS, s_begin + steps_per_split);
+    if (s_begin >= s_end) return;
+    const int nst = s_end - s_begin;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, fr = lane & 31;
+    const int m0 = mt * kPTM, n0 = nt * kPTN + 32 * wave;
+
+    // activation staging: 16 lanes cover one row's 64 columns (256 contiguous bytes per load
+    // instruction and row); thread -> columns 4 ap .. 4 ap + 3 of rows ar0 and ar0 + 32
+    const int ap = tid & 15, ar0 = tid >> 4;
+    const float* abase = A + 4 * ap;
+    int arow_off[2], aw[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        arow_off[i] = min(m0 + ar0 + 32 * i, M - 1) * K;  // M * K < 2^31
+        aw[i] = p_off(ar0 + 32 * i, ap >> 1) + 8 * (ap & 1);
+    }
+    float amax[2] = {0.0f, 0.0f};
+
+    // weight copy: the wave's rows n0c + r (clamped to N - 1), chunk c = 64 i + lane of the
+    // group's 32 * kRowBytes bytes -> row c / (kRowBytes / 16), 16-byte piece c % (kRowBytes / 16)
+    constexpr int kPieces = W::kRowBytes / 16, kChunks = 32 * kPieces, kLoads = (kChunks + 63) / 64;
+    const int n0c = min(n0, N - 1);
+    const uint8_t* const wbase = B + static_cast<long>(n0c) * row_bytes;
+    int woff[kLoads];  // < 32 rows: 32 * row_bytes < 2^31 is a launch condition
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int c = min(64 * i + lane, kChunks - 1);
+        const int r = c / kPieces;
+        woff[i] = (min(n0 + r, N - 1) - n0c) * static_cast<int>(row_bytes) + 16 * (c % kPieces);
+    }
+    char* const warea = lds + 8 * kPStage + wave * 32 * W::kRowBytes;
+    const char* const wrow = warea + fr * W::kRowBytes;  // this lane's row in the area
+
+    // A-operand fetch offsets: m tile u, sub-step s -> row 32 u + fr, the chunk of the
+    // k that this half-wave's B fragment holds
+    int aoff[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) aoff[u][s] = p_off(32 * u + fr, W::chunk(s, h));
+
+    pf16v acc[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[u][i] = 0.0f;
+
+    // The k loop runs in groups of four steps.  At the start of group q the
+    // bytes of group q + 1 are requested in one batch -- the wave's weight
+    // bytes and this thread's activation values of the four steps -- and
+    // consumed within the same group: the weight bytes are written to the
+    // wave's LDS area after group q's last read of it (third iteration), its
+    // first step decoded in the fourth, which also stages the activations
+    // into the other LDS buffer.  So every load is waited for in the code
+    // block that issued it, two to three iterations later.  Loads past the
+    // split's last step repeat it (in bounds); the padding steps that make
+    // the trip count a multiple of four stage zero activations, so their
+    // MFMAs add nothing.
+    const int nst4 = (nst + 3) & ~3, ngrp = nst4 >> 2;
+    auto step_of = [&](int t) { return s_begin + min(t, nst - 1); };
+    f32x4 av[4][2];  // activations of the next group: [step][row]
+    u32x4 wr[kLoads];  // weight bytes of the next group
+    auto load_next = [&](int q) {
+        const uint8_t* g = wbase + W::group_offset(step_of(4 * q));
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const pu4a4 v = *reinterpret_cast<const pu4a4*>(g + woff[i]);  // Q8_0 rows are only dword-aligned
+            wr[i] = u32x4{v.x, v.y, v.z, v.w};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) av[j][i] = ld_f32x4(abase + step_of(4 * q + j) * kPKS + arow_off[i]);
+    };
+    auto write_w = [&]() {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i)
+            if (64 * i + lane < kChunks) *reinterpret_cast<u32x4*>(warea + 16 * (64 * i + lane)) = wr[i];
+    };
+    // step j, row i of the next group into buffer buf (tile j)
+    auto stage = [&](char* buf, int q, int j, int i) {
+        const float vf = 4 * q + j < nst ? 1.0f : 0.0f;
+        const f32x4 v = av[j][i];
+        const float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        amax[i] = fmaxf(amax[i], mx * vf);  // a padding step's inf * 0 is NaN, which fmaxf ignores
+        const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(pf2{v.x, v.y}, ph2));
+        const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(pf2{v.z, v.w}, ph2));
+        *reinterpret_cast<pu2*>(buf + j * kPStage + aw[i]) = pu2{vf != 0.0f ? lo : 0u, vf != 0.0f ? hi : 0u};
+    };
+    auto afrag = [&](const char* tile, int u, int s) { return *reinterpret_cast<const ph8*>(tile + aoff[u][s]); };
+    auto mma2 = [&](const ph8 (&a)[2], const uint32_t (&bf)[4][4], int s) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                a[u], __builtin_bit_cast(ph8, u32x4{bf[s][0], bf[s][1], bf[s][2], bf[s][3]}), acc[u], 0, 0, 0);
+    };
+
+    // One iteration: step 4q + j's B fragments are in bc and its activation
+    // fragments in ac; fc holds the bytes of the next step (position J of its
+    // group).  Four phases, one per 16-column sub-step, each: that sub-step's
+    // two MFMAs, then -- while the matrix cores run them -- the B fragments of
+    // the same sub-step of the next step (bn) and the same sub-step's
+    // activation fragments of the next tile (an, when there is one in this
+    // buffer); in the group's last iteration each phase instead stages two of
+    // the next group's eight activation pieces into nxt.  Phase 0 also reads
+    // the bytes of the step after next (fn, position J + 1), after writing the
+    // next group's weight bytes when J == 3.  The phases are fenced so the
+    // compiler keeps this order.
+    auto iter = [&](auto pos, const ph8 (&ac)[2][4], ph8 (&an)[2][4], const char* next_tile,
+                    const uint32_t (&bc)[4][4], uint32_t (&bn)[4][4], const typename W::Frag& fc,
+                    typename W::Frag& fn, char* nxt, int qn) {
+        constexpr int J = decltype(pos)::value;
+        constexpr bool kLast = J == 0;  // the group's last iteration decodes the next group's first step
+        typename W::Consts k;
+        W::template prep<J>(fc, k);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const ph8 a[2] = {ac[0][s], ac[1][s]};
+            mma2(a, bc, s);
+            if (s == 0) {
+                W::template sub<0>(fc, k, bn[0]);
+                if constexpr (J == 3) write_w();
+                W::template read<(J + 1) & 3>(fn, wrow, h);
+            }
+            if (s == 1) W::template sub<1>(fc, k, bn[1]);
+            if (s == 2) W::template sub<2>(fc, k, bn[2]);
+            if (s == 3) W::template sub<3>(fc, k, bn[3]);
+            if constexpr (kLast) {
+                stage(nxt, qn, s, 0);
+                stage(nxt, qn, s, 1);
+            } else {
+                an[0][s] = afrag(next_tile, 0, s);
+                an[1][s] = afrag(next_tile, 1, s);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    ph8 fa[2][4], fb[2][4];
+    typename W::Frag f0, f1;
+    // group q, reading LDS activation buffer rd and staging the next group into wr
+    auto group = [&](int q, const char* rd, char* wr_buf, uint32_t (&x)[4][4], uint32_t (&y)[4][4]) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) fa[u][s4] = afrag(rd, u, s4);
+        load_next(q + 1);
+        iter(pos_t<1>{}, fa, fb, rd + kPStage, x, y, f1, f0, wr_buf, q + 1);
+        iter(pos_t<2>{}, fb, fa, rd + 2 * kPStage, y, x, f0, f1, wr_buf, q + 1);
+        iter(pos_t<3>{}, fa, fb, rd + 3 * kPStage, x, y, f1, f0, wr_buf, q + 1);
+        iter(pos_t<0>{}, fb, fa, rd, y, x, f0, f1, wr_buf, q + 1);
+        __syncthreads();
+    };
+
+    uint32_t b0[4][4], b1[4][4];
+    load_next(0);
+    write_w();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        stage(lds, 0, j, 0);
+        stage(lds, 0, j, 1);
+    }
+    W::template read<0>(f0, wrow, h);
+    {
+        typename W::Consts k;
+        W::template prep<0>(f0, k);
+        W::template sub<0>(f0, k, b0[0]);
+        W::template sub<1>(f0, k, b0[1]);
+        W::template sub<2>(f0, k, b0[2]);
+        W::template sub<3>(f0, k, b0[3]);
+    }
+    W::template read<1>(f1, wrow, h);
+    __syncthreads();
+    char* const buf0 = lds;
+    char* const buf1 = lds + 4 * kPStage;
+    for (int q = 0; q < ngrp; q += 2) {
+        group(q, buf0, buf1, b0, b1);
+        if (q + 1 >= ngrp) break;
+        group(q + 1, buf1, buf0, b0, b1);
+    }
+
+    // rows whose activations left fp16's range take the fp32 path below
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        float v = amax[i];
+        v = fmaxf(v, __shfl_xor(v, 1));
+        v = fmaxf(v, __shfl_xor(v, 2));
+        v = fmaxf(v, __shfl_xor(v, 4));
+        v = fmaxf(v, __shfl_xor(v, 8));
+        if (ap == 0) rowflag[ar0 + 32 * i] = (v >= kPRowMax || (v > 0.0f && v < kPRowMin)) ? 1 : 0;
+    }
+    __syncthreads();
+    // the 64 flags as one wave-uniform mask (bit ml: row m0 + ml takes the fp32 path)
+    const unsigned long long flagged = __ballot(rowflag[lane] != 0);
+
+    // lane: column n0 + fr, rows m0 + 32 u + 8 g + 4 h + r (accumulator 4 g + r); the stores
+    // stream past the caches (the output is not read again by this kernel)
+    const int n = n0 + fr;
+    const int mrows = M - m0;  // rows of this tile inside C
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int ml = 32 * u + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (ml < mrows && n < N && !((flagged >> ml) & 1ull)) {
+                float* cp = C + static_cast<long>(m0 + ml) * N + n;
+                if (atomic)
+                    atomicAdd(cp, acc[u][i]);
+                else
+                    __builtin_nontemporal_store(acc[u][i], cp);
+            }
+        }
+
+    // fp32 path for flagged rows: thread -> column nt * 256 + (tid & 255) of the flagged rows
+    // of parity tid >> 8, the reference's per-element decode and a sequential fp32 sum over
+    // this workgroup's k range
+    const int fmt = W::kBlockK == 256 ? kFmtQ4_K : kFmtQ8_0;
+    for (unsigned long long rest = flagged & (0x5555555555555555ull << (tid >> 8)); rest != 0; rest &= rest - 1) {
+        const int ml = __builtin_ctzll(rest);
+        const int m = m0 + ml, nn = nt * kPTN + (tid & 255);
+        if (m >= M || nn >= N) continue;
+        const float* x = A + static_cast<long>(m) * K;
+        const uint8_t* wp = B + static_cast<long>(nn) * row_bytes;
+        float sum = 0.0f;
+        for (int k = s_begin * kPKS; k < s_end * kPKS; ++k) sum = __builtin_fmaf(x[k], decode_row_elem(fmt, wp, k), sum);
+        float* cp = C + static_cast<long>(m) * N + nn;
+        if (atomic)
+            atomicAdd(cp, sum);
+        else
+            *cp = sum;
+    }
+}
+
+}  // namespace
+}  // namespace dev
+
+namespace detail {
+
+bool prefill_supported(int fmt, int M, int N, int K, const void* A, const void* B) {
+    if (fmt != kFmtQ4_K && fmt != kFmtQ8_0) return false;
+    // whole groups of four 64-column steps (one Q4_K super-block, 272 bytes of a Q8_0 row)
+    if (M < 1 || N < 1 || K < 4 * dev::kPKS || K % (4 * dev::kPKS) != 0) return false;
+    if (static_cast<long>(M) * K >= (1L << 31) || 32 * row_bytes(fmt, K) >= (1L << 31)) return false;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(A), b = reinterpret_cast<uintptr_t>(B);
+    // activations are read as 16-byte vectors, weights as 16-byte pieces of dword-aligned rows
+    return (a & 15) == 0 && (b & 3) == 0;
+}
+
+namespace {
+
+// The kernels use more than the default 64 KB of LDS; the limit is raised once per kernel and device.
+template <class W>
+int launch_w(dim3 grid, hipStream_t stream, const float* A, const uint8_t* B, float* C, int M, int N, int K, long rb,
+             int MT, int NT, int sps, int remap, int atomic) {
+    constexpr int kMaxDevices = 64;
+    constexpr int kLds = dev::prefill_lds_bytes<W>();
+    static std::atomic<bool> ready[kMaxDevices];
+    int devid = 0;
+    if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return kFailed;
+    if (!ready[devid].load(std::memory_order_acquire)) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::prefill_gemm_kernel<W>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kLds) != hipSuccess)
+            return kFailed;
+        ready[devid].store(true, std::memory_order_release);
+    }
+    hipLaunchKernelGGL(dev::prefill_gemm_kernel<W>, grid, dim3(dev::kPThreads), kLds, stream, A, B, C, M, N, K, rb,
+                       MT, NT, sps, remap, atomic);
+    return 0;  // the launch's own status is read by the caller
+}
+
+}  // namespace
+
+int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream) {
+    const int MT = (M + dev::kPTM - 1) / dev::kPTM;
+    const int NT = (N + dev::kPTN - 1) / dev::kPTN;
+    const long tiles = static_cast<long>(MT) * NT;
+    const int nsteps = K / dev::kPKS;
+    int ks = 1;
+    while (tiles * ks < 256 && nsteps >= 16 * ks) ks *= 2;
+    int sps = (nsteps + ks - 1) / ks;
+    sps = (sps + 3) / 4 * 4;  // groups of four steps: splits start on one
+    ks = (nsteps + sps - 1) / sps;
+    const long grid = tiles * ks;
+    if (grid > 0x7FFFFFFFL) return kDeclined;
+    const int remap = grid % 8 == 0 ? 1 : 0;
+    const int atomic = ks > 1 ? 1 : 0;
+    if (atomic) launch_fill_zero(C, static_cast<long>(M) * N, stream);
+    const long rb = row_bytes(fmt, K);
+    const dim3 g(static_cast<unsigned>(grid));
+    const uint8_t* Bb = static_cast<const uint8_t*>(B);
+    if (fmt == kFmtQ4_K) return launch_w<dev::PQ4K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
+    return launch_w<dev::PQ8_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
+}
+
+}  // namespace detail
+}  // namespace cri

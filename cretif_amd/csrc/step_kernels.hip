@@ -5,6 +5,7 @@
 // The position lives in device memory and every kernel that needs it reads it
 // there, so a HIP graph of the step stays valid as the sequence grows: the
 // counter is advanced by the last kernel of the step.
+#include <algorithm>
 #include <cmath>
 
 #include "common.hpp"
@@ -16,12 +17,18 @@ namespace dev {
 // One thread per rotated pair (q heads, then k heads) plus one per v element
 // pair of a row; grid.y = row.  The rotation is the reference's
 // (ref:src/kernels/elementwise.cu:232-257): pair i of a head (elements 2i and
-// 2i+1) turns by pos * theta^(-2i / head_dim), with the same fp32 expression
-// for the angle.  Rotated k and the unchanged v go to cache row pos, as
-// KVCache::append copies them (ref:src/kv_cache.cu:181-196).
+// 2i+1) turns by the angle pos * theta^(-2i / head_dim).  Its cosine and sine
+// come from `rot`, a [max_seq, head_dim / 2] table of (cos, sin) built once on
+// the host with the reference's fp32 expressions for the frequency and the
+// angle and cos/sin rounded once to fp32 (the position amplifies a one-ulp
+// difference in the frequency ~pos times, so these are computed exactly rather
+// than with fast device approximations).  The products are rounded separately
+// (no contraction), as in the reference's fp32 expression.  Rotated k and the
+// unchanged v go to cache row pos, as KVCache::append copies them
+// (ref:src/kv_cache.cu:181-196).
 __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q, long ldq, const float* __restrict__ k,
                                                           long ldk, const float* __restrict__ v, long ldv, int n_heads,
-                                                          int n_kv_heads, int head_dim, float theta,
+                                                          int n_kv_heads, int head_dim, const f32x2* __restrict__ rot,
                                                           const int* __restrict__ pos_dev, float* __restrict__ kc,
                                                           float* __restrict__ vc) {
     const int m = blockIdx.y;
@@ -35,20 +42,12 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q,
         const bool isq = i < qpairs;
         const int pi = isq ? i : i - qpairs;
         const int head = pi / half, lp = pi - head * half;
-        // theta^e, cos and sin are evaluated in double and rounded once to fp32, i.e. the
-        // correctly rounded values the fp32 expressions stand for (the position amplifies a
-        // one-ulp difference in the frequency ~pos times); the angle and the rotation are the
-        // reference's fp32 operations, the products rounded separately (no contraction)
-        const float e = (2.0f * static_cast<float>(lp)) / static_cast<float>(head_dim);
-        const float freq = 1.0f / static_cast<float>(pow(static_cast<double>(theta), static_cast<double>(e)));
-        const float ang = static_cast<float>(pos) * freq;
-        const float cs = static_cast<float>(cos(static_cast<double>(ang)));
-        const float sn = static_cast<float>(sin(static_cast<double>(ang)));
+        const f32x2 cs = rot[static_cast<long>(pos) * half + lp];
         const long off = static_cast<long>(head) * head_dim + 2 * lp;
         const float* src = isq ? q + m * ldq + off : k + m * ldk + off;
         const float x0 = src[0], x1 = src[1];
-        const float y0 = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
-        const float y1 = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
+        const float y0 = __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y));
+        const float y1 = __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
         float* dst = isq ? q + m * ldq + off : krow + off;
         dst[0] = y0;
         dst[1] = y1;
@@ -60,13 +59,16 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q,
     }
 }
 
-// One workgroup of 1024 threads per row.  A thread keeps the first index of
-// its strided elements' maximum (the comparison v > best skips NaN and keeps
-// the earlier index on ties); the workgroup then merges (value, index) pairs
-// preferring the larger value, then the smaller index -- the reference's
-// kernel_argmax (ref:src/embedding.cu:155-200), whose start value -FLT_MAX at
-// index 0 is kept too.
-constexpr int kArgmaxThreads = 1024;
+// Greedy token of each row, kernel_argmax's rule (ref:src/embedding.cu:155-200):
+// the largest value (a comparison v > best, so NaN never wins), the smallest
+// index among equal maxima, starting from (-FLT_MAX, 0).  The rule is a total
+// order on (value, index), so any merge order gives the same answer.  Each
+// row is cut into gridDim.x slices; a workgroup reduces its slice and writes
+// (value, index) to `part`; the last workgroup of the row (release / acquire
+// fences around a counter, reset afterwards) merges the slices.  The last
+// workgroup of row 0 also advances the position counter by `pos_add` when
+// `pos` is not null (the step's final kernel).
+constexpr int kArgmaxThreads = 256;
 
 __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
     if (ov > v || (ov == v && oi < i)) {
@@ -75,20 +77,9 @@ __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi)
     }
 }
 
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const float* __restrict__ logits, long ld, int n,
-                                                                     int* __restrict__ out) {
+__device__ __forceinline__ void argmax_block(float& best, int& bi) {
     __shared__ float sv[kArgmaxThreads / 64];
     __shared__ int si[kArgmaxThreads / 64];
-    const float* row = logits + blockIdx.x * ld;
-    float best = -3.402823466e38f;
-    int bi = 0;
-    for (int j = threadIdx.x; j < n; j += kArgmaxThreads) {
-        const float x = row[j];
-        if (x > best) {
-            best = x;
-            bi = j;
-        }
-    }
 #pragma unroll
     for (int s = 1; s < 64; s <<= 1) {
         const float ov = __shfl_xor(best, s);
@@ -101,9 +92,49 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const float
         si[wave] = bi;
     }
     __syncthreads();
+    best = sv[0];
+    bi = si[0];
+    for (int w = 1; w < kArgmaxThreads / 64; ++w) argmax_merge(best, bi, sv[w], si[w]);
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const float* __restrict__ logits, long ld, int n,
+                                                                     int* __restrict__ out, f32x2* __restrict__ part,
+                                                                     unsigned* __restrict__ counters,
+                                                                     int* __restrict__ pos, int pos_add) {
+    const int row = blockIdx.y, nb = gridDim.x, b = blockIdx.x;
+    const float* r = logits + row * ld;
+    const int per = (n + nb - 1) / nb;
+    const int j0 = b * per, j1 = min(n, j0 + per);
+    float best = -3.402823466e38f;
+    int bi = 0;
+    for (int j = j0 + threadIdx.x; j < j1; j += kArgmaxThreads) {
+        const float x = r[j];
+        if (x > best) {
+            best = x;
+            bi = j;
+        }
+    }
+    argmax_block(best, bi);
+    __shared__ int last;
     if (threadIdx.x == 0) {
-        for (int w = 1; w < kArgmaxThreads / 64; ++w) argmax_merge(best, bi, sv[w], si[w]);
-        out[blockIdx.x] = bi;
+        part[static_cast<long>(row) * nb + b] = f32x2{best, __int_as_float(bi)};
+        __threadfence();  // release: the slice result before the count
+        last = atomicAdd(&counters[row], 1u) == static_cast<unsigned>(nb - 1);
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();  // acquire: every slice's result
+    best = -3.402823466e38f;
+    bi = 0;
+    for (int s = threadIdx.x; s < nb; s += kArgmaxThreads) {
+        const f32x2 p = part[static_cast<long>(row) * nb + s];
+        argmax_merge(best, bi, p.x, __float_as_int(p.y));
+    }
+    argmax_block(best, bi);
+    if (threadIdx.x == 0) {
+        out[row] = bi;
+        counters[row] = 0u;
+        if (pos && row == 0) *pos += pos_add;
     }
 }
 
@@ -116,7 +147,7 @@ __global__ void pos_update_kernel(int* pos, int value, int add) {
 namespace detail {
 
 int launch_rope_append(float* q, long ldq, const float* k, long ldk, const float* v, long ldv, int rows, int n_heads,
-                       int n_kv_heads, int head_dim, float theta, const int* pos, float* k_cache, float* v_cache,
+                       int n_kv_heads, int head_dim, const float* rot, const int* pos, float* k_cache, float* v_cache,
                        hipStream_t stream) {
     if (rows < 1 || rows > 65535 || head_dim < 2 || head_dim % 2 != 0) return kDeclined;
     const long kvd = static_cast<long>(n_kv_heads) * head_dim;
@@ -124,15 +155,19 @@ int launch_rope_append(float* q, long ldq, const float* k, long ldk, const float
     const long blocks = (work + 255) / 256;
     if (blocks > 0x7FFFFFFFL) return kDeclined;
     hipLaunchKernelGGL(dev::rope_append_kernel, dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(rows)),
-                       dim3(256), 0, stream, q, ldq, k, ldk, v, ldv, n_heads, n_kv_heads, head_dim, theta, pos, k_cache,
-                       v_cache);
+                       dim3(256), 0, stream, q, ldq, k, ldk, v, ldv, n_heads, n_kv_heads, head_dim,
+                       reinterpret_cast<const dev::f32x2*>(rot), pos, k_cache, v_cache);
     return 0;
 }
 
-int launch_argmax_rows(const float* logits, long ld, int rows, int n, int* out, hipStream_t stream) {
-    if (rows < 1 || n < 1) return kDeclined;
-    hipLaunchKernelGGL(dev::argmax_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(dev::kArgmaxThreads), 0, stream,
-                       logits, ld, n, out);
+int argmax_slices(int n) { return static_cast<int>(std::min<long>(64, std::max<long>(1, (n + 8191) / 8192))); }
+
+int launch_argmax_rows(const float* logits, long ld, int rows, int n, int* out, float* part, unsigned* counters,
+                       int* pos, int pos_add, hipStream_t stream) {
+    if (rows < 1 || rows > 65535 || n < 1) return kDeclined;
+    hipLaunchKernelGGL(dev::argmax_rows_kernel, dim3(static_cast<unsigned>(argmax_slices(n)), static_cast<unsigned>(rows)),
+                       dim3(dev::kArgmaxThreads), 0, stream, logits, ld, n, out, reinterpret_cast<dev::f32x2*>(part),
+                       counters, pos, pos_add);
     return 0;
 }
 

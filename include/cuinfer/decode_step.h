@@ -127,6 +127,7 @@ private:
     bool tok_set_ = false, out_set_ = false, lm_tied_ = false;
     Tensor k_cache_, v_cache_, pos_dev_;
     Tensor hid_[2], normed_, qkv_, ctx_, attn_out_, ff_, act_, ffn_out_, attn_ws_;
+    Tensor argmax_part_, argmax_count_, rope_;
     int pos_host_ = 0;
     hipGraph_t graph_ = nullptr;
     hipGraphExec_t graph_exec_ = nullptr;

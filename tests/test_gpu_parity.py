@@ -320,16 +320,19 @@ def test_prefill_matches_oracle(orc, fmt, M, N, K):
 @pytest.mark.parametrize("fmt", ["q8_0", "q4_k"])
 @pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192)])
 def test_prefill_baseline_config(orc, fmt, N, K):
-    # 512 tokens x Llama-3.2-1B FFN gate/up and down; the oracle checks 3 bands of 128 output columns
+    # 512 tokens x Llama-3.2-1B FFN gate/up and down, every output against the oracle (its
+    # columns split over host threads), and every 64 x 256 tile on its own: a tile-mapping or
+    # split-k error in any one tile fails
     M = 512
     A = quant.randn(M * K, seed=K).reshape(M, K)
     Bq = weights(fmt, N, K, seed=N)
     got = run_matmul(fmt, A, Bq, N, K)
-    assert np.all(np.isfinite(got))
-    for n0 in (0, N // 2 - 64, N - 128):
-        ref = orc.matmul_quant(fmt, A, Bq, N, K, rows=(n0, n0 + 128))[:, n0:n0 + 128]
-        err = normwise_rel_err(got[:, n0:n0 + 128], ref)
-        assert err <= PREFILL_TOL, (n0, err)
+    ref = orc.matmul_quant_mt(fmt, A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= PREFILL_TOL
+    for m0 in range(0, M, 64):
+        for n0 in range(0, N, 256):
+            t = (slice(m0, m0 + 64), slice(n0, n0 + 256))
+            assert normwise_rel_err(got[t], ref[t]) <= PREFILL_TOL, (m0, n0)
 
 
 @pytest.mark.parametrize("fmt", FMTS)
@@ -392,6 +395,30 @@ def test_prefill_large_activations(orc):
     got = run_matmul("q8_0", A, Bq, N, K)
     ref = orc.matmul_quant("q8_0", A, Bq, N, K)
     assert normwise_rel_err(got, ref) <= PREFILL_TOL
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_k"])
+@pytest.mark.parametrize("case", ["huge", "tiny", "mixed"])
+def test_prefill_activation_range(orc, fmt, case):
+    # fp16 holds |x| < 65504, and rows of very small values only as subnormals: rows of
+    # activations ~1e5 (inf in fp16) or ~1e-7 must still meet the bar, each row against its own
+    # norm; 'mixed' puts such rows among ordinary ones (and into a split-k launch)
+    M, N, K = (64, 300, 2048) if case != "mixed" else (40, 128, 8192)
+    A = quant.randn(M * K, seed=17).reshape(M, K)
+    if case == "huge":
+        A *= 1e5
+    elif case == "tiny":
+        A *= 1e-7
+    else:
+        A[3] *= 1e5
+        A[21] *= 3e-8
+        A[39, 100] = 7e4
+    Bq = weights(fmt, N, K, seed=18)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert np.all(np.isfinite(got))
+    for r in range(M):
+        assert normwise_rel_err(got[r], ref[r]) <= PREFILL_TOL, (r, normwise_rel_err(got[r], ref[r]))
 
 
 def test_k_zero_writes_zeros():
