@@ -22,10 +22,18 @@
 namespace cri {
 namespace dev {
 
+// p[0 .. n) = 0: 16-byte stores over the 16-byte aligned body, single floats at the ends
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, long n) {
     const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
     const long stride = static_cast<long>(gridDim.x) * blockDim.x;
-    for (long j = i; j < n; j += stride) p[j] = 0.0f;
+    const long head = static_cast<long>((16 - (reinterpret_cast<uintptr_t>(p) & 15)) & 15) / 4;  // p is 4-aligned
+    const long lead = head < n ? head : n;
+    const long nv = (n - lead) / 4;
+    f32x4* body = reinterpret_cast<f32x4*>(p + lead);
+    for (long j = i; j < nv; j += stride) body[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (i < lead) p[i] = 0.0f;
+    const long tail = lead + 4 * nv;
+    if (tail + i < n) p[tail + i] = 0.0f;
 }
 
 // ---- GQA kernel -----------------------------------------------------------------
@@ -107,7 +115,8 @@ namespace detail {
 
 void launch_fill_zero(float* C, long n, hipStream_t stream) {
     if (n <= 0) return;
-    const long blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+    const long vec = (n + 3) / 4;  // one 16-byte store per thread and pass
+    const long blocks = (vec + 255) / 256 < 2048 ? (vec + 255) / 256 : 2048;
     hipLaunchKernelGGL(dev::fill_zero_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, C, n);
 }
 

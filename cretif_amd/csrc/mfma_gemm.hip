@@ -33,6 +33,7 @@
 #include <atomic>
 
 #include "common.hpp"
+#include "decode.hpp"
 #include "internal.hpp"
 
 namespace cri {
@@ -97,6 +98,7 @@ __device__ __forceinline__ int lds_off(int r, int c) { return (r << 7) + ((c ^ s
 // ref:src/kernels/dequantize.cu:45-47 -- x = d * q, q int8.  Two 34-byte blocks
 // per step; the pair starts 4-byte aligned, the second block 2 bytes off.
 struct WQ8_0 {
+    static constexpr int kFmt = kFmtQ8_0;
     static constexpr int kRegs = 9;
     static __device__ __forceinline__ void load(uint32_t (&w)[kRegs], const uint8_t* row, int step, int h) {
         const uint8_t* p = row + step * 68 + 32 * h;
@@ -131,6 +133,7 @@ struct WQ8_0 {
 // ref:src/kernels/dequantize.cu:84-100 -- element e <- qs[e/2], low nibble for
 // even e; x = d * (nib - 8).  18-byte blocks, pair of 36 bytes per step.
 struct WQ4_0 {
+    static constexpr int kFmt = kFmtQ4_0;
     static constexpr int kRegs = 5;
     static __device__ __forceinline__ void load(uint32_t (&w)[kRegs], const uint8_t* row, int step, int h) {
         const uint8_t* p = row + step * 36 + 16 * h;
@@ -170,6 +173,7 @@ struct WQ4_0 {
 // nibble of qs[e-16] otherwise, bit e of the little-endian qh as bit 4;
 // x = d * (q5 - 16).  22-byte blocks, pair of 44 bytes per step.
 struct WQ5_0 {
+    static constexpr int kFmt = kFmtQ5_0;
     static constexpr int kRegs = 6;
     static __device__ __forceinline__ void load(uint32_t (&w)[kRegs], const uint8_t* row, int step, int h) {
         const uint8_t* p = row + step * 44 + 20 * h;
@@ -214,6 +218,7 @@ struct WQ5_0 {
 // 64j + 32 + l its high nibble in sub-block 2j + 1; x = d*sc*q - dmin*mn.
 // One k step = one 64-element chunk j; h picks the sub-block.
 struct WQ4_K {
+    static constexpr int kFmt = kFmtQ4_K;
     static constexpr int kRegs = 12;
     static __device__ __forceinline__ void load(uint32_t (&w)[kRegs], const uint8_t* row, int step, int h) {
         const uint8_t* sb = row + (step >> 2) * 144;
@@ -262,6 +267,7 @@ struct WQ4_K {
 // (c, q in {0,1} or {2,3}) of a 128-element chunk; h picks q within it.  The
 // super-blocks are only 2-byte aligned, so the loads funnel-shift.
 struct WQ6_K {
+    static constexpr int kFmt = kFmtQ6_K;
     static constexpr int kRegs = 20;
     static __device__ __forceinline__ void load(uint32_t (&w)[kRegs], const uint8_t* row, int step, int h) {
         const uint8_t* sb = row + (step >> 2) * 210;
@@ -308,6 +314,7 @@ struct WQ6_K {
 
 // ref:src/kernels/matmul_quant.cu:510-558 -- fp16 weights, used as they are.
 struct WF16 {
+    static constexpr int kFmt = kFmtF16;
     static constexpr int kRegs = 16;
     static __device__ __forceinline__ void load(uint32_t (&w)[kRegs], const uint8_t* row, int step, int h) {
         const uint8_t* p = row + step * 128 + 64 * h;
@@ -409,9 +416,13 @@ __device__ __forceinline__ void run_tile(const TileJob& J, char* lds) {
     };
     // valid = false (the padding step of an odd step count) stores zero
     // activations, so that step's MFMAs add nothing.
+    float amax[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // largest |activation| of the staged rows
     auto stage_store = [&](const Stage<W, !AST>& st, int step, char* buf, bool valid) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            const f4 v = st.a[i];
+            const float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+            amax[i] = valid ? fmaxf(amax[i], mx) : amax[i];
             const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{st.a[i].x, st.a[i].y}, h2));
             const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{st.a[i].z, st.a[i].w}, h2));
             *reinterpret_cast<u32x2*>(buf + ast + 4096 * i) = u32x2{valid ? lo : 0u, valid ? hi : 0u};
@@ -499,6 +510,21 @@ __device__ __forceinline__ void run_tile(const TileJob& J, char* lds) {
         iter(R1, R0, S1, S0, t + 1);
     }
 
+    // Rows whose activations left fp16's comfortable range (>= 65504 is inf; a
+    // nonzero row below 2^-10 keeps only subnormal precision) are flagged in an
+    // LDS area above the staged C tile; their fp16 results are not stored and
+    // they are recomputed in fp32 at the end.
+    int* const rowflag = reinterpret_cast<int*>(lds + kLdsBytes) - kTileM;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float v = amax[i];
+        v = fmaxf(v, __shfl_xor(v, 1));
+        v = fmaxf(v, __shfl_xor(v, 2));
+        v = fmaxf(v, __shfl_xor(v, 4));
+        v = fmaxf(v, __shfl_xor(v, 8));
+        if (acol == 0) rowflag[arow0 + 32 * i] = (v >= 65504.0f || (v > 0.0f && v < 0x1p-10f)) ? 1 : 0;
+    }
+
     // Add the two k halves: wave (wm, wn, wk) keeps n tile t = wk and hands
     // t = 1 - wk to its partner (wave ^ 1) through LDS (8 KB per wave).
     constexpr int keep = WK, give = 1 - WK;
@@ -523,7 +549,7 @@ __device__ __forceinline__ void run_tile(const TileJob& J, char* lds) {
     // 86 us this way).  Read back along rows, an instruction covers 64
     // consecutive floats (atomics) or two full 512-byte rows (stores).
     constexpr int kCS = kTileN + 4;  // row stride (floats) of the staged tile
-    static_assert(kTileM * kCS * 4 <= kLdsBytes, "the staged C tile must fit in the LDS ring");
+    static_assert(kTileM * kCS * 4 + kTileM * 4 <= kLdsBytes, "the staged C tile and the row flags must fit in the LDS ring");
     float* ct = reinterpret_cast<float*>(lds);
     __syncthreads();  // every partner read of the k-half exchange is done
 #pragma unroll
@@ -541,14 +567,14 @@ __device__ __forceinline__ void run_tile(const TileJob& J, char* lds) {
 #pragma unroll 8
         for (int i = 0; i < kTileM / 4; ++i) {
             const int r = (tid >> 7) + 4 * i, m = m0 + r;
-            if (m < J.M && n < J.N) atomicAdd(J.C + static_cast<long>(m) * J.N + n, ct[r * kCS + c]);
+            if (m < J.M && n < J.N && !rowflag[r]) atomicAdd(J.C + static_cast<long>(m) * J.N + n, ct[r * kCS + c]);
         }
     } else if (J.vec_store) {  // N % 4 == 0, C 16-byte aligned
         const int c = (tid & 31) * 4, n = n0 + c;
 #pragma unroll
         for (int i = 0; i < kTileM / 16; ++i) {
             const int r = (tid >> 5) + 16 * i, m = m0 + r;
-            if (m < J.M && n < J.N)
+            if (m < J.M && n < J.N && !rowflag[r])
                 *reinterpret_cast<f4*>(J.C + static_cast<long>(m) * J.N + n) = *reinterpret_cast<const f4*>(ct + r * kCS + c);
         }
     } else {
@@ -556,8 +582,27 @@ __device__ __forceinline__ void run_tile(const TileJob& J, char* lds) {
 #pragma unroll 8
         for (int i = 0; i < kTileM / 4; ++i) {
             const int r = (tid >> 7) + 4 * i, m = m0 + r;
-            if (m < J.M && n < J.N) J.C[static_cast<long>(m) * J.N + n] = ct[r * kCS + c];
+            if (m < J.M && n < J.N && !rowflag[r]) J.C[static_cast<long>(m) * J.N + n] = ct[r * kCS + c];
         }
+    }
+
+    // fp32 path for flagged rows: thread -> column n0 + (tid & 127) of the flagged rows
+    // r = tid >> 7 (mod 4), the reference's per-element decode and a sequential fp32 sum over
+    // this workgroup's k range
+    for (int r = tid >> 7; r < kTileM; r += 4) {
+        if (!rowflag[r]) continue;  // uniform over each wave
+        const int m = m0 + r, n = n0 + (tid & 127);
+        if (m >= J.M || n >= J.N) continue;
+        const float* x = J.A + static_cast<long>(m) * J.K;
+        const uint8_t* wp = J.B + static_cast<long>(n) * J.row_bytes;
+        float sum = 0.0f;
+        for (int k = J.s_begin * kStepK; k < J.s_end * kStepK; ++k)
+            sum = __builtin_fmaf(x[k], decode_row_elem(W::kFmt, wp, k), sum);
+        float* cp = J.C + static_cast<long>(m) * J.N + n;
+        if (J.atomic)
+            atomicAdd(cp, sum);
+        else
+            *cp = sum;
     }
 }
 

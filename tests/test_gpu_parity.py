@@ -397,13 +397,17 @@ def test_prefill_large_activations(orc):
     assert normwise_rel_err(got, ref) <= PREFILL_TOL
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_k"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0", "q5_0", "q4_k", "q6_k", "fp16", "q8_0_k576"])
 @pytest.mark.parametrize("case", ["huge", "tiny", "mixed"])
 def test_prefill_activation_range(orc, fmt, case):
     # fp16 holds |x| < 65504, and rows of very small values only as subnormals: rows of
     # activations ~1e5 (inf in fp16) or ~1e-7 must still meet the bar, each row against its own
-    # norm; 'mixed' puts such rows among ordinary ones (and into a split-k launch)
+    # norm; 'mixed' puts such rows among ordinary ones (and into a split-k launch).  Q4_K and
+    # Q8_0 with K % 256 == 0 run the register-decode prefill kernel, the other formats and
+    # q8_0 at K = 576 the LDS-staged one; both flag such rows and recompute them in fp32.
     M, N, K = (64, 300, 2048) if case != "mixed" else (40, 128, 8192)
+    if fmt == "q8_0_k576":
+        fmt, K = "q8_0", 576
     A = quant.randn(M * K, seed=17).reshape(M, K)
     if case == "huge":
         A *= 1e5
