@@ -47,6 +47,8 @@ PREFILL_WORKLOADS = {
 SKINNY_WORKLOADS = {
     "q4_k_gemv_m16": ("q4_k", 16, 8192, 2048),
     "q4_k_gemv_down_m16": ("q4_k", 16, 2048, 8192),
+    # the tied fp32 LM head at decode batch 16 (matmul_transposed_b, ref:src/embedding.cu:85-135)
+    "fp32_tied_lm_head_m16": ("fp32", 16, 128256, 2048),
 }
 
 GEMV_WORKLOADS = {

@@ -2,8 +2,10 @@
 //
 // matmul_transposed_b: C = A * B^T with B [N,K] fp32 (the tied LM head,
 //   ref:src/embedding.cu:85-135).  M == 1 runs the streaming GEMV (one pass over
-//   B with coalesced 16-byte loads, activations in VGPRs); other shapes use the
-//   LDS-tiled fallback.
+//   B with coalesced 16-byte loads, activations in VGPRs); 2 <= M <= 16 (a
+//   decode batch) streams B once through v_mfma_f32_16x16x4_f32, fp32 products
+//   summed in fp32, with the M activation rows staged in LDS (below); other
+//   shapes use the LDS-tiled fallback.
 // batched_matmul_gqa: C[h] = A[h] * B[h / G] with A [H,M,K], B [Hkv,K,N]
 //   (ref:src/attention.cu:192-218).  The G query heads sharing a KV head are
 //   served together, so each B element is read once per row tile of its KV
@@ -16,6 +18,8 @@
 //   plainly (deterministic); long K (PV over the cache length) is also split
 //   over blocks until ~8 blocks per CU run, and those partial tiles are added
 //   with fp32 atomics into a zero-filled C.
+#include <atomic>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -109,6 +113,91 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(const float* __restrict_
     }
 }
 
+
+// ---- A * B^T for 2 <= M <= 16: one pass over B on the fp32 matrix cores ----
+// A wave owns 16 rows of B (one 16 x 16 output tile: B rows x activation rows,
+// the activation rows past M are zeros) and walks K in groups of 16 columns:
+// lane (i, q) = (lane & 15, lane >> 4) loads B[n0 + i][k + 4q .. + 3] (16 bytes;
+// the 64 lanes cover 16 rows x 64 contiguous bytes) and reads A[i][k + 4q .. + 3]
+// from LDS, and element j of both feeds the j-th of four MFMAs -- the k order
+// inside a group differs from k order, the products and their fp32 sums are
+// the reference's.  Weight loads run eight groups ahead (two register sets).
+// The activation rows are staged per chunk of up to kTbChunk columns; with more
+// than one chunk (K > kTbChunk) every row task restages them.
+constexpr int kTbChunk = 2048;
+constexpr int kTbLd = kTbChunk + 4;  // LDS row stride (floats): the 16 rows' chunks fall in distinct bank groups
+constexpr int kTbThreads = 512;
+constexpr int kTbBatch = 8;          // 16-column groups per batch of weight loads
+constexpr int kTbLdsBytes = 16 * kTbLd * 4;
+
+__global__ __launch_bounds__(kTbThreads) void tb_stream_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                               float* __restrict__ C, int M, int N, int K,
+                                                               int tasks_per_wave) {
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // 16 rows x kTbLd
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 15, q = lane >> 4;
+    const long nwaves = static_cast<long>(gridDim.x) * (kTbThreads / 64);
+    const long ngroups = (static_cast<long>(N) + 15) / 16;
+    const int nchunks = (K + kTbChunk - 1) / kTbChunk;
+    const float* xrow = xs + li * kTbLd + 4 * q;
+
+    for (int t = 0; t < tasks_per_wave; ++t) {
+        const long g = static_cast<long>(blockIdx.x) * (kTbThreads / 64) + wave + t * nwaves;
+        const long n0 = (g < ngroups ? g : ngroups - 1) * 16;  // idle waves repeat the last group (no store)
+        const float* wrow = B + min(n0 + li, static_cast<long>(N) - 1) * K + 4 * q;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < nchunks; ++c) {
+            const int k0 = c * kTbChunk, kc = min(kTbChunk, K - k0);
+            if (nchunks > 1 || t == 0) {  // uniform over the workgroup
+                __syncthreads();
+                const int per = kc >> 2;  // 16-byte pieces per row
+                for (int e = tid; e < 16 * per; e += kTbThreads) {
+                    const int m = e / per, j = e - m * per;
+                    const f32x4 v = m < M ? ld_f32x4(A + static_cast<long>(m) * K + k0 + 4 * j)
+                                          : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    *reinterpret_cast<f32x4*>(xs + m * kTbLd + 4 * j) = v;
+                }
+                __syncthreads();
+            }
+            const int ng = kc >> 4;  // 16-column groups in this chunk
+            const float* wp = wrow + k0;
+            auto load = [&](f32x4 (&w)[kTbBatch], int s0) {
+#pragma unroll
+                for (int u = 0; u < kTbBatch; ++u) w[u] = ld_f32x4(wp + 16 * min(s0 + u, ng - 1));  // in bounds
+            };
+            auto mma = [&](const f32x4 (&w)[kTbBatch], int s0) {
+#pragma unroll
+                for (int u = 0; u < kTbBatch; ++u) {
+                    if (s0 + u >= ng) break;  // uniform
+                    const f32x4 x = *reinterpret_cast<const f32x4*>(xrow + 16 * (s0 + u));
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w[u].x, x.x, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w[u].y, x.y, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w[u].z, x.z, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w[u].w, x.w, acc, 0, 0, 0);
+                }
+            };
+            f32x4 wa[kTbBatch], wb[kTbBatch];
+            load(wa, 0);
+            for (int s0 = 0; s0 < ng; s0 += 2 * kTbBatch) {
+                load(wb, s0 + kTbBatch);
+                mma(wa, s0);
+                load(wa, s0 + 2 * kTbBatch);
+                mma(wb, s0 + kTbBatch);
+            }
+        }
+        // lane (i, q): C[m = i][n0 + 4q + r], r = 0..3
+        if (g < ngroups && li < M) {
+            const long n = n0 + 4 * q;
+            float* cp = C + static_cast<long>(li) * N + n;
+            if (n + 0 < N) cp[0] = acc.x;
+            if (n + 1 < N) cp[1] = acc.y;
+            if (n + 2 < N) cp[2] = acc.z;
+            if (n + 3 < N) cp[3] = acc.w;
+        }
+    }
+}
+
 }  // namespace dev
 
 namespace detail {
@@ -120,8 +209,33 @@ void launch_fill_zero(float* C, long n, hipStream_t stream) {
     hipLaunchKernelGGL(dev::fill_zero_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, C, n);
 }
 
+// the streaming kernel uses more than the default 64 KB of LDS: the limit is raised once per device
+static int launch_tb_stream(const float* A, const float* B, float* C, int M, int N, int K, hipStream_t stream) {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<bool> ready[kMaxDevices];
+    int devid = 0;
+    if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return kFailed;
+    if (!ready[devid].load(std::memory_order_acquire)) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::tb_stream_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, dev::kTbLdsBytes) != hipSuccess)
+            return kFailed;
+        ready[devid].store(true, std::memory_order_release);
+    }
+    const long groups = (static_cast<long>(N) + 15) / 16;
+    constexpr int kWavesPerBlock = dev::kTbThreads / 64;
+    long blocks = (groups + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (blocks > 256) blocks = 256;  // one workgroup per CU (the staged rows fill most of its LDS)
+    const long waves = blocks * kWavesPerBlock;
+    const int tasks = static_cast<int>((groups + waves - 1) / waves);
+    hipLaunchKernelGGL(dev::tb_stream_kernel, dim3(static_cast<unsigned>(blocks)), dim3(dev::kTbThreads),
+                       dev::kTbLdsBytes, stream, A, B, C, M, N, K, tasks);
+    return 0;
+}
+
 int launch_transposed_b(const float* A, const float* B, float* C, int M, int N, int K, hipStream_t stream) {
     if (M == 1 && gemv_supported(kFmtF32, K, B)) return launch_gemv(kFmtF32, A, B, C, N, K, stream);
+    const bool aligned = ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15) == 0;
+    if (M >= 2 && M <= 16 && K % 16 == 0 && aligned) return launch_tb_stream(A, B, C, M, N, K, stream);
     return launch_generic_matmul(kFmtF32, A, B, C, M, N, K, stream);
 }
 

@@ -448,13 +448,30 @@ def test_nondefault_stream(orc):
 
 # ------------------------------------------------------------------ fp32 neighbours
 @pytest.mark.parametrize("M,N,K", [(1, 4, 3), (2, 4, 3), (64, 64, 64), (1, 5000, 2048), (3, 1000, 2048),
-                                   (1, 333, 100), (16, 4096, 2048)])
+                                   (1, 333, 100), (16, 4096, 2048), (2, 64, 16), (5, 1001, 3072), (16, 77, 4096),
+                                   (4, 100, 100), (17, 300, 256)])
 def test_transposed_b(orc, M, N, K):
     A = quant.randn(M * K, seed=M + K).reshape(M, K)
     B = quant.randn(N * K, seed=N + K).reshape(N, K)
     C = torch.empty(M, N, device="cuda")
     cri.matmul_transposed_b(dev(A), dev(B), C, M, N, K)
     assert normwise_rel_err(host(C), orc.matmul_transposed_b(A, B)) <= GEMV_TOL
+
+
+def test_transposed_b_tied_head_batch16():
+    # the tied LM head at decode batch 16 (ref:src/embedding.cu:85-135): 128256 x 2048 fp32
+    # streamed once through the fp32 matrix cores, against a float64 product
+    M, N, K = 16, 128256, 2048
+    rng = np.random.default_rng(21)
+    A = rng.standard_normal((M, K), dtype=np.float32)
+    B = (rng.standard_normal((N, K), dtype=np.float32) * 0.02).astype(np.float32)
+    C = torch.empty(M, N, device="cuda")
+    cri.matmul_transposed_b(dev(A), dev(B), C, M, N, K)
+    ref = A.astype(np.float64) @ B.astype(np.float64).T
+    got = host(C)
+    assert normwise_rel_err(got, ref) <= GEMV_TOL
+    for r in (0, 7, 15):
+        assert normwise_rel_err(got[r], ref[r]) <= GEMV_TOL
 
 
 @pytest.mark.parametrize("H,Hkv,M,N,K", [
