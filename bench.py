@@ -404,21 +404,23 @@ class AttentionRig:
 
 
 class GqaRig:
-    """batched_matmul_gqa (32 query heads over 8 KV heads, head_dim 64, T = 2048):
+    """batched_matmul_gqa (32 query heads over 8 KV heads, head_dim 64, T keys):
     'qk' is Q K^T (A [32, M, 64], B [8, 64, T]), 'pv' is P V (A [32, M, T],
     B [8, T, 64]).  Both operands rotate over `copies` distinct buffers (>= 2 x
-    the MALL) in one captured graph.  Algorithmic bytes: 4 (H M K + Hkv K N + H M N)."""
+    the MALL) in one captured graph.  Algorithmic bytes: 4 (H M K + Hkv K N + H M N);
+    flops 2 H M K N."""
 
-    H, HKV, HD, T = 32, 8, 64, 2048
+    H, HKV, HD = 32, 8, 64
 
-    def __init__(self, product, M, min_bytes=2 * MALL_BYTES):
+    def __init__(self, product, M, T=2048, min_bytes=2 * MALL_BYTES):
         import torch
 
         import cretif_amd as cri
 
         H, HKV = self.H, self.HKV
         self.M = M
-        self.K, self.N = (self.HD, self.T) if product == "qk" else (self.T, self.HD)
+        self.T = T
+        self.K, self.N = (self.HD, T) if product == "qk" else (T, self.HD)
         K, N = self.K, self.N
         per = 4 * (H * M * K + HKV * K * N)
         self.copies = int(max(2, min(256, -(-min_bytes // per))))
@@ -443,6 +445,9 @@ class GqaRig:
 
     def bytes_per_call(self):
         return 4 * (self.H * self.M * self.K + self.HKV * self.K * self.N + self.H * self.M * self.N)
+
+    def flops_per_call(self):
+        return 2.0 * self.H * self.M * self.K * self.N
 
     samples = GemvRig.samples
     time = GemvRig.time
@@ -518,6 +523,7 @@ def main():
     ap.add_argument("--workload", default="q4_k_gemv", choices=sorted(GEMV_WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-details", action="store_true", help="skip the per-format side measurements")
+    ap.add_argument("--gqa", default=None, help="time one batched_matmul_gqa shape: qk|pv,M,T")
     ap.add_argument("--prefill", default=None, choices=sorted(PREFILL_WORKLOADS),
                     help="only time one prefill GEMM workload (for profiling) and print its figures")
     ap.add_argument("--gemv", default=None, choices=sorted(GEMV_WORKLOADS) + sorted(SKINNY_WORKLOADS),
@@ -574,6 +580,13 @@ def main():
         ms_step = r.time(samples)
         print(json.dumps({"workload": "decode_step", "M": args.decode_step, "ms_per_step": round(ms_step, 4),
                           "tokens/s": round(args.decode_step / (ms_step * 1e-3), 1)}))
+        return
+    if args.gqa:
+        product, m_, t_ = args.gqa.split(",")
+        r = GqaRig(product, int(m_), T=int(t_))
+        ms_call = r.time(samples)
+        print(json.dumps({"workload": "gqa_%s" % product, "M": int(m_), "T": int(t_), "us": round(ms_call * 1e3, 3),
+                          "TFLOP/s": round(r.flops_per_call() / (ms_call * 1e-3) / 1e12, 2)}))
         return
     if args.prefill:
         f, m_, n, k = PREFILL_WORKLOADS[args.prefill]
@@ -656,6 +669,14 @@ def main():
                     "copies": r.copies}
                 r.free()
                 torch.cuda.empty_cache()
+            # prefill: a 512-token prompt attends to itself (ref:src/attention.cu:837-861), fp32 products
+            r = GqaRig(product, 512, T=512)
+            ms_call = r.time(9)
+            details["gqa_%s_m512_T512" % product] = {
+                "us": round(ms_call * 1e3, 3), "TFLOP/s": round(r.flops_per_call() / (ms_call * 1e-3) / 1e12, 2),
+                "GB/s": round(r.bytes_per_call() / (ms_call * 1e-3) / 1e9, 1), "copies": r.copies}
+            r.free()
+            torch.cuda.empty_cache()
         for m_ in (1, 16):
             r = DecodeStepRig(m_)
             ms_step = r.time(9)

@@ -114,6 +114,128 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(const float* __restrict_
 }
 
 
+// ---- batched_matmul_gqa at prefill M: fp32 matrix cores ----
+// The G query heads of one KV head are consecutive in A and C, so per KV head
+// the product is one GEMM C_kv [R = G M, N] = A_kv [R, K] * B_kv [K, N].  A
+// workgroup owns a 64 x 64 tile of it, its four waves one 32 x 32
+// v_mfma_f32_32x32x2_f32 tile each (fp32 products summed in fp32).  Each k
+// stage (KS columns) of A (rows) and B (stored transposed, [n][k]) goes
+// through double-buffered LDS, so each lane's KS / 2 k values of a stage are
+// 16-byte reads; lane (i, h) feeds k = (KS / 2) h + j to the j-th MFMA of the
+// stage in both operands (a k order of its own, the same products and sums).
+// The global loads run D stages ahead of the stage being computed (D register
+// sets): short K (Q K^T over head_dim) takes 16-column stages two deep, long K
+// (P V over the keys) 32-column stages four deep, where one workgroup per CU
+// has to keep enough requests in flight.
+// Requires K, N >= 4, K % 4 == 0, N % 4 == 0 and 16-byte aligned A, B; every
+// load address is clamped into its row, k past K stages zero activations, rows
+// past R and columns past N are computed from clamped values and not stored.
+typedef float gm_f16v __attribute__((ext_vector_type(16)));
+constexpr int kGmT = 64;
+
+// KS: k per stage (16 or 32); D: stages of loads in flight (2 or 4 register sets)
+template <int KS, int D>
+__global__ __launch_bounds__(256) void gqa_mfma_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                       float* __restrict__ C, int R, int N, int K) {
+    constexpr int LD = KS + 4;   // LDS row stride (floats): 16-byte reads of 16 rows fall in distinct bank groups
+    constexpr int AP = KS / 16;  // staged pieces per thread and operand
+    __shared__ __attribute__((aligned(16))) float sa[2][kGmT * LD];
+    __shared__ __attribute__((aligned(16))) float sb[2][kGmT * LD];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kv = blockIdx.y;
+    const int r0 = blockIdx.z * kGmT, n0 = blockIdx.x * kGmT;
+    const float* Akv = A + static_cast<long>(kv) * R * K;
+    const float* Bkv = B + static_cast<long>(kv) * K * N;
+    float* Ckv = C + static_cast<long>(kv) * R * N;
+
+    // staging, AP pieces per thread and operand: A rows ai + (256 / (KS / 4)) p, columns
+    // 4 aq .. + 3 of the stage; B rows (k) bk + 16 p, columns 4 bc .. + 3
+    constexpr int APR = KS / 4;            // 16-byte pieces per staged A row
+    constexpr int AROWS = 256 / APR;       // A rows per pass of the 256 threads
+    const int ai = tid / APR, aq = tid % APR, bk = tid >> 4, bc = tid & 15;
+    const float* arow[AP];
+#pragma unroll
+    for (int p = 0; p < AP; ++p) arow[p] = Akv + static_cast<long>(min(r0 + ai + AROWS * p, R - 1)) * K;
+    const float* bcol = Bkv + min(n0 + 4 * bc, N - 4);
+    const int nsteps = (K + KS - 1) / KS;
+    struct Regs {
+        f32x4 a[AP], b[AP];
+    };
+    // every load is unconditional (a clamped in-bounds address; values past K are zeroed
+    // after the load), so the compiler knows how many are in flight
+    auto gload = [&](Regs& g, int s) {
+        const int k0 = s * KS;
+        const bool in = k0 + 4 * aq < K;
+        const int ka = min(k0 + 4 * aq, K - 4);  // within the row (K >= 4); = k0 + 4 aq whenever in
+        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int p = 0; p < AP; ++p) {
+            const f32x4 v = ld_f32x4(arow[p] + ka);
+            g.a[p] = in ? v : z;
+            g.b[p] = ld_f32x4(bcol + static_cast<long>(min(k0 + bk + 16 * p, K - 1)) * N);
+        }
+    };
+    auto swrite = [&](const Regs& g, int buf) {
+#pragma unroll
+        for (int p = 0; p < AP; ++p) {
+            *reinterpret_cast<f32x4*>(&sa[buf][(ai + AROWS * p) * LD + 4 * aq]) = g.a[p];
+            float* t = &sb[buf][(4 * bc) * LD + bk + 16 * p];
+            t[0] = g.b[p].x;
+            t[LD] = g.b[p].y;
+            t[2 * LD] = g.b[p].z;
+            t[3 * LD] = g.b[p].w;
+        }
+    };
+    const int wr = wave >> 1, wc = wave & 1, i = lane & 31, h = lane >> 5;
+    constexpr int KH = KS / 2;  // k per half-wave per stage
+    const int aoff = (32 * wr + i) * LD + KH * h, boff = (32 * wc + i) * LD + KH * h;
+    gm_f16v acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < KH / 4; ++c) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(&sa[buf][aoff + 4 * c]);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(&sb[buf][boff + 4 * c]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, acc, 0, 0, 0);
+        }
+    };
+
+    // Iteration s: stage s is in LDS buffer s & 1, stages s + 1 .. s + D - 1 are in the
+    // register sets other than set s % D, which receives stage s + D's loads; it computes
+    // stage s, writes stage s + 1 to the other buffer and syncs once.  The stage count is
+    // padded to a multiple of D with stages past K, which hold zero activations.
+    const int nstepsD = (nsteps + D - 1) / D * D;
+    Regs g[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) gload(g[d], d);
+    swrite(g[0], 0);
+    __syncthreads();
+    for (int s = 0; s < nstepsD; s += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            gload(g[d], s + d + D);
+            __builtin_amdgcn_sched_barrier(0);  // the loads go out before this stage's work
+            compute((s + d) & 1);
+            swrite(g[(d + 1) % D], (s + d + 1) & 1);
+            __syncthreads();
+        }
+    }
+
+    // lane (i, h), accumulator v: row 32 wr + 8 (v >> 2) + 4 h + (v & 3), column 32 wc + i
+    const int n = n0 + 32 * wc + i;
+    if (n >= N) return;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int r = r0 + 32 * wr + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (r < R) Ckv[static_cast<long>(r) * N + n] = acc[v];
+    }
+}
+
 // ---- A * B^T for 2 <= M <= 16: one pass over B on the fp32 matrix cores ----
 // A wave owns 16 rows of B (one 16 x 16 output tile: B rows x activation rows,
 // the activation rows past M are zeros) and walks K in groups of 16 columns:
@@ -243,6 +365,18 @@ int launch_gqa(const float* A, const float* B, float* C, int n_heads, int n_kv_h
                hipStream_t stream) {
     const int G = n_heads / n_kv_heads;
     const long R = static_cast<long>(G) * M;
+    // prefill (many rows per KV head): the matrix-core tiles
+    const bool aligned = ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15) == 0;
+    if (M >= 32 && K >= 4 && N >= 4 && K % 4 == 0 && N % 4 == 0 && aligned && (R + 63) / 64 <= 65535) {
+        const dim3 grid((N + 63) / 64, n_kv_heads, static_cast<unsigned>((R + 63) / 64));
+        if (K <= 128)
+            hipLaunchKernelGGL((dev::gqa_mfma_kernel<16, 2>), grid, dim3(256), 0, stream, A, B, C,
+                               static_cast<int>(R), N, K);
+        else
+            hipLaunchKernelGGL((dev::gqa_mfma_kernel<32, 4>), grid, dim3(256), 0, stream, A, B, C,
+                               static_cast<int>(R), N, K);
+        return 0;
+    }
     // split K over blocks while (column tiles x row tiles x KV heads) gives fewer than ~8
     // blocks per CU: a block's stages run one after another, so several resident blocks
     // per CU hide each other's load latency (P V at M = 16 with 16-row blocks: 21.2 us

@@ -482,9 +482,15 @@ def test_transposed_b_tied_head_batch16():
     (32, 8, 16, 64, 2048),
     (6, 3, 5, 37, 45),
     (8, 8, 3, 10, 700),
-    (32, 8, 40, 1500, 300),   # columns kernel: 160 rows per KV head, several k stages, ragged n
+    (32, 8, 40, 1500, 300),   # matrix cores: 160 rows per KV head (ragged row tile), ragged n, k stages
     (4, 1, 7, 90, 1030),      # split kernel: ragged k stage, 28 rows
-    (32, 8, 512, 64, 512),    # prefill-sized P V: many row tiles
+    (32, 8, 512, 64, 512),    # prefill P V (ref:src/attention.cu:837-861): matrix cores
+    (32, 8, 512, 512, 64),    # prefill Q K^T: matrix cores
+    (8, 2, 70, 100, 36),      # matrix cores: R = 280, N = 100, K = 36 (a partial k stage)
+    (8, 4, 33, 8, 8),         # matrix cores: one partial tile each way, K = 8 (< one stage)
+    (4, 2, 40, 4, 4),         # matrix cores: the smallest K and N
+    (4, 1, 32, 64, 300),      # matrix cores, long-K variant: partial last stage, stage count padded
+    (8, 2, 40, 102, 36),      # N % 4 != 0: the split kernel
 ])
 def test_gqa(orc, H, Hkv, M, N, K):
     A = quant.randn(H * M * K, seed=H + M).reshape(H, M, K)
