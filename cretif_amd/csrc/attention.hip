@@ -380,6 +380,172 @@ __global__ __launch_bounds__(256 / HQ) void decode_attn_split_kernel(const float
     }
 }
 
+// ---- multi-row split form on the fp32 matrix cores (head_dim 64) ---------------
+//
+// For a batch of M query rows (consecutive tokens) one wave takes 32 queries
+// -- q = m G + g over the rows m and the G query heads of KV head kvh -- and one
+// chunk of positions, so each K and V row of the chunk is read once for all of
+// them instead of once per row.  Per tile of 32 positions:
+//   * S = Q K^T, 32 x 32, as 32 v_mfma_f32_32x32x2_f32: lane (i, h) holds dims
+//     32 h .. 32 h + 31 of query i, lane (j, h) the same dims of key j, and the
+//     t-th MFMA takes dim 32 h + t from both (fp32 products, fp32 sums);
+//   * causal mask (row m sees positions < Tb + m), online softmax in base 2 per
+//     query row: the row max is a reduction over the 32 lanes of a half-wave,
+//     each lane keeps its partial sum;
+//   * P goes through LDS (32 x 32) to become the A operand of O += P V, two
+//     32 x 32 tiles of output dims, 16 MFMAs each, V read one row per k slot;
+// and the chunk's (max, sum, acc[64]) per (row, head) go to the same records as
+// the per-row kernel, merged by the same combine kernel.  All rows share one
+// chunk length (from the longest row); chunks past a row's end write empty
+// records.
+constexpr int kMrD = 64;
+constexpr int kMrPld = 36;  // LDS row stride of the P tile (floats)
+
+__global__ __launch_bounds__(64) void decode_attn_mrow_kernel(const float* __restrict__ Q, const float* __restrict__ Kc,
+                                                              const float* __restrict__ Vc, float* __restrict__ ws,
+                                                              int G, int n_kv, int M, const int* __restrict__ kv_dev,
+                                                              int kv0, float qscale, int nchunks, long ldq) {
+    __shared__ __attribute__((aligned(16))) float pt[32 * kMrPld];
+    typedef float mr_f16v __attribute__((ext_vector_type(16)));
+    const int lane = threadIdx.x, i = lane & 31, h = lane >> 5;
+    const int nq = M * G, nqh = (nq + 31) / 32;
+    const int qh = blockIdx.x % nqh, c = (blockIdx.x / nqh) % nchunks, kvh = blockIdx.x / (nqh * nchunks);
+    const int H = G * n_kv, kvd = n_kv * kMrD;
+    const int Tb = (kv_dev ? *kv_dev : 0) + kv0;  // row m attends to positions [0, Tb + m)
+    const int Tmax = Tb + M - 1;
+    const int Tc = kSplitTile * ((((Tmax + kSplitTile - 1) / kSplitTile) + nchunks - 1) / nchunks);
+    const int t0 = c * Tc, t1 = min(Tmax, t0 + Tc);
+
+    // the lane's query (A operand row i): dims 32 h .. + 31, scaled into base 2
+    float qa[32];
+    {
+        const int q = qh * 32 + i, m = q / G, g = q - m * G;
+        const bool ok = q < nq;
+        const float* qp = Q + static_cast<long>(ok ? m : 0) * ldq + static_cast<long>(kvh * G + (ok ? g : 0)) * kMrD + 32 * h;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const f32x4 v = ld_f32x4(qp + 4 * u) * qscale;
+            qa[4 * u] = ok ? v.x : 0.0f;
+            qa[4 * u + 1] = ok ? v.y : 0.0f;
+            qa[4 * u + 2] = ok ? v.z : 0.0f;
+            qa[4 * u + 3] = ok ? v.w : 0.0f;
+        }
+    }
+    // accumulator row v of this lane (S, O layout): query row 8 (v >> 2) + 4 h + (v & 3);
+    // lim: positions below it are visible to that row inside this chunk
+    int lim[16];
+    float mx[16], l[16];
+    mr_f16v o0, o1;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int q = qh * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        lim[v] = q < nq ? min(Tb + q / G, t1) : 0;
+        mx[v] = -INFINITY;
+        l[v] = 0.0f;
+        o0[v] = 0.0f;
+        o1[v] = 0.0f;
+    }
+    const float* Kh = Kc + static_cast<long>(kvh) * kMrD;
+    const float* Vh = Vc + static_cast<long>(kvh) * kMrD;
+
+    // one tile's operands in registers: keys (B operand column j = i, dims 32 h .. + 31) and
+    // values (B operand of P V: position tb + 16 h + t, dims e 32 + i); past the end: the last key
+    struct Tile {
+        f32x4 k[8];
+        float v0[16], v1[16];
+    };
+    auto load_tile = [&](Tile& T, int tb) {
+        const float* kp = Kh + static_cast<long>(min(tb + i, Tmax - 1)) * kvd + 32 * h;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) T.k[u] = ld_f32x4(kp + 4 * u);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const float* vp = Vh + static_cast<long>(min(tb + 16 * h + t, Tmax - 1)) * kvd + i;
+            T.v0[t] = vp[0];
+            T.v1[t] = vp[32];
+        }
+    };
+    auto run_tile = [&](const Tile& T, int tb) {
+        // two independent chains (even and odd t): half the sequential accumulation depth
+        mr_f16v sa0, sa1;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            sa0[v] = 0.0f;
+            sa1[v] = 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            sa0 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[4 * u], T.k[u].x, sa0, 0, 0, 0);
+            sa1 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[4 * u + 1], T.k[u].y, sa1, 0, 0, 0);
+            sa0 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[4 * u + 2], T.k[u].z, sa0, 0, 0, 0);
+            sa1 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[4 * u + 3], T.k[u].w, sa1, 0, 0, 0);
+        }
+        const int pos = tb + i;  // this lane's position (column j = i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const float sv = pos < lim[v] ? sa0[v] + sa1[v] : -INFINITY;
+            float tmax = sv;  // max over the 32 lanes of this half-wave
+            tmax = fmaxf(tmax, dpp<kQuadPerm1032>(tmax));
+            tmax = fmaxf(tmax, dpp<kQuadPerm2301>(tmax));
+            tmax = fmaxf(tmax, dpp<kRowHalfMirror>(tmax));
+            tmax = fmaxf(tmax, dpp<kRowMirror>(tmax));
+            tmax = fmaxf(tmax, swizzle_xor16(tmax));
+            const float mnew = fmaxf(mx[v], tmax);
+            const float cf = mnew == -INFINITY ? 1.0f : exp2f(mx[v] - mnew);
+            const float p = sv == -INFINITY ? 0.0f : exp2f(sv - mnew);
+            mx[v] = mnew;
+            l[v] = __builtin_fmaf(l[v], cf, p);
+            o0[v] *= cf;
+            o1[v] *= cf;
+            pt[(8 * (v >> 2) + 4 * h + (v & 3)) * kMrPld + i] = p;
+        }
+        __syncthreads();
+        // P row i, positions 16 h .. + 15 (A operand of P V)
+        f32x4 pa[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pa[u] = *reinterpret_cast<const f32x4*>(&pt[i * kMrPld + 16 * h + 4 * u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].x, T.v0[4 * u], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].x, T.v1[4 * u], o1, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].y, T.v0[4 * u + 1], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].y, T.v1[4 * u + 1], o1, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].z, T.v0[4 * u + 2], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].z, T.v1[4 * u + 2], o1, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].w, T.v0[4 * u + 3], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].w, T.v1[4 * u + 3], o1, 0, 0, 0);
+        }
+        __syncthreads();  // the P tile is rewritten by the next tile
+    };
+    // the next tile's loads are in flight while the current one is computed
+    Tile T0, T1;
+    load_tile(T0, t0);
+    for (int tb = t0; tb < t1; tb += 2 * kSplitTile) {
+        load_tile(T1, tb + kSplitTile);  // past t1: clamped reads, not computed
+        run_tile(T0, tb);
+        if (tb + kSplitTile >= t1) break;
+        load_tile(T0, tb + 2 * kSplitTile);
+        run_tile(T1, tb + kSplitTile);
+    }
+
+    // records: (max, sum, acc[64]) per query, the sum over the half-wave's lanes
+    const int stride = kMrD + 4;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const float lsum = group_sum_t<5>(l[v]);
+        const int q = qh * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (q >= nq) continue;
+        const int m = q / G, g = q - m * G;
+        float* rec = ws + ((static_cast<long>(m) * H + kvh * G + g) * nchunks + c) * stride;
+        rec[4 + i] = o0[v];
+        rec[4 + 32 + i] = o1[v];
+        if (i == 0) {
+            rec[0] = mx[v];
+            rec[1] = lsum;
+        }
+    }
+}
+
 // out[m][h][d] = sum_c 2^(m_c - M) acc_c[d] / sum_c 2^(m_c - M) l_c, M = max_c m_c,
 // for query row m = blockIdx.y (output rows ldo floats apart).  One wave per
 // (row, head): lanes take the chunks for the max and the sum (their loads are
@@ -431,6 +597,7 @@ static void launch_att(bool vec, dim3 grid, hipStream_t stream, const float* Q, 
 }
 
 constexpr int kSplitHeadsPerWave = 1;  // 4 waves per workgroup, one query head each
+constexpr int kMrowMinRows = 4;        // from this many query rows on, head_dim 64 takes the matrix-core form
 
 // Split form: number of chunks (of whole 32-position tiles) that gives ~256
 // workgroups per query row at kv_len positions (measured: 512 or 1024 smaller
@@ -449,6 +616,13 @@ static int split_chunks(int n_heads, int n_kv_heads, int D, int kv_len, int rows
     if (ws_floats >= 0 && nchunks * rec > ws_floats) nchunks = ws_floats / rec;
     return static_cast<int>(nchunks);
 }
+
+// The multi-row (matrix-core) form takes one chunk per 32-position tile, up to
+// kMrowMaxChunks: its waves each take 32 queries, so a decode batch has few of
+// them per chunk and needs the chunks for parallelism.
+constexpr int kMrowMaxChunks = 64;
+
+static bool use_mrow(int rows, int head_dim) { return head_dim == dev::kMrD && rows >= kMrowMinRows; }
 
 bool decode_attention_split_supported(const float* Q, const float* K, const float* V, int head_dim) {
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
@@ -469,6 +643,17 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
     const long blocks = static_cast<long>(n_kv_heads) * nhq * nchunks;
     if (blocks > 0x7FFFFFFFL) return kDeclined;
     const float qscale = scale * 1.44269504088896341f;
+    if (use_mrow(rows, D)) {
+        // several query rows: the rows share each chunk's K / V reads on the matrix cores
+        const long nqh = (static_cast<long>(rows) * G + 31) / 32;
+        const long waves = static_cast<long>(n_kv_heads) * nchunks * nqh;
+        if (waves > 0x7FFFFFFFL) return kDeclined;
+        hipLaunchKernelGGL(dev::decode_attn_mrow_kernel, dim3(static_cast<unsigned>(waves)), dim3(64), 0, stream, Q, K,
+                           V, ws, G, n_kv_heads, rows, kv_dev, kv0, qscale, nchunks, ldq);
+        hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads, static_cast<unsigned>(rows)), dim3(64), 0,
+                           stream, ws, out, D, nchunks, ldo);
+        return 0;
+    }
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(rows));
     if (D <= 64)
         hipLaunchKernelGGL((dev::decode_attn_split_kernel<kSplitHeadsPerWave, 4>), grid, dim3(256 / kSplitHeadsPerWave),
@@ -481,7 +666,11 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
     return 0;
 }
 
-int decode_attention_rows_chunks(int n_heads, int n_kv_heads, int head_dim, int max_kv_len) {
+int decode_attention_rows_chunks(int n_heads, int n_kv_heads, int head_dim, int max_kv_len, int rows) {
+    if (use_mrow(rows, head_dim)) {
+        const int tiles = (max_kv_len + dev::kSplitTile - 1) / dev::kSplitTile;
+        return tiles < 1 ? 1 : (tiles < kMrowMaxChunks ? tiles : kMrowMaxChunks);
+    }
     return split_chunks(n_heads, n_kv_heads, head_dim, max_kv_len, 1, -1);
 }
 

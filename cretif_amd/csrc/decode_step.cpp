@@ -9,6 +9,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <stdexcept>
@@ -133,8 +134,10 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     ff_ = Tensor::empty({MB, 2 * static_cast<int64_t>(c.intermediate_size)});
     act_ = Tensor::empty({MB, static_cast<int64_t>(c.intermediate_size)});
     ffn_out_ = Tensor::empty({MB, static_cast<int64_t>(c.dim)});
-    nchunks_ = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len);
-    attn_ws_ = Tensor::empty({MB * c.n_heads * nchunks_ * (c.head_dim + 4)});
+    // records for the larger of the one-row and the multi-row chunk counts
+    const int ch1 = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, 1);
+    const int chm = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, MB);
+    attn_ws_ = Tensor::empty({MB * c.n_heads * std::max(ch1, chm) * (c.head_dim + 4)});
     // zeroed once; the argmax kernel that counts in them leaves them zero again
     argmax_part_ = Tensor::empty({MB * cri::detail::argmax_slices(c.vocab_size) * 2});
     argmax_count_ = Tensor::zeros({MB});
@@ -337,9 +340,11 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
                  "rope/append");
     // row m attends to positions [0, pos + m] (ref:src/attention.cu:60-75; one token: :410-511)
     const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
+    const int nchunks = cri::detail::decode_attention_rows_chunks(cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim,
+                                                                  cfg_.max_seq_len, M);
     check_status(cri::detail::launch_decode_attention_rows(q, ldq, k_cache(li), v_cache(li), ctx_.data_as<float>(), QD,
                                                            M, cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim, pos, 1,
-                                                           nchunks_, scale, attn_ws_.data_as<float>(), s),
+                                                           nchunks, scale, attn_ws_.data_as<float>(), s),
                  "attention");
     matmul_dispatch(ctx_.data_as<float>(), L.o, attn_out_.data_as<float>(), M, D, QD, L.o_fmt, s);
     res = attn_out_.data_as<float>();

@@ -120,7 +120,7 @@ private:
     void ffn_block(Layer& L, int M, int& cur, const float*& res, hipStream_t s);
 
     DecodeStepConfig cfg_;
-    int q_dim_ = 0, kv_dim_ = 0, nchunks_ = 0;
+    int q_dim_ = 0, kv_dim_ = 0;
     std::vector<std::unique_ptr<Layer>> layers_;
     Tensor tok_table_, out_norm_, lm_head_;
     WeightFormat tok_fmt_ = WeightFormat::FP32, lm_fmt_ = WeightFormat::FP32;
