@@ -58,7 +58,7 @@ constexpr int kPrefillMinM = 16;
 int fill_zero(float* C, long n, hipStream_t stream, const char* fn);
 
 int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream,
-                const char* fn) {
+                const char* fn, float* ws = nullptr, long ws_floats = 0) {
     if (M < 0 || N < 0 || K < 0)
         return fail(CRI_ERR_INVALID_ARGUMENT, fn,
                     "negative dimension (M=" + std::to_string(M) + ", N=" + std::to_string(N) +
@@ -85,7 +85,8 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
         cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv2(fmt, A, B, C, M, N, K, stream);
     else if (cri::detail::skinny_supported(fmt, M, K, B))
-        rc = cri::detail::launch_skinny(fmt, A, B, C, M, N, K, stream);
+        rc = cri::detail::launch_skinny_act(cri::kActPlain, fmt, cri::ActIn{A, nullptr, nullptr, nullptr, K, 0.0f}, B,
+                                            C, M, N, K, stream, ws, ws_floats);
     else if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv(fmt, A, B, C, N, K, stream);
     else if (M > kPrefillMinM && cri::detail::prefill_supported(fmt, M, N, K, A, B))
@@ -251,7 +252,7 @@ bool overlaps(const void* a, long abytes, const void* b, long bbytes) {
 constexpr int kFusedMaxM = 16;
 
 int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float* C, int M, int N, int K,
-                 hipStream_t stream, const char* fn) {
+                 hipStream_t stream, const char* fn, float* ws = nullptr, long ws_floats = 0) {
     if (fmt < cri::kFmtQ8_0 || fmt > cri::kFmtF16) return fail(CRI_ERR_UNSUPPORTED, fn, "unknown format id");
     if (M < 0 || N < 0 || K < 0) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative dimension");
     const int be = cri::block_elems(fmt);
@@ -268,7 +269,7 @@ int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float*
     clear_pending_error();
     int rc = cri::detail::kDeclined;
     if (cri::detail::skinny_supported(fmt, M, K, B))
-        rc = cri::detail::launch_skinny_act(mode, fmt, act, B, C, M, N, K, stream);
+        rc = cri::detail::launch_skinny_act(mode, fmt, act, B, C, M, N, K, stream, ws, ws_floats);
     if (rc == cri::detail::kDeclined && M == 1 && cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv_act(mode, fmt, act, B, C, N, K, stream);
     if (rc == cri::detail::kDeclined) rc = cri::detail::launch_generic_matmul_act(mode, fmt, act, B, C, M, N, K, stream);
@@ -294,16 +295,22 @@ int cri_matmul_rmsnorm(int format, const float* hidden, const float* residual, c
     return fused_matmul(cri::kActRMSNorm, format, act, B, C, M, N, K, s, fn);
 }
 
-int cri_matmul_swiglu(int format, const float* gate, const float* up, int ld, const void* B, float* C, int M, int N,
-                      int K, hipStream_t s) {
-    const char* fn = "cri_matmul_swiglu";
+namespace {
+int swiglu_impl(int format, const float* gate, const float* up, int ld, const void* B, float* C, int M, int N, int K,
+                hipStream_t s, const char* fn, float* ws, long ws_floats) {
     if (M > 0 && N > 0 && K > 0) {
         if (!gate || !up) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null gate or up");
         if (ld < K) return fail(CRI_ERR_SHAPE, fn, "ld=" + std::to_string(ld) + " is below K=" + std::to_string(K));
         if (!aligned(gate, 4) || !aligned(up, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "gate and up must be 4-byte aligned");
     }
     const cri::ActIn act{gate, up, nullptr, nullptr, ld, 0.0f};
-    return fused_matmul(cri::kActSwiGLU, format, act, B, C, M, N, K, s, fn);
+    return fused_matmul(cri::kActSwiGLU, format, act, B, C, M, N, K, s, fn, ws, ws_floats);
+}
+}  // namespace
+
+int cri_matmul_swiglu(int format, const float* gate, const float* up, int ld, const void* B, float* C, int M, int N,
+                      int K, hipStream_t s) {
+    return swiglu_impl(format, gate, up, ld, B, C, M, N, K, s, "cri_matmul_swiglu", nullptr, 0);
 }
 
 int cri_rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output,
@@ -470,3 +477,18 @@ int cri_block_elems(int format) { return format >= 0 && format <= 5 ? cri::block
 int cri_version(void) { return 100; }
 
 }  // extern "C"
+
+// In-library callers that own a workspace (the decode step): the same products, with the
+// skinny kernel's split partial sums reduced in a fixed order (deterministic).
+namespace cri {
+namespace detail {
+int matmul_split_ws(int fmt, const float* A, const void* B, float* C, int M, int N, int K, float* ws, long ws_floats,
+                    hipStream_t s) {
+    return matmul_impl(fmt, A, B, C, M, N, K, s, "matmul (decode step)", ws, ws_floats);
+}
+int matmul_swiglu_split_ws(int fmt, const float* gate, const float* up, int ld, const void* B, float* C, int M, int N,
+                           int K, float* ws, long ws_floats, hipStream_t s) {
+    return swiglu_impl(fmt, gate, up, ld, B, C, M, N, K, s, "matmul_swiglu (decode step)", ws, ws_floats);
+}
+}  // namespace detail
+}  // namespace cri

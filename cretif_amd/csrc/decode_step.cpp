@@ -73,6 +73,11 @@ void check_status(int rc, const char* what) {
 
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
+// a cri_status from the C ABI's dispatch
+void check_cri(int rc, const char* what) {
+    if (rc != CRI_OK) throw std::runtime_error(std::string("DecodeStep: ") + what + ": " + cri_last_error_string());
+}
+
 int cri_id(WeightFormat f) {
     switch (f) {
         case WeightFormat::FP32: return CRI_FP32;
@@ -138,6 +143,8 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     const int ch1 = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, 1);
     const int chm = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, MB);
     attn_ws_ = Tensor::empty({MB * c.n_heads * std::max(ch1, chm) * (c.head_dim + 4)});
+    // partial sums of the o and down projections when their K is split over workgroups
+    split_ws_ = Tensor::empty({cri::detail::skinny_workspace_floats(MB, c.dim)});
     // zeroed once; the argmax kernel that counts in them leaves them zero again
     argmax_part_ = Tensor::empty({MB * cri::detail::argmax_slices(c.vocab_size) * 2});
     argmax_count_ = Tensor::zeros({MB});
@@ -346,7 +353,10 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
                                                            M, cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim, pos, 1,
                                                            nchunks, scale, attn_ws_.data_as<float>(), s),
                  "attention");
-    matmul_dispatch(ctx_.data_as<float>(), L.o, attn_out_.data_as<float>(), M, D, QD, L.o_fmt, s);
+    check_cri(cri::detail::matmul_split_ws(cri_id(L.o_fmt), ctx_.data_as<float>(), L.o.data(),
+                                           attn_out_.data_as<float>(), M, D, QD, split_ws_.data_as<float>(),
+                                           split_ws_.numel(), s),
+              "o projection");
     res = attn_out_.data_as<float>();
 }
 
@@ -363,13 +373,17 @@ void DecodeStep::ffn_block(Layer& L, int M, int& cur, const float*& res, hipStre
             // ff rows: [gate (F) | up (F)]
             matmul_dispatch_rmsnorm(h, res, L.ffn_norm.data_as<float>(), h_next, L.gu, ff, M, 2 * F, D, L.gu_fmt, eps,
                                     s);
-            matmul_dispatch_swiglu(ff, ff + F, 2 * F, L.down, ffn_out, M, D, F, L.down_fmt, s);
+            check_cri(cri::detail::matmul_swiglu_split_ws(cri_id(L.down_fmt), ff, ff + F, 2 * F, L.down.data(), ffn_out,
+                                                          M, D, F, split_ws_.data_as<float>(), split_ws_.numel(), s),
+                      "down projection");
         } else {
             float* up = ff + static_cast<long>(MB) * F;
             matmul_dispatch_rmsnorm(h, res, L.ffn_norm.data_as<float>(), h_next, L.gate, ff, M, F, D, L.gate_fmt, eps,
                                     s);
             matmul_dispatch_rmsnorm(h, res, L.ffn_norm.data_as<float>(), nullptr, L.up, up, M, F, D, L.up_fmt, eps, s);
-            matmul_dispatch_swiglu(ff, up, F, L.down, ffn_out, M, D, F, L.down_fmt, s);
+            check_cri(cri::detail::matmul_swiglu_split_ws(cri_id(L.down_fmt), ff, up, F, L.down.data(), ffn_out, M, D,
+                                                          F, split_ws_.data_as<float>(), split_ws_.numel(), s),
+                      "down projection");
         }
         cur = 1 - cur;
     } else {

@@ -732,7 +732,7 @@ template <class F, int NW, int MODE, bool PAIR, int NPT, bool XPF>
 __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restrict__ B, float* __restrict__ C,
                                                              const float* __restrict__ A, int M, int N, int K, int KC,
                                                              int ks_log2, int ngroups, int nchunks, int nblocks,
-                                                             int cs_log2, const ActIn Pin) {
+                                                             int cs_log2, float* __restrict__ part, const ActIn Pin) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const ActIn P{A, Pin.b, Pin.w, Pin.h_out, Pin.lda, Pin.eps};
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -745,9 +745,21 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
     const int nitems = (sb_chunk - my_split + KS - 1) >> ks_log2;  // super-blocks per wave per chunk
     // chunk split across workgroups (cs_log2 > 0): workgroup b takes chunks
     // [c_begin, c_begin + cps) of groups b >> cs_log2, + gstride, ..., and adds
-    // its partial sums into C (zero-filled by the launcher)
+    // its partial sums into C (zero-filled by the launcher), or, with a
+    // workspace, stores them to part[split][m][n] for a fixed-order reduction
     const int cps = nchunks >> cs_log2;
-    const int c_begin = (static_cast<int>(blockIdx.x) & ((1 << cs_log2) - 1)) * cps;
+    const int split = static_cast<int>(blockIdx.x) & ((1 << cs_log2) - 1);
+    const int c_begin = split * cps;
+    float* const mypart = part ? part + static_cast<long>(split) * M * N : nullptr;
+    auto put = [&](int m, int n, float v) {
+        float* dst = C + static_cast<long>(m) * N + n;
+        if (!cs_log2)
+            *dst = v;
+        else if (mypart)
+            mypart[static_cast<long>(m) * N + n] = v;
+        else
+            atomicAdd(dst, v);
+    };
     const int grp0 = static_cast<int>(blockIdx.x) >> cs_log2, gstride = nblocks >> cs_log2;
     // at most NPT activation items per thread (the launcher guarantees it for NPT > 1)
     const bool few = NPT > 1 || M * (KC / 8) <= 64 * NW;
@@ -845,11 +857,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
 #pragma unroll
             for (int r = 0; r < kRows; ++r) {
                 const int m = kRows * g + r, n = tile * 16 + nl;
-                if (m < M && n < N && tile < ntiles) {
-                    float* dst = C + static_cast<long>(m) * N + n;
-                    if (cs_log2) atomicAdd(dst, out[r] * row_factor(m));
-                    else *dst = out[r] * row_factor(m);
-                }
+                if (m < M && n < N && tile < ntiles) put(m, n, out[r] * row_factor(m));
             }
         } else {
 #pragma unroll
@@ -863,11 +871,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
                 const float sum = ks_log2 == 1 ? sum_splits<2>(rp) : ks_log2 == 2 ? sum_splits<4>(rp) : sum_splits<8>(rp);
                 const int tt = grp * TW + t;
                 const int m = kRows * (ln >> 4) + r, n = tt * 16 + (ln & 15);
-                if (m < M && n < N && tt < ntiles) {
-                    float* dst = C + static_cast<long>(m) * N + n;
-                    if (cs_log2) atomicAdd(dst, sum * row_factor(m));
-                    else *dst = sum * row_factor(m);
-                }
+                if (m < M && n < N && tt < ntiles) put(m, n, sum * row_factor(m));
             }
             if (grp + gstride < ngroups) __syncthreads();  // the next group reuses red[]
         }
@@ -930,6 +934,17 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
     }
 }
 
+// C[i] = part[0][i] + part[1][i] + ... + part[S - 1][i], in that order (n = M N floats per split)
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, float* __restrict__ C, long n,
+                                                           int S) {
+    const long stride = static_cast<long>(gridDim.x) * blockDim.x;
+    for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+        float v = part[i];
+        for (int s = 1; s < S; ++s) v += part[static_cast<long>(s) * n + i];
+        C[i] = v;
+    }
+}
+
 }  // namespace dev
 
 namespace detail {
@@ -949,7 +964,7 @@ bool skinny_supported(int fmt, int M, int K, const void* B) {
 
 template <class F, int NW, int MODE, bool PAIR, int NPT, bool XPF = false>
 static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int K, int KC, int KS,
-                     hipStream_t stream) {
+                     hipStream_t stream, int cs_force = -1, float* ws = nullptr, long ws_floats = 0) {
     // large chunks need more than the default 64 KB of dynamic LDS: raise the limit once per kernel and device
     constexpr int kMaxDevices = 64;
     static std::atomic<bool> ready[kMaxDevices];
@@ -979,29 +994,43 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
     // chunk's sum of squares in one workgroup and is not split.
     const int nchunks = K / KC;
     int cs_log2 = 0;
-    if (MODE != kActRMSNorm && 2 * groups <= 2048 / NW && nchunks % 2 == 0) cs_log2 = 1;
+    if (cs_force >= 0)
+        cs_log2 = cs_force;
+    else if (MODE != kActRMSNorm && 2 * groups <= 2048 / NW && nchunks % 2 == 0)
+        cs_log2 = 1;
+    // More than two partial sums per output: with a workspace for them they are stored and
+    // added in a fixed order (deterministic); without one, fp32 atomics into a zero-filled C
+    // (the last bits can then vary between runs).  Two partials: atomics, exact in either order.
+    const long mn = static_cast<long>(M) * N;
+    float* part = nullptr;
+    if (cs_log2 > 1 && ws && ws_floats >= (mn << cs_log2)) part = ws;
     if (cs_log2 > 0) {
         blocks = groups << cs_log2;
-        launch_fill_zero(C, static_cast<long>(M) * N, stream);
+        if (!part) launch_fill_zero(C, mn, stream);
     }
     hipLaunchKernelGGL((dev::skinny_kernel<F, NW, MODE, PAIR, NPT, XPF>), dim3(blocks), dim3(64 * NW), L.bytes, stream,
                        static_cast<const uint8_t*>(B), C, A.a, M, N, K, KC, ks_log2, groups, nchunks, blocks, cs_log2,
-                       A);
+                       part, A);
+    if (part) {
+        const long rb = (mn + 255) / 256;
+        hipLaunchKernelGGL(dev::split_reduce_kernel, dim3(static_cast<unsigned>(rb < 1024 ? rb : 1024)), dim3(256), 0,
+                           stream, part, C, mn, 1 << cs_log2);
+    }
     return 0;
 }
 
 // up to 8 activation rows: hi and lo parts share each MFMA (paired lane rows)
 template <class F, int MODE>
 static int launch_sk_rows(const ActIn& A, const void* B, float* C, int M, int N, int K, int KC, int KS,
-                          hipStream_t stream) {
+                          hipStream_t stream, int cs = -1, float* ws = nullptr, long wsf = 0) {
     if (M <= 8) {
         // Q4_K with two activation items per thread (M = 1 at K = 8192, the FFN down
         // projection): their loads are issued at entry as well instead of after the
         // weights (measured 7.5 -> 6.7 us); the one-item kernel stays as it is
         if constexpr (std::is_same<F, dev::SkQ4K>::value)
             if (M * (KC / 8) > 512 && M * (KC / 8) <= 1024)
-                return launch_sk<F, 8, MODE, true, 2>(A, B, C, M, N, K, KC, KS, stream);
-        return launch_sk<F, 8, MODE, true, 1>(A, B, C, M, N, K, KC, KS, stream);
+                return launch_sk<F, 8, MODE, true, 2>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
+        return launch_sk<F, 8, MODE, true, 1>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
     }
     // Q4_K, more than 8 rows, plain activations, up to eight items per thread:
     // all of a chunk's activation loads are in registers ahead of time, and with
@@ -1010,15 +1039,16 @@ static int launch_sk_rows(const ActIn& A, const void* B, float* C, int M, int N,
     // chunk is faster without that request: 2048 x 2048 8.3 against 9.1 us)
     if constexpr (std::is_same<F, dev::SkQ4K>::value && MODE == kActPlain)
         if (M * (KC / 8) > 512 && M * (KC / 8) <= 4096) {
-            if (K > KC) return launch_sk<F, 8, MODE, false, 8, true>(A, B, C, M, N, K, KC, KS, stream);
-            return launch_sk<F, 8, MODE, false, 8, false>(A, B, C, M, N, K, KC, KS, stream);
+            if (K > KC && cs != static_cast<int>(__builtin_ctz(static_cast<unsigned>(K / KC))))
+                return launch_sk<F, 8, MODE, false, 8, true>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
+            return launch_sk<F, 8, MODE, false, 8, false>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
         }
-    return launch_sk<F, 8, MODE, false, 1>(A, B, C, M, N, K, KC, KS, stream);
+    return launch_sk<F, 8, MODE, false, 1>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
 }
 
 template <int MODE>
 static int launch_skinny_m(int fmt, const ActIn& A, const void* B, float* C, int M, int N, int K,
-                           hipStream_t stream) {
+                           hipStream_t stream, float* ws = nullptr, long wsf = 0) {
     // activation chunk: the largest multiple of 256 dividing K with M * KC <= kSkChunk
     // (few chunks: every chunk is staged once per workgroup)
     const int ntiles = (N + 15) / 16;
@@ -1030,15 +1060,32 @@ static int launch_skinny_m(int fmt, const ActIn& A, const void* B, float* C, int
     // split K over the waves of a workgroup when there are too few tiles for ~2048 waves
     int KS = 1;
     while (KS < 8 && KS * 2 <= sb && static_cast<long>(ntiles) * KS < 2048) KS *= 2;
+    // Without the RMSNorm prologue (which needs each row's whole sum of squares in one
+    // workgroup), split K over workgroups instead: every wave takes its own 16-row tile (8
+    // per workgroup) and each workgroup one chunk of K, the chunks sized so that ~256
+    // workgroups run.  A staged activation then feeds 8 tiles instead of 8 / KS, and each
+    // workgroup stages only its chunk; the partial sums are added into a zero-filled C.
+    int cs = -1;
+    if (MODE != kActRMSNorm && M > 8) {
+        const long groups8 = (ntiles + 7) / 8;
+        int split = 1;
+        while (split < 16 && groups8 * split * 2 <= 256 && K % (256 * split * 2) == 0) split *= 2;
+        if (split > 1) {
+            KC = K / split;
+            KS = 1;
+            cs = __builtin_ctz(static_cast<unsigned>(split));
+            if (M * KC > dev::kSkChunk) return -1;  // cannot happen: split > 1 only shrinks KC
+        }
+    }
     // eight waves per workgroup (8 / KS tiles each): measured faster than four for
     // every decode shape, from 512 x 2048 to the 128256 x 2048 lm_head
     switch (fmt) {
-        case kFmtQ6_K: return launch_sk_rows<dev::SkQ6K, MODE>(A, B, C, M, N, K, KC, KS, stream);
-        case kFmtQ4_K: return launch_sk_rows<dev::SkQ4K, MODE>(A, B, C, M, N, K, KC, KS, stream);
-        case kFmtQ8_0: return launch_sk_rows<dev::SkQ8_0, MODE>(A, B, C, M, N, K, KC, KS, stream);
-        case kFmtQ4_0: return launch_sk_rows<dev::SkQ4_0, MODE>(A, B, C, M, N, K, KC, KS, stream);
-        case kFmtQ5_0: return launch_sk_rows<dev::SkQ5_0, MODE>(A, B, C, M, N, K, KC, KS, stream);
-        case kFmtF16: return launch_sk_rows<dev::SkF16, MODE>(A, B, C, M, N, K, KC, KS, stream);
+        case kFmtQ6_K: return launch_sk_rows<dev::SkQ6K, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
+        case kFmtQ4_K: return launch_sk_rows<dev::SkQ4K, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
+        case kFmtQ8_0: return launch_sk_rows<dev::SkQ8_0, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
+        case kFmtQ4_0: return launch_sk_rows<dev::SkQ4_0, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
+        case kFmtQ5_0: return launch_sk_rows<dev::SkQ5_0, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
+        case kFmtF16: return launch_sk_rows<dev::SkF16, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
     }
     return -1;
 }
@@ -1049,14 +1096,16 @@ int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N
 }
 
 int launch_skinny_act(int mode, int fmt, const ActIn& act, const void* B, float* C, int M, int N, int K,
-                      hipStream_t stream) {
+                      hipStream_t stream, float* ws, long ws_floats) {
     switch (mode) {
-        case kActPlain: return launch_skinny_m<kActPlain>(fmt, act, B, C, M, N, K, stream);
-        case kActSwiGLU: return launch_skinny_m<kActSwiGLU>(fmt, act, B, C, M, N, K, stream);
-        case kActRMSNorm: return launch_skinny_m<kActRMSNorm>(fmt, act, B, C, M, N, K, stream);
+        case kActPlain: return launch_skinny_m<kActPlain>(fmt, act, B, C, M, N, K, stream, ws, ws_floats);
+        case kActSwiGLU: return launch_skinny_m<kActSwiGLU>(fmt, act, B, C, M, N, K, stream, ws, ws_floats);
+        case kActRMSNorm: return launch_skinny_m<kActRMSNorm>(fmt, act, B, C, M, N, K, stream, ws, ws_floats);
     }
     return -1;
 }
+
+long skinny_workspace_floats(int M, int N) { return static_cast<long>(M) * N * 16; }
 
 }  // namespace detail
 }  // namespace cri

@@ -250,13 +250,29 @@ def test_row_pair_gemv(orc, fmt, M, N, K):
 
 @pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
 def test_skinny_chunk_split_is_deterministic(fmt):
-    # two partial sums per output added atomically in either order: the same bits every call
-    M, N, K = 16, 2048, 8192
+    # M <= 8: two partial sums per output added atomically in either order, the same bits
+    # every call
+    M, N, K = 5, 2048, 8192
     A = quant.randn(M * K, seed=91).reshape(M, K)
     Bq = weights(fmt, N, K, seed=92)
     first = run_matmul(fmt, A, Bq, N, K)
     for _ in range(3):
         assert np.array_equal(run_matmul(fmt, A, Bq, N, K), first)
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+def test_skinny_many_splits_differ_only_in_order(orc, fmt):
+    # M > 8 without a workspace (the bare C ABI): K split over 16 workgroups whose fp32
+    # partial sums are added atomically, so calls may differ in the last bits -- by no more
+    # than a reordering of 16 terms can (the decode step passes a workspace and gets a fixed
+    # order: its replay test checks bit equality)
+    M, N, K = 16, 2048, 8192
+    A = quant.randn(M * K, seed=91).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=92)
+    first = run_matmul(fmt, A, Bq, N, K)
+    assert normwise_rel_err(first, orc.matmul_quant(fmt, A, Bq, N, K)) <= GEMV_TOL
+    for _ in range(3):
+        assert normwise_rel_err(run_matmul(fmt, A, Bq, N, K), first) <= 16 * 2.0 ** -24
 
 
 @pytest.mark.parametrize("M", [2, 7, 16])
