@@ -41,6 +41,8 @@ PREFILL_WORKLOADS = {
     "q8_0_prefill_down": ("q8_0", 512, 2048, 8192),
     "q4_k_prefill": ("q4_k", 512, 8192, 2048),
     "q4_k_prefill_down": ("q4_k", 512, 2048, 8192),
+    # the LDS-staged kernel (mfma_gemm.hip) that the other formats take
+    "q6_k_prefill": ("q6_k", 512, 8192, 2048),
 }
 
 # batched decode GEMVs (BASELINE config 5 at M = 16): name -> (fmt, M, N, K)
@@ -456,6 +458,55 @@ class GqaRig:
         self.A = self.B = self.graphs = None
 
 
+def read_probe_us(nb, per, grid, samples=7):
+    """us per launch of cri_stream_read_ex over nb bytes (per 16-byte loads per thread, issued
+    before any is used; grid 0 = one-shot, one pass of the buffer, else that many workgroups
+    striding over it), the buffers rotated over >= 2x the Infinity Cache in one graph."""
+    import torch
+
+    import cretif_amd as cri
+
+    copies = int(max(2, min(256, -(-2 * MALL_BYTES // nb))))
+    base = torch.zeros(nb, dtype=torch.uint8, device="cuda")
+    W = [base] + [base.clone() for _ in range(copies - 1)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for w in W:
+            cri.stream_read_ex(w, nb, sink, per, grid)
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for w in W:
+            cri.stream_read_ex(w, nb, sink, per, grid)
+    t = time_graphs([g], samples, copies, copies, s)
+    del g, W
+    torch.cuda.empty_cache()
+    return float(np.median(t)) / copies * 1e3
+
+
+def read_sweep():
+    """The achievable read rate at the headline's size, and how it grows with size: one JSON
+    line per point, then the best 9.4 MB shape and the fraction of 8 TB/s it reaches."""
+    nb, best = 9437184, None
+    for per in (1, 2, 4, 8, 16):
+        for grid in (0, 256, 512, 1024, 2048, 4096):
+            us = read_probe_us(nb, per, grid)
+            print(json.dumps({"read_sweep": "9.4MB", "loads_per_thread": per, "grid": grid or "one-shot",
+                              "us": round(us, 3), "GB/s": round(nb / us / 1e3, 1)}), flush=True)
+            if best is None or us < best[0]:
+                best = (us, per, grid)
+    us, per, grid = best
+    for mb in (0.25, 0.5, 1, 2, 4.7, 9.4, 18.9, 37.7, 75.5, 151, 302, 604):
+        n = int(mb * 1e6) // 4096 * 4096
+        t = read_probe_us(n, per, grid)
+        print(json.dumps({"read_sweep": "size", "MB": mb, "loads_per_thread": per, "grid": grid or "one-shot",
+                          "us": round(t, 3), "GB/s": round(n / t / 1e3, 1)}), flush=True)
+    print(json.dumps({"read_sweep": "best_9.4MB", "us": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
+                      "fraction_of_8TB/s": round(nb / us / 1e3 / 8000, 3),
+                      "us_needed_for_70pct": round(nb / (0.7 * 8000) / 1e3, 3)}), flush=True)
+
+
 def measured_traffic(workload):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary of this
     workload (profiles/<kernel>_<shape>.md, line `traffic_bytes_per_launch:`), or None."""
@@ -524,6 +575,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-details", action="store_true", help="skip the per-format side measurements")
     ap.add_argument("--gqa", default=None, help="time one batched_matmul_gqa shape: qk|pv,M,T")
+    ap.add_argument("--read-sweep", action="store_true",
+                    help="the read probe (cri_stream_read_ex) over loads per thread x grid shapes at the "
+                         "headline's 9.4 MB, then the best shape over sizes 0.25 MB .. 604 MB")
     ap.add_argument("--prefill", default=None, choices=sorted(PREFILL_WORKLOADS),
                     help="only time one prefill GEMM workload (for profiling) and print its figures")
     ap.add_argument("--gemv", default=None, choices=sorted(GEMV_WORKLOADS) + sorted(SKINNY_WORKLOADS),
@@ -580,6 +634,9 @@ def main():
         ms_step = r.time(samples)
         print(json.dumps({"workload": "decode_step", "M": args.decode_step, "ms_per_step": round(ms_step, 4),
                           "tokens/s": round(args.decode_step / (ms_step * 1e-3), 1)}))
+        return
+    if args.read_sweep:
+        read_sweep()
         return
     if args.gqa:
         product, m_, t_ = args.gqa.split(",")
