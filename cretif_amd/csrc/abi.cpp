@@ -278,9 +278,10 @@ int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float*
 
 }  // namespace
 
-int cri_matmul_rmsnorm(int format, const float* hidden, const float* residual, const float* norm_weight,
-                       float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, hipStream_t s) {
-    const char* fn = "cri_matmul_rmsnorm";
+namespace {
+int rmsnorm_impl(int format, const float* hidden, const float* residual, const float* norm_weight,
+                 float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, hipStream_t s,
+                 const char* fn, float* ws, long ws_floats) {
     if (M > 0 && N > 0 && K == 0) return fail(CRI_ERR_SHAPE, fn, "K=0: the RMS of an empty row is undefined");
     if (M > 0 && N > 0 && K > 0) {
         if (!hidden || !norm_weight) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null hidden or norm_weight");
@@ -292,7 +293,14 @@ int cri_matmul_rmsnorm(int format, const float* hidden, const float* residual, c
                         "hidden_out overlaps hidden or residual (other workgroups still read them)");
     }
     const cri::ActIn act{hidden, residual, norm_weight, hidden_out, K, eps};
-    return fused_matmul(cri::kActRMSNorm, format, act, B, C, M, N, K, s, fn);
+    return fused_matmul(cri::kActRMSNorm, format, act, B, C, M, N, K, s, fn, ws, ws_floats);
+}
+}  // namespace
+
+int cri_matmul_rmsnorm(int format, const float* hidden, const float* residual, const float* norm_weight,
+                       float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, hipStream_t s) {
+    return rmsnorm_impl(format, hidden, residual, norm_weight, hidden_out, B, C, M, N, K, eps, s,
+                        "cri_matmul_rmsnorm", nullptr, 0);
 }
 
 namespace {
@@ -489,6 +497,12 @@ int matmul_split_ws(int fmt, const float* A, const void* B, float* C, int M, int
 int matmul_swiglu_split_ws(int fmt, const float* gate, const float* up, int ld, const void* B, float* C, int M, int N,
                            int K, float* ws, long ws_floats, hipStream_t s) {
     return swiglu_impl(fmt, gate, up, ld, B, C, M, N, K, s, "matmul_swiglu (decode step)", ws, ws_floats);
+}
+int matmul_rmsnorm_split_ws(int fmt, const float* hidden, const float* residual, const float* norm_weight,
+                            float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, float* ws,
+                            long ws_floats, hipStream_t s) {
+    return rmsnorm_impl(fmt, hidden, residual, norm_weight, hidden_out, B, C, M, N, K, eps, s,
+                        "matmul_rmsnorm (decode step)", ws, ws_floats);
 }
 }  // namespace detail
 }  // namespace cri

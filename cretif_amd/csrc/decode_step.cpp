@@ -91,6 +91,15 @@ int cri_id(WeightFormat f) {
     return -1;
 }
 
+// RMSNorm(h + res) times W on the decode-batch kernels, with the step's split workspace (the
+// first call of a layer writes h + res to h_out)
+void norm_matmul(const float* h, const float* res, const float* norm_w, float* h_out, const Tensor& W, WeightFormat f,
+                 float* C, int M, int N, int K, float eps, Tensor& ws, hipStream_t s, const char* what) {
+    check_cri(cri::detail::matmul_rmsnorm_split_ws(cri_id(f), h, res, norm_w, h_out, W.data(), C, M, N, K, eps,
+                                                    ws.data_as<float>(), ws.numel(), s),
+              what);
+}
+
 }  // namespace
 
 struct DecodeStep::Layer {
@@ -143,7 +152,7 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     const int ch1 = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, 1);
     const int chm = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, MB);
     attn_ws_ = Tensor::empty({MB * c.n_heads * std::max(ch1, chm) * (c.head_dim + 4)});
-    // partial sums of the o and down projections when their K is split over workgroups
+    // partial sums of the decode-batch matmuls whose K is split over workgroups
     split_ws_ = Tensor::empty({cri::detail::skinny_workspace_floats(MB, c.dim)});
     // zeroed once; the argmax kernel that counts in them leaves them zero again
     argmax_part_ = Tensor::empty({MB * cri::detail::argmax_slices(c.vocab_size) * 2});
@@ -320,12 +329,13 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
     if (M <= kFusedMaxBatch) {
         // h_next = h + res; projections of RMSNorm(h_next) (the first writes h_next)
         if (L.qkv_fused) {
-            matmul_dispatch_rmsnorm(h, res, L.attn_norm.data_as<float>(), h_next, L.qkv, q, M, QD + 2 * KVD, D,
-                                    L.qkv_fmt, eps, s);
+            norm_matmul(h, res, L.attn_norm.data_as<float>(), h_next, L.qkv, L.qkv_fmt, q, M, QD + 2 * KVD, D, eps,
+                        split_ws_, s, "q/k/v projection");
         } else {
-            matmul_dispatch_rmsnorm(h, res, L.attn_norm.data_as<float>(), h_next, L.q, q, M, QD, D, L.q_fmt, eps, s);
-            matmul_dispatch_rmsnorm(h, res, L.attn_norm.data_as<float>(), nullptr, L.k, k, M, KVD, D, L.k_fmt, eps, s);
-            matmul_dispatch_rmsnorm(h, res, L.attn_norm.data_as<float>(), nullptr, L.v, v, M, KVD, D, L.v_fmt, eps, s);
+            const float* an = L.attn_norm.data_as<float>();
+            norm_matmul(h, res, an, h_next, L.q, L.q_fmt, q, M, QD, D, eps, split_ws_, s, "q projection");
+            norm_matmul(h, res, an, nullptr, L.k, L.k_fmt, k, M, KVD, D, eps, split_ws_, s, "k projection");
+            norm_matmul(h, res, an, nullptr, L.v, L.v_fmt, v, M, KVD, D, eps, split_ws_, s, "v projection");
         }
         cur = 1 - cur;
     } else {
@@ -371,16 +381,17 @@ void DecodeStep::ffn_block(Layer& L, int M, int& cur, const float*& res, hipStre
     if (M <= kFusedMaxBatch) {
         if (L.gu_fused) {
             // ff rows: [gate (F) | up (F)]
-            matmul_dispatch_rmsnorm(h, res, L.ffn_norm.data_as<float>(), h_next, L.gu, ff, M, 2 * F, D, L.gu_fmt, eps,
-                                    s);
+            norm_matmul(h, res, L.ffn_norm.data_as<float>(), h_next, L.gu, L.gu_fmt, ff, M, 2 * F, D, eps, split_ws_,
+                        s, "gate/up projection");
             check_cri(cri::detail::matmul_swiglu_split_ws(cri_id(L.down_fmt), ff, ff + F, 2 * F, L.down.data(), ffn_out,
                                                           M, D, F, split_ws_.data_as<float>(), split_ws_.numel(), s),
                       "down projection");
         } else {
             float* up = ff + static_cast<long>(MB) * F;
-            matmul_dispatch_rmsnorm(h, res, L.ffn_norm.data_as<float>(), h_next, L.gate, ff, M, F, D, L.gate_fmt, eps,
-                                    s);
-            matmul_dispatch_rmsnorm(h, res, L.ffn_norm.data_as<float>(), nullptr, L.up, up, M, F, D, L.up_fmt, eps, s);
+            norm_matmul(h, res, L.ffn_norm.data_as<float>(), h_next, L.gate, L.gate_fmt, ff, M, F, D, eps, split_ws_, s,
+                        "gate projection");
+            norm_matmul(h, res, L.ffn_norm.data_as<float>(), nullptr, L.up, L.up_fmt, up, M, F, D, eps, split_ws_, s,
+                        "up projection");
             check_cri(cri::detail::matmul_swiglu_split_ws(cri_id(L.down_fmt), ff, up, F, L.down.data(), ffn_out, M, D,
                                                           F, split_ws_.data_as<float>(), split_ws_.numel(), s),
                       "down projection");

@@ -73,15 +73,20 @@ int launch_gemv_act(int mode, int fmt, const ActIn& act, const void* W, float* y
 // 1 <= M <= 16 fused dequant matmul on the matrix cores (mfma_skinny.hip)
 bool skinny_supported(int fmt, int M, int K, const void* B);
 int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
-// ws (optional, skinny_workspace_floats(M, N) floats): partial sums of a K split over more
-// than two workgroups are stored there and added in a fixed order (deterministic); without
-// it they are added into C with fp32 atomics
+// ws (optional, skinny_workspace_floats(M, N) floats, 16-byte aligned): the partial sums of a K
+// split over workgroups are stored there and a second launch adds them in a fixed order
+// (deterministic; the RMSNorm prologue splits too).  Without it a split (plain and SwiGLU
+// prologues, several activation chunks) adds into C with fp32 atomics.  Calls sharing one
+// workspace must be ordered on one stream.
 int launch_skinny_act(int mode, int fmt, const ActIn& act, const void* B, float* C, int M, int N, int K,
                       hipStream_t stream, float* ws = nullptr, long ws_floats = 0);
 long skinny_workspace_floats(int M, int N);
-// cri_matmul / cri_matmul_swiglu with that workspace (abi.cpp); return a cri_status
+// cri_matmul / cri_matmul_swiglu / cri_matmul_rmsnorm with that workspace (abi.cpp); return a cri_status
 int matmul_split_ws(int fmt, const float* A, const void* B, float* C, int M, int N, int K, float* ws, long ws_floats,
                     hipStream_t s);
+int matmul_rmsnorm_split_ws(int fmt, const float* hidden, const float* residual, const float* norm_weight,
+                            float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, float* ws,
+                            long ws_floats, hipStream_t s);
 int matmul_swiglu_split_ws(int fmt, const float* gate, const float* up, int ld, const void* B, float* C, int M, int N,
                            int K, float* ws, long ws_floats, hipStream_t s);
 

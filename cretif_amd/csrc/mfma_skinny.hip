@@ -50,6 +50,11 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int kSkMaxItems = 6;
 // Activation chunk bound: M * KC <= kSkChunk (fp16 hi + lo copies: 4 * kSkChunk bytes of LDS).
 constexpr int kSkChunk = 32768;
+// Workspace of a K split over workgroups (floats): the RMSNorm sums of squares [split][16 rows],
+// then the partial sums [split][M][N].  Groups x splits <= 256 and a group is 128 columns, so
+// N x splits <= 32768 and the partial sums take at most 32768 M floats.
+constexpr int kSkMaxSplits = 16;
+constexpr long kSkPartOff = kSkMaxSplits * 16;
 
 // Order of the 8 k values of one k8 group inside an operand register set: the
 // nibble unpack produces (0,2), (1,3), (4,6), (5,7) pairs.
@@ -178,11 +183,10 @@ __device__ __forceinline__ void sk_clear_unscale(int M, int KC, float* unscale) 
 // batch's loads issued before any of its items is converted.  Per-sub-block
 // sums (times 2^-6) feed the mins MFMA.  One barrier.
 template <int MODE, int NT>
-__device__ void sk_stage(const ActIn& P, int M, int K, int k0, int KC, char* lds, const SkLds& L) {
+__device__ void sk_stage(const ActIn& P, int M, int K, int k0, int KC, char* lds, const SkLds& L, bool write_h) {
     const int tid = threadIdx.x;
     constexpr int nth = NT;
     const long lda = MODE == kActPlain ? K : P.lda;
-    const bool write_h = blockIdx.x == 0;
     float* ssq = MODE == kActRMSNorm ? reinterpret_cast<float*>(lds + L.ssq) + (k0 >> 8) * 16 : nullptr;
     _Float16* xh = reinterpret_cast<_Float16*>(lds + L.xh);
     _Float16* xl = reinterpret_cast<_Float16*>(lds + L.xl);
@@ -249,7 +253,8 @@ __device__ __forceinline__ void sk_load_few(const ActIn& P, int M, int K, int k0
 }
 template <int MODE, int NT, int NPT>
 __device__ __forceinline__ void sk_stage_few(const ActRaw<MODE> (&ra)[NPT], const ActRaw<MODE> (&rb)[NPT],
-                                             const ActIn& P, int M, int K, int k0, int KC, char* lds, const SkLds& L) {
+                                             const ActIn& P, int M, int K, int k0, int KC, char* lds, const SkLds& L,
+                                             bool write_h) {
     _Float16* xh = reinterpret_cast<_Float16*>(lds + L.xh);
     _Float16* xl = reinterpret_cast<_Float16*>(lds + L.xl);
     _Float16* xs = reinterpret_cast<_Float16*>(lds + L.xs);
@@ -269,8 +274,8 @@ __device__ __forceinline__ void sk_stage_few(const ActRaw<MODE> (&ra)[NPT], cons
                 float ss = 0.0f;
                 f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = a;
                 if (live) {
-                    a = act_finish<MODE>(ra[i], P, m, k0 + 8 * g8, K, ss, blockIdx.x == 0);
-                    b = act_finish<MODE>(rb[i], P, m, k0 + 8 * g8 + 4, K, ss, blockIdx.x == 0);
+                    a = act_finish<MODE>(ra[i], P, m, k0 + 8 * g8, K, ss, write_h);
+                    b = act_finish<MODE>(rb[i], P, m, k0 + 8 * g8 + 4, K, ss, write_h);
                 }
                 float* ssq = MODE == kActRMSNorm ? reinterpret_cast<float*>(lds + L.ssq) + (k0 >> 8) * 16 : nullptr;
                 sk_convert_item(a, b, live, m, g8, KC, xh, xl, xs, unscale, ss, ssq);
@@ -720,6 +725,42 @@ __device__ __forceinline__ float sum_splits(const float* p) {
     return s;
 }
 
+// C = the S partial sums of a workspace K split added in split order, times the RMSNorm row
+// factor of all S sums of squares.  Four consecutive outputs per thread (N % 4 == 0, C 16-byte
+// aligned: the launcher checks); every load is unconditional (splits past S read split S - 1,
+// unused), so all of a thread's loads are in flight together.
+template <int MODE>
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ ws, float* __restrict__ C, int M,
+                                                           int N, int K, int S, float eps) {
+    const long i4 = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    const long mn = static_cast<long>(M) * N;
+    if (4 * i4 >= mn) return;
+    const float* src = ws + kSkPartOff + 4 * i4;
+    f32x4 p[kSkMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kSkMaxSplits; ++s) p[s] = *reinterpret_cast<const f32x4*>(src + min(s, S - 1) * mn);
+    float fac = 1.0f;
+    if constexpr (MODE == kActRMSNorm) {
+        const int m = static_cast<int>(4 * i4 / N);
+        float sq[kSkMaxSplits];
+#pragma unroll
+        for (int s = 0; s < kSkMaxSplits; ++s) sq[s] = ws[min(s, S - 1) * 16 + m];
+        float ss = sq[0];
+#pragma unroll
+        for (int s = 1; s < kSkMaxSplits; ++s)
+            if (s < S) ss += sq[s];
+        fac = rms_factor(ss, K, eps);
+    } else {
+        (void)K;
+        (void)eps;
+    }
+    f32x4 v = p[0];
+#pragma unroll
+    for (int s = 1; s < kSkMaxSplits; ++s)
+        if (s < S) v += p[s];
+    *reinterpret_cast<f32x4*>(C + 4 * i4) = v * fac;
+}
+
 // Workgroup = NW waves = (NW / KS) tiles x KS k-splits.  The grid strides
 // over groups of NW / KS tiles; wave w works on tile w / KS of the group and
 // on super-blocks j = w % KS, + KS, ... of the current activation chunk.
@@ -750,7 +791,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
     const int cps = nchunks >> cs_log2;
     const int split = static_cast<int>(blockIdx.x) & ((1 << cs_log2) - 1);
     const int c_begin = split * cps;
-    float* const mypart = part ? part + static_cast<long>(split) * M * N : nullptr;
+    float* const mypart = part ? part + kSkPartOff + static_cast<long>(split) * M * N : nullptr;
     auto put = [&](int m, int n, float v) {
         float* dst = C + static_cast<long>(m) * N + n;
         if (!cs_log2)
@@ -761,6 +802,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
             atomicAdd(dst, v);
     };
     const int grp0 = static_cast<int>(blockIdx.x) >> cs_log2, gstride = nblocks >> cs_log2;
+    // RMSNorm: h + r goes to hidden_out from the workgroups of the first group (each stages its chunks)
+    const bool write_h = grp0 == 0;
     // at most NPT activation items per thread (the launcher guarantees it for NPT > 1)
     const bool few = NPT > 1 || M * (KC / 8) <= 64 * NW;
     // weight row of this lane in group grp (clamped: the last tile may be partial)
@@ -833,9 +876,11 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
         }
         acc += F::template block<PAIR>(d, x0 + jj * 256, x1 + jj * 256, xsr + 16 * jj, odd, g, us);
     };
-    // RMSNorm: the row factor of output row m (the sums of every chunk stay in LDS)
+    // RMSNorm: the row factor of output row m (the sums of every chunk stay in LDS); with K split
+    // over workgroups the factor is applied where the partial sums are added
     auto row_factor = [&](int m) {
         if constexpr (MODE == kActRMSNorm) {
+            if (cs_log2) return 1.0f;
             const float* ssq = reinterpret_cast<const float*>(lds + L.ssq);
             float ss = 0.0f;
             for (int sb = 0; sb < (K >> 8); ++sb) ss += ssq[sb * 16 + min(m, M - 1)];
@@ -886,8 +931,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
         // activations are staged for every chunk of the first group, and for
         // every group when the workgroup has several chunks
         if (grp == grp0 || cps > 1) {
-            if (few) sk_stage_few<MODE, 64 * NW, NPT>(xa, xb, P, M, K, k0, KC, lds, L);
-            else sk_stage<MODE, 64 * NW>(P, M, K, k0, KC, lds, L);
+            if (few) sk_stage_few<MODE, 64 * NW, NPT>(xa, xb, P, M, K, k0, KC, lds, L, write_h);
+            else sk_stage<MODE, 64 * NW>(P, M, K, k0, KC, lds, L, write_h);
         }
         // XPF (several chunks, register staging): the next chunk's activations are
         // requested now, so their latency hides behind this chunk's items; always
@@ -932,16 +977,15 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
         grp = ngrp;
         c = nc;
     }
-}
-
-// C[i] = part[0][i] + part[1][i] + ... + part[S - 1][i], in that order (n = M N floats per split)
-__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, float* __restrict__ C, long n,
-                                                           int S) {
-    const long stride = static_cast<long>(gridDim.x) * blockDim.x;
-    for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
-        float v = part[i];
-        for (int s = 1; s < S; ++s) v += part[static_cast<long>(s) * n + i];
-        C[i] = v;
+    // RMSNorm with a workspace split: the workgroups of the first group store their chunks'
+    // sums of squares per row for the reduction (the other groups' are the same)
+    if constexpr (MODE == kActRMSNorm) {
+        if (mypart && grp0 == 0 && threadIdx.x < 16) {
+            const float* ssq = reinterpret_cast<const float*>(lds + L.ssq) + ((c_begin * KC) >> 8) * 16;
+            float ss = 0.0f;
+            for (int sb = 0; sb < (cps * KC) >> 8; ++sb) ss += ssq[sb * 16 + threadIdx.x];
+            part[split * 16 + threadIdx.x] = ss;
+        }
     }
 }
 
@@ -960,6 +1004,15 @@ bool skinny_supported(int fmt, int M, int K, const void* B) {
     if (fmt == kFmtQ8_0 || fmt == kFmtQ4_0 || fmt == kFmtQ5_0 || fmt == kFmtF16)
         return M >= 2 && (reinterpret_cast<uintptr_t>(B) & 3u) == 0;
     return false;
+}
+
+// A workspace of a K split over workgroups holds the sums of squares and partial sums of this
+// shape, and the reduction's 16-byte stores of C are aligned.
+static bool split_ws_fits(const float* ws, long ws_floats, const float* C, int M, int N, int groups, int cs_log2) {
+    (void)groups;
+    return ws && (1 << cs_log2) <= dev::kSkMaxSplits && N % 4 == 0 &&
+           (reinterpret_cast<uintptr_t>(C) & 15u) == 0 && (reinterpret_cast<uintptr_t>(ws) & 15u) == 0 &&
+           ws_floats >= dev::kSkPartOff + (static_cast<long>(M) * N << cs_log2);
 }
 
 template <class F, int NW, int MODE, bool PAIR, int NPT, bool XPF = false>
@@ -998,12 +1051,17 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
         cs_log2 = cs_force;
     else if (MODE != kActRMSNorm && 2 * groups <= 2048 / NW && nchunks % 2 == 0)
         cs_log2 = 1;
-    // More than two partial sums per output: with a workspace for them they are stored and
-    // added in a fixed order (deterministic); without one, fp32 atomics into a zero-filled C
-    // (the last bits can then vary between runs).  Two partials: atomics, exact in either order.
+    // With a workspace the partial sums are stored and a second launch adds them in split order
+    // (deterministic; the RMSNorm row factor is applied there).  Without one, fp32 atomics into
+    // a zero-filled C: exact in either order for two partials, otherwise the last bits can vary
+    // between runs.  The RMSNorm prologue splits only with a workspace (its row factor needs
+    // every split).  An in-kernel reduction by the last workgroup of each group to finish was
+    // measured: its agent-scope release/acquire fences (L2 write-back and invalidate on every
+    // XCD) made the decode step slower, 1.35 -> 1.91 ms at M = 16.
     const long mn = static_cast<long>(M) * N;
     float* part = nullptr;
-    if (cs_log2 > 1 && ws && ws_floats >= (mn << cs_log2)) part = ws;
+    if (cs_log2 > 0 && split_ws_fits(ws, ws_floats, C, M, N, groups, cs_log2)) part = ws;
+    if (MODE == kActRMSNorm && cs_log2 > 0 && !part) return -1;
     if (cs_log2 > 0) {
         blocks = groups << cs_log2;
         if (!part) launch_fill_zero(C, mn, stream);
@@ -1011,11 +1069,9 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
     hipLaunchKernelGGL((dev::skinny_kernel<F, NW, MODE, PAIR, NPT, XPF>), dim3(blocks), dim3(64 * NW), L.bytes, stream,
                        static_cast<const uint8_t*>(B), C, A.a, M, N, K, KC, ks_log2, groups, nchunks, blocks, cs_log2,
                        part, A);
-    if (part) {
-        const long rb = (mn + 255) / 256;
-        hipLaunchKernelGGL(dev::split_reduce_kernel, dim3(static_cast<unsigned>(rb < 1024 ? rb : 1024)), dim3(256), 0,
-                           stream, part, C, mn, 1 << cs_log2);
-    }
+    if (part)
+        hipLaunchKernelGGL(dev::split_reduce_kernel<MODE>, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256),
+                           0, stream, part, C, M, N, K, 1 << cs_log2, A.eps);
     return 0;
 }
 
@@ -1060,16 +1116,19 @@ static int launch_skinny_m(int fmt, const ActIn& A, const void* B, float* C, int
     // split K over the waves of a workgroup when there are too few tiles for ~2048 waves
     int KS = 1;
     while (KS < 8 && KS * 2 <= sb && static_cast<long>(ntiles) * KS < 2048) KS *= 2;
-    // Without the RMSNorm prologue (which needs each row's whole sum of squares in one
-    // workgroup), split K over workgroups instead: every wave takes its own 16-row tile (8
-    // per workgroup) and each workgroup one chunk of K, the chunks sized so that ~256
-    // workgroups run.  A staged activation then feeds 8 tiles instead of 8 / KS, and each
-    // workgroup stages only its chunk; the partial sums are added into a zero-filled C.
-    // Only when the activations take several chunks (K > KC, the FFN down projection): with a
-    // single chunk the split saves no staging and its reduction costs more than it gains
-    // (2048 x 2048 at M = 16: 8.5 us unsplit, 5.2 + 5.3 us split into 8 and reduced).
+    // Split K over workgroups instead: every wave takes its own 16-row tile (8 per workgroup)
+    // and each workgroup one chunk of K, the chunks sized so that ~256 workgroups run.  A
+    // staged activation then feeds 8 tiles instead of 8 / KS, and each workgroup stages only
+    // its chunk.  With a workspace the last workgroup of each tile group adds the partial sums
+    // (and applies the RMSNorm row factor): every shape splits.  Without one, the partial sums
+    // go into a zero-filled C with atomics, which pays only when the activations take several
+    // chunks (K > KC, the FFN down projection; 2048 x 2048 at M = 16 measured 8.5 us unsplit,
+    // 5.2 + 5.3 us split into 8 and reduced by a second launch), and not for the RMSNorm
+    // prologue, whose row factor needs every chunk's sum of squares.
+    const bool ws_split = ws && N % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15u) == 0 &&
+                          wsf >= skinny_workspace_floats(M, N);
     int cs = -1;
-    if (MODE != kActRMSNorm && M > 8 && K > KC) {
+    if (M > 8 && (ws_split || (MODE != kActRMSNorm && K > KC))) {
         const long groups8 = (ntiles + 7) / 8;
         int split = 1;
         while (split < 16 && groups8 * split * 2 <= 256 && K % (256 * split * 2) == 0) split *= 2;
@@ -1108,7 +1167,11 @@ int launch_skinny_act(int mode, int fmt, const ActIn& act, const void* B, float*
     return -1;
 }
 
-long skinny_workspace_floats(int M, int N) { return static_cast<long>(M) * N * 16; }
+// groups x splits <= 256 and 128 columns per group: N x splits <= 32768 (see kSkPartOff)
+long skinny_workspace_floats(int M, int N) {
+    (void)N;
+    return dev::kSkPartOff + 32768L * M;
+}
 
 }  // namespace detail
 }  // namespace cri
