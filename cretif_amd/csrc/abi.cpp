@@ -252,7 +252,9 @@ bool overlaps(const void* a, long abytes, const void* b, long bbytes) {
 constexpr int kFusedMaxM = 16;
 
 int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float* C, int M, int N, int K,
-                 hipStream_t stream, const char* fn, float* ws = nullptr, long ws_floats = 0) {
+                 hipStream_t stream, const char* fn, float* ws = nullptr, long ws_floats = 0,
+                 cri::SplitSums* defer = nullptr, int defer_S = 0) {
+    if (defer) defer->S = 0;
     if (fmt < cri::kFmtQ8_0 || fmt > cri::kFmtF16) return fail(CRI_ERR_UNSUPPORTED, fn, "unknown format id");
     if (M < 0 || N < 0 || K < 0) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative dimension");
     const int be = cri::block_elems(fmt);
@@ -269,7 +271,9 @@ int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float*
     clear_pending_error();
     int rc = cri::detail::kDeclined;
     if (cri::detail::skinny_supported(fmt, M, K, B))
-        rc = cri::detail::launch_skinny_act(mode, fmt, act, B, C, M, N, K, stream, ws, ws_floats);
+        rc = cri::detail::launch_skinny_act(mode, fmt, act, B, C, M, N, K, stream, ws, ws_floats, defer, defer_S);
+    if (rc == cri::detail::kDeclined && mode == cri::kActSwiGLU2)
+        return fail(CRI_ERR_UNSUPPORTED, fn, "the two-split SwiGLU prologue runs on the skinny kernel only");
     if (rc == cri::detail::kDeclined && M == 1 && cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv_act(mode, fmt, act, B, C, N, K, stream);
     if (rc == cri::detail::kDeclined) rc = cri::detail::launch_generic_matmul_act(mode, fmt, act, B, C, M, N, K, stream);
@@ -281,7 +285,8 @@ int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float*
 namespace {
 int rmsnorm_impl(int format, const float* hidden, const float* residual, const float* norm_weight,
                  float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, hipStream_t s,
-                 const char* fn, float* ws, long ws_floats) {
+                 const char* fn, float* ws, long ws_floats, cri::SplitSums* defer = nullptr, int defer_S = 0) {
+    if (defer) defer->S = 0;
     if (M > 0 && N > 0 && K == 0) return fail(CRI_ERR_SHAPE, fn, "K=0: the RMS of an empty row is undefined");
     if (M > 0 && N > 0 && K > 0) {
         if (!hidden || !norm_weight) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null hidden or norm_weight");
@@ -293,7 +298,7 @@ int rmsnorm_impl(int format, const float* hidden, const float* residual, const f
                         "hidden_out overlaps hidden or residual (other workgroups still read them)");
     }
     const cri::ActIn act{hidden, residual, norm_weight, hidden_out, K, eps};
-    return fused_matmul(cri::kActRMSNorm, format, act, B, C, M, N, K, s, fn, ws, ws_floats);
+    return fused_matmul(cri::kActRMSNorm, format, act, B, C, M, N, K, s, fn, ws, ws_floats, defer, defer_S);
 }
 }  // namespace
 
@@ -500,9 +505,19 @@ int matmul_swiglu_split_ws(int fmt, const float* gate, const float* up, int ld, 
 }
 int matmul_rmsnorm_split_ws(int fmt, const float* hidden, const float* residual, const float* norm_weight,
                             float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, float* ws,
-                            long ws_floats, hipStream_t s) {
+                            long ws_floats, hipStream_t s, SplitSums* defer, int defer_S) {
     return rmsnorm_impl(fmt, hidden, residual, norm_weight, hidden_out, B, C, M, N, K, eps, s,
-                        "matmul_rmsnorm (decode step)", ws, ws_floats);
+                        "matmul_rmsnorm (decode step)", ws, ws_floats, defer, defer_S);
+}
+int matmul_swiglu2_split_ws(int fmt, const SplitSums& gu, long up_off, int ld, const void* B, float* C, int M, int N,
+                            int K, float* ws, long ws_floats, hipStream_t s) {
+    const char* fn = "matmul_swiglu2 (decode step)";
+    if (gu.S != 2 || !gu.part || !gu.ssq || ld < K || up_off < K)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "expects the two partial sums of an RMSNorm gate/up matmul");
+    cri::ActIn act{gu.part, gu.part + up_off, gu.ssq, nullptr, ld, gu.eps};
+    act.split = gu.stride;
+    act.kn = gu.K;
+    return fused_matmul(cri::kActSwiGLU2, fmt, act, B, C, M, N, K, s, fn, ws, ws_floats);
 }
 }  // namespace detail
 }  // namespace cri

@@ -30,6 +30,11 @@ template <>
 struct ActRaw<kActRMSNorm> {
     f32x4 h, r, w;
 };
+template <>
+struct ActRaw<kActSwiGLU2> {
+    f32x4 g0, g1, u0, u1;
+    float s0, s1;  // the two splits' sums of squares of row m
+};
 
 // Loads of x[m][k .. k+4) (k % 4 == 0, all four in range); rows lda floats apart
 // (the kernels pass K in plain mode, so P.lda is not read there).
@@ -41,6 +46,13 @@ __device__ __forceinline__ void act_load(ActRaw<MODE>& raw, const ActIn& P, int 
     } else if constexpr (MODE == kActSwiGLU) {
         raw.g = ld_f32x4(P.a + off);
         raw.u = ld_f32x4(P.b + off);
+    } else if constexpr (MODE == kActSwiGLU2) {
+        raw.g0 = ld_f32x4(P.a + off);
+        raw.g1 = ld_f32x4(P.a + P.split + off);
+        raw.u0 = ld_f32x4(P.b + off);
+        raw.u1 = ld_f32x4(P.b + P.split + off);
+        raw.s0 = P.w[m];
+        raw.s1 = P.w[16 + m];
     } else {
         raw.h = ld_f32x4(P.a + off);
         raw.r = P.b ? ld_f32x4(P.b + off) : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -70,6 +82,12 @@ __device__ __forceinline__ f32x4 act_finish(const ActRaw<MODE>& raw, const ActIn
         (void)m; (void)k; (void)K; (void)ss; (void)write_h;
         return f32x4{silu_f(raw.g.x) * raw.u.x, silu_f(raw.g.y) * raw.u.y, silu_f(raw.g.z) * raw.u.z,
                      silu_f(raw.g.w) * raw.u.w};
+    } else if constexpr (MODE == kActSwiGLU2) {
+        (void)m; (void)k; (void)K; (void)ss; (void)write_h;
+        // the reduction kernel's steps: (split 0 + split 1) * row factor
+        const float f = 1.0f / sqrtf((raw.s0 + raw.s1) / static_cast<float>(P.kn) + P.eps);
+        const f32x4 g = (raw.g0 + raw.g1) * f, u = (raw.u0 + raw.u1) * f;
+        return f32x4{silu_f(g.x) * u.x, silu_f(g.y) * u.y, silu_f(g.z) * u.z, silu_f(g.w) * u.w};
     } else {
         const f32x4 v = raw.h + raw.r;
         ss = __builtin_fmaf(v.x, v.x, ss);

@@ -91,12 +91,14 @@ int cri_id(WeightFormat f) {
     return -1;
 }
 
-// RMSNorm(h + res) times W on the decode-batch kernels, with the step's split workspace (the
-// first call of a layer writes h + res to h_out)
+// RMSNorm(h + res) times W on the decode-batch kernels, with a split workspace (the first call
+// of a layer writes h + res to h_out); with defer, a K split into defer_S partial sums (any
+// count for 0) is left in ws for the consumer (defer->S = 0: C was written)
 void norm_matmul(const float* h, const float* res, const float* norm_w, float* h_out, const Tensor& W, WeightFormat f,
-                 float* C, int M, int N, int K, float eps, Tensor& ws, hipStream_t s, const char* what) {
+                 float* C, int M, int N, int K, float eps, Tensor& ws, hipStream_t s, const char* what,
+                 cri::SplitSums* defer = nullptr, int defer_S = 0) {
     check_cri(cri::detail::matmul_rmsnorm_split_ws(cri_id(f), h, res, norm_w, h_out, W.data(), C, M, N, K, eps,
-                                                    ws.data_as<float>(), ws.numel(), s),
+                                                    ws.data_as<float>(), ws.numel(), s, defer, defer_S),
               what);
 }
 
@@ -154,6 +156,10 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     attn_ws_ = Tensor::empty({MB * c.n_heads * std::max(ch1, chm) * (c.head_dim + 4)});
     // partial sums of the decode-batch matmuls whose K is split over workgroups
     split_ws_ = Tensor::empty({cri::detail::skinny_workspace_floats(MB, c.dim)});
+    // the q/k/v and gate/up projections' partial sums, left for RoPE and the down projection's
+    // prologue to add up (a second workspace: the down projection splits into split_ws_ while
+    // it reads these)
+    defer_ws_ = Tensor::empty({cri::detail::skinny_workspace_floats(MB, c.dim)});
     // zeroed once; the argmax kernel that counts in them leaves them zero again
     argmax_part_ = Tensor::empty({MB * cri::detail::argmax_slices(c.vocab_size) * 2});
     argmax_count_ = Tensor::zeros({MB});
@@ -326,11 +332,12 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
         ldq = QD;
         ldk = ldv = KVD;
     }
+    cri::SplitSums qkv_sums;  // S > 0: the fused projection's partial sums, added up by RoPE
     if (M <= kFusedMaxBatch) {
         // h_next = h + res; projections of RMSNorm(h_next) (the first writes h_next)
         if (L.qkv_fused) {
             norm_matmul(h, res, L.attn_norm.data_as<float>(), h_next, L.qkv, L.qkv_fmt, q, M, QD + 2 * KVD, D, eps,
-                        split_ws_, s, "q/k/v projection");
+                        defer_ws_, s, "q/k/v projection", &qkv_sums);
         } else {
             const float* an = L.attn_norm.data_as<float>();
             norm_matmul(h, res, an, h_next, L.q, L.q_fmt, q, M, QD, D, eps, split_ws_, s, "q projection");
@@ -353,7 +360,7 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
     const int* pos = static_cast<const int*>(pos_dev_.data());
     check_status(cri::detail::launch_rope_append(q, ldq, k, ldk, v, ldv, M, cfg_.n_heads, cfg_.n_kv_heads,
                                                  cfg_.head_dim, rope_.data_as<float>(), pos, k_cache(li),
-                                                 v_cache(li), s),
+                                                 v_cache(li), s, &qkv_sums, QD, QD + KVD),
                  "rope/append");
     // row m attends to positions [0, pos + m] (ref:src/attention.cu:60-75; one token: :410-511)
     const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
@@ -381,11 +388,19 @@ void DecodeStep::ffn_block(Layer& L, int M, int& cur, const float*& res, hipStre
     if (M <= kFusedMaxBatch) {
         if (L.gu_fused) {
             // ff rows: [gate (F) | up (F)]
-            norm_matmul(h, res, L.ffn_norm.data_as<float>(), h_next, L.gu, L.gu_fmt, ff, M, 2 * F, D, eps, split_ws_,
-                        s, "gate/up projection");
-            check_cri(cri::detail::matmul_swiglu_split_ws(cri_id(L.down_fmt), ff, ff + F, 2 * F, L.down.data(), ffn_out,
-                                                          M, D, F, split_ws_.data_as<float>(), split_ws_.numel(), s),
-                      "down projection");
+            // a two-way K split of gate/up is added up inside the down projection's prologue
+            cri::SplitSums gu;
+            norm_matmul(h, res, L.ffn_norm.data_as<float>(), h_next, L.gu, L.gu_fmt, ff, M, 2 * F, D, eps, defer_ws_,
+                        s, "gate/up projection", &gu, 2);
+            if (gu.S)
+                check_cri(cri::detail::matmul_swiglu2_split_ws(cri_id(L.down_fmt), gu, F, 2 * F, L.down.data(), ffn_out,
+                                                               M, D, F, split_ws_.data_as<float>(), split_ws_.numel(), s),
+                          "down projection");
+            else
+                check_cri(cri::detail::matmul_swiglu_split_ws(cri_id(L.down_fmt), ff, ff + F, 2 * F, L.down.data(),
+                                                              ffn_out, M, D, F, split_ws_.data_as<float>(),
+                                                              split_ws_.numel(), s),
+                          "down projection");
         } else {
             float* up = ff + static_cast<long>(MB) * F;
             norm_matmul(h, res, L.ffn_norm.data_as<float>(), h_next, L.gate, L.gate_fmt, ff, M, F, D, eps, split_ws_, s,

@@ -43,7 +43,12 @@ inline long row_bytes(int fmt, int K) { return static_cast<long>(K / block_elems
 //   kActRMSNorm : v = a[m*lda + k] + b[m*lda + k] (b may be null), x = v * w[k],
 //                 the output row m scaled by 1/sqrt(mean_k v^2 + eps), and v
 //                 written to h_out[m*K + k] when h_out is not null
-enum : int { kActPlain = 0, kActSwiGLU = 1, kActRMSNorm = 2 };
+//   kActSwiGLU2 : SwiGLU of gate/up outputs left as the two partial sums of an
+//                 RMSNorm matmul whose K was split over workgroups (SplitSums):
+//                 g = f_m (a[off] + a[off + split]), u likewise from b, with
+//                 f_m = 1/sqrt((w[m] + w[16 + m]) / kn + eps) (w: the two splits'
+//                 sums of squares), then silu(g) * u
+enum : int { kActPlain = 0, kActSwiGLU = 1, kActRMSNorm = 2, kActSwiGLU2 = 3 };
 struct ActIn {
     const float* a;
     const float* b;
@@ -51,6 +56,20 @@ struct ActIn {
     float* h_out;
     long lda;
     float eps;
+    long split = 0;  // kActSwiGLU2: floats between the two partial sums
+    int kn = 0;      // kActSwiGLU2: K of the RMSNorm
+};
+
+// A decode-batch matmul whose K split over workgroups is left unreduced for its consumer:
+// C[m][n] = (part[m N + n] + part[stride + m N + n] + ... in split order) * f_m, with
+// f_m = 1/sqrt(sum over splits of ssq[s * 16 + m] / K + eps) when ssq is not null (RMSNorm),
+// else 1.  S = 0: C itself was written.
+struct SplitSums {
+    const float* part = nullptr;
+    const float* ssq = nullptr;
+    long stride = 0;
+    int S = 0, N = 0, K = 0;
+    float eps = 0.0f;
 };
 
 namespace detail {
@@ -78,15 +97,23 @@ int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N
 // (deterministic; the RMSNorm prologue splits too).  Without it a split (plain and SwiGLU
 // prologues, several activation chunks) adds into C with fp32 atomics.  Calls sharing one
 // workspace must be ordered on one stream.
+// defer (with ws): when the launch splits K into defer_S partial sums (any count for defer_S
+// = 0), the reduction is not launched and *defer describes the partial sums; otherwise
+// defer->S = 0 and C holds the result.
 int launch_skinny_act(int mode, int fmt, const ActIn& act, const void* B, float* C, int M, int N, int K,
-                      hipStream_t stream, float* ws = nullptr, long ws_floats = 0);
+                      hipStream_t stream, float* ws = nullptr, long ws_floats = 0, SplitSums* defer = nullptr,
+                      int defer_S = 0);
 long skinny_workspace_floats(int M, int N);
 // cri_matmul / cri_matmul_swiglu / cri_matmul_rmsnorm with that workspace (abi.cpp); return a cri_status
 int matmul_split_ws(int fmt, const float* A, const void* B, float* C, int M, int N, int K, float* ws, long ws_floats,
                     hipStream_t s);
 int matmul_rmsnorm_split_ws(int fmt, const float* hidden, const float* residual, const float* norm_weight,
                             float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, float* ws,
-                            long ws_floats, hipStream_t s);
+                            long ws_floats, hipStream_t s, SplitSums* defer = nullptr, int defer_S = 0);
+// the SwiGLU matmul of gate/up outputs left as two partial sums (kActSwiGLU2): gate at
+// gu.part, up at gu.part + up_off, the row factor from gu.ssq
+int matmul_swiglu2_split_ws(int fmt, const SplitSums& gu, long up_off, int ld, const void* B, float* C, int M, int N,
+                            int K, float* ws, long ws_floats, hipStream_t s);
 int matmul_swiglu_split_ws(int fmt, const float* gate, const float* up, int ld, const void* B, float* C, int M, int N,
                            int K, float* ws, long ws_floats, hipStream_t s);
 
@@ -162,9 +189,12 @@ int noalloc_scratch(float** out);
 // q rotated in place, rotated k and v written to the caches' rows *pos + m
 // (KVCache::append, ref:src/kv_cache.cu:157-211); caches [max_seq, n_kv_heads, head_dim];
 // rot: the (cos, sin) table [max_seq, head_dim / 2] of fp32 pairs
+// qkv (optional, S > 0): the q/k/v projection left as partial sums; q, k and v are then its
+// columns [0, ..), [kcol, ..) and [vcol, ..), reduced here, and q is written to q (row m at
+// q + m*ldq) rotated
 int launch_rope_append(float* q, long ldq, const float* k, long ldk, const float* v, long ldv, int rows, int n_heads,
                        int n_kv_heads, int head_dim, const float* rot, const int* pos, float* k_cache, float* v_cache,
-                       hipStream_t stream);
+                       hipStream_t stream, const SplitSums* qkv = nullptr, int kcol = 0, int vcol = 0);
 // out[m] = index of the largest logits[m][i], the smallest index among equal maxima, NaN ignored
 // (kernel_argmax, ref:src/embedding.cu:155-200); rows are cut into argmax_slices(n) slices whose
 // (value, index) go to part (2 floats each, rows * slices); counters: rows zeroed words (re-zeroed

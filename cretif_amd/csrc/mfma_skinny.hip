@@ -38,6 +38,7 @@
 #include "act.hpp"
 #include "common.hpp"
 #include "internal.hpp"
+#include "split.hpp"
 
 namespace cri {
 namespace dev {
@@ -55,6 +56,7 @@ constexpr int kSkChunk = 32768;
 // N x splits <= 32768 and the partial sums take at most 32768 M floats.
 constexpr int kSkMaxSplits = 16;
 constexpr long kSkPartOff = kSkMaxSplits * 16;
+static_assert(kSkMaxSplits <= kSplitMaxS, "the reduction reads up to kSplitMaxS splits");
 
 // Order of the 8 k values of one k8 group inside an operand register set: the
 // nibble unpack produces (0,2), (1,3), (4,6), (5,7) pairs.
@@ -195,8 +197,9 @@ __device__ void sk_stage(const ActIn& P, int M, int K, int k0, int KC, char* lds
     const int groups = KC / 8;  // k8 groups per row; a multiple of 32
     sk_clear_unscale<NT>(M, KC, unscale);
     const int total = M * groups;  // a multiple of 32
-    // items per load batch: the prologues hold 2x (SwiGLU) or 3x (RMSNorm) the raw values per item
-    constexpr int kItems = MODE == kActPlain ? kSkMaxItems : (MODE == kActSwiGLU ? 4 : 3);
+    // items per load batch: the prologues hold 2x (SwiGLU), 3x (RMSNorm) or 4x (SwiGLU of two
+    // partial sums) the raw values per item
+    constexpr int kItems = MODE == kActPlain ? kSkMaxItems : (MODE == kActSwiGLU ? 4 : (MODE == kActRMSNorm ? 3 : 2));
     for (int e_batch = 0; e_batch < total; e_batch += kItems * nth) {
         ActRaw<MODE> ra[kItems], rb[kItems];
 #pragma unroll
@@ -726,39 +729,23 @@ __device__ __forceinline__ float sum_splits(const float* p) {
 }
 
 // C = the S partial sums of a workspace K split added in split order, times the RMSNorm row
-// factor of all S sums of squares.  Four consecutive outputs per thread (N % 4 == 0, C 16-byte
+// factor of all S sums of squares (split.hpp's steps, which the consumers that read the
+// partial sums directly repeat).  Four consecutive outputs per thread (N % 4 == 0, C 16-byte
 // aligned: the launcher checks); every load is unconditional (splits past S read split S - 1,
 // unused), so all of a thread's loads are in flight together.
-template <int MODE>
-__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ ws, float* __restrict__ C, int M,
-                                                           int N, int K, int S, float eps) {
+__global__ __launch_bounds__(256) void split_reduce_kernel(const SplitSums p, float* __restrict__ C, int M) {
     const long i4 = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
-    const long mn = static_cast<long>(M) * N;
-    if (4 * i4 >= mn) return;
-    const float* src = ws + kSkPartOff + 4 * i4;
-    f32x4 p[kSkMaxSplits];
+    if (4 * i4 >= static_cast<long>(M) * p.N) return;
+    const float* src = p.part + 4 * i4;
+    f32x4 v[kSplitMaxS];
 #pragma unroll
-    for (int s = 0; s < kSkMaxSplits; ++s) p[s] = *reinterpret_cast<const f32x4*>(src + min(s, S - 1) * mn);
-    float fac = 1.0f;
-    if constexpr (MODE == kActRMSNorm) {
-        const int m = static_cast<int>(4 * i4 / N);
-        float sq[kSkMaxSplits];
+    for (int s = 0; s < kSplitMaxS; ++s) v[s] = *reinterpret_cast<const f32x4*>(src + min(s, p.S - 1) * p.stride);
+    const float fac = split_factor(p, static_cast<int>(4 * i4 / p.N));
+    f32x4 t = v[0];
 #pragma unroll
-        for (int s = 0; s < kSkMaxSplits; ++s) sq[s] = ws[min(s, S - 1) * 16 + m];
-        float ss = sq[0];
-#pragma unroll
-        for (int s = 1; s < kSkMaxSplits; ++s)
-            if (s < S) ss += sq[s];
-        fac = rms_factor(ss, K, eps);
-    } else {
-        (void)K;
-        (void)eps;
-    }
-    f32x4 v = p[0];
-#pragma unroll
-    for (int s = 1; s < kSkMaxSplits; ++s)
-        if (s < S) v += p[s];
-    *reinterpret_cast<f32x4*>(C + 4 * i4) = v * fac;
+    for (int s = 1; s < kSplitMaxS; ++s)
+        if (s < p.S) t += v[s];
+    *reinterpret_cast<f32x4*>(C + 4 * i4) = t * fac;
 }
 
 // Workgroup = NW waves = (NW / KS) tiles x KS k-splits.  The grid strides
@@ -775,7 +762,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
                                                              int ks_log2, int ngroups, int nchunks, int nblocks,
                                                              int cs_log2, float* __restrict__ part, const ActIn Pin) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const ActIn P{A, Pin.b, Pin.w, Pin.h_out, Pin.lda, Pin.eps};
+    const ActIn P{A, Pin.b, Pin.w, Pin.h_out, Pin.lda, Pin.eps, Pin.split, Pin.kn};
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, nl = lane & 15;
     const int KS = 1 << ks_log2;              // k-splits per tile (power of two)
@@ -1017,7 +1004,9 @@ static bool split_ws_fits(const float* ws, long ws_floats, const float* C, int M
 
 template <class F, int NW, int MODE, bool PAIR, int NPT, bool XPF = false>
 static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int K, int KC, int KS,
-                     hipStream_t stream, int cs_force = -1, float* ws = nullptr, long ws_floats = 0) {
+                     hipStream_t stream, int cs_force = -1, float* ws = nullptr, long ws_floats = 0,
+                     SplitSums* defer = nullptr, int defer_S = 0) {
+    if (defer) defer->S = 0;
     // large chunks need more than the default 64 KB of dynamic LDS: raise the limit once per kernel and device
     constexpr int kMaxDevices = 64;
     static std::atomic<bool> ready[kMaxDevices];
@@ -1069,24 +1058,37 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
     hipLaunchKernelGGL((dev::skinny_kernel<F, NW, MODE, PAIR, NPT, XPF>), dim3(blocks), dim3(64 * NW), L.bytes, stream,
                        static_cast<const uint8_t*>(B), C, A.a, M, N, K, KC, ks_log2, groups, nchunks, blocks, cs_log2,
                        part, A);
-    if (part)
-        hipLaunchKernelGGL(dev::split_reduce_kernel<MODE>, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256),
-                           0, stream, part, C, M, N, K, 1 << cs_log2, A.eps);
+    if (part) {
+        SplitSums sums;
+        sums.part = part + dev::kSkPartOff;
+        sums.ssq = MODE == kActRMSNorm ? part : nullptr;
+        sums.stride = mn;
+        sums.S = 1 << cs_log2;
+        sums.N = N;
+        sums.K = K;
+        sums.eps = A.eps;
+        if (defer && (defer_S == 0 || defer_S == sums.S))
+            *defer = sums;  // the consumer adds them up
+        else
+            hipLaunchKernelGGL(dev::split_reduce_kernel, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256),
+                               0, stream, sums, C, M);
+    }
     return 0;
 }
 
 // up to 8 activation rows: hi and lo parts share each MFMA (paired lane rows)
 template <class F, int MODE>
 static int launch_sk_rows(const ActIn& A, const void* B, float* C, int M, int N, int K, int KC, int KS,
-                          hipStream_t stream, int cs = -1, float* ws = nullptr, long wsf = 0) {
+                          hipStream_t stream, int cs = -1, float* ws = nullptr, long wsf = 0,
+                          SplitSums* df = nullptr, int dS = 0) {
     if (M <= 8) {
         // Q4_K with two activation items per thread (M = 1 at K = 8192, the FFN down
         // projection): their loads are issued at entry as well instead of after the
         // weights (measured 7.5 -> 6.7 us); the one-item kernel stays as it is
         if constexpr (std::is_same<F, dev::SkQ4K>::value)
             if (M * (KC / 8) > 512 && M * (KC / 8) <= 1024)
-                return launch_sk<F, 8, MODE, true, 2>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
-        return launch_sk<F, 8, MODE, true, 1>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
+                return launch_sk<F, 8, MODE, true, 2>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf, df, dS);
+        return launch_sk<F, 8, MODE, true, 1>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf, df, dS);
     }
     // Q4_K, more than 8 rows, plain activations, up to eight items per thread:
     // all of a chunk's activation loads are in registers ahead of time, and with
@@ -1096,15 +1098,17 @@ static int launch_sk_rows(const ActIn& A, const void* B, float* C, int M, int N,
     if constexpr (std::is_same<F, dev::SkQ4K>::value && MODE == kActPlain)
         if (M * (KC / 8) > 512 && M * (KC / 8) <= 4096) {
             if (K > KC && cs != static_cast<int>(__builtin_ctz(static_cast<unsigned>(K / KC))))
-                return launch_sk<F, 8, MODE, false, 8, true>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
-            return launch_sk<F, 8, MODE, false, 8, false>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
+                return launch_sk<F, 8, MODE, false, 8, true>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf, df, dS);
+            return launch_sk<F, 8, MODE, false, 8, false>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf, df, dS);
         }
-    return launch_sk<F, 8, MODE, false, 1>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
+    return launch_sk<F, 8, MODE, false, 1>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf, df, dS);
 }
 
 template <int MODE>
 static int launch_skinny_m(int fmt, const ActIn& A, const void* B, float* C, int M, int N, int K,
-                           hipStream_t stream, float* ws = nullptr, long wsf = 0) {
+                           hipStream_t stream, float* ws = nullptr, long wsf = 0, SplitSums* df = nullptr,
+                           int dS = 0) {
+    if (df) df->S = 0;
     // activation chunk: the largest multiple of 256 dividing K with M * KC <= kSkChunk
     // (few chunks: every chunk is staged once per workgroup)
     const int ntiles = (N + 15) / 16;
@@ -1119,12 +1123,15 @@ static int launch_skinny_m(int fmt, const ActIn& A, const void* B, float* C, int
     // Split K over workgroups instead: every wave takes its own 16-row tile (8 per workgroup)
     // and each workgroup one chunk of K, the chunks sized so that ~256 workgroups run.  A
     // staged activation then feeds 8 tiles instead of 8 / KS, and each workgroup stages only
-    // its chunk.  With a workspace the last workgroup of each tile group adds the partial sums
-    // (and applies the RMSNorm row factor): every shape splits.  Without one, the partial sums
+    // its chunk.  With a workspace a second launch (or the consumer) adds the partial sums and
+    // applies the RMSNorm row factor: every shape splits.  Without one, the partial sums
     // go into a zero-filled C with atomics, which pays only when the activations take several
     // chunks (K > KC, the FFN down projection; 2048 x 2048 at M = 16 measured 8.5 us unsplit,
     // 5.2 + 5.3 us split into 8 and reduced by a second launch), and not for the RMSNorm
     // prologue, whose row factor needs every chunk's sum of squares.
+    // (The single-chunk o projection, 2048 x 2048 at M = 16, traces 5.2 + 4.7 us split and
+    // reduced against 9.0 unsplit, yet the graph-replayed decode step is faster with the split:
+    // 1.135 against 1.168 ms.)
     const bool ws_split = ws && N % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15u) == 0 &&
                           wsf >= skinny_workspace_floats(M, N);
     int cs = -1;
@@ -1142,12 +1149,12 @@ static int launch_skinny_m(int fmt, const ActIn& A, const void* B, float* C, int
     // eight waves per workgroup (8 / KS tiles each): measured faster than four for
     // every decode shape, from 512 x 2048 to the 128256 x 2048 lm_head
     switch (fmt) {
-        case kFmtQ6_K: return launch_sk_rows<dev::SkQ6K, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
-        case kFmtQ4_K: return launch_sk_rows<dev::SkQ4K, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
-        case kFmtQ8_0: return launch_sk_rows<dev::SkQ8_0, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
-        case kFmtQ4_0: return launch_sk_rows<dev::SkQ4_0, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
-        case kFmtQ5_0: return launch_sk_rows<dev::SkQ5_0, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
-        case kFmtF16: return launch_sk_rows<dev::SkF16, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf);
+        case kFmtQ6_K: return launch_sk_rows<dev::SkQ6K, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf, df, dS);
+        case kFmtQ4_K: return launch_sk_rows<dev::SkQ4K, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf, df, dS);
+        case kFmtQ8_0: return launch_sk_rows<dev::SkQ8_0, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf, df, dS);
+        case kFmtQ4_0: return launch_sk_rows<dev::SkQ4_0, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf, df, dS);
+        case kFmtQ5_0: return launch_sk_rows<dev::SkQ5_0, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf, df, dS);
+        case kFmtF16: return launch_sk_rows<dev::SkF16, MODE>(A, B, C, M, N, K, KC, KS, stream, cs, ws, wsf, df, dS);
     }
     return -1;
 }
@@ -1158,11 +1165,17 @@ int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N
 }
 
 int launch_skinny_act(int mode, int fmt, const ActIn& act, const void* B, float* C, int M, int N, int K,
-                      hipStream_t stream, float* ws, long ws_floats) {
+                      hipStream_t stream, float* ws, long ws_floats, SplitSums* defer, int defer_S) {
+    if (defer) defer->S = 0;
     switch (mode) {
-        case kActPlain: return launch_skinny_m<kActPlain>(fmt, act, B, C, M, N, K, stream, ws, ws_floats);
-        case kActSwiGLU: return launch_skinny_m<kActSwiGLU>(fmt, act, B, C, M, N, K, stream, ws, ws_floats);
-        case kActRMSNorm: return launch_skinny_m<kActRMSNorm>(fmt, act, B, C, M, N, K, stream, ws, ws_floats);
+        case kActPlain:
+            return launch_skinny_m<kActPlain>(fmt, act, B, C, M, N, K, stream, ws, ws_floats, defer, defer_S);
+        case kActSwiGLU:
+            return launch_skinny_m<kActSwiGLU>(fmt, act, B, C, M, N, K, stream, ws, ws_floats, defer, defer_S);
+        case kActRMSNorm:
+            return launch_skinny_m<kActRMSNorm>(fmt, act, B, C, M, N, K, stream, ws, ws_floats, defer, defer_S);
+        case kActSwiGLU2:
+            return launch_skinny_m<kActSwiGLU2>(fmt, act, B, C, M, N, K, stream, ws, ws_floats, defer, defer_S);
     }
     return -1;
 }

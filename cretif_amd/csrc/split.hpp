@@ -1,0 +1,43 @@
+// split.hpp -- reading a decode-batch matmul whose K was split over workgroups
+// and left unreduced (SplitSums): the partial sums added in split order, times
+// the RMSNorm row factor of all splits' sums of squares.  The reduction kernel
+// and the consumers that take the partial sums directly use these same steps,
+// so C comes out bit-identical whichever of them adds it up.
+#pragma once
+
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace cri {
+namespace dev {
+
+constexpr int kSplitMaxS = 16;
+
+// 1/sqrt(sum_s ssq[s*16 + m] / K + eps) in split order, or 1 without RMSNorm;
+// every load unconditional (splits past S read split S - 1, unused)
+__device__ __forceinline__ float split_factor(const SplitSums& p, int m) {
+    if (!p.ssq) return 1.0f;
+    float sq[kSplitMaxS];
+#pragma unroll
+    for (int s = 0; s < kSplitMaxS; ++s) sq[s] = p.ssq[min(s, p.S - 1) * 16 + m];
+    float ss = sq[0];
+#pragma unroll
+    for (int s = 1; s < kSplitMaxS; ++s)
+        if (s < p.S) ss += sq[s];
+    return 1.0f / sqrtf(ss / static_cast<float>(p.K) + p.eps);
+}
+
+// sum over splits of part[s][off] in split order (off = m N + n)
+__device__ __forceinline__ float split_sum(const SplitSums& p, long off) {
+    float v[kSplitMaxS];
+#pragma unroll
+    for (int s = 0; s < kSplitMaxS; ++s) v[s] = p.part[min(s, p.S - 1) * p.stride + off];
+    float t = v[0];
+#pragma unroll
+    for (int s = 1; s < kSplitMaxS; ++s)
+        if (s < p.S) t += v[s];
+    return t;
+}
+
+}  // namespace dev
+}  // namespace cri

@@ -10,6 +10,7 @@
 
 #include "common.hpp"
 #include "internal.hpp"
+#include "split.hpp"
 
 namespace cri {
 namespace dev {
@@ -25,12 +26,16 @@ namespace dev {
 // than with fast device approximations).  The products are rounded separately
 // (no contraction), as in the reference's fp32 expression.  Rotated k and the
 // unchanged v go to cache row pos, as KVCache::append copies them
-// (ref:src/kv_cache.cu:181-196).
+// (ref:src/kv_cache.cu:181-196).  With qkv.S > 0 the q/k/v projection arrives
+// as its unreduced partial sums: q, k and v are its columns [0, ..), [kcol, ..)
+// and [vcol, ..), reduced here exactly as the reduction kernel would, and the
+// rotated q is written to q.
 __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q, long ldq, const float* __restrict__ k,
                                                           long ldk, const float* __restrict__ v, long ldv, int n_heads,
                                                           int n_kv_heads, int head_dim, const f32x2* __restrict__ rot,
                                                           const int* __restrict__ pos_dev, float* __restrict__ kc,
-                                                          float* __restrict__ vc) {
+                                                          float* __restrict__ vc, const SplitSums qkv, int kcol,
+                                                          int vcol) {
     const int m = blockIdx.y;
     const int pos = *pos_dev + m;
     const int half = head_dim / 2;
@@ -44,8 +49,17 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q,
         const int head = pi / half, lp = pi - head * half;
         const f32x2 cs = rot[static_cast<long>(pos) * half + lp];
         const long off = static_cast<long>(head) * head_dim + 2 * lp;
-        const float* src = isq ? q + m * ldq + off : k + m * ldk + off;
-        const float x0 = src[0], x1 = src[1];
+        float x0, x1;
+        if (qkv.S) {
+            const long e = static_cast<long>(m) * qkv.N + (isq ? 0 : kcol) + off;
+            const float f = split_factor(qkv, m);
+            x0 = split_sum(qkv, e) * f;
+            x1 = split_sum(qkv, e + 1) * f;
+        } else {
+            const float* src = isq ? q + m * ldq + off : k + m * ldk + off;
+            x0 = src[0];
+            x1 = src[1];
+        }
         const float y0 = __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y));
         const float y1 = __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
         float* dst = isq ? q + m * ldq + off : krow + off;
@@ -54,8 +68,15 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q,
     } else if (i < qpairs + kpairs + (kvd + 1) / 2) {
         const long e = 2L * (i - qpairs - kpairs);
         float* vrow = vc + static_cast<long>(pos) * kvd;
-        vrow[e] = v[m * ldv + e];
-        if (e + 1 < kvd) vrow[e + 1] = v[m * ldv + e + 1];
+        if (qkv.S) {
+            const long o = static_cast<long>(m) * qkv.N + vcol + e;
+            const float f = split_factor(qkv, m);
+            vrow[e] = split_sum(qkv, o) * f;
+            if (e + 1 < kvd) vrow[e + 1] = split_sum(qkv, o + 1) * f;
+        } else {
+            vrow[e] = v[m * ldv + e];
+            if (e + 1 < kvd) vrow[e + 1] = v[m * ldv + e + 1];
+        }
     }
 }
 
@@ -148,15 +169,17 @@ namespace detail {
 
 int launch_rope_append(float* q, long ldq, const float* k, long ldk, const float* v, long ldv, int rows, int n_heads,
                        int n_kv_heads, int head_dim, const float* rot, const int* pos, float* k_cache, float* v_cache,
-                       hipStream_t stream) {
+                       hipStream_t stream, const SplitSums* qkv, int kcol, int vcol) {
     if (rows < 1 || rows > 65535 || head_dim < 2 || head_dim % 2 != 0) return kDeclined;
+    const SplitSums none;
+    if (qkv && qkv->S > dev::kSplitMaxS) return kDeclined;
     const long kvd = static_cast<long>(n_kv_heads) * head_dim;
     const long work = static_cast<long>(n_heads + n_kv_heads) * (head_dim / 2) + (kvd + 1) / 2;
     const long blocks = (work + 255) / 256;
     if (blocks > 0x7FFFFFFFL) return kDeclined;
     hipLaunchKernelGGL(dev::rope_append_kernel, dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(rows)),
                        dim3(256), 0, stream, q, ldq, k, ldk, v, ldv, n_heads, n_kv_heads, head_dim,
-                       reinterpret_cast<const dev::f32x2*>(rot), pos, k_cache, v_cache);
+                       reinterpret_cast<const dev::f32x2*>(rot), pos, k_cache, v_cache, qkv ? *qkv : none, kcol, vcol);
     return 0;
 }
 

@@ -126,7 +126,7 @@ private:
     WeightFormat tok_fmt_ = WeightFormat::FP32, lm_fmt_ = WeightFormat::FP32;
     bool tok_set_ = false, out_set_ = false, lm_tied_ = false;
     Tensor k_cache_, v_cache_, pos_dev_;
-    Tensor hid_[2], normed_, qkv_, ctx_, attn_out_, ff_, act_, ffn_out_, attn_ws_, split_ws_;
+    Tensor hid_[2], normed_, qkv_, ctx_, attn_out_, ff_, act_, ffn_out_, attn_ws_, split_ws_, defer_ws_;
     Tensor argmax_part_, argmax_count_, rope_;
     int pos_host_ = 0;
     hipGraph_t graph_ = nullptr;

@@ -250,6 +250,38 @@ def test_step_mixed_formats_tied_fp32_head(orc, M):
     check_ids(nxt.cpu().numpy(), got, ref, ref_ids, tol)
 
 
+@pytest.mark.parametrize("fmt,M", [("q8_0", 12), ("q6_k", 9), ("fp16", 16)])
+def test_step_fused_projections_split(orc, fmt, M):
+    # one format throughout, so q/k/v and gate/up are stored fused; at 9..16 rows their K is
+    # split over workgroups and the partial sums are left for RoPE (q/k/v) and for the down
+    # projection's prologue (a two-way gate/up split) to add up
+    m = make_model(2, dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=2048, vocab=3000, seed=17,
+                   fmts={n: fmt for n in ("q", "k", "v", "o", "gate", "up", "down")}, tok="q8_0", lm=fmt,
+                   big_tables=False)
+    dec = make_decoder(m, max_seq=512)
+    kc, vc = random_cache(m, 512, 21)
+    load_cache(dec, kc, vc)
+    pos = 300
+    ids = np.random.default_rng(M + 5).integers(0, m["vocab"], M).astype(np.int32)
+    logits = torch.empty(M, m["vocab"], device="cuda")
+    nxt = torch.empty(M, dtype=torch.int32, device="cuda")
+    dec.set_position(pos)
+    dec.forward(torch.from_numpy(ids).cuda(), M, logits, nxt)
+    got = logits.cpu().numpy()
+    ref, ref_ids = orc.decode_step(m, list(ids), pos, kc, vc)
+    err = normwise_rel_err(got, ref)
+    print("fused-projection step %s M=%d: normwise err %.2e" % (fmt, M, err))
+    assert err <= TOL
+    check_ids(nxt.cpu().numpy(), got, ref, ref_ids, TOL)
+    k_tol = TOL + (pos + M) * 2.0 ** -23
+    for i in range(len(m["layers"])):
+        ka, va = dec.kv_cache(i)
+        shape = (512, m["n_kv_heads"], m["head_dim"])
+        gk, gv = from_device(ka, shape), from_device(va, shape)
+        assert normwise_rel_err(gk[pos:pos + M], kc[i][pos:pos + M]) <= k_tol
+        assert normwise_rel_err(gv[pos:pos + M], vc[i][pos:pos + M]) <= TOL
+
+
 def test_decoder_errors():
     m = make_model(1, dim=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=100, big_tables=False)
     with pytest.raises(cri.CretifError):  # n_heads not a multiple of n_kv_heads
