@@ -333,7 +333,29 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
         ldk = ldv = KVD;
     }
     cri::SplitSums qkv_sums;  // S > 0: the fused projection's partial sums, added up by RoPE
-    if (M <= kFusedMaxBatch) {
+    const int* pos = static_cast<const int*>(pos_dev_.data());
+    // one token, fused q/k/v: the GEMV rotates q and k and appends k and v to the caches in its
+    // epilogue (false: its layout declined, the RoPE kernel runs after the projection)
+    auto rope_gemv = [&]() {
+        cri::RopeOut R;
+        R.pos = pos;
+        R.rot = rope_.data_as<float>();
+        R.kc = k_cache(li);
+        R.vc = v_cache(li);
+        R.qd = QD;
+        R.kvd = KVD;
+        R.half = cfg_.head_dim / 2;
+        const cri::ActIn act{h, res, L.attn_norm.data_as<float>(), h_next, D, eps};
+        const int rc = cri::detail::launch_gemv_rope(cri_id(L.qkv_fmt), act, L.qkv.data(), q, QD + 2 * KVD, D, R, s);
+        if (rc == cri::detail::kDeclined) return false;
+        check_status(rc, "q/k/v projection with RoPE");
+        return true;
+    };
+    bool roped = false;
+    if (M == 1 && L.qkv_fused && rope_gemv()) {
+        roped = true;
+        cur = 1 - cur;
+    } else if (M <= kFusedMaxBatch) {
         // h_next = h + res; projections of RMSNorm(h_next) (the first writes h_next)
         if (L.qkv_fused) {
             norm_matmul(h, res, L.attn_norm.data_as<float>(), h_next, L.qkv, L.qkv_fmt, q, M, QD + 2 * KVD, D, eps,
@@ -357,11 +379,11 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
             matmul_dispatch(n, L.v, v, M, KVD, D, L.v_fmt, s);
         }
     }
-    const int* pos = static_cast<const int*>(pos_dev_.data());
-    check_status(cri::detail::launch_rope_append(q, ldq, k, ldk, v, ldv, M, cfg_.n_heads, cfg_.n_kv_heads,
-                                                 cfg_.head_dim, rope_.data_as<float>(), pos, k_cache(li),
-                                                 v_cache(li), s, &qkv_sums, QD, QD + KVD),
-                 "rope/append");
+    if (!roped)
+        check_status(cri::detail::launch_rope_append(q, ldq, k, ldk, v, ldv, M, cfg_.n_heads, cfg_.n_kv_heads,
+                                                     cfg_.head_dim, rope_.data_as<float>(), pos, k_cache(li),
+                                                     v_cache(li), s, &qkv_sums, QD, QD + KVD),
+                     "rope/append");
     // row m attends to positions [0, pos + m] (ref:src/attention.cu:60-75; one token: :410-511)
     const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
     const int nchunks = cri::detail::decode_attention_rows_chunks(cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim,

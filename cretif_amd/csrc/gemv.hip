@@ -41,10 +41,39 @@ namespace dev {
 // weights is multiplied with both rows, so a batch of two streams the weights once.
 // Workgroup row blockIdx.y takes activation rows MR y .. MR y + MR - 1 of mrows
 // (past the last row: the last row again, not stored).
-template <class F, int UPL, int PREF, int MODE, int MR = 1>
+// Output column n (value x, its pair partner xp) of the fused q/k/v projection: q and k
+// rotated by the angle of (position, pair) as the RoPE kernel does, q to q_out, k and v to
+// cache row pos.
+__device__ __forceinline__ void rope_out(const RopeOut& R, float* q_out, int n, float x, float xp) {
+    const int pos = *R.pos;
+    const long kvrow = static_cast<long>(pos) * R.kvd;
+    if (n < R.qd + R.kvd) {
+        const int nn = n < R.qd ? n : n - R.qd;
+        const int lp = (nn % (2 * R.half)) >> 1;
+        const f32x2 cs = reinterpret_cast<const f32x2*>(R.rot)[static_cast<long>(pos) * R.half + lp];
+        const bool odd = n & 1;
+        const float x0 = odd ? xp : x, x1 = odd ? x : xp;
+        const float v = odd ? __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x))
+                            : __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y));
+        if (n < R.qd)
+            q_out[n] = v;
+        else
+            R.kc[kvrow + nn] = v;
+    } else {
+        R.vc[kvrow + (n - R.qd - R.kvd)] = x;
+    }
+}
+
+// ROPE: the fused q/k/v projection of one token (RopeOut).  A wave's rows b .. b + 64 / LPR - 1
+// start at an even b (rows per iteration and the stride are even for LPR <= 32), so the
+// rotated pair (2i, 2i + 1) sits in lane groups rsub and rsub ^ 1, one shuffle apart; the
+// rotation is the RoPE kernel's (same table, products rounded separately).
+template <class F, int UPL, int PREF, int MODE, int MR = 1, bool ROPE = false>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W, float* __restrict__ y, int N, int K,
-                                                   int units, long row_bytes, int lpr_log2, const ActIn P, int mrows) {
+                                                   int units, long row_bytes, int lpr_log2, const ActIn P, int mrows,
+                                                   const RopeOut R) {
     static_assert(MR == 1 || MODE == kActPlain, "two activation rows: plain activations only");
+    static_assert(!ROPE || (MR == 1 && MODE == kActRMSNorm), "RoPE epilogue: the one-row RMSNorm GEMV");
     extern __shared__ float xs[];  // MR x K activations (padded, xpad), staged once per workgroup (+4 partial sums)
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
@@ -141,7 +170,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
             acc = group_sum(acc, lpr_log2);
             const int r = b + rsub;
             const int orow = MR * static_cast<int>(blockIdx.y) + m;
-            if (u0 == 0 && r < N && orow < mrows) y[static_cast<long>(orow) * N + r] = MODE == kActRMSNorm ? acc * rs : acc;
+            if constexpr (ROPE) {
+                const float x = acc * rs;
+                const float xp = __shfl_xor(x, 1 << lpr_log2);  // row r ^ 1 (every lane takes part)
+                if (u0 == 0 && r < N) rope_out(R, y, r, x, xp);
+            } else {
+                if (u0 == 0 && r < N && orow < mrows)
+                    y[static_cast<long>(orow) * N + r] = MODE == kActRMSNorm ? acc * rs : acc;
+            }
         }
     };
     for (int b = base0; b < N; b += PREF * stride) {
@@ -158,9 +194,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 
 namespace detail {
 
-template <class F, int UPL, int PREF, int MODE, int MR = 1>
+template <class F, int UPL, int PREF, int MODE, int MR = 1, bool ROPE = false>
 static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K, int units, long row_bytes,
-                          int lpr_log2, hipStream_t stream, int mrows = 1) {
+                          int lpr_log2, hipStream_t stream, int mrows = 1, const RopeOut& rope = RopeOut{}) {
     const int rows_per_iter = 64 >> lpr_log2;
     const long groups = (static_cast<long>(N) + rows_per_iter - 1) / rows_per_iter;
     // one wave per PREF row-groups (all of a small matrix is requested at once),
@@ -179,14 +215,15 @@ static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K
         int devid = 0;
         if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return kFailed;
         if (!ready[devid].load(std::memory_order_acquire)) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::gemv_kernel<F, UPL, PREF, MODE, MR>),
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::gemv_kernel<F, UPL, PREF, MODE, MR, ROPE>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
                 return kFailed;
             ready[devid].store(true, std::memory_order_release);
         }
     }
-    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE, MR>), dim3(blocks, (mrows + MR - 1) / MR), dim3(256), lds,
-                       stream, static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act, mrows);
+    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE, MR, ROPE>), dim3(blocks, (mrows + MR - 1) / MR), dim3(256),
+                       lds, stream, static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act, mrows,
+                       rope);
     return 0;
 }
 
@@ -260,6 +297,36 @@ int launch_gemv2(int fmt, const float* x, const void* W, float* y, int M, int N,
 int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream) {
     const ActIn act{x, nullptr, nullptr, nullptr, K, 0.0f};
     return launch_gemv_m<kActPlain>(fmt, act, W, y, N, K, stream);
+}
+
+// The RoPE epilogue needs each rotated pair inside one wave: at most 32 lanes per row (K <= 2048
+// at one unit per lane), which also keeps one unit per lane.
+template <class F>
+static int launch_gemv_rope_f(const ActIn& x, const void* W, float* q_out, int N, int K, long row_bytes,
+                              const RopeOut& rope, hipStream_t stream) {
+    const int units = K / 64;
+    int lpr_log2 = 0;
+    while ((1 << lpr_log2) < units && lpr_log2 < 6) ++lpr_log2;
+    if (units > 32 || lpr_log2 > 5) return kDeclined;
+    return launch_gemv_t<F, 1, F::kPref1, kActRMSNorm, 1, true>(x, W, q_out, N, K, units, row_bytes, lpr_log2, stream,
+                                                                 1, rope);
+}
+
+int launch_gemv_rope(int fmt, const ActIn& act, const void* W, float* q_out, int N, int K, const RopeOut& rope,
+                     hipStream_t stream) {
+    if ((dev::xpad(K) + 4) * 4 > 160 * 1024 || !gemv_supported(fmt, K, W)) return kDeclined;
+    if (rope.qd % 2 || rope.kvd % 2 || rope.half < 1 || rope.qd % (2 * rope.half) || rope.kvd % (2 * rope.half) ||
+        N != rope.qd + 2 * rope.kvd)
+        return kDeclined;
+    switch (fmt) {
+        case kFmtQ8_0: return launch_gemv_rope_f<dev::GemvQ8_0>(act, W, q_out, N, K, (K / 32) * 34L, rope, stream);
+        case kFmtQ4_0: return launch_gemv_rope_f<dev::GemvQ4_0>(act, W, q_out, N, K, (K / 32) * 18L, rope, stream);
+        case kFmtQ5_0: return launch_gemv_rope_f<dev::GemvQ5_0>(act, W, q_out, N, K, (K / 32) * 22L, rope, stream);
+        case kFmtQ4_K: return launch_gemv_rope_f<dev::GemvQ4K>(act, W, q_out, N, K, (K / 256) * 144L, rope, stream);
+        case kFmtQ6_K: return launch_gemv_rope_f<dev::GemvQ6K>(act, W, q_out, N, K, (K / 256) * 210L, rope, stream);
+        case kFmtF16: return launch_gemv_rope_f<dev::GemvF16>(act, W, q_out, N, K, K * 2L, rope, stream);
+    }
+    return kDeclined;
 }
 
 int launch_gemv_act(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t stream) {

@@ -60,6 +60,18 @@ struct ActIn {
     int kn = 0;      // kActSwiGLU2: K of the RMSNorm
 };
 
+// The q/k/v projection's outputs at one decode position, rotated and appended in the GEMV's
+// epilogue: columns [0, qd) are q (rotated, to the output), [qd, qd + kvd) k (rotated, to
+// kc + pos kvd) and [qd + kvd, qd + 2 kvd) v (to vc + pos kvd); pos = *pos_dev; rot: the
+// [max_seq, half] table of (cos, sin) pairs of the RoPE kernel (half = head_dim / 2).
+struct RopeOut {
+    const int* pos = nullptr;
+    const float* rot = nullptr;
+    float* kc = nullptr;
+    float* vc = nullptr;
+    int qd = 0, kvd = 0, half = 0;
+};
+
 // A decode-batch matmul whose K split over workgroups is left unreduced for its consumer:
 // C[m][n] = (part[m N + n] + part[stride + m N + n] + ... in split order) * f_m, with
 // f_m = 1/sqrt(sum over splits of ssq[s * 16 + m] / K + eps) when ssq is not null (RMSNorm),
@@ -88,6 +100,10 @@ bool gemv_supported(int fmt, int K, const void* W);
 int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream);
 int launch_gemv2(int fmt, const float* x, const void* W, float* y, int M, int N, int K, hipStream_t stream);
 int launch_gemv_act(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t stream);
+// the RMSNorm-prologue GEMV of a fused q/k/v projection with RoPE and the cache append in its
+// epilogue (RopeOut); kDeclined when the layout does not put each rotated pair in one wave
+int launch_gemv_rope(int fmt, const ActIn& act, const void* W, float* q_out, int N, int K, const RopeOut& rope,
+                     hipStream_t stream);
 
 // 1 <= M <= 16 fused dequant matmul on the matrix cores (mfma_skinny.hip)
 bool skinny_supported(int fmt, int M, int K, const void* B);

@@ -250,11 +250,12 @@ def test_step_mixed_formats_tied_fp32_head(orc, M):
     check_ids(nxt.cpu().numpy(), got, ref, ref_ids, tol)
 
 
-@pytest.mark.parametrize("fmt,M", [("q8_0", 12), ("q6_k", 9), ("fp16", 16)])
+@pytest.mark.parametrize("fmt,M", [("q8_0", 12), ("q6_k", 9), ("fp16", 16), ("q5_0", 1), ("q6_k", 1)])
 def test_step_fused_projections_split(orc, fmt, M):
     # one format throughout, so q/k/v and gate/up are stored fused; at 9..16 rows their K is
     # split over workgroups and the partial sums are left for RoPE (q/k/v) and for the down
-    # projection's prologue (a two-way gate/up split) to add up
+    # projection's prologue (a two-way gate/up split) to add up; at one row the q/k/v GEMV
+    # rotates and appends to the caches in its epilogue
     m = make_model(2, dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=2048, vocab=3000, seed=17,
                    fmts={n: fmt for n in ("q", "k", "v", "o", "gate", "up", "down")}, tok="q8_0", lm=fmt,
                    big_tables=False)
