@@ -269,6 +269,11 @@ int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float*
     if (!aligned(C, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "C must be 4-byte aligned");
     if (fmt == cri::kFmtF16 && !aligned(B, 2)) return fail(CRI_ERR_ALIGNMENT, fn, "FP16 B must be 2-byte aligned");
     clear_pending_error();
+    if (mode == cri::kActRMSNormS) {  // one token on the batch-1 GEMV only
+        if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
+            return finish_matmul(cri::detail::launch_gemv_act(mode, fmt, act, B, C, N, K, stream), fn);
+        return fail(CRI_ERR_UNSUPPORTED, fn, "a split residual is taken by the batch-1 GEMV only");
+    }
     int rc = cri::detail::kDeclined;
     if (cri::detail::skinny_supported(fmt, M, K, B))
         rc = cri::detail::launch_skinny_act(mode, fmt, act, B, C, M, N, K, stream, ws, ws_floats, defer, defer_S);
@@ -508,6 +513,17 @@ int matmul_rmsnorm_split_ws(int fmt, const float* hidden, const float* residual,
                             long ws_floats, hipStream_t s, SplitSums* defer, int defer_S) {
     return rmsnorm_impl(fmt, hidden, residual, norm_weight, hidden_out, B, C, M, N, K, eps, s,
                         "matmul_rmsnorm (decode step)", ws, ws_floats, defer, defer_S);
+}
+int matmul_rmsnorm_splitres(int fmt, const float* hidden, const float* res_parts, int splits, long split,
+                            const float* norm_weight, float* hidden_out, const void* B, float* C, int N, int K,
+                            float eps, hipStream_t s) {
+    const char* fn = "matmul_rmsnorm with a split residual (decode step)";
+    if (splits < 1 || splits > kResMaxSplits || split < K || !hidden || !res_parts || !norm_weight)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "bad residual partial sums");
+    cri::ActIn act{hidden, res_parts, norm_weight, hidden_out, K, eps};
+    act.split = split;
+    act.kn = splits;
+    return fused_matmul(cri::kActRMSNormS, fmt, act, B, C, 1, N, K, s, fn);
 }
 int matmul_swiglu2_split_ws(int fmt, const SplitSums& gu, long up_off, int ld, const void* B, float* C, int M, int N,
                             int K, float* ws, long ws_floats, hipStream_t s) {

@@ -31,6 +31,10 @@ struct ActRaw<kActRMSNorm> {
     f32x4 h, r, w;
 };
 template <>
+struct ActRaw<kActRMSNormS> {
+    f32x4 h, r[kResMaxSplits], w;
+};
+template <>
 struct ActRaw<kActSwiGLU2> {
     f32x4 g0, g1, u0, u1;
     float s0, s1;  // the two splits' sums of squares of row m
@@ -46,6 +50,11 @@ __device__ __forceinline__ void act_load(ActRaw<MODE>& raw, const ActIn& P, int 
     } else if constexpr (MODE == kActSwiGLU) {
         raw.g = ld_f32x4(P.a + off);
         raw.u = ld_f32x4(P.b + off);
+    } else if constexpr (MODE == kActRMSNormS) {
+        raw.h = ld_f32x4(P.a + off);
+#pragma unroll
+        for (int s = 0; s < kResMaxSplits; ++s) raw.r[s] = ld_f32x4(P.b + min(s, P.kn - 1) * P.split + off);
+        raw.w = ld_f32x4(P.w + k);
     } else if constexpr (MODE == kActSwiGLU2) {
         raw.g0 = ld_f32x4(P.a + off);
         raw.g1 = ld_f32x4(P.a + P.split + off);
@@ -89,7 +98,16 @@ __device__ __forceinline__ f32x4 act_finish(const ActRaw<MODE>& raw, const ActIn
         const f32x4 g = (raw.g0 + raw.g1) * f, u = (raw.u0 + raw.u1) * f;
         return f32x4{silu_f(g.x) * u.x, silu_f(g.y) * u.y, silu_f(g.z) * u.z, silu_f(g.w) * u.w};
     } else {
-        const f32x4 v = raw.h + raw.r;
+        f32x4 r;
+        if constexpr (MODE == kActRMSNormS) {  // the residual's partial sums, in split order
+            r = raw.r[0];
+#pragma unroll
+            for (int s = 1; s < kResMaxSplits; ++s)
+                if (s < P.kn) r += raw.r[s];
+        } else {
+            r = raw.r;
+        }
+        const f32x4 v = raw.h + r;
         ss = __builtin_fmaf(v.x, v.x, ss);
         ss = __builtin_fmaf(v.y, v.y, ss);
         ss = __builtin_fmaf(v.z, v.z, ss);

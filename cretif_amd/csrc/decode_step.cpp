@@ -27,6 +27,9 @@ namespace {
 
 // Batches up to this many tokens take the fused RMSNorm / SwiGLU prologues.
 constexpr int kFusedMaxBatch = 16;
+// K parts of the one-token down projection (its partial sums go to the next RMSNorm prologue)
+constexpr int kDownSplits = 4;
+static_assert(kDownSplits <= cri::kResMaxSplits, "the RMSNorm prologue adds up at most kResMaxSplits parts");
 
 DType dtype_of(WeightFormat f) {
     switch (f) {
@@ -163,6 +166,7 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     // zeroed once; the argmax kernel that counts in them leaves them zero again
     argmax_part_ = Tensor::empty({MB * cri::detail::argmax_slices(c.vocab_size) * 2});
     argmax_count_ = Tensor::zeros({MB});
+    res_parts_ = Tensor::empty({static_cast<int64_t>(cri::kResMaxSplits) * c.dim});
     // RoPE (cos, sin) per (position, pair), ref:src/kernels/elementwise.cu:241-248: the frequency
     // 1 / theta^(2i / head_dim) and the angle pos * freq with the reference's fp32 operations,
     // theta^e, cos and sin in double rounded once to fp32
@@ -345,8 +349,11 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
         R.qd = QD;
         R.kvd = KVD;
         R.half = cfg_.head_dim / 2;
-        const cri::ActIn act{h, res, L.attn_norm.data_as<float>(), h_next, D, eps};
-        const int rc = cri::detail::launch_gemv_rope(cri_id(L.qkv_fmt), act, L.qkv.data(), q, QD + 2 * KVD, D, R, s);
+        cri::ActIn act{h, res, L.attn_norm.data_as<float>(), h_next, D, eps};
+        act.split = D;
+        act.kn = res_splits_;
+        const int rc = cri::detail::launch_gemv_rope(cri_id(L.qkv_fmt), act, L.qkv.data(), q, QD + 2 * KVD, D, R, s,
+                                                     res_splits_ > 0);
         if (rc == cri::detail::kDeclined) return false;
         check_status(rc, "q/k/v projection with RoPE");
         return true;
@@ -354,6 +361,16 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
     bool roped = false;
     if (M == 1 && L.qkv_fused && rope_gemv()) {
         roped = true;
+        cur = 1 - cur;
+    } else if (res_splits_) {  // one token, the residual as partial sums (q/k/v GEMVs add them up)
+        const float* an = L.attn_norm.data_as<float>();
+        if (L.qkv_fused) {
+            norm_matmul_splitres(h, an, h_next, L.qkv, L.qkv_fmt, q, QD + 2 * KVD, s, "q/k/v projection");
+        } else {
+            norm_matmul_splitres(h, an, h_next, L.q, L.q_fmt, q, QD, s, "q projection");
+            norm_matmul_splitres(h, an, nullptr, L.k, L.k_fmt, k, KVD, s, "k projection");
+            norm_matmul_splitres(h, an, nullptr, L.v, L.v_fmt, v, KVD, s, "v projection");
+        }
         cur = 1 - cur;
     } else if (M <= kFusedMaxBatch) {
         // h_next = h + res; projections of RMSNorm(h_next) (the first writes h_next)
@@ -397,16 +414,52 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
                                            split_ws_.numel(), s),
               "o projection");
     res = attn_out_.data_as<float>();
+    res_splits_ = 0;
+}
+
+bool DecodeStep::next_takes_split(int li) const {
+    const int D = cfg_.dim;
+    if (li + 1 < cfg_.n_layers) {
+        const Layer& N = *layers_[li + 1];
+        if (N.qkv_fused) return cri::detail::gemv_supported(cri_id(N.qkv_fmt), D, N.qkv.data());
+        return cri::detail::gemv_supported(cri_id(N.q_fmt), D, N.q.data()) &&
+               cri::detail::gemv_supported(cri_id(N.k_fmt), D, N.k.data()) &&
+               cri::detail::gemv_supported(cri_id(N.v_fmt), D, N.v.data());
+    }
+    const Tensor& W = lm_tied_ ? tok_table_ : lm_head_;
+    const WeightFormat wf = lm_tied_ ? tok_fmt_ : lm_fmt_;
+    return wf != WeightFormat::FP32 && cri::detail::gemv_supported(cri_id(wf), D, W.data());
+}
+
+void DecodeStep::norm_matmul_splitres(const float* h, const float* norm_w, float* h_out, const Tensor& W,
+                                      WeightFormat f, float* C, int N, hipStream_t s, const char* what) {
+    const int D = cfg_.dim;
+    check_cri(cri::detail::matmul_rmsnorm_splitres(cri_id(f), h, res_parts_.data_as<float>(), res_splits_, D, norm_w,
+                                                   h_out, W.data(), C, N, D, cfg_.rms_norm_eps, s),
+              what);
 }
 
 // hidden[cur] (+ attn_out) -> RMSNorm -> gate/up -> SiLU(gate) * up -> down: ffn_out
-void DecodeStep::ffn_block(Layer& L, int M, int& cur, const float*& res, hipStream_t s) {
+void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res, hipStream_t s) {
     const int D = cfg_.dim, F = cfg_.intermediate_size, MB = cfg_.max_batch;
     const float eps = cfg_.rms_norm_eps;
     float* h = hid_[cur].data_as<float>();
     float* h_next = hid_[1 - cur].data_as<float>();
     float* ff = ff_.data_as<float>();
     float* ffn_out = ffn_out_.data_as<float>();
+    // One token: the down GEMV splits K into kDownSplits parts (each workgroup stages that share
+    // of the SwiGLU activations instead of all of them) and leaves the partial sums for the next
+    // RMSNorm prologue to add up (false: not taken, C is computed whole).
+    bool split_down = false;
+    auto down_split = [&](const float* gate, const float* up, int ld) {
+        if (M != 1 || !next_takes_split(li)) return false;
+        const cri::ActIn act{gate, up, nullptr, nullptr, ld, 0.0f};
+        const int rc = cri::detail::launch_gemv_ksplit(cri::kActSwiGLU, cri_id(L.down_fmt), act, L.down.data(),
+                                                       res_parts_.data_as<float>(), D, F, kDownSplits, s);
+        if (rc == cri::detail::kDeclined) return false;
+        check_status(rc, "down projection (K split)");
+        return true;
+    };
     if (M <= kFusedMaxBatch) {
         if (L.gu_fused) {
             // ff rows: [gate (F) | up (F)]
@@ -418,7 +471,7 @@ void DecodeStep::ffn_block(Layer& L, int M, int& cur, const float*& res, hipStre
                 check_cri(cri::detail::matmul_swiglu2_split_ws(cri_id(L.down_fmt), gu, F, 2 * F, L.down.data(), ffn_out,
                                                                M, D, F, split_ws_.data_as<float>(), split_ws_.numel(), s),
                           "down projection");
-            else
+            else if (!(split_down = down_split(ff, ff + F, 2 * F)))
                 check_cri(cri::detail::matmul_swiglu_split_ws(cri_id(L.down_fmt), ff, ff + F, 2 * F, L.down.data(),
                                                               ffn_out, M, D, F, split_ws_.data_as<float>(),
                                                               split_ws_.numel(), s),
@@ -429,9 +482,10 @@ void DecodeStep::ffn_block(Layer& L, int M, int& cur, const float*& res, hipStre
                         "gate projection");
             norm_matmul(h, res, L.ffn_norm.data_as<float>(), nullptr, L.up, L.up_fmt, up, M, F, D, eps, split_ws_, s,
                         "up projection");
-            check_cri(cri::detail::matmul_swiglu_split_ws(cri_id(L.down_fmt), ff, up, F, L.down.data(), ffn_out, M, D,
-                                                          F, split_ws_.data_as<float>(), split_ws_.numel(), s),
-                      "down projection");
+            if (!(split_down = down_split(ff, up, F)))
+                check_cri(cri::detail::matmul_swiglu_split_ws(cri_id(L.down_fmt), ff, up, F, L.down.data(), ffn_out, M,
+                                                              D, F, split_ws_.data_as<float>(), split_ws_.numel(), s),
+                          "down projection");
         }
         cur = 1 - cur;
     } else {
@@ -451,7 +505,12 @@ void DecodeStep::ffn_block(Layer& L, int M, int& cur, const float*& res, hipStre
         silu_mul(gate, up, act_.data_as<float>(), static_cast<long long>(M) * F, s);  // ref:src/model.cu:996-997
         matmul_dispatch(act_.data_as<float>(), L.down, ffn_out, M, D, F, L.down_fmt, s);
     }
-    res = ffn_out;
+    if (split_down) {
+        res = res_parts_.data_as<float>();
+        res_splits_ = kDownSplits;
+    } else {
+        res = ffn_out;
+    }
 }
 
 void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s) {
@@ -463,16 +522,21 @@ void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next
         cri_embedding_rows(cri_id(tok_fmt_), tok_table_.data(), ids, hid_[0].data_as<float>(), M, D, V, s));
     int cur = 0;
     const float* res = nullptr;  // residual still to be added to hidden[cur]
+    res_splits_ = 0;
     for (int li = 0; li < cfg_.n_layers; ++li) {
         Layer& L = *layers_[li];
         attn_block(L, li, M, cur, res, s);
-        ffn_block(L, M, cur, res, s);
+        ffn_block(L, li, M, cur, res, s);
     }
     // final RMSNorm(hidden + ffn_out) and the LM head
     const Tensor& W = lm_tied_ ? tok_table_ : lm_head_;
     const WeightFormat wf = lm_tied_ ? tok_fmt_ : lm_fmt_;
     float* h = hid_[cur].data_as<float>();
-    if (wf != WeightFormat::FP32 && M <= kFusedMaxBatch) {
+    if (res_splits_) {  // one token, the last down projection's partial sums
+        norm_matmul_splitres(h, out_norm_.data_as<float>(), hid_[1 - cur].data_as<float>(), W, wf, logits, V, s,
+                             "LM head");
+        res_splits_ = 0;
+    } else if (wf != WeightFormat::FP32 && M <= kFusedMaxBatch) {
         matmul_dispatch_rmsnorm(h, res, out_norm_.data_as<float>(), hid_[1 - cur].data_as<float>(), W, logits, M, V,
                                 D, wf, eps, s);
     } else {

@@ -68,12 +68,24 @@ __device__ __forceinline__ void rope_out(const RopeOut& R, float* q_out, int n, 
 // start at an even b (rows per iteration and the stride are even for LPR <= 32), so the
 // rotated pair (2i, 2i + 1) sits in lane groups rsub and rsub ^ 1, one shuffle apart; the
 // rotation is the RoPE kernel's (same table, products rounded separately).
-template <class F, int UPL, int PREF, int MODE, int MR = 1, bool ROPE = false>
+// KSPLIT: K is cut into gridDim.y parts; workgroup row blockIdx.y takes columns
+// [K blockIdx.y, K (blockIdx.y + 1)) of the weights (K, units: one part's) and of the
+// activations, and writes its partial sums to y + blockIdx.y N.
+template <class F, int UPL, int PREF, int MODE, int MR = 1, bool ROPE = false, bool KSPLIT = false>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W, float* __restrict__ y, int N, int K,
-                                                   int units, long row_bytes, int lpr_log2, const ActIn P, int mrows,
+                                                   int units, long row_bytes, int lpr_log2, const ActIn Pin, int mrows,
                                                    const RopeOut R) {
+    constexpr bool kRms = MODE == kActRMSNorm || MODE == kActRMSNormS;
     static_assert(MR == 1 || MODE == kActPlain, "two activation rows: plain activations only");
-    static_assert(!ROPE || (MR == 1 && MODE == kActRMSNorm), "RoPE epilogue: the one-row RMSNorm GEMV");
+    static_assert(!ROPE || (MR == 1 && kRms), "RoPE epilogue: the one-row RMSNorm GEMV");
+    static_assert(!KSPLIT || (MR == 1 && !kRms && !ROPE), "K split: one row, no row factor");
+    ActIn P = Pin;
+    const int kp = KSPLIT ? static_cast<int>(blockIdx.y) : 0;
+    if constexpr (KSPLIT) {
+        P.a += static_cast<long>(kp) * K;
+        if (P.b) P.b += static_cast<long>(kp) * K;
+        y += static_cast<long>(kp) * N;
+    }
     extern __shared__ float xs[];  // MR x K activations (padded, xpad), staged once per workgroup (+4 partial sums)
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
@@ -84,13 +96,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     const int stride = nwaves * rows_per_iter;  // rows between a wave's consecutive row-groups
 
-    int unit[UPL];
+    int unit[UPL], wunit[UPL];  // unit inside the staged activations / the weight row
     bool valid[UPL];
 #pragma unroll
     for (int u = 0; u < UPL; ++u) {
         const int un = u0 + u * lpr;
         valid[u] = un < units;
         unit[u] = valid[u] ? un : 0;  // idle lanes decode a real unit and discard it
+        wunit[u] = unit[u] + kp * units;  // a part starts on a 256-column boundary: unit % 4 is kept
     }
 
     // 1. activations: global -> registers (issued first, tiny), weights in flight behind them
@@ -102,7 +115,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int j = threadIdx.x + 256 * i;
-            if (j < nx4) act_load<MODE>(xv[m][i], P, min(MR * static_cast<int>(blockIdx.y) + m, mrows - 1), 4 * j, P.lda);
+            if (j < nx4) act_load<MODE>(xv[m][i], P, min(MR * (KSPLIT ? 0 : static_cast<int>(blockIdx.y)) + m, mrows - 1), 4 * j, P.lda);
         }
     typename F::Data buf[PREF][UPL];
     const int base0 = gwave * rows_per_iter;
@@ -113,7 +126,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
         const int r = min(b + rsub, N - 1);
         const uint8_t* rp = real ? W + static_cast<long>(r) * row_bytes : W;
 #pragma unroll
-        for (int u = 0; u < UPL; ++u) F::load(dst[u], rp, real ? unit[u] : 0);
+        for (int u = 0; u < UPL; ++u) F::load(dst[u], rp, real ? wunit[u] : 0);
     };
     // Every prefetch is issued unconditionally (row-groups past the end are
     // placeholder reads): a load under a condition leaves the compiler unsure how
@@ -138,16 +151,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             ActRaw<MODE> raw;
-            act_load<MODE>(raw, P, min(MR * static_cast<int>(blockIdx.y) + m, mrows - 1), 4 * j, P.lda);
+            act_load<MODE>(raw, P, min(MR * (KSPLIT ? 0 : static_cast<int>(blockIdx.y)) + m, mrows - 1), 4 * j, P.lda);
             *reinterpret_cast<f32x4*>(xs + m * xrow + xpad(4 * j)) = act_finish<MODE>(raw, P, m, 4 * j, K, ss, write_h);
         }
-    if constexpr (MODE == kActRMSNorm) {
+    if constexpr (kRms) {
         ss = group_sum_t<6>(ss);
         if (lane == 0) xs[xpad(K) + (threadIdx.x >> 6)] = ss;
     }
     __syncthreads();
     float rs = 1.0f;
-    if constexpr (MODE == kActRMSNorm) {
+    if constexpr (kRms) {
         const float* part = xs + xpad(K);
         rs = rms_factor(((part[0] + part[1]) + part[2]) + part[3], K, P.eps);
     }
@@ -169,14 +182,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
             }
             acc = group_sum(acc, lpr_log2);
             const int r = b + rsub;
-            const int orow = MR * static_cast<int>(blockIdx.y) + m;
+            const int orow = MR * (KSPLIT ? 0 : static_cast<int>(blockIdx.y)) + m;
             if constexpr (ROPE) {
                 const float x = acc * rs;
                 const float xp = __shfl_xor(x, 1 << lpr_log2);  // row r ^ 1 (every lane takes part)
                 if (u0 == 0 && r < N) rope_out(R, y, r, x, xp);
             } else {
                 if (u0 == 0 && r < N && orow < mrows)
-                    y[static_cast<long>(orow) * N + r] = MODE == kActRMSNorm ? acc * rs : acc;
+                    y[static_cast<long>(orow) * N + r] = kRms ? acc * rs : acc;
             }
         }
     };
@@ -194,9 +207,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 
 namespace detail {
 
-template <class F, int UPL, int PREF, int MODE, int MR = 1, bool ROPE = false>
+template <class F, int UPL, int PREF, int MODE, int MR = 1, bool ROPE = false, bool KSPLIT = false>
 static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K, int units, long row_bytes,
-                          int lpr_log2, hipStream_t stream, int mrows = 1, const RopeOut& rope = RopeOut{}) {
+                          int lpr_log2, hipStream_t stream, int mrows = 1, const RopeOut& rope = RopeOut{},
+                          int splits = 1) {
     const int rows_per_iter = 64 >> lpr_log2;
     const long groups = (static_cast<long>(N) + rows_per_iter - 1) / rows_per_iter;
     // one wave per PREF row-groups (all of a small matrix is requested at once),
@@ -206,24 +220,26 @@ static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K
     // 4.08 us, 512 x 2048 5.14 -> 3.90, Q8_0 1536 x 576 3.11 -> 2.81) are bound
     // by each wave's serial chain, not by bytes in flight
     long waves = (UPL == 1 && (F::kSpread || groups <= kGemvTargetWaves)) ? groups : (groups + PREF - 1) / PREF;
-    if (waves > kGemvTargetWaves) waves = kGemvTargetWaves;
+    const long budget = KSPLIT ? kGemvTargetWaves / splits : kGemvTargetWaves;  // over all K parts
+    if (waves > budget) waves = budget;
     const int blocks = static_cast<int>((waves + 3) / 4);
-    const int lds = (MR * dev::xpad(K) + (MODE == kActRMSNorm ? 4 : 0)) * static_cast<int>(sizeof(float));
+    constexpr bool kRms = MODE == kActRMSNorm || MODE == kActRMSNormS;
+    const int lds = (MR * dev::xpad(K) + (kRms ? 4 : 0)) * static_cast<int>(sizeof(float));
     if (lds > 65536) {  // beyond the default dynamic-LDS limit: raise it once per kernel and device
         constexpr int kMaxDevices = 64;
         static std::atomic<bool> ready[kMaxDevices];
         int devid = 0;
         if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return kFailed;
         if (!ready[devid].load(std::memory_order_acquire)) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::gemv_kernel<F, UPL, PREF, MODE, MR, ROPE>),
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::gemv_kernel<F, UPL, PREF, MODE, MR, ROPE, KSPLIT>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
                 return kFailed;
             ready[devid].store(true, std::memory_order_release);
         }
     }
-    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE, MR, ROPE>), dim3(blocks, (mrows + MR - 1) / MR), dim3(256),
-                       lds, stream, static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act, mrows,
-                       rope);
+    const unsigned gy = KSPLIT ? static_cast<unsigned>(splits) : static_cast<unsigned>((mrows + MR - 1) / MR);
+    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE, MR, ROPE, KSPLIT>), dim3(blocks, gy), dim3(256), lds,
+                       stream, static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act, mrows, rope);
     return 0;
 }
 
@@ -303,28 +319,68 @@ int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, 
 // at one unit per lane), which also keeps one unit per lane.
 template <class F>
 static int launch_gemv_rope_f(const ActIn& x, const void* W, float* q_out, int N, int K, long row_bytes,
-                              const RopeOut& rope, hipStream_t stream) {
+                              const RopeOut& rope, hipStream_t stream, bool split_res) {
     const int units = K / 64;
     int lpr_log2 = 0;
     while ((1 << lpr_log2) < units && lpr_log2 < 6) ++lpr_log2;
     if (units > 32 || lpr_log2 > 5) return kDeclined;
+    if (split_res)
+        return launch_gemv_t<F, 1, F::kPref1, kActRMSNormS, 1, true>(x, W, q_out, N, K, units, row_bytes, lpr_log2,
+                                                                      stream, 1, rope);
     return launch_gemv_t<F, 1, F::kPref1, kActRMSNorm, 1, true>(x, W, q_out, N, K, units, row_bytes, lpr_log2, stream,
                                                                  1, rope);
 }
 
+// K split: one unit per lane where it fits (the part's units <= 64)
+template <class F, int MODE>
+static int launch_gemv_ksplit_f(const ActIn& x, const void* W, float* y, int N, int K, long row_bytes, int splits,
+                                hipStream_t stream) {
+    const int Ks = K / splits, units = Ks / 64;
+    int lpr_log2 = 0;
+    while ((1 << lpr_log2) < units && lpr_log2 < 6) ++lpr_log2;
+    if (units > 64) return kDeclined;
+    return launch_gemv_t<F, 1, F::kPref1, MODE, 1, false, true>(x, W, y, N, Ks, units, row_bytes, lpr_log2, stream, 1,
+                                                                 RopeOut{}, splits);
+}
+
+template <int MODE>
+static int launch_gemv_ksplit_m(int fmt, const ActIn& act, const void* W, float* y, int N, int K, int splits,
+                                hipStream_t stream) {
+    switch (fmt) {
+        case kFmtQ8_0: return launch_gemv_ksplit_f<dev::GemvQ8_0, MODE>(act, W, y, N, K, (K / 32) * 34L, splits, stream);
+        case kFmtQ4_0: return launch_gemv_ksplit_f<dev::GemvQ4_0, MODE>(act, W, y, N, K, (K / 32) * 18L, splits, stream);
+        case kFmtQ5_0: return launch_gemv_ksplit_f<dev::GemvQ5_0, MODE>(act, W, y, N, K, (K / 32) * 22L, splits, stream);
+        case kFmtQ4_K: return launch_gemv_ksplit_f<dev::GemvQ4K, MODE>(act, W, y, N, K, (K / 256) * 144L, splits, stream);
+        case kFmtQ6_K: return launch_gemv_ksplit_f<dev::GemvQ6K, MODE>(act, W, y, N, K, (K / 256) * 210L, splits, stream);
+        case kFmtF16: return launch_gemv_ksplit_f<dev::GemvF16, MODE>(act, W, y, N, K, K * 2L, splits, stream);
+    }
+    return kDeclined;
+}
+
+int launch_gemv_ksplit(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, int splits,
+                       hipStream_t stream) {
+    if (splits < 2 || splits > kResMaxSplits || K % (256 * splits) != 0 || !gemv_supported(fmt, K, W)) return kDeclined;
+    if ((dev::xpad(K / splits) + 4) * 4 > 160 * 1024) return kDeclined;
+    switch (mode) {
+        case kActPlain: return launch_gemv_ksplit_m<kActPlain>(fmt, act, W, y, N, K, splits, stream);
+        case kActSwiGLU: return launch_gemv_ksplit_m<kActSwiGLU>(fmt, act, W, y, N, K, splits, stream);
+    }
+    return kDeclined;
+}
+
 int launch_gemv_rope(int fmt, const ActIn& act, const void* W, float* q_out, int N, int K, const RopeOut& rope,
-                     hipStream_t stream) {
+                     hipStream_t stream, bool split_res) {
     if ((dev::xpad(K) + 4) * 4 > 160 * 1024 || !gemv_supported(fmt, K, W)) return kDeclined;
     if (rope.qd % 2 || rope.kvd % 2 || rope.half < 1 || rope.qd % (2 * rope.half) || rope.kvd % (2 * rope.half) ||
         N != rope.qd + 2 * rope.kvd)
         return kDeclined;
     switch (fmt) {
-        case kFmtQ8_0: return launch_gemv_rope_f<dev::GemvQ8_0>(act, W, q_out, N, K, (K / 32) * 34L, rope, stream);
-        case kFmtQ4_0: return launch_gemv_rope_f<dev::GemvQ4_0>(act, W, q_out, N, K, (K / 32) * 18L, rope, stream);
-        case kFmtQ5_0: return launch_gemv_rope_f<dev::GemvQ5_0>(act, W, q_out, N, K, (K / 32) * 22L, rope, stream);
-        case kFmtQ4_K: return launch_gemv_rope_f<dev::GemvQ4K>(act, W, q_out, N, K, (K / 256) * 144L, rope, stream);
-        case kFmtQ6_K: return launch_gemv_rope_f<dev::GemvQ6K>(act, W, q_out, N, K, (K / 256) * 210L, rope, stream);
-        case kFmtF16: return launch_gemv_rope_f<dev::GemvF16>(act, W, q_out, N, K, K * 2L, rope, stream);
+        case kFmtQ8_0: return launch_gemv_rope_f<dev::GemvQ8_0>(act, W, q_out, N, K, (K / 32) * 34L, rope, stream, split_res);
+        case kFmtQ4_0: return launch_gemv_rope_f<dev::GemvQ4_0>(act, W, q_out, N, K, (K / 32) * 18L, rope, stream, split_res);
+        case kFmtQ5_0: return launch_gemv_rope_f<dev::GemvQ5_0>(act, W, q_out, N, K, (K / 32) * 22L, rope, stream, split_res);
+        case kFmtQ4_K: return launch_gemv_rope_f<dev::GemvQ4K>(act, W, q_out, N, K, (K / 256) * 144L, rope, stream, split_res);
+        case kFmtQ6_K: return launch_gemv_rope_f<dev::GemvQ6K>(act, W, q_out, N, K, (K / 256) * 210L, rope, stream, split_res);
+        case kFmtF16: return launch_gemv_rope_f<dev::GemvF16>(act, W, q_out, N, K, K * 2L, rope, stream, split_res);
     }
     return kDeclined;
 }
@@ -335,6 +391,7 @@ int launch_gemv_act(int mode, int fmt, const ActIn& act, const void* W, float* y
         case kActPlain: return launch_gemv_m<kActPlain>(fmt, act, W, y, N, K, stream);
         case kActSwiGLU: return launch_gemv_m<kActSwiGLU>(fmt, act, W, y, N, K, stream);
         case kActRMSNorm: return launch_gemv_m<kActRMSNorm>(fmt, act, W, y, N, K, stream);
+        case kActRMSNormS: return launch_gemv_m<kActRMSNormS>(fmt, act, W, y, N, K, stream);
     }
     return -1;
 }

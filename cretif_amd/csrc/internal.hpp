@@ -48,7 +48,10 @@ inline long row_bytes(int fmt, int K) { return static_cast<long>(K / block_elems
 //                 g = f_m (a[off] + a[off + split]), u likewise from b, with
 //                 f_m = 1/sqrt((w[m] + w[16 + m]) / kn + eps) (w: the two splits'
 //                 sums of squares), then silu(g) * u
-enum : int { kActPlain = 0, kActSwiGLU = 1, kActRMSNorm = 2, kActSwiGLU2 = 3 };
+//   kActRMSNormS: kActRMSNorm with the residual left as kn (<= 4) partial sums of a K
+//                 split: r = b[off] + b[off + split] + ... in split order (the batch-1 GEMV)
+enum : int { kActPlain = 0, kActSwiGLU = 1, kActRMSNorm = 2, kActSwiGLU2 = 3, kActRMSNormS = 4 };
+constexpr int kResMaxSplits = 4;
 struct ActIn {
     const float* a;
     const float* b;
@@ -56,8 +59,8 @@ struct ActIn {
     float* h_out;
     long lda;
     float eps;
-    long split = 0;  // kActSwiGLU2: floats between the two partial sums
-    int kn = 0;      // kActSwiGLU2: K of the RMSNorm
+    long split = 0;  // kActSwiGLU2, kActRMSNormS: floats between consecutive partial sums
+    int kn = 0;      // kActSwiGLU2: K of the RMSNorm; kActRMSNormS: number of partial sums
 };
 
 // The q/k/v projection's outputs at one decode position, rotated and appended in the GEMV's
@@ -100,10 +103,15 @@ bool gemv_supported(int fmt, int K, const void* W);
 int launch_gemv(int fmt, const float* x, const void* W, float* y, int N, int K, hipStream_t stream);
 int launch_gemv2(int fmt, const float* x, const void* W, float* y, int M, int N, int K, hipStream_t stream);
 int launch_gemv_act(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t stream);
+// batch-1 GEMV with K split into `splits` parts (grid.y), part s written to y + s N (partial
+// sums for a kActRMSNormS consumer); plain or SwiGLU prologue, K / splits a multiple of 256
+int launch_gemv_ksplit(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, int splits,
+                       hipStream_t stream);
 // the RMSNorm-prologue GEMV of a fused q/k/v projection with RoPE and the cache append in its
 // epilogue (RopeOut); kDeclined when the layout does not put each rotated pair in one wave
+// (split_res: the residual arrives as partial sums, kActRMSNormS)
 int launch_gemv_rope(int fmt, const ActIn& act, const void* W, float* q_out, int N, int K, const RopeOut& rope,
-                     hipStream_t stream);
+                     hipStream_t stream, bool split_res = false);
 
 // 1 <= M <= 16 fused dequant matmul on the matrix cores (mfma_skinny.hip)
 bool skinny_supported(int fmt, int M, int K, const void* B);
@@ -126,6 +134,11 @@ int matmul_split_ws(int fmt, const float* A, const void* B, float* C, int M, int
 int matmul_rmsnorm_split_ws(int fmt, const float* hidden, const float* residual, const float* norm_weight,
                             float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, float* ws,
                             long ws_floats, hipStream_t s, SplitSums* defer = nullptr, int defer_S = 0);
+// RMSNorm(hidden + residual) times B for one token, the residual given as `splits` partial sums
+// `split` floats apart (kActRMSNormS); hidden_out as in cri_matmul_rmsnorm
+int matmul_rmsnorm_splitres(int fmt, const float* hidden, const float* res_parts, int splits, long split,
+                            const float* norm_weight, float* hidden_out, const void* B, float* C, int N, int K,
+                            float eps, hipStream_t s);
 // the SwiGLU matmul of gate/up outputs left as two partial sums (kActSwiGLU2): gate at
 // gu.part, up at gu.part + up_off, the row factor from gu.ssq
 int matmul_swiglu2_split_ws(int fmt, const SplitSums& gu, long up_off, int ld, const void* B, float* C, int M, int N,

@@ -117,7 +117,13 @@ private:
     void enqueue(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, hipStream_t stream);
     void check_ready() const;
     void attn_block(Layer& L, int li, int M, int& cur, const float*& res, hipStream_t s);
-    void ffn_block(Layer& L, int M, int& cur, const float*& res, hipStream_t s);
+    void ffn_block(Layer& L, int li, int M, int& cur, const float*& res, hipStream_t s);
+    // the consumer of layer li's FFN output (the next q/k/v or the LM head) is a batch-1 GEMV
+    // that can add the down projection's K-split partial sums itself
+    bool next_takes_split(int li) const;
+    // RMSNorm(h + res) times W for one token with res as res_splits_ partial sums
+    void norm_matmul_splitres(const float* h, const float* norm_w, float* h_out, const Tensor& W, WeightFormat f,
+                              float* C, int N, hipStream_t s, const char* what);
 
     DecodeStepConfig cfg_;
     int q_dim_ = 0, kv_dim_ = 0;
@@ -128,6 +134,8 @@ private:
     Tensor k_cache_, v_cache_, pos_dev_;
     Tensor hid_[2], normed_, qkv_, ctx_, attn_out_, ff_, act_, ffn_out_, attn_ws_, split_ws_, defer_ws_;
     Tensor argmax_part_, argmax_count_, rope_;
+    Tensor res_parts_;    // the down projection's K-split partial sums at one token
+    int res_splits_ = 0;  // > 0: the pending residual is that many partial sums in res_parts_
     int pos_host_ = 0;
     hipGraph_t graph_ = nullptr;
     hipGraphExec_t graph_exec_ = nullptr;

@@ -222,13 +222,14 @@ def test_batch16_replay_equals_eager(llama2):
     assert np.array_equal(b.cpu().numpy().view(np.uint32), eager.view(np.uint32))
 
 
-@pytest.mark.parametrize("M", [17, 12, 3])
+@pytest.mark.parametrize("M", [17, 12, 3, 1])
 def test_step_mixed_formats_tied_fp32_head(orc, M):
     # q/k/v and gate/up of different formats (three / two separate matrices), an FP32 token
     # table tied to the LM head (matmul_transposed_b), head_dim 128 (the 8-slice attention
     # layout); for M = 12 every format's K split over workgroups with the step's workspace (the
-    # RMSNorm prologue included), and for M = 17 the unfused path (rmsnorm_residual, prefill
-    # GEMM, silu_mul)
+    # RMSNorm prologue included), for M = 17 the unfused path (rmsnorm_residual, prefill GEMM,
+    # silu_mul), for M = 1 the first layer's down projection split into partial sums that the
+    # separate q, k and v GEMVs of the second add up (the FP32 head takes a whole residual)
     m = make_model(2, dim=512, n_heads=4, n_kv_heads=2, head_dim=128, ffn=1024, vocab=1000, seed=7,
                    fmts={"q": "q8_0", "k": "q4_0", "v": "q5_0", "o": "fp16", "gate": "q6_k", "up": "q4_k",
                          "down": "q8_0"}, tok="fp32", lm=None, big_tables=False)
