@@ -517,15 +517,20 @@ __global__ __launch_bounds__(64) void decode_attn_mrow_kernel(const float* __res
         }
         __syncthreads();  // the P tile is rewritten by the next tile
     };
-    // the next tile's loads are in flight while the current one is computed
+    // the next tile's loads are in flight while the current one is computed; a chunk of one
+    // tile (the decode batch at up to 64 x 32 positions) loads just that tile
     Tile T0, T1;
     load_tile(T0, t0);
-    for (int tb = t0; tb < t1; tb += 2 * kSplitTile) {
-        load_tile(T1, tb + kSplitTile);  // past t1: clamped reads, not computed
-        run_tile(T0, tb);
-        if (tb + kSplitTile >= t1) break;
-        load_tile(T0, tb + 2 * kSplitTile);
-        run_tile(T1, tb + kSplitTile);
+    if (t1 - t0 <= kSplitTile) {
+        if (t0 < t1) run_tile(T0, t0);
+    } else {
+        for (int tb = t0; tb < t1; tb += 2 * kSplitTile) {
+            load_tile(T1, tb + kSplitTile);  // past t1: clamped reads, not computed
+            run_tile(T0, tb);
+            if (tb + kSplitTile >= t1) break;
+            load_tile(T0, tb + 2 * kSplitTile);
+            run_tile(T1, tb + kSplitTile);
+        }
     }
 
     // records: (max, sum, acc[64]) per query, the sum over the half-wave's lanes
