@@ -58,7 +58,9 @@ constexpr int kPrefillMinM = 16;
 int fill_zero(float* C, long n, hipStream_t stream, const char* fn);
 
 int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream,
-                const char* fn, float* ws = nullptr, long ws_floats = 0) {
+                const char* fn, float* ws = nullptr, long ws_floats = 0, cri::SplitSums* defer = nullptr,
+                int defer_S = 0) {
+    if (defer) defer->S = 0;
     if (M < 0 || N < 0 || K < 0)
         return fail(CRI_ERR_INVALID_ARGUMENT, fn,
                     "negative dimension (M=" + std::to_string(M) + ", N=" + std::to_string(N) +
@@ -86,7 +88,7 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
         rc = cri::detail::launch_gemv2(fmt, A, B, C, M, N, K, stream);
     else if (cri::detail::skinny_supported(fmt, M, K, B))
         rc = cri::detail::launch_skinny_act(cri::kActPlain, fmt, cri::ActIn{A, nullptr, nullptr, nullptr, K, 0.0f}, B,
-                                            C, M, N, K, stream, ws, ws_floats);
+                                            C, M, N, K, stream, ws, ws_floats, defer, defer_S);
     else if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv(fmt, A, B, C, N, K, stream);
     else if (M > kPrefillMinM && cri::detail::prefill_supported(fmt, M, N, K, A, B))
@@ -315,14 +317,15 @@ int cri_matmul_rmsnorm(int format, const float* hidden, const float* residual, c
 
 namespace {
 int swiglu_impl(int format, const float* gate, const float* up, int ld, const void* B, float* C, int M, int N, int K,
-                hipStream_t s, const char* fn, float* ws, long ws_floats) {
+                hipStream_t s, const char* fn, float* ws, long ws_floats, cri::SplitSums* defer = nullptr,
+                int defer_S = 0) {
     if (M > 0 && N > 0 && K > 0) {
         if (!gate || !up) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null gate or up");
         if (ld < K) return fail(CRI_ERR_SHAPE, fn, "ld=" + std::to_string(ld) + " is below K=" + std::to_string(K));
         if (!aligned(gate, 4) || !aligned(up, 4)) return fail(CRI_ERR_ALIGNMENT, fn, "gate and up must be 4-byte aligned");
     }
     const cri::ActIn act{gate, up, nullptr, nullptr, ld, 0.0f};
-    return fused_matmul(cri::kActSwiGLU, format, act, B, C, M, N, K, s, fn, ws, ws_floats);
+    return fused_matmul(cri::kActSwiGLU, format, act, B, C, M, N, K, s, fn, ws, ws_floats, defer, defer_S);
 }
 }  // namespace
 
@@ -501,12 +504,13 @@ int cri_version(void) { return 100; }
 namespace cri {
 namespace detail {
 int matmul_split_ws(int fmt, const float* A, const void* B, float* C, int M, int N, int K, float* ws, long ws_floats,
-                    hipStream_t s) {
-    return matmul_impl(fmt, A, B, C, M, N, K, s, "matmul (decode step)", ws, ws_floats);
+                    hipStream_t s, SplitSums* defer, int defer_S) {
+    return matmul_impl(fmt, A, B, C, M, N, K, s, "matmul (decode step)", ws, ws_floats, defer, defer_S);
 }
 int matmul_swiglu_split_ws(int fmt, const float* gate, const float* up, int ld, const void* B, float* C, int M, int N,
-                           int K, float* ws, long ws_floats, hipStream_t s) {
-    return swiglu_impl(fmt, gate, up, ld, B, C, M, N, K, s, "matmul_swiglu (decode step)", ws, ws_floats);
+                           int K, float* ws, long ws_floats, hipStream_t s, SplitSums* defer, int defer_S) {
+    return swiglu_impl(fmt, gate, up, ld, B, C, M, N, K, s, "matmul_swiglu (decode step)", ws, ws_floats, defer,
+                       defer_S);
 }
 int matmul_rmsnorm_split_ws(int fmt, const float* hidden, const float* residual, const float* norm_weight,
                             float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, float* ws,
@@ -526,14 +530,17 @@ int matmul_rmsnorm_splitres(int fmt, const float* hidden, const float* res_parts
     return fused_matmul(cri::kActRMSNormS, fmt, act, B, C, 1, N, K, s, fn);
 }
 int matmul_swiglu2_split_ws(int fmt, const SplitSums& gu, long up_off, int ld, const void* B, float* C, int M, int N,
-                            int K, float* ws, long ws_floats, hipStream_t s) {
+                            int K, float* ws, long ws_floats, hipStream_t s, SplitSums* defer, int defer_S) {
     const char* fn = "matmul_swiglu2 (decode step)";
-    if (gu.S != 2 || !gu.part || !gu.ssq || ld < K || up_off < K)
-        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "expects the two partial sums of an RMSNorm gate/up matmul");
+    if ((gu.S != 1 && gu.S != 2) || !gu.part || ld < K || up_off < K)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "expects one or two partial sums of a gate/up matmul");
     cri::ActIn act{gu.part, gu.part + up_off, gu.ssq, nullptr, ld, gu.eps};
-    act.split = gu.stride;
+    act.split = gu.S == 2 ? gu.stride : 0;
+    act.nss = gu.nss ? gu.nss : gu.S;
+    if (act.nss < 1 || act.nss > cri::kResMaxSplits)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "up to four sums of squares per row");
     act.kn = gu.K;
-    return fused_matmul(cri::kActSwiGLU2, fmt, act, B, C, M, N, K, s, fn, ws, ws_floats);
+    return fused_matmul(cri::kActSwiGLU2, fmt, act, B, C, M, N, K, s, fn, ws, ws_floats, defer, defer_S);
 }
 }  // namespace detail
 }  // namespace cri

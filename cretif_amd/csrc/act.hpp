@@ -37,7 +37,7 @@ struct ActRaw<kActRMSNormS> {
 template <>
 struct ActRaw<kActSwiGLU2> {
     f32x4 g0, g1, u0, u1;
-    float s0, s1;  // the two splits' sums of squares of row m
+    float s[kResMaxSplits];  // the sums of squares of row m (nss of them used)
 };
 
 // Loads of x[m][k .. k+4) (k % 4 == 0, all four in range); rows lda floats apart
@@ -60,8 +60,9 @@ __device__ __forceinline__ void act_load(ActRaw<MODE>& raw, const ActIn& P, int 
         raw.g1 = ld_f32x4(P.a + P.split + off);
         raw.u0 = ld_f32x4(P.b + off);
         raw.u1 = ld_f32x4(P.b + P.split + off);
-        raw.s0 = P.w[m];
-        raw.s1 = P.w[16 + m];
+        const float* sq = P.w ? P.w : P.a;  // without sums of squares: an unused in-bounds read
+#pragma unroll
+        for (int i = 0; i < kResMaxSplits; ++i) raw.s[i] = sq[16 * min(i, P.nss - 1) + m];
     } else {
         raw.h = ld_f32x4(P.a + off);
         raw.r = P.b ? ld_f32x4(P.b + off) : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -93,9 +94,14 @@ __device__ __forceinline__ f32x4 act_finish(const ActRaw<MODE>& raw, const ActIn
                      silu_f(raw.g.w) * raw.u.w};
     } else if constexpr (MODE == kActSwiGLU2) {
         (void)m; (void)k; (void)K; (void)ss; (void)write_h;
-        // the reduction kernel's steps: (split 0 + split 1) * row factor
-        const float f = 1.0f / sqrtf((raw.s0 + raw.s1) / static_cast<float>(P.kn) + P.eps);
-        const f32x4 g = (raw.g0 + raw.g1) * f, u = (raw.u0 + raw.u1) * f;
+        // the reduction kernel's steps: (split 0 + split 1) * row factor (1 without RMSNorm)
+        float ss = raw.s[0];
+#pragma unroll
+        for (int i = 1; i < kResMaxSplits; ++i)
+            if (i < P.nss) ss += raw.s[i];
+        const float f = P.w ? 1.0f / sqrtf(ss / static_cast<float>(P.kn) + P.eps) : 1.0f;
+        // (split 0: one partial sum, the second load read it again)
+        const f32x4 g = (P.split ? raw.g0 + raw.g1 : raw.g0) * f, u = (P.split ? raw.u0 + raw.u1 : raw.u0) * f;
         return f32x4{silu_f(g.x) * u.x, silu_f(g.y) * u.y, silu_f(g.z) * u.z, silu_f(g.w) * u.w};
     } else {
         f32x4 r;

@@ -97,6 +97,22 @@ int cri_id(WeightFormat f) {
 // RMSNorm(h + res) times W on the decode-batch kernels, with a split workspace (the first call
 // of a layer writes h + res to h_out); with defer, a K split into defer_S partial sums (any
 // count for 0) is left in ws for the consumer (defer->S = 0: C was written)
+// the residual for launch_split_norm: `count` partial sums `stride` floats apart, or the plain
+// residual (one part), or none
+cri::SplitSums residual_sums(const float* part, long stride, int count, const float* res, int dim) {
+    cri::SplitSums r;
+    r.N = dim;
+    if (count > 0) {
+        r.part = part;
+        r.stride = stride;
+        r.S = count;
+    } else if (res) {
+        r.part = res;
+        r.S = 1;
+    }
+    return r;
+}
+
 void norm_matmul(const float* h, const float* res, const float* norm_w, float* h_out, const Tensor& W, WeightFormat f,
                  float* C, int M, int N, int K, float eps, Tensor& ws, hipStream_t s, const char* what,
                  cri::SplitSums* defer = nullptr, int defer_S = 0) {
@@ -167,6 +183,7 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     argmax_part_ = Tensor::empty({MB * cri::detail::argmax_slices(c.vocab_size) * 2});
     argmax_count_ = Tensor::zeros({MB});
     res_parts_ = Tensor::empty({static_cast<int64_t>(cri::kResMaxSplits) * c.dim});
+    norm_ss_ = Tensor::zeros({256});
     // RoPE (cos, sin) per (position, pair), ref:src/kernels/elementwise.cu:241-248: the frequency
     // 1 / theta^(2i / head_dim) and the angle pos * freq with the reference's fp32 operations,
     // theta^e, cos and sin in double rounded once to fp32
@@ -409,12 +426,21 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
                                                            M, cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim, pos, 1,
                                                            nchunks, scale, attn_ws_.data_as<float>(), s),
                  "attention");
+    // (9..16 tokens: its partial sums are left for the FFN's RMSNorm row kernel)
+    cri::SplitSums o_sums;
     check_cri(cri::detail::matmul_split_ws(cri_id(L.o_fmt), ctx_.data_as<float>(), L.o.data(),
                                            attn_out_.data_as<float>(), M, D, QD, split_ws_.data_as<float>(),
-                                           split_ws_.numel(), s),
+                                           split_ws_.numel(), s, split_flow(M) ? &o_sums : nullptr),
               "o projection");
     res = attn_out_.data_as<float>();
     res_splits_ = 0;
+    res_part_ = o_sums.part;
+    res_part_stride_ = o_sums.stride;
+    res_part_count_ = o_sums.S;
+}
+
+bool DecodeStep::split_flow(int M) const {
+    return M > 8 && M <= kFusedMaxBatch && cfg_.dim % (4 * cri::detail::kNormParts) == 0 && cfg_.dim <= 4096;
 }
 
 bool DecodeStep::next_takes_split(int li) const {
@@ -460,7 +486,48 @@ void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res,
         check_status(rc, "down projection (K split)");
         return true;
     };
-    if (M <= kFusedMaxBatch) {
+    if (split_flow(M)) {
+        // for the fused gate/up the row factor is left out of normed and applied by the down
+        // projection's prologue to gate/up's sums, which also adds up a two-way split of them
+        float* ss = L.gu_fused ? norm_ss_.data_as<float>() : nullptr;
+        check_status(cri::detail::launch_split_norm(h, residual_sums(res_part_, res_part_stride_, res_part_count_, res, D),
+                                                    L.ffn_norm.data_as<float>(), h_next, normed_.data_as<float>(), M,
+                                                    D, eps, s, ss),
+                     "FFN RMSNorm");
+        const float* n = normed_.data_as<float>();
+        float* w = split_ws_.data_as<float>();
+        const long wn = split_ws_.numel();
+        if (L.gu_fused) {
+            cri::SplitSums gu;
+            check_cri(cri::detail::matmul_split_ws(cri_id(L.gu_fmt), n, L.gu.data(), ff, M, 2 * F, D,
+                                                   defer_ws_.data_as<float>(), defer_ws_.numel(), s, &gu, 2),
+                      "gate/up projection");
+            if (!gu.S) {  // reduced (or never split) into ff: one partial sum
+                gu.part = ff;
+                gu.stride = 0;
+                gu.S = 1;
+            }
+            gu.ssq = ss;
+            gu.nss = cri::detail::kNormParts;
+            gu.K = D;
+            gu.eps = eps;
+            check_cri(cri::detail::matmul_swiglu2_split_ws(cri_id(L.down_fmt), gu, F, 2 * F, L.down.data(), ffn_out, M,
+                                                           D, F, w, wn, s),
+                      "down projection");
+        } else {
+            float* up = ff + static_cast<long>(MB) * F;
+            float* dw = defer_ws_.data_as<float>();
+            const long dwn = defer_ws_.numel();
+            check_cri(cri::detail::matmul_split_ws(cri_id(L.gate_fmt), n, L.gate.data(), ff, M, F, D, dw, dwn, s),
+                      "gate projection");
+            check_cri(cri::detail::matmul_split_ws(cri_id(L.up_fmt), n, L.up.data(), up, M, F, D, dw, dwn, s),
+                      "up projection");
+            check_cri(cri::detail::matmul_swiglu_split_ws(cri_id(L.down_fmt), ff, up, F, L.down.data(), ffn_out, M, D,
+                                                          F, w, wn, s),
+                      "down projection");
+        }
+        cur = 1 - cur;
+    } else if (M <= kFusedMaxBatch) {
         if (L.gu_fused) {
             // ff rows: [gate (F) | up (F)]
             // a two-way K split of gate/up is added up inside the down projection's prologue
@@ -511,6 +578,7 @@ void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res,
     } else {
         res = ffn_out;
     }
+    res_part_count_ = 0;
 }
 
 void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s) {
@@ -523,6 +591,7 @@ void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next
     int cur = 0;
     const float* res = nullptr;  // residual still to be added to hidden[cur]
     res_splits_ = 0;
+    res_part_count_ = 0;
     for (int li = 0; li < cfg_.n_layers; ++li) {
         Layer& L = *layers_[li];
         attn_block(L, li, M, cur, res, s);
@@ -532,7 +601,19 @@ void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next
     const Tensor& W = lm_tied_ ? tok_table_ : lm_head_;
     const WeightFormat wf = lm_tied_ ? tok_fmt_ : lm_fmt_;
     float* h = hid_[cur].data_as<float>();
-    if (res_splits_) {  // one token, the last down projection's partial sums
+    if (split_flow(M)) {  // the final RMSNorm as a row kernel, the LM head on plain activations
+        check_status(cri::detail::launch_split_norm(h, residual_sums(res_part_, res_part_stride_, res_part_count_, res, D),
+                                                    out_norm_.data_as<float>(), hid_[1 - cur].data_as<float>(),
+                                                    normed_.data_as<float>(), M, D, eps, s),
+                     "final RMSNorm");
+        res_part_count_ = 0;
+        if (wf == WeightFormat::FP32)
+            matmul_transposed_b(normed_.data_as<float>(), W.data_as<float>(), logits, M, V, D, s);
+        else
+            check_cri(cri::detail::matmul_split_ws(cri_id(wf), normed_.data_as<float>(), W.data(), logits, M, V, D,
+                                                   split_ws_.data_as<float>(), split_ws_.numel(), s),
+                      "LM head");
+    } else if (res_splits_) {  // one token, the last down projection's partial sums
         norm_matmul_splitres(h, out_norm_.data_as<float>(), hid_[1 - cur].data_as<float>(), W, wf, logits, V, s,
                              "LM head");
         res_splits_ = 0;

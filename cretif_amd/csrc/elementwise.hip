@@ -11,6 +11,7 @@
 #include "act.hpp"
 #include "common.hpp"
 #include "internal.hpp"
+#include "split.hpp"
 
 namespace cri {
 namespace dev {
@@ -85,6 +86,70 @@ __global__ __launch_bounds__(256) void rmsnorm_residual_vec_kernel(const float* 
     }
 }
 
+// rmsnorm_residual_vec_kernel with the residual given as the partial sums of a decode-batch
+// matmul whose K was split over workgroups (SplitSums r, no row factor; r.S = 0: no residual):
+// they are added in split order (split.hpp's steps, so h_out equals what the reduction
+// kernel followed by rmsnorm_residual would give), then output = h + r and normed as above.
+// With row_ss, normed = v * weight without the row factor: workgroup (g, row) takes columns
+// [g n / G, (g + 1) n / G) of the row (G = gridDim.x parts, more workgroups reading the partial
+// sums) and writes their sum of v^2 to row_ss[16 g + row], for consumers that apply the factor
+// to their fp32 outputs (SplitSums.ssq).  Without it G = 1.  Parts of up to 4096 floats,
+// 16-byte aligned.
+__global__ __launch_bounds__(256) void split_norm_kernel(const float* __restrict__ h, const SplitSums r,
+                                                         const float* __restrict__ weight, float* __restrict__ output,
+                                                         float* __restrict__ normed, int n, float eps,
+                                                         float* __restrict__ row_ss) {
+    __shared__ float part[4];
+    const long row = blockIdx.y;
+    const int cw = n / static_cast<int>(gridDim.x), c0 = static_cast<int>(blockIdx.x) * cw;
+    f32x4 v[4], w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int o = 4 * (threadIdx.x + 256 * j), i = c0 + o;
+        if (o < cw) {
+            v[j] = *reinterpret_cast<const f32x4*>(h + row * n + i);
+            if (r.S) {
+                const float* src = r.part + row * r.N + i;
+                f32x4 p[kSplitMaxS];
+#pragma unroll
+                for (int s = 0; s < kSplitMaxS; ++s) p[s] = *reinterpret_cast<const f32x4*>(src + min(s, r.S - 1) * r.stride);
+                f32x4 t = p[0];
+#pragma unroll
+                for (int s = 1; s < kSplitMaxS; ++s)
+                    if (s < r.S) t += p[s];
+                v[j] += t;
+            }
+            w[j] = *reinterpret_cast<const f32x4*>(weight + i);
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int o = 4 * (threadIdx.x + 256 * j), i = c0 + o;
+        if (o < cw) {
+            *reinterpret_cast<f32x4*>(output + row * n + i) = v[j];
+            ss = __builtin_fmaf(v[j].x, v[j].x, ss);
+            ss = __builtin_fmaf(v[j].y, v[j].y, ss);
+            ss = __builtin_fmaf(v[j].z, v[j].z, ss);
+            ss = __builtin_fmaf(v[j].w, v[j].w, ss);
+        }
+    }
+    ss = group_sum_t<6>(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float sum = ((part[0] + part[1]) + part[2]) + part[3];
+    const float f = row_ss ? 1.0f : rms_factor(sum, n, eps);
+    if (row_ss && threadIdx.x == 0) row_ss[16 * blockIdx.x + row] = sum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int o = 4 * (threadIdx.x + 256 * j), i = c0 + o;
+        if (o < cw) {
+            const f32x4 x = v[j] * w[j];
+            *reinterpret_cast<f32x4*>(normed + row * n + i) = row_ss ? x : x * f;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float* gate, const float* up, float* out, long n) {
     const long stride = static_cast<long>(gridDim.x) * 256;
     for (long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
@@ -104,6 +169,19 @@ int launch_rmsnorm_residual(const float* input, const float* residual, const flo
     else
         hipLaunchKernelGGL(dev::rmsnorm_residual_kernel, dim3(rows), dim3(256), 0, stream, input, residual, weight,
                            output, normed, n, eps);
+    return 0;
+}
+
+int launch_split_norm(const float* h, const SplitSums& r, const float* weight, float* output, float* normed, int rows,
+                      int n, float eps, hipStream_t stream, float* row_ss) {
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    const int parts = row_ss ? kNormParts : 1;
+    if (rows < 1 || rows > 16 || n % (4 * parts) != 0 || n / parts > 4096 || !a16(h) || !a16(weight) || !a16(output) ||
+        !a16(normed))
+        return kDeclined;
+    if (r.S && (r.S > dev::kSplitMaxS || r.N % 4 != 0 || r.stride % 4 != 0 || !a16(r.part))) return kDeclined;
+    hipLaunchKernelGGL(dev::split_norm_kernel, dim3(parts, rows), dim3(256), 0, stream, h, r, weight, output, normed, n,
+                       eps, row_ss);
     return 0;
 }
 

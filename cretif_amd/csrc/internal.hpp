@@ -46,8 +46,9 @@ inline long row_bytes(int fmt, int K) { return static_cast<long>(K / block_elems
 //   kActSwiGLU2 : SwiGLU of gate/up outputs left as the two partial sums of an
 //                 RMSNorm matmul whose K was split over workgroups (SplitSums):
 //                 g = f_m (a[off] + a[off + split]), u likewise from b, with
-//                 f_m = 1/sqrt((w[m] + w[16 + m]) / kn + eps) (w: the two splits'
-//                 sums of squares), then silu(g) * u
+//                 f_m = 1/sqrt((w[m] + w[16 + m] + ... nss terms) / kn + eps) (w: the
+//                 splits' sums of squares; w null: f_m = 1, a plain gate/up), then silu(g) * u;
+//                 split = 0: one partial sum (g = f_m a[off])
 //   kActRMSNormS: kActRMSNorm with the residual left as kn (<= 4) partial sums of a K
 //                 split: r = b[off] + b[off + split] + ... in split order (the batch-1 GEMV)
 enum : int { kActPlain = 0, kActSwiGLU = 1, kActRMSNorm = 2, kActSwiGLU2 = 3, kActRMSNormS = 4 };
@@ -61,6 +62,7 @@ struct ActIn {
     float eps;
     long split = 0;  // kActSwiGLU2, kActRMSNormS: floats between consecutive partial sums
     int kn = 0;      // kActSwiGLU2: K of the RMSNorm; kActRMSNormS: number of partial sums
+    int nss = 2;     // kActSwiGLU2: sums of squares added for the row factor (w[16 s + m], s < nss <= 4)
 };
 
 // The q/k/v projection's outputs at one decode position, rotated and appended in the GEMV's
@@ -85,6 +87,7 @@ struct SplitSums {
     long stride = 0;
     int S = 0, N = 0, K = 0;
     float eps = 0.0f;
+    int nss = 0;  // sums of squares added for the row factor (0: S of them)
 };
 
 namespace detail {
@@ -130,7 +133,7 @@ int launch_skinny_act(int mode, int fmt, const ActIn& act, const void* B, float*
 long skinny_workspace_floats(int M, int N);
 // cri_matmul / cri_matmul_swiglu / cri_matmul_rmsnorm with that workspace (abi.cpp); return a cri_status
 int matmul_split_ws(int fmt, const float* A, const void* B, float* C, int M, int N, int K, float* ws, long ws_floats,
-                    hipStream_t s);
+                    hipStream_t s, SplitSums* defer = nullptr, int defer_S = 0);
 int matmul_rmsnorm_split_ws(int fmt, const float* hidden, const float* residual, const float* norm_weight,
                             float* hidden_out, const void* B, float* C, int M, int N, int K, float eps, float* ws,
                             long ws_floats, hipStream_t s, SplitSums* defer = nullptr, int defer_S = 0);
@@ -139,12 +142,15 @@ int matmul_rmsnorm_split_ws(int fmt, const float* hidden, const float* residual,
 int matmul_rmsnorm_splitres(int fmt, const float* hidden, const float* res_parts, int splits, long split,
                             const float* norm_weight, float* hidden_out, const void* B, float* C, int N, int K,
                             float eps, hipStream_t s);
-// the SwiGLU matmul of gate/up outputs left as two partial sums (kActSwiGLU2): gate at
-// gu.part, up at gu.part + up_off, the row factor from gu.ssq
+// the SwiGLU matmul of gate/up outputs left as two partial sums (kActSwiGLU2; gu.S = 1: one,
+// the whole product without its row factor): gate at gu.part, up at gu.part + up_off, the row
+// factor from gu.ssq (null: none)
 int matmul_swiglu2_split_ws(int fmt, const SplitSums& gu, long up_off, int ld, const void* B, float* C, int M, int N,
-                            int K, float* ws, long ws_floats, hipStream_t s);
+                            int K, float* ws, long ws_floats, hipStream_t s, SplitSums* defer = nullptr,
+                            int defer_S = 0);
 int matmul_swiglu_split_ws(int fmt, const float* gate, const float* up, int ld, const void* B, float* C, int M, int N,
-                           int K, float* ws, long ws_floats, hipStream_t s);
+                           int K, float* ws, long ws_floats, hipStream_t s, SplitSums* defer = nullptr,
+                           int defer_S = 0);
 
 // multi-token fused dequant GEMM on the matrix cores, fp16 operands (mfma_gemm.hip)
 bool mfma_gemm_supported(int fmt, int M, int N, int K, const void* A, const void* B);
@@ -164,6 +170,14 @@ int launch_generic_matmul_act(int mode, int fmt, const ActIn& act, const void* B
 int launch_rmsnorm_residual(const float* input, const float* residual, const float* weight, float* output,
                             float* normed, int rows, int n, float eps, hipStream_t stream);
 int launch_silu_mul(const float* gate, const float* up, float* out, long n, hipStream_t stream);
+// rmsnorm_residual with the residual as the partial sums of a split decode-batch matmul
+// (r.S = 0: none); rows of up to 4096 floats, 16-byte aligned (else kDeclined).  row_ss (not
+// null): normed = (h + r) * weight without the row factor, and each row is cut into
+// kNormParts column ranges whose sums of squares go to row_ss[16 part + row] (the layout of
+// SplitSums.ssq; the consumer adds kNormParts of them), n % (4 kNormParts) == 0
+constexpr int kNormParts = 4;
+int launch_split_norm(const float* h, const SplitSums& r, const float* weight, float* output, float* normed, int rows,
+                      int n, float eps, hipStream_t stream, float* row_ss = nullptr);
 // token rows of a (quantized) embedding table, dequantized (elementwise.hip)
 int launch_stream_read(const void* src, long n_bytes, uint32_t* sink, hipStream_t stream);
 // the device's 100 MHz wall clock written to *dst (probe.hip)

@@ -762,7 +762,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(const uint8_t* __restri
                                                              int ks_log2, int ngroups, int nchunks, int nblocks,
                                                              int cs_log2, float* __restrict__ part, const ActIn Pin) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const ActIn P{A, Pin.b, Pin.w, Pin.h_out, Pin.lda, Pin.eps, Pin.split, Pin.kn};
+    ActIn P = Pin;  // the activation pointer from its own (preloaded) argument
+    P.a = A;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, nl = lane & 15;
     const int KS = 1 << ks_log2;              // k-splits per tile (power of two)

@@ -13,17 +13,18 @@ namespace dev {
 
 constexpr int kSplitMaxS = 16;
 
-// 1/sqrt(sum_s ssq[s*16 + m] / K + eps) in split order, or 1 without RMSNorm;
+// 1/sqrt(sum_s ssq[s*16 + m] / K + eps) over the nss (else S) sums in order, or 1 without RMSNorm;
 // every load unconditional (splits past S read split S - 1, unused)
 __device__ __forceinline__ float split_factor(const SplitSums& p, int m) {
     if (!p.ssq) return 1.0f;
+    const int ns = p.nss ? p.nss : p.S;
     float sq[kSplitMaxS];
 #pragma unroll
-    for (int s = 0; s < kSplitMaxS; ++s) sq[s] = p.ssq[min(s, p.S - 1) * 16 + m];
+    for (int s = 0; s < kSplitMaxS; ++s) sq[s] = p.ssq[min(s, ns - 1) * 16 + m];
     float ss = sq[0];
 #pragma unroll
     for (int s = 1; s < kSplitMaxS; ++s)
-        if (s < p.S) ss += sq[s];
+        if (s < ns) ss += sq[s];
     return 1.0f / sqrtf(ss / static_cast<float>(p.K) + p.eps);
 }
 
