@@ -118,33 +118,56 @@ __device__ __forceinline__ void argmax_block(float& best, int& bi) {
     for (int w = 1; w < kArgmaxThreads / 64; ++w) argmax_merge(best, bi, sv[w], si[w]);
 }
 
+// vec (rows 16-byte aligned): the slice is read as 16-byte loads, eight per thread issued
+// before any is compared (a loop of dependent scalar loads took ~14 us for one 128256-logit
+// row); slices start on multiples of four.
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const float* __restrict__ logits, long ld, int n,
                                                                      int* __restrict__ out, f32x2* __restrict__ part,
                                                                      unsigned* __restrict__ counters,
-                                                                     int* __restrict__ pos, int pos_add) {
+                                                                     int* __restrict__ pos, int pos_add, int vec) {
     const int row = blockIdx.y, nb = gridDim.x, b = blockIdx.x;
     const float* r = logits + row * ld;
-    const int per = (n + nb - 1) / nb;
-    const int j0 = b * per, j1 = min(n, j0 + per);
+    const int per = ((n + nb - 1) / nb + 3) & ~3;
+    const int j0 = min(n, b * per), j1 = min(n, j0 + per);
     float best = -3.402823466e38f;
     int bi = 0;
-    for (int j = j0 + threadIdx.x; j < j1; j += kArgmaxThreads) {
-        const float x = r[j];
-        if (x > best) {
-            best = x;
-            bi = j;
+    int js = j0;  // first element of the scalar tail
+    if (vec) {
+        constexpr int kBatch = 8;
+        const int nv = (j1 - j0) >> 2;  // whole 16-byte groups of the slice
+        for (int q0 = 0; q0 < nv; q0 += kBatch * kArgmaxThreads) {
+            f32x4 x[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {  // clamped, so every load is in bounds and unconditional
+                const int q = min(q0 + u * kArgmaxThreads + static_cast<int>(threadIdx.x), nv - 1);
+                x[u] = *reinterpret_cast<const f32x4*>(r + j0 + 4 * q);
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int q = q0 + u * kArgmaxThreads + static_cast<int>(threadIdx.x);
+                if (q < nv) {
+                    const int j = j0 + 4 * q;
+                    argmax_merge(best, bi, x[u].x, j);
+                    argmax_merge(best, bi, x[u].y, j + 1);
+                    argmax_merge(best, bi, x[u].z, j + 2);
+                    argmax_merge(best, bi, x[u].w, j + 3);
+                }
+            }
         }
+        js = j0 + 4 * nv;
     }
+    for (int j = js + threadIdx.x; j < j1; j += kArgmaxThreads) argmax_merge(best, bi, r[j], j);
     argmax_block(best, bi);
     __shared__ int last;
     if (threadIdx.x == 0) {
         part[static_cast<long>(row) * nb + b] = f32x2{best, __int_as_float(bi)};
-        __threadfence();  // release: the slice result before the count
+        // release: the slice result before the count (a release alone: no L2 invalidate here)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         last = atomicAdd(&counters[row], 1u) == static_cast<unsigned>(nb - 1);
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();  // acquire: every slice's result
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // acquire: every slice's result
     best = -3.402823466e38f;
     bi = 0;
     for (int s = threadIdx.x; s < nb; s += kArgmaxThreads) {
@@ -188,9 +211,10 @@ int argmax_slices(int n) { return static_cast<int>(std::min<long>(64, std::max<l
 int launch_argmax_rows(const float* logits, long ld, int rows, int n, int* out, float* part, unsigned* counters,
                        int* pos, int pos_add, hipStream_t stream) {
     if (rows < 1 || rows > 65535 || n < 1) return kDeclined;
+    const int vec = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 && ld % 4 == 0;
     hipLaunchKernelGGL(dev::argmax_rows_kernel, dim3(static_cast<unsigned>(argmax_slices(n)), static_cast<unsigned>(rows)),
                        dim3(dev::kArgmaxThreads), 0, stream, logits, ld, n, out, reinterpret_cast<dev::f32x2*>(part),
-                       counters, pos, pos_add);
+                       counters, pos, pos_add, vec);
     return 0;
 }
 
