@@ -523,6 +523,10 @@ __global__ __launch_bounds__(64) void decode_attn_mrow_kernel(const float* __res
     load_tile(T0, t0);
     if (t1 - t0 <= kSplitTile) {
         if (t0 < t1) run_tile(T0, t0);
+    } else if (t1 - t0 <= 2 * kSplitTile) {  // two tiles: both requested before the first is computed
+        load_tile(T1, t0 + kSplitTile);
+        run_tile(T0, t0);
+        run_tile(T1, t0 + kSplitTile);
     } else {
         for (int tb = t0; tb < t1; tb += 2 * kSplitTile) {
             load_tile(T1, tb + kSplitTile);  // past t1: clamped reads, not computed
