@@ -284,6 +284,25 @@ def test_step_fused_projections_split(orc, fmt, M):
         assert normwise_rel_err(gv[pos:pos + M], vc[i][pos:pos + M]) <= TOL
 
 
+@pytest.mark.parametrize("M,pos,max_seq", [(16, 3000, 4096), (8, 5000, 8192), (5, 8180, 8192)])
+def test_step_long_context(orc, M, pos, max_seq):
+    # past 64 x 32 positions the multi-row attention's chunks hold two (4096) or three or more
+    # (8192) 32-position tiles each
+    m = make_model(1, dim=256, n_heads=8, n_kv_heads=2, head_dim=64, ffn=512, vocab=500, seed=23,
+                   big_tables=False)
+    dec = make_decoder(m, max_seq=max_seq)
+    kc, vc = random_cache(m, max_seq, 31)
+    load_cache(dec, kc, vc)
+    ids = np.random.default_rng(pos).integers(0, m["vocab"], M).astype(np.int32)
+    logits = torch.empty(M, m["vocab"], device="cuda")
+    dec.set_position(pos)
+    dec.forward(torch.from_numpy(ids).cuda(), M, logits)
+    ref, _ = orc.decode_step(m, list(ids), pos, kc, vc)
+    err = normwise_rel_err(logits.cpu().numpy(), ref)
+    print("long-context step M=%d pos=%d: normwise err %.2e" % (M, pos, err))
+    assert err <= TOL
+
+
 def test_decoder_errors():
     m = make_model(1, dim=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=100, big_tables=False)
     with pytest.raises(cri.CretifError):  # n_heads not a multiple of n_kv_heads
