@@ -5,9 +5,11 @@ Headline (the `value` of the JSON line): weight GB/s of the batch-1 Q4_K
 decode GEMV at the Llama-3.2-1B FFN gate/up shape (N=8192, K=2048).  One
 "step" is one GEMV launch over one batch of synthetic input.  The weights are
 rotated over enough distinct copies (>= 2x the 256 MB Infinity Cache) that each
-launch streams its matrix from HBM; the launches are captured once in a HIP
-graph and replayed, and the timed region is bracketed by HIP events on the
-replay stream plus device synchronisation.
+launch streams its matrix from HBM; the launches are captured in one HIP graph
+with a device timestamp kernel between samples (so no graph boundary falls
+inside a sample), and the timed replay is bracketed by HIP events on the replay
+stream plus device synchronisation.  Every line in `details` is timed the same
+way.
 
 GB/s counts algorithmic bytes only: N*(K/bs)*block_bytes + 4*M*K + 4*M*N.
 
@@ -121,7 +123,61 @@ def time_graphs(graphs, samples, warmup_steps, steps, stream):
     return [ev[i].elapsed_time(ev[i + 1]) for i in range(samples)]
 
 
-class GemvRig:
+def chain_samples(call, steps, samples, stream):
+    """ms per call of each of `samples` consecutive samples of exactly `steps` calls, all in one
+    captured graph with a device timestamp kernel (cri_timestamp, 100 MHz clock) between the
+    samples, so no graph boundary falls inside the timed region (each boundary costs ~13 us on
+    this box, which a sample of a few large launches would otherwise carry).  call(n) enqueues
+    call n of the weight rotation, which continues through the samples.  The graph runs once
+    untimed, once timed.  Also returns the hipEvent time of the whole timed replay (ms), which
+    brackets the samples."""
+    import torch
+
+    import cretif_amd as cri
+
+    ts = torch.zeros(samples + 1, dtype=torch.int64, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    n = 0
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(samples):
+            cri.timestamp(ts.data_ptr() + 8 * i)
+            for _ in range(steps):
+                call(n)
+                n += 1
+        cri.timestamp(ts.data_ptr() + 8 * samples)
+    torch.cuda.synchronize()
+    g.replay()  # warm-up pass
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    t = ts.cpu().numpy().astype(np.int64)
+    per = [(t[i + 1] - t[i]) * 1e-5 / steps for i in range(samples)]  # 100 MHz ticks -> ms per call
+    del g
+    return per, e0.elapsed_time(e1)
+
+
+class ChainTimed:
+    """time(): warm-up replays of the rig's graphs, then the median of chain_samples.  A rig
+    defines call(n), steps, stream and graphs."""
+
+    def samples(self, samples, warmup):
+        """ms per call of each sample (one replay = `steps` calls, events between replays)."""
+        return [t / self.steps for t in time_graphs(self.graphs, samples, warmup, self.steps, self.stream)]
+
+    def chain_samples(self, samples):
+        return chain_samples(self.call, self.steps, samples, self.stream)
+
+    def time(self, samples=9, warmup=64):
+        """Median ms per call over `samples` samples of `steps` calls each."""
+        self.samples(1, warmup)  # untimed warm-up
+        return float(np.median(self.chain_samples(samples)[0]))
+
+
+class GemvRig(ChainTimed):
     """Weights replicated over enough device copies that each launch streams from HBM;
     `steps` launches per captured graph (see rotation_plan)."""
 
@@ -169,55 +225,18 @@ class GemvRig:
     def bytes_per_launch(self):
         return algo_bytes(self.fmt, self.M, self.N, self.K)
 
-    def chain_samples(self, samples):
-        """ms per launch of `samples` consecutive samples of exactly `steps` launches, all in
-        one captured graph with a device timestamp kernel (cri_timestamp, 100 MHz clock)
-        between the samples, so no graph boundary falls inside the timed region (each
-        boundary costs ~13 us on this box).  The graph runs once untimed, once timed; the
-        rotation over the weight copies continues through it.  Also returns the hipEvent
-        time of the whole timed replay (ms), which brackets the samples."""
-        import torch
-
-        K, cri = self.steps, self.cri
-        ts = torch.zeros(samples + 1, dtype=torch.int64, device="cuda")
-        g = torch.cuda.CUDAGraph()
-        n = 0
-        with torch.cuda.graph(g, stream=self.stream):
-            for i in range(samples):
-                cri.timestamp(ts.data_ptr() + 8 * i)
-                for _ in range(K):
-                    self._run(self.W[n % self.copies])
-                    n += 1
-            cri.timestamp(ts.data_ptr() + 8 * samples)
-        torch.cuda.synchronize()
-        g.replay()  # warm-up pass
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(self.stream):
-            e0.record(self.stream)
-            g.replay()
-            e1.record(self.stream)
-        torch.cuda.synchronize()
-        t = ts.cpu().numpy().astype(np.int64)
-        per = [(t[i + 1] - t[i]) * 1e-5 / K for i in range(samples)]  # 100 MHz ticks -> ms per launch
-        return per, e0.elapsed_time(e1)
-
-    def samples(self, samples, warmup):
-        """ms per launch of each sample (one replay = `steps` launches)."""
-        return [t / self.steps for t in time_graphs(self.graphs, samples, warmup, self.steps, self.stream)]
-
-    def time(self, samples=9, warmup=64):
-        """Median ms per launch over `samples` samples."""
-        return float(np.median(self.samples(samples, warmup)))
+    def call(self, n):
+        self._run(self.W[n % self.copies])
 
     def free(self):
         self.W = None
         self.graphs = None
 
 
-class StreamRig:
-    """The achievable streaming-read line: cri_stream_read over `copies` buffers of n_bytes (rotated
-    over >= 2x the Infinity Cache, as the GEMVs), one rotation per captured graph."""
+class StreamRig(ChainTimed):
+    """The achievable streaming-read line: cri_stream_read_ex over `copies` buffers of n_bytes
+    (rotated over >= 2x the Infinity Cache, as the GEMVs) in the shape the read sweep found
+    fastest at the headline's size: one 16-byte load per thread, one pass of the buffer."""
 
     def __init__(self, n_bytes, min_bytes=2 * MALL_BYTES, max_copies=64):
         import torch
@@ -230,19 +249,20 @@ class StreamRig:
         self.W = [base] + [base.clone() for _ in range(self.copies - 1)]
         self.sink = torch.zeros(1, dtype=torch.int32, device="cuda")
         self.stream = torch.cuda.Stream()
+        self.cri = cri
         with torch.cuda.stream(self.stream):
-            for Wi in self.W:
-                cri.stream_read(Wi, n_bytes, self.sink)
+            for n in range(self.copies):
+                self.call(n)
         self.stream.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=self.stream):
-            for Wi in self.W:
-                cri.stream_read(Wi, n_bytes, self.sink)
+            for n in range(self.copies):
+                self.call(n)
         self.graphs = [g]
         torch.cuda.synchronize()
 
-    samples = GemvRig.samples
-    time = GemvRig.time
+    def call(self, n):
+        self.cri.stream_read_ex(self.W[n % self.copies], self.n_bytes, self.sink, 1, 0)
 
     def free(self):
         self.W = None
@@ -352,7 +372,7 @@ class DecodeStepRig:
         self.dec = None
 
 
-class AttentionRig:
+class AttentionRig(ChainTimed):
     """Fused decode attention of one token (32 query heads over 8 KV heads,
     head_dim 64) over an fp32 cache of T positions in the [T, 8, 64] layout, for
     `copies` distinct caches (>= 2 x the MALL) captured in one graph and replayed.
@@ -377,12 +397,18 @@ class AttentionRig:
         self.out = torch.empty(H * HD, device="cuda")
         self.ws = torch.empty(max(4, cri.decode_attention_workspace_size(H, HKV, HD, T) // 4), device="cuda")
 
+        def call(n):
+            k, v = self.K[n % self.copies], self.V[n % self.copies]
+            if form == "plain":
+                cri.fused_decode_attention(self.q, k, v, self.out, H, HKV, HD, T, 0.125)
+            else:
+                cri.fused_decode_attention_ws(self.q, k, v, self.out, H, HKV, HD, T, 0.125, self.ws)
+
         def run():
-            for k, v in zip(self.K, self.V):
-                if form == "plain":
-                    cri.fused_decode_attention(self.q, k, v, self.out, H, HKV, HD, T, 0.125)
-                else:
-                    cri.fused_decode_attention_ws(self.q, k, v, self.out, H, HKV, HD, T, 0.125, self.ws)
+            for n in range(self.copies):
+                call(n)
+
+        self.call = call
 
         self.stream = torch.cuda.Stream()
         with torch.cuda.stream(self.stream):
@@ -398,14 +424,11 @@ class AttentionRig:
         # algorithmic: q, out and every K and V value of the T positions, once
         return 4 * (2 * self.H * self.HD + 2 * self.T * self.HKV * self.HD)
 
-    samples = GemvRig.samples
-    time = GemvRig.time
-
     def free(self):
         self.K = self.V = self.graphs = None
 
 
-class GqaRig:
+class GqaRig(ChainTimed):
     """batched_matmul_gqa (32 query heads over 8 KV heads, head_dim 64, T keys):
     'qk' is Q K^T (A [32, M, 64], B [8, 64, T]), 'pv' is P V (A [32, M, T],
     B [8, T, 64]).  Both operands rotate over `copies` distinct buffers (>= 2 x
@@ -431,9 +454,14 @@ class GqaRig:
         self.B = [torch.randn(HKV, K, N, device="cuda", generator=g) for _ in range(self.copies)]
         self.C = torch.empty(H, M, N, device="cuda")
 
+        def call(n):
+            cri.batched_matmul_gqa(self.A[n % self.copies], self.B[n % self.copies], self.C, H, HKV, M, N, K)
+
         def run():
-            for a_, b_ in zip(self.A, self.B):
-                cri.batched_matmul_gqa(a_, b_, self.C, H, HKV, M, N, K)
+            for n in range(self.copies):
+                call(n)
+
+        self.call = call
 
         self.stream = torch.cuda.Stream()
         with torch.cuda.stream(self.stream):
@@ -451,9 +479,6 @@ class GqaRig:
     def flops_per_call(self):
         return 2.0 * self.H * self.M * self.K * self.N
 
-    samples = GemvRig.samples
-    time = GemvRig.time
-
     def free(self):
         self.A = self.B = self.graphs = None
 
@@ -461,7 +486,7 @@ class GqaRig:
 def read_probe_us(nb, per, grid, samples=7):
     """us per launch of cri_stream_read_ex over nb bytes (per 16-byte loads per thread, issued
     before any is used; grid 0 = one-shot, one pass of the buffer, else that many workgroups
-    striding over it), the buffers rotated over >= 2x the Infinity Cache in one graph."""
+    striding over it), the buffers rotated over >= 2x the Infinity Cache (chain_samples)."""
     import torch
 
     import cretif_amd as cri
@@ -475,14 +500,10 @@ def read_probe_us(nb, per, grid, samples=7):
         for w in W:
             cri.stream_read_ex(w, nb, sink, per, grid)
     s.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=s):
-        for w in W:
-            cri.stream_read_ex(w, nb, sink, per, grid)
-    t = time_graphs([g], samples, copies, copies, s)
-    del g, W
+    t, _ = chain_samples(lambda n: cri.stream_read_ex(W[n % copies], nb, sink, per, grid), copies, samples, s)
+    del W
     torch.cuda.empty_cache()
-    return float(np.median(t)) / copies * 1e3
+    return float(np.median(t)) * 1e3
 
 
 def read_sweep():
