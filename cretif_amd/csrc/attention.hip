@@ -556,37 +556,61 @@ __global__ __launch_bounds__(64) void decode_attn_mrow_kernel(const float* __res
 }
 
 // out[m][h][d] = sum_c 2^(m_c - M) acc_c[d] / sum_c 2^(m_c - M) l_c, M = max_c m_c,
-// for query row m = blockIdx.y (output rows ldo floats apart).  One wave per
-// (row, head): lanes take the chunks for the max and the sum (their loads are
-// independent), the factors go through LDS, and the accumulator loop over the
-// chunks is unrolled so its loads are in flight together.  Empty chunks (max
-// -inf) get the factor 0; chunk 0 always holds a position.
+// for query row m = blockIdx.y (output rows ldo floats apart).  One workgroup of
+// kCombineWaves waves per (row, head): its threads take the chunks for the max and
+// the sum (their loads are independent), the factors go through LDS; wave w adds up
+// the accumulators of chunks w, w + kCombineWaves, ... (eight loads in flight), and
+// the waves' partial numerators are added in wave order.  Empty chunks (max -inf)
+// get the factor 0; chunk 0 always holds a position.
 constexpr int kCombineMaxChunks = 4096;
+constexpr int kCombineWaves = 4;
 
-__global__ __launch_bounds__(64) void decode_attn_combine_kernel(const float* __restrict__ ws, float* __restrict__ out,
-                                                                 int D, int nchunks, long ldo) {
+__global__ __launch_bounds__(64 * kCombineWaves) void decode_attn_combine_kernel(const float* __restrict__ ws,
+                                                                                 float* __restrict__ out, int D,
+                                                                                 int nchunks, long ldo) {
+    constexpr int kT = 64 * kCombineWaves;
     __shared__ float fs[kCombineMaxChunks];
-    const int h = blockIdx.x, mrow = blockIdx.y, lane = threadIdx.x;
+    __shared__ float red[kCombineWaves];
+    __shared__ float part[kCombineWaves][detail::kDecodeAttnSplitMaxHeadDim];
+    const int h = blockIdx.x, mrow = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int stride = D + 4;
     const float* P = ws + (static_cast<long>(mrow) * gridDim.x + h) * nchunks * stride;
     float mloc = -INFINITY;
-    for (int c = lane; c < nchunks; c += 64) mloc = fmaxf(mloc, P[static_cast<long>(c) * stride]);
-    const float M = wave_max(mloc);
+    for (int c = tid; c < nchunks; c += kT) mloc = fmaxf(mloc, P[static_cast<long>(c) * stride]);
+    mloc = wave_max(mloc);
+    if (lane == 0) red[wave] = mloc;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < kCombineWaves; ++w) M = fmaxf(M, red[w]);
+    __syncthreads();  // red is reused below
     float lloc = 0.0f;
-    for (int c = lane; c < nchunks; c += 64) {
+    for (int c = tid; c < nchunks; c += kT) {
         const float f = exp2f(P[static_cast<long>(c) * stride] - M);
         fs[c] = f;
         lloc = __builtin_fmaf(f, P[static_cast<long>(c) * stride + 1], lloc);
     }
-    const float den = group_sum_t<6>(lloc);
+    lloc = group_sum_t<6>(lloc);
+    if (lane == 0) red[wave] = lloc;
     __syncthreads();
-    float* o = out + mrow * ldo + static_cast<long>(h) * D;
+    float den = red[0];
+#pragma unroll
+    for (int w = 1; w < kCombineWaves; ++w) den += red[w];
     for (int d0 = 0; d0 < D; d0 += 64) {
         const int d = min(d0 + lane, D - 1);
         float num = 0.0f;
 #pragma unroll 8
-        for (int c = 0; c < nchunks; ++c) num = __builtin_fmaf(fs[c], P[static_cast<long>(c) * stride + 4 + d], num);
-        if (d0 + lane < D) o[d0 + lane] = num / den;
+        for (int c = wave; c < nchunks; c += kCombineWaves)
+            num = __builtin_fmaf(fs[c], P[static_cast<long>(c) * stride + 4 + d], num);
+        if (d0 + lane < D) part[wave][d0 + lane] = num;
+    }
+    __syncthreads();
+    float* o = out + mrow * ldo + static_cast<long>(h) * D;
+    for (int d = tid; d < D; d += kT) {
+        float num = part[0][d];
+#pragma unroll
+        for (int w = 1; w < kCombineWaves; ++w) num += part[w][d];
+        o[d] = num / den;
     }
 }
 
@@ -659,8 +683,8 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
         if (waves > 0x7FFFFFFFL) return kDeclined;
         hipLaunchKernelGGL(dev::decode_attn_mrow_kernel, dim3(static_cast<unsigned>(waves)), dim3(64), 0, stream, Q, K,
                            V, ws, G, n_kv_heads, rows, kv_dev, kv0, qscale, nchunks, ldq);
-        hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads, static_cast<unsigned>(rows)), dim3(64), 0,
-                           stream, ws, out, D, nchunks, ldo);
+        hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads, static_cast<unsigned>(rows)),
+                           dim3(64 * dev::kCombineWaves), 0, stream, ws, out, D, nchunks, ldo);
         return 0;
     }
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(rows));
@@ -670,8 +694,8 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
     else
         hipLaunchKernelGGL((dev::decode_attn_split_kernel<kSplitHeadsPerWave, 8>), grid, dim3(256 / kSplitHeadsPerWave),
                            0, stream, Q, K, V, ws, G, n_kv_heads * D, D, kv_dev, kv0, qscale, nchunks, nhq, ldq);
-    hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads, static_cast<unsigned>(rows)), dim3(64), 0, stream,
-                       ws, out, D, nchunks, ldo);
+    hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads, static_cast<unsigned>(rows)),
+                       dim3(64 * dev::kCombineWaves), 0, stream, ws, out, D, nchunks, ldo);
     return 0;
 }
 
