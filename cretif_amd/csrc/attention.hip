@@ -295,8 +295,8 @@ __global__ __launch_bounds__(256 / HQ) void decode_attn_split_kernel(const float
         for (int i = 0; i < NQ; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int base = t0; base < t1; base += kSplitTile) {
-        f32x4 kv[2][NQ], vv[2][NQ];
+    // a tile: positions base + 16 g + q4 (clamped to T - 1) for g = 0, 1
+    auto load_tile = [&](f32x4 (&kv)[2][NQ], f32x4 (&vv)[2][NQ], int base) {
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
             const long row = static_cast<long>(min(base + 16 * g + q4, T - 1)) * kvd;
@@ -307,7 +307,8 @@ __global__ __launch_bounds__(256 / HQ) void decode_attn_split_kernel(const float
                 vv[g][i] = ld_f32x4(Vh + row + d);
             }
         }
-        __builtin_amdgcn_sched_barrier(0);  // the tile's loads stay in flight together
+    };
+    auto run_tile = [&](const f32x4 (&kv)[2][NQ], const f32x4 (&vv)[2][NQ], int base) {
 #pragma unroll
         for (int j = 0; j < HQ; ++j) {
             float s_own = -INFINITY;  // lanes r = 2, 3 own no position of a 32-position tile
@@ -348,6 +349,21 @@ __global__ __launch_bounds__(256 / HQ) void decode_attn_split_kernel(const float
                 a.w = __builtin_fmaf(p1, vv[1][i].w, a.w);
                 acc[j][i] = a;
             }
+        }
+    };
+    f32x4 k0[2][NQ], v0[2][NQ];
+    if (t1 - t0 == 2 * kSplitTile) {  // two tiles: both requested before the first is computed
+        f32x4 k1[2][NQ], v1[2][NQ];
+        load_tile(k0, v0, t0);
+        load_tile(k1, v1, t0 + kSplitTile);
+        __builtin_amdgcn_sched_barrier(0);
+        run_tile(k0, v0, t0);
+        run_tile(k1, v1, t0 + kSplitTile);
+    } else {
+        for (int base = t0; base < t1; base += kSplitTile) {
+            load_tile(k0, v0, base);
+            __builtin_amdgcn_sched_barrier(0);  // the tile's loads stay in flight together
+            run_tile(k0, v0, base);
         }
     }
 
