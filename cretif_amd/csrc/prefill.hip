@@ -294,11 +294,12 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     // wave's LDS area after group q's last read of it (third iteration), its
     // first step decoded in the fourth, which also stages the activations
     // into the other LDS buffer.  So every load is waited for in the code
-    // block that issued it, two to three iterations later.  Loads past the
-    // split's last step repeat it (in bounds); the padding steps that make
-    // the trip count a multiple of four stage zero activations, so their
-    // MFMAs add nothing.
-    const int nst4 = (nst + 3) & ~3, ngrp = nst4 >> 2;
+    // block that issued it, two to three iterations later.  A split is whole
+    // groups (K % 256 == 0 and splits start on a group), so nst is a
+    // multiple of four; the loads issued after the last group repeat the
+    // split's last step (in bounds) and what they stage is never read (their
+    // values are that step's again, so the range guard's maxima stay the same).
+    const int ngrp = nst >> 2;
     auto step_of = [&](int t) { return s_begin + min(t, nst - 1); };
     f32x4 av[4][2];  // activations of the next group: [step][row]
     u32x4 wr[kLoads];  // weight bytes of the next group
@@ -320,14 +321,13 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
             if (64 * i + lane < kChunks) *reinterpret_cast<u32x4*>(warea + 16 * (64 * i + lane)) = wr[i];
     };
     // step j, row i of the next group into buffer buf (tile j)
-    auto stage = [&](char* buf, int q, int j, int i) {
-        const float vf = 4 * q + j < nst ? 1.0f : 0.0f;
+    auto stage = [&](char* buf, int j, int i) {
         const f32x4 v = av[j][i];
         const float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        amax[i] = fmaxf(amax[i], mx * vf);  // a padding step's inf * 0 is NaN, which fmaxf ignores
+        amax[i] = fmaxf(amax[i], mx);
         const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(pf2{v.x, v.y}, ph2));
         const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(pf2{v.z, v.w}, ph2));
-        *reinterpret_cast<pu2*>(buf + j * kPStage + aw[i]) = pu2{vf != 0.0f ? lo : 0u, vf != 0.0f ? hi : 0u};
+        *reinterpret_cast<pu2*>(buf + j * kPStage + aw[i]) = pu2{lo, hi};
     };
     auto afrag = [&](const char* tile, int u, int s) { return *reinterpret_cast<const ph8*>(tile + aoff[u][s]); };
     auto mma2 = [&](const ph8 (&a)[2], const uint32_t (&bf)[4][4], int s) {
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     // compiler keeps this order.
     auto iter = [&](auto pos, const ph8 (&ac)[2][4], ph8 (&an)[2][4], const char* next_tile,
                     const uint32_t (&bc)[4][4], uint32_t (&bn)[4][4], const typename W::Frag& fc,
-                    typename W::Frag& fn, char* nxt, int qn) {
+                    typename W::Frag& fn, char* nxt) {
         constexpr int J = decltype(pos)::value;
         constexpr bool kLast = J == 0;  // the group's last iteration decodes the next group's first step
         typename W::Consts k;
@@ -369,8 +369,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
             if (s == 2) W::template sub<2>(fc, k, bn[2]);
             if (s == 3) W::template sub<3>(fc, k, bn[3]);
             if constexpr (kLast) {
-                stage(nxt, qn, s, 0);
-                stage(nxt, qn, s, 1);
+                stage(nxt, s, 0);
+                stage(nxt, s, 1);
             } else {
                 an[0][s] = afrag(next_tile, 0, s);
                 an[1][s] = afrag(next_tile, 1, s);
@@ -387,10 +387,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4) fa[u][s4] = afrag(rd, u, s4);
         load_next(q + 1);
-        iter(pos_t<1>{}, fa, fb, rd + kPStage, x, y, f1, f0, wr_buf, q + 1);
-        iter(pos_t<2>{}, fb, fa, rd + 2 * kPStage, y, x, f0, f1, wr_buf, q + 1);
-        iter(pos_t<3>{}, fa, fb, rd + 3 * kPStage, x, y, f1, f0, wr_buf, q + 1);
-        iter(pos_t<0>{}, fb, fa, rd, y, x, f0, f1, wr_buf, q + 1);
+        iter(pos_t<1>{}, fa, fb, rd + kPStage, x, y, f1, f0, wr_buf);
+        iter(pos_t<2>{}, fb, fa, rd + 2 * kPStage, y, x, f0, f1, wr_buf);
+        iter(pos_t<3>{}, fa, fb, rd + 3 * kPStage, x, y, f1, f0, wr_buf);
+        iter(pos_t<0>{}, fb, fa, rd, y, x, f0, f1, wr_buf);
         __syncthreads();
     };
 
@@ -399,8 +399,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     write_w();
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        stage(lds, 0, j, 0);
-        stage(lds, 0, j, 1);
+        stage(lds, j, 0);
+        stage(lds, j, 1);
     }
     W::template read<0>(f0, wrow, h);
     {
