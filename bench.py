@@ -65,6 +65,14 @@ GEMV_WORKLOADS = {
     "fp16_gemv": ("fp16", 8192, 2048),
     "q4_k_gemv_down": ("q4_k", 2048, 8192),
     "q8_0_gemv_down": ("q8_0", 2048, 8192),
+    # the other BASELINE GEMV shapes: config 1 (SmolLM2-135M FFN up), config 2 (FFN down),
+    # config 3 (q/o and k/v projections)
+    "q8_0_gemv_1536x576": ("q8_0", 1536, 576),
+    "q4_0_gemv_down": ("q4_0", 2048, 8192),
+    "q5_0_gemv_down": ("q5_0", 2048, 8192),
+    "q4_k_gemv_2048x2048": ("q4_k", 2048, 2048),
+    "q4_k_gemv_512x2048": ("q4_k", 512, 2048),
+    "q6_k_gemv_512x2048": ("q6_k", 512, 2048),
     "q6_k_lm_head": ("q6_k", 128256, 2048),
     # the reference's tied LM head: the token table dequantized to fp32 and multiplied by
     # matmul_transposed_b (ref:src/model.cu:1027-1029); against q6_k_lm_head / q8_0_lm_head it
@@ -678,7 +686,7 @@ def main():
             f, m_, n, k = SKINNY_WORKLOADS[args.gemv]
         else:
             (f, n, k), m_ = GEMV_WORKLOADS[args.gemv], 1
-        r = GemvRig(f, n, k, M=m_)
+        r = GemvRig(f, n, k, M=m_, max_copies=1024)
         m = r.time(samples, 64)
         print(json.dumps({"workload": args.gemv, "M": m_, "N": n, "K": k, "launches_per_sample": r.steps,
                           "us": round(m * 1e3, 3), "GB/s": round(r.bytes_per_launch() / (m * 1e-3) / 1e9, 1)}))
@@ -711,7 +719,7 @@ def main():
         for name, (f, n, k) in GEMV_WORKLOADS.items():
             if name == args.workload:
                 continue
-            r = GemvRig(f, n, k)
+            r = GemvRig(f, n, k, max_copies=1024)  # small matrices too rotate over >= 2x the MALL
             details[name] = gemv_line(r, r.time(9, 64))
             r.free()
             torch.cuda.empty_cache()
