@@ -256,6 +256,10 @@ static int launch_gemv_f(const ActIn& x, const void* W, float* y, int N, int K, 
     const int upl = (units + lpr - 1) / lpr;
     switch (upl) {
         case 1:
+            // one row group per wave (a short matrix): nothing to prefetch behind it
+            if constexpr (F::kPref1 > 1)
+                if (static_cast<long>(N) <= kGemvTargetWaves * (64 >> lpr_log2))
+                    return launch_gemv_t<F, 1, 1, MODE, MR>(x, W, y, N, K, units, row_bytes, lpr_log2, stream, mrows);
             return launch_gemv_t<F, 1, F::kPref1, MODE, MR>(x, W, y, N, K, units, row_bytes, lpr_log2, stream, mrows);
         case 2:
             if constexpr (MR > 1) return -1;  // two activation rows: one unit per lane (K <= 4096)
