@@ -426,7 +426,7 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
                                                            M, cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim, pos, 1,
                                                            nchunks, scale, attn_ws_.data_as<float>(), s),
                  "attention");
-    // (9..16 tokens: its partial sums are left for the FFN's RMSNorm row kernel)
+    // (2..16 tokens: its partial sums are left for the FFN's RMSNorm row kernel)
     cri::SplitSums o_sums;
     check_cri(cri::detail::matmul_split_ws(cri_id(L.o_fmt), ctx_.data_as<float>(), L.o.data(),
                                            attn_out_.data_as<float>(), M, D, QD, split_ws_.data_as<float>(),
@@ -440,7 +440,7 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
 }
 
 bool DecodeStep::split_flow(int M) const {
-    return M > 8 && M <= kFusedMaxBatch && cfg_.dim % (4 * cri::detail::kNormParts) == 0 && cfg_.dim <= 4096;
+    return M > 1 && M <= kFusedMaxBatch && cfg_.dim % (4 * cri::detail::kNormParts) == 0 && cfg_.dim <= 4096;
 }
 
 bool DecodeStep::next_takes_split(int li) const {

@@ -1121,8 +1121,9 @@ static int launch_skinny_m(int fmt, const ActIn& A, const void* B, float* C, int
     // split K over the waves of a workgroup when there are too few tiles for ~2048 waves
     int KS = 1;
     while (KS < 8 && KS * 2 <= sb && static_cast<long>(ntiles) * KS < 2048) KS *= 2;
-    // Split K over workgroups instead: every wave takes its own 16-row tile (8 per workgroup)
-    // and each workgroup one chunk of K, the chunks sized so that ~256 workgroups run.  A
+    // Split K over workgroups instead (from 2 rows with a workspace, from 9 without): every wave
+    // takes its own 16-row tile (8 per workgroup) and each workgroup one chunk of K, the chunks
+    // sized so that ~256 workgroups run.  A
     // staged activation then feeds 8 tiles instead of 8 / KS, and each workgroup stages only
     // its chunk.  With a workspace a second launch (or the consumer) adds the partial sums and
     // applies the RMSNorm row factor: every shape splits.  Without one, the partial sums
@@ -1136,7 +1137,7 @@ static int launch_skinny_m(int fmt, const ActIn& A, const void* B, float* C, int
     const bool ws_split = ws && N % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15u) == 0 &&
                           wsf >= skinny_workspace_floats(M, N);
     int cs = -1;
-    if (M > 8 && (ws_split || (MODE != kActRMSNorm && K > KC))) {
+    if ((M > 1 && ws_split) || (M > 8 && MODE != kActRMSNorm && K > KC)) {
         const long groups8 = (ntiles + 7) / 8;
         int split = 1;
         while (split < 16 && groups8 * split * 2 <= 256 && K % (256 * split * 2) == 0) split *= 2;

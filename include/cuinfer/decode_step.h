@@ -136,7 +136,7 @@ private:
     Tensor argmax_part_, argmax_count_, rope_;
     Tensor res_parts_;    // the down projection's K-split partial sums at one token
     int res_splits_ = 0;  // > 0: the pending residual is that many partial sums in res_parts_
-    // 9..16 tokens: the pending residual as the unreduced partial sums of the o projection
+    // 2..16 tokens: the pending residual as the unreduced partial sums of the o projection
     // (res_part_count_ partial sums res_part_stride_ floats apart from res_part_; 0: the plain
     // residual pointer); the FFN's RMSNorm row kernel adds them to the hidden state and
     // normalizes, and gate/up take plain activations

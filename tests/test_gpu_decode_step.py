@@ -135,7 +135,7 @@ def llama2():
     return m, dec
 
 
-@pytest.mark.parametrize("M,pos", [(1, 2047), (16, 2032), (1, 0), (5, 700)])
+@pytest.mark.parametrize("M,pos", [(1, 2047), (16, 2032), (1, 0), (5, 700), (8, 2040), (2, 1500)])
 def test_step_llama_shapes(orc, llama2, M, pos):
     m, dec = llama2
     kc, vc = random_cache(m, 2048, 3000 + pos)
@@ -226,8 +226,8 @@ def test_batch16_replay_equals_eager(llama2):
 def test_step_mixed_formats_tied_fp32_head(orc, M):
     # q/k/v and gate/up of different formats (three / two separate matrices), an FP32 token
     # table tied to the LM head (matmul_transposed_b), head_dim 128 (the 8-slice attention
-    # layout); for M = 12 every format's K split over workgroups with the step's workspace (the
-    # RMSNorm prologue included), for M = 17 the unfused path (rmsnorm_residual, prefill GEMM,
+    # layout); for M = 3 and 12 every format's K split over workgroups with the step's workspace
+    # (the RMSNorm prologue included), for M = 17 the unfused path (rmsnorm_residual, prefill GEMM,
     # silu_mul), for M = 1 the first layer's down projection split into partial sums that the
     # separate q, k and v GEMVs of the second add up (the FP32 head takes a whole residual)
     m = make_model(2, dim=512, n_heads=4, n_kv_heads=2, head_dim=128, ffn=1024, vocab=1000, seed=7,
@@ -251,9 +251,10 @@ def test_step_mixed_formats_tied_fp32_head(orc, M):
     check_ids(nxt.cpu().numpy(), got, ref, ref_ids, tol)
 
 
-@pytest.mark.parametrize("fmt,M", [("q8_0", 12), ("q6_k", 9), ("fp16", 16), ("q5_0", 1), ("q6_k", 1)])
+@pytest.mark.parametrize("fmt,M", [("q8_0", 12), ("q6_k", 9), ("fp16", 16), ("q5_0", 1), ("q6_k", 1),
+                                   ("q4_k", 2), ("q8_0", 5), ("q4_0", 8), ("q6_k", 4), ("fp16", 3)])
 def test_step_fused_projections_split(orc, fmt, M):
-    # one format throughout, so q/k/v and gate/up are stored fused; at 9..16 rows their K is
+    # one format throughout, so q/k/v and gate/up are stored fused; at 2..16 rows their K is
     # split over workgroups and the partial sums are left for RoPE (q/k/v) and for the down
     # projection's prologue (a two-way gate/up split) to add up; at one row the q/k/v GEMV
     # rotates and appends to the caches in its epilogue
