@@ -21,6 +21,7 @@
 // gate/up outputs, or RMSNorm of hidden + residual (the row factor multiplies
 // y, the workgroup-wide sum of squares is reduced through LDS).
 #include <atomic>
+#include <type_traits>
 
 #include "act.hpp"
 #include "common.hpp"
@@ -29,6 +30,7 @@
 
 namespace cri {
 namespace dev {
+
 
 // PREF row-groups of weight bytes are kept in flight per wave: a wave issues
 // the loads of its first PREF row-groups before anything else, then stages
@@ -71,8 +73,9 @@ __device__ __forceinline__ void rope_out(const RopeOut& R, float* q_out, int n, 
 // KSPLIT: K is cut into gridDim.y parts; workgroup row blockIdx.y takes columns
 // [K blockIdx.y, K (blockIdx.y + 1)) of the weights (K, units: one part's) and of the
 // activations, and writes its partial sums to y + blockIdx.y N.
-template <class F, int UPL, int PREF, int MODE, int MR = 1, bool ROPE = false, bool KSPLIT = false>
-__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W, float* __restrict__ y, int N, int K,
+// BLK: threads per workgroup (256 or 512); every workgroup stages the whole activation vector.
+template <class F, int UPL, int PREF, int MODE, int MR = 1, bool ROPE = false, bool KSPLIT = false, int BLK = 256>
+__global__ __launch_bounds__(BLK) void gemv_kernel(const uint8_t* __restrict__ W, float* __restrict__ y, int N, int K,
                                                    int units, long row_bytes, int lpr_log2, const ActIn Pin, int mrows,
                                                    const RopeOut R) {
     constexpr bool kRms = MODE == kActRMSNorm || MODE == kActRMSNormS;
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
         if (P.b) P.b += static_cast<long>(kp) * K;
         y += static_cast<long>(kp) * N;
     }
-    extern __shared__ float xs[];  // MR x K activations (padded, xpad), staged once per workgroup (+4 partial sums)
+    extern __shared__ float xs[];  // MR x K activations (padded, xpad), staged once per workgroup (+ one partial sum per wave)
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
     const int u0 = lane & (lpr - 1);
@@ -107,14 +110,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
     }
 
     // 1. activations: global -> registers (issued first, tiny), weights in flight behind them
-    ActRaw<MODE> xv[MR][4];
+    constexpr int kXI = 1024 / BLK;  // 16-byte activation loads per thread covering K <= 4096
+    ActRaw<MODE> xv[MR][kXI];
     const int nx4 = K >> 2;
     const int xrow = xpad(K);  // LDS floats per staged activation row
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int j = threadIdx.x + 256 * i;
+        for (int i = 0; i < kXI; ++i) {
+            const int j = threadIdx.x + BLK * i;
             if (j < nx4) act_load<MODE>(xv[m][i], P, min(MR * (KSPLIT ? 0 : static_cast<int>(blockIdx.y)) + m, mrows - 1), 4 * j, P.lda);
         }
     typename F::Data buf[PREF][UPL];
@@ -135,19 +139,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 #pragma unroll
     for (int p = 0; p < PREF; ++p) load_rows(buf[p], base0 + p * stride);
 
-    // 2. stage activations in LDS (K <= 4096 is covered by the four loads above)
+    // 2. stage activations in LDS (K <= 4096 is covered by the loads above)
     float ss = 0.0f;
     const bool write_h = blockIdx.x == 0;
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int j = threadIdx.x + 256 * i;
+        for (int i = 0; i < kXI; ++i) {
+            const int j = threadIdx.x + BLK * i;
             if (j < nx4)
                 *reinterpret_cast<f32x4*>(xs + m * xrow + xpad(4 * j)) =
                     act_finish<MODE>(xv[m][i], P, m, 4 * j, K, ss, write_h);
         }
-    for (int j = threadIdx.x + 1024; j < nx4; j += 256)
+    for (int j = threadIdx.x + 1024; j < nx4; j += BLK)
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             ActRaw<MODE> raw;
@@ -162,7 +166,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
     float rs = 1.0f;
     if constexpr (kRms) {
         const float* part = xs + xpad(K);
-        rs = rms_factor(((part[0] + part[1]) + part[2]) + part[3], K, P.eps);
+        float t = part[0];
+#pragma unroll
+        for (int w = 1; w < BLK / 64; ++w) t += part[w];  // in wave order
+        rs = rms_factor(t, K, P.eps);
     }
     typename F::Xr xr[MR][UPL];
 #pragma unroll
@@ -207,6 +214,31 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ W
 
 namespace detail {
 
+template <class F, int UPL, int PREF, int MODE, int MR, bool ROPE, bool KSPLIT, int BLK>
+static int launch_gemv_blk(const ActIn& act, const void* W, float* y, int N, int K, int units, long row_bytes,
+                           int lpr_log2, hipStream_t stream, int mrows, const RopeOut& rope, int splits, long waves) {
+    constexpr int kW = BLK / 64;  // waves per workgroup
+    const int blocks = static_cast<int>((waves + kW - 1) / kW);
+    constexpr bool kRms = MODE == kActRMSNorm || MODE == kActRMSNormS;
+    const int lds = (MR * dev::xpad(K) + (kRms ? kW : 0)) * static_cast<int>(sizeof(float));
+    if (lds > 65536) {  // beyond the default dynamic-LDS limit: raise it once per kernel and device
+        constexpr int kMaxDevices = 64;
+        static std::atomic<bool> ready[kMaxDevices];
+        int devid = 0;
+        if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return kFailed;
+        if (!ready[devid].load(std::memory_order_acquire)) {
+            const void* fn = reinterpret_cast<const void*>(&dev::gemv_kernel<F, UPL, PREF, MODE, MR, ROPE, KSPLIT, BLK>);
+            if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+                return kFailed;
+            ready[devid].store(true, std::memory_order_release);
+        }
+    }
+    const unsigned gy = KSPLIT ? static_cast<unsigned>(splits) : static_cast<unsigned>((mrows + MR - 1) / MR);
+    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE, MR, ROPE, KSPLIT, BLK>), dim3(blocks, gy), dim3(BLK), lds,
+                       stream, static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act, mrows, rope);
+    return 0;
+}
+
 template <class F, int UPL, int PREF, int MODE, int MR = 1, bool ROPE = false, bool KSPLIT = false>
 static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K, int units, long row_bytes,
                           int lpr_log2, hipStream_t stream, int mrows = 1, const RopeOut& rope = RopeOut{},
@@ -222,25 +254,17 @@ static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K
     long waves = (UPL == 1 && (F::kSpread || groups <= kGemvTargetWaves)) ? groups : (groups + PREF - 1) / PREF;
     const long budget = KSPLIT ? kGemvTargetWaves / splits : kGemvTargetWaves;  // over all K parts
     if (waves > budget) waves = budget;
-    const int blocks = static_cast<int>((waves + 3) / 4);
-    constexpr bool kRms = MODE == kActRMSNorm || MODE == kActRMSNormS;
-    const int lds = (MR * dev::xpad(K) + (kRms ? 4 : 0)) * static_cast<int>(sizeof(float));
-    if (lds > 65536) {  // beyond the default dynamic-LDS limit: raise it once per kernel and device
-        constexpr int kMaxDevices = 64;
-        static std::atomic<bool> ready[kMaxDevices];
-        int devid = 0;
-        if (hipGetDevice(&devid) != hipSuccess || devid < 0 || devid >= kMaxDevices) return kFailed;
-        if (!ready[devid].load(std::memory_order_acquire)) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(&dev::gemv_kernel<F, UPL, PREF, MODE, MR, ROPE, KSPLIT>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-                return kFailed;
-            ready[devid].store(true, std::memory_order_release);
-        }
-    }
-    const unsigned gy = KSPLIT ? static_cast<unsigned>(splits) : static_cast<unsigned>((mrows + MR - 1) / MR);
-    hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE, MR, ROPE, KSPLIT>), dim3(blocks, gy), dim3(256), lds,
-                       stream, static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act, mrows, rope);
-    return 0;
+    // 512-thread workgroups (one per CU at the wave budget, so each CU stages the activations
+    // once) for the plain GEMVs that measured faster that way: Q8_0 at 2048 waves (8192 x 2048
+    // 5.90 -> 5.52 us) and the long activation vectors (2048 x 8192 Q4_K 6.44 -> 6.24 us); Q4_K
+    // 8192 x 2048 is even, short matrices (fewer CUs in use) and the RMSNorm prologue are slower
+    if constexpr (MODE == kActPlain && MR == 1 && !ROPE && !KSPLIT)
+        if (waves >= kGemvTargetWaves && (std::is_same<F, dev::GemvQ8_0>::value || K >= 4096))
+            return launch_gemv_blk<F, UPL, PREF, MODE, MR, ROPE, KSPLIT, 512>(act, W, y, N, K, units, row_bytes,
+                                                                               lpr_log2, stream, mrows, rope, splits,
+                                                                               waves);
+    return launch_gemv_blk<F, UPL, PREF, MODE, MR, ROPE, KSPLIT, 256>(act, W, y, N, K, units, row_bytes, lpr_log2,
+                                                                       stream, mrows, rope, splits, waves);
 }
 
 template <class F, int MODE, int MR = 1>
@@ -364,7 +388,7 @@ static int launch_gemv_ksplit_m(int fmt, const ActIn& act, const void* W, float*
 int launch_gemv_ksplit(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, int splits,
                        hipStream_t stream) {
     if (splits < 2 || splits > kResMaxSplits || K % (256 * splits) != 0 || !gemv_supported(fmt, K, W)) return kDeclined;
-    if ((dev::xpad(K / splits) + 4) * 4 > 160 * 1024) return kDeclined;
+    if ((dev::xpad(K / splits) + 8) * 4 > 160 * 1024) return kDeclined;
     switch (mode) {
         case kActPlain: return launch_gemv_ksplit_m<kActPlain>(fmt, act, W, y, N, K, splits, stream);
         case kActSwiGLU: return launch_gemv_ksplit_m<kActSwiGLU>(fmt, act, W, y, N, K, splits, stream);
@@ -374,7 +398,7 @@ int launch_gemv_ksplit(int mode, int fmt, const ActIn& act, const void* W, float
 
 int launch_gemv_rope(int fmt, const ActIn& act, const void* W, float* q_out, int N, int K, const RopeOut& rope,
                      hipStream_t stream, bool split_res) {
-    if ((dev::xpad(K) + 4) * 4 > 160 * 1024 || !gemv_supported(fmt, K, W)) return kDeclined;
+    if ((dev::xpad(K) + 8) * 4 > 160 * 1024 || !gemv_supported(fmt, K, W)) return kDeclined;
     if (rope.qd % 2 || rope.kvd % 2 || rope.half < 1 || rope.qd % (2 * rope.half) || rope.kvd % (2 * rope.half) ||
         N != rope.qd + 2 * rope.kvd)
         return kDeclined;
@@ -390,7 +414,7 @@ int launch_gemv_rope(int fmt, const ActIn& act, const void* W, float* q_out, int
 }
 
 int launch_gemv_act(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t stream) {
-    if ((dev::xpad(K) + 4) * 4 > 160 * 1024) return -1;  // the staged activations (+ 4 partial sums) fit in LDS
+    if ((dev::xpad(K) + 8) * 4 > 160 * 1024) return -1;  // the staged activations (+ one partial sum per wave) fit in LDS
     switch (mode) {
         case kActPlain: return launch_gemv_m<kActPlain>(fmt, act, W, y, N, K, stream);
         case kActSwiGLU: return launch_gemv_m<kActSwiGLU>(fmt, act, W, y, N, K, stream);
