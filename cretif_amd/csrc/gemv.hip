@@ -258,7 +258,8 @@ static int launch_gemv_t(const ActIn& act, const void* W, float* y, int N, int K
     // once) for the plain GEMVs that measured faster that way: Q8_0 at 2048 waves (8192 x 2048
     // 5.90 -> 5.52 us) and the long activation vectors (2048 x 8192 Q4_K 6.44 -> 6.24 us); Q4_K
     // 8192 x 2048 is even, short matrices (fewer CUs in use) and the RMSNorm prologue are slower
-    if constexpr (MODE == kActPlain && MR == 1 && !ROPE && !KSPLIT)
+    // (at most two units per lane and not FP32: wider variants spill at 256 registers per lane)
+    if constexpr (MODE == kActPlain && MR == 1 && !ROPE && !KSPLIT && UPL <= 2 && !std::is_same<F, dev::GemvF32>::value)
         if (waves >= kGemvTargetWaves && (std::is_same<F, dev::GemvQ8_0>::value || K >= 4096))
             return launch_gemv_blk<F, UPL, PREF, MODE, MR, ROPE, KSPLIT, 512>(act, W, y, N, K, units, row_bytes,
                                                                                lpr_log2, stream, mrows, rope, splits,
