@@ -122,6 +122,19 @@ def test_gemv_baseline_shapes(orc, fmt, N, K):
     assert err <= GEMV_TOL, err
 
 
+# ragged row counts on the 512-thread workgroups (plain GEMVs at the 2048-wave budget: Q8_0, or
+# K >= 4096), including a last workgroup that is only partly used
+@pytest.mark.parametrize("fmt,N,K", [("q8_0", 5001, 2048), ("q8_0", 4097, 1024), ("q4_k", 4099, 4096),
+                                     ("q4_0", 2053, 8192), ("q5_0", 3001, 4096), ("q6_k", 2051, 8192),
+                                     ("fp16", 2049, 4096)])
+def test_gemv_wide_workgroups_ragged(orc, fmt, N, K):
+    A = quant.randn(K, seed=3 * K + N).reshape(1, K)
+    Bq = weights(fmt, N, K, seed=N + 11 * K)
+    got = run_matmul(fmt, A, Bq, N, K)
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    assert normwise_rel_err(got, ref) <= GEMV_TOL
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("N", [1, 3, 17, 130, 1001])
 @pytest.mark.parametrize("K", [256, 768, 4096, 16384])
