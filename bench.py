@@ -305,6 +305,40 @@ def hip_memcpy(dst, src, nbytes, kind):
         raise RuntimeError("hipMemcpy failed")
 
 
+class VendorGemmRig(ChainTimed):
+    """A point of comparison, not part of the library: torch.mm on fp16 operands with fp32
+    output (hipBLASLt on this image, its default heuristic) at a prefill workload's shape,
+    C[M, N] = A[M, K] B[N, K]^T -- the vendor library's plain fp16 GEMM with the weights
+    already fp16, so no dequantization and no activation conversion.  The weights rotate over
+    `copies` device copies in one captured graph, like the prefill rig's."""
+
+    def __init__(self, M, N, K, copies=16):
+        import torch
+
+        g = torch.Generator(device="cuda").manual_seed(4000)
+        self.A = torch.randn(M, K, device="cuda", dtype=torch.float16, generator=g)
+        self.W = [(torch.randn(N, K, device="cuda", dtype=torch.float16, generator=g) * 0.02) for _ in range(copies)]
+        self.steps = copies
+
+        def call(n):
+            torch.mm(self.A, self.W[n % copies].t(), out_dtype=torch.float32)
+
+        def run():
+            for n in range(copies):
+                call(n)
+
+        self.call = call
+        self.stream = torch.cuda.Stream()
+        with torch.cuda.stream(self.stream):
+            run()
+        self.stream.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=self.stream):
+            run()
+        self.graphs = [gr]
+        torch.cuda.synchronize()
+
+
 class DecodeStepRig:
     """BASELINE config 5 through the product decode step (cri_decoder_*, C++
     cuinfer::DecodeStep): a synthetic Llama-3.2-1B -- 16 layers of Q4_K q (2048x2048),
@@ -612,6 +646,9 @@ def main():
                          "headline's 9.4 MB, then the best shape over sizes 0.25 MB .. 604 MB")
     ap.add_argument("--prefill", default=None, choices=sorted(PREFILL_WORKLOADS),
                     help="only time one prefill GEMM workload (for profiling) and print its figures")
+    ap.add_argument("--vendor-gemm", default=None, choices=sorted(PREFILL_WORKLOADS),
+                    help="only time the vendor library's plain fp16 GEMM (torch.mm, fp32 output) at that prefill "
+                         "workload's shape, as a point of comparison for the fused kernels")
     ap.add_argument("--gemv", default=None, choices=sorted(GEMV_WORKLOADS) + sorted(SKINNY_WORKLOADS),
                     help="only time one GEMV workload (for profiling) and print its figures")
     ap.add_argument("--decode-step", type=int, default=None, metavar="M",
@@ -683,6 +720,14 @@ def main():
         m = r.time(samples, 16)
         print(json.dumps({"workload": args.prefill, "M": m_, "N": n, "K": k, "launches_per_sample": r.steps,
                           "us": round(m * 1e3, 3), "TFLOP/s": round(2.0 * m_ * n * k / (m * 1e-3) / 1e12, 1)}))
+        return
+    if args.vendor_gemm:
+        _, m_, n, k = PREFILL_WORKLOADS[args.vendor_gemm]
+        r = VendorGemmRig(m_, n, k)
+        m = r.time(samples, 16)
+        print(json.dumps({"workload": "vendor_fp16_gemm " + args.vendor_gemm, "M": m_, "N": n, "K": k,
+                          "launches_per_sample": r.steps, "us": round(m * 1e3, 3),
+                          "TFLOP/s": round(2.0 * m_ * n * k / (m * 1e-3) / 1e12, 1)}))
         return
     if args.gemv:
         if args.gemv in SKINNY_WORKLOADS:
