@@ -1,10 +1,10 @@
 // prefill.hip -- fused dequant GEMM for multi-token (prefill) batches on the
-// matrix cores, C[M,N] = A[M,K] * dequant(B[N,K])^T, for the Q4_K and Q8_0
-// weights of BASELINE's prefill configuration (the other formats keep the
-// LDS-staged kernel of mfma_gemm.hip).
+// matrix cores, C[M,N] = A[M,K] * dequant(B[N,K])^T, for Q4_K, Q8_0 and Q6_K
+// weights (the other formats keep the LDS-staged kernel of mfma_gemm.hip).
 //
 // The reference computes the product with one fp32 FMA chain per output
-// (ref:src/kernels/matmul_quant.cu:64-130 Q8_0, :309-386 Q4_K).  Here:
+// (ref:src/kernels/matmul_quant.cu:64-130 Q8_0, :309-386 Q4_K, :398-498 Q6_K).
+// Here:
 //   * a workgroup of eight waves (two per SIMD, so one wave's dependency
 //     stalls are filled by the other's work) owns a 64(m) x 256(n) output
 //     tile; wave w owns the 32 weight rows [32 w, 32 w + 32) and all 64 m, as
@@ -16,7 +16,8 @@
 //   * weights are the B operand and never touch LDS: each lane decodes the
 //     bytes of its own weight row (its output column) in registers, to the
 //     reference's dequantized value rounded once to fp16 (Q8_0: d * q; Q4_K:
-//     d * (sc * q) - dmin * mn, sc * q exact), two weights per packed op;
+//     d * (sc * q) - dmin * mn, sc * q exact; Q6_K: twice, (q - 32) fp16(d sc)),
+//     two weights per packed op;
 //   * a lane's bytes of one step are one contiguous run (Q4_K: 16 quant bytes
 //     of the super-block chunk; Q8_0: one whole 34-byte block), so the 8 k of
 //     each MFMA sub-step are not consecutive k; the activation fragment of
@@ -85,16 +86,25 @@ __device__ __forceinline__ uint32_t p_mul(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(ph2, a) * __builtin_bit_cast(ph2, b));
 }
 
+// 16 bytes at a dword-aligned address (Q8_0 rows are only dword-aligned)
+__device__ __forceinline__ u32x4 p_load16(const uint8_t* p) {
+    const pu4a4 v = *reinterpret_cast<const pu4a4*>(p);
+    return u32x4{v.x, v.y, v.z, v.w};
+}
+
 // ---------------------------------------------------------------------------
 // B-operand formats.  A wave's weight bytes of one group (four k steps) are
-// kRowBytes consecutive bytes of each of its 32 rows; they are copied into a
-// per-wave LDS area row after row with coalesced 16-byte loads (kRowBytes / 16
-// lanes per row), so each cache line is requested once.  read<J>(): one
-// lane's bytes of step J of the group from that area.  prep<J>(): the step's
-// scale constants.  sub<S>(): the 8 fp16 weights (4 dwords) of MFMA sub-step
-// S.  chunk(S, h): which 8-column chunk of the 64-column step those 8 weights
-// are, so the activation fragment is fetched from the same k.  Splits start
-// on a multiple of four steps, so J = step mod 4 is a compile-time position.
+// kCopyPieces 16-byte pieces of each of its 32 rows (load_piece from the row's
+// group start, piece_bytes what is stored); they are copied into a per-wave
+// LDS area, kRowBytes per row, with coalesced loads (kCopyPieces lanes per
+// row), so each cache line is requested once; kTail formats add one dword per
+// row (load_tail, stored after the rows).  read<J>(): one lane's bytes of step
+// J of the group from that area.  prep<J>(): the step's scale constants.
+// sub<J, S>(): the 8 fp16 weights (4 dwords) of MFMA sub-step S of a step at
+// position J.  chunk(S, h): which 8-column chunk of the 64-column step those 8
+// weights are, so the activation fragment is fetched from the same k.  Splits
+// start on a multiple of four steps, so J = step mod 4 is a compile-time
+// position.
 
 // ref:src/kernels/dequantize.cu:289-324.  Step j of a super-block is its
 // 64-element chunk j: elements 64j + e (e < 32) are the low nibbles of
@@ -104,8 +114,16 @@ __device__ __forceinline__ uint32_t p_mul(uint32_t a, uint32_t b) {
 // (k = 64j + 16h + 0..15), sub-steps 2, 3 their high nibbles (k + 32).  A
 // group is one super-block (144 bytes per row).
 struct PQ4K {
+    static constexpr int kFmt = kFmtQ4_K;
     static constexpr int kBlockK = 256;
     static constexpr int kRowBytes = 144;
+    static constexpr int kCopyPieces = kRowBytes / 16;
+    static constexpr bool kTail = false;
+    using Piece = u32x4;
+    static constexpr int kAreaBytes = 32 * kRowBytes;
+    static constexpr int kReadPhase = 0;  // the next step's bytes are read in phase 0
+    static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
+    static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return (first_step >> 2) * 144L; }
     struct Frag {
         u32x4 hdr;  // d, dmin (fp16), scales[12]
@@ -149,7 +167,7 @@ struct PQ4K {
         k.m[1] = p_mul(mn1, nd);
     }
     // B fragment of sub-step S: d (sc q) - dmin mn, one rounding to fp16
-    template <int S>
+    template <int J, int S>
     static __device__ __forceinline__ void sub(const Frag& f, const Consts& k, uint32_t (&b)[4]) {
         constexpr int hi = S >= 2 ? 1 : 0;
         constexpr uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
@@ -171,8 +189,16 @@ struct PQ4K {
 // quants at 68j + 34h + 2.  A lane reads the 9 dwords from byte 68j + 32h
 // and funnel-shifts its quants by 2 (h = 0) or 4 (h = 1) bytes.
 struct PQ8_0 {
+    static constexpr int kFmt = kFmtQ8_0;
     static constexpr int kBlockK = 32;
     static constexpr int kRowBytes = 272;
+    static constexpr int kCopyPieces = kRowBytes / 16;
+    static constexpr bool kTail = false;
+    using Piece = u32x4;
+    static constexpr int kAreaBytes = 32 * kRowBytes;
+    static constexpr int kReadPhase = 0;  // the next step's bytes are read in phase 0
+    static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
+    static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return first_step * 68L; }
     struct Frag {
         uint32_t dw[9];
@@ -194,7 +220,7 @@ struct PQ8_0 {
         k.sel = h1 ? 0x07060504u : 0x05040302u;  // dword pair -> quants shifted by 4 or 2 bytes
     }
     // B fragment of sub-step S: d * q, one rounding to fp16
-    template <int S>
+    template <int J, int S>
     static __device__ __forceinline__ void sub(const Frag& f, const Consts& k, uint32_t (&b)[4]) {
         const uint32_t bias = p_const(-1152.0f, -1152.0f);  // 1024 + 128
 #pragma unroll
@@ -203,6 +229,112 @@ struct PQ8_0 {
             const uint32_t x = q ^ 0x80808080u;  // int8 -> q + 128
             b[2 * i] = p_mul(p_add(p_mlo(x), bias), k.d2);
             b[2 * i + 1] = p_mul(p_add(p_mhi(x), bias), k.d2);
+        }
+    }
+};
+
+// ref:src/kernels/dequantize.cu:179-244, x = d * sc * (q - 32) with q the 6-bit
+// value of a low/high nibble of ql and two bits of qh.  Step j of a super-block
+// is its 64 elements 64j ..: half c = j / 2 (128 elements), quarters 2 (j & 1) +
+// qq, qq = 0, 1; element l (< 32) of a quarter takes ql[64c + 32qq + l] (low
+// nibble for j even, high for j odd), bits 2 (2 (j & 1) + qq) of qh[32c + l] and
+// scale sc[8c + 4 (j & 1) + 2qq + l / 16].  Lane half h takes l in [16h, 16h +
+// 16): sub-step S is quarter qq = S & 1, l = 16h + 8 (S >> 1) + 0..7 (each sub-step
+// has one scale; a lane's low qh and ql dwords are done after sub-step 1).  A group is one super-block
+// (210 bytes per row: ql[128], qh[64], scales[16], d at 208), which starts 2
+// bytes after a dword boundary for odd super-blocks (and for alternate rows when
+// K / 256 is odd).  The copy reads 13 dword-aligned 16-byte pieces from the
+// dword boundary at or below the super-block plus the dword after each piece,
+// and stores the pieces shifted into place (v_alignbyte), so LDS holds super-block
+// bytes 0 .. 207 at offsets 0 .. 207 (the last piece's final two bytes, sc[14]
+// and sc[15] after a 2-byte shift, are not kept); a tail dword {sc[14], sc[15],
+// d} read with two 16-bit loads sits after the wave's 32 rows.  Every byte read lies inside
+// the super-block or the 2 bytes before it, which are the previous super-block's
+// (a super-block at the buffer's dword-aligned start has no shift).  Weights are
+// rounded twice: fp16(d * sc), then (q - 32) times it.
+struct PQ6K {
+    static constexpr int kFmt = kFmtQ6_K;
+    static constexpr int kBlockK = 256;
+    static constexpr int kRowBytes = 208;  // 13 pieces
+    static constexpr int kCopyPieces = 13;
+    static constexpr bool kTail = true;
+    static constexpr int kAreaBytes = 32 * kRowBytes + 32 * 4;  // the rows, then one tail dword per row
+    // the next step's bytes are read in phase 2, after half of this step's are decoded (registers)
+    static constexpr int kReadPhase = 2;
+    static __device__ __forceinline__ long group_offset(int first_step) { return (first_step >> 2) * 210L; }
+    struct Piece {
+        u32x4 v;     // the 16 bytes from the dword boundary
+        uint32_t e;  // bytes 0, 1: the two bytes after them; bits 16..17: the shift (0 or 2)
+    };
+    // ptr: the super-block start of the row plus 16 * piece
+    static __device__ __forceinline__ Piece load_piece(const uint8_t* ptr) {
+        const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ptr) & 3);
+        const uint8_t* a = ptr - sh;
+        Piece p;
+        p.v = p_load16(a);
+        // shift 2: the dword after the piece (for the last piece, bytes 206 .. 209 of the
+        // super-block); shift 0 needs none and reads the piece's own last dword, so no read
+        // passes the super-block's end
+        p.e = (*reinterpret_cast<const uint32_t*>(a + 12 + 2 * sh) & 0xFFFFu) | (sh << 16);
+        return p;
+    }
+    static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) {
+        const uint32_t sh = p.e >> 16;
+        return u32x4{__builtin_amdgcn_alignbyte(p.v.y, p.v.x, sh), __builtin_amdgcn_alignbyte(p.v.z, p.v.y, sh),
+                     __builtin_amdgcn_alignbyte(p.v.w, p.v.z, sh), __builtin_amdgcn_alignbyte(p.e, p.v.w, sh)};
+    }
+    // {sc[14], sc[15], d}: two 16-bit loads at even addresses inside the super-block
+    static __device__ __forceinline__ uint32_t load_tail(const uint8_t* grow) {
+        return static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(grow + 206)) |
+               (static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(grow + 208)) << 16);
+    }
+    struct Frag {
+        u32x4 l0, l1;  // ql[64c + 16h .. + 16), ql[64c + 32 + 16h .. + 16)
+        u32x4 qh;      // qh[32c + 16h .. + 16)
+        uint32_t scw;  // sc[8c + 4 (j & 1) .. + 4)
+        uint32_t tail; // sc[14], sc[15], d
+    };
+    template <int J>
+    static __device__ __forceinline__ void read(Frag& f, const char* row, int h) {
+        constexpr int c = J >> 1, odd = J & 1;
+        f.l0 = *reinterpret_cast<const u32x4*>(row + 64 * c + 16 * h);
+        f.l1 = *reinterpret_cast<const u32x4*>(row + 64 * c + 32 + 16 * h);
+        f.qh = *reinterpret_cast<const u32x4*>(row + 128 + 32 * c + 16 * h);
+        f.scw = *reinterpret_cast<const uint32_t*>(row + 192 + 8 * c + 4 * odd);
+        const int fr = __lane_id() & 31;  // row is the area's row fr; the tails follow the 32 rows
+        f.tail = *reinterpret_cast<const uint32_t*>(row + (32 - fr) * kRowBytes + 4 * fr);
+    }
+    static __device__ __forceinline__ constexpr int chunk(int s, int h) { return 4 * (s & 1) + 2 * h + (s >> 1); }
+    struct Consts {
+        uint32_t dsc[2];  // fp16(d * sc) pairs of quarters qq = 0, 1
+    };
+    // sc byte b of w (int8) as the fp16 pair (sc, sc): (1024 + (sc + 128)) - 1152, exact
+    static __device__ __forceinline__ uint32_t sc_pair(uint32_t w, uint32_t b) {
+        return p_add(p_perm(kPMagic, w ^ 0x80808080u, 0x04000400u | (b << 16) | b), p_const(-1152.0f, -1152.0f));
+    }
+    template <int J>
+    static __device__ __forceinline__ void prep(const Frag& f, Consts& k) {
+        const uint32_t h = __lane_id() >> 5;
+        const uint32_t d2 = p_perm(f.tail, f.tail, 0x03020302u);  // (d, d)
+        k.dsc[0] = p_mul(sc_pair(f.scw, h), d2);
+        k.dsc[1] = p_mul(J == 3 ? sc_pair(f.tail, h) : sc_pair(f.scw, h + 2), d2);
+    }
+    // B fragment of sub-step S: (q - 32) fp16(d sc)
+    template <int J, int S>
+    static __device__ __forceinline__ void sub(const Frag& f, const Consts& k, uint32_t (&b)[4]) {
+        constexpr int odd = J & 1, qq = S & 1, half = S >> 1;
+        constexpr int hs = 4 - (4 * odd + 2 * qq);  // qh bits 4 odd + 2 qq -> bits 4..5 of each byte
+        const u32x4& l = qq ? f.l1 : f.l0;
+        const uint32_t lw[2] = {half ? l.z : l.x, half ? l.w : l.y};
+        const uint32_t hw[2] = {half ? f.qh.z : f.qh.x, half ? f.qh.w : f.qh.y};
+        const uint32_t bias = p_const(-1056.0f, -1056.0f);  // 1024 + 32
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t lo = odd ? (lw[i] >> 4) : lw[i];
+            const uint32_t hb = (hs >= 0 ? (hw[i] << (hs >= 0 ? hs : 0)) : (hw[i] >> (hs < 0 ? -hs : 0))) & 0x30303030u;
+            const uint32_t u = (lo & 0x0F0F0F0Fu) | hb;
+            b[2 * i] = p_mul(p_add(p_mlo(u), bias), k.dsc[qq]);
+            b[2 * i + 1] = p_mul(p_add(p_mhi(u), bias), k.dsc[qq]);
         }
     }
 };
@@ -218,7 +350,7 @@ using pos_t = std::integral_constant<int, J>;
 // dynamic LDS: two activation buffers of four step tiles, then one weight area per wave
 template <class W>
 constexpr int prefill_lds_bytes() {
-    return 8 * kPStage + (kPThreads / 64) * 32 * W::kRowBytes;
+    return 8 * kPStage + (kPThreads / 64) * W::kAreaBytes;
 }
 
 template <class W>
@@ -259,8 +391,9 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     float amax[2] = {0.0f, 0.0f};
 
     // weight copy: the wave's rows n0c + r (clamped to N - 1), chunk c = 64 i + lane of the
-    // group's 32 * kRowBytes bytes -> row c / (kRowBytes / 16), 16-byte piece c % (kRowBytes / 16)
-    constexpr int kPieces = W::kRowBytes / 16, kChunks = 32 * kPieces, kLoads = (kChunks + 63) / 64;
+    // group's 32 * kCopyPieces pieces -> row c / kCopyPieces, piece c % kCopyPieces, stored at
+    // byte 16 c of the wave's area (rows kRowBytes = 16 kCopyPieces apart), tails after the rows
+    constexpr int kPieces = W::kCopyPieces, kChunks = 32 * kPieces, kLoads = (kChunks + 63) / 64;
     const int n0c = min(n0, N - 1);
     const uint8_t* const wbase = B + static_cast<long>(n0c) * row_bytes;
     int woff[kLoads];  // < 32 rows: 32 * row_bytes < 2^31 is a launch condition
@@ -270,7 +403,9 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         const int r = c / kPieces;
         woff[i] = (min(n0 + r, N - 1) - n0c) * static_cast<int>(row_bytes) + 16 * (c % kPieces);
     }
-    char* const warea = lds + 8 * kPStage + wave * 32 * W::kRowBytes;
+    // kTail formats: lane l (and l + 32, a duplicate) reads row l's tail dword
+    const int wtoff = (min(n0 + (lane & 31), N - 1) - n0c) * static_cast<int>(row_bytes);
+    char* const warea = lds + 8 * kPStage + wave * W::kAreaBytes;
     const char* const wrow = warea + fr * W::kRowBytes;  // this lane's row in the area
 
     // A-operand fetch offsets: m tile u, sub-step s -> row 32 u + fr, the chunk of the
@@ -302,14 +437,13 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const int ngrp = nst >> 2;
     auto step_of = [&](int t) { return s_begin + min(t, nst - 1); };
     f32x4 av[4][2];  // activations of the next group: [step][row]
-    u32x4 wr[kLoads];  // weight bytes of the next group
+    typename W::Piece wr[kLoads];  // weight bytes of the next group
+    uint32_t wt = 0;               // kTail formats: this lane's row's tail dword of the next group
     auto load_next = [&](int q) {
         const uint8_t* g = wbase + W::group_offset(step_of(4 * q));
 #pragma unroll
-        for (int i = 0; i < kLoads; ++i) {
-            const pu4a4 v = *reinterpret_cast<const pu4a4*>(g + woff[i]);  // Q8_0 rows are only dword-aligned
-            wr[i] = u32x4{v.x, v.y, v.z, v.w};
-        }
+        for (int i = 0; i < kLoads; ++i) wr[i] = W::load_piece(g + woff[i]);
+        if constexpr (W::kTail) wt = W::load_tail(g + wtoff);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -318,7 +452,9 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     auto write_w = [&]() {
 #pragma unroll
         for (int i = 0; i < kLoads; ++i)
-            if (64 * i + lane < kChunks) *reinterpret_cast<u32x4*>(warea + 16 * (64 * i + lane)) = wr[i];
+            if (64 * i + lane < kChunks) *reinterpret_cast<u32x4*>(warea + 16 * (64 * i + lane)) = W::piece_bytes(wr[i]);
+        if constexpr (W::kTail)
+            if (lane < 32) *reinterpret_cast<uint32_t*>(warea + 32 * W::kRowBytes + 4 * lane) = wt;
     };
     // step j, row i of the next group into buffer buf (tile j)
     auto stage = [&](char* buf, int j, int i) {
@@ -361,13 +497,13 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
             const ph8 a[2] = {ac[0][s], ac[1][s]};
             mma2(a, bc, s);
             if (s == 0) {
-                W::template sub<0>(fc, k, bn[0]);
+                W::template sub<J, 0>(fc, k, bn[0]);
                 if constexpr (J == 3) write_w();
-                W::template read<(J + 1) & 3>(fn, wrow, h);
             }
-            if (s == 1) W::template sub<1>(fc, k, bn[1]);
-            if (s == 2) W::template sub<2>(fc, k, bn[2]);
-            if (s == 3) W::template sub<3>(fc, k, bn[3]);
+            if (s == 1) W::template sub<J, 1>(fc, k, bn[1]);
+            if (s == 2) W::template sub<J, 2>(fc, k, bn[2]);
+            if (s == 3) W::template sub<J, 3>(fc, k, bn[3]);
+            if (s == W::kReadPhase) W::template read<(J + 1) & 3>(fn, wrow, h);
             if constexpr (kLast) {
                 stage(nxt, s, 0);
                 stage(nxt, s, 1);
@@ -406,10 +542,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     {
         typename W::Consts k;
         W::template prep<0>(f0, k);
-        W::template sub<0>(f0, k, b0[0]);
-        W::template sub<1>(f0, k, b0[1]);
-        W::template sub<2>(f0, k, b0[2]);
-        W::template sub<3>(f0, k, b0[3]);
+        W::template sub<0, 0>(f0, k, b0[0]);
+        W::template sub<0, 1>(f0, k, b0[1]);
+        W::template sub<0, 2>(f0, k, b0[2]);
+        W::template sub<0, 3>(f0, k, b0[3]);
     }
     W::template read<1>(f1, wrow, h);
     __syncthreads();
@@ -456,7 +592,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     // fp32 path for flagged rows: thread -> column nt * 256 + (tid & 255) of the flagged rows
     // of parity tid >> 8, the reference's per-element decode and a sequential fp32 sum over
     // this workgroup's k range
-    const int fmt = W::kBlockK == 256 ? kFmtQ4_K : kFmtQ8_0;
+    const int fmt = W::kFmt;
     for (unsigned long long rest = flagged & (0x5555555555555555ull << (tid >> 8)); rest != 0; rest &= rest - 1) {
         const int ml = __builtin_ctzll(rest);
         const int m = m0 + ml, nn = nt * kPTN + (tid & 255);
@@ -479,8 +615,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 namespace detail {
 
 bool prefill_supported(int fmt, int M, int N, int K, const void* A, const void* B) {
-    if (fmt != kFmtQ4_K && fmt != kFmtQ8_0) return false;
-    // whole groups of four 64-column steps (one Q4_K super-block, 272 bytes of a Q8_0 row)
+    if (fmt != kFmtQ4_K && fmt != kFmtQ8_0 && fmt != kFmtQ6_K) return false;
+    // whole groups of four 64-column steps (one Q4_K / Q6_K super-block, 272 bytes of a Q8_0 row)
     if (M < 1 || N < 1 || K < 4 * dev::kPKS || K % (4 * dev::kPKS) != 0) return false;
     if (static_cast<long>(M) * K >= (1L << 31) || 32 * row_bytes(fmt, K) >= (1L << 31)) return false;
     const uintptr_t a = reinterpret_cast<uintptr_t>(A), b = reinterpret_cast<uintptr_t>(B);
@@ -531,6 +667,7 @@ int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int 
     const dim3 g(static_cast<unsigned>(grid));
     const uint8_t* Bb = static_cast<const uint8_t*>(B);
     if (fmt == kFmtQ4_K) return launch_w<dev::PQ4K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
+    if (fmt == kFmtQ6_K) return launch_w<dev::PQ6K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
     return launch_w<dev::PQ8_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
 }
 

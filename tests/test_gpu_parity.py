@@ -346,7 +346,7 @@ def test_prefill_matches_oracle(orc, fmt, M, N, K):
     assert err <= PREFILL_TOL, err
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_k"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_k", "q6_k"])
 @pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192)])
 def test_prefill_baseline_config(orc, fmt, N, K):
     # 512 tokens x Llama-3.2-1B FFN gate/up and down, every output against the oracle (its
@@ -431,8 +431,8 @@ def test_prefill_large_activations(orc):
 def test_prefill_activation_range(orc, fmt, case):
     # fp16 holds |x| < 65504, and rows of very small values only as subnormals: rows of
     # activations ~1e5 (inf in fp16) or ~1e-7 must still meet the bar, each row against its own
-    # norm; 'mixed' puts such rows among ordinary ones (and into a split-k launch).  Q4_K and
-    # Q8_0 with K % 256 == 0 run the register-decode prefill kernel, the other formats and
+    # norm; 'mixed' puts such rows among ordinary ones (and into a split-k launch).  Q4_K, Q6_K
+    # and Q8_0 with K % 256 == 0 run the register-decode prefill kernel, the other formats and
     # q8_0 at K = 576 the LDS-staged one; both flag such rows and recompute them in fp32.
     M, N, K = (64, 300, 2048) if case != "mixed" else (40, 128, 8192)
     if fmt == "q8_0_k576":
