@@ -156,7 +156,7 @@ int matmul_swiglu_split_ws(int fmt, const float* gate, const float* up, int ld, 
 bool mfma_gemm_supported(int fmt, int M, int N, int K, const void* A, const void* B);
 int launch_mfma_gemm(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
 
-// multi-token GEMM with weights decoded straight into MFMA operands, Q4_K and Q8_0 (prefill.hip)
+// multi-token GEMM with weights decoded straight into MFMA operands, Q4_K, Q6_K and Q8_0 (prefill.hip)
 bool prefill_supported(int fmt, int M, int N, int K, const void* A, const void* B);
 int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
 
