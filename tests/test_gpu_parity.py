@@ -312,6 +312,22 @@ def test_q6_k_skinny_unaligned(orc, off):
     assert normwise_rel_err(host(C), orc.matmul_quant("q6_k", A, Bq, N, K)) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("K", [256, 768, 2048])
+@pytest.mark.parametrize("off", [0, 4])
+def test_q6_k_prefill_super_block_alignments(orc, K, off):
+    # the register-decode prefill kernel copies 210-byte super-blocks that start 0 or 2 bytes past
+    # a dword boundary (odd super-blocks; alternate rows when K/256 is odd); N odd puts the
+    # buffer's last super-block on either alignment, and the weights end where the buffer does
+    M, N = 40, 33
+    A = quant.randn(M * K, seed=K + off).reshape(M, K)
+    Bq = weights("q6_k", N, K, seed=K + off + 1)
+    buf = torch.zeros(Bq.size + off, dtype=torch.uint8, device="cuda")
+    buf[off:] = dev(Bq)
+    C = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    cri.matmul_q6_k(dev(A), buf.data_ptr() + off, C, M, N, K)
+    assert normwise_rel_err(host(C), orc.matmul_quant("q6_k", A, Bq, N, K)) <= PREFILL_TOL
+
+
 def test_reference_test_shapes(orc):
     # shapes and LCG data of ref:tests/test_matmul_quant.cu (MatmulQ8_0/Q4_0/Q4_K/Q5_0/Q6_K/FP16)
     cases = [
