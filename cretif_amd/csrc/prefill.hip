@@ -13,13 +13,15 @@
 //     thread converts 8 fp32 values of two rows to fp16 and writes them to a
 //     double-buffered LDS tile of 64 rows x 64 halves, which all eight waves
 //     read (8 ds_read_b128 per wave and step);
-//   * weights are the B operand and never touch LDS: each lane decodes the
-//     bytes of its own weight row (its output column) in registers, to the
-//     reference's dequantized value rounded once to fp16 (Q8_0: d * q; Q4_K:
-//     d * (sc * q) - dmin * mn, sc * q exact; Q6_K: twice, (q - 32) fp16(d sc)),
-//     two weights per packed op;
-//   * a lane's bytes of one step are one contiguous run (Q4_K: 16 quant bytes
-//     of the super-block chunk; Q8_0: one whole 34-byte block), so the 8 k of
+//   * weights are the B operand: each wave copies its 32 rows' bytes of a
+//     group of four steps into its own LDS area with coalesced loads, and each
+//     lane decodes the bytes of its own weight row (its output column) from
+//     there in registers, to the reference's dequantized value rounded once to
+//     fp16 (Q8_0: d * q; Q4_K: d * (sc * q) - dmin * mn, sc * q exact; Q6_K:
+//     twice, (q - 32) fp16(d sc)), two weights per packed op;
+//   * a lane's bytes of one step are contiguous runs (Q4_K: 16 quant bytes of
+//     the super-block chunk; Q8_0: one whole 34-byte block; Q6_K: 16 bytes of
+//     each of two ql runs and of qh), so the 8 k of
 //     each MFMA sub-step are not consecutive k; the activation fragment of
 //     every sub-step is fetched from the LDS columns of the same k, so the
 //     products and sums are the same as in k order;
