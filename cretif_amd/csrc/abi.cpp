@@ -89,6 +89,9 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
     else if (cri::detail::skinny_supported(fmt, M, K, B))
         rc = cri::detail::launch_skinny_act(cri::kActPlain, fmt, cri::ActIn{A, nullptr, nullptr, nullptr, K, 0.0f}, B,
                                             C, M, N, K, stream, ws, ws_floats, defer, defer_S);
+    else if (M == 1 && cri::detail::slice_gemv_supported(fmt, K, B))
+        rc = cri::detail::launch_slice_gemv(cri::kActPlain, fmt, cri::ActIn{A, nullptr, nullptr, nullptr, K, 0.0f}, B,
+                                            C, N, K, stream);
     else if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv(fmt, A, B, C, N, K, stream);
     else if (M > kPrefillMinM && cri::detail::prefill_supported(fmt, M, N, K, A, B))
@@ -272,12 +275,16 @@ int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float*
     if (fmt == cri::kFmtF16 && !aligned(B, 2)) return fail(CRI_ERR_ALIGNMENT, fn, "FP16 B must be 2-byte aligned");
     clear_pending_error();
     if (mode == cri::kActRMSNormS) {  // one token on the batch-1 GEMV only
+        if (M == 1 && cri::detail::slice_gemv_supported(fmt, K, B))
+            return finish_matmul(cri::detail::launch_slice_gemv(mode, fmt, act, B, C, N, K, stream), fn);
         if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
             return finish_matmul(cri::detail::launch_gemv_act(mode, fmt, act, B, C, N, K, stream), fn);
         return fail(CRI_ERR_UNSUPPORTED, fn, "a split residual is taken by the batch-1 GEMV only");
     }
     int rc = cri::detail::kDeclined;
-    if (cri::detail::skinny_supported(fmt, M, K, B))
+    if (M == 1 && mode != cri::kActSwiGLU2 && cri::detail::slice_gemv_supported(fmt, K, B))
+        rc = cri::detail::launch_slice_gemv(mode, fmt, act, B, C, N, K, stream);
+    if (rc == cri::detail::kDeclined && cri::detail::skinny_supported(fmt, M, K, B))
         rc = cri::detail::launch_skinny_act(mode, fmt, act, B, C, M, N, K, stream, ws, ws_floats, defer, defer_S);
     if (rc == cri::detail::kDeclined && mode == cri::kActSwiGLU2)
         return fail(CRI_ERR_UNSUPPORTED, fn, "the two-split SwiGLU prologue runs on the skinny kernel only");

@@ -27,10 +27,10 @@
 #include "common.hpp"
 #include "gemv_formats.hpp"
 #include "internal.hpp"
+#include "rope.hpp"
 
 namespace cri {
 namespace dev {
-
 
 // PREF row-groups of weight bytes are kept in flight per wave: a wave issues
 // the loads of its first PREF row-groups before anything else, then stages
@@ -43,29 +43,6 @@ namespace dev {
 // weights is multiplied with both rows, so a batch of two streams the weights once.
 // Workgroup row blockIdx.y takes activation rows MR y .. MR y + MR - 1 of mrows
 // (past the last row: the last row again, not stored).
-// Output column n (value x, its pair partner xp) of the fused q/k/v projection: q and k
-// rotated by the angle of (position, pair) as the RoPE kernel does, q to q_out, k and v to
-// cache row pos.
-__device__ __forceinline__ void rope_out(const RopeOut& R, float* q_out, int n, float x, float xp) {
-    const int pos = *R.pos;
-    const long kvrow = static_cast<long>(pos) * R.kvd;
-    if (n < R.qd + R.kvd) {
-        const int nn = n < R.qd ? n : n - R.qd;
-        const int lp = (nn % (2 * R.half)) >> 1;
-        const f32x2 cs = reinterpret_cast<const f32x2*>(R.rot)[static_cast<long>(pos) * R.half + lp];
-        const bool odd = n & 1;
-        const float x0 = odd ? xp : x, x1 = odd ? x : xp;
-        const float v = odd ? __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x))
-                            : __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y));
-        if (n < R.qd)
-            q_out[n] = v;
-        else
-            R.kc[kvrow + nn] = v;
-    } else {
-        R.vc[kvrow + (n - R.qd - R.kvd)] = x;
-    }
-}
-
 // ROPE: the fused q/k/v projection of one token (RopeOut).  A wave's rows b .. b + 64 / LPR - 1
 // start at an even b (rows per iteration and the stride are even for LPR <= 32), so the
 // rotated pair (2i, 2i + 1) sits in lane groups rsub and rsub ^ 1, one shuffle apart; the

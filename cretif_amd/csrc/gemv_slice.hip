@@ -1,0 +1,280 @@
+// gemv_slice.hip -- batch-1 GEMV y[N] = W[N,K] x[K] with K sliced over the four waves of a
+// workgroup, for Q4_K weights (the decode GEMVs of a Q4_K model and the C ABI's M = 1 case).
+//
+// Replaces the M == 1 case of ref:src/kernels/matmul_quant.cu:309-397 (one 32x32 thread
+// block per 32 outputs, 31/32 of the lanes idle at M = 1).
+//
+// Work decomposition (wave64, 256 threads = 4 waves per workgroup):
+//   * a workgroup owns R consecutive rows; wave w owns K slice [K w / 4, K (w + 1) / 4) of
+//     all of them, so the four waves' partial sums meet once, through LDS, at the end;
+//   * a "piece" is 32 weights of one row (half of a 64-element Q4_K chunk: 16 bytes of qs,
+//     low nibbles = 16 elements, high nibbles = the 16 elements 32 further on); L = K / 128
+//     lanes share a row (L pieces = one K slice), so a wave takes 64 / L rows per step and
+//     IT steps (R = IT * 64 / L);
+//   * a lane's 32 activations stay in VGPRs for all of its IT rows (computed from the
+//     prologue's inputs when MODE is not plain), loaded straight from global memory: every
+//     wave of the grid reads the same K floats, which the L1/L2 serve; LDS staging, with its
+//     barrier and 4x-replicated reads, measured slower;
+//   * every weight load of the wave is issued at kernel entry, before the activation loads
+//     (which are L2 hits and would otherwise delay the HBM requests behind them), two row
+//     steps ahead of them so the first steps' decode can start while later rows stream in;
+//   * the arguments a weight address needs (W, row bytes, N) are plain scalars in the
+//     first kernel-argument dwords, which the hardware preloads into SGPRs: no weight load
+//     waits on a kernel-argument fetch, and the kernel reads no hidden argument (blockDim,
+//     gridDim) at all.
+// Per piece a lane loads the 16-byte super-block header (d, dmin, 12 scale bytes; the 8 lanes
+// of one super-block read the same 16 bytes in one instruction) and its 16 quant bytes, both
+// 16-byte aligned; consecutive lanes read consecutive quant bytes.
+//
+// MODE (see ActIn): kActPlain, kActSwiGLU, kActRMSNorm, kActRMSNormS; the RMSNorm row
+// factor multiplies the finished sum (each wave adds the squares of its slice, the four
+// parts are added in wave order).  ROPE: the fused q/k/v projection of one token with the
+// rotation and the KV-cache append in the epilogue (RopeOut; rows come in even/odd pairs in
+// one wave of the final reduction).
+#include "act.hpp"
+#include "common.hpp"
+#include "internal.hpp"
+#include "rope.hpp"
+
+namespace cri {
+namespace dev {
+
+// Q4_K piece p of a row: super-block p >> 3, chunk j = (p >> 1) & 3, half h = p & 1.  Quant
+// bytes 16 + 32 j + 16 h .. +16 of the super-block; low nibble of byte i = element
+// 64 j + 16 h + i, high nibble = element 64 j + 32 + 16 h + i (ref:src/kernels/dequantize.cu:307-319).
+struct SliceQ4K {
+    struct Data {
+        u32x4 hd, q;
+    };
+    static __device__ __forceinline__ int x_first(int p) { return (p >> 3) * 256 + 64 * ((p >> 1) & 3) + 16 * (p & 1); }
+    static __device__ __forceinline__ void load(Data& d, const uint8_t* __restrict__ row, int p) {
+        const uint8_t* sb = row + (p >> 3) * 144;
+        d.hd = ld_u32x4(sb);
+        d.q = ld_u32x4(sb + 16 + 32 * ((p >> 1) & 3) + 16 * (p & 1));
+    }
+    // sum over the piece of w * x, xa = elements x_first .. +16, xb = x_first + 32 .. +16,
+    // sa / sb their sums (for the -dmin * mn term)
+    static __device__ __forceinline__ float dot(const Data& d, const float (&xa)[16], const float (&xb)[16],
+                                                float sa, float sb, int p) {
+        // 6-bit scale and min of sub-blocks 2j (low nibbles) and 2j + 1 (high nibbles)
+        // (ref:src/kernels/dequantize.cu:298-305):
+        //   j < 2:  sc = s[sb] & 63, mn = s[sb + 4] & 63
+        //   j >= 2: sc = (s[sb + 4] & 15) | (s[sb - 4] >> 6) << 4, mn = (s[sb + 4] >> 4) | (s[sb] >> 6) << 4
+        const int j = (p >> 1) & 3;
+        const bool low = j < 2;
+        const uint32_t o = (j & 1) * 16;
+        const uint32_t h1 = d.hd.y, h2 = d.hd.z, h3 = d.hd.w;
+        const uint32_t a_sc = low ? h1 : h3;
+        const uint32_t a_mn = low ? h2 : h3;
+        const uint32_t wa = low ? 6 : 4;
+        const uint32_t wb = low ? 0 : 2;
+        const uint32_t om = low ? 0 : 4;
+        const uint32_t sc_lo = ubfe(a_sc, o, wa) | (ubfe(h1, o + 6, wb) << 4);
+        const uint32_t mn_lo = ubfe(a_mn, o + om, wa) | (ubfe(h2, o + 6, wb) << 4);
+        const uint32_t sc_hi = ubfe(a_sc, o + 8, wa) | (ubfe(h1, o + 14, wb) << 4);
+        const uint32_t mn_hi = ubfe(a_mn, o + 8 + om, wa) | (ubfe(h2, o + 14, wb) << 4);
+        // nibbles as binary16 subnormals q * 2^-24 in the halves of a dword: one v_fma_mix_f32 each
+        float l0 = 0.f, l1 = 0.f, g0 = 0.f, g1 = 0.f;
+        const uint32_t q[4] = {d.q.x, d.q.y, d.q.z, d.q.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t w = q[t], u = w >> 8;
+            const uint32_t a = w & 0x000F000Fu;  // low nibbles of bytes 4t, 4t + 2
+            const uint32_t b = w & 0x00F000F0u;  // 16 * high nibbles of bytes 4t, 4t + 2
+            const uint32_t e = u & 0x000F000Fu;  // low nibbles of bytes 4t + 1, 4t + 3
+            const uint32_t f = u & 0x00F000F0u;  // 16 * high nibbles of bytes 4t + 1, 4t + 3
+            l0 = __builtin_fmaf(h_lo(a), xa[4 * t + 0], l0);
+            l1 = __builtin_fmaf(h_lo(e), xa[4 * t + 1], l1);
+            l0 = __builtin_fmaf(h_hi(a), xa[4 * t + 2], l0);
+            l1 = __builtin_fmaf(h_hi(e), xa[4 * t + 3], l1);
+            g0 = __builtin_fmaf(h_lo(b), xb[4 * t + 0], g0);
+            g1 = __builtin_fmaf(h_lo(f), xb[4 * t + 1], g1);
+            g0 = __builtin_fmaf(h_hi(b), xb[4 * t + 2], g0);
+            g1 = __builtin_fmaf(h_hi(f), xb[4 * t + 3], g1);
+        }
+        const float dd = h_lo(d.hd.x), dmin = h_hi(d.hd.x);
+        const float t = (l0 + l1) * static_cast<float>(sc_lo) + (g0 + g1) * (static_cast<float>(sc_hi) * 0.0625f);
+        const float m = static_cast<float>(mn_lo) * sa + static_cast<float>(mn_hi) * sb;
+        return (dd * kTwo24) * t - dmin * m;
+    }
+};
+
+constexpr int kSliceWaves = 4;   // waves per workgroup, one K slice each
+constexpr int kSliceXAfter = 2;  // row steps whose weight loads go before the activation loads
+
+template <class F, int LG, int IT, int MODE, bool ROPE>
+__global__ __launch_bounds__(64 * kSliceWaves) void slice_gemv_kernel(const uint8_t* __restrict__ W,
+                                                                      float* __restrict__ y,
+                                                                      const float* __restrict__ xa_ptr, int N,
+                                                                      int row_bytes, const ActIn Pin,
+                                                                      const RopeOut R) {
+    constexpr int L = 1 << LG, RPI = 64 / L, RW = IT * RPI;  // lanes per row, rows per step, rows per workgroup
+    constexpr int K = kSliceWaves * L * 32;
+    constexpr bool kRms = MODE == kActRMSNorm || MODE == kActRMSNormS;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int sub = lane & (L - 1), rsub = lane >> LG;
+    const int p = wv * L + sub;  // piece index along the row
+    const int row0 = blockIdx.x * RW;
+
+    ActIn P = Pin;
+    if constexpr (MODE == kActPlain) P.a = xa_ptr;
+    float xa[16], xb[16];
+    float ss = 0.0f;
+    auto xload = [&]() {
+        const int k0 = F::x_first(p);
+        ActRaw<MODE> ra[4], rb[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            act_load<MODE>(ra[v], P, 0, k0 + 4 * v, P.lda);
+            act_load<MODE>(rb[v], P, 0, k0 + 32 + 4 * v, P.lda);
+        }
+        // the hidden state is written by workgroup 0's first row group (each element once)
+        const bool wh = blockIdx.x == 0 && rsub == 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const f32x4 a = act_finish<MODE>(ra[v], P, 0, k0 + 4 * v, K, ss, wh);
+            const f32x4 b = act_finish<MODE>(rb[v], P, 0, k0 + 32 + 4 * v, K, ss, wh);
+            xa[4 * v] = a.x; xa[4 * v + 1] = a.y; xa[4 * v + 2] = a.z; xa[4 * v + 3] = a.w;
+            xb[4 * v] = b.x; xb[4 * v + 1] = b.y; xb[4 * v + 2] = b.z; xb[4 * v + 3] = b.w;
+        }
+    };
+    typename F::Data buf[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        if (it == kSliceXAfter) xload();
+        // rows past the end read row N - 1 again (unconditional loads keep every request in flight)
+        const uint8_t* rp = W + static_cast<long>(min(row0 + it * RPI + rsub, N - 1)) * row_bytes;
+        F::load(buf[it], rp, p);
+    }
+    if constexpr (IT <= kSliceXAfter) xload();
+
+    float sa = 0.f, sb = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        sa += xa[v];
+        sb += xb[v];
+    }
+    float acc[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) acc[it] = group_sum_t<LG>(F::dot(buf[it], xa, xb, sa, sb, p));
+
+    __shared__ float red[kSliceWaves][RW];
+    __shared__ float ssq[kSliceWaves];
+#pragma unroll
+    for (int it = 0; it < IT; ++it)
+        if (sub == 0) red[wv][it * RPI + rsub] = acc[it];
+    if constexpr (kRms) {
+        ss = group_sum_t<LG>(ss);  // the wave's slice (the row groups hold the same activations)
+        if (lane == 0) ssq[wv] = ss;
+    }
+    __syncthreads();
+    if (threadIdx.x < RW) {
+        const int t = threadIdx.x;
+        float v = red[0][t];
+#pragma unroll
+        for (int w = 1; w < kSliceWaves; ++w) v += red[w][t];  // in wave order
+        if constexpr (kRms) {
+            float q = ssq[0];
+#pragma unroll
+            for (int w = 1; w < kSliceWaves; ++w) q += ssq[w];
+            v *= rms_factor(q, K, P.eps);
+        }
+        const int r = row0 + t;
+        if constexpr (ROPE) {
+            const float vp = __shfl_xor(v, 1);  // row r ^ 1 (RW is even and row0 a multiple of RW)
+            if (r < N) rope_out(R, y, r, v, vp);
+        } else {
+            if (r < N) y[r] = v;
+        }
+    }
+}
+
+}  // namespace dev
+
+namespace detail {
+
+namespace {
+
+// lanes per row = K / 128 (K in {1024, 2048, 4096, 8192}); log2 of it, or -1
+int slice_lg(int K) {
+    switch (K) {
+        case 1024: return 3;
+        case 2048: return 4;
+        case 4096: return 5;
+        case 8192: return 6;
+    }
+    return -1;
+}
+
+// Row steps per wave: IT rows per lane share one activation load, so the grid's activation reads
+// are N K / (IT 64 / L) floats; IT = 8 measured fastest at the Llama-3.2-1B shapes (8192 x 2048:
+// 256 workgroups of 32 rows, 3.94 us against 4.56 us on the unsliced GEMV; 2048 x 8192: 256 of
+// 8 rows, 4.71 against 6.2 us).  Fewer for short matrices, so that ~256 workgroups still run.
+int slice_steps(int N, int LG) {
+    const long rows_per_step = 64 >> LG;
+    int it = 8;
+    while (it > 1 && (static_cast<long>(N) + it * rows_per_step - 1) / (it * rows_per_step) < 256) it >>= 1;
+    return it;
+}
+
+template <class F, int LG, int IT, int MODE, bool ROPE>
+int launch_slice_t(const ActIn& act, const void* W, float* y, int N, int K, const RopeOut& rope, hipStream_t s) {
+    constexpr int RW = IT * (64 >> LG);
+    const int blocks = (N + RW - 1) / RW;
+    const int rbytes = static_cast<int>(cri::row_bytes(kFmtQ4_K, K));
+    hipLaunchKernelGGL((dev::slice_gemv_kernel<F, LG, IT, MODE, ROPE>), dim3(blocks), dim3(64 * dev::kSliceWaves), 0,
+                       s, static_cast<const uint8_t*>(W), y, act.a, N, rbytes, act, rope);
+    return 0;
+}
+
+template <class F, int LG, int MODE, bool ROPE>
+int launch_slice_it(const ActIn& act, const void* W, float* y, int N, int K, const RopeOut& rope, hipStream_t s) {
+    switch (slice_steps(N, LG)) {
+        case 8: return launch_slice_t<F, LG, 8, MODE, ROPE>(act, W, y, N, K, rope, s);
+        case 4: return launch_slice_t<F, LG, 4, MODE, ROPE>(act, W, y, N, K, rope, s);
+        case 2: return launch_slice_t<F, LG, 2, MODE, ROPE>(act, W, y, N, K, rope, s);
+        default: return launch_slice_t<F, LG, 1, MODE, ROPE>(act, W, y, N, K, rope, s);
+    }
+}
+
+template <int MODE, bool ROPE>
+int launch_slice_m(const ActIn& act, const void* W, float* y, int N, int K, const RopeOut& rope, hipStream_t s) {
+    switch (slice_lg(K)) {
+        case 3: return launch_slice_it<dev::SliceQ4K, 3, MODE, ROPE>(act, W, y, N, K, rope, s);
+        case 4: return launch_slice_it<dev::SliceQ4K, 4, MODE, ROPE>(act, W, y, N, K, rope, s);
+        case 5: return launch_slice_it<dev::SliceQ4K, 5, MODE, ROPE>(act, W, y, N, K, rope, s);
+        case 6: return launch_slice_it<dev::SliceQ4K, 6, MODE, ROPE>(act, W, y, N, K, rope, s);
+    }
+    return kDeclined;
+}
+
+}  // namespace
+
+bool slice_gemv_supported(int fmt, int K, const void* W) {
+    return fmt == kFmtQ4_K && slice_lg(K) >= 0 && (reinterpret_cast<uintptr_t>(W) & 3u) == 0;
+}
+
+int launch_slice_gemv(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
+    if (!slice_gemv_supported(fmt, K, W)) return kDeclined;
+    const RopeOut none{};
+    switch (mode) {
+        case kActPlain: return launch_slice_m<kActPlain, false>(act, W, y, N, K, none, s);
+        case kActSwiGLU: return launch_slice_m<kActSwiGLU, false>(act, W, y, N, K, none, s);
+        case kActRMSNorm: return launch_slice_m<kActRMSNorm, false>(act, W, y, N, K, none, s);
+        case kActRMSNormS: return launch_slice_m<kActRMSNormS, false>(act, W, y, N, K, none, s);
+    }
+    return kDeclined;
+}
+
+int launch_slice_gemv_rope(const ActIn& act, const void* W, float* q_out, int N, int K, const RopeOut& rope,
+                           hipStream_t s, bool split_res) {
+    if (!slice_gemv_supported(kFmtQ4_K, K, W)) return kDeclined;
+    if (rope.qd % 2 || rope.kvd % 2 || rope.half < 1 || rope.qd % (2 * rope.half) || rope.kvd % (2 * rope.half) ||
+        N != rope.qd + 2 * rope.kvd)
+        return kDeclined;
+    if (split_res) return launch_slice_m<kActRMSNormS, true>(act, W, q_out, N, K, rope, s);
+    return launch_slice_m<kActRMSNorm, true>(act, W, q_out, N, K, rope, s);
+}
+
+}  // namespace detail
+}  // namespace cri

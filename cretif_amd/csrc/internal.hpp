@@ -116,6 +116,15 @@ int launch_gemv_ksplit(int mode, int fmt, const ActIn& act, const void* W, float
 int launch_gemv_rope(int fmt, const ActIn& act, const void* W, float* q_out, int N, int K, const RopeOut& rope,
                      hipStream_t stream, bool split_res = false);
 
+// batch-1 Q4_K GEMV with K sliced over the four waves of a workgroup (gemv_slice.hip), for K in
+// {1024, 2048, 4096, 8192} and dword-aligned weights; plain, SwiGLU, RMSNorm or split-residual
+// RMSNorm prologue (kDeclined otherwise)
+bool slice_gemv_supported(int fmt, int K, const void* W);
+int launch_slice_gemv(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t stream);
+// the same with the fused q/k/v projection's RoPE + cache-append epilogue (as launch_gemv_rope)
+int launch_slice_gemv_rope(const ActIn& act, const void* W, float* q_out, int N, int K, const RopeOut& rope,
+                           hipStream_t stream, bool split_res = false);
+
 // 1 <= M <= 16 fused dequant matmul on the matrix cores (mfma_skinny.hip)
 bool skinny_supported(int fmt, int M, int K, const void* B);
 int launch_skinny(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);

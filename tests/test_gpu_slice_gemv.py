@@ -1,0 +1,98 @@
+"""GPU parity of the K-sliced batch-1 Q4_K GEMV (gemv_slice.hip) through the C ABI.
+
+cri_matmul_q4_k at M = 1 with K in {1024, 2048, 4096, 8192} takes this kernel; the row
+count decides how many rows a workgroup takes (1, 2, 4 or 8 row steps), so N runs over
+values that give each step count, a last workgroup only partly used, and a single row.
+The fused prologues (cri_matmul_rmsnorm, cri_matmul_swiglu) at M = 1 take it too.
+
+Bars as in test_gpu_parity.py / test_gpu_fused.py: ||C - C_ref||_inf <= 1e-5 ||C_ref||_inf
+against the oracle (ref:src/kernels/matmul_quant.cu:309-397 restated); exact-integer
+inputs bit-exact (every partial sum an integer well below 2^24, so any summation order
+gives the same bits); hidden_out bit-exact."""
+import numpy as np
+import pytest
+
+from conftest import bits_equal, normwise_rel_err
+
+torch = pytest.importorskip("torch")
+import cretif_amd as cri  # noqa: E402
+from cretif_amd import quant  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+SLICE_K = [1024, 2048, 4096, 8192]
+# row counts: one row, ragged small, the 256-workgroup thresholds of each step count, large
+SLICE_N = [1, 5, 33, 257, 1030, 2048, 4099, 8192]
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rnd(shape, seed, scale=1.0):
+    return (np.random.default_rng(seed).standard_normal(shape) * scale).astype(np.float32)
+
+
+@pytest.mark.parametrize("K", SLICE_K)
+@pytest.mark.parametrize("N", SLICE_N)
+def test_slice_gemv_plain(orc, N, K):
+    A = quant.randn(K, seed=N + K).reshape(1, K)
+    W = quant.synthetic_weights("q4_k", N, K, seed=3 * N + K)
+    C = torch.full((1, N), float("nan"), device="cuda")
+    cri.matmul_q4_k(dev(A), dev(W), C, 1, N, K)
+    assert normwise_rel_err(host(C), orc.matmul_quant("q4_k", A, W, N, K)) <= TOL
+
+
+@pytest.mark.parametrize("K", [1024, 2048])
+def test_slice_gemv_exact_integer(orc, K):
+    from test_oracle_matmul import exact_case
+
+    N = 515
+    A, W = exact_case("q4_k", 1, N, K, seed=K)
+    C = torch.full((1, N), float("nan"), device="cuda")
+    cri.matmul_q4_k(dev(A), dev(W), C, 1, N, K)
+    assert bits_equal(host(C), orc.matmul_quant("q4_k", A, W, N, K))
+
+
+@pytest.mark.parametrize("K", SLICE_K)
+@pytest.mark.parametrize("N", [7, 640, 3072])
+def test_slice_gemv_rmsnorm(orc, N, K):
+    W = quant.synthetic_weights("q4_k", N, K, seed=N + 5)
+    h, r, w = rnd((1, K), 1 + K), rnd((1, K), 2 + K, 0.5), rnd(K, 3 + K)
+    hout = torch.full((1, K), float("nan"), device="cuda")
+    C = torch.full((1, N), float("nan"), device="cuda")
+    cri.matmul_rmsnorm("q4_k", dev(h), dev(r), dev(w), hout, dev(W), C, 1, N, K, 1e-5)
+    out_ref, normed = orc.rmsnorm_residual(h, r, w, 1e-5)
+    assert np.array_equal(host(hout), out_ref)
+    assert normwise_rel_err(host(C), orc.matmul_quant("q4_k", normed, W, N, K)) <= TOL
+
+
+@pytest.mark.parametrize("K", SLICE_K)
+@pytest.mark.parametrize("N", [9, 2048])
+def test_slice_gemv_swiglu(orc, N, K):
+    W = quant.synthetic_weights("q4_k", N, K, seed=N + 7)
+    gu = rnd((1, 2 * K), 4 + K, 2.0)  # [gate | up] in one row, ld = 2K
+    C = torch.full((1, N), float("nan"), device="cuda")
+    g = dev(gu)
+    cri.matmul_swiglu("q4_k", g, g[:, K:], 2 * K, dev(W), C, 1, N, K)
+    act = orc.silu_mul(gu[:, :K], gu[:, K:])
+    assert normwise_rel_err(host(C), orc.matmul_quant("q4_k", act, W, N, K)) <= TOL
+
+
+def test_slice_gemv_offset_weights(orc):
+    """A weight pointer 4 bytes past a 16-byte boundary: the kernel's 16-byte loads at dword
+    alignment (a 2-byte offset is not dword aligned and takes another kernel)."""
+    N, K = 300, 2048
+    W = quant.synthetic_weights("q4_k", N, K, seed=9)
+    buf = torch.zeros(W.size + 16, dtype=torch.uint8, device="cuda")
+    buf[4:4 + W.size] = dev(W)
+    A = quant.randn(K, seed=10).reshape(1, K)
+    C = torch.full((1, N), float("nan"), device="cuda")
+    cri.matmul_q4_k(dev(A), buf[4:], C, 1, N, K)
+    assert normwise_rel_err(host(C), orc.matmul_quant("q4_k", A, W, N, K)) <= TOL
