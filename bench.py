@@ -382,7 +382,9 @@ class DecodeStepRig:
                 t = torch.randn(T * HKV * HD, device="cuda", generator=g)
                 torch.cuda.synchronize()
                 hip_memcpy(addr, t.data_ptr(), t.numel() * 4, 3)
-        self.weight_bytes = dec.weight_bytes
+        # the bytes one step reads: every layer's weights and norms, the LM head and the M token rows
+        # (not the whole token table, which the step only gathers from)
+        self.weight_bytes = dec.step_weight_bytes(M)
         self.kv_bytes = 2 * self.LAYERS * T * HKV * HD * 4
         self.ids = torch.from_numpy(rng.integers(0, V, M).astype(np.int32)).cuda()
         self.logits = torch.empty(M, V, device="cuda")
@@ -703,7 +705,9 @@ def main():
         r = DecodeStepRig(args.decode_step)
         ms_step = r.time(samples)
         print(json.dumps({"workload": "decode_step", "M": args.decode_step, "ms_per_step": round(ms_step, 4),
-                          "tokens/s": round(args.decode_step / (ms_step * 1e-3), 1)}))
+                          "tokens/s": round(args.decode_step / (ms_step * 1e-3), 1),
+                          "weight_GB/s": round(r.weight_bytes / (ms_step * 1e-3) / 1e9, 1),
+                          "weight_frac_of_hbm_peak": round(r.weight_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}))
         return
     if args.read_sweep:
         read_sweep()
@@ -817,7 +821,9 @@ def main():
             ms_step = r.time(9)
             details["decode_step_m%d" % m_] = {
                 "tokens/s": round(m_ / (ms_step * 1e-3), 1), "ms_per_step": round(ms_step, 4),
+                "step_weight_bytes": r.weight_bytes,
                 "weight_GB/s": round(r.weight_bytes / (ms_step * 1e-3) / 1e9, 1),
+                "weight_frac_of_hbm_peak": round(r.weight_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 "weight+kv_GB/s": round((r.weight_bytes + r.kv_bytes) / (ms_step * 1e-3) / 1e9, 1),
                 "timing": "median of 9 replays of the captured cri_decoder step at position %d" % r.pos0}
             r.free()

@@ -108,12 +108,14 @@ ABI_SYMBOLS = (
         "cri_decoder_set_embedding",
         "cri_decoder_set_output",
         "cri_decoder_forward",
+        "cri_decoder_forward_taps",
         "cri_decoder_capture",
         "cri_decoder_replay",
         "cri_decoder_set_position",
         "cri_decoder_position",
         "cri_decoder_kv_cache",
         "cri_decoder_weight_bytes",
+        "cri_decoder_step_weight_bytes",
         "cri_stream_read",
         "cri_stream_read_ex",
         "cri_timestamp",
@@ -267,6 +269,8 @@ def lib():
     for n in ("cri_decoder_forward", "cri_decoder_capture"):
         getattr(L, n).argtypes = [vp, vp, i32, vp, vp, vp]
         getattr(L, n).restype = i32
+    L.cri_decoder_forward_taps.argtypes = [vp, vp, i32, vp, vp, vp, vp]
+    L.cri_decoder_forward_taps.restype = i32
     L.cri_decoder_replay.argtypes = [vp, vp]
     L.cri_decoder_replay.restype = i32
     L.cri_decoder_set_position.argtypes = [vp, i32, vp]
@@ -277,6 +281,8 @@ def lib():
     L.cri_decoder_kv_cache.restype = i32
     L.cri_decoder_weight_bytes.argtypes = [vp]
     L.cri_decoder_weight_bytes.restype = ll
+    L.cri_decoder_step_weight_bytes.argtypes = [vp, i32]
+    L.cri_decoder_step_weight_bytes.restype = ll
     L.cri_last_error_string.argtypes = []
     L.cri_last_error_string.restype = ctypes.c_char_p
     L.cri_block_bytes.argtypes = [i32]
@@ -683,6 +689,12 @@ class Decoder:
         _check(lib().cri_decoder_forward(self._h, _ptr(token_ids), M, _ptr(logits), _ptr(next_ids),
                                          _stream(stream)))
 
+    def forward_taps(self, token_ids, M, logits, hidden_taps, next_ids=None, stream=None):
+        """forward() that also writes the residual stream entering each layer and the final
+        norm into hidden_taps (device fp32 [n_layers + 1, M, dim])."""
+        _check(lib().cri_decoder_forward_taps(self._h, _ptr(token_ids), M, _ptr(logits), _ptr(next_ids),
+                                              _ptr(hidden_taps), _stream(stream)))
+
     def capture(self, token_ids, M, logits, next_ids=None, stream=None):
         _check(lib().cri_decoder_capture(self._h, _ptr(token_ids), M, _ptr(logits), _ptr(next_ids),
                                          _stream(stream)))
@@ -706,3 +718,7 @@ class Decoder:
     @property
     def weight_bytes(self):
         return int(lib().cri_decoder_weight_bytes(self._h))
+
+    def step_weight_bytes(self, M):
+        """Weight bytes one step of M tokens reads (M token-table rows, not the whole table)."""
+        return int(lib().cri_decoder_step_weight_bytes(self._h, M))

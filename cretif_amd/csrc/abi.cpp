@@ -275,14 +275,16 @@ int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float*
     if (fmt == cri::kFmtF16 && !aligned(B, 2)) return fail(CRI_ERR_ALIGNMENT, fn, "FP16 B must be 2-byte aligned");
     clear_pending_error();
     if (mode == cri::kActRMSNormS) {  // one token on the batch-1 GEMV only
-        if (M == 1 && cri::detail::slice_gemv_supported(fmt, K, B))
-            return finish_matmul(cri::detail::launch_slice_gemv(mode, fmt, act, B, C, N, K, stream), fn);
         if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
             return finish_matmul(cri::detail::launch_gemv_act(mode, fmt, act, B, C, N, K, stream), fn);
         return fail(CRI_ERR_UNSUPPORTED, fn, "a split residual is taken by the batch-1 GEMV only");
     }
     int rc = cri::detail::kDeclined;
-    if (M == 1 && mode != cri::kActSwiGLU2 && cri::detail::slice_gemv_supported(fmt, K, B))
+    // SwiGLU at one row: the K-sliced GEMV where each lane's activations are its own (K = 8192:
+    // 2048 x 8192 Q4_K 4.97 us against 6.73 on the batch-1 GEMV); it recomputes the prologue in
+    // every lane, so with an RMSNorm prologue (three loads per activation) the batch-1 GEMV, which
+    // stages it once per workgroup, is faster (16384 x 2048: 7.1 against 8.1 us)
+    if (M == 1 && mode == cri::kActSwiGLU && K == 8192 && cri::detail::slice_gemv_supported(fmt, K, B))
         rc = cri::detail::launch_slice_gemv(mode, fmt, act, B, C, N, K, stream);
     if (rc == cri::detail::kDeclined && cri::detail::skinny_supported(fmt, M, K, B))
         rc = cri::detail::launch_skinny_act(mode, fmt, act, B, C, M, N, K, stream, ws, ws_floats, defer, defer_S);

@@ -689,7 +689,8 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
                                  int nchunks, float scale, float* ws, hipStream_t stream) {
     const int D = head_dim, G = n_heads / n_kv_heads, nhq = (G + 3) / 4;
     if (nchunks < 1 || nchunks > dev::kCombineMaxChunks || rows < 1 || rows > 65535) return kDeclined;
-    if (D < 4 || D > kDecodeAttnSplitMaxHeadDim || D % 4 != 0) return kDeclined;  // the record and combine layouts
+    // the record and combine layouts, and the kernels' 16-byte loads of Q rows (ldq floats apart), K and V
+    if (!decode_attention_split_supported(Q, K, V, D) || ldq % 4 != 0) return kDeclined;
     const long blocks = static_cast<long>(n_kv_heads) * nhq * nchunks;
     if (blocks > 0x7FFFFFFFL) return kDeclined;
     const float qscale = scale * 1.44269504088896341f;

@@ -201,14 +201,23 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     rope_ = Tensor::from_host(rot.data(), {static_cast<int64_t>(rot.size())});
 }
 
-DecodeStep::~DecodeStep() {
-    if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
-    if (graph_) (void)hipGraphDestroy(graph_);
+DecodeStep::~DecodeStep() { drop_graph(); }
+
+void DecodeStep::drop_graph() {
+    if (graph_exec_) {
+        (void)hipDeviceSynchronize();  // a replay still running keeps its launch; the buffers may go after it
+        (void)hipGraphExecDestroy(graph_exec_);
+        graph_exec_ = nullptr;
+    }
+    if (graph_) {
+        (void)hipGraphDestroy(graph_);
+        graph_ = nullptr;
+    }
+    graph_m_ = 0;
 }
 
 void DecodeStep::set_layer(int li, const LayerWeightsRef& w) {
     if (li < 0 || li >= cfg_.n_layers) throw std::out_of_range("DecodeStep::set_layer: layer out of range");
-    Layer& L = *layers_[li];
     const int64_t D = cfg_.dim, F = cfg_.intermediate_size, QD = q_dim_, KVD = kv_dim_;
     check_k(w.q.format, D, "q");
     check_k(w.k.format, D, "k");
@@ -217,6 +226,10 @@ void DecodeStep::set_layer(int li, const LayerWeightsRef& w) {
     check_k(w.gate.format, D, "gate");
     check_k(w.up.format, D, "up");
     check_k(w.down.format, F, "down");
+    drop_graph();
+    // filled in a new layer; the old one (and its buffers) is replaced only once every copy succeeded
+    auto fresh = std::make_unique<Layer>();
+    Layer& L = *fresh;
     L.attn_norm = Tensor::empty({D});
     L.ffn_norm = Tensor::empty({D});
     copy_in(L.attn_norm.data(), w.attn_norm, D * 4, "attn_norm");
@@ -273,29 +286,35 @@ void DecodeStep::set_layer(int li, const LayerWeightsRef& w) {
     L.down = Tensor::empty({D, F}, dtype_of(L.down_fmt));
     copy_in(L.down.data(), w.down.data, L.down.size_bytes(), "down");
     L.set = true;
+    layers_[li] = std::move(fresh);
 }
 
 void DecodeStep::set_token_embedding(const WeightRef& table) {
     if (table.format != WeightFormat::FP32) check_k(table.format, cfg_.dim, "token embedding");
+    drop_graph();
+    Tensor t = Tensor::empty({static_cast<int64_t>(cfg_.vocab_size), static_cast<int64_t>(cfg_.dim)},
+                             dtype_of(table.format));
+    copy_in(t.data(), table.data, t.size_bytes(), "token embedding");
+    tok_table_ = std::move(t);
     tok_fmt_ = table.format;
-    tok_table_ = Tensor::empty({static_cast<int64_t>(cfg_.vocab_size), static_cast<int64_t>(cfg_.dim)},
-                               dtype_of(tok_fmt_));
-    copy_in(tok_table_.data(), table.data, tok_table_.size_bytes(), "token embedding");
     tok_set_ = true;
 }
 
 void DecodeStep::set_output(const float* output_norm, const WeightRef* lm_head) {
-    out_norm_ = Tensor::empty({static_cast<int64_t>(cfg_.dim)});
-    copy_in(out_norm_.data(), output_norm, static_cast<size_t>(cfg_.dim) * 4, "output_norm");
-    lm_tied_ = lm_head == nullptr;
-    lm_head_ = Tensor();
-    if (!lm_tied_) {
-        if (lm_head->format != WeightFormat::FP32) check_k(lm_head->format, cfg_.dim, "lm_head");
+    if (lm_head && lm_head->format != WeightFormat::FP32) check_k(lm_head->format, cfg_.dim, "lm_head");
+    drop_graph();
+    Tensor norm = Tensor::empty({static_cast<int64_t>(cfg_.dim)});
+    copy_in(norm.data(), output_norm, static_cast<size_t>(cfg_.dim) * 4, "output_norm");
+    Tensor head;
+    if (lm_head) {
+        head = Tensor::empty({static_cast<int64_t>(cfg_.vocab_size), static_cast<int64_t>(cfg_.dim)},
+                             dtype_of(lm_head->format));
+        copy_in(head.data(), lm_head->data, head.size_bytes(), "lm_head");
         lm_fmt_ = lm_head->format;
-        lm_head_ = Tensor::empty({static_cast<int64_t>(cfg_.vocab_size), static_cast<int64_t>(cfg_.dim)},
-                                 dtype_of(lm_fmt_));
-        copy_in(lm_head_.data(), lm_head->data, lm_head_.size_bytes(), "lm_head");
     }
+    out_norm_ = std::move(norm);
+    lm_head_ = std::move(head);
+    lm_tied_ = lm_head == nullptr;
     out_set_ = true;
 }
 
@@ -316,12 +335,34 @@ float* DecodeStep::v_cache(int layer) {
     return v_cache_.data_as<float>() + static_cast<int64_t>(layer) * cfg_.max_seq_len * kv_dim_;
 }
 
-size_t DecodeStep::weight_bytes() const {
-    size_t n = tok_table_.size_bytes() + out_norm_.size_bytes() + lm_head_.size_bytes();
+namespace {
+// device bytes a tensor holds (an unset Tensor reports a one-element shape but holds nothing)
+size_t held_bytes(const Tensor& t) { return t.data() ? t.size_bytes() : 0; }
+}  // namespace
+
+size_t DecodeStep::step_weight_bytes(int M) const {
+    size_t n = held_bytes(out_norm_);
+    if (lm_tied_) {
+        n += held_bytes(tok_table_);  // the LM head reads the whole table, the token rows among it
+    } else {
+        n += held_bytes(lm_head_);
+        const int rows = std::max(0, std::min(M, cfg_.vocab_size));
+        n += static_cast<size_t>(rows) * (tok_fmt_ == WeightFormat::FP32 ? static_cast<size_t>(cfg_.dim) * 4
+                                                                          : row_bytes(tok_fmt_, cfg_.dim));
+    }
     for (const auto& L : layers_)
         for (const Tensor* t : {&L->attn_norm, &L->ffn_norm, &L->qkv, &L->q, &L->k, &L->v, &L->o, &L->gu, &L->gate,
                                 &L->up, &L->down})
-            n += t->size_bytes();
+            n += held_bytes(*t);
+    return n;
+}
+
+size_t DecodeStep::weight_bytes() const {
+    size_t n = held_bytes(tok_table_) + held_bytes(out_norm_) + held_bytes(lm_head_);
+    for (const auto& L : layers_)
+        for (const Tensor* t : {&L->attn_norm, &L->ffn_norm, &L->qkv, &L->q, &L->k, &L->v, &L->o, &L->gu, &L->gate,
+                                &L->up, &L->down})
+            n += held_bytes(*t);
     return n;
 }
 
@@ -581,7 +622,7 @@ void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res,
     res_part_count_ = 0;
 }
 
-void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s) {
+void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s, float* taps) {
     const int D = cfg_.dim, V = cfg_.vocab_size;
     const float eps = cfg_.rms_norm_eps;
     // token rows straight from the table in its own format (the reference's Embedding::forward
@@ -592,11 +633,22 @@ void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next
     const float* res = nullptr;  // residual still to be added to hidden[cur]
     res_splits_ = 0;
     res_part_count_ = 0;
+    // the residual stream entering layer i (i = n_layers: the final norm): hidden + the pending residual
+    auto tap = [&](int i) {
+        if (!taps) return;
+        const cri::SplitSums r = res_splits_ ? residual_sums(res_parts_.data_as<float>(), D, res_splits_, nullptr, D)
+                                             : residual_sums(nullptr, 0, 0, res, D);
+        check_status(cri::detail::launch_hidden_tap(hid_[cur].data_as<float>(), r,
+                                                    taps + static_cast<long>(i) * M * D, M, D, s),
+                     "layer tap");
+    };
     for (int li = 0; li < cfg_.n_layers; ++li) {
         Layer& L = *layers_[li];
+        tap(li);
         attn_block(L, li, M, cur, res, s);
         ffn_block(L, li, M, cur, res, s);
     }
+    tap(cfg_.n_layers);
     // final RMSNorm(hidden + ffn_out) and the LM head
     const Tensor& W = lm_tied_ ? tok_table_ : lm_head_;
     const WeightFormat wf = lm_tied_ ? tok_fmt_ : lm_fmt_;
@@ -636,18 +688,31 @@ void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next
         check_status(cri::detail::launch_pos_add(pos, M, s), "position update");
 }
 
-void DecodeStep::forward(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s) {
+void DecodeStep::check_call(const int32_t* ids, int M, float* logits, int32_t* next_ids, const char* what) const {
     check_ready();
+    const std::string fn = std::string("DecodeStep::") + what + ": ";
     if (M < 1 || M > cfg_.max_batch)
-        throw std::invalid_argument("DecodeStep::forward: M = " + std::to_string(M) + " outside [1, max_batch = " +
+        throw std::invalid_argument(fn + "M = " + std::to_string(M) + " outside [1, max_batch = " +
                                     std::to_string(cfg_.max_batch) + "]");
-    if (!ids || !logits) throw std::invalid_argument("DecodeStep::forward: null token_ids or logits");
+    if (!ids || !logits) throw std::invalid_argument(fn + "null token_ids or logits");
     if (!aligned4(ids) || !aligned4(logits) || !aligned4(next_ids))
-        throw std::invalid_argument("DecodeStep::forward: token_ids, logits and next_ids must be 4-byte aligned");
+        throw std::invalid_argument(fn + "token_ids, logits and next_ids must be 4-byte aligned");
     if (pos_host_ + M > cfg_.max_seq_len)  // ref:src/model.cu:845-851
-        throw std::overflow_error("DecodeStep::forward: would exceed max sequence length (" +
-                                  std::to_string(pos_host_ + M) + " > " + std::to_string(cfg_.max_seq_len) + ")");
+        throw std::overflow_error(fn + "would exceed max sequence length (" + std::to_string(pos_host_ + M) + " > " +
+                                  std::to_string(cfg_.max_seq_len) + ")");
+}
+
+void DecodeStep::forward(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s) {
+    check_call(ids, M, logits, next_ids, "forward");
     enqueue(ids, M, logits, next_ids, s);
+    pos_host_ += M;
+}
+
+void DecodeStep::forward_taps(const int32_t* ids, int M, float* logits, int32_t* next_ids, float* taps,
+                              hipStream_t s) {
+    check_call(ids, M, logits, next_ids, "forward_taps");
+    if (!taps || !aligned4(taps)) throw std::invalid_argument("DecodeStep::forward_taps: null or unaligned hidden_taps");
+    enqueue(ids, M, logits, next_ids, s, taps);
     pos_host_ += M;
 }
 
@@ -658,15 +723,7 @@ void DecodeStep::capture(const int32_t* ids, int M, float* logits, int32_t* next
     if (!ids || !logits) throw std::invalid_argument("DecodeStep::capture: null token_ids or logits");
     if (!aligned4(ids) || !aligned4(logits) || !aligned4(next_ids))
         throw std::invalid_argument("DecodeStep::capture: token_ids, logits and next_ids must be 4-byte aligned");
-    if (graph_exec_) {
-        (void)hipGraphExecDestroy(graph_exec_);
-        graph_exec_ = nullptr;
-    }
-    if (graph_) {
-        (void)hipGraphDestroy(graph_);
-        graph_ = nullptr;
-    }
-    graph_m_ = 0;
+    drop_graph();
     CUINFER_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     try {
         enqueue(ids, M, logits, next_ids, s);
@@ -814,6 +871,13 @@ int cri_decoder_forward(cri_decoder* d, const int* token_ids, int M, float* logi
     return guarded(fn, [&] { d->step.forward(token_ids, M, logits, next_ids, s); });
 }
 
+int cri_decoder_forward_taps(cri_decoder* d, const int* token_ids, int M, float* logits, int* next_ids,
+                             float* hidden_taps, hipStream_t s) {
+    const char* fn = "cri_decoder_forward_taps";
+    if (!d) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null decoder");
+    return guarded(fn, [&] { d->step.forward_taps(token_ids, M, logits, next_ids, hidden_taps, s); });
+}
+
 int cri_decoder_capture(cri_decoder* d, const int* token_ids, int M, float* logits, int* next_ids, hipStream_t s) {
     const char* fn = "cri_decoder_capture";
     if (!d) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null decoder");
@@ -845,6 +909,11 @@ int cri_decoder_kv_cache(cri_decoder* d, int layer, float** k, float** v) {
 
 long long cri_decoder_weight_bytes(const cri_decoder* d) {
     return d ? static_cast<long long>(d->step.weight_bytes()) : CRI_ERR_INVALID_ARGUMENT;
+}
+
+long long cri_decoder_step_weight_bytes(const cri_decoder* d, int M) {
+    if (!d || M < 1) return CRI_ERR_INVALID_ARGUMENT;
+    return static_cast<long long>(d->step.step_weight_bytes(M));
 }
 
 }  // extern "C"

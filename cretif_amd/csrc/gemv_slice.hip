@@ -1,5 +1,6 @@
 // gemv_slice.hip -- batch-1 GEMV y[N] = W[N,K] x[K] with K sliced over the four waves of a
-// workgroup, for Q4_K weights (the decode GEMVs of a Q4_K model and the C ABI's M = 1 case).
+// workgroup, for Q4_K weights: the C ABI's M = 1 case (plain activations, and SwiGLU ones at
+// K = 8192, the FFN down projection).
 //
 // Replaces the M == 1 case of ref:src/kernels/matmul_quant.cu:309-397 (one 32x32 thread
 // block per 32 outputs, 31/32 of the lanes idle at M = 1).
@@ -18,23 +19,21 @@
 //   * every weight load of the wave is issued at kernel entry, before the activation loads
 //     (which are L2 hits and would otherwise delay the HBM requests behind them), two row
 //     steps ahead of them so the first steps' decode can start while later rows stream in;
-//   * the arguments a weight address needs (W, row bytes, N) are plain scalars in the
-//     first kernel-argument dwords, which the hardware preloads into SGPRs: no weight load
-//     waits on a kernel-argument fetch, and the kernel reads no hidden argument (blockDim,
-//     gridDim) at all.
+//   * every argument is a plain scalar in the first kernel-argument dwords, which the
+//     hardware preloads into SGPRs: no load waits on a kernel-argument fetch (an aggregate
+//     argument is fetched with scalar loads), and the kernel reads no hidden argument
+//     (blockDim, gridDim) at all.
 // Per piece a lane loads the 16-byte super-block header (d, dmin, 12 scale bytes; the 8 lanes
 // of one super-block read the same 16 bytes in one instruction) and its 16 quant bytes, both
 // 16-byte aligned; consecutive lanes read consecutive quant bytes.
 //
-// MODE (see ActIn): kActPlain, kActSwiGLU, kActRMSNorm, kActRMSNormS; the RMSNorm row
-// factor multiplies the finished sum (each wave adds the squares of its slice, the four
-// parts are added in wave order).  ROPE: the fused q/k/v projection of one token with the
-// rotation and the KV-cache append in the epilogue (RopeOut; rows come in even/odd pairs in
-// one wave of the final reduction).
+// MODE (see ActIn): kActPlain or kActSwiGLU.  Each lane computes the prologue of its own 32
+// activations, so at L < 64 lanes per row the 64 / L row groups of a wave compute the same
+// values; with an RMSNorm prologue (three loads per activation, a workgroup reduction) that
+// costs more than staging once per workgroup, and the batch-1 GEMV of gemv.hip takes those.
 #include "act.hpp"
 #include "common.hpp"
 #include "internal.hpp"
-#include "rope.hpp"
 
 namespace cri {
 namespace dev {
@@ -102,24 +101,26 @@ struct SliceQ4K {
 constexpr int kSliceWaves = 4;   // waves per workgroup, one K slice each
 constexpr int kSliceXAfter = 2;  // row steps whose weight loads go before the activation loads
 
-template <class F, int LG, int IT, int MODE, bool ROPE>
+// The prologue's pointers and integers are separate scalar arguments (16 dwords up to kn), all
+// preloaded into SGPRs: an aggregate argument is fetched with scalar loads, and activation loads
+// waiting on that fetch would hold back the weight loads issued after them.
+template <class F, int LG, int IT, int MODE>
 __global__ __launch_bounds__(64 * kSliceWaves) void slice_gemv_kernel(const uint8_t* __restrict__ W,
                                                                       float* __restrict__ y,
-                                                                      const float* __restrict__ xa_ptr, int N,
-                                                                      int row_bytes, const ActIn Pin,
-                                                                      const RopeOut R) {
+                                                                      const float* __restrict__ a,
+                                                                      const float* __restrict__ b, int N,
+                                                                      int row_bytes) {
+    static_assert(MODE == kActPlain || MODE == kActSwiGLU, "plain or SwiGLU prologue");
     constexpr int L = 1 << LG, RPI = 64 / L, RW = IT * RPI;  // lanes per row, rows per step, rows per workgroup
     constexpr int K = kSliceWaves * L * 32;
-    constexpr bool kRms = MODE == kActRMSNorm || MODE == kActRMSNormS;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int sub = lane & (L - 1), rsub = lane >> LG;
     const int p = wv * L + sub;  // piece index along the row
     const int row0 = blockIdx.x * RW;
 
-    ActIn P = Pin;
-    if constexpr (MODE == kActPlain) P.a = xa_ptr;
+    const ActIn P{a, b, nullptr, nullptr, 0, 0.0f};  // lda is not read: one activation row
     float xa[16], xb[16];
-    float ss = 0.0f;
+    float ss = 0.0f;  // (unused without RMSNorm)
     auto xload = [&]() {
         const int k0 = F::x_first(p);
         ActRaw<MODE> ra[4], rb[4];
@@ -128,12 +129,10 @@ __global__ __launch_bounds__(64 * kSliceWaves) void slice_gemv_kernel(const uint
             act_load<MODE>(ra[v], P, 0, k0 + 4 * v, P.lda);
             act_load<MODE>(rb[v], P, 0, k0 + 32 + 4 * v, P.lda);
         }
-        // the hidden state is written by workgroup 0's first row group (each element once)
-        const bool wh = blockIdx.x == 0 && rsub == 0;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const f32x4 a = act_finish<MODE>(ra[v], P, 0, k0 + 4 * v, K, ss, wh);
-            const f32x4 b = act_finish<MODE>(rb[v], P, 0, k0 + 32 + 4 * v, K, ss, wh);
+            const f32x4 a = act_finish<MODE>(ra[v], P, 0, k0 + 4 * v, K, ss, false);
+            const f32x4 b = act_finish<MODE>(rb[v], P, 0, k0 + 32 + 4 * v, K, ss, false);
             xa[4 * v] = a.x; xa[4 * v + 1] = a.y; xa[4 * v + 2] = a.z; xa[4 * v + 3] = a.w;
             xb[4 * v] = b.x; xb[4 * v + 1] = b.y; xb[4 * v + 2] = b.z; xb[4 * v + 3] = b.w;
         }
@@ -159,33 +158,16 @@ __global__ __launch_bounds__(64 * kSliceWaves) void slice_gemv_kernel(const uint
     for (int it = 0; it < IT; ++it) acc[it] = group_sum_t<LG>(F::dot(buf[it], xa, xb, sa, sb, p));
 
     __shared__ float red[kSliceWaves][RW];
-    __shared__ float ssq[kSliceWaves];
 #pragma unroll
     for (int it = 0; it < IT; ++it)
         if (sub == 0) red[wv][it * RPI + rsub] = acc[it];
-    if constexpr (kRms) {
-        ss = group_sum_t<LG>(ss);  // the wave's slice (the row groups hold the same activations)
-        if (lane == 0) ssq[wv] = ss;
-    }
     __syncthreads();
     if (threadIdx.x < RW) {
         const int t = threadIdx.x;
         float v = red[0][t];
 #pragma unroll
         for (int w = 1; w < kSliceWaves; ++w) v += red[w][t];  // in wave order
-        if constexpr (kRms) {
-            float q = ssq[0];
-#pragma unroll
-            for (int w = 1; w < kSliceWaves; ++w) q += ssq[w];
-            v *= rms_factor(q, K, P.eps);
-        }
-        const int r = row0 + t;
-        if constexpr (ROPE) {
-            const float vp = __shfl_xor(v, 1);  // row r ^ 1 (RW is even and row0 a multiple of RW)
-            if (r < N) rope_out(R, y, r, v, vp);
-        } else {
-            if (r < N) y[r] = v;
-        }
+        if (row0 + t < N) y[row0 + t] = v;
     }
 }
 
@@ -217,33 +199,33 @@ int slice_steps(int N, int LG) {
     return it;
 }
 
-template <class F, int LG, int IT, int MODE, bool ROPE>
-int launch_slice_t(const ActIn& act, const void* W, float* y, int N, int K, const RopeOut& rope, hipStream_t s) {
+template <class F, int LG, int IT, int MODE>
+int launch_slice_t(const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
     constexpr int RW = IT * (64 >> LG);
     const int blocks = (N + RW - 1) / RW;
     const int rbytes = static_cast<int>(cri::row_bytes(kFmtQ4_K, K));
-    hipLaunchKernelGGL((dev::slice_gemv_kernel<F, LG, IT, MODE, ROPE>), dim3(blocks), dim3(64 * dev::kSliceWaves), 0,
-                       s, static_cast<const uint8_t*>(W), y, act.a, N, rbytes, act, rope);
+    hipLaunchKernelGGL((dev::slice_gemv_kernel<F, LG, IT, MODE>), dim3(blocks), dim3(64 * dev::kSliceWaves), 0, s,
+                       static_cast<const uint8_t*>(W), y, act.a, act.b, N, rbytes);
     return 0;
 }
 
-template <class F, int LG, int MODE, bool ROPE>
-int launch_slice_it(const ActIn& act, const void* W, float* y, int N, int K, const RopeOut& rope, hipStream_t s) {
+template <class F, int LG, int MODE>
+int launch_slice_it(const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
     switch (slice_steps(N, LG)) {
-        case 8: return launch_slice_t<F, LG, 8, MODE, ROPE>(act, W, y, N, K, rope, s);
-        case 4: return launch_slice_t<F, LG, 4, MODE, ROPE>(act, W, y, N, K, rope, s);
-        case 2: return launch_slice_t<F, LG, 2, MODE, ROPE>(act, W, y, N, K, rope, s);
-        default: return launch_slice_t<F, LG, 1, MODE, ROPE>(act, W, y, N, K, rope, s);
+        case 8: return launch_slice_t<F, LG, 8, MODE>(act, W, y, N, K, s);
+        case 4: return launch_slice_t<F, LG, 4, MODE>(act, W, y, N, K, s);
+        case 2: return launch_slice_t<F, LG, 2, MODE>(act, W, y, N, K, s);
+        default: return launch_slice_t<F, LG, 1, MODE>(act, W, y, N, K, s);
     }
 }
 
-template <int MODE, bool ROPE>
-int launch_slice_m(const ActIn& act, const void* W, float* y, int N, int K, const RopeOut& rope, hipStream_t s) {
+template <int MODE>
+int launch_slice_m(const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
     switch (slice_lg(K)) {
-        case 3: return launch_slice_it<dev::SliceQ4K, 3, MODE, ROPE>(act, W, y, N, K, rope, s);
-        case 4: return launch_slice_it<dev::SliceQ4K, 4, MODE, ROPE>(act, W, y, N, K, rope, s);
-        case 5: return launch_slice_it<dev::SliceQ4K, 5, MODE, ROPE>(act, W, y, N, K, rope, s);
-        case 6: return launch_slice_it<dev::SliceQ4K, 6, MODE, ROPE>(act, W, y, N, K, rope, s);
+        case 3: return launch_slice_it<dev::SliceQ4K, 3, MODE>(act, W, y, N, K, s);
+        case 4: return launch_slice_it<dev::SliceQ4K, 4, MODE>(act, W, y, N, K, s);
+        case 5: return launch_slice_it<dev::SliceQ4K, 5, MODE>(act, W, y, N, K, s);
+        case 6: return launch_slice_it<dev::SliceQ4K, 6, MODE>(act, W, y, N, K, s);
     }
     return kDeclined;
 }
@@ -256,24 +238,13 @@ bool slice_gemv_supported(int fmt, int K, const void* W) {
 
 int launch_slice_gemv(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
     if (!slice_gemv_supported(fmt, K, W)) return kDeclined;
-    const RopeOut none{};
     switch (mode) {
-        case kActPlain: return launch_slice_m<kActPlain, false>(act, W, y, N, K, none, s);
-        case kActSwiGLU: return launch_slice_m<kActSwiGLU, false>(act, W, y, N, K, none, s);
-        case kActRMSNorm: return launch_slice_m<kActRMSNorm, false>(act, W, y, N, K, none, s);
-        case kActRMSNormS: return launch_slice_m<kActRMSNormS, false>(act, W, y, N, K, none, s);
+        case kActPlain: return launch_slice_m<kActPlain>(act, W, y, N, K, s);
+        case kActSwiGLU:
+            // the up rows ld floats after the gate rows: the kernel reads one row, so ld is not needed
+            return launch_slice_m<kActSwiGLU>(act, W, y, N, K, s);
     }
     return kDeclined;
-}
-
-int launch_slice_gemv_rope(const ActIn& act, const void* W, float* q_out, int N, int K, const RopeOut& rope,
-                           hipStream_t s, bool split_res) {
-    if (!slice_gemv_supported(kFmtQ4_K, K, W)) return kDeclined;
-    if (rope.qd % 2 || rope.kvd % 2 || rope.half < 1 || rope.qd % (2 * rope.half) || rope.kvd % (2 * rope.half) ||
-        N != rope.qd + 2 * rope.kvd)
-        return kDeclined;
-    if (split_res) return launch_slice_m<kActRMSNormS, true>(act, W, q_out, N, K, rope, s);
-    return launch_slice_m<kActRMSNorm, true>(act, W, q_out, N, K, rope, s);
 }
 
 }  // namespace detail

@@ -117,13 +117,9 @@ int launch_gemv_rope(int fmt, const ActIn& act, const void* W, float* q_out, int
                      hipStream_t stream, bool split_res = false);
 
 // batch-1 Q4_K GEMV with K sliced over the four waves of a workgroup (gemv_slice.hip), for K in
-// {1024, 2048, 4096, 8192} and dword-aligned weights; plain, SwiGLU, RMSNorm or split-residual
-// RMSNorm prologue (kDeclined otherwise)
+// {1024, 2048, 4096, 8192} and dword-aligned weights; plain or SwiGLU prologue (kDeclined otherwise)
 bool slice_gemv_supported(int fmt, int K, const void* W);
 int launch_slice_gemv(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t stream);
-// the same with the fused q/k/v projection's RoPE + cache-append epilogue (as launch_gemv_rope)
-int launch_slice_gemv_rope(const ActIn& act, const void* W, float* q_out, int N, int K, const RopeOut& rope,
-                           hipStream_t stream, bool split_res = false);
 
 // 1 <= M <= 16 fused dequant matmul on the matrix cores (mfma_skinny.hip)
 bool skinny_supported(int fmt, int M, int K, const void* B);
@@ -257,6 +253,9 @@ int launch_argmax_rows(const float* logits, long ld, int rows, int n, int* out, 
 // *pos += delta / *pos = value
 int launch_pos_add(int* pos, int delta, hipStream_t stream);
 int launch_pos_set(int* pos, int value, hipStream_t stream);
+// out[rows, n] = h + the pending residual r (r.S partial sums r.stride floats apart, rows r.N
+// floats apart, added in split order; r.S = 0: none): a step's layer taps
+int launch_hidden_tap(const float* h, const SplitSums& r, float* out, int rows, int n, hipStream_t stream);
 
 }  // namespace detail
 }  // namespace cri

@@ -250,9 +250,9 @@ struct PQ8_0 {
 // K / 256 is odd).  The copy reads 13 dword-aligned 16-byte pieces from the
 // dword boundary at or below the super-block plus the dword after each piece,
 // and stores the pieces shifted into place (v_alignbyte), so LDS holds super-block
-// bytes 0 .. 207 at offsets 0 .. 207 (the last piece's final two bytes, sc[14]
-// and sc[15] after a 2-byte shift, are not kept); a tail dword {sc[14], sc[15],
-// d} read with two 16-bit loads sits after the wave's 32 rows.  Every byte read lies inside
+// bytes 0 .. 207 (sc[12..15] at 204 .. 207) at offsets 0 .. 207 for either shift; d
+// (bytes 208, 209) lies past the copied area, so a tail dword {sc[14], sc[15], d}
+// read with two 16-bit loads sits after the wave's 32 rows.  Every byte read lies inside
 // the super-block or the 2 bytes before it, which are the previous super-block's
 // (a super-block at the buffer's dword-aligned start has no shift).  Weights are
 // rounded twice: fp16(d * sc), then (q - 32) times it.

@@ -182,6 +182,23 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const float
     }
 }
 
+// The residual stream entering a layer, for a step's layer taps: out = h + (the pending
+// residual: its partial sums added in split order, as the next RMSNorm prologue adds them).
+__global__ __launch_bounds__(256) void hidden_tap_kernel(const float* __restrict__ h, const SplitSums r,
+                                                         float* __restrict__ out, int rows, int n) {
+    const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= static_cast<long>(rows) * n) return;
+    float v = h[i];
+    if (r.S) {
+        const long row = i / n, col = i - row * n;
+        const float* src = r.part + row * r.N + col;
+        float t = src[0];
+        for (int s = 1; s < r.S; ++s) t += src[s * r.stride];
+        v += t;
+    }
+    out[i] = v;
+}
+
 __global__ void pos_update_kernel(int* pos, int value, int add) {
     if (threadIdx.x == 0) *pos = add ? *pos + value : value;
 }
@@ -220,6 +237,14 @@ int launch_argmax_rows(const float* logits, long ld, int rows, int n, int* out, 
 
 int launch_pos_add(int* pos, int delta, hipStream_t stream) {
     hipLaunchKernelGGL(dev::pos_update_kernel, dim3(1), dim3(64), 0, stream, pos, delta, 1);
+    return 0;
+}
+
+int launch_hidden_tap(const float* h, const SplitSums& r, float* out, int rows, int n, hipStream_t stream) {
+    const long total = static_cast<long>(rows) * n;
+    if (total <= 0) return 0;
+    hipLaunchKernelGGL(dev::hidden_tap_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream,
+                       h, r, out, rows, n);
     return 0;
 }
 

@@ -273,6 +273,14 @@ int cri_decoder_forward(cri_decoder* dec, const int* token_ids, int M, float* lo
                         hipStream_t stream);
 /* capture the same call as one HIP graph on a non-null stream (nothing runs), and replay it:
  * each replay is one more step of M tokens; next_ids == token_ids generates greedily */
+/* cri_decoder_forward that also writes the residual stream entering each layer and the final
+ * norm: hidden_taps (device fp32 [n_layers + 1, M, dim]) slice i = the hidden state layer i
+ * reads (slice n_layers: the final RMSNorm's input).  Same kernels as cri_decoder_forward plus
+ * one small kernel per slice; for checking a step layer by layer.  Has no counterpart in the
+ * reference (its forward keeps no per-layer state). */
+int cri_decoder_forward_taps(cri_decoder* dec, const int* token_ids, int M, float* logits, int* next_ids,
+                             float* hidden_taps, hipStream_t stream);
+/* any cri_decoder_set_* call discards a captured graph (replay then fails until the next capture) */
 int cri_decoder_capture(cri_decoder* dec, const int* token_ids, int M, float* logits, int* next_ids,
                         hipStream_t stream);
 int cri_decoder_replay(cri_decoder* dec, hipStream_t stream);
@@ -282,6 +290,9 @@ int cri_decoder_position(const cri_decoder* dec);
 /* the layer's K and V cache, [max_seq_len, n_kv_heads, head_dim] fp32 device memory */
 int cri_decoder_kv_cache(cri_decoder* dec, int layer, float** k_cache, float** v_cache);
 long long cri_decoder_weight_bytes(const cri_decoder* dec);
+/* weight bytes one step of M tokens reads: every layer's matrices and norms, the final norm and
+ * LM head, and M token-table rows (the whole table when the head is tied to it) */
+long long cri_decoder_step_weight_bytes(const cri_decoder* dec, int M);
 
 /* ---- diagnostics ---------------------------------------------------------- */
 

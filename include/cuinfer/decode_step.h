@@ -80,6 +80,10 @@ public:
     DecodeStep(const DecodeStep&) = delete;
     DecodeStep& operator=(const DecodeStep&) = delete;
 
+    // The setters copy into new buffers and swap them in only when every copy succeeded (a
+    // throw leaves the earlier tensors in place), and every setter discards a captured graph
+    // (it holds the old buffers' addresses and kernel choices): replay() then throws until
+    // capture() runs again.
     void set_layer(int layer, const LayerWeightsRef& w);
     // token embedding table [vocab, dim]: FP32 or any matmul format
     void set_token_embedding(const WeightRef& table);
@@ -93,6 +97,13 @@ public:
     // [M, vocab]); next_ids (device int32 [M], may be null) receives the
     // argmax of each logits row.  Enqueued on `stream`; advances position().
     void forward(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, hipStream_t stream = 0);
+    // forward() that also writes the residual stream entering each layer and the final norm:
+    // hidden_taps (device fp32 [n_layers + 1, M, dim]) slice i = the hidden state layer i
+    // reads (slice n_layers: the one the final RMSNorm reads), each added up from its pending
+    // residual the way the next RMSNorm adds it.  The same kernels run as in forward(), plus
+    // one small kernel per slice; for checking a step layer by layer.
+    void forward_taps(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, float* hidden_taps,
+                      hipStream_t stream = 0);
 
     // Captures forward(token_ids, M, logits, next_ids) on `stream` (not the
     // null stream) as one HIP graph, replacing any earlier capture; nothing
@@ -109,13 +120,19 @@ public:
     float* k_cache(int layer);  // [max_seq_len, n_kv_heads, head_dim]
     float* v_cache(int layer);
     const DecodeStepConfig& config() const { return cfg_; }
-    size_t weight_bytes() const;
+    size_t weight_bytes() const;  // every weight and norm byte held on the device
+    // the weight bytes one step of M tokens reads: every layer's matrices and norms, the final
+    // norm and LM head, and M rows of the token table (all of it when the head is tied to it)
+    size_t step_weight_bytes(int M) const;
     int captured_batch() const { return graph_m_; }
 
 private:
     struct Layer;
-    void enqueue(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, hipStream_t stream);
+    void enqueue(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, hipStream_t stream,
+                 float* taps = nullptr);
     void check_ready() const;
+    void check_call(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, const char* what) const;
+    void drop_graph();
     void attn_block(Layer& L, int li, int M, int& cur, const float*& res, hipStream_t s);
     void ffn_block(Layer& L, int li, int M, int& cur, const float*& res, hipStream_t s);
     // the consumer of layer li's FFN output (the next q/k/v or the LM head) is a batch-1 GEMV

@@ -223,6 +223,67 @@ def argmax(x):
     return int(lib().orc_argmax(_p(x), x.size))
 
 
+def _mm(w, x, N, K):
+    fmt, data = w
+    return matmul_quant_mt(fmt, x, data, N, K)
+
+
+def embed(model, ids):
+    """The token rows of the step's input (ref:src/embedding.cu:237-263 reads an FP32 table; a
+    quantized table's row is its blocks dequantized: dequantize + gather)."""
+    V, dim = model["vocab"], model["dim"]
+    tfmt, table = model["tok"]
+    if tfmt == "fp32":
+        return _f32(np.asarray(table, np.float32).reshape(V, dim)[list(ids)])
+    rb = dim // BLOCK_ELEMS[tfmt] * BLOCK_BYTES[tfmt]
+    t = _u8(table)
+    return np.stack([dequantize(tfmt, t[i * rb:(i + 1) * rb], dim) for i in ids])
+
+
+def decode_layer(model, i, hidden, normed, pos, k_cache, v_cache):
+    """Layer i of the reference's quantized forward pass (ref:src/model.cu:887-1019) on the
+    residual stream `hidden` [M, dim] and its RMSNorm `normed` (with layer i's attn_norm), at
+    positions pos .. pos + M - 1.  k_cache / v_cache: this layer's [max_seq, n_kv_heads,
+    head_dim] arrays, appended to in place.  Returns (hidden + attention + FFN output: the
+    stream entering layer i + 1, before its norm; the FFN output)."""
+    H, Hkv, D = model["n_heads"], model["n_kv_heads"], model["head_dim"]
+    dim, F = model["dim"], model["ffn"]
+    eps, theta = model["eps"], model["theta"]
+    M = hidden.shape[0]
+    qd, kvd = H * D, Hkv * D
+    L = model["layers"][i]
+    scale = np.float32(1.0) / np.float32(np.sqrt(np.float32(D)))
+    q = _mm(L["q"], normed, qd, dim)  # ref:src/model.cu:910-918
+    k = _mm(L["k"], normed, kvd, dim)
+    v = _mm(L["v"], normed, kvd, dim)
+    for t in range(M):  # ref:src/model.cu:921-926
+        q[t] = rope(q[t], pos + t, D, H, theta)
+        k[t] = rope(k[t], pos + t, D, Hkv, theta)
+    k_cache[pos:pos + M] = k.reshape(M, Hkv, D)  # KVCache::append, ref:src/kv_cache.cu:157-211
+    v_cache[pos:pos + M] = v.reshape(M, Hkv, D)
+    ctx = np.stack([decode_attention(q[t], k_cache, v_cache, H, Hkv, D, pos + t + 1, scale)
+                    for t in range(M)])  # row t sees positions <= pos + t (ref:src/attention.cu:60-75)
+    attn_out = _mm(L["o"], ctx, dim, qd)
+    hidden, normed = rmsnorm_residual(hidden, attn_out, L["ffn_norm"], eps)  # ref:src/model.cu:963-967
+    gate = _mm(L["gate"], normed, F, dim)  # ref:src/model.cu:986-994
+    up = _mm(L["up"], normed, F, dim)
+    act = silu_mul(gate, up)  # ref:src/model.cu:996-997
+    ffn_out = _mm(L["down"], act, dim, F)
+    return hidden, ffn_out
+
+
+def lm_head(model, normed):
+    """Logits of the final-normed rows (ref:src/model.cu:1023-1037; a tied FP32 table through
+    matmul_transposed_b, ref:src/model.cu:1027-1029) and their argmax ids."""
+    V, dim = model["vocab"], model["dim"]
+    lm = model["lm"] if model["lm"] is not None else model["tok"]
+    if lm[0] == "fp32":
+        logits = matmul_transposed_b(normed, np.asarray(lm[1], np.float32).reshape(V, dim))
+    else:
+        logits = _mm(lm, normed, V, dim)
+    return logits, np.array([argmax(r) for r in logits], np.int32)
+
+
 def decode_step(model, ids, pos, k_cache, v_cache):
     """One forward of the tokens `ids` at positions pos .. pos + M - 1, composed from
     the oracle's functions in the order of the reference's quantized forward pass
@@ -232,52 +293,16 @@ def decode_step(model, ids, pos, k_cache, v_cache):
     gate, up, down), 'out_norm' and 'lm' ((fmt, bytes), or None for a head tied to
     the token table).  k_cache / v_cache: one [max_seq, n_kv_heads, head_dim] fp32
     array per layer, appended to in place.  Returns (logits [M, vocab], argmax ids)."""
-    H, Hkv, D = model["n_heads"], model["n_kv_heads"], model["head_dim"]
-    dim, F, V = model["dim"], model["ffn"], model["vocab"]
-    eps, theta = model["eps"], model["theta"]
-    M = len(ids)
-    qd, kvd = H * D, Hkv * D
-
-    def mm(w, x, N, K):
-        fmt, data = w
-        return matmul_quant_mt(fmt, x, data, N, K)
-
-    tfmt, table = model["tok"]
-    if tfmt == "fp32":
-        hidden = _f32(np.asarray(table, np.float32).reshape(V, dim)[list(ids)])
-    else:  # the row's blocks dequantized: dequantize + gather
-        rb = dim // BLOCK_ELEMS[tfmt] * BLOCK_BYTES[tfmt]
-        t = _u8(table)
-        hidden = np.stack([dequantize(tfmt, t[i * rb:(i + 1) * rb], dim) for i in ids])
+    eps = model["eps"]
     layers = model["layers"]
+    hidden = embed(model, ids)
     # first layer's standalone RMSNorm (ref:src/model.cu:882-885)
     hidden, normed = rmsnorm_residual(hidden, None, layers[0]["attn_norm"], eps)
-    scale = np.float32(1.0) / np.float32(np.sqrt(np.float32(D)))
-    for i, L in enumerate(layers):
-        q = mm(L["q"], normed, qd, dim)  # ref:src/model.cu:910-918
-        k = mm(L["k"], normed, kvd, dim)
-        v = mm(L["v"], normed, kvd, dim)
-        for t in range(M):  # ref:src/model.cu:921-926
-            q[t] = rope(q[t], pos + t, D, H, theta)
-            k[t] = rope(k[t], pos + t, D, Hkv, theta)
-        k_cache[i][pos:pos + M] = k.reshape(M, Hkv, D)  # KVCache::append, ref:src/kv_cache.cu:157-211
-        v_cache[i][pos:pos + M] = v.reshape(M, Hkv, D)
-        ctx = np.stack([decode_attention(q[t], k_cache[i], v_cache[i], H, Hkv, D, pos + t + 1, scale)
-                        for t in range(M)])  # row t sees positions <= pos + t (ref:src/attention.cu:60-75)
-        attn_out = mm(L["o"], ctx, dim, qd)
-        hidden, normed = rmsnorm_residual(hidden, attn_out, L["ffn_norm"], eps)  # ref:src/model.cu:963-967
-        gate = mm(L["gate"], normed, F, dim)  # ref:src/model.cu:986-994
-        up = mm(L["up"], normed, F, dim)
-        act = silu_mul(gate, up)  # ref:src/model.cu:996-997
-        ffn_out = mm(L["down"], act, dim, F)
+    for i in range(len(layers)):
+        hidden, ffn_out = decode_layer(model, i, hidden, normed, pos, k_cache[i], v_cache[i])
         nxt = layers[i + 1]["attn_norm"] if i + 1 < len(layers) else model["out_norm"]
         hidden, normed = rmsnorm_residual(hidden, ffn_out, nxt, eps)  # ref:src/model.cu:1008-1018
-    lm = model["lm"] if model["lm"] is not None else model["tok"]
-    if lm[0] == "fp32":  # tied FP32 table, ref:src/model.cu:1027-1029
-        logits = matmul_transposed_b(normed, np.asarray(lm[1], np.float32).reshape(V, dim))
-    else:
-        logits = mm(lm, normed, V, dim)
-    return logits, np.array([argmax(r) for r in logits], np.int32)
+    return lm_head(model, normed)
 
 
 # ---------------------------------------------------------------- quantizers

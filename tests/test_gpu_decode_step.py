@@ -333,3 +333,65 @@ def test_decoder_errors():
         d.set_position(9)
     d.set_position(0)
     torch.cuda.synchronize()
+
+
+def test_setters_drop_the_captured_graph_and_keep_old_weights_on_failure():
+    # every setter discards a captured graph (it holds the old buffers and kernel choices), and a
+    # set_layer that fails part way (a null matrix after the others were copied) leaves the old
+    # layer in place: the next step gives the same logits bit for bit
+    m = make_model(2, dim=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=300, seed=41,
+                   big_tables=False)
+    dec = make_decoder(m, max_seq=64)
+    kc, vc = random_cache(m, 64, 42)
+    ids = torch.tensor([5, 17], dtype=torch.int32, device="cuda")
+    a = torch.empty(2, m["vocab"], device="cuda")
+    load_cache(dec, kc, vc)
+    dec.set_position(10)
+    dec.forward(ids, 2, a)
+    before = a.cpu().numpy().copy()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        dec.capture(ids, 2, a, None, stream=s)
+        dec.set_position(10, stream=s)
+        dec.replay(stream=s)
+    s.synchronize()
+    L = m["layers"][1]
+    mats = {k: L[k] for k in ("q", "k", "v", "o", "gate", "up", "down")}
+    dec.set_layer(1, L["attn_norm"], L["ffn_norm"], **mats)
+    with pytest.raises(cri.CretifError):
+        dec.replay()  # discarded by set_layer
+    with pytest.raises(cri.CretifError):
+        dec.set_layer(1, L["attn_norm"], L["ffn_norm"], **dict(mats, down=(mats["down"][0], None)))
+    for setter in (lambda: dec.set_embedding(*m["tok"]), lambda: dec.set_output(m["out_norm"], m["lm"])):
+        with torch.cuda.stream(s):
+            dec.capture(ids, 2, a, None, stream=s)
+        setter()
+        with pytest.raises(cri.CretifError):
+            dec.replay()
+    load_cache(dec, kc, vc)
+    dec.set_position(10)
+    dec.forward(ids, 2, a)
+    assert np.array_equal(a.cpu().numpy().view(np.uint32), before.view(np.uint32))
+
+
+@pytest.mark.parametrize("dim,M", [(4096, 1), (5120, 4), (5120, 12), (4352, 1), (4352, 3)])
+def test_step_wide_models(orc, dim, M):
+    # branches the Llama-3.2-1B shapes do not reach: a 4096-wide model at one token (the fused
+    # q/k/v GEMV with RoPE on the K-sliced kernel), widths past 4096 at 2..16 tokens (the q/k/v
+    # partial sums added up by RoPE, the two-way gate/up SwiGLU on the skinny kernel's own sums
+    # of squares), and a width the K-sliced and 32-lane RoPE GEMVs decline (4352 = 17 x 256) at
+    # one token (the RMSNorm GEMV, then the RoPE kernel) and at three
+    m = make_model(1, dim=dim, n_heads=dim // 64, n_kv_heads=4, head_dim=64, ffn=2 * dim, vocab=700, seed=dim + M,
+                   big_tables=False)
+    dec = make_decoder(m, max_seq=128)
+    kc, vc = random_cache(m, 128, dim)
+    load_cache(dec, kc, vc)
+    pos = 50
+    ids = np.random.default_rng(dim + M).integers(0, m["vocab"], M).astype(np.int32)
+    logits = torch.empty(M, m["vocab"], device="cuda")
+    dec.set_position(pos)
+    dec.forward(torch.from_numpy(ids).cuda(), M, logits)
+    ref, _ = orc.decode_step(m, list(ids), pos, kc, vc)
+    err = normwise_rel_err(logits.cpu().numpy(), ref)
+    print("wide-model step dim=%d M=%d: normwise err %.2e" % (dim, M, err))
+    assert err <= TOL
