@@ -622,6 +622,36 @@ def cpu_baseline(fmt, N, K, budget_s=12.0):
     }
 
 
+def cpu_baseline_prefill(fmt, M, N, K, cols=64, budget_s=6.0):
+    """The reference's CPU path for a BASELINE config-4 prefill GEMM (M activation rows, weights
+    [N, K]) on a column sample: the first `cols` output columns for all M rows, single-threaded,
+    median of >= 3 calls (ref:tests/test_matmul_quant.cu:30-41 restated in oracle/oracle.c)."""
+    import oracle as orc
+    from cretif_amd import quant
+
+    w = quant.synthetic_weights(fmt, cols, K, seed=9)
+    x = quant.randn(M * K, seed=10).reshape(M, K)
+    calls = []
+    t0 = time.perf_counter()
+    while True:
+        t = time.perf_counter()
+        orc.matmul_quant(fmt, x, w, cols, K)
+        calls.append(time.perf_counter() - t)
+        el = time.perf_counter() - t0
+        if el >= budget_s and len(calls) >= 3:
+            break
+    per_call = float(np.median(calls))
+    return {
+        "value": round(2.0 * M * cols * K / per_call / 1e9, 3),
+        "unit": "GFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": "%s prefill GEMM M=%d, %d of %d output columns x K=%d, median of %d calls over %.1f s "
+        "(oracle/oracle.c, gcc -O2 -ffp-contract=off, 1 thread; host %s)" % (
+            fmt, M, cols, N, K, len(calls), el, cpu_model()),
+    }
+
+
 def cpu_model():
     """The host CPU's model name (from /proc/cpuinfo), else the platform's machine string."""
     try:
@@ -856,6 +886,11 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(fmt, N, K)
+        if not args.no_details:
+            # the CPU path for the metric's other half (the Q8_0 GEMV) and for config 4 (prefill), beside
+            # the GPU lines in details
+            details["cpu_baseline_q8_0_gemv"] = cpu_baseline("q8_0", 8192, 2048, budget_s=6.0)
+            details["cpu_baseline_q4_k_prefill"] = cpu_baseline_prefill("q4_k", 512, 8192, 2048)
     if details:
         line["details"] = details
     print(json.dumps(line))
