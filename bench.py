@@ -357,7 +357,7 @@ class DecodeStepRig:
 
     LAYERS, D, H, HKV, HD, FF, VOCAB, T = 16, 2048, 32, 8, 64, 8192, 128256, 2048
 
-    def __init__(self, M, seed=1100):
+    def __init__(self, M, seed=1100, capture=True):
         import torch
 
         import cretif_amd as cri
@@ -368,7 +368,8 @@ class DecodeStepRig:
                   "up": (FF, D), "down": (D, FF)}
         w = {n: ("q4_k", tiled_weights("q4_k", r, c, seed + i)) for i, (n, (r, c)) in enumerate(shapes.items())}
         rng = np.random.default_rng(seed)
-        self.dec = dec = cri.Decoder(self.LAYERS, D, H, HKV, HD, FF, V, T, max_batch=16, rope_theta=500000.0)
+        self.dec = dec = cri.Decoder(self.LAYERS, D, H, HKV, HD, FF, V, T, max_batch=max(16, M),
+                                     rope_theta=500000.0)
         for li in range(self.LAYERS):
             dec.set_layer(li, (1 + 0.1 * rng.standard_normal(D)).astype(np.float32),
                           (1 + 0.1 * rng.standard_normal(D)).astype(np.float32), **w)
@@ -392,7 +393,25 @@ class DecodeStepRig:
         self.stream = torch.cuda.Stream()
         self.pos0 = T - M
         torch.cuda.synchronize()
-        dec.capture(self.ids, M, self.logits, self.next_ids, stream=self.stream)
+        if capture:
+            dec.capture(self.ids, M, self.logits, self.next_ids, stream=self.stream)
+
+    def prompt_samples(self, samples=5, warmup=1):
+        """ms of each of `samples` eager steps of the M tokens at position 0 (a prompt into an empty
+        cache: the attention spans only the positions the prompt sees)."""
+        import torch
+
+        s = self.stream
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(samples)]
+        for i in range(warmup + samples):
+            self.dec.set_position(0, stream=s)
+            if i >= warmup:
+                ev[i - warmup][0].record(s)
+            self.dec.forward(self.ids, self.M, self.logits, self.next_ids, stream=s)
+            if i >= warmup:
+                ev[i - warmup][1].record(s)
+        torch.cuda.synchronize()
+        return [a.elapsed_time(b) for a, b in ev]
 
     def samples(self, samples=9, warmup=3):
         """ms of each of `samples` replays at position 2048 - M."""
@@ -686,6 +705,8 @@ def main():
                     help="only time one GEMV workload (for profiling) and print its figures")
     ap.add_argument("--decode-step", type=int, default=None, metavar="M",
                     help="only time the synthetic Llama-3.2-1B decode step for M tokens (for profiling)")
+    ap.add_argument("--prompt", type=int, default=None, metavar="M",
+                    help="time an M-token prompt (eager steps at position 0) through the 16-layer decode step")
     ap.add_argument("--attention", default=None, choices=["plain", "ws"],
                     help="only time the fused decode attention at 2048 positions (for profiling)")
     ap.add_argument("--launch-floor", action="store_true",
@@ -738,6 +759,12 @@ def main():
                           "tokens/s": round(args.decode_step / (ms_step * 1e-3), 1),
                           "weight_GB/s": round(r.weight_bytes / (ms_step * 1e-3) / 1e9, 1),
                           "weight_frac_of_hbm_peak": round(r.weight_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}))
+        return
+    if args.prompt:
+        r = DecodeStepRig(args.prompt, capture=False)
+        ms = float(np.median(r.prompt_samples(samples)))
+        print(json.dumps({"workload": "prompt", "M": args.prompt, "ms_per_prompt": round(ms, 4),
+                          "prompt_tokens/s": round(args.prompt / (ms * 1e-3), 1)}))
         return
     if args.read_sweep:
         read_sweep()
@@ -858,6 +885,14 @@ def main():
                 "timing": "median of 9 replays of the captured cri_decoder step at position %d" % r.pos0}
             r.free()
             torch.cuda.empty_cache()
+        # a 512-token prompt (BASELINE config 4's M) through the same step: the prefill GEMMs and the
+        # reference's prefill attention on batched_matmul_gqa, eager steps at position 0
+        r = DecodeStepRig(512, capture=False)
+        ms = float(np.median(r.prompt_samples(5)))
+        details["prompt_m512"] = {"prompt_tokens/s": round(512 / (ms * 1e-3), 1), "ms_per_prompt": round(ms, 4),
+                                  "timing": "median of 5 eager cri_decoder steps of 512 tokens at position 0"}
+        r.free()
+        torch.cuda.empty_cache()
 
     line = {
         "metric": "weight GB/s (% of HBM peak) for Q4_K/Q8_0 decode GEMV; prefill GEMM TFLOP/s",

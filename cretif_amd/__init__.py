@@ -39,6 +39,8 @@ __all__ = [
     "batched_matmul_gqa",
     "fused_decode_attention",
     "fused_decode_attention_ws",
+    "prefill_attention",
+    "prefill_attention_workspace_bytes",
     "fused_decode_attention_noalloc",
     "decode_attention_workspace_size",
     "matmul_rmsnorm",
@@ -78,6 +80,8 @@ ABI_SYMBOLS = (
         "cri_batched_matmul_gqa",
         "cri_fused_decode_attention",
         "cri_fused_decode_attention_ws",
+        "cri_prefill_attention",
+        "cri_prefill_attention_workspace_bytes",
         "cri_fused_decode_attention_noalloc",
         "cri_fused_decode_attention_workspace_size",
         "cri_matmul_rmsnorm",
@@ -208,6 +212,11 @@ def lib():
     L.cri_fused_decode_attention_ws.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp,
                                                  ctypes.c_longlong, vp]
     L.cri_fused_decode_attention_ws.restype = i32
+    L.cri_prefill_attention.argtypes = [vp, i32, vp, vp, vp, i32, i32, i32, i32, i32, ctypes.c_float, vp,
+                                        ctypes.c_longlong, vp]
+    L.cri_prefill_attention.restype = i32
+    L.cri_prefill_attention_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
+    L.cri_prefill_attention_workspace_bytes.restype = ctypes.c_longlong
     L.cri_fused_decode_attention_noalloc.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp]
     L.cri_fused_decode_attention_noalloc.restype = i32
     L.cri_fused_decode_attention_workspace_size.argtypes = [i32, i32, i32, i32]
@@ -414,6 +423,28 @@ def decode_attention_workspace_size(n_heads, n_kv_heads, head_dim, kv_len):
     if n < 0:
         _check(int(n))
     return int(n)
+
+
+def prefill_attention_workspace_bytes(M, n_heads, n_kv_heads, head_dim, kv_len):
+    return int(lib().cri_prefill_attention_workspace_bytes(M, n_heads, n_kv_heads, head_dim, kv_len))
+
+
+def prefill_attention(Q, ldq, K_cache, V_cache, output, M, n_heads, n_kv_heads, head_dim, pos, scale,
+                      workspace=None, workspace_bytes=None, stream=None):
+    """Prompt attention, the reference's prefill flow (ref:src/attention.cu:809-871): M rotated
+    query rows (ldq floats apart) at positions pos .. pos + M - 1 over the [kv_len, n_kv_heads,
+    head_dim] caches, row m attending to positions <= pos + m.  workspace: a device tensor (one is
+    allocated when None)."""
+    need = prefill_attention_workspace_bytes(M, n_heads, n_kv_heads, head_dim, pos + M)
+    if workspace is None:
+        import torch
+
+        workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device="cuda")
+    if workspace_bytes is None:
+        workspace_bytes = workspace.numel() * workspace.element_size()
+    _check(lib().cri_prefill_attention(_ptr(Q), ldq, _ptr(K_cache), _ptr(V_cache), _ptr(output), M, n_heads,
+                                       n_kv_heads, head_dim, pos, float(scale), _ptr(workspace), int(workspace_bytes),
+                                       _stream(stream)))
 
 
 def fused_decode_attention_ws(Q, K_cache, V_cache, output, n_heads, n_kv_heads, head_dim, kv_len, scale,

@@ -10,6 +10,7 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <algorithm>
 #include <string>
 
 #include "internal.hpp"
@@ -447,6 +448,72 @@ int cri_fused_decode_attention_ws(const float* Q, const float* K_cache, const fl
                     "workspace of " + std::to_string(workspace_bytes) + " bytes holds less than one record per head (" +
                         std::to_string(static_cast<long>(n_heads) * (head_dim + 4) * 4) + " bytes)");
     if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
+    return check_launch(fn);
+}
+
+namespace {
+// workspace layout of cri_prefill_attention: the position (16 bytes), then q heads and output heads
+// (n_heads x rows x head_dim each), K^T and V heads (n_kv_heads x T4 x head_dim each), scores
+// (n_heads x rows x T4), for rows = min(M, kPromptRows) and T4 = kv_len rounded up to 4
+struct PrefillWs {
+    long qh, oh, kt, vh, sc, total;  // float offsets after the 16-byte position slot; total bytes
+};
+PrefillWs prefill_ws(int M, int H, int Hkv, int D, int kv_len) {
+    const long rows = std::min(M, cri::detail::kPromptRows), T4 = (static_cast<long>(kv_len) + 3) / 4 * 4;
+    PrefillWs w;
+    w.qh = 0;
+    w.oh = w.qh + H * rows * D;
+    w.kt = w.oh + H * rows * D;
+    w.vh = w.kt + Hkv * T4 * D;
+    w.sc = w.vh + Hkv * T4 * D;
+    w.total = 16 + 4 * (w.sc + H * rows * T4);
+    return w;
+}
+}  // namespace
+
+long long cri_prefill_attention_workspace_bytes(int M, int n_heads, int n_kv_heads, int head_dim, int kv_len) {
+    if (M < 1 || n_heads < 1 || n_kv_heads < 1 || head_dim < 1 || kv_len < 1) return 0;
+    return prefill_ws(M, n_heads, n_kv_heads, head_dim, kv_len).total;
+}
+
+int cri_prefill_attention(const float* Q, int ldq, const float* K_cache, const float* V_cache, float* output, int M,
+                          int n_heads, int n_kv_heads, int head_dim, int pos, float scale, void* workspace,
+                          long long workspace_bytes, hipStream_t s) {
+    const char* fn = "cri_prefill_attention";
+    if (M < 0 || n_heads < 0 || n_kv_heads < 0 || head_dim < 0 || pos < 0 || workspace_bytes < 0)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "negative argument");
+    if (M == 0 || n_heads == 0) return CRI_OK;
+    if (n_kv_heads == 0 || n_heads % n_kv_heads != 0)
+        return fail(CRI_ERR_INVALID_ARGUMENT, fn, "n_heads is not a multiple of n_kv_heads");
+    if (head_dim % 4 != 0 || head_dim < 4 || head_dim > cri::detail::kDecodeAttnSplitMaxHeadDim)
+        return fail(CRI_ERR_UNSUPPORTED, fn, "head_dim must be a multiple of 4 in [4, 128]");
+    if (ldq < n_heads * head_dim || ldq % 4 != 0)
+        return fail(CRI_ERR_SHAPE, fn, "ldq must be a multiple of 4 and at least n_heads * head_dim");
+    if (!Q || !K_cache || !V_cache || !output || !workspace) return fail(CRI_ERR_INVALID_ARGUMENT, fn, "null pointer");
+    if (!aligned(Q, 4) || !aligned(K_cache, 16) || !aligned(V_cache, 16) || !aligned(output, 16) ||
+        !aligned(workspace, 16))
+        return fail(CRI_ERR_ALIGNMENT, fn, "Q must be 4-byte aligned, K_cache, V_cache, output and workspace 16-byte");
+    const long kv_len = static_cast<long>(pos) + M;
+    if (kv_len * n_kv_heads * head_dim > kMaxElems || static_cast<long>(M) * ldq > kMaxElems)
+        return fail(CRI_ERR_SHAPE, fn, "problem too large");
+    const PrefillWs w = prefill_ws(M, n_heads, n_kv_heads, head_dim, static_cast<int>(kv_len));
+    if (workspace_bytes < w.total)
+        return fail(CRI_ERR_SHAPE, fn, "workspace of " + std::to_string(workspace_bytes) + " bytes, " +
+                                           std::to_string(w.total) + " needed");
+    clear_pending_error();
+    int* pos_dev = static_cast<int*>(workspace);
+    float* base = reinterpret_cast<float*>(static_cast<char*>(workspace) + 16);
+    if (cri::detail::launch_pos_set(pos_dev, pos, s) != 0) return fail(CRI_ERR_LAUNCH, fn, "launch failed");
+    const int QD = n_heads * head_dim;
+    for (int m0 = 0; m0 < M; m0 += cri::detail::kPromptRows) {
+        const int mb = std::min(cri::detail::kPromptRows, M - m0);
+        const int T4 = (pos + m0 + mb + 3) / 4 * 4;
+        const int rc = cri::detail::launch_prefill_attention(
+            Q + static_cast<long>(m0) * ldq, ldq, K_cache, V_cache, output + static_cast<long>(m0) * QD, m0, mb,
+            n_heads, n_kv_heads, head_dim, T4, pos_dev, scale, base + w.qh, base + w.kt, base + w.vh, base + w.sc,
+            base + w.oh, s);
+        if (rc != 0) return fail(CRI_ERR_UNSUPPORTED, fn, "no kernel for this shape");
+    }
     return check_launch(fn);
 }
 

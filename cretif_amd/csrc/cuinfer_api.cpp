@@ -72,6 +72,16 @@ void fused_decode_attention(const float* Q, const float* K_cache, const float* V
                                                  scale, s));
 }
 
+void prefill_attention(const float* Q, int ldq, const float* K_cache, const float* V_cache, float* output, int M,
+                       int n_heads, int n_kv_heads, int head_dim, int pos, float scale, hipStream_t stream) {
+    const long long bytes = cri_prefill_attention_workspace_bytes(M, n_heads, n_kv_heads, head_dim, pos + M);
+    Tensor ws = Tensor::empty({std::max<int64_t>(1, (bytes + 3) / 4)});
+    CUINFER_CHECK_CRI(cri_prefill_attention(Q, ldq, K_cache, V_cache, output, M, n_heads, n_kv_heads, head_dim, pos,
+                                            scale, ws.data(), bytes, stream));
+    // the workspace is released when this returns: wait for the kernels that use it
+    CUINFER_CHECK_HIP(hipStreamSynchronize(stream));
+}
+
 // ---------------------------------------------------------------- dispatch
 const char* weight_format_name(WeightFormat fmt) {
     switch (fmt) {

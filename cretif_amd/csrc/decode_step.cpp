@@ -27,6 +27,11 @@ namespace {
 
 // Batches up to this many tokens take the fused RMSNorm / SwiGLU prologues.
 constexpr int kFusedMaxBatch = 16;
+// Larger batches (a prompt) run attention through batched_matmul_gqa in row blocks of
+// cri::detail::kPromptRows rows (the scores workspace holds n_heads x that x max_seq_len floats).
+using cri::detail::kPromptRows;
+
+int round4(int n) { return (n + 3) / 4 * 4; }
 // K parts of the one-token down projection (its partial sums go to the next RMSNorm prologue)
 constexpr int kDownSplits = 4;
 static_assert(kDownSplits <= cri::kResMaxSplits, "the RMSNorm prologue adds up at most kResMaxSplits parts");
@@ -170,9 +175,12 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     act_ = Tensor::empty({MB, static_cast<int64_t>(c.intermediate_size)});
     ffn_out_ = Tensor::empty({MB, static_cast<int64_t>(c.dim)});
     // records for the larger of the one-row and the multi-row chunk counts
+    // (the split attention serves batches of up to kFusedMaxBatch rows; larger ones take the prompt flow)
+    const int64_t arows = std::min<int64_t>(MB, kFusedMaxBatch);
     const int ch1 = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, 1);
-    const int chm = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, MB);
-    attn_ws_ = Tensor::empty({MB * c.n_heads * std::max(ch1, chm) * (c.head_dim + 4)});
+    const int chm = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len,
+                                                              static_cast<int>(arows));
+    attn_ws_ = Tensor::empty({arows * c.n_heads * std::max(ch1, chm) * (c.head_dim + 4)});
     // partial sums of the decode-batch matmuls whose K is split over workgroups
     split_ws_ = Tensor::empty({cri::detail::skinny_workspace_floats(MB, c.dim)});
     // the q/k/v and gate/up projections' partial sums, left for RoPE and the down projection's
@@ -184,6 +192,14 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     argmax_count_ = Tensor::zeros({MB});
     res_parts_ = Tensor::empty({static_cast<int64_t>(cri::kResMaxSplits) * c.dim});
     norm_ss_ = Tensor::zeros({256});
+    if (MB > kFusedMaxBatch) {
+        const int64_t rows = std::min<int64_t>(MB, kPromptRows), T4 = round4(c.max_seq_len);
+        gqa_q_ = Tensor::empty({c.n_heads * rows * c.head_dim});
+        gqa_o_ = Tensor::empty({c.n_heads * rows * c.head_dim});
+        gqa_k_ = Tensor::empty({c.n_kv_heads * T4 * c.head_dim});
+        gqa_v_ = Tensor::empty({c.n_kv_heads * T4 * c.head_dim});
+        gqa_s_ = Tensor::empty({c.n_heads * rows * T4});
+    }
     // RoPE (cos, sin) per (position, pair), ref:src/kernels/elementwise.cu:241-248: the frequency
     // 1 / theta^(2i / head_dim) and the angle pos * freq with the reference's fp32 operations,
     // theta^e, cos and sin in double rounded once to fp32
@@ -461,12 +477,31 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
                      "rope/append");
     // row m attends to positions [0, pos + m] (ref:src/attention.cu:60-75; one token: :410-511)
     const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
-    const int nchunks = cri::detail::decode_attention_rows_chunks(cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim,
-                                                                  cfg_.max_seq_len, M);
-    check_status(cri::detail::launch_decode_attention_rows(q, ldq, k_cache(li), v_cache(li), ctx_.data_as<float>(), QD,
-                                                           M, cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim, pos, 1,
-                                                           nchunks, scale, attn_ws_.data_as<float>(), s),
-                 "attention");
+    if (M > kFusedMaxBatch) {
+        // a prompt: Q K^T and P V through batched_matmul_gqa around a causal softmax, in row blocks
+        // (ref:src/attention.cu:809-871); the products span the cache positions the block can see,
+        // rounded up to a multiple of 4 -- the whole cache when recording a graph, which is then
+        // correct at any position it is replayed at
+        for (int m0 = 0; m0 < M; m0 += kPromptRows) {
+            const int mb = std::min(kPromptRows, M - m0);
+            const int T4 = capturing_ ? round4(cfg_.max_seq_len)
+                                      : std::min(round4(pos_host_ + m0 + mb), round4(cfg_.max_seq_len));
+            check_status(cri::detail::launch_prefill_attention(
+                             q + static_cast<long>(m0) * ldq, ldq, k_cache(li), v_cache(li),
+                             ctx_.data_as<float>() + static_cast<long>(m0) * QD, m0, mb, cfg_.n_heads,
+                             cfg_.n_kv_heads, cfg_.head_dim, T4, pos, scale, gqa_q_.data_as<float>(),
+                             gqa_k_.data_as<float>(), gqa_v_.data_as<float>(), gqa_s_.data_as<float>(),
+                             gqa_o_.data_as<float>(), s),
+                         "prompt attention");
+        }
+    } else {
+        const int nchunks = cri::detail::decode_attention_rows_chunks(cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim,
+                                                                      cfg_.max_seq_len, M);
+        check_status(cri::detail::launch_decode_attention_rows(q, ldq, k_cache(li), v_cache(li), ctx_.data_as<float>(),
+                                                               QD, M, cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim,
+                                                               pos, 1, nchunks, scale, attn_ws_.data_as<float>(), s),
+                     "attention");
+    }
     // (2..16 tokens: its partial sums are left for the FFN's RMSNorm row kernel)
     cri::SplitSums o_sums;
     check_cri(cri::detail::matmul_split_ws(cri_id(L.o_fmt), ctx_.data_as<float>(), L.o.data(),
@@ -725,14 +760,17 @@ void DecodeStep::capture(const int32_t* ids, int M, float* logits, int32_t* next
         throw std::invalid_argument("DecodeStep::capture: token_ids, logits and next_ids must be 4-byte aligned");
     drop_graph();
     CUINFER_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    capturing_ = true;
     try {
         enqueue(ids, M, logits, next_ids, s);
     } catch (...) {
+        capturing_ = false;
         hipGraph_t g = nullptr;
         (void)hipStreamEndCapture(s, &g);
         if (g) (void)hipGraphDestroy(g);
         throw;
     }
+    capturing_ = false;
     CUINFER_CHECK_HIP(hipStreamEndCapture(s, &graph_));
     CUINFER_CHECK_HIP(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
     graph_m_ = M;

@@ -253,6 +253,18 @@ int launch_argmax_rows(const float* logits, long ld, int rows, int n, int* out, 
 // *pos += delta / *pos = value
 int launch_pos_add(int* pos, int delta, hipStream_t stream);
 int launch_pos_set(int* pos, int value, hipStream_t stream);
+// Prompt attention over the [T, Hkv, D] caches through batched_matmul_gqa, as the reference's
+// prefill (ref:src/attention.cu:809-871): q rows [M][ldq] -> ctx rows [M][H D] for the batch rows
+// m0 .. m0 + M - 1 of a step at position *pos (row m0 + m sees cache positions <= *pos + m0 + m).
+// Workspaces: qh and oh H M D floats, kt and vh Hkv D T4, sc H M T4 (T4 % 4 == 0, T4 >= *pos + m0 +
+// M when it runs; cache rows past that are not read into the products).  kDeclined for an
+// unsupported shape.
+int launch_prefill_attention(const float* q, long ldq, const float* kc, const float* vc, float* ctx, int m0, int M,
+                             int H, int Hkv, int D, int T4, const int* pos, float scale, float* qh, float* kt,
+                             float* vh, float* sc, float* oh, hipStream_t stream);
+// rows per launch_prefill_attention call of the C ABI and the decode step (the scores workspace
+// holds n_heads x this many rows x the cache length)
+constexpr int kPromptRows = 512;
 // out[rows, n] = h + the pending residual r (r.S partial sums r.stride floats apart, rows r.N
 // floats apart, added in split order; r.S = 0: none): a step's layer taps
 int launch_hidden_tap(const float* h, const SplitSums& r, float* out, int rows, int n, hipStream_t stream);

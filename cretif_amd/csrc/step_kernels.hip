@@ -182,6 +182,94 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const float
     }
 }
 
+// ---- prompt attention through batched_matmul_gqa (the reference's prefill, ref:src/attention.cu:809-871)
+// Every kernel reads the position from device memory: rows t >= kv_len = pos + M of a cache operand
+// are written as zeros and score columns past row m's causal limit pos + m + 1 are masked, so the
+// padded width T4 (a multiple of 4, >= kv_len) may exceed kv_len -- a captured step uses the cache's
+// full length and stays correct at every position it is replayed at.
+
+// q rows [M][ldq] (head h at columns h D .. h D + D - 1) -> qh [H][M][D] (transpose_seq_heads)
+__global__ __launch_bounds__(256) void heads_from_rows_kernel(const float* __restrict__ q, long ldq,
+                                                              float* __restrict__ qh, int M, int H, int D) {
+    const long i = (static_cast<long>(blockIdx.x) * 256 + threadIdx.x) * 4;  // element of qh
+    if (i >= static_cast<long>(H) * M * D) return;
+    const int d = static_cast<int>(i % D);
+    const long hm = i / D;
+    const int m = static_cast<int>(hm % M), h = static_cast<int>(hm / M);
+    *reinterpret_cast<f32x4*>(qh + i) = ld_f32x4(q + m * ldq + h * D + d);
+}
+
+// o [H][M][D] -> ctx rows [M][H D] (transpose_heads_seq)
+__global__ __launch_bounds__(256) void rows_from_heads_kernel(const float* __restrict__ o, float* __restrict__ ctx,
+                                                              int M, int H, int D) {
+    const long i = (static_cast<long>(blockIdx.x) * 256 + threadIdx.x) * 4;  // element of ctx
+    if (i >= static_cast<long>(H) * M * D) return;
+    const int hd = static_cast<int>(i % (static_cast<long>(H) * D));
+    const int m = static_cast<int>(i / (static_cast<long>(H) * D));
+    const int h = hd / D, d = hd % D;
+    *reinterpret_cast<f32x4*>(ctx + i) = *reinterpret_cast<const f32x4*>(o + (static_cast<long>(h) * M + m) * D + d);
+}
+
+// cache [T][Hkv][D] -> vh [Hkv][T4][D] (rows t >= pos + kv_rows zero)
+__global__ __launch_bounds__(256) void v_heads_kernel(const float* __restrict__ vc, float* __restrict__ vh, int Hkv,
+                                                      int D, int T4, const int* __restrict__ pos, int kv_rows) {
+    const long i = (static_cast<long>(blockIdx.x) * 256 + threadIdx.x) * 4;  // element of vh
+    if (i >= static_cast<long>(Hkv) * T4 * D) return;
+    const int kv_len = *pos + kv_rows;
+    const int d = static_cast<int>(i % D);
+    const long kt = i / D;
+    const int t = static_cast<int>(kt % T4), kv = static_cast<int>(kt / T4);
+    f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (t < kv_len) v = *reinterpret_cast<const f32x4*>(vc + (static_cast<long>(t) * Hkv + kv) * D + d);
+    *reinterpret_cast<f32x4*>(vh + i) = v;
+}
+
+// cache [T][Hkv][D] -> kt [Hkv][D][T4] (transpose_seq_heads + transpose_k; columns t >= pos +
+// kv_rows zero): a 64-position x D tile through LDS per workgroup, read along d and written along t
+__global__ __launch_bounds__(256) void k_transpose_kernel(const float* __restrict__ kc, float* __restrict__ kt,
+                                                          int Hkv, int D, int T4, const int* __restrict__ pos,
+                                                          int kv_rows) {
+    __shared__ float tile[64][detail::kDecodeAttnSplitMaxHeadDim + 1];
+    const int kv = blockIdx.y, t0 = blockIdx.x * 64;
+    const int kv_len = *pos + kv_rows;
+    for (int e = threadIdx.x; e < 64 * D; e += 256) {
+        const int tt = e / D, d = e % D, t = t0 + tt;
+        tile[tt][d] = t < kv_len && t < T4 ? kc[(static_cast<long>(t) * Hkv + kv) * D + d] : 0.0f;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < 64 * D; e += 256) {
+        const int d = e / 64, tt = e % 64, t = t0 + tt;
+        if (t < T4) kt[(static_cast<long>(kv) * D + d) * T4 + t] = tile[tt][d];
+    }
+}
+
+// s [H][M][T4] in place: row (h, m) keeps columns j < pos + m0 + m + 1, scaled (scale) and softmax-ed
+// (max subtracted, exponentiated, divided by the row sum; ref:src/attention.cu:849-855 runs scale,
+// causal_mask and softmax as three kernels), the others set to 0.  One workgroup per row.
+__global__ __launch_bounds__(256) void causal_softmax_kernel(float* __restrict__ s, int M, int T4, float scale,
+                                                             const int* __restrict__ pos, int m0) {
+    __shared__ float red[4];
+    const long row = blockIdx.x;
+    const int m = static_cast<int>(row % M);
+    const int valid = min(*pos + m0 + m + 1, T4);
+    float* r = s + row * T4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < valid; j += 256) mx = fmaxf(mx, r[j] * scale);
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float sum = 0.0f;
+    for (int j = threadIdx.x; j < valid; j += 256) sum += expf(r[j] * scale - mx);
+    sum = group_sum_t<6>(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    const float inv = 1.0f / (((red[0] + red[1]) + red[2]) + red[3]);
+    for (int j = threadIdx.x; j < T4; j += 256) r[j] = j < valid ? expf(r[j] * scale - mx) * inv : 0.0f;
+}
+
 // The residual stream entering a layer, for a step's layer taps: out = h + (the pending
 // residual: its partial sums added in split order, as the next RMSNorm prologue adds them).
 __global__ __launch_bounds__(256) void hidden_tap_kernel(const float* __restrict__ h, const SplitSums r,
@@ -237,6 +325,31 @@ int launch_argmax_rows(const float* logits, long ld, int rows, int n, int* out, 
 
 int launch_pos_add(int* pos, int delta, hipStream_t stream) {
     hipLaunchKernelGGL(dev::pos_update_kernel, dim3(1), dim3(64), 0, stream, pos, delta, 1);
+    return 0;
+}
+
+int launch_prefill_attention(const float* q, long ldq, const float* kc, const float* vc, float* ctx, int m0, int M,
+                             int H, int Hkv, int D, int T4, const int* pos, float scale, float* qh, float* kt,
+                             float* vh, float* sc, float* oh, hipStream_t stream) {
+    if (M < 1 || D % 4 != 0 || D > kDecodeAttnSplitMaxHeadDim || T4 % 4 != 0 || T4 < 4 || H % Hkv != 0 ||
+        ldq % 4 != 0)
+        return kDeclined;
+    auto grid4 = [](long n) { return dim3(static_cast<unsigned>((n / 4 + 255) / 256)); };
+    const long nq = static_cast<long>(H) * M * D;
+    hipLaunchKernelGGL(dev::heads_from_rows_kernel, grid4(nq), dim3(256), 0, stream, q, ldq, qh, M, H, D);
+    hipLaunchKernelGGL(dev::k_transpose_kernel, dim3(static_cast<unsigned>((T4 + 63) / 64), Hkv), dim3(256), 0, stream,
+                       kc, kt, Hkv, D, T4, pos, m0 + M);
+    hipLaunchKernelGGL(dev::v_heads_kernel, grid4(static_cast<long>(Hkv) * T4 * D), dim3(256), 0, stream, vc, vh, Hkv,
+                       D, T4, pos, m0 + M);
+    // scores = Q K^T per KV head, [H][M][T4] (batched_matmul_gqa, ref:src/attention.cu:837-841)
+    int rc = launch_gqa(qh, kt, sc, H, Hkv, M, T4, D, stream);
+    if (rc != 0) return rc;
+    hipLaunchKernelGGL(dev::causal_softmax_kernel, dim3(static_cast<unsigned>(static_cast<long>(H) * M)), dim3(256), 0,
+                       stream, sc, M, T4, scale, pos, m0);
+    // out = P V, [H][M][D] (ref:src/attention.cu:857-861)
+    rc = launch_gqa(sc, vh, oh, H, Hkv, M, D, T4, stream);
+    if (rc != 0) return rc;
+    hipLaunchKernelGGL(dev::rows_from_heads_kernel, grid4(nq), dim3(256), 0, stream, oh, ctx, M, H, D);
     return 0;
 }
 

@@ -138,6 +138,19 @@ int cri_fused_decode_attention_ws(const float* Q, const float* K_cache, const fl
 int cri_fused_decode_attention_noalloc(const float* Q, const float* K_cache, const float* V_cache, float* output,
                                        int n_heads, int n_kv_heads, int head_dim, int kv_len, float scale,
                                        hipStream_t stream);
+/* Prompt attention over the [kv_len, n_kv_heads, head_dim] caches, the reference's prefill flow
+ * (AttentionBlock::forward_from_qkv after the cache append, ref:src/attention.cu:809-871: Q K^T and
+ * P V through batched_matmul_gqa around scale, causal mask and softmax): M query rows (already
+ * rotated) at Q + m * ldq, [n_heads * head_dim] each, at positions pos .. pos + M - 1; row m
+ * attends to cache positions [0, pos + m]; output row m at output + m * n_heads * head_dim.  The
+ * caches must hold rows 0 .. pos + M - 1 (rows past them are never read into the products).
+ * head_dim a multiple of 4 up to 128, ldq a multiple of 4; K_cache, V_cache, output and the
+ * workspace 16-byte aligned; workspace_bytes at least
+ * cri_prefill_attention_workspace_bytes(M, n_heads, n_kv_heads, head_dim, pos + M). */
+int cri_prefill_attention(const float* Q, int ldq, const float* K_cache, const float* V_cache, float* output, int M,
+                          int n_heads, int n_kv_heads, int head_dim, int pos, float scale, void* workspace,
+                          long long workspace_bytes, hipStream_t stream);
+long long cri_prefill_attention_workspace_bytes(int M, int n_heads, int n_kv_heads, int head_dim, int kv_len);
 /* Workspace bytes cri_fused_decode_attention_ws uses for this shape (0 for an
  * empty problem; a negative cri_status for invalid arguments). */
 long long cri_fused_decode_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, int kv_len);

@@ -18,4 +18,11 @@ void batched_matmul_gqa(const float* A, const float* B, float* C, int n_heads, i
 void fused_decode_attention(const float* Q, const float* K_cache, const float* V_cache, float* output, int n_heads,
                             int n_kv_heads, int head_dim, int kv_len, float scale, hipStream_t stream = 0);
 
+// Prompt attention (the prefill branch of ref:src/attention.cu:809-871 after the cache append):
+// M rotated query rows at Q + m * ldq at positions pos .. pos + M - 1, row m attending to cache
+// positions [0, pos + m]; output [M, n_heads * head_dim].  Allocates its workspace for the call
+// (cri_prefill_attention takes a caller's).  Throws std::runtime_error on an unsupported shape.
+void prefill_attention(const float* Q, int ldq, const float* K_cache, const float* V_cache, float* output, int M,
+                       int n_heads, int n_kv_heads, int head_dim, int pos, float scale, hipStream_t stream = 0);
+
 }  // namespace cuinfer

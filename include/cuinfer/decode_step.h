@@ -17,10 +17,12 @@
 //   * for batches of up to 16 tokens the RMSNorm (with the residual add) and
 //     SiLU * up are computed inside the next matmul's activation staging
 //     (matmul_dispatch_rmsnorm / matmul_dispatch_swiglu);
-//   * attention is one split online-softmax kernel for every batch size: row m
-//     of the batch sees the first position() + m + 1 cache positions, which is
-//     the reference's causal mask (ref:src/attention.cu:60-75) for a
-//     multi-token call and its fused decode attention for one token;
+//   * attention is a split online-softmax kernel for batches of up to 16 tokens
+//     and, above that (a prompt), the reference's prefill flow of Q K^T and P V
+//     through batched_matmul_gqa around a causal softmax (ref:src/attention.cu:
+//     809-871); row m of the batch sees the first position() + m + 1 cache
+//     positions, which is the reference's causal mask (ref:src/attention.cu:60-75)
+//     for a multi-token call and its fused decode attention for one token;
 //   * the sequence position lives in device memory and the step's own last
 //     kernel advances it, so a captured step can be replayed for every
 //     following token without being captured again.
@@ -151,6 +153,10 @@ private:
     Tensor k_cache_, v_cache_, pos_dev_;
     Tensor hid_[2], normed_, qkv_, ctx_, attn_out_, ff_, act_, ffn_out_, attn_ws_, split_ws_, defer_ws_;
     Tensor argmax_part_, argmax_count_, rope_;
+    // batches above 16 rows (a prompt): attention through batched_matmul_gqa in row blocks of up to
+    // kPromptRows, on Q / K^T / V / scores / output workspaces (allocated when max_batch > 16)
+    Tensor gqa_q_, gqa_k_, gqa_v_, gqa_s_, gqa_o_;
+    bool capturing_ = false;  // enqueue() is recording a graph: shapes independent of the position
     Tensor res_parts_;    // the down projection's K-split partial sums at one token
     int res_splits_ = 0;  // > 0: the pending residual is that many partial sums in res_parts_
     // 2..16 tokens: the pending residual as the unreduced partial sums of the o projection

@@ -245,3 +245,54 @@ def test_ws_graph_replay(orc):
         g.replay()
         torch.cuda.synchronize()
         assert normwise_rel_err(host(out), ref) <= ATTN_TOL
+
+
+# ---- prompt attention (cri_prefill_attention): the reference's prefill flow, ref:src/attention.cu:809-871
+def _oracle_rows(orc, q, kc, vc, H, Hkv, D, pos, scale):
+    """Row m against the oracle's decode attention over positions [0, pos + m] (threads over rows)."""
+    import concurrent.futures as cf
+
+    with cf.ThreadPoolExecutor(8) as ex:
+        rows = list(ex.map(lambda m: orc.decode_attention(q[m, :H * D], kc, vc, H, Hkv, D, pos + m + 1, scale),
+                           range(q.shape[0])))
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("H,Hkv,D,M,pos", [(32, 8, 64, 17, 0), (32, 8, 64, 64, 100), (32, 8, 64, 512, 0),
+                                           (32, 8, 64, 512, 1400), (32, 8, 64, 600, 37), (4, 2, 128, 100, 30),
+                                           (8, 8, 32, 33, 5)])
+def test_prefill_attention_matches_oracle(orc, H, Hkv, D, M, pos):
+    # Q rows as the fused q/k/v projection leaves them (ldq = q + k + v widths); the cache rows past
+    # pos + M hold NaN, which no product may read; 600 rows run as two row blocks (512 + 88)
+    rng = np.random.default_rng(M + pos + D)
+    ldq = H * D + 2 * Hkv * D
+    q = rng.standard_normal((M, ldq)).astype(np.float32)
+    T = pos + M + 40
+    kc = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    vc = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    kc[pos + M:] = np.nan
+    vc[pos + M:] = np.nan
+    scale = 1.0 / np.sqrt(D)
+    out = torch.full((M, H * D), float("nan"), device="cuda")
+    cri.prefill_attention(dev(q), ldq, dev(kc), dev(vc), out, M, H, Hkv, D, pos, scale)
+    got = host(out)
+    ref = _oracle_rows(orc, q, kc, vc, H, Hkv, D, pos, np.float32(scale))
+    err = normwise_rel_err(got, ref)
+    print("prefill attention H=%d/%d D=%d M=%d pos=%d: %.2e" % (H, Hkv, D, M, pos, err))
+    assert np.isfinite(got).all() and err <= 1e-5
+
+
+def test_prefill_attention_errors():
+    q = torch.zeros(20, 2048, device="cuda")
+    c = torch.zeros(64, 8, 64, device="cuda")
+    out = torch.zeros(20, 2048, device="cuda")
+    ws = torch.zeros(16, device="cuda")
+    with pytest.raises(cri.CretifError):  # workspace too small
+        cri.prefill_attention(q, 2048, c, c, out, 20, 32, 8, 64, 0, 0.125, workspace=ws)
+    with pytest.raises(cri.CretifError):  # ldq below n_heads * head_dim
+        cri.prefill_attention(q, 1024, c, c, out, 20, 32, 8, 64, 0, 0.125)
+    with pytest.raises(cri.CretifError):  # head_dim past the layout
+        cri.prefill_attention(q, 2048, c, c, out, 20, 8, 8, 256, 0, 0.125)
+    with pytest.raises(cri.CretifError):  # misaligned output
+        cri.prefill_attention(q, 2048, c, c, out.view(-1)[1:].view(-1)[:20 * 2047].view(20, 2047), 20, 32, 8, 64, 0,
+                              0.125)

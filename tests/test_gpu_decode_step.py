@@ -395,3 +395,74 @@ def test_step_wide_models(orc, dim, M):
     err = normwise_rel_err(logits.cpu().numpy(), ref)
     print("wide-model step dim=%d M=%d: normwise err %.2e" % (dim, M, err))
     assert err <= TOL
+
+
+@pytest.mark.parametrize("pos", [0, 1000])
+def test_prompt_two_layers_through_gqa(orc, pos):
+    # a 512-token prompt through two full-size Llama-3.2-1B layers: above 16 rows the step runs the
+    # reference's prefill flow (ref:src/attention.cu:809-871), Q K^T and P V on batched_matmul_gqa
+    # around a causal softmax (pinned on its own at 1e-5 in test_gpu_attention.py), with every
+    # projection on the prefill GEMMs (fp16 operands; the stated bar 2e-3).  FP16 weights ~N(0, 0.02):
+    # the random-block Q4_K weights of the other tests are not zero-mean (d sc q - dmin mn is mostly
+    # positive), which gives q and k a large shared component, sharp attention rows, and a softmax
+    # that amplifies the fp16 operand rounding past the bar (~6e-2 at 512 tokens, the same with the
+    # multi-row attention kernel that served prompts before)
+    m = make_model(2, dim=2048, n_heads=32, n_kv_heads=8, head_dim=64, ffn=8192, vocab=2000, seed=61 + pos,
+                   fmts={n: "fp16" for n in ("q", "k", "v", "o", "gate", "up", "down")}, tok="q8_0", lm="fp16",
+                   big_tables=False)
+    dec = make_decoder(m, max_seq=2048, max_batch=512)
+    kc, vc = random_cache(m, 2048, 62 + pos)
+    load_cache(dec, kc, vc)
+    M = 512
+    ids = np.random.default_rng(pos + 3).integers(0, m["vocab"], M).astype(np.int32)
+    logits = torch.empty(M, m["vocab"], device="cuda")
+    dec.set_position(pos)
+    dec.forward(torch.from_numpy(ids).cuda(), M, logits)
+    got = logits.cpu().numpy()
+    ref, _ = orc.decode_step(m, list(ids), pos, kc, vc)
+    err = normwise_rel_err(got, ref)
+    print("prompt M=%d pos=%d: logits normwise err %.2e" % (M, pos, err))
+    assert err <= PREFILL_TOL
+    for i in range(2):
+        ka, va = dec.kv_cache(i)
+        shape = (2048, m["n_kv_heads"], m["head_dim"])
+        gk, gv = from_device(ka, shape), from_device(va, shape)
+        assert normwise_rel_err(gk[pos:pos + M], kc[i][pos:pos + M]) <= PREFILL_TOL + (pos + M) * 2.0 ** -23
+        assert normwise_rel_err(gv[pos:pos + M], vc[i][pos:pos + M]) <= PREFILL_TOL
+
+
+def test_prompt_row_blocks_nan_cache_and_replay(orc):
+    # 600 rows: two row blocks of the prompt flow (512 + 88); cache rows past the step's positions
+    # hold NaN, which no product may read; a graph captured at one position (its products span the
+    # whole cache) and replayed at another equals the eager step there
+    m = make_model(2, dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1024, vocab=900, seed=71,
+                   fmts={n: "fp16" for n in ("q", "k", "v", "o", "gate", "up", "down")}, tok="q8_0", lm="fp16",
+                   big_tables=False)
+    max_seq = 1024
+    dec = make_decoder(m, max_seq=max_seq, max_batch=640)
+    kc, vc = random_cache(m, max_seq, 72)
+    M, pos = 600, 37
+    for arr in kc + vc:
+        arr[pos + M:] = np.nan
+    load_cache(dec, kc, vc)
+    ids = torch.from_numpy(np.random.default_rng(73).integers(0, m["vocab"], M).astype(np.int32)).cuda()
+    a = torch.empty(M, m["vocab"], device="cuda")
+    dec.set_position(pos)
+    dec.forward(ids, M, a)
+    eager = a.cpu().numpy().copy()
+    ref, _ = orc.decode_step(m, list(ids.cpu().numpy()), pos, [k.copy() for k in kc], [v.copy() for v in vc])
+    err = normwise_rel_err(eager, ref)
+    print("prompt M=600 (two row blocks), NaN past the step: normwise err %.2e" % err)
+    assert np.isfinite(eager).all() and err <= PREFILL_TOL
+    # captured at another position, replayed at pos: the same logits (the products span the whole
+    # cache there, with the extra columns masked and the extra rows zero)
+    load_cache(dec, kc, vc)
+    s = torch.cuda.Stream()
+    b = torch.empty(M, m["vocab"], device="cuda")
+    with torch.cuda.stream(s):
+        dec.set_position(200, stream=s)
+        dec.capture(ids, M, b, None, stream=s)
+        dec.set_position(pos, stream=s)
+        dec.replay(stream=s)
+    s.synchronize()
+    assert normwise_rel_err(b.cpu().numpy(), eager) <= 1e-5
