@@ -398,74 +398,85 @@ __global__ __launch_bounds__(256 / HQ) void decode_attn_split_kernel(const float
 
 // ---- multi-row split form on the fp32 matrix cores (head_dim 64) ---------------
 //
-// For a batch of M query rows (consecutive tokens) one wave takes 32 queries
-// -- q = m G + g over the rows m and the G query heads of KV head kvh -- and one
-// chunk of positions, so each K and V row of the chunk is read once for all of
-// them instead of once per row.  Per tile of 32 positions:
-//   * S = Q K^T, 32 x 32, as 32 v_mfma_f32_32x32x2_f32: lane (i, h) holds dims
-//     32 h .. 32 h + 31 of query i, lane (j, h) the same dims of key j, and the
-//     t-th MFMA takes dim 32 h + t from both (fp32 products, fp32 sums);
-//   * causal mask (row m sees positions < Tb + m), online softmax in base 2 per
-//     query row: the row max is a reduction over the 32 lanes of a half-wave,
-//     each lane keeps its partial sum;
-//   * P goes through LDS (32 x 32) to become the A operand of O += P V, two
-//     32 x 32 tiles of output dims, 16 MFMAs each, V read one row per k slot;
-// and the chunk's (max, sum, acc[64]) per (row, head) go to the same records as
-// the per-row kernel, merged by the same combine kernel.  All rows share one
+// For a batch of M query rows (consecutive tokens) one workgroup takes 32
+// queries -- q = m G + g over the rows m and the G query heads of KV head kvh --
+// and one chunk of positions; its kMrWaves waves take the chunk's 32-position
+// tiles in turn (wave w: tiles w, w + kMrWaves, ...), so each K and V row of the
+// chunk is read once for all 32 queries.  The products run transposed, so that a
+// lane owns one query.  Per tile:
+//   * S^T = K Q^T, 32 positions x 32 queries, as 32 v_mfma_f32_32x32x2_f32: the
+//     u-th takes dim 32 h + u from lane (i, h) for key i (A) and for query i (B);
+//     lane (j, h) receives query j's scores at positions 8 (v >> 2) + 4 h + (v & 3),
+//     v = 0..15 (fp32 products, fp32 sums);
+//   * causal mask (query row m sees positions < Tb + m), online softmax in base
+//     2: the query's tile max is over the lane's 16 scores and the other
+//     half-wave's 16, each lane keeps its partial sum;
+//   * O^T += V^T P^T, 64 dims x 32 queries as two 32 x 32 tiles of 16 MFMAs: the
+//     s-th takes position 8 (s >> 2) + 4 h + (s & 3) from lane (i, h), which is
+//     exactly the probability lane (j, h) holds in its register s, so P stays in
+//     registers;
+// then the waves' (max, sum, acc) meet in LDS and the workgroup writes one
+// record per (row, head) -- the per-row kernel's format, merged by the same
+// combine kernel -- adding the waves' parts in wave order.  All rows share one
 // chunk length (from the longest row); chunks past a row's end write empty
-// records.
+// records (max -inf, sum 0).
+//
+// Workgroup order: the query halves of one (KV head, chunk) are consecutive
+// work indices, and when the grid is a multiple of the 8 XCDs each XCD
+// (workgroup id mod 8) takes a contiguous range of work indices, so both halves
+// read the chunk's K and V through the same L2.
 constexpr int kMrD = 64;
-constexpr int kMrPld = 36;  // LDS row stride of the P tile (floats)
+constexpr int kMrWaves = 4;
+constexpr int kMrAld = kMrD + 4;  // LDS row stride of a wave's accumulators (floats)
+constexpr int kXcds = 8;
 
-__global__ __launch_bounds__(64) void decode_attn_mrow_kernel(const float* __restrict__ Q, const float* __restrict__ Kc,
-                                                              const float* __restrict__ Vc, float* __restrict__ ws,
-                                                              int G, int n_kv, int M, const int* __restrict__ kv_dev,
-                                                              int kv0, float qscale, int nchunks, long ldq) {
-    __shared__ __attribute__((aligned(16))) float pt[32 * kMrPld];
+__global__ __launch_bounds__(64 * kMrWaves) void decode_attn_mrow_kernel(
+    const float* __restrict__ Q, const float* __restrict__ Kc, const float* __restrict__ Vc, float* __restrict__ ws,
+    int G, int n_kv, int M, const int* __restrict__ kv_dev, int kv0, float qscale, int nchunks, long ldq) {
+    __shared__ __attribute__((aligned(16))) float acc_s[kMrWaves][32 * kMrAld];
+    __shared__ float mx_s[kMrWaves][32];
+    __shared__ float l_s[kMrWaves][32];
     typedef float mr_f16v __attribute__((ext_vector_type(16)));
-    const int lane = threadIdx.x, i = lane & 31, h = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, i = lane & 31, h = lane >> 5;
     const int nq = M * G, nqh = (nq + 31) / 32;
-    const int qh = blockIdx.x % nqh, c = (blockIdx.x / nqh) % nchunks, kvh = blockIdx.x / (nqh * nchunks);
+    const int nb = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
+    const int wi = nb % kXcds == 0 ? (b % kXcds) * (nb / kXcds) + b / kXcds : b;
+    const int qh = wi % nqh, c = (wi / nqh) % nchunks, kvh = wi / (nqh * nchunks);
     const int H = G * n_kv, kvd = n_kv * kMrD;
     const int Tb = (kv_dev ? *kv_dev : 0) + kv0;  // row m attends to positions [0, Tb + m)
     const int Tmax = Tb + M - 1;
     const int Tc = kSplitTile * ((((Tmax + kSplitTile - 1) / kSplitTile) + nchunks - 1) / nchunks);
     const int t0 = c * Tc, t1 = min(Tmax, t0 + Tc);
 
-    // the lane's query (A operand row i): dims 32 h .. + 31, scaled into base 2
-    float qa[32];
+    // the lane's query (column i of S^T and O^T): row qm, head qg; positions below lim are visible
+    const int q = qh * 32 + i;
+    const bool qok = q < nq;
+    const int qm = qok ? q / G : 0, qg = qok ? q - qm * G : 0;
+    const int lim = qok ? min(Tb + qm, t1) : 0;
+    float qb[32];  // B operand of S^T: dims 32 h .. + 31 of the query, scaled into base 2
     {
-        const int q = qh * 32 + i, m = q / G, g = q - m * G;
-        const bool ok = q < nq;
-        const float* qp = Q + static_cast<long>(ok ? m : 0) * ldq + static_cast<long>(kvh * G + (ok ? g : 0)) * kMrD + 32 * h;
+        const float* qp = Q + static_cast<long>(qm) * ldq + static_cast<long>(kvh * G + qg) * kMrD + 32 * h;
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const f32x4 v = ld_f32x4(qp + 4 * u) * qscale;
-            qa[4 * u] = ok ? v.x : 0.0f;
-            qa[4 * u + 1] = ok ? v.y : 0.0f;
-            qa[4 * u + 2] = ok ? v.z : 0.0f;
-            qa[4 * u + 3] = ok ? v.w : 0.0f;
+            qb[4 * u] = qok ? v.x : 0.0f;
+            qb[4 * u + 1] = qok ? v.y : 0.0f;
+            qb[4 * u + 2] = qok ? v.z : 0.0f;
+            qb[4 * u + 3] = qok ? v.w : 0.0f;
         }
     }
-    // accumulator row v of this lane (S, O layout): query row 8 (v >> 2) + 4 h + (v & 3);
-    // lim: positions below it are visible to that row inside this chunk
-    int lim[16];
-    float mx[16], l[16];
+    float mx = -INFINITY, l = 0.0f;
     mr_f16v o0, o1;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-        const int q = qh * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        lim[v] = q < nq ? min(Tb + q / G, t1) : 0;
-        mx[v] = -INFINITY;
-        l[v] = 0.0f;
         o0[v] = 0.0f;
         o1[v] = 0.0f;
     }
     const float* Kh = Kc + static_cast<long>(kvh) * kMrD;
     const float* Vh = Vc + static_cast<long>(kvh) * kMrD;
 
-    // one tile's operands in registers: keys (B operand column j = i, dims 32 h .. + 31) and
-    // values (B operand of P V: position tb + 16 h + t, dims e 32 + i); past the end: the last key
+    // one tile's operands: key i's dims 32 h .. + 31 (A of S^T) and, for k slot s, dims i and 32 + i of
+    // position 8 (s >> 2) + 4 h + (s & 3) (A of O^T); positions past the end read the last row
     struct Tile {
         f32x4 k[8];
         float v0[16], v1[16];
@@ -475,99 +486,116 @@ __global__ __launch_bounds__(64) void decode_attn_mrow_kernel(const float* __res
 #pragma unroll
         for (int u = 0; u < 8; ++u) T.k[u] = ld_f32x4(kp + 4 * u);
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const float* vp = Vh + static_cast<long>(min(tb + 16 * h + t, Tmax - 1)) * kvd + i;
-            T.v0[t] = vp[0];
-            T.v1[t] = vp[32];
+        for (int s = 0; s < 16; ++s) {
+            const float* vp = Vh + static_cast<long>(min(tb + 8 * (s >> 2) + 4 * h + (s & 3), Tmax - 1)) * kvd + i;
+            T.v0[s] = vp[0];
+            T.v1[s] = vp[32];
         }
     };
     auto run_tile = [&](const Tile& T, int tb) {
-        // two independent chains (even and odd t): half the sequential accumulation depth
-        mr_f16v sa0, sa1;
+        mr_f16v sa, sb;  // two independent chains (even and odd dims)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            sa0[v] = 0.0f;
-            sa1[v] = 0.0f;
+            sa[v] = 0.0f;
+            sb[v] = 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            sa0 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[4 * u], T.k[u].x, sa0, 0, 0, 0);
-            sa1 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[4 * u + 1], T.k[u].y, sa1, 0, 0, 0);
-            sa0 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[4 * u + 2], T.k[u].z, sa0, 0, 0, 0);
-            sa1 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[4 * u + 3], T.k[u].w, sa1, 0, 0, 0);
+            sa = __builtin_amdgcn_mfma_f32_32x32x2f32(T.k[u].x, qb[4 * u], sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_32x32x2f32(T.k[u].y, qb[4 * u + 1], sb, 0, 0, 0);
+            sa = __builtin_amdgcn_mfma_f32_32x32x2f32(T.k[u].z, qb[4 * u + 2], sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_32x32x2f32(T.k[u].w, qb[4 * u + 3], sb, 0, 0, 0);
         }
-        const int pos = tb + i;  // this lane's position (column j = i)
+        float p[16];
+        float tmax = -INFINITY;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const float sv = pos < lim[v] ? sa0[v] + sa1[v] : -INFINITY;
-            float tmax = sv;  // max over the 32 lanes of this half-wave
-            tmax = fmaxf(tmax, dpp<kQuadPerm1032>(tmax));
-            tmax = fmaxf(tmax, dpp<kQuadPerm2301>(tmax));
-            tmax = fmaxf(tmax, dpp<kRowHalfMirror>(tmax));
-            tmax = fmaxf(tmax, dpp<kRowMirror>(tmax));
-            tmax = fmaxf(tmax, swizzle_xor16(tmax));
-            const float mnew = fmaxf(mx[v], tmax);
-            const float cf = mnew == -INFINITY ? 1.0f : exp2f(mx[v] - mnew);
-            const float p = sv == -INFINITY ? 0.0f : exp2f(sv - mnew);
-            mx[v] = mnew;
-            l[v] = __builtin_fmaf(l[v], cf, p);
-            o0[v] *= cf;
-            o1[v] *= cf;
-            pt[(8 * (v >> 2) + 4 * h + (v & 3)) * kMrPld + i] = p;
+            p[v] = tb + 8 * (v >> 2) + 4 * h + (v & 3) < lim ? sa[v] + sb[v] : -INFINITY;
+            tmax = fmaxf(tmax, p[v]);
         }
-        __syncthreads();
-        // P row i, positions 16 h .. + 15 (A operand of P V)
-        f32x4 pa[4];
+        tmax = fmaxf(tmax, shfl_xor32(tmax));  // the query's other 16 positions
+        const float mnew = fmaxf(mx, tmax);
+        const float base = mnew == -INFINITY ? 0.0f : mnew;  // no visible position yet: every factor 0
+        const float cf = __builtin_amdgcn_exp2f(mx - base);
+        mx = mnew;
+        float ps = 0.0f;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) pa[u] = *reinterpret_cast<const f32x4*>(&pt[i * kMrPld + 16 * h + 4 * u]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].x, T.v0[4 * u], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].x, T.v1[4 * u], o1, 0, 0, 0);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].y, T.v0[4 * u + 1], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].y, T.v1[4 * u + 1], o1, 0, 0, 0);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].z, T.v0[4 * u + 2], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].z, T.v1[4 * u + 2], o1, 0, 0, 0);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].w, T.v0[4 * u + 3], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[u].w, T.v1[4 * u + 3], o1, 0, 0, 0);
+        for (int v = 0; v < 16; ++v) {
+            p[v] = __builtin_amdgcn_exp2f(p[v] - base);
+            ps += p[v];
         }
-        __syncthreads();  // the P tile is rewritten by the next tile
+        l = __builtin_fmaf(l, cf, ps);
+        o0 *= cf;
+        o1 *= cf;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(T.v0[s], p[s], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(T.v1[s], p[s], o1, 0, 0, 0);
+        }
     };
-    // the next tile's loads are in flight while the current one is computed; a chunk of one
-    // tile (the decode batch at up to 64 x 32 positions) loads just that tile
-    Tile T0, T1;
-    load_tile(T0, t0);
-    if (t1 - t0 <= kSplitTile) {
-        if (t0 < t1) run_tile(T0, t0);
-    } else if (t1 - t0 <= 2 * kSplitTile) {  // two tiles: both requested before the first is computed
-        load_tile(T1, t0 + kSplitTile);
-        run_tile(T0, t0);
-        run_tile(T1, t0 + kSplitTile);
-    } else {
-        for (int tb = t0; tb < t1; tb += 2 * kSplitTile) {
-            load_tile(T1, tb + kSplitTile);  // past t1: clamped reads, not computed
+    // the wave's tiles: the next one's loads are in flight while the current one is computed
+    constexpr int kStep = kMrWaves * kSplitTile;
+    int tb = t0 + w * kSplitTile;
+    if (tb < t1) {
+        Tile T0, T1;
+        load_tile(T0, tb);
+        while (true) {
+            if (tb + kStep >= t1) {
+                run_tile(T0, tb);
+                break;
+            }
+            load_tile(T1, tb + kStep);
             run_tile(T0, tb);
-            if (tb + kSplitTile >= t1) break;
-            load_tile(T0, tb + 2 * kSplitTile);
-            run_tile(T1, tb + kSplitTile);
+            tb += kStep;
+            if (tb + kStep >= t1) {
+                run_tile(T1, tb);
+                break;
+            }
+            load_tile(T0, tb + kStep);
+            run_tile(T1, tb);
+            tb += kStep;
         }
     }
 
-    // records: (max, sum, acc[64]) per query, the sum over the half-wave's lanes
-    const int stride = kMrD + 4;
+    // the waves meet in LDS: max and sum per query, accumulators per (query, dim)
+    const float lq = l + shfl_xor32(l);
+    if (h == 0) {
+        mx_s[w][i] = mx;
+        l_s[w][i] = lq;
+    }
+    float* a = acc_s[w] + i * kMrAld + 4 * h;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const float lsum = group_sum_t<5>(l[v]);
-        const int q = qh * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (q >= nq) continue;
-        const int m = q / G, g = q - m * G;
-        float* rec = ws + ((static_cast<long>(m) * H + kvh * G + g) * nchunks + c) * stride;
-        rec[4 + i] = o0[v];
-        rec[4 + 32 + i] = o1[v];
-        if (i == 0) {
-            rec[0] = mx[v];
-            rec[1] = lsum;
-        }
+    for (int g = 0; g < 4; ++g) {
+        *reinterpret_cast<f32x4*>(a + 8 * g) = f32x4{o0[4 * g], o0[4 * g + 1], o0[4 * g + 2], o0[4 * g + 3]};
+        *reinterpret_cast<f32x4*>(a + 32 + 8 * g) = f32x4{o1[4 * g], o1[4 * g + 1], o1[4 * g + 2], o1[4 * g + 3]};
+    }
+    __syncthreads();
+    // records: eight threads per query, eight dims each
+    const int rq = tid >> 3, d0 = 8 * (tid & 7), qq = qh * 32 + rq;
+    if (qq >= nq) return;
+    float mw[kMrWaves], Mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kMrWaves; ++u) {
+        mw[u] = mx_s[u][rq];
+        Mx = fmaxf(Mx, mw[u]);
+    }
+    float L = 0.0f;
+    f32x4 r0 = {0.0f, 0.0f, 0.0f, 0.0f}, r1 = r0;
+#pragma unroll
+    for (int u = 0; u < kMrWaves; ++u) {
+        const float f = mw[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[u] - Mx);
+        L = __builtin_fmaf(f, l_s[u][rq], L);
+        const float* src = acc_s[u] + rq * kMrAld + d0;
+        r0 += f * *reinterpret_cast<const f32x4*>(src);
+        r1 += f * *reinterpret_cast<const f32x4*>(src + 4);
+    }
+    const int m = qq / G, g = qq - m * G;
+    float* rec = ws + ((static_cast<long>(m) * H + kvh * G + g) * nchunks + c) * (kMrD + 4);
+    *reinterpret_cast<f32x4*>(rec + 4 + d0) = r0;
+    *reinterpret_cast<f32x4*>(rec + 8 + d0) = r1;
+    if (d0 == 0) {
+        rec[0] = Mx;
+        rec[1] = L;
     }
 }
 
@@ -666,10 +694,10 @@ static int split_chunks(int n_heads, int n_kv_heads, int D, int kv_len, int rows
     return static_cast<int>(nchunks);
 }
 
-// The multi-row (matrix-core) form takes one chunk per 32-position tile, up to
-// kMrowMaxChunks: its waves each take 32 queries, so a decode batch has few of
-// them per chunk and needs the chunks for parallelism.
-constexpr int kMrowMaxChunks = 64;
+// The multi-row (matrix-core) form gives each workgroup's kMrWaves waves one
+// 32-position tile each per chunk, up to kMrowMaxChunks chunks (at 2048 positions:
+// 16 chunks x 8 KV heads x 2 query halves = 256 workgroups for a batch of 16).
+constexpr int kMrowMaxChunks = 16;
 
 static bool use_mrow(int rows, int head_dim) { return head_dim == dev::kMrD && rows >= kMrowMinRows; }
 
@@ -697,10 +725,10 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
     if (use_mrow(rows, D)) {
         // several query rows: the rows share each chunk's K / V reads on the matrix cores
         const long nqh = (static_cast<long>(rows) * G + 31) / 32;
-        const long waves = static_cast<long>(n_kv_heads) * nchunks * nqh;
-        if (waves > 0x7FFFFFFFL) return kDeclined;
-        hipLaunchKernelGGL(dev::decode_attn_mrow_kernel, dim3(static_cast<unsigned>(waves)), dim3(64), 0, stream, Q, K,
-                           V, ws, G, n_kv_heads, rows, kv_dev, kv0, qscale, nchunks, ldq);
+        const long wgs = static_cast<long>(n_kv_heads) * nchunks * nqh;
+        if (wgs > 0x7FFFFFFFL) return kDeclined;
+        hipLaunchKernelGGL(dev::decode_attn_mrow_kernel, dim3(static_cast<unsigned>(wgs)), dim3(64 * dev::kMrWaves), 0,
+                           stream, Q, K, V, ws, G, n_kv_heads, rows, kv_dev, kv0, qscale, nchunks, ldq);
         hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads, static_cast<unsigned>(rows)),
                            dim3(64 * dev::kCombineWaves), 0, stream, ws, out, D, nchunks, ldo);
         return 0;
@@ -713,14 +741,15 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
         hipLaunchKernelGGL((dev::decode_attn_split_kernel<kSplitHeadsPerWave, 8>), grid, dim3(256 / kSplitHeadsPerWave),
                            0, stream, Q, K, V, ws, G, n_kv_heads * D, D, kv_dev, kv0, qscale, nchunks, nhq, ldq);
     hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads, static_cast<unsigned>(rows)),
-                       dim3(64 * dev::kCombineWaves), 0, stream, ws, out, D, nchunks, ldo);
+                           dim3(64 * dev::kCombineWaves), 0, stream, ws, out, D, nchunks, ldo);
     return 0;
 }
 
 int decode_attention_rows_chunks(int n_heads, int n_kv_heads, int head_dim, int max_kv_len, int rows) {
     if (use_mrow(rows, head_dim)) {
         const int tiles = (max_kv_len + dev::kSplitTile - 1) / dev::kSplitTile;
-        return tiles < 1 ? 1 : (tiles < kMrowMaxChunks ? tiles : kMrowMaxChunks);
+        const int per_wg = (tiles + dev::kMrWaves - 1) / dev::kMrWaves;
+        return per_wg < 1 ? 1 : (per_wg < kMrowMaxChunks ? per_wg : kMrowMaxChunks);
     }
     return split_chunks(n_heads, n_kv_heads, head_dim, max_kv_len, 1, -1);
 }

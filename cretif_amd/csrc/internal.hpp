@@ -220,8 +220,9 @@ int launch_decode_attention_split(const float* Q, const float* K, const float* V
 // the split form for `rows` consecutive query tokens (row m at Q + m*ldq, output at out + m*ldo):
 // row m attends to the first kv0 + m positions (+ *kv_dev when kv_dev is not null);
 // nchunks chunks per row (decode_attention_rows_chunks gives the count suited to `rows` rows at
-// max_kv_len: ~256 workgroups per row for one row, one 32-position tile per chunk, up to 64,
-// for the multi-row form); ws holds rows * n_heads * nchunks records of head_dim + 4 floats
+// max_kv_len: ~256 workgroups per row for one row; for the multi-row form one 32-position tile
+// per wave of a four-wave workgroup, up to 16 chunks); ws holds rows * n_heads * nchunks records
+// of head_dim + 4 floats
 int decode_attention_rows_chunks(int n_heads, int n_kv_heads, int head_dim, int max_kv_len, int rows);
 int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const float* V, float* out, long ldo,
                                  int rows, int n_heads, int n_kv_heads, int head_dim, const int* kv_dev, int kv0,
