@@ -805,9 +805,9 @@ def main():
     rig = GemvRig(fmt, N, K, steps=max(1, args.steps))
     rig.samples(1, args.warmup)  # W untimed warm-up launches
     per_launch, event_ms = rig.chain_samples(samples)
-    ms = float(np.median(per_launch))
+    ms_launch = float(np.median(per_launch))
     bpl = rig.bytes_per_launch()
-    gbs = bpl / (ms * 1e-3) / 1e9
+    gbs = bpl / (ms_launch * 1e-3) / 1e9
     copies = rig.copies
     rig.free()
     torch.cuda.empty_cache()
@@ -888,8 +888,9 @@ def main():
         # a 512-token prompt (BASELINE config 4's M) through the same step: the prefill GEMMs and the
         # reference's prefill attention on batched_matmul_gqa, eager steps at position 0
         r = DecodeStepRig(512, capture=False)
-        ms = float(np.median(r.prompt_samples(5)))
-        details["prompt_m512"] = {"prompt_tokens/s": round(512 / (ms * 1e-3), 1), "ms_per_prompt": round(ms, 4),
+        ms_prompt = float(np.median(r.prompt_samples(5)))
+        details["prompt_m512"] = {"prompt_tokens/s": round(512 / (ms_prompt * 1e-3), 1),
+                                  "ms_per_prompt": round(ms_prompt, 4),
                                   "timing": "median of 5 eager cri_decoder steps of 512 tokens at position 0"}
         r.free()
         torch.cuda.empty_cache()
@@ -901,7 +902,7 @@ def main():
         "n_gpus": 1,
         "steps": rig.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 6),
+        "ms_per_step": round(ms_launch, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -910,7 +911,7 @@ def main():
         "config": {"workload": "%s decode GEMV M=1" % fmt.upper(), "N": N, "K": K, "M": 1,
                    "weight_copies": copies, "rotation_bytes": copies * (bpl - 4 * K - 4 * N),
                    "samples": samples,
-                   "us_per_launch_min_median_max": [round(min(per_launch) * 1e3, 3), round(ms * 1e3, 3),
+                   "us_per_launch_min_median_max": [round(min(per_launch) * 1e3, 3), round(ms_launch * 1e3, 3),
                                                     round(max(per_launch) * 1e3, 3)],
                    "event_ms_all_samples": round(event_ms, 4),
                    "timing": "%d back-to-back samples of exactly %d launches in one captured graph, a device "

@@ -1,6 +1,6 @@
 // gemv_slice.hip -- batch-1 GEMV y[N] = W[N,K] x[K] with K sliced over the four waves of a
-// workgroup, for Q4_K weights: the C ABI's M = 1 case (plain activations, and SwiGLU ones at
-// K = 8192, the FFN down projection).
+// workgroup, for Q4_K weights and Q8_0 ones at K = 8192: the C ABI's M = 1 case (plain
+// activations, and SwiGLU ones at K = 8192, the FFN down projection).
 //
 // Replaces the M == 1 case of ref:src/kernels/matmul_quant.cu:309-397 (one 32x32 thread
 // block per 32 outputs, 31/32 of the lanes idle at M = 1).
@@ -9,7 +9,8 @@
 //   * a workgroup owns R consecutive rows; wave w owns K slice [K w / 4, K (w + 1) / 4) of
 //     all of them, so the four waves' partial sums meet once, through LDS, at the end;
 //   * a "piece" is 32 weights of one row (half of a 64-element Q4_K chunk: 16 bytes of qs,
-//     low nibbles = 16 elements, high nibbles = the 16 elements 32 further on); L = K / 128
+//     low nibbles = 16 elements, high nibbles = the 16 elements 32 further on; one Q8_0
+//     block); L = K / 128
 //     lanes share a row (L pieces = one K slice), so a wave takes 64 / L rows per step and
 //     IT steps (R = IT * 64 / L);
 //   * a lane's 32 activations stay in VGPRs for all of its IT rows (computed from the
@@ -42,6 +43,9 @@ namespace dev {
 // bytes 16 + 32 j + 16 h .. +16 of the super-block; low nibble of byte i = element
 // 64 j + 16 h + i, high nibble = element 64 j + 32 + 16 h + i (ref:src/kernels/dequantize.cu:307-319).
 struct SliceQ4K {
+    static constexpr int kFmt = kFmtQ4_K;
+    static constexpr int kXb = 32;        // xb: elements x_first + 32 .. +16
+    static constexpr int kMaxSteps = 8;   // row steps per workgroup at most
     struct Data {
         u32x4 hd, q;
     };
@@ -98,6 +102,48 @@ struct SliceQ4K {
     }
 };
 
+// Q8_0 piece p of a row: block p (34 bytes: fp16 d, 32 int8 quants; ref:src/kernels/dequantize.cu:60-70),
+// elements 32 p .. +32.  Blocks start at 34 p: dword aligned for even p, two bytes past a dword
+// boundary for odd p, so a lane loads the nine dwords from the one holding d (34 p - 2 (p & 1)) and
+// realigns the quants in registers; with an even number of blocks per row the nine dwords end
+// inside the row.  Quants enter as q + 128 (bytes xor 0x80, converted with v_cvt_f32_ubyteN) and
+// 128 sum(x) comes off at the end.
+struct SliceQ80 {
+    static constexpr int kFmt = kFmtQ8_0;
+    static constexpr int kXb = 16;  // xb: elements x_first + 16 .. +16
+    // 2048 x 8192: 6.73 us at four row steps, 7.05 at eight, 7.92 at two (the batch-1 GEMV: 7.42)
+    static constexpr int kMaxSteps = 4;
+    struct Data {
+        u32x4 a, b;
+        uint32_t c;
+    };
+    static __device__ __forceinline__ int x_first(int p) { return 32 * p; }
+    static __device__ __forceinline__ void load(Data& d, const uint8_t* __restrict__ row, int p) {
+        const uint8_t* s = row + 34 * p - 2 * (p & 1);
+        d.a = ld_u32x4(s);
+        d.b = ld_u32x4(s + 16);
+        d.c = ld_u32(s + 32);
+    }
+    static __device__ __forceinline__ float dot(const Data& d, const float (&xa)[16], const float (&xb)[16],
+                                                float sa, float sb, int p) {
+        const bool odd = p & 1;
+        const uint32_t D[9] = {d.a.x, d.a.y, d.a.z, d.a.w, d.b.x, d.b.y, d.b.z, d.b.w, d.c};
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            // quant bytes 4 k .. 4 k + 3 of the block (block bytes 2 + 4 k ..)
+            const uint32_t q = (odd ? D[k + 1] : align_bytes(D[k + 1], D[k], 2)) ^ 0x80808080u;
+            const float* x = k < 4 ? xa + 4 * k : xb + 4 * (k - 4);
+            s0 = __builtin_fmaf(static_cast<float>(q & 0xFFu), x[0], s0);
+            s1 = __builtin_fmaf(static_cast<float>((q >> 8) & 0xFFu), x[1], s1);
+            s0 = __builtin_fmaf(static_cast<float>((q >> 16) & 0xFFu), x[2], s0);
+            s1 = __builtin_fmaf(static_cast<float>(q >> 24), x[3], s1);
+        }
+        const float dd = odd ? h_hi(D[0]) : h_lo(D[0]);
+        return dd * ((s0 + s1) - 128.0f * (sa + sb));
+    }
+};
+
 constexpr int kSliceWaves = 4;   // waves per workgroup, one K slice each
 constexpr int kSliceXAfter = 2;  // row steps whose weight loads go before the activation loads
 
@@ -127,12 +173,12 @@ __global__ __launch_bounds__(64 * kSliceWaves) void slice_gemv_kernel(const uint
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             act_load<MODE>(ra[v], P, 0, k0 + 4 * v, P.lda);
-            act_load<MODE>(rb[v], P, 0, k0 + 32 + 4 * v, P.lda);
+            act_load<MODE>(rb[v], P, 0, k0 + F::kXb + 4 * v, P.lda);
         }
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const f32x4 a = act_finish<MODE>(ra[v], P, 0, k0 + 4 * v, K, ss, false);
-            const f32x4 b = act_finish<MODE>(rb[v], P, 0, k0 + 32 + 4 * v, K, ss, false);
+            const f32x4 b = act_finish<MODE>(rb[v], P, 0, k0 + F::kXb + 4 * v, K, ss, false);
             xa[4 * v] = a.x; xa[4 * v + 1] = a.y; xa[4 * v + 2] = a.z; xa[4 * v + 3] = a.w;
             xb[4 * v] = b.x; xb[4 * v + 1] = b.y; xb[4 * v + 2] = b.z; xb[4 * v + 3] = b.w;
         }
@@ -192,9 +238,9 @@ int slice_lg(int K) {
 // are N K / (IT 64 / L) floats; IT = 8 measured fastest at the Llama-3.2-1B shapes (8192 x 2048:
 // 256 workgroups of 32 rows, 3.94 us against 4.56 us on the unsliced GEMV; 2048 x 8192: 256 of
 // 8 rows, 4.71 against 6.2 us).  Fewer for short matrices, so that ~256 workgroups still run.
-int slice_steps(int N, int LG) {
+int slice_steps(int N, int LG, int max_steps) {
     const long rows_per_step = 64 >> LG;
-    int it = 8;
+    int it = max_steps;
     while (it > 1 && (static_cast<long>(N) + it * rows_per_step - 1) / (it * rows_per_step) < 256) it >>= 1;
     return it;
 }
@@ -203,7 +249,7 @@ template <class F, int LG, int IT, int MODE>
 int launch_slice_t(const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
     constexpr int RW = IT * (64 >> LG);
     const int blocks = (N + RW - 1) / RW;
-    const int rbytes = static_cast<int>(cri::row_bytes(kFmtQ4_K, K));
+    const int rbytes = static_cast<int>(cri::row_bytes(F::kFmt, K));
     hipLaunchKernelGGL((dev::slice_gemv_kernel<F, LG, IT, MODE>), dim3(blocks), dim3(64 * dev::kSliceWaves), 0, s,
                        static_cast<const uint8_t*>(W), y, act.a, act.b, N, rbytes);
     return 0;
@@ -211,7 +257,7 @@ int launch_slice_t(const ActIn& act, const void* W, float* y, int N, int K, hipS
 
 template <class F, int LG, int MODE>
 int launch_slice_it(const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
-    switch (slice_steps(N, LG)) {
+    switch (slice_steps(N, LG, F::kMaxSteps)) {
         case 8: return launch_slice_t<F, LG, 8, MODE>(act, W, y, N, K, s);
         case 4: return launch_slice_t<F, LG, 4, MODE>(act, W, y, N, K, s);
         case 2: return launch_slice_t<F, LG, 2, MODE>(act, W, y, N, K, s);
@@ -219,32 +265,41 @@ int launch_slice_it(const ActIn& act, const void* W, float* y, int N, int K, hip
     }
 }
 
-template <int MODE>
+template <class F, int MODE>
 int launch_slice_m(const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
     switch (slice_lg(K)) {
-        case 3: return launch_slice_it<dev::SliceQ4K, 3, MODE>(act, W, y, N, K, s);
-        case 4: return launch_slice_it<dev::SliceQ4K, 4, MODE>(act, W, y, N, K, s);
-        case 5: return launch_slice_it<dev::SliceQ4K, 5, MODE>(act, W, y, N, K, s);
-        case 6: return launch_slice_it<dev::SliceQ4K, 6, MODE>(act, W, y, N, K, s);
+        case 3: return launch_slice_it<F, 3, MODE>(act, W, y, N, K, s);
+        case 4: return launch_slice_it<F, 4, MODE>(act, W, y, N, K, s);
+        case 5: return launch_slice_it<F, 5, MODE>(act, W, y, N, K, s);
+        case 6: return launch_slice_it<F, 6, MODE>(act, W, y, N, K, s);
+    }
+    return kDeclined;
+}
+
+template <class F>
+int launch_slice_f(int mode, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
+    switch (mode) {
+        case kActPlain: return launch_slice_m<F, kActPlain>(act, W, y, N, K, s);
+        case kActSwiGLU:
+            // the up rows ld floats after the gate rows: the kernel reads one row, so ld is not needed
+            return launch_slice_m<F, kActSwiGLU>(act, W, y, N, K, s);
     }
     return kDeclined;
 }
 
 }  // namespace
 
+// Q8_0 only at K = 8192: at 8192 x 2048 the batch-1 GEMV of gemv.hip (two blocks per lane) is
+// faster (5.51 us against 5.96 at four row steps, same box)
 bool slice_gemv_supported(int fmt, int K, const void* W) {
-    return fmt == kFmtQ4_K && slice_lg(K) >= 0 && (reinterpret_cast<uintptr_t>(W) & 3u) == 0;
+    return (fmt == kFmtQ4_K || (fmt == kFmtQ8_0 && K == 8192)) && slice_lg(K) >= 0 &&
+           (reinterpret_cast<uintptr_t>(W) & 3u) == 0;
 }
 
 int launch_slice_gemv(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
     if (!slice_gemv_supported(fmt, K, W)) return kDeclined;
-    switch (mode) {
-        case kActPlain: return launch_slice_m<kActPlain>(act, W, y, N, K, s);
-        case kActSwiGLU:
-            // the up rows ld floats after the gate rows: the kernel reads one row, so ld is not needed
-            return launch_slice_m<kActSwiGLU>(act, W, y, N, K, s);
-    }
-    return kDeclined;
+    return fmt == kFmtQ4_K ? launch_slice_f<dev::SliceQ4K>(mode, act, W, y, N, K, s)
+                           : launch_slice_f<dev::SliceQ80>(mode, act, W, y, N, K, s);
 }
 
 }  // namespace detail

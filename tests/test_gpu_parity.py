@@ -240,8 +240,11 @@ def test_two_row_gemv(orc, fmt, N, K):
     ref = orc.matmul_quant(fmt, A, Bq, N, K)
     assert normwise_rel_err(got, ref) <= GEMV_TOL
     # each row alone through the batch-1 GEMV gives the same bits, unless the batch-1 GEMV
-    # takes two units per lane there (Q4_0, Q5_0, Q4_K at K = 2048 from 8192 rows)
-    if not (fmt in ("q4_0", "q5_0", "q4_k") and K == 2048 and N >= 8192):
+    # takes two units per lane there (Q4_0, Q5_0, Q4_K at K = 2048 from 8192 rows) or is the
+    # K-sliced GEMV, which adds in another order (Q4_K at K in {1024, 2048, 4096, 8192}, Q8_0
+    # at K = 8192)
+    sliced = (fmt == "q4_k" and K in (1024, 2048, 4096, 8192)) or (fmt == "q8_0" and K == 8192)
+    if not (sliced or (fmt in ("q4_0", "q5_0", "q4_k") and K == 2048 and N >= 8192)):
         for m in range(2):
             assert np.array_equal(run_matmul(fmt, A[m:m + 1], Bq, N, K), got[m:m + 1])
 
@@ -256,7 +259,9 @@ def test_row_pair_gemv(orc, fmt, M, N, K):
     Bq = weights(fmt, N, K, seed=N + M + K)
     got = run_matmul(fmt, A, Bq, N, K)
     assert normwise_rel_err(got, orc.matmul_quant(fmt, A, Bq, N, K)) <= GEMV_TOL
-    if not (fmt in ("q4_0", "q5_0", "q4_k") and K == 2048 and N >= 8192):
+    # the batch-1 GEMV gives each row's bits where it is the same kernel family (see above)
+    sliced = (fmt == "q4_k" and K in (1024, 2048, 4096, 8192)) or (fmt == "q8_0" and K == 8192)
+    if not (sliced or (fmt in ("q4_0", "q5_0", "q4_k") and K == 2048 and N >= 8192)):
         for m in (0, M - 1):
             assert np.array_equal(run_matmul(fmt, A[m:m + 1], Bq, N, K), got[m:m + 1])
 
