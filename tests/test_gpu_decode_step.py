@@ -431,6 +431,54 @@ def test_prompt_two_layers_through_gqa(orc, pos):
         assert normwise_rel_err(gv[pos:pos + M], vc[i][pos:pos + M]) <= PREFILL_TOL
 
 
+@pytest.mark.parametrize("M,pos", [(16, 0), (4, 0), (8, 31), (16, 120), (5, 1000), (16, 1008)])
+def test_batch_attention_rope_nan_cache(orc, M, pos):
+    # 4..16 rows on the multi-row attention: every cache row from pos on holds NaN before the step,
+    # so a product that read a row before the step wrote it, or one past the batch's last position
+    # (a clamped read past a chunk's end, the V operand's 0 * NaN), would poison the logits.
+    # Positions: 0 (every row the batch's own), new rows across a tile boundary (31) and across a
+    # chunk boundary (120 at 16 rows: chunks of one tile), the last positions of the cache (1008 + 16
+    # = 1024).  Rows past the batch stay NaN; a replay equals the eager step.
+    m = make_model(2, dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1024, vocab=900, seed=81 + pos,
+                   big_tables=False)
+    max_seq = 1024
+    dec = make_decoder(m, max_seq=max_seq)
+    kc, vc = random_cache(m, max_seq, 82 + pos)
+    for arr in kc + vc:
+        arr[pos:] = np.nan
+    load_cache(dec, kc, vc)
+    ids = np.random.default_rng(83 + M).integers(0, m["vocab"], M).astype(np.int32)
+    dids = torch.from_numpy(ids).cuda()
+    a = torch.empty(M, m["vocab"], device="cuda")
+    dec.set_position(pos)
+    dec.forward(dids, M, a)
+    eager = a.cpu().numpy().copy()
+    rk, rv = [k.copy() for k in kc], [v.copy() for v in vc]
+    ref, _ = orc.decode_step(m, list(ids), pos, rk, rv)
+    err = normwise_rel_err(eager, ref)
+    print("batch M=%d pos=%d, NaN from pos on: normwise err %.2e" % (M, pos, err))
+    assert np.isfinite(eager).all() and err <= TOL
+    k_tol = TOL + (pos + M) * 2.0 ** -23
+    for i in range(len(m["layers"])):
+        ka, va = dec.kv_cache(i)
+        shape = (max_seq, m["n_kv_heads"], m["head_dim"])
+        gk, gv = from_device(ka, shape), from_device(va, shape)
+        assert normwise_rel_err(gk[pos:pos + M], rk[i][pos:pos + M]) <= k_tol
+        assert normwise_rel_err(gv[pos:pos + M], rv[i][pos:pos + M]) <= TOL
+        assert np.array_equal(gk[:pos], kc[i][:pos]) and np.isnan(gk[pos + M:]).all()
+    # a captured step replayed at the same position on the same cache: the same bits
+    load_cache(dec, kc, vc)
+    s = torch.cuda.Stream()
+    b = torch.empty(M, m["vocab"], device="cuda")
+    with torch.cuda.stream(s):
+        dec.set_position(pos, stream=s)
+        dec.capture(dids, M, b, None, stream=s)
+        dec.set_position(pos, stream=s)
+        dec.replay(stream=s)
+    s.synchronize()
+    assert np.array_equal(b.cpu().numpy(), eager)
+
+
 def test_prompt_row_blocks_nan_cache_and_replay(orc):
     # 600 rows: two row blocks of the prompt flow (512 + 88); cache rows past the step's positions
     # hold NaN, which no product may read; a graph captured at one position (its products span the
