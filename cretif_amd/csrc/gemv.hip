@@ -53,8 +53,8 @@ namespace dev {
 // BLK: threads per workgroup (256 or 512); every workgroup stages the whole activation vector.
 template <class F, int UPL, int PREF, int MODE, int MR = 1, bool ROPE = false, bool KSPLIT = false, int BLK = 256>
 __global__ __launch_bounds__(BLK) void gemv_kernel(const uint8_t* __restrict__ W, float* __restrict__ y, int N, int K,
-                                                   int units, long row_bytes, int lpr_log2, const ActIn Pin, int mrows,
-                                                   const RopeOut R) {
+                                                   int units, long row_bytes, int lpr_log2, int nblocks,
+                                                   const ActIn Pin, int mrows, const RopeOut R) {
     constexpr bool kRms = MODE == kActRMSNorm || MODE == kActRMSNormS;
     static_assert(MR == 1 || MODE == kActPlain, "two activation rows: plain activations only");
     static_assert(!ROPE || (MR == 1 && kRms), "RoPE epilogue: the one-row RMSNorm GEMV");
@@ -72,8 +72,10 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const uint8_t* __restrict__ W
     const int u0 = lane & (lpr - 1);
     const int rsub = lane >> lpr_log2;
     const int rows_per_iter = 64 >> lpr_log2;
-    const int gwave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    // the weight addresses depend only on arguments among the first 16 dwords (preloaded into
+    // SGPRs) and on compile-time constants: no hidden argument (blockDim, gridDim) is read
+    const int gwave = (static_cast<int>(blockIdx.x) * BLK + static_cast<int>(threadIdx.x)) >> 6;
+    const int nwaves = (nblocks * BLK) >> 6;
     const int stride = nwaves * rows_per_iter;  // rows between a wave's consecutive row-groups
 
     int unit[UPL], wunit[UPL];  // unit inside the staged activations / the weight row
@@ -212,7 +214,8 @@ static int launch_gemv_blk(const ActIn& act, const void* W, float* y, int N, int
     }
     const unsigned gy = KSPLIT ? static_cast<unsigned>(splits) : static_cast<unsigned>((mrows + MR - 1) / MR);
     hipLaunchKernelGGL((dev::gemv_kernel<F, UPL, PREF, MODE, MR, ROPE, KSPLIT, BLK>), dim3(blocks, gy), dim3(BLK), lds,
-                       stream, static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, act, mrows, rope);
+                       stream, static_cast<const uint8_t*>(W), y, N, K, units, row_bytes, lpr_log2, blocks, act, mrows,
+                       rope);
     return 0;
 }
 
