@@ -1,18 +1,17 @@
-// gemv_slice.hip -- batch-1 GEMV y[N] = W[N,K] x[K] with K sliced over the four waves of a
-// workgroup, for Q4_K weights and Q8_0 ones at K = 8192: the C ABI's M = 1 case (plain
-// activations, and SwiGLU ones at K = 8192, the FFN down projection).
+// gemv_slice.hip -- batch-1 GEMV y[N] = W[N,K] x[K] with K sliced over the waves of a
+// workgroup (four for Q4_K, eight for Q8_0), for Q4_K weights and Q8_0 ones at K = 8192: the
+// C ABI's M = 1 case (plain activations, and SwiGLU ones at K = 8192, the FFN down projection).
 //
 // Replaces the M == 1 case of ref:src/kernels/matmul_quant.cu:309-397 (one 32x32 thread
 // block per 32 outputs, 31/32 of the lanes idle at M = 1).
 //
-// Work decomposition (wave64, 256 threads = 4 waves per workgroup):
-//   * a workgroup owns R consecutive rows; wave w owns K slice [K w / 4, K (w + 1) / 4) of
-//     all of them, so the four waves' partial sums meet once, through LDS, at the end;
+// Work decomposition (wave64, W = F::kWaves waves per workgroup):
+//   * a workgroup owns R consecutive rows; wave w owns K slice [K w / W, K (w + 1) / W) of
+//     all of them, so the W waves' partial sums meet once, through LDS, at the end;
 //   * a "piece" is 32 weights of one row (half of a 64-element Q4_K chunk: 16 bytes of qs,
 //     low nibbles = 16 elements, high nibbles = the 16 elements 32 further on; one Q8_0
-//     block); L = K / 128
-//     lanes share a row (L pieces = one K slice), so a wave takes 64 / L rows per step and
-//     IT steps (R = IT * 64 / L);
+//     block); L = K / (32 W) lanes share a row (L pieces = one K slice), so a wave takes
+//     64 / L rows per step and IT steps (R = IT * 64 / L);
 //   * a lane's 32 activations stay in VGPRs for all of its IT rows (computed from the
 //     prologue's inputs when MODE is not plain), loaded straight from global memory: every
 //     wave of the grid reads the same K floats, which the L1/L2 serve; LDS staging, with its
@@ -46,6 +45,7 @@ struct SliceQ4K {
     static constexpr int kFmt = kFmtQ4_K;
     static constexpr int kXb = 32;        // xb: elements x_first + 32 .. +16
     static constexpr int kMaxSteps = 8;   // row steps per workgroup at most
+    static constexpr int kWaves = 4;      // waves per workgroup (K slices); eight measured slower (3.96 -> 4.80 us)
     struct Data {
         u32x4 hd, q;
     };
@@ -111,8 +111,10 @@ struct SliceQ4K {
 struct SliceQ80 {
     static constexpr int kFmt = kFmtQ8_0;
     static constexpr int kXb = 16;  // xb: elements x_first + 16 .. +16
-    // 2048 x 8192: 6.73 us at four row steps, 7.05 at eight, 7.92 at two (the batch-1 GEMV: 7.42)
+    // 2048 x 8192, same box: eight waves (K slices of 1024) 6.12 us against 6.86 at four; four
+    // row steps 6.12, eight 6.12, two 6.74 (the batch-1 GEMV: 7.42)
     static constexpr int kMaxSteps = 4;
+    static constexpr int kWaves = 8;
     struct Data {
         u32x4 a, b;
         uint32_t c;
@@ -144,20 +146,22 @@ struct SliceQ80 {
     }
 };
 
-constexpr int kSliceWaves = 4;   // waves per workgroup, one K slice each
-constexpr int kSliceXAfter = 2;  // row steps whose weight loads go before the activation loads
+constexpr int kSliceMaxWaves = 8;  // waves per workgroup (F::kWaves), one K slice each
+constexpr int kSliceXAfter = 2;    // row steps whose weight loads go before the activation loads
 
 // The prologue's pointers and integers are separate scalar arguments (16 dwords up to kn), all
 // preloaded into SGPRs: an aggregate argument is fetched with scalar loads, and activation loads
 // waiting on that fetch would hold back the weight loads issued after them.
 template <class F, int LG, int IT, int MODE>
-__global__ __launch_bounds__(64 * kSliceWaves) void slice_gemv_kernel(const uint8_t* __restrict__ W,
+__global__ __launch_bounds__(64 * F::kWaves) void slice_gemv_kernel(const uint8_t* __restrict__ W,
                                                                       float* __restrict__ y,
                                                                       const float* __restrict__ a,
                                                                       const float* __restrict__ b, int N,
                                                                       int row_bytes) {
     static_assert(MODE == kActPlain || MODE == kActSwiGLU, "plain or SwiGLU prologue");
     constexpr int L = 1 << LG, RPI = 64 / L, RW = IT * RPI;  // lanes per row, rows per step, rows per workgroup
+    constexpr int kSliceWaves = F::kWaves;
+    static_assert(kSliceWaves <= kSliceMaxWaves, "waves per workgroup");
     constexpr int K = kSliceWaves * L * 32;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int sub = lane & (L - 1), rsub = lane >> LG;
@@ -223,15 +227,18 @@ namespace detail {
 
 namespace {
 
-// lanes per row = K / 128 (K in {1024, 2048, 4096, 8192}); log2 of it, or -1
-int slice_lg(int K) {
+// lanes per row = K / (32 waves) (K in {1024, 2048, 4096, 8192}); log2 of it, or -1
+int slice_lg(int K, int waves) {
+    int lg = -1;
     switch (K) {
-        case 1024: return 3;
-        case 2048: return 4;
-        case 4096: return 5;
-        case 8192: return 6;
+        case 1024: lg = 5; break;
+        case 2048: lg = 6; break;
+        case 4096: lg = 7; break;
+        case 8192: lg = 8; break;
     }
-    return -1;
+    if (lg < 0) return -1;
+    lg -= waves == 8 ? 3 : 2;  // K / 32 pieces over the waves
+    return lg >= 2 && lg <= 6 ? lg : -1;
 }
 
 // Row steps per wave: IT rows per lane share one activation load, so the grid's activation reads
@@ -250,7 +257,7 @@ int launch_slice_t(const ActIn& act, const void* W, float* y, int N, int K, hipS
     constexpr int RW = IT * (64 >> LG);
     const int blocks = (N + RW - 1) / RW;
     const int rbytes = static_cast<int>(cri::row_bytes(F::kFmt, K));
-    hipLaunchKernelGGL((dev::slice_gemv_kernel<F, LG, IT, MODE>), dim3(blocks), dim3(64 * dev::kSliceWaves), 0, s,
+    hipLaunchKernelGGL((dev::slice_gemv_kernel<F, LG, IT, MODE>), dim3(blocks), dim3(64 * F::kWaves), 0, s,
                        static_cast<const uint8_t*>(W), y, act.a, act.b, N, rbytes);
     return 0;
 }
@@ -267,7 +274,8 @@ int launch_slice_it(const ActIn& act, const void* W, float* y, int N, int K, hip
 
 template <class F, int MODE>
 int launch_slice_m(const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
-    switch (slice_lg(K)) {
+    switch (slice_lg(K, F::kWaves)) {
+        case 2: return launch_slice_it<F, 2, MODE>(act, W, y, N, K, s);
         case 3: return launch_slice_it<F, 3, MODE>(act, W, y, N, K, s);
         case 4: return launch_slice_it<F, 4, MODE>(act, W, y, N, K, s);
         case 5: return launch_slice_it<F, 5, MODE>(act, W, y, N, K, s);
@@ -292,7 +300,8 @@ int launch_slice_f(int mode, const ActIn& act, const void* W, float* y, int N, i
 // Q8_0 only at K = 8192: at 8192 x 2048 the batch-1 GEMV of gemv.hip (two blocks per lane) is
 // faster (5.51 us against 5.96 at four row steps, same box)
 bool slice_gemv_supported(int fmt, int K, const void* W) {
-    return (fmt == kFmtQ4_K || (fmt == kFmtQ8_0 && K == 8192)) && slice_lg(K) >= 0 &&
+    const int waves = fmt == kFmtQ8_0 ? dev::SliceQ80::kWaves : dev::SliceQ4K::kWaves;
+    return (fmt == kFmtQ4_K || (fmt == kFmtQ8_0 && K == 8192)) && slice_lg(K, waves) >= 0 &&
            (reinterpret_cast<uintptr_t>(W) & 3u) == 0;
 }
 
