@@ -1,6 +1,7 @@
 // gemv_slice.hip -- batch-1 GEMV y[N] = W[N,K] x[K] with K sliced over the waves of a
-// workgroup (four for Q4_K, eight for Q8_0), for Q4_K weights and Q8_0 ones at K = 8192: the
-// C ABI's M = 1 case (plain activations, and SwiGLU ones at K = 8192, the FFN down projection).
+// workgroup (four for Q4_K, eight for the 32-element formats), for Q4_K weights and Q8_0, Q4_0
+// and Q5_0 ones at K = 8192: the C ABI's M = 1 case (plain activations, and SwiGLU ones at
+// K = 8192, the FFN down projection).
 //
 // Replaces the M == 1 case of ref:src/kernels/matmul_quant.cu:309-397 (one 32x32 thread
 // block per 32 outputs, 31/32 of the lanes idle at M = 1).
@@ -9,8 +10,8 @@
 //   * a workgroup owns R consecutive rows; wave w owns K slice [K w / W, K (w + 1) / W) of
 //     all of them, so the W waves' partial sums meet once, through LDS, at the end;
 //   * a "piece" is 32 weights of one row (half of a 64-element Q4_K chunk: 16 bytes of qs,
-//     low nibbles = 16 elements, high nibbles = the 16 elements 32 further on; one Q8_0
-//     block); L = K / (32 W) lanes share a row (L pieces = one K slice), so a wave takes
+//     low nibbles = 16 elements, high nibbles = the 16 elements 32 further on; one Q8_0,
+//     Q4_0 or Q5_0 block); L = K / (32 W) lanes share a row (L pieces = one K slice), so a wave takes
 //     64 / L rows per step and IT steps (R = IT * 64 / L);
 //   * a lane's 32 activations stay in VGPRs for all of its IT rows (computed from the
 //     prologue's inputs when MODE is not plain), loaded straight from global memory: every
@@ -143,6 +144,90 @@ struct SliceQ80 {
         }
         const float dd = odd ? h_hi(D[0]) : h_lo(D[0]);
         return dd * ((s0 + s1) - 128.0f * (sa + sb));
+    }
+};
+
+// Q4_0 piece p of a row: block p (18 bytes: fp16 d, 16 quant bytes; ref:src/kernels/dequantize.cu:73-101),
+// element i <- quant byte i / 2, low nibble for even i; x = d (q - 8).  Blocks start at 18 p: dword
+// aligned for even p, two bytes off for odd p; a lane loads the five dwords from the one holding d
+// (the extra two bytes of an even block are the next block's d: rows hold an even number of blocks).
+struct SliceQ40 {
+    static constexpr int kFmt = kFmtQ4_0;
+    static constexpr int kXb = 16;
+    static constexpr int kMaxSteps = 8;
+    static constexpr int kWaves = 8;  // 2048 x 8192: 4.67 us at eight, 5.20 at four (the batch-1 GEMV: 5.71)
+    struct Data {
+        u32x4 a;
+        uint32_t b;
+    };
+    static __device__ __forceinline__ int x_first(int p) { return 32 * p; }
+    static __device__ __forceinline__ void load(Data& d, const uint8_t* __restrict__ row, int p) {
+        const uint8_t* s = row + 18 * p - 2 * (p & 1);
+        d.a = ld_u32x4(s);
+        d.b = ld_u32(s + 16);
+    }
+    static __device__ __forceinline__ float dot(const Data& d, const float (&xa)[16], const float (&xb)[16],
+                                                float sa, float sb, int p) {
+        const bool odd = p & 1;
+        const uint32_t D[5] = {d.a.x, d.a.y, d.a.z, d.a.w, d.b};
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            // quant bytes 4 t .. 4 t + 3: elements 8 t + 2 b (low nibble) and 8 t + 2 b + 1 (high)
+            const uint32_t w = odd ? D[t + 1] : align_bytes(D[t + 1], D[t], 2);
+            const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+            const float* x = t < 2 ? xa + 8 * t : xb + 8 * (t - 2);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                s0 = __builtin_fmaf(ubyte(lo, b), x[2 * b], s0);
+                s1 = __builtin_fmaf(ubyte(hi, b), x[2 * b + 1], s1);
+            }
+        }
+        const float dd = odd ? h_hi(D[0]) : h_lo(D[0]);
+        return dd * ((s0 + s1) - 8.0f * (sa + sb));
+    }
+};
+
+// Q5_0 piece p of a row: block p (22 bytes: fp16 d, qh[4], qs[16]; ref:src/kernels/dequantize.cu:126-165),
+// element i: low nibble of qs[i] (i < 16) or high nibble of qs[i - 16], bit i of qh as bit 4;
+// x = d (q - 16).  Blocks start at 22 p (two bytes off for odd p): six dwords from the one holding d.
+struct SliceQ50 {
+    static constexpr int kFmt = kFmtQ5_0;
+    static constexpr int kXb = 16;
+    static constexpr int kMaxSteps = 8;
+    static constexpr int kWaves = 8;  // 2048 x 8192: 5.08 us at eight, 7.11 at four (the batch-1 GEMV: 6.51)
+    struct Data {
+        u32x4 a;
+        uint32_t b, c;
+    };
+    static __device__ __forceinline__ int x_first(int p) { return 32 * p; }
+    static __device__ __forceinline__ void load(Data& d, const uint8_t* __restrict__ row, int p) {
+        const uint8_t* s = row + 22 * p - 2 * (p & 1);
+        d.a = ld_u32x4(s);
+        d.b = ld_u32(s + 16);
+        d.c = ld_u32(s + 20);
+    }
+    static __device__ __forceinline__ float dot(const Data& d, const float (&xa)[16], const float (&xb)[16],
+                                                float sa, float sb, int p) {
+        const bool odd = p & 1;
+        const uint32_t D[6] = {d.a.x, d.a.y, d.a.z, d.a.w, d.b, d.c};
+        const uint32_t qh = odd ? D[1] : align_bytes(D[1], D[0], 2);
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t w = odd ? D[t + 2] : align_bytes(D[t + 2], D[t + 1], 2);
+            const uint32_t nlo = ubfe(qh, 4 * t, 4), nhi = ubfe(qh, 16 + 4 * t, 4);
+            // the four high bits spread to bit 4 of each byte (no carries between the copies)
+            const uint32_t lo = (w & 0x0F0F0F0Fu) | ((nlo * 0x02040810u) & 0x10101010u);
+            const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | ((nhi * 0x02040810u) & 0x10101010u);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                s0 = __builtin_fmaf(ubyte(lo, b), xa[4 * t + b], s0);
+                s1 = __builtin_fmaf(ubyte(hi, b), xb[4 * t + b], s1);
+            }
+        }
+        const float dd = odd ? h_hi(D[0]) : h_lo(D[0]);
+        return dd * ((s0 + s1) - 16.0f * (sa + sb));
     }
 };
 
@@ -299,16 +384,40 @@ int launch_slice_f(int mode, const ActIn& act, const void* W, float* y, int N, i
 
 // Q8_0 only at K = 8192: at 8192 x 2048 the batch-1 GEMV of gemv.hip (two blocks per lane) is
 // faster (5.51 us against 5.96 at four row steps, same box)
+// Q8_0, Q4_0 and Q5_0 only at K = 8192 (the FFN down shape): at 8192 x 2048 the batch-1 GEMV of
+// gemv.hip is faster for them (same box: Q8_0 5.18 against 5.96 / 6.06 us at four / eight waves,
+// Q4_0 4.13 against 4.77, Q5_0 4.92 against 5.11 at eight waves)
+static bool slice_fmt(int fmt, int K) {
+    switch (fmt) {
+        case kFmtQ4_K: return true;
+        case kFmtQ8_0:
+        case kFmtQ4_0:
+        case kFmtQ5_0: return K == 8192;
+    }
+    return false;
+}
+static int slice_waves(int fmt) {
+    switch (fmt) {
+        case kFmtQ8_0: return dev::SliceQ80::kWaves;
+        case kFmtQ4_0: return dev::SliceQ40::kWaves;
+        case kFmtQ5_0: return dev::SliceQ50::kWaves;
+    }
+    return dev::SliceQ4K::kWaves;
+}
+
 bool slice_gemv_supported(int fmt, int K, const void* W) {
-    const int waves = fmt == kFmtQ8_0 ? dev::SliceQ80::kWaves : dev::SliceQ4K::kWaves;
-    return (fmt == kFmtQ4_K || (fmt == kFmtQ8_0 && K == 8192)) && slice_lg(K, waves) >= 0 &&
-           (reinterpret_cast<uintptr_t>(W) & 3u) == 0;
+    return slice_fmt(fmt, K) && slice_lg(K, slice_waves(fmt)) >= 0 && (reinterpret_cast<uintptr_t>(W) & 3u) == 0;
 }
 
 int launch_slice_gemv(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
     if (!slice_gemv_supported(fmt, K, W)) return kDeclined;
-    return fmt == kFmtQ4_K ? launch_slice_f<dev::SliceQ4K>(mode, act, W, y, N, K, s)
-                           : launch_slice_f<dev::SliceQ80>(mode, act, W, y, N, K, s);
+    switch (fmt) {
+        case kFmtQ4_K: return launch_slice_f<dev::SliceQ4K>(mode, act, W, y, N, K, s);
+        case kFmtQ8_0: return launch_slice_f<dev::SliceQ80>(mode, act, W, y, N, K, s);
+        case kFmtQ4_0: return launch_slice_f<dev::SliceQ40>(mode, act, W, y, N, K, s);
+        case kFmtQ5_0: return launch_slice_f<dev::SliceQ50>(mode, act, W, y, N, K, s);
+    }
+    return kDeclined;
 }
 
 }  // namespace detail

@@ -241,9 +241,9 @@ def test_two_row_gemv(orc, fmt, N, K):
     assert normwise_rel_err(got, ref) <= GEMV_TOL
     # each row alone through the batch-1 GEMV gives the same bits, unless the batch-1 GEMV
     # takes two units per lane there (Q4_0, Q5_0, Q4_K at K = 2048 from 8192 rows) or is the
-    # K-sliced GEMV, which adds in another order (Q4_K at K in {1024, 2048, 4096, 8192}, Q8_0
-    # at K = 8192)
-    sliced = (fmt == "q4_k" and K in (1024, 2048, 4096, 8192)) or (fmt == "q8_0" and K == 8192)
+    # K-sliced GEMV, which adds in another order (Q4_K at K in {1024, 2048, 4096, 8192}, Q8_0,
+    # Q4_0 and Q5_0 at K = 8192)
+    sliced = (fmt == "q4_k" and K in (1024, 2048, 4096, 8192)) or (fmt in ("q8_0", "q4_0", "q5_0") and K == 8192)
     if not (sliced or (fmt in ("q4_0", "q5_0", "q4_k") and K == 2048 and N >= 8192)):
         for m in range(2):
             assert np.array_equal(run_matmul(fmt, A[m:m + 1], Bq, N, K), got[m:m + 1])
@@ -260,7 +260,7 @@ def test_row_pair_gemv(orc, fmt, M, N, K):
     got = run_matmul(fmt, A, Bq, N, K)
     assert normwise_rel_err(got, orc.matmul_quant(fmt, A, Bq, N, K)) <= GEMV_TOL
     # the batch-1 GEMV gives each row's bits where it is the same kernel family (see above)
-    sliced = (fmt == "q4_k" and K in (1024, 2048, 4096, 8192)) or (fmt == "q8_0" and K == 8192)
+    sliced = (fmt == "q4_k" and K in (1024, 2048, 4096, 8192)) or (fmt in ("q8_0", "q4_0", "q5_0") and K == 8192)
     if not (sliced or (fmt in ("q4_0", "q5_0", "q4_k") and K == 2048 and N >= 8192)):
         for m in (0, M - 1):
             assert np.array_equal(run_matmul(fmt, A[m:m + 1], Bq, N, K), got[m:m + 1])
