@@ -55,6 +55,10 @@ PREFILL_WORKLOADS = {
 SKINNY_WORKLOADS = {
     "q4_k_gemv_m16": ("q4_k", 16, 8192, 2048),
     "q4_k_gemv_down_m16": ("q4_k", 16, 2048, 8192),
+    # the same through cri_matmul_ws: the K split's partial sums added in a fixed order (the same
+    # bits every call) instead of with atomics
+    "q4_k_gemv_m16_ws": ("q4_k", 16, 8192, 2048),
+    "q4_k_gemv_down_m16_ws": ("q4_k", 16, 2048, 8192),
     # the tied fp32 LM head at decode batch 16 (matmul_transposed_b, ref:src/embedding.cu:85-135)
     "fp32_tied_lm_head_m16": ("fp32", 16, 128256, 2048),
 }
@@ -193,7 +197,8 @@ class GemvRig(ChainTimed):
     """Weights replicated over enough device copies that each launch streams from HBM;
     `steps` launches per captured graph (see rotation_plan)."""
 
-    def __init__(self, fmt, N, K, M=1, seed=1, min_bytes=2 * MALL_BYTES, max_copies=64, steps=None):
+    def __init__(self, fmt, N, K, M=1, seed=1, min_bytes=2 * MALL_BYTES, max_copies=64, steps=None,
+                 workspace=False):
         import torch
 
         import cretif_amd as cri
@@ -211,12 +216,16 @@ class GemvRig(ChainTimed):
         self.x = torch.from_numpy(quant.randn(M * K, seed=seed + 1).reshape(M, K)).cuda()
         self.y = torch.empty(M, N, device="cuda")
         self.cri = cri
+        wsb = cri.matmul_workspace_bytes(fmt, M, N, K) if workspace else 0
+        self.ws = torch.empty(max(1, wsb // 4), dtype=torch.float32, device="cuda") if wsb else None
         torch.cuda.synchronize()
         self.stream = torch.cuda.Stream()
 
         def run(Wi):
             if fmt == "fp32":
                 cri.matmul_transposed_b(self.x, Wi, self.y, M, N, K)
+            elif self.ws is not None:
+                cri.matmul_ws(fmt, self.x, Wi, self.y, M, N, K, self.ws)
             else:
                 cri.matmul(fmt, self.x, Wi, self.y, M, N, K)
 
@@ -796,7 +805,7 @@ def main():
             f, m_, n, k = SKINNY_WORKLOADS[args.gemv]
         else:
             (f, n, k), m_ = GEMV_WORKLOADS[args.gemv], 1
-        r = GemvRig(f, n, k, M=m_, max_copies=1024)
+        r = GemvRig(f, n, k, M=m_, max_copies=1024, workspace=args.gemv.endswith("_ws"))
         m = r.time(samples, 64)
         print(json.dumps({"workload": args.gemv, "M": m_, "N": n, "K": k, "launches_per_sample": r.steps,
                           "us": round(m * 1e3, 3), "GB/s": round(r.bytes_per_launch() / (m * 1e-3) / 1e9, 1)}))
@@ -835,7 +844,7 @@ def main():
             torch.cuda.empty_cache()
         # batched decode (BASELINE config 5 at M = 16): reported against the HBM and the fp16 MFMA roofs
         for name, (f, m_, n, k) in SKINNY_WORKLOADS.items():
-            r = GemvRig(f, n, k, M=m_)
+            r = GemvRig(f, n, k, M=m_, workspace=name.endswith("_ws"))
             m = r.time(9, 64)
             details[name] = dict(gemv_line(r, m), M=m_, **{"TFLOP/s": round(2.0 * m_ * n * k / (m * 1e-3) / 1e12, 2)})
             r.free()

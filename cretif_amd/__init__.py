@@ -24,6 +24,8 @@ __all__ = [
     "library_path",
     "matmul",
     "matmul_q8_0",
+    "matmul_ws",
+    "matmul_workspace_bytes",
     "matmul_q4_0",
     "matmul_q5_0",
     "matmul_q4_k",
@@ -73,7 +75,7 @@ _MATMUL = ["cri_matmul_" + f for f in ("q8_0", "q4_0", "q5_0", "q4_k", "q6_k", "
 _DEQUANT = ["cri_dequantize_" + f for f in ("q8_0", "q4_0", "q5_0", "q6_k", "q4_k")]
 ABI_SYMBOLS = (
     _MATMUL
-    + ["cri_matmul"]
+    + ["cri_matmul", "cri_matmul_ws", "cri_matmul_workspace_bytes"]
     + _DEQUANT
     + [
         "cri_matmul_transposed_b",
@@ -199,6 +201,10 @@ def lib():
         f.restype = i32
     L.cri_matmul.argtypes = [i32, vp, vp, vp, i32, i32, i32, vp]
     L.cri_matmul.restype = i32
+    L.cri_matmul_ws.argtypes = [i32, vp, vp, vp, i32, i32, i32, vp, ctypes.c_longlong, vp]
+    L.cri_matmul_ws.restype = i32
+    L.cri_matmul_workspace_bytes.argtypes = [i32, i32, i32, i32]
+    L.cri_matmul_workspace_bytes.restype = ctypes.c_longlong
     for name in _DEQUANT:
         f = getattr(L, name)
         f.argtypes = [vp, vp, i32, vp]
@@ -356,6 +362,25 @@ def matmul(fmt, A, B, C, M, N, K, stream=None):
     """Format-switched fused matmul (the switch of matmul_dispatch, ref:src/model.cu:797-825)."""
     fid = FORMAT_IDS[fmt] if isinstance(fmt, str) else int(fmt)
     _check(lib().cri_matmul(fid, _ptr(A), _ptr(B), _ptr(C), M, N, K, _stream(stream)))
+
+
+def matmul_workspace_bytes(fmt, M, N, K):
+    """Workspace bytes matmul_ws uses for this shape (0 when none)."""
+    fid = FORMAT_IDS[fmt] if isinstance(fmt, str) else int(fmt)
+    n = lib().cri_matmul_workspace_bytes(fid, M, N, K)
+    if n < 0:
+        _check(int(n))
+    return int(n)
+
+
+def matmul_ws(fmt, A, B, C, M, N, K, workspace, workspace_bytes=None, stream=None):
+    """matmul with a caller workspace: 2..16-row products add their K-split partial sums in a
+    fixed order (the same bits on every call).  No counterpart in the reference."""
+    fid = FORMAT_IDS[fmt] if isinstance(fmt, str) else int(fmt)
+    if workspace_bytes is None:
+        workspace_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(lib().cri_matmul_ws(fid, _ptr(A), _ptr(B), _ptr(C), M, N, K, _ptr(workspace), workspace_bytes,
+                               _stream(stream)))
 
 
 def _dq(name):

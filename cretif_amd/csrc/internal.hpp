@@ -136,6 +136,9 @@ int launch_skinny_act(int mode, int fmt, const ActIn& act, const void* B, float*
                       hipStream_t stream, float* ws = nullptr, long ws_floats = 0, SplitSums* defer = nullptr,
                       int defer_S = 0);
 long skinny_workspace_floats(int M, int N);
+// whether launch_skinny_act without a workspace splits K over workgroups with fp32 atomics (plain
+// activations, M rows); with a workspace those partial sums are added in a fixed order instead
+bool skinny_atomic_split(int M, int K);
 // cri_matmul / cri_matmul_swiglu / cri_matmul_rmsnorm with that workspace (abi.cpp); return a cri_status
 int matmul_split_ws(int fmt, const float* A, const void* B, float* C, int M, int N, int K, float* ws, long ws_floats,
                     hipStream_t s, SplitSums* defer = nullptr, int defer_S = 0);

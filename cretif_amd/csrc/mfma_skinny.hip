@@ -1183,6 +1183,16 @@ int launch_skinny_act(int mode, int fmt, const ActIn& act, const void* B, float*
 }
 
 // groups x splits <= 256 and 128 columns per group: N x splits <= 32768 (see kSkPartOff)
+bool skinny_atomic_split(int M, int K) {
+    // launch_skinny_m without a workspace: plain activations split K over workgroups (fp32 atomics
+    // into C) from 9 rows when the activations take several chunks
+    if (M <= 8 || M > 16 || K % 256 != 0) return false;
+    int KC = (dev::kSkChunk / M) / 256 * 256;
+    if (KC > K) KC = K;
+    while (KC > 256 && K % KC != 0) KC -= 256;
+    return KC >= 256 && K > KC;
+}
+
 long skinny_workspace_floats(int M, int N) {
     (void)N;
     return dev::kSkPartOff + 32768L * M;

@@ -593,3 +593,51 @@ def test_stream_read_probe(n_bytes):
         src.view(torch.int32)[0] = int(np.uint32(0x9E3779B9).view(np.int32))
         cri.stream_read(src, n_bytes, sink)
         assert np.uint32(host(sink)[0]) == np.uint32(0x9E3779B9)
+
+
+# ------------------------------------------------------------------ cri_matmul_ws
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0", "q6_k", "q4_0"])
+@pytest.mark.parametrize("M,N,K", [(16, 2048, 8192), (12, 512, 4096), (9, 300, 8192), (5, 256, 2048), (2, 1024, 2048)])
+def test_matmul_ws_same_bits_every_call(orc, fmt, M, N, K):
+    # 2..16 rows with a workspace: the K split's partial sums are added in split order, so three
+    # calls give the same bits (the atomic path of cri_matmul need not), within the bar of the oracle
+    A = quant.randn(M * K, seed=M + N + K).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=N + K)
+    need = cri.matmul_workspace_bytes(fmt, M, N, K)
+    assert need > 0
+    ws = torch.empty(need // 4, dtype=torch.float32, device="cuda")
+    dA, dB = dev(A), dev(Bq)
+    outs = []
+    for _ in range(3):
+        C = torch.full((M, N), float("nan"), device="cuda")
+        cri.matmul_ws(fmt, dA, dB, C, M, N, K, ws)
+        outs.append(host(C))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    assert normwise_rel_err(outs[0], orc.matmul_quant(fmt, A, Bq, N, K)) <= GEMV_TOL
+
+
+def test_matmul_ws_errors_and_other_row_counts(orc):
+    fmt, N, K = "q4_k", 512, 2048
+    A = quant.randn(16 * K, seed=3).reshape(16, K)
+    Bq = weights(fmt, N, K, seed=4)
+    need = cri.matmul_workspace_bytes(fmt, 16, N, K)
+    ws = torch.empty(need // 4, dtype=torch.float32, device="cuda")
+    C = torch.empty(16, N, device="cuda")
+    with pytest.raises(cri.CretifError):  # too small
+        cri.matmul_ws(fmt, dev(A), dev(Bq), C, 16, N, K, ws, need - 16)
+    with pytest.raises(cri.CretifError):  # none at all
+        cri.matmul_ws(fmt, dev(A), dev(Bq), C, 16, N, K, None)
+    wide = torch.empty(16, N + 4, device="cuda")
+    with pytest.raises(cri.CretifError):  # C 4 bytes past a 16-byte boundary
+        cri.matmul_ws(fmt, dev(A), dev(Bq), wide.view(-1)[1:1 + 16 * N], 16, N, K, ws)
+    with pytest.raises(cri.CretifError):  # N not a multiple of 4
+        cri.matmul_ws(fmt, dev(A), dev(Bq), C, 16, N - 2, K, ws)
+    with pytest.raises(cri.CretifError):
+        cri.matmul_ws(9, dev(A), dev(Bq), C, 16, N, K, ws)
+    # one row and prefill-sized batches use no workspace (null is fine) and match cri_matmul
+    assert cri.matmul_workspace_bytes(fmt, 1, N, K) == 0 and cri.matmul_workspace_bytes(fmt, 17, N, K) == 0
+    for M in (1, 17):
+        Am = quant.randn(M * K, seed=M).reshape(M, K)
+        C1 = torch.empty(M, N, device="cuda")
+        cri.matmul_ws(fmt, dev(Am), dev(Bq), C1, M, N, K, None)
+        assert normwise_rel_err(host(C1), orc.matmul_quant(fmt, Am, Bq, N, K)) <= tol_for(M)
