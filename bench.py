@@ -45,9 +45,11 @@ PREFILL_WORKLOADS = {
     "q4_k_prefill_down": ("q4_k", 512, 2048, 8192),
     "q6_k_prefill": ("q6_k", 512, 8192, 2048),
     "q6_k_prefill_down": ("q6_k", 512, 2048, 8192),
-    # the LDS-staged kernel (mfma_gemm.hip) that the other formats take
     "q4_0_prefill": ("q4_0", 512, 8192, 2048),
+    "q4_0_prefill_down": ("q4_0", 512, 2048, 8192),
     "q5_0_prefill": ("q5_0", 512, 8192, 2048),
+    "q5_0_prefill_down": ("q5_0", 512, 2048, 8192),
+    # the LDS-staged kernel (mfma_gemm.hip) that FP16 takes
     "fp16_prefill": ("fp16", 512, 8192, 2048),
 }
 

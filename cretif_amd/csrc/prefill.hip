@@ -1,9 +1,10 @@
 // prefill.hip -- fused dequant GEMM for multi-token (prefill) batches on the
-// matrix cores, C[M,N] = A[M,K] * dequant(B[N,K])^T, for Q4_K, Q8_0 and Q6_K
-// weights (the other formats keep the LDS-staged kernel of mfma_gemm.hip).
+// matrix cores, C[M,N] = A[M,K] * dequant(B[N,K])^T, for Q4_K, Q8_0, Q6_K,
+// Q4_0 and Q5_0 weights (FP16 keeps the LDS-staged kernel of mfma_gemm.hip).
 //
 // The reference computes the product with one fp32 FMA chain per output
-// (ref:src/kernels/matmul_quant.cu:64-130 Q8_0, :309-386 Q4_K, :398-498 Q6_K).
+// (ref:src/kernels/matmul_quant.cu:64-130 Q8_0, :142-205 Q4_0, :215-290 Q5_0,
+// :309-386 Q4_K, :398-498 Q6_K).
 // Here:
 //   * a workgroup of eight waves (two per SIMD, so one wave's dependency
 //     stalls are filled by the other's work) owns a 64(m) x 256(n) output
@@ -17,10 +18,11 @@
 //     group of four steps into its own LDS area with coalesced loads, and each
 //     lane decodes the bytes of its own weight row (its output column) from
 //     there in registers, to the reference's dequantized value rounded once to
-//     fp16 (Q8_0: d * q; Q4_K: d * (sc * q) - dmin * mn, sc * q exact; Q6_K:
-//     twice, (q - 32) fp16(d sc)), two weights per packed op;
+//     fp16 (Q8_0: d * q; Q4_0, Q5_0: d * (q - 8), d * (q - 16); Q4_K:
+//     d * (sc * q) - dmin * mn, sc * q exact; Q6_K: twice, (q - 32) fp16(d sc)),
+//     two weights per packed op;
 //   * a lane's bytes of one step are contiguous runs (Q4_K: 16 quant bytes of
-//     the super-block chunk; Q8_0: one whole 34-byte block; Q6_K: 16 bytes of
+//     the super-block chunk; Q8_0, Q4_0, Q5_0: one whole block; Q6_K: 16 bytes of
 //     each of two ql runs and of qh), so the 8 k of
 //     each MFMA sub-step are not consecutive k; the activation fragment of
 //     every sub-step is fetched from the LDS columns of the same k, so the
@@ -125,6 +127,7 @@ struct PQ4K {
     static constexpr int kAreaBytes = 32 * kRowBytes;
     static constexpr int kReadPhase = 0;  // the next step's bytes are read in phase 0
     static constexpr int kMfmaPrio = 0;   // wave priority while issuing a phase's MFMAs (none)
+    static constexpr bool kActSwap = false;  // activation chunks in k order
     static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
     static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return (first_step >> 2) * 144L; }
@@ -201,6 +204,7 @@ struct PQ8_0 {
     static constexpr int kAreaBytes = 32 * kRowBytes;
     static constexpr int kReadPhase = 0;  // the next step's bytes are read in phase 0
     static constexpr int kMfmaPrio = 0;   // wave priority while issuing a phase's MFMAs (none)
+    static constexpr bool kActSwap = false;
     static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
     static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return first_step * 68L; }
@@ -237,6 +241,127 @@ struct PQ8_0 {
     }
 };
 
+// Shared by the two 32-element formats with 4-bit quants below: lane half h decodes block 2j + h of
+// step j, whose fp16 d sits in the low (h = 0) or high (h = 1) half of the first dword the lane reads;
+// sel realigns the bytes after d (two bytes past a dword for h = 0, four for h = 1).
+struct P32Consts {
+    uint32_t d2, sel, qh;
+};
+__device__ __forceinline__ void p32_prep(uint32_t dw0, P32Consts& k) {
+    const bool h1 = (__lane_id() >> 5) != 0;
+    k.d2 = p_perm(dw0, dw0, h1 ? 0x03020302u : 0x01000100u);
+    k.sel = h1 ? 0x07060504u : 0x05040302u;
+}
+
+// ref:src/kernels/dequantize.cu:73-101, x = d * (q - 8), element i the low
+// (even i) or high (odd i) nibble of quant byte i / 2.  Step j covers the
+// 18-byte blocks 2j and 2j + 1 (a group of four steps is 144 bytes per row
+// and starts dword-aligned, K % 256 == 0); lane half h decodes block 2j + h
+// whole from the five dwords at byte 36j + 16h of the group.  Sub-step S is
+// quant bytes 4S .. 4S + 3, elements 8S .. 8S + 7, in the order (0, 2, 1, 3,
+// 4, 6, 5, 7): the low nibbles of two bytes form one fp16 pair, their high
+// nibbles (masked in place, 16 q) the next; the activations are staged in the
+// same order (kActSwap), so the products and sums are those of k order.
+struct PQ4_0 {
+    static constexpr int kFmt = kFmtQ4_0;
+    static constexpr int kBlockK = 32;
+    static constexpr int kRowBytes = 144;
+    static constexpr int kCopyPieces = kRowBytes / 16;
+    static constexpr bool kTail = false;
+    using Piece = u32x4;
+    static constexpr int kAreaBytes = 32 * kRowBytes;
+    static constexpr int kReadPhase = 0;
+    static constexpr int kMfmaPrio = 0;
+    static constexpr bool kActSwap = true;  // chunk halves (x0, x2, x1, x3, x4, x6, x5, x7)
+    static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
+    static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
+    static __device__ __forceinline__ long group_offset(int first_step) { return first_step * 36L; }
+    struct Frag {
+        uint32_t dw[5];
+    };
+    template <int J>
+    static __device__ __forceinline__ void read(Frag& f, const char* row, int h) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 36 * J + 16 * h);
+#pragma unroll
+        for (int i = 0; i < 5; ++i) f.dw[i] = p[i];
+    }
+    static __device__ __forceinline__ constexpr int chunk(int s, int h) { return 4 * h + s; }
+    using Consts = P32Consts;
+    template <int J>
+    static __device__ __forceinline__ void prep(const Frag& f, Consts& k) {
+        p32_prep(f.dw[0], k);
+    }
+    // B fragment of sub-step S: d (q - 8), one rounding to fp16; (1024 + q) - 1032 and
+    // (1024 + 16 q) / 16 - 72 are exact
+    template <int J, int S>
+    static __device__ __forceinline__ void sub(const Frag& f, const Consts& k, uint32_t (&b)[4]) {
+        const uint32_t w = p_perm(f.dw[S + 1], f.dw[S], k.sel);
+        const uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;
+        const uint32_t bl = p_const(-1032.0f, -1032.0f);
+        const uint32_t c16 = p_const(0.0625f, 0.0625f), bh = p_const(-72.0f, -72.0f);
+        b[0] = p_mul(p_add(p_mlo(lo), bl), k.d2);        // elements 8S, 8S + 2
+        b[1] = p_mul(p_fma(p_mlo(hi), c16, bh), k.d2);   // 8S + 1, 8S + 3
+        b[2] = p_mul(p_add(p_mhi(lo), bl), k.d2);        // 8S + 4, 8S + 6
+        b[3] = p_mul(p_fma(p_mhi(hi), c16, bh), k.d2);   // 8S + 5, 8S + 7
+    }
+};
+
+// ref:src/kernels/dequantize.cu:126-165, x = d * (q - 16) with q = the low
+// (element i < 16) or high (i >= 16) nibble of qs[i % 16] and bit i of qh as
+// bit 4.  Step j covers the 22-byte blocks 2j and 2j + 1 (176 bytes per row
+// and group); lane half h decodes block 2j + h from the six dwords at byte
+// 44j + 20h.  Sub-step S is elements 8S .. 8S + 7 in k order: the low (S < 2)
+// or high nibbles of qs dwords 2 (S & 1), + 1.  Each element becomes the fp16
+// 1024 + 16 q: its nibble times 16 in the low byte and its qh bit as bit 0 of
+// the 0x64 high byte (256 = 16 * 16).
+struct PQ5_0 {
+    static constexpr int kFmt = kFmtQ5_0;
+    static constexpr int kBlockK = 32;
+    static constexpr int kRowBytes = 176;
+    static constexpr int kCopyPieces = kRowBytes / 16;
+    static constexpr bool kTail = false;
+    using Piece = u32x4;
+    static constexpr int kAreaBytes = 32 * kRowBytes;
+    static constexpr int kReadPhase = 0;
+    static constexpr int kMfmaPrio = 0;
+    static constexpr bool kActSwap = false;
+    static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
+    static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
+    static __device__ __forceinline__ long group_offset(int first_step) { return first_step * 44L; }
+    struct Frag {
+        uint32_t dw[6];
+    };
+    template <int J>
+    static __device__ __forceinline__ void read(Frag& f, const char* row, int h) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 44 * J + 20 * h);
+#pragma unroll
+        for (int i = 0; i < 6; ++i) f.dw[i] = p[i];
+    }
+    static __device__ __forceinline__ constexpr int chunk(int s, int h) { return 4 * h + s; }
+    using Consts = P32Consts;
+    template <int J>
+    static __device__ __forceinline__ void prep(const Frag& f, Consts& k) {
+        p32_prep(f.dw[0], k);
+        k.qh = p_perm(f.dw[1], f.dw[0], k.sel);
+    }
+    // B fragment of sub-step S: d (q - 16), one rounding to fp16; (1024 + 16 q) / 16 - 80 is exact
+    template <int J, int S>
+    static __device__ __forceinline__ void sub(const Frag& f, const Consts& k, uint32_t (&b)[4]) {
+        const uint32_t c16 = p_const(0.0625f, 0.0625f), bias = p_const(-80.0f, -80.0f);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int t = 2 * (S & 1) + i;  // qs dword: elements 8S + 4i .. + 3 in its bytes
+            const uint32_t w = p_perm(f.dw[t + 2], f.dw[t + 1], k.sel);
+            const uint32_t u = (S >= 2 ? w : (w << 4)) & 0xF0F0F0F0u;
+            // their four qh bits to bit 0 of the bytes of 0x64646464 (the products do not overlap)
+            const uint32_t n = (k.qh >> (8 * S + 4 * i)) & 0xFu;
+            const uint32_t mw = (__umul24(n, 0x204081u) & 0x01010101u) | 0x64646464u;
+            b[2 * i] = p_mul(p_fma(p_perm(mw, u, 0x05010400u), c16, bias), k.d2);
+            b[2 * i + 1] = p_mul(p_fma(p_perm(mw, u, 0x07030602u), c16, bias), k.d2);
+        }
+    }
+};
+
 // ref:src/kernels/dequantize.cu:179-244, x = d * sc * (q - 32) with q the 6-bit
 // value of a low/high nibble of ql and two bits of qh.  Step j of a super-block
 // is its 64 elements 64j ..: half c = j / 2 (128 elements), quarters 2 (j & 1) +
@@ -269,6 +394,7 @@ struct PQ6K {
     // measured 46.5 -> 44.8-45.2 us at 512 x 8192 x 2048, the down shape unchanged (Q4_K and Q8_0
     // ran 1-3% slower with it)
     static constexpr int kMfmaPrio = 3;
+    static constexpr bool kActSwap = false;
     static __device__ __forceinline__ long group_offset(int first_step) { return (first_step >> 2) * 210L; }
     struct Piece {
         u32x4 v;     // the 16 bytes from the dword boundary
@@ -469,8 +595,11 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         const f32x4 v = av[j][i];
         const float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
         amax[i] = fmaxf(amax[i], mx);
-        const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(pf2{v.x, v.y}, ph2));
-        const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(pf2{v.z, v.w}, ph2));
+        // kActSwap: halves (x0, x2, x1, x3) of the thread's four columns, the B order of PQ4_0
+        const pf2 p0 = W::kActSwap ? pf2{v.x, v.z} : pf2{v.x, v.y};
+        const pf2 p1 = W::kActSwap ? pf2{v.y, v.w} : pf2{v.z, v.w};
+        const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(p0, ph2));
+        const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(p1, ph2));
         *reinterpret_cast<pu2*>(buf + j * kPStage + aw[i]) = pu2{lo, hi};
     };
     auto afrag = [&](const char* tile, int u, int s) { return *reinterpret_cast<const ph8*>(tile + aoff[u][s]); };
@@ -625,8 +754,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 namespace detail {
 
 bool prefill_supported(int fmt, int M, int N, int K, const void* A, const void* B) {
-    if (fmt != kFmtQ4_K && fmt != kFmtQ8_0 && fmt != kFmtQ6_K) return false;
-    // whole groups of four 64-column steps (one Q4_K / Q6_K super-block, 272 bytes of a Q8_0 row)
+    if (fmt != kFmtQ4_K && fmt != kFmtQ8_0 && fmt != kFmtQ6_K && fmt != kFmtQ4_0 && fmt != kFmtQ5_0) return false;
+    // whole groups of four 64-column steps (one Q4_K / Q6_K super-block, eight 32-element blocks)
     if (M < 1 || N < 1 || K < 4 * dev::kPKS || K % (4 * dev::kPKS) != 0) return false;
     if (static_cast<long>(M) * K >= (1L << 31) || 32 * row_bytes(fmt, K) >= (1L << 31)) return false;
     const uintptr_t a = reinterpret_cast<uintptr_t>(A), b = reinterpret_cast<uintptr_t>(B);
@@ -678,6 +807,8 @@ int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int 
     const uint8_t* Bb = static_cast<const uint8_t*>(B);
     if (fmt == kFmtQ4_K) return launch_w<dev::PQ4K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
     if (fmt == kFmtQ6_K) return launch_w<dev::PQ6K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
+    if (fmt == kFmtQ4_0) return launch_w<dev::PQ4_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
+    if (fmt == kFmtQ5_0) return launch_w<dev::PQ5_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
     return launch_w<dev::PQ8_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
 }
 
