@@ -1,10 +1,11 @@
 // prefill.hip -- fused dequant GEMM for multi-token (prefill) batches on the
 // matrix cores, C[M,N] = A[M,K] * dequant(B[N,K])^T, for Q4_K, Q8_0, Q6_K,
-// Q4_0 and Q5_0 weights (FP16 keeps the LDS-staged kernel of mfma_gemm.hip).
+// Q4_0, Q5_0 and FP16 weights with K % 256 == 0 (other K keep the LDS-staged
+// kernel of mfma_gemm.hip).
 //
 // The reference computes the product with one fp32 FMA chain per output
 // (ref:src/kernels/matmul_quant.cu:64-130 Q8_0, :142-205 Q4_0, :215-290 Q5_0,
-// :309-386 Q4_K, :398-498 Q6_K).
+// :309-386 Q4_K, :398-498 Q6_K, :510-557 FP16).
 // Here:
 //   * a workgroup of eight waves (two per SIMD, so one wave's dependency
 //     stalls are filled by the other's work) owns a 64(m) x 256(n) output
@@ -15,7 +16,9 @@
 //     double-buffered LDS tile of 64 rows x 64 halves, which all eight waves
 //     read (8 ds_read_b128 per wave and step);
 //   * weights are the B operand: each wave copies its 32 rows' bytes of a
-//     group of four steps into its own LDS area with coalesced loads, and each
+//     group of four steps into its own LDS area with coalesced loads (FP16,
+//     with nothing to decode, loads each lane's bytes straight into its B
+//     fragments instead: kDirect), and each
 //     lane decodes the bytes of its own weight row (its output column) from
 //     there in registers, to the reference's dequantized value rounded once to
 //     fp16 (Q8_0: d * q; Q4_0, Q5_0: d * (q - 8), d * (q - 16); Q4_K:
@@ -128,6 +131,7 @@ struct PQ4K {
     static constexpr int kReadPhase = 0;  // the next step's bytes are read in phase 0
     static constexpr int kMfmaPrio = 0;   // wave priority while issuing a phase's MFMAs (none)
     static constexpr bool kActSwap = false;  // activation chunks in k order
+    static constexpr bool kDirect = false;  // bytes copied through the wave's LDS area
     static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
     static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return (first_step >> 2) * 144L; }
@@ -205,6 +209,7 @@ struct PQ8_0 {
     static constexpr int kReadPhase = 0;  // the next step's bytes are read in phase 0
     static constexpr int kMfmaPrio = 0;   // wave priority while issuing a phase's MFMAs (none)
     static constexpr bool kActSwap = false;
+    static constexpr bool kDirect = false;  // bytes copied through the wave's LDS area
     static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
     static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return first_step * 68L; }
@@ -273,6 +278,7 @@ struct PQ4_0 {
     static constexpr int kReadPhase = 0;
     static constexpr int kMfmaPrio = 0;
     static constexpr bool kActSwap = true;  // chunk halves (x0, x2, x1, x3, x4, x6, x5, x7)
+    static constexpr bool kDirect = false;  // bytes copied through the wave's LDS area
     static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
     static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return first_step * 36L; }
@@ -325,6 +331,7 @@ struct PQ5_0 {
     static constexpr int kReadPhase = 0;
     static constexpr int kMfmaPrio = 0;
     static constexpr bool kActSwap = false;
+    static constexpr bool kDirect = false;  // bytes copied through the wave's LDS area
     static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
     static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return first_step * 44L; }
@@ -362,6 +369,46 @@ struct PQ5_0 {
     }
 };
 
+// ref:src/kernels/matmul_quant.cu:510-557, FP16 weights: no decode, so there is
+// no copy through LDS either (a group's 512 bytes per row would take 16 KB of
+// LDS per wave); each lane loads its own bytes of a step straight from global
+// memory into the registers that are its B fragments, two steps ahead of the
+// MFMAs that use them (kDirect).  Lane half h takes the step's columns
+// 32h .. 32h + 31, 64 contiguous bytes of its row; sub-step S is columns
+// 32h + 8S .. + 8, k order.  The eight m blocks that share a weight block run
+// back to back on one XCD, so most of these loads are L2 hits.
+struct PF16 {
+    static constexpr int kFmt = kFmtF16;
+    static constexpr int kRowBytes = 0;
+    static constexpr int kCopyPieces = 0;
+    static constexpr bool kTail = false;
+    static constexpr bool kDirect = true;
+    using Piece = u32x4;
+    static constexpr int kAreaBytes = 0;
+    static constexpr int kReadPhase = 0;
+    static constexpr int kMfmaPrio = 0;
+    static constexpr bool kActSwap = false;
+    struct Frag {
+        u32x4 q[4];
+    };
+    // p: the lane's row, plus 128 bytes per step and 64 h
+    static __device__ __forceinline__ void read_direct(Frag& f, const uint8_t* p) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) f.q[s] = p_load16(p + 16 * s);
+    }
+    static __device__ __forceinline__ constexpr int chunk(int s, int h) { return 4 * h + s; }
+    struct Consts {};
+    template <int J>
+    static __device__ __forceinline__ void prep(const Frag&, Consts&) {}
+    template <int J, int S>
+    static __device__ __forceinline__ void sub(const Frag& f, const Consts&, uint32_t (&b)[4]) {
+        b[0] = f.q[S].x;
+        b[1] = f.q[S].y;
+        b[2] = f.q[S].z;
+        b[3] = f.q[S].w;
+    }
+};
+
 // ref:src/kernels/dequantize.cu:179-244, x = d * sc * (q - 32) with q the 6-bit
 // value of a low/high nibble of ql and two bits of qh.  Step j of a super-block
 // is its 64 elements 64j ..: half c = j / 2 (128 elements), quarters 2 (j & 1) +
@@ -395,6 +442,7 @@ struct PQ6K {
     // ran 1-3% slower with it)
     static constexpr int kMfmaPrio = 3;
     static constexpr bool kActSwap = false;
+    static constexpr bool kDirect = false;  // bytes copied through the wave's LDS area
     static __device__ __forceinline__ long group_offset(int first_step) { return (first_step >> 2) * 210L; }
     struct Piece {
         u32x4 v;     // the 16 bytes from the dword boundary
@@ -528,19 +576,23 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     // group's 32 * kCopyPieces pieces -> row c / kCopyPieces, piece c % kCopyPieces, stored at
     // byte 16 c of the wave's area (rows kRowBytes = 16 kCopyPieces apart), tails after the rows
     constexpr int kPieces = W::kCopyPieces, kChunks = 32 * kPieces, kLoads = (kChunks + 63) / 64;
+    constexpr int kLoadsA = kLoads > 0 ? kLoads : 1;  // array extent (kDirect formats copy nothing)
     const int n0c = min(n0, N - 1);
     const uint8_t* const wbase = B + static_cast<long>(n0c) * row_bytes;
-    int woff[kLoads];  // < 32 rows: 32 * row_bytes < 2^31 is a launch condition
+    int woff[kLoadsA];  // < 32 rows: 32 * row_bytes < 2^31 is a launch condition
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
+        constexpr int kP = kPieces > 0 ? kPieces : 1;
         const int c = min(64 * i + lane, kChunks - 1);
-        const int r = c / kPieces;
-        woff[i] = (min(n0 + r, N - 1) - n0c) * static_cast<int>(row_bytes) + 16 * (c % kPieces);
+        const int r = c / kP;
+        woff[i] = (min(n0 + r, N - 1) - n0c) * static_cast<int>(row_bytes) + 16 * (c % kP);
     }
     // kTail formats: lane l (and l + 32, a duplicate) reads row l's tail dword
     const int wtoff = (min(n0 + (lane & 31), N - 1) - n0c) * static_cast<int>(row_bytes);
     char* const warea = lds + 8 * kPStage + wave * W::kAreaBytes;
     const char* const wrow = warea + fr * W::kRowBytes;  // this lane's row in the area
+    // kDirect formats: this lane's bytes of its row, 2 * kPKS bytes per step
+    const uint8_t* const grow = B + static_cast<long>(min(n0 + fr, N - 1)) * row_bytes + kPKS * h;
 
     // A-operand fetch offsets: m tile u, sub-step s -> row 32 u + fr, the chunk of the
     // k that this half-wave's B fragment holds
@@ -571,24 +623,29 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const int ngrp = nst >> 2;
     auto step_of = [&](int t) { return s_begin + min(t, nst - 1); };
     f32x4 av[4][2];  // activations of the next group: [step][row]
-    typename W::Piece wr[kLoads];  // weight bytes of the next group
+    typename W::Piece wr[kLoadsA];  // weight bytes of the next group
     uint32_t wt = 0;               // kTail formats: this lane's row's tail dword of the next group
     auto load_next = [&](int q) {
-        const uint8_t* g = wbase + W::group_offset(step_of(4 * q));
+        if constexpr (!W::kDirect) {
+            const uint8_t* g = wbase + W::group_offset(step_of(4 * q));
 #pragma unroll
-        for (int i = 0; i < kLoads; ++i) wr[i] = W::load_piece(g + woff[i]);
-        if constexpr (W::kTail) wt = W::load_tail(g + wtoff);
+            for (int i = 0; i < kLoads; ++i) wr[i] = W::load_piece(g + woff[i]);
+            if constexpr (W::kTail) wt = W::load_tail(g + wtoff);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < 2; ++i) av[j][i] = ld_f32x4(abase + step_of(4 * q + j) * kPKS + arow_off[i]);
     };
     auto write_w = [&]() {
+        if constexpr (!W::kDirect) {
 #pragma unroll
-        for (int i = 0; i < kLoads; ++i)
-            if (64 * i + lane < kChunks) *reinterpret_cast<u32x4*>(warea + 16 * (64 * i + lane)) = W::piece_bytes(wr[i]);
-        if constexpr (W::kTail)
-            if (lane < 32) *reinterpret_cast<uint32_t*>(warea + 32 * W::kRowBytes + 4 * lane) = wt;
+            for (int i = 0; i < kLoads; ++i)
+                if (64 * i + lane < kChunks)
+                    *reinterpret_cast<u32x4*>(warea + 16 * (64 * i + lane)) = W::piece_bytes(wr[i]);
+            if constexpr (W::kTail)
+                if (lane < 32) *reinterpret_cast<uint32_t*>(warea + 32 * W::kRowBytes + 4 * lane) = wt;
+        }
     };
     // step j, row i of the next group into buffer buf (tile j)
     auto stage = [&](char* buf, int j, int i) {
@@ -621,7 +678,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     // the bytes of the step after next (fn, position J + 1), after writing the
     // next group's weight bytes when J == 3.  The phases are fenced so the
     // compiler keeps this order.
-    auto iter = [&](auto pos, const ph8 (&ac)[2][4], ph8 (&an)[2][4], const char* next_tile,
+    auto iter = [&](auto pos, int q, const ph8 (&ac)[2][4], ph8 (&an)[2][4], const char* next_tile,
                     const uint32_t (&bc)[4][4], uint32_t (&bn)[4][4], const typename W::Frag& fc,
                     typename W::Frag& fn, char* nxt) {
         constexpr int J = decltype(pos)::value;
@@ -642,7 +699,12 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
             if (s == 1) W::template sub<J, 1>(fc, k, bn[1]);
             if (s == 2) W::template sub<J, 2>(fc, k, bn[2]);
             if (s == 3) W::template sub<J, 3>(fc, k, bn[3]);
-            if (s == W::kReadPhase) W::template read<(J + 1) & 3>(fn, wrow, h);
+            if (s == W::kReadPhase) {
+                if constexpr (W::kDirect)  // step 4q + J + 1 (4q + 5 in the group's last iteration)
+                    W::read_direct(fn, grow + static_cast<long>(step_of(4 * q + (J == 0 ? 5 : J + 1))) * (2 * kPKS));
+                else
+                    W::template read<(J + 1) & 3>(fn, wrow, h);
+            }
             if constexpr (kLast) {
                 stage(nxt, s, 0);
                 stage(nxt, s, 1);
@@ -662,10 +724,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4) fa[u][s4] = afrag(rd, u, s4);
         load_next(q + 1);
-        iter(pos_t<1>{}, fa, fb, rd + kPStage, x, y, f1, f0, wr_buf);
-        iter(pos_t<2>{}, fb, fa, rd + 2 * kPStage, y, x, f0, f1, wr_buf);
-        iter(pos_t<3>{}, fa, fb, rd + 3 * kPStage, x, y, f1, f0, wr_buf);
-        iter(pos_t<0>{}, fb, fa, rd, y, x, f0, f1, wr_buf);
+        iter(pos_t<1>{}, q, fa, fb, rd + kPStage, x, y, f1, f0, wr_buf);
+        iter(pos_t<2>{}, q, fb, fa, rd + 2 * kPStage, y, x, f0, f1, wr_buf);
+        iter(pos_t<3>{}, q, fa, fb, rd + 3 * kPStage, x, y, f1, f0, wr_buf);
+        iter(pos_t<0>{}, q, fb, fa, rd, y, x, f0, f1, wr_buf);
         __syncthreads();
     };
 
@@ -677,7 +739,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         stage(lds, j, 0);
         stage(lds, j, 1);
     }
-    W::template read<0>(f0, wrow, h);
+    if constexpr (W::kDirect)
+        W::read_direct(f0, grow + static_cast<long>(step_of(0)) * (2 * kPKS));
+    else
+        W::template read<0>(f0, wrow, h);
     {
         typename W::Consts k;
         W::template prep<0>(f0, k);
@@ -686,14 +751,31 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         W::template sub<0, 2>(f0, k, b0[2]);
         W::template sub<0, 3>(f0, k, b0[3]);
     }
-    W::template read<1>(f1, wrow, h);
+    if constexpr (W::kDirect)
+        W::read_direct(f1, grow + static_cast<long>(step_of(1)) * (2 * kPKS));
+    else
+        W::template read<1>(f1, wrow, h);
     __syncthreads();
     char* const buf0 = lds;
     char* const buf1 = lds + 4 * kPStage;
-    for (int q = 0; q < ngrp; q += 2) {
-        group(q, buf0, buf1, b0, b1);
-        if (q + 1 >= ngrp) break;
-        group(q + 1, buf1, buf0, b0, b1);
+    if constexpr (W::kDirect) {
+        // one group per trip, the buffers swapped: the global loads of the next group's first
+        // steps (issued in this group's last two iterations) stay ahead of their use; after an
+        // unrolled pair with a break between them the compiler sinks them past the break
+        char* rd = buf0;
+        char* wb = buf1;
+        for (int q = 0; q < ngrp; ++q) {
+            group(q, rd, wb, b0, b1);
+            char* const t = rd;
+            rd = wb;
+            wb = t;
+        }
+    } else {
+        for (int q = 0; q < ngrp; q += 2) {
+            group(q, buf0, buf1, b0, b1);
+            if (q + 1 >= ngrp) break;
+            group(q + 1, buf1, buf0, b0, b1);
+        }
     }
 
     // rows whose activations left fp16's range take the fp32 path below
@@ -754,7 +836,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 namespace detail {
 
 bool prefill_supported(int fmt, int M, int N, int K, const void* A, const void* B) {
-    if (fmt != kFmtQ4_K && fmt != kFmtQ8_0 && fmt != kFmtQ6_K && fmt != kFmtQ4_0 && fmt != kFmtQ5_0) return false;
+    if (fmt != kFmtQ4_K && fmt != kFmtQ8_0 && fmt != kFmtQ6_K && fmt != kFmtQ4_0 && fmt != kFmtQ5_0 && fmt != kFmtF16)
+        return false;
     // whole groups of four 64-column steps (one Q4_K / Q6_K super-block, eight 32-element blocks)
     if (M < 1 || N < 1 || K < 4 * dev::kPKS || K % (4 * dev::kPKS) != 0) return false;
     if (static_cast<long>(M) * K >= (1L << 31) || 32 * row_bytes(fmt, K) >= (1L << 31)) return false;
@@ -809,6 +892,7 @@ int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int 
     if (fmt == kFmtQ6_K) return launch_w<dev::PQ6K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
     if (fmt == kFmtQ4_0) return launch_w<dev::PQ4_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
     if (fmt == kFmtQ5_0) return launch_w<dev::PQ5_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
+    if (fmt == kFmtF16) return launch_w<dev::PF16>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
     return launch_w<dev::PQ8_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
 }
 

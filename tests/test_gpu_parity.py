@@ -333,13 +333,14 @@ def test_q6_k_prefill_super_block_alignments(orc, K, off):
     assert normwise_rel_err(host(C), orc.matmul_quant("q6_k", A, Bq, N, K)) <= PREFILL_TOL
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q5_0", "q8_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q5_0", "q8_0", "fp16"])
 @pytest.mark.parametrize("off", [0, 2, 4])
 @pytest.mark.parametrize("N", [33, 64])
-def test_prefill_32_element_block_alignments(orc, fmt, off, N):
-    # the register-decode prefill kernel reads 18 / 22 / 34-byte blocks from dword-aligned rows
-    # (offsets 0 and 4; 4 is not 16-byte aligned); at offset 2 the rows are not dword-aligned and
-    # the LDS-staged kernel takes the product.  The weights end where the buffer does.
+def test_prefill_block_alignments(orc, fmt, off, N):
+    # the register-decode prefill kernel reads 18 / 22 / 34-byte blocks (FP16: each lane's 64
+    # bytes of a step) from dword-aligned rows (offsets 0 and 4; 4 is not 16-byte aligned); at
+    # offset 2 the rows are not dword-aligned and the LDS-staged kernel takes the product.  The
+    # weights end where the buffer does.
     M, K = 40, 512
     A = quant.randn(M * K, seed=N + off).reshape(M, K)
     Bq = weights(fmt, N, K, seed=N + off + 1)
@@ -384,7 +385,7 @@ def test_prefill_matches_oracle(orc, fmt, M, N, K):
     assert err <= PREFILL_TOL, err
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q4_k", "q6_k", "q4_0", "q5_0"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_k", "q6_k", "q4_0", "q5_0", "fp16"])
 @pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192)])
 def test_prefill_baseline_config(orc, fmt, N, K):
     # 512 tokens x Llama-3.2-1B FFN gate/up and down, every output against the oracle (its
@@ -469,9 +470,9 @@ def test_prefill_large_activations(orc):
 def test_prefill_activation_range(orc, fmt, case):
     # fp16 holds |x| < 65504, and rows of very small values only as subnormals: rows of
     # activations ~1e5 (inf in fp16) or ~1e-7 must still meet the bar, each row against its own
-    # norm; 'mixed' puts such rows among ordinary ones (and into a split-k launch).  The quantized
-    # formats with K % 256 == 0 run the register-decode prefill kernel, FP16 and q8_0 at K = 576
-    # the LDS-staged one; both flag such rows and recompute them in fp32.
+    # norm; 'mixed' puts such rows among ordinary ones (and into a split-k launch).  Every format
+    # with K % 256 == 0 runs the register-decode prefill kernel, q8_0 at K = 576 the LDS-staged
+    # one; both flag such rows and recompute them in fp32.
     M, N, K = (64, 300, 2048) if case != "mixed" else (40, 128, 8192)
     if fmt == "q8_0_k576":
         fmt, K = "q8_0", 576
