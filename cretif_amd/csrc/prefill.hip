@@ -99,6 +99,21 @@ __device__ __forceinline__ u32x4 p_load16(const uint8_t* p) {
     return u32x4{v.x, v.y, v.z, v.w};
 }
 
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt left at their
+// no-wait maxima).  The compiler does not order a global_load_lds into LDS before later ds_reads
+// of the same bytes, so the FP16 path waits for its copies itself.
+template <int N>
+__device__ __forceinline__ void p_wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS tile of 64 fp16 columns per row (activations; FP16 weight steps): row r
+// (128 bytes) holds 8 chunks of 8 halves; chunk c is stored in slot c ^ (r & 7)
+// ^ ((r >> 3) & 1) (conflict-free for 32-row operand fetches, one chunk per
+// half-wave).
+__device__ __forceinline__ int p_off(int r, int c) { return (r << 7) + ((c ^ (r & 7) ^ ((r >> 3) & 1)) << 4); }
+
 // ---------------------------------------------------------------------------
 // B-operand formats.  A wave's weight bytes of one group (four k steps) are
 // kCopyPieces 16-byte pieces of each of its 32 rows (load_piece from the row's
@@ -373,14 +388,18 @@ struct PQ5_0 {
     }
 };
 
-// ref:src/kernels/matmul_quant.cu:510-557, FP16 weights: no decode, so there is
-// no copy through LDS either (a group's 512 bytes per row would take 16 KB of
-// LDS per wave); each lane loads its own bytes of a step straight from global
-// memory into the registers that are its B fragments, two steps ahead of the
-// MFMAs that use them (kDirect).  Lane half h takes the step's columns
-// 32h .. 32h + 31, 64 contiguous bytes of its row; sub-step S is columns
-// 32h + 8S .. + 8, k order.  The eight m blocks that share a weight block run
-// back to back on one XCD, so most of these loads are L2 hits.
+// ref:src/kernels/matmul_quant.cu:510-557, FP16 weights: nothing to decode, but
+// 512 bytes per row and group (16 KB of LDS per wave, more than the area
+// allows), so the copy is per step instead (kDirect): each wave's 32 rows x 128
+// bytes of a step go to LDS in four global_load_lds_dwordx4 (one row per 8
+// lanes, so each cache line is requested once, and no registers), into a ring of
+// three step buffers in the activation tile's swizzled layout; the copy of step
+// t + 3 is issued while step t is multiplied, and lanes read their B fragments
+// (lane half h: columns 32h .. 32h + 31, sub-step S: 32h + 8S .. + 8, k order)
+// one step ahead, as the other formats do.  Loading each lane's 64 bytes of its
+// own row straight into registers instead touches 32 cache lines per load
+// instruction: 44.6 us at 512 x 8192 x 2048, against 32.3 us for the same loads
+// made coalesced.
 struct PF16 {
     static constexpr int kFmt = kFmtF16;
     static constexpr int kRowBytes = 0;
@@ -389,17 +408,18 @@ struct PF16 {
     static constexpr bool kDirect = true;
     static constexpr bool kOneGroupPerTrip = true;
     using Piece = u32x4;
-    static constexpr int kAreaBytes = 0;
+    static constexpr int kStepBytes = 32 * 128;     // one step buffer of the wave's rows
+    static constexpr int kAreaBytes = 3 * kStepBytes;
     static constexpr int kReadPhase = 0;
     static constexpr int kMfmaPrio = 0;
     static constexpr bool kActSwap = false;
     struct Frag {
         u32x4 q[4];
     };
-    // p: the lane's row, plus 128 bytes per step and 64 h
-    static __device__ __forceinline__ void read_direct(Frag& f, const uint8_t* p) {
+    // buf: the step's buffer; fr: the lane's row
+    static __device__ __forceinline__ void read_buf(Frag& f, const char* buf, int fr, int h) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) f.q[s] = p_load16(p + 16 * s);
+        for (int s = 0; s < 4; ++s) f.q[s] = *reinterpret_cast<const u32x4*>(buf + p_off(fr, 4 * h + s));
     }
     static __device__ __forceinline__ constexpr int chunk(int s, int h) { return 4 * h + s; }
     struct Consts {};
@@ -528,10 +548,6 @@ struct PQ6K {
     }
 };
 
-// LDS activation tile: row r (128 bytes) holds 8 chunks of 8 halves; chunk c is
-// stored in slot c ^ (r & 7) ^ ((r >> 3) & 1) (conflict-free for 32-row
-// operand fetches, one chunk per half-wave).
-__device__ __forceinline__ int p_off(int r, int c) { return (r << 7) + ((c ^ (r & 7) ^ ((r >> 3) & 1)) << 4); }
 
 template <int J>
 using pos_t = std::integral_constant<int, J>;
@@ -598,8 +614,16 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const int wtoff = (min(n0 + (lane & 31), N - 1) - n0c) * static_cast<int>(row_bytes);
     char* const warea = lds + 8 * kPStage + wave * W::kAreaBytes;
     const char* const wrow = warea + fr * W::kRowBytes;  // this lane's row in the area
-    // kDirect formats: this lane's bytes of its row, 2 * kPKS bytes per step
-    const uint8_t* const grow = B + static_cast<long>(min(n0 + fr, N - 1)) * row_bytes + kPKS * h;
+    // kDirect formats: copy instruction i of a step takes row r = 8 i + lane / 8 of the wave's
+    // rows; its lane writes LDS bytes 16 lane of the instruction's kilobyte, which p_off puts at
+    // chunk c = (lane & 7) ^ (r & 7) ^ ((r >> 3) & 1) of row r
+    int doff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 8 * i + (lane >> 3);
+        const int c = (lane & 7) ^ (r & 7) ^ ((r >> 3) & 1);
+        doff[i] = (min(n0 + r, N - 1) - n0c) * static_cast<int>(row_bytes) + 16 * c;
+    }
 
     // A-operand fetch offsets: m tile u, sub-step s -> row 32 u + fr, the chunk of the
     // k that this half-wave's B fragment holds
@@ -629,6 +653,14 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     // values are that step's again, so the range guard's maxima stay the same).
     const int ngrp = nst >> 2;
     auto step_of = [&](int t) { return s_begin + min(t, nst - 1); };
+    // relative step t of the split -> its buffer in the ring (kDirect)
+    auto step_buf = [&](int t) { return warea + (t % 3) * 4096; };
+    auto dma = [&](int t) {
+        char* const buf = step_buf(t);
+        const uint8_t* const g = wbase + static_cast<long>(step_of(t)) * (2 * kPKS);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) __builtin_amdgcn_global_load_lds(g + doff[i], buf + 1024 * i, 16, 0, 0);
+    };
     f32x4 av[4][2];  // activations of the next group: [step][row]
     typename W::Piece wr[kLoadsA];  // weight bytes of the next group
     uint32_t wt = 0;               // kTail formats: this lane's row's tail dword of the next group
@@ -690,6 +722,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
                     typename W::Frag& fn, char* nxt) {
         constexpr int J = decltype(pos)::value;
         constexpr bool kLast = J == 0;  // the group's last iteration decodes the next group's first step
+        const int tr = 4 * q + (J == 0 ? 5 : J + 1);  // the step whose bytes this iteration reads
         typename W::Consts k;
         W::template prep<J>(fc, k);
         __builtin_amdgcn_sched_barrier(0);
@@ -707,10 +740,23 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
             if (s == 2) W::template sub<J, 2>(fc, k, bn[2]);
             if (s == 3) W::template sub<J, 3>(fc, k, bn[3]);
             if (s == W::kReadPhase) {
-                if constexpr (W::kDirect)  // step 4q + J + 1 (4q + 5 in the group's last iteration)
-                    W::read_direct(fn, grow + static_cast<long>(step_of(4 * q + (J == 0 ? 5 : J + 1))) * (2 * kPKS));
-                else
+                if constexpr (W::kDirect) {
+                    // step t = 4q + J + 1 (4q + 5 in the group's last iteration), copied one
+                    // iteration earlier: the group's first iteration has this group's eight
+                    // activation loads behind that copy, the others nothing older to spare.
+                    // Then the copy of step t + 1, into the buffer of the step this iteration
+                    // multiplies (its fragments were read two iterations ago); the last
+                    // iteration's copy is issued at the next group's start instead, since the
+                    // barrier waits for every copy in flight
+                    if constexpr (J == 1)
+                        p_wait_vm<8>();
+                    else
+                        p_wait_vm<0>();
+                    W::read_buf(fn, step_buf(tr), fr, h);
+                    if constexpr (!kLast) dma(tr + 1);
+                } else {
                     W::template read<(J + 1) & 3>(fn, wrow, h);
+                }
             }
             if constexpr (kLast) {
                 stage(nxt, s, 0);
@@ -730,6 +776,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4) fa[u][s4] = afrag(rd, u, s4);
+        if constexpr (W::kDirect) {
+            dma(4 * q + 2);  // before the eight activation loads: the first iteration's wait counts them
+            __builtin_amdgcn_sched_barrier(0);
+        }
         load_next(q + 1);
         iter(pos_t<1>{}, q, fa, fb, rd + kPStage, x, y, f1, f0, wr_buf);
         iter(pos_t<2>{}, q, fb, fa, rd + 2 * kPStage, y, x, f0, f1, wr_buf);
@@ -739,6 +789,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     };
 
     uint32_t b0[4][4], b1[4][4];
+    if constexpr (W::kDirect) {
+        dma(0);
+        dma(1);
+    }
     load_next(0);
     write_w();
 #pragma unroll
@@ -746,9 +800,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         stage(lds, j, 0);
         stage(lds, j, 1);
     }
-    if constexpr (W::kDirect)
-        W::read_direct(f0, grow + static_cast<long>(step_of(0)) * (2 * kPKS));
-    else
+    if constexpr (W::kDirect) {
+        p_wait_vm<0>();  // the copies of steps 0 and 1
+        W::read_buf(f0, step_buf(0), fr, h);
+    } else
         W::template read<0>(f0, wrow, h);
     {
         typename W::Consts k;
@@ -759,7 +814,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         W::template sub<0, 3>(f0, k, b0[3]);
     }
     if constexpr (W::kDirect)
-        W::read_direct(f1, grow + static_cast<long>(step_of(1)) * (2 * kPKS));
+        W::read_buf(f1, step_buf(1), fr, h);
     else
         W::template read<1>(f1, wrow, h);
     __syncthreads();
@@ -785,6 +840,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
             group(q + 1, buf1, buf0, b0, b1);
         }
     }
+
+    // kDirect: the copies issued for steps past the split's end land before the workgroup's LDS
+    // is released
+    if constexpr (W::kDirect) p_wait_vm<0>();
 
     // rows whose activations left fp16's range take the fp32 path below
 #pragma unroll

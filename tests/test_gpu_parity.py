@@ -339,7 +339,7 @@ def test_q6_k_prefill_super_block_alignments(orc, K, off):
 def test_prefill_block_alignments(orc, fmt, off, N):
     # the register-decode prefill kernel reads 18 / 22 / 34-byte blocks (FP16: each lane's 64
     # bytes of a step) from dword-aligned rows (offsets 0 and 4; 4 is not 16-byte aligned); at
-    # offset 2 the rows are not dword-aligned and the LDS-staged kernel takes the product.  The
+    # offset 2 the rows are not dword-aligned and the element-wise kernel takes the product.  The
     # weights end where the buffer does.
     M, K = 40, 512
     A = quant.randn(M * K, seed=N + off).reshape(M, K)
