@@ -99,6 +99,11 @@ __device__ __forceinline__ u32x4 p_load16(const uint8_t* p) {
     return u32x4{v.x, v.y, v.z, v.w};
 }
 
+// 16 bytes per lane from global memory straight into LDS (lane l: bytes 16 l from lds, which is
+// wave-uniform).  A helper of its own: with the builtin written inside the kernel's lambdas, the
+// host compilation pass emitted no launch stub for some instantiations.
+__device__ __forceinline__ void p_dma16(const uint8_t* g, char* lds) { __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0); }
+
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt left at their
 // no-wait maxima).  The compiler does not order a global_load_lds into LDS before later ds_reads
 // of the same bytes, so the FP16 path waits for its copies itself.
@@ -148,6 +153,7 @@ struct PQ4K {
     static constexpr bool kActSwap = false;  // activation chunks in k order
     static constexpr bool kDirect = false;  // bytes copied through the wave's LDS area
     static constexpr bool kOneGroupPerTrip = false;
+    static constexpr bool kDmaGroup = true;
     static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
     static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return (first_step >> 2) * 144L; }
@@ -227,6 +233,7 @@ struct PQ8_0 {
     static constexpr bool kActSwap = false;
     static constexpr bool kDirect = false;  // bytes copied through the wave's LDS area
     static constexpr bool kOneGroupPerTrip = false;
+    static constexpr bool kDmaGroup = false;
     static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
     static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return first_step * 68L; }
@@ -297,6 +304,7 @@ struct PQ4_0 {
     static constexpr bool kActSwap = true;  // chunk halves (x0, x2, x1, x3, x4, x6, x5, x7)
     static constexpr bool kDirect = false;  // bytes copied through the wave's LDS area
     static constexpr bool kOneGroupPerTrip = false;
+    static constexpr bool kDmaGroup = true;
     static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
     static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return first_step * 36L; }
@@ -351,6 +359,7 @@ struct PQ5_0 {
     static constexpr bool kActSwap = false;
     static constexpr bool kDirect = false;  // bytes copied through the wave's LDS area
     static constexpr bool kOneGroupPerTrip = false;
+    static constexpr bool kDmaGroup = true;
     static __device__ __forceinline__ Piece load_piece(const uint8_t* p) { return p_load16(p); }
     static __device__ __forceinline__ u32x4 piece_bytes(const Piece& p) { return p; }
     static __device__ __forceinline__ long group_offset(int first_step) { return first_step * 44L; }
@@ -407,6 +416,7 @@ struct PF16 {
     static constexpr bool kTail = false;
     static constexpr bool kDirect = true;
     static constexpr bool kOneGroupPerTrip = true;
+    static constexpr bool kDmaGroup = false;
     using Piece = u32x4;
     static constexpr int kStepBytes = 32 * 128;     // one step buffer of the wave's rows
     static constexpr int kAreaBytes = 3 * kStepBytes;
@@ -470,6 +480,7 @@ struct PQ6K {
     static constexpr bool kDirect = false;  // bytes copied through the wave's LDS area
     // one group per loop trip: 45.9 -> 44.5 us at 512 x 8192 x 2048, same box (no gain for Q4_K, Q8_0, Q4_0)
     static constexpr bool kOneGroupPerTrip = true;
+    static constexpr bool kDmaGroup = false;
     static __device__ __forceinline__ long group_offset(int first_step) { return (first_step >> 2) * 210L; }
     struct Piece {
         u32x4 v;     // the 16 bytes from the dword boundary
@@ -555,7 +566,7 @@ using pos_t = std::integral_constant<int, J>;
 // dynamic LDS: two activation buffers of four step tiles, then one weight area per wave
 template <class W>
 constexpr int prefill_lds_bytes() {
-    return 8 * kPStage + (kPThreads / 64) * W::kAreaBytes;
+    return 8 * kPStage + (kPThreads / 64) * W::kAreaBytes * (W::kDmaGroup ? 2 : 1);
 }
 
 template <class W>
@@ -612,8 +623,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     }
     // kTail formats: lane l (and l + 32, a duplicate) reads row l's tail dword
     const int wtoff = (min(n0 + (lane & 31), N - 1) - n0c) * static_cast<int>(row_bytes);
-    char* const warea = lds + 8 * kPStage + wave * W::kAreaBytes;
+    char* const warea = lds + 8 * kPStage + wave * W::kAreaBytes * (W::kDmaGroup ? 2 : 1);
     const char* const wrow = warea + fr * W::kRowBytes;  // this lane's row in the area
+    // kDmaGroup formats: group q's bytes in area buffer q & 1
+    auto wrow_b = [&](int b) { return wrow + b * W::kAreaBytes; };
     // kDirect formats: copy instruction i of a step takes row r = 8 i + lane / 8 of the wave's
     // rows; its lane writes LDS bytes 16 lane of the instruction's kilobyte, which p_off puts at
     // chunk c = (lane & 7) ^ (r & 7) ^ ((r >> 3) & 1) of row r
@@ -659,13 +672,24 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         char* const buf = step_buf(t);
         const uint8_t* const g = wbase + static_cast<long>(step_of(t)) * (2 * kPKS);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) __builtin_amdgcn_global_load_lds(g + doff[i], buf + 1024 * i, 16, 0, 0);
+        for (int i = 0; i < 4; ++i) p_dma16(g + doff[i], buf + 1024 * i);
     };
     f32x4 av[4][2];  // activations of the next group: [step][row]
     typename W::Piece wr[kLoadsA];  // weight bytes of the next group
     uint32_t wt = 0;               // kTail formats: this lane's row's tail dword of the next group
+    // kDmaGroup: group q's weight bytes straight into LDS buffer q & 1 (piece c = 64 i + lane at
+    // byte 16 c, the layout write_w stores)
+    auto dma_group = [&](int q) {
+        if constexpr (W::kDmaGroup) {
+            const uint8_t* g = wbase + W::group_offset(step_of(4 * q));
+            char* const buf = warea + (q & 1) * W::kAreaBytes;
+#pragma unroll
+            for (int i = 0; i < kLoads; ++i)
+                if (64 * i + lane < kChunks) p_dma16(g + woff[i], buf + 1024 * i);
+        }
+    };
     auto load_next = [&](int q) {
-        if constexpr (!W::kDirect) {
+        if constexpr (!W::kDirect && !W::kDmaGroup) {
             const uint8_t* g = wbase + W::group_offset(step_of(4 * q));
 #pragma unroll
             for (int i = 0; i < kLoads; ++i) wr[i] = W::load_piece(g + woff[i]);
@@ -677,7 +701,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
             for (int i = 0; i < 2; ++i) av[j][i] = ld_f32x4(abase + step_of(4 * q + j) * kPKS + arow_off[i]);
     };
     auto write_w = [&]() {
-        if constexpr (!W::kDirect) {
+        if constexpr (!W::kDirect && !W::kDmaGroup) {
 #pragma unroll
             for (int i = 0; i < kLoads; ++i)
                 if (64 * i + lane < kChunks)
@@ -754,6 +778,11 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
                         p_wait_vm<0>();
                     W::read_buf(fn, step_buf(tr), fr, h);
                     if constexpr (!kLast) dma(tr + 1);
+                } else if constexpr (W::kDmaGroup) {
+                    // positions 2, 3 of this group, then 0, 1 of the next (its copy, issued at this
+                    // group's start, has this group's eight activation loads behind it)
+                    if constexpr (J == 3) p_wait_vm<8>();
+                    W::template read<(J + 1) & 3>(fn, wrow_b(J == 3 || J == 0 ? (q + 1) & 1 : q & 1), h);
                 } else {
                     W::template read<(J + 1) & 3>(fn, wrow, h);
                 }
@@ -780,6 +809,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
             dma(4 * q + 2);  // before the eight activation loads: the first iteration's wait counts them
             __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (W::kDmaGroup) {
+            dma_group(q + 1);  // before the eight activation loads: the third iteration's wait counts them
+            __builtin_amdgcn_sched_barrier(0);
+        }
         load_next(q + 1);
         iter(pos_t<1>{}, q, fa, fb, rd + kPStage, x, y, f1, f0, wr_buf);
         iter(pos_t<2>{}, q, fb, fa, rd + 2 * kPStage, y, x, f0, f1, wr_buf);
@@ -793,6 +826,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         dma(0);
         dma(1);
     }
+    if constexpr (W::kDmaGroup) dma_group(0);
     load_next(0);
     write_w();
 #pragma unroll
@@ -803,6 +837,9 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     if constexpr (W::kDirect) {
         p_wait_vm<0>();  // the copies of steps 0 and 1
         W::read_buf(f0, step_buf(0), fr, h);
+    } else if constexpr (W::kDmaGroup) {
+        p_wait_vm<0>();  // group 0's copy
+        W::template read<0>(f0, wrow_b(0), h);
     } else
         W::template read<0>(f0, wrow, h);
     {
@@ -816,7 +853,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     if constexpr (W::kDirect)
         W::read_buf(f1, step_buf(1), fr, h);
     else
-        W::template read<1>(f1, wrow, h);
+        W::template read<1>(f1, wrow_b(0), h);
     __syncthreads();
     char* const buf0 = lds;
     char* const buf1 = lds + 4 * kPStage;
@@ -843,7 +880,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
     // kDirect: the copies issued for steps past the split's end land before the workgroup's LDS
     // is released
-    if constexpr (W::kDirect) p_wait_vm<0>();
+    if constexpr (W::kDirect || W::kDmaGroup) p_wait_vm<0>();
 
     // rows whose activations left fp16's range take the fp32 path below
 #pragma unroll
