@@ -16,9 +16,10 @@
 //     double-buffered LDS tile of 64 rows x 64 halves, which all eight waves
 //     read (8 ds_read_b128 per wave and step);
 //   * weights are the B operand: each wave copies its 32 rows' bytes of a
-//     group of four steps into its own LDS area with coalesced loads (FP16,
-//     with nothing to decode, loads each lane's bytes straight into its B
-//     fragments instead: kDirect), and each
+//     group of four steps into its own LDS area with coalesced loads (Q4_K,
+//     Q4_0, Q5_0: global_load_lds into the other of two areas, a group ahead,
+//     kDmaGroup; Q8_0, Q6_K: through registers; FP16, 512 bytes per row and
+//     group, per step into a ring of three step buffers, kDirect), and each
 //     lane decodes the bytes of its own weight row (its output column) from
 //     there in registers, to the reference's dequantized value rounded once to
 //     fp16 (Q8_0: d * q; Q4_0, Q5_0: d * (q - 8), d * (q - 16); Q4_K:
