@@ -658,9 +658,68 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_attn_combine_kernel
     }
 }
 
+// The same merge for head_dim 64 and at most 32 chunks (the decode steps' shapes) in one round
+// trip: thread t takes chunk t / 8 and dims 8 (t % 8) .. + 8 and issues its record loads (max,
+// sum, 8 accumulators) before anything is reduced; the chunk factors stay in registers, each
+// wave adds its 8 chunks with cross-lane sums (lanes t, t ^ 8, t ^ 16, t ^ 32 hold the same dims),
+// and the four waves' parts are added in wave order through LDS.  The general kernel above
+// loads the maxima, reduces them, and only then loads the accumulators.
+constexpr int kCombine64MaxChunks = 32;
+
+__global__ __launch_bounds__(256) void decode_attn_combine64_kernel(const float* __restrict__ ws,
+                                                                    float* __restrict__ out, int nchunks, long ldo) {
+    constexpr int D = 64, stride = D + 4;
+    __shared__ float red[2][4];
+    __shared__ float part[4][D];
+    const int h = blockIdx.x, mrow = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = tid >> 3, j = tid & 7;
+    const float* rec = ws + ((static_cast<long>(mrow) * gridDim.x + h) * nchunks + min(c, nchunks - 1)) * stride;
+    const bool live = c < nchunks;
+    const float mc = live ? rec[0] : -INFINITY;
+    const float lc = live ? rec[1] : 0.0f;
+    const f32x4 a0 = ld_f32x4(rec + 4 + 8 * j), a1 = ld_f32x4(rec + 8 + 8 * j);
+    const float wm = wave_max(mc);
+    if (lane == 0) red[0][wave] = wm;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    const float f = live ? exp2f(mc - M) : 0.0f;  // empty chunks (max -inf): 0
+    const float ls = group_sum_t<6>(j == 0 ? f * lc : 0.0f);
+    float v[8] = {f * a0.x, f * a0.y, f * a0.z, f * a0.w, f * a1.x, f * a1.y, f * a1.z, f * a1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        float x = v[e];
+        x += dpp<0x128>(x);  // row_ror:8 (lane ^ 8 inside a row of 16)
+        x += swizzle_xor16(x);
+        x += shfl_xor32(x);
+        v[e] = x;
+    }
+    if (lane < 8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part[wave][8 * lane + e] = v[e];
+    }
+    if (lane == 0) red[1][wave] = ls;
+    __syncthreads();
+    if (tid < D) {
+        const float den = ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3];
+        const float num = ((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid];
+        out[mrow * ldo + static_cast<long>(h) * D + tid] = num / den;
+    }
+}
+
 }  // namespace dev
 
 namespace detail {
+
+// merge the chunk records of every (row, head)
+static void launch_combine(const float* ws, float* out, int n_heads, int rows, int D, int nchunks, long ldo,
+                           hipStream_t stream) {
+    const dim3 grid(n_heads, static_cast<unsigned>(rows));
+    if (D == 64 && nchunks <= dev::kCombine64MaxChunks)
+        hipLaunchKernelGGL(dev::decode_attn_combine64_kernel, grid, dim3(256), 0, stream, ws, out, nchunks, ldo);
+    else
+        hipLaunchKernelGGL(dev::decode_attn_combine_kernel, grid, dim3(64 * dev::kCombineWaves), 0, stream, ws, out,
+                           D, nchunks, ldo);
+}
 
 template <int NQ>
 static void launch_att(bool vec, dim3 grid, hipStream_t stream, const float* Q, const float* K, const float* V,
@@ -729,8 +788,7 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
         if (wgs > 0x7FFFFFFFL) return kDeclined;
         hipLaunchKernelGGL(dev::decode_attn_mrow_kernel, dim3(static_cast<unsigned>(wgs)), dim3(64 * dev::kMrWaves), 0,
                            stream, Q, K, V, ws, G, n_kv_heads, rows, kv_dev, kv0, qscale, nchunks, ldq);
-        hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads, static_cast<unsigned>(rows)),
-                           dim3(64 * dev::kCombineWaves), 0, stream, ws, out, D, nchunks, ldo);
+        launch_combine(ws, out, n_heads, rows, D, nchunks, ldo, stream);
         return 0;
     }
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(rows));
@@ -740,8 +798,7 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
     else
         hipLaunchKernelGGL((dev::decode_attn_split_kernel<kSplitHeadsPerWave, 8>), grid, dim3(256 / kSplitHeadsPerWave),
                            0, stream, Q, K, V, ws, G, n_kv_heads * D, D, kv_dev, kv0, qscale, nchunks, nhq, ldq);
-    hipLaunchKernelGGL(dev::decode_attn_combine_kernel, dim3(n_heads, static_cast<unsigned>(rows)),
-                           dim3(64 * dev::kCombineWaves), 0, stream, ws, out, D, nchunks, ldo);
+    launch_combine(ws, out, n_heads, rows, D, nchunks, ldo, stream);
     return 0;
 }
 
