@@ -1,5 +1,8 @@
 // mfma_gemm.hip -- fused dequant GEMM on the matrix cores for multi-token
 // (prefill) batches: C[M,N] = A[M,K] * dequant(B[N,K])^T, every weight format.
+// The C ABI sends it the prefill shapes that the register-decode kernel of
+// prefill.hip does not take: K % 64 == 0 but K % 256 != 0 (e.g. K = 576), or
+// activations that are not 16-byte aligned.
 //
 // The reference computes the same product with one fp32 FMA chain per output
 // (ref:src/kernels/matmul_quant.cu:64-130 Q8_0, :142-204 Q4_0, :216-297 Q5_0,
