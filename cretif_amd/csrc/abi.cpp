@@ -90,7 +90,7 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
     else if (cri::detail::skinny_supported(fmt, M, K, B))
         rc = cri::detail::launch_skinny_act(cri::kActPlain, fmt, cri::ActIn{A, nullptr, nullptr, nullptr, K, 0.0f}, B,
                                             C, M, N, K, stream, ws, ws_floats, defer, defer_S);
-    else if (M == 1 && cri::detail::slice_gemv_supported(fmt, K, B))
+    else if (M == 1 && cri::detail::slice_gemv_supported(fmt, N, K, B))
         rc = cri::detail::launch_slice_gemv(cri::kActPlain, fmt, cri::ActIn{A, nullptr, nullptr, nullptr, K, 0.0f}, B,
                                             C, N, K, stream);
     else if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
@@ -321,7 +321,7 @@ int fused_matmul(int mode, int fmt, const cri::ActIn& act, const void* B, float*
     // 2048 x 8192 Q4_K 4.97 us against 6.73 on the batch-1 GEMV); it recomputes the prologue in
     // every lane, so with an RMSNorm prologue (three loads per activation) the batch-1 GEMV, which
     // stages it once per workgroup, is faster (16384 x 2048: 7.1 against 8.1 us)
-    if (M == 1 && mode == cri::kActSwiGLU && K == 8192 && cri::detail::slice_gemv_supported(fmt, K, B))
+    if (M == 1 && mode == cri::kActSwiGLU && K == 8192 && cri::detail::slice_gemv_supported(fmt, N, K, B))
         rc = cri::detail::launch_slice_gemv(mode, fmt, act, B, C, N, K, stream);
     if (rc == cri::detail::kDeclined && cri::detail::skinny_supported(fmt, M, K, B))
         rc = cri::detail::launch_skinny_act(mode, fmt, act, B, C, M, N, K, stream, ws, ws_floats, defer, defer_S);

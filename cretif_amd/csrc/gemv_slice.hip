@@ -42,11 +42,15 @@ namespace dev {
 // Q4_K piece p of a row: super-block p >> 3, chunk j = (p >> 1) & 3, half h = p & 1.  Quant
 // bytes 16 + 32 j + 16 h .. +16 of the super-block; low nibble of byte i = element
 // 64 j + 16 h + i, high nibble = element 64 j + 32 + 16 h + i (ref:src/kernels/dequantize.cu:307-319).
-struct SliceQ4K {
+// WAVES: waves per workgroup (K slices).  Four from 8192 x 2048 on (eight measured slower, 3.96
+// -> 4.80 us; two 4.82 us, and 5.81 against 4.05 at 2048 x 8192); two up to 2048 x 2048, where
+// they halve the number of waves (2048 x 2048 2.70 -> 2.57 us, 512 x 2048 2.15 -> 2.09).
+template <int WAVES>
+struct SliceQ4KW {
     static constexpr int kFmt = kFmtQ4_K;
     static constexpr int kXb = 32;        // xb: elements x_first + 32 .. +16
     static constexpr int kMaxSteps = 8;   // row steps per workgroup at most
-    static constexpr int kWaves = 4;      // waves per workgroup (K slices); eight measured slower (3.96 -> 4.80 us)
+    static constexpr int kWaves = WAVES;
     struct Data {
         u32x4 hd, q;
     };
@@ -102,6 +106,8 @@ struct SliceQ4K {
         return (dd * kTwo24) * t - dmin * m;
     }
 };
+using SliceQ4K = SliceQ4KW<4>;
+using SliceQ4K2 = SliceQ4KW<2>;
 
 // Q8_0 piece p of a row: block p (34 bytes: fp16 d, 32 int8 quants; ref:src/kernels/dequantize.cu:60-70),
 // elements 32 p .. +32.  Blocks start at 34 p: dword aligned for even p, two bytes past a dword
@@ -322,7 +328,7 @@ int slice_lg(int K, int waves) {
         case 8192: lg = 8; break;
     }
     if (lg < 0) return -1;
-    lg -= waves == 8 ? 3 : 2;  // K / 32 pieces over the waves
+    lg -= waves == 8 ? 3 : (waves == 4 ? 2 : 1);  // K / 32 pieces over the waves
     return lg >= 2 && lg <= 6 ? lg : -1;
 }
 
@@ -396,23 +402,27 @@ static bool slice_fmt(int fmt, int K) {
     }
     return false;
 }
-static int slice_waves(int fmt) {
+// Q4_K up to 2048 x 2048 on two waves per workgroup
+static bool q4k_two_waves(int N, int K) { return N <= 2048 && K <= 2048; }
+static int slice_waves(int fmt, int N, int K) {
     switch (fmt) {
         case kFmtQ8_0: return dev::SliceQ80::kWaves;
         case kFmtQ4_0: return dev::SliceQ40::kWaves;
         case kFmtQ5_0: return dev::SliceQ50::kWaves;
     }
-    return dev::SliceQ4K::kWaves;
+    return q4k_two_waves(N, K) ? dev::SliceQ4K2::kWaves : dev::SliceQ4K::kWaves;
 }
 
-bool slice_gemv_supported(int fmt, int K, const void* W) {
-    return slice_fmt(fmt, K) && slice_lg(K, slice_waves(fmt)) >= 0 && (reinterpret_cast<uintptr_t>(W) & 3u) == 0;
+bool slice_gemv_supported(int fmt, int N, int K, const void* W) {
+    return slice_fmt(fmt, K) && slice_lg(K, slice_waves(fmt, N, K)) >= 0 && (reinterpret_cast<uintptr_t>(W) & 3u) == 0;
 }
 
 int launch_slice_gemv(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t s) {
-    if (!slice_gemv_supported(fmt, K, W)) return kDeclined;
+    if (!slice_gemv_supported(fmt, N, K, W)) return kDeclined;
     switch (fmt) {
-        case kFmtQ4_K: return launch_slice_f<dev::SliceQ4K>(mode, act, W, y, N, K, s);
+        case kFmtQ4_K:
+            if (q4k_two_waves(N, K)) return launch_slice_f<dev::SliceQ4K2>(mode, act, W, y, N, K, s);
+            return launch_slice_f<dev::SliceQ4K>(mode, act, W, y, N, K, s);
         case kFmtQ8_0: return launch_slice_f<dev::SliceQ80>(mode, act, W, y, N, K, s);
         case kFmtQ4_0: return launch_slice_f<dev::SliceQ40>(mode, act, W, y, N, K, s);
         case kFmtQ5_0: return launch_slice_f<dev::SliceQ50>(mode, act, W, y, N, K, s);

@@ -116,9 +116,10 @@ int launch_gemv_ksplit(int mode, int fmt, const ActIn& act, const void* W, float
 int launch_gemv_rope(int fmt, const ActIn& act, const void* W, float* q_out, int N, int K, const RopeOut& rope,
                      hipStream_t stream, bool split_res = false);
 
-// batch-1 Q4_K GEMV with K sliced over the four waves of a workgroup (gemv_slice.hip), for K in
+// batch-1 GEMV with K sliced over the waves of a workgroup (gemv_slice.hip; Q4_K: two waves up to
+// 2048 x 2048, four above), for K in
 // {1024, 2048, 4096, 8192} and dword-aligned weights; plain or SwiGLU prologue (kDeclined otherwise)
-bool slice_gemv_supported(int fmt, int K, const void* W);
+bool slice_gemv_supported(int fmt, int N, int K, const void* W);
 int launch_slice_gemv(int mode, int fmt, const ActIn& act, const void* W, float* y, int N, int K, hipStream_t stream);
 
 // 1 <= M <= 16 fused dequant matmul on the matrix cores (mfma_skinny.hip)

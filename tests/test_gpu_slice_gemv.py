@@ -3,7 +3,8 @@
 cri_matmul_q4_k at M = 1 with K in {1024, 2048, 4096, 8192}, and cri_matmul_q8_0 / _q4_0 / _q5_0
 at K = 8192, take this kernel; the row count decides how many rows a workgroup takes (1, 2, 4 or 8 row
 steps), so N runs over values that give each step count, a last workgroup only partly used,
-and a single row.  cri_matmul_swiglu at M = 1 takes it at K = 8192 (the other K run the
+and a single row.  Q4_K up to 2048 x 2048 runs two waves per workgroup, larger shapes four, so
+both forms are covered (N <= 2048 with K <= 2048, and the rest).  cri_matmul_swiglu at M = 1 takes it at K = 8192 (the other K run the
 batch-1 GEMV and are checked here as well).  Q8_0, Q4_0 and Q5_0 blocks (34, 18, 22 bytes)
 alternate between dword-aligned and two-bytes-off starts, so every case covers both.
 
