@@ -64,6 +64,7 @@ typedef uint32_t pu4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int kPTM = 64, kPTN = 256, kPKS = 64, kPThreads = 512;
 constexpr int kPStage = kPTM * kPKS * 2;  // one fp16 activation tile, bytes
+constexpr int kPDirectStep = 32 * kPKS * 2;  // one FP16 weight step buffer: a wave's 32 rows x 64 halves
 constexpr uint32_t kPMagic = 0x64646464u;
 constexpr float kPRowMax = 65504.0f;      // at or above: fp16 infinity
 constexpr float kPRowMin = 0x1p-10f;      // below (and nonzero): subnormal precision only
@@ -419,8 +420,7 @@ struct PF16 {
     static constexpr bool kOneGroupPerTrip = true;
     static constexpr bool kDmaGroup = false;
     using Piece = u32x4;
-    static constexpr int kStepBytes = 32 * 128;     // one step buffer of the wave's rows
-    static constexpr int kAreaBytes = 3 * kStepBytes;
+    static constexpr int kAreaBytes = 3 * kPDirectStep;  // the ring of three step buffers
     static constexpr int kReadPhase = 0;
     static constexpr int kMfmaPrio = 0;
     static constexpr bool kActSwap = false;
@@ -660,7 +660,12 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     // wave's LDS area after group q's last read of it (third iteration), its
     // first step decoded in the fourth, which also stages the activations
     // into the other LDS buffer.  So every load is waited for in the code
-    // block that issued it, two to three iterations later.  A split is whole
+    // block that issued it, two to three iterations later.  kDmaGroup formats
+    // copy the weight bytes straight into the other of two areas instead (no
+    // registers, no LDS write), waited for where the third iteration first
+    // reads them; kDirect (FP16) copies one step at a time into a ring of
+    // three step buffers, each copy issued two iterations before the
+    // iteration that reads it (see iter).  A split is whole
     // groups (K % 256 == 0 and splits start on a group), so nst is a
     // multiple of four; the loads issued after the last group repeat the
     // split's last step (in bounds) and what they stage is never read (their
@@ -668,12 +673,12 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const int ngrp = nst >> 2;
     auto step_of = [&](int t) { return s_begin + min(t, nst - 1); };
     // relative step t of the split -> its buffer in the ring (kDirect)
-    auto step_buf = [&](int t) { return warea + (t % 3) * 4096; };
-    auto dma = [&](int t) {
+    auto step_buf = [&](int t) { return warea + (t % 3) * kPDirectStep; };
+    auto dma = [&](int t) {  // four copy instructions of 8 rows x 128 bytes
         char* const buf = step_buf(t);
         const uint8_t* const g = wbase + static_cast<long>(step_of(t)) * (2 * kPKS);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p_dma16(g + doff[i], buf + 1024 * i);
+        for (int i = 0; i < 4; ++i) p_dma16(g + doff[i], buf + (kPDirectStep / 4) * i);
     };
     f32x4 av[4][2];  // activations of the next group: [step][row]
     typename W::Piece wr[kLoadsA];  // weight bytes of the next group
