@@ -407,9 +407,10 @@ class DecodeStepRig:
         if capture:
             dec.capture(self.ids, M, self.logits, self.next_ids, stream=self.stream)
 
-    def prompt_samples(self, samples=5, warmup=1):
+    def prompt_samples(self, samples=5, warmup=1, last_only=False):
         """ms of each of `samples` eager steps of the M tokens at position 0 (a prompt into an empty
-        cache: the attention spans only the positions the prompt sees)."""
+        cache: the attention spans only the positions the prompt sees).  last_only: cri_decoder_prefill,
+        the LM head and argmax of the last token only (what the reference's generate() reads)."""
         import torch
 
         s = self.stream
@@ -418,7 +419,10 @@ class DecodeStepRig:
             self.dec.set_position(0, stream=s)
             if i >= warmup:
                 ev[i - warmup][0].record(s)
-            self.dec.forward(self.ids, self.M, self.logits, self.next_ids, stream=s)
+            if last_only:
+                self.dec.prefill(self.ids, self.M, self.logits, self.next_ids, stream=s)
+            else:
+                self.dec.forward(self.ids, self.M, self.logits, self.next_ids, stream=s)
             if i >= warmup:
                 ev[i - warmup][1].record(s)
         torch.cuda.synchronize()
@@ -718,6 +722,8 @@ def main():
                     help="only time the synthetic Llama-3.2-1B decode step for M tokens (for profiling)")
     ap.add_argument("--prompt", type=int, default=None, metavar="M",
                     help="time an M-token prompt (eager steps at position 0) through the 16-layer decode step")
+    ap.add_argument("--prompt-last-row", action="store_true",
+                    help="with --prompt: cri_decoder_prefill (the LM head of the last token only)")
     ap.add_argument("--attention", default=None, choices=["plain", "ws"],
                     help="only time the fused decode attention at 2048 positions (for profiling)")
     ap.add_argument("--launch-floor", action="store_true",
@@ -773,7 +779,7 @@ def main():
         return
     if args.prompt:
         r = DecodeStepRig(args.prompt, capture=False)
-        ms = float(np.median(r.prompt_samples(samples)))
+        ms = float(np.median(r.prompt_samples(samples, last_only=args.prompt_last_row)))
         print(json.dumps({"workload": "prompt", "M": args.prompt, "ms_per_prompt": round(ms, 4),
                           "prompt_tokens/s": round(args.prompt / (ms * 1e-3), 1)}))
         return
@@ -903,6 +909,13 @@ def main():
         details["prompt_m512"] = {"prompt_tokens/s": round(512 / (ms_prompt * 1e-3), 1),
                                   "ms_per_prompt": round(ms_prompt, 4),
                                   "timing": "median of 5 eager cri_decoder steps of 512 tokens at position 0"}
+        # the same prompt as generate() consumes it (ref:src/model.cu:1063-1078): every layer on the
+        # 512 tokens, the LM head and argmax of the last one only (cri_decoder_prefill)
+        ms_gen = float(np.median(r.prompt_samples(5, last_only=True)))
+        details["prompt_m512_last_row"] = {"prompt_tokens/s": round(512 / (ms_gen * 1e-3), 1),
+                                           "ms_per_prompt": round(ms_gen, 4),
+                                           "timing": "median of 5 eager cri_decoder_prefill calls of 512 tokens "
+                                                     "at position 0"}
         r.free()
         torch.cuda.empty_cache()
 

@@ -114,6 +114,7 @@ ABI_SYMBOLS = (
         "cri_decoder_set_embedding",
         "cri_decoder_set_output",
         "cri_decoder_forward",
+        "cri_decoder_prefill",
         "cri_decoder_forward_taps",
         "cri_decoder_capture",
         "cri_decoder_replay",
@@ -281,7 +282,7 @@ def lib():
     L.cri_decoder_set_embedding.restype = i32
     L.cri_decoder_set_output.argtypes = [vp, vp, i32, vp]
     L.cri_decoder_set_output.restype = i32
-    for n in ("cri_decoder_forward", "cri_decoder_capture"):
+    for n in ("cri_decoder_forward", "cri_decoder_capture", "cri_decoder_prefill"):
         getattr(L, n).argtypes = [vp, vp, i32, vp, vp, vp]
         getattr(L, n).restype = i32
     L.cri_decoder_forward_taps.argtypes = [vp, vp, i32, vp, vp, vp, vp]
@@ -743,6 +744,12 @@ class Decoder:
 
     def forward(self, token_ids, M, logits, next_ids=None, stream=None):
         _check(lib().cri_decoder_forward(self._h, _ptr(token_ids), M, _ptr(logits), _ptr(next_ids),
+                                         _stream(stream)))
+
+    def prefill(self, token_ids, M, logits, next_id=None, stream=None):
+        """A prompt as the reference's generate() consumes it: every layer on the M tokens, the
+        LM head and argmax for the last token only (logits: device fp32 [vocab])."""
+        _check(lib().cri_decoder_prefill(self._h, _ptr(token_ids), M, _ptr(logits), _ptr(next_id),
                                          _stream(stream)))
 
     def forward_taps(self, token_ids, M, logits, hidden_taps, next_ids=None, stream=None):

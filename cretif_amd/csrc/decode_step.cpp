@@ -657,7 +657,8 @@ void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res,
     res_part_count_ = 0;
 }
 
-void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s, float* taps) {
+void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s, float* taps,
+                         bool last_only) {
     const int D = cfg_.dim, V = cfg_.vocab_size;
     const float eps = cfg_.rms_norm_eps;
     // token rows straight from the table in its own format (the reference's Embedding::forward
@@ -688,6 +689,38 @@ void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next
     const Tensor& W = lm_tied_ ? tok_table_ : lm_head_;
     const WeightFormat wf = lm_tied_ ? tok_fmt_ : lm_fmt_;
     float* h = hid_[cur].data_as<float>();
+    int* pos = static_cast<int*>(pos_dev_.data());
+    if (last_only && M > 1) {
+        // the final RMSNorm, the LM head and the argmax of row M - 1 alone (prefill())
+        const long last = static_cast<long>(M - 1) * D;
+        if (split_flow(M)) {  // the pending residual as partial sums: the row kernel adds them for every row
+            check_status(cri::detail::launch_split_norm(h, residual_sums(res_part_, res_part_stride_, res_part_count_,
+                                                                         res, D),
+                                                        out_norm_.data_as<float>(), hid_[1 - cur].data_as<float>(),
+                                                        normed_.data_as<float>(), M, D, eps, s),
+                         "final RMSNorm");
+            res_part_count_ = 0;
+            const float* n = normed_.data_as<float>() + last;
+            if (wf == WeightFormat::FP32)
+                matmul_transposed_b(n, W.data_as<float>(), logits, 1, V, D, s);
+            else
+                matmul_dispatch(n, W, logits, 1, V, D, wf, s);
+        } else if (wf != WeightFormat::FP32) {  // a plain residual: RMSNorm inside the LM head's prologue
+            matmul_dispatch_rmsnorm(h + last, res ? res + last : nullptr, out_norm_.data_as<float>(),
+                                    hid_[1 - cur].data_as<float>() + last, W, logits, 1, V, D, wf, eps, s);
+        } else {
+            rmsnorm_residual(h + last, res ? res + last : nullptr, out_norm_.data_as<float>(), h + last,
+                             normed_.data_as<float>(), 1, D, eps, s);
+            matmul_transposed_b(normed_.data_as<float>(), W.data_as<float>(), logits, 1, V, D, s);
+        }
+        if (next_ids)
+            check_status(cri::detail::launch_argmax_rows(logits, V, 1, V, next_ids, argmax_part_.data_as<float>(),
+                                                         static_cast<unsigned*>(argmax_count_.data()), pos, M, s),
+                         "argmax");
+        else
+            check_status(cri::detail::launch_pos_add(pos, M, s), "position update");
+        return;
+    }
     if (split_flow(M)) {  // the final RMSNorm as a row kernel, the LM head on plain activations
         check_status(cri::detail::launch_split_norm(h, residual_sums(res_part_, res_part_stride_, res_part_count_, res, D),
                                                     out_norm_.data_as<float>(), hid_[1 - cur].data_as<float>(),
@@ -714,7 +747,6 @@ void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next
         else
             matmul_dispatch(normed_.data_as<float>(), W, logits, M, V, D, wf, s);
     }
-    int* pos = static_cast<int*>(pos_dev_.data());
     if (next_ids)  // the argmax's last workgroup also advances the position
         check_status(cri::detail::launch_argmax_rows(logits, V, M, V, next_ids, argmax_part_.data_as<float>(),
                                                      static_cast<unsigned*>(argmax_count_.data()), pos, M, s),
@@ -740,6 +772,12 @@ void DecodeStep::check_call(const int32_t* ids, int M, float* logits, int32_t* n
 void DecodeStep::forward(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s) {
     check_call(ids, M, logits, next_ids, "forward");
     enqueue(ids, M, logits, next_ids, s);
+    pos_host_ += M;
+}
+
+void DecodeStep::prefill(const int32_t* ids, int M, float* logits, int32_t* next_id, hipStream_t s) {
+    check_call(ids, M, logits, next_id, "prefill");
+    enqueue(ids, M, logits, next_id, s, nullptr, true);
     pos_host_ += M;
 }
 
@@ -907,6 +945,12 @@ int cri_decoder_forward(cri_decoder* d, const int* token_ids, int M, float* logi
     const char* fn = "cri_decoder_forward";
     if (!d) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null decoder");
     return guarded(fn, [&] { d->step.forward(token_ids, M, logits, next_ids, s); });
+}
+
+int cri_decoder_prefill(cri_decoder* d, const int* token_ids, int M, float* logits, int* next_id, hipStream_t s) {
+    const char* fn = "cri_decoder_prefill";
+    if (!d) return dec_fail(CRI_ERR_INVALID_ARGUMENT, fn, "null decoder");
+    return guarded(fn, [&] { d->step.prefill(token_ids, M, logits, next_id, s); });
 }
 
 int cri_decoder_forward_taps(cri_decoder* d, const int* token_ids, int M, float* logits, int* next_ids,

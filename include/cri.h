@@ -298,6 +298,13 @@ int cri_decoder_set_output(cri_decoder* dec, const float* output_norm, int forma
  * CRI_ERR_SHAPE when position() + M would exceed max_seq_len. */
 int cri_decoder_forward(cri_decoder* dec, const int* token_ids, int M, float* logits, int* next_ids,
                         hipStream_t stream);
+/* A prompt as the reference's generate() consumes it (ref:src/model.cu:1063-1078, which runs
+ * forward() and reads only the last row's logits): every layer runs on the M tokens (caches
+ * appended, position advanced by M), the final RMSNorm, LM head and argmax for token M - 1 only:
+ * logits (device fp32 [vocab]), next_id (device int32 [1] or NULL).  No counterpart in the
+ * reference's API (its forward() always returns every row). */
+int cri_decoder_prefill(cri_decoder* dec, const int* token_ids, int M, float* logits, int* next_id,
+                        hipStream_t stream);
 /* capture the same call as one HIP graph on a non-null stream (nothing runs), and replay it:
  * each replay is one more step of M tokens; next_ids == token_ids generates greedily */
 /* cri_decoder_forward that also writes the residual stream entering each layer and the final

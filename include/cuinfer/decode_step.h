@@ -99,6 +99,13 @@ public:
     // [M, vocab]); next_ids (device int32 [M], may be null) receives the
     // argmax of each logits row.  Enqueued on `stream`; advances position().
     void forward(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, hipStream_t stream = 0);
+    // A prompt the way the reference's generate() consumes it (ref:src/model.cu:1063-1078): every
+    // layer runs on the M tokens (the caches take their keys and values, position() advances by
+    // M), and the final RMSNorm, the LM head and the argmax run for the last row only: logits
+    // (device fp32 [vocab]) of token M - 1, next_id (device int32 [1], may be null) its argmax.
+    // forward() computes every row's logits as the reference's forward() does; this skips the
+    // M - 1 rows generate() never reads.
+    void prefill(const int32_t* token_ids, int M, float* logits, int32_t* next_id, hipStream_t stream = 0);
     // forward() that also writes the residual stream entering each layer and the final norm:
     // hidden_taps (device fp32 [n_layers + 1, M, dim]) slice i = the hidden state layer i
     // reads (slice n_layers: the one the final RMSNorm reads), each added up from its pending
@@ -131,7 +138,7 @@ public:
 private:
     struct Layer;
     void enqueue(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, hipStream_t stream,
-                 float* taps = nullptr);
+                 float* taps = nullptr, bool last_only = false);
     void check_ready() const;
     void check_call(const int32_t* token_ids, int M, float* logits, int32_t* next_ids, const char* what) const;
     void drop_graph();

@@ -431,6 +431,56 @@ def test_prompt_two_layers_through_gqa(orc, pos):
         assert normwise_rel_err(gv[pos:pos + M], vc[i][pos:pos + M]) <= PREFILL_TOL
 
 
+@pytest.mark.parametrize("M,pos", [(512, 0), (17, 100), (12, 40), (5, 700), (1, 9)])
+def test_prefill_last_row_equals_forward(orc, M, pos):
+    # cri_decoder_prefill (generate()'s use of a prompt, ref:src/model.cu:1063-1078): forward()'s
+    # layers on the M tokens, then the final RMSNorm, LM head and argmax of the last token only.
+    # The caches and position must match a forward() of the same tokens (bit for bit up to 16 rows;
+    # above, the prefill GEMMs add K-split partial sums with atomics, in any order, and the next
+    # layer's fp16 operand rounding carries those last-bit differences on: two forward() calls of
+    # the same prompt differ by ~3e-4 in the second layer's cache, so the 2e-3 bar), its logits forward()'s
+    # last row (above 16 rows those come from the fp16-operand prefill GEMM: the 2e-3 bar) and, up
+    # to 17 rows, the oracle's last row; next_id is the argmax of its own logits.  M = 1 is forward().
+    big = M > 16
+    fm = {n: "fp16" for n in ("q", "k", "v", "o", "gate", "up", "down")} if big else None
+    m = make_model(2, dim=2048, n_heads=32, n_kv_heads=8, head_dim=64, ffn=8192, vocab=2000, seed=71 + M,
+                   fmts=fm, tok="q8_0", lm="fp16" if big else "q6_k", big_tables=False)
+    dec = make_decoder(m, max_seq=2048, max_batch=max(M, 16))
+    kc, vc = random_cache(m, 2048, 72 + M)
+    ids = np.random.default_rng(M + pos).integers(0, m["vocab"], M).astype(np.int32)
+    dids = torch.from_numpy(ids).cuda()
+    V, shape = m["vocab"], (2048, m["n_kv_heads"], m["head_dim"])
+
+    load_cache(dec, kc, vc)
+    dec.set_position(pos)
+    full = torch.full((M, V), float("nan"), device="cuda")
+    dec.forward(dids, M, full)
+    caches = [tuple(from_device(a, shape) for a in dec.kv_cache(i)) for i in range(2)]
+
+    load_cache(dec, kc, vc)
+    dec.set_position(pos)
+    last = torch.full((V,), float("nan"), device="cuda")
+    nid = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    dec.prefill(dids, M, last, nid)
+    assert dec.position == pos + M
+    got = last.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert int(nid.cpu().numpy()[0]) == int(np.argmax(got))
+    tol = PREFILL_TOL if big else TOL
+    err = normwise_rel_err(got, full.cpu().numpy()[M - 1])
+    print("prefill M=%d pos=%d: last-row logits against forward %.2e" % (M, pos, err))
+    assert err <= tol
+    for i in range(2):
+        gk, gv = (from_device(a, shape) for a in dec.kv_cache(i))
+        if big:
+            assert normwise_rel_err(gk, caches[i][0]) <= PREFILL_TOL and normwise_rel_err(gv, caches[i][1]) <= PREFILL_TOL
+        else:
+            assert np.array_equal(gk, caches[i][0]) and np.array_equal(gv, caches[i][1])
+    if M <= 17:
+        ref, _ = orc.decode_step(m, list(ids), pos, kc, vc)
+        assert normwise_rel_err(got, ref[M - 1]) <= tol
+
+
 @pytest.mark.parametrize("M,pos", [(16, 0), (4, 0), (8, 31), (16, 120), (5, 1000), (16, 1008)])
 def test_batch_attention_rope_nan_cache(orc, M, pos):
     # 4..16 rows on the multi-row attention: every cache row from pos on holds NaN before the step,
