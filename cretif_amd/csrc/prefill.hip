@@ -719,8 +719,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     // step j, row i of the next group into buffer buf (tile j)
     auto stage = [&](char* buf, int j, int i) {
         const f32x4 v = av[j][i];
-        const float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        amax[i] = fmaxf(amax[i], mx);
+        // two v_max3_f32 (abs source modifiers) per four values
+        amax[i] = fmaxf(fmaxf(fmaxf(fmaxf(amax[i], fabsf(v.x)), fabsf(v.y)), fabsf(v.z)), fabsf(v.w));
         // kActSwap: halves (x0, x2, x1, x3) of the thread's four columns, the B order of PQ4_0
         const pf2 p0 = W::kActSwap ? pf2{v.x, v.z} : pf2{v.x, v.y};
         const pf2 p1 = W::kActSwap ? pf2{v.y, v.w} : pf2{v.z, v.w};
