@@ -49,8 +49,13 @@ PREFILL_WORKLOADS = {
     "q4_0_prefill_down": ("q4_0", 512, 2048, 8192),
     "q5_0_prefill": ("q5_0", 512, 8192, 2048),
     "q5_0_prefill_down": ("q5_0", 512, 2048, 8192),
-    # the LDS-staged kernel (mfma_gemm.hip) that FP16 takes
+    # FP16 on the register-decode kernel, copied per step with global_load_lds
     "fp16_prefill": ("fp16", 512, 8192, 2048),
+    # through cri_matmul_ws: the down shape's K split (four ways, 64 output tiles) stores its
+    # partial sums in the workspace and a second launch adds them in order, instead of fp32
+    # atomics into a zero-filled C
+    "q4_k_prefill_down_ws": ("q4_k", 512, 2048, 8192),
+    "q8_0_prefill_down_ws": ("q8_0", 512, 2048, 8192),
 }
 
 # batched decode GEMVs (BASELINE config 5 at M = 16): name -> (fmt, M, N, K)
@@ -795,7 +800,7 @@ def main():
         return
     if args.prefill:
         f, m_, n, k = PREFILL_WORKLOADS[args.prefill]
-        r = GemvRig(f, n, k, M=m_, max_copies=16)
+        r = GemvRig(f, n, k, M=m_, max_copies=16, workspace=args.prefill.endswith("_ws"))
         m = r.time(samples, 16)
         print(json.dumps({"workload": args.prefill, "M": m_, "N": n, "K": k, "launches_per_sample": r.steps,
                           "us": round(m * 1e3, 3), "TFLOP/s": round(2.0 * m_ * n * k / (m * 1e-3) / 1e12, 1)}))
@@ -858,7 +863,7 @@ def main():
             r.free()
             torch.cuda.empty_cache()
         for name, (f, m_, n, k) in PREFILL_WORKLOADS.items():
-            r = GemvRig(f, n, k, M=m_, max_copies=16)
+            r = GemvRig(f, n, k, M=m_, max_copies=16, workspace=name.endswith("_ws"))
             m = r.time(9, 16)
             tf = 2.0 * m_ * n * k / (m * 1e-3) / 1e12
             details[name] = {"TFLOP/s": round(tf, 1), "us": round(m * 1e3, 3), "M": m_, "copies": r.copies,

@@ -96,7 +96,7 @@ int matmul_impl(int fmt, const float* A, const void* B, float* C, int M, int N, 
     else if (M == 1 && cri::detail::gemv_supported(fmt, K, B))
         rc = cri::detail::launch_gemv(fmt, A, B, C, N, K, stream);
     else if (M > kPrefillMinM && cri::detail::prefill_supported(fmt, M, N, K, A, B))
-        rc = cri::detail::launch_prefill(fmt, A, B, C, M, N, K, stream);
+        rc = cri::detail::launch_prefill(fmt, A, B, C, M, N, K, stream, ws, ws_floats, defer, defer_S);
     else if (M > kPrefillMinM && cri::detail::mfma_gemm_supported(fmt, M, N, K, A, B))
         rc = cri::detail::launch_mfma_gemm(fmt, A, B, C, M, N, K, stream);
     else if (M <= 16 && fmt32 && K <= 4096 && cri::detail::gemv_supported(fmt, K, B))
@@ -168,7 +168,11 @@ int cri_matmul(int format, const float* A, const void* B, float* C, int M, int N
 
 long long cri_matmul_workspace_bytes(int format, int M, int N, int K) {
     if (format < CRI_Q8_0 || format > CRI_FP16 || M < 0 || N < 0 || K < 0) return CRI_ERR_INVALID_ARGUMENT;
-    if (M < 2 || M > 16) return 0;  // no partial sums outside the decode-batch products
+    if (M < 2 || N == 0 || K == 0) return 0;
+    // above 16 rows: the prefill kernel's K split (formats and K it takes; the other kernels split nothing
+    // a workspace would hold)
+    if (M > kPrefillMinM)
+        return K % 256 == 0 ? static_cast<long long>(cri::detail::prefill_workspace_floats(M, N, K)) * 4 : 0;
     return static_cast<long long>(cri::detail::skinny_workspace_floats(M, N)) * 4;
 }
 
@@ -194,6 +198,21 @@ int cri_matmul_ws(int format, const float* A, const void* B, float* C, int M, in
         // choice is already deterministic and as fast or faster (8192 x 2048 at 16 rows: 9.7 us
         // unsplit against 11.1 split with a workspace)
         if (cri::detail::skinny_atomic_split(M, K)) {
+            ws = static_cast<float*>(workspace);
+            ws_floats = static_cast<long>(workspace_bytes / 4);
+        }
+    } else if (M > kPrefillMinM && N > 0 && K > 0) {
+        // the prefill GEMM's K split (few output tiles, e.g. 512 x 2048 x 8192): its partial sums go
+        // to the workspace and a second launch adds them in split order, in place of atomics into a
+        // zero-filled C (the same bits on every call)
+        const long long need = cri_matmul_workspace_bytes(format, M, N, K);
+        if (need > 0 && cri::detail::prefill_supported(format, M, N, K, A, B)) {
+            if (!workspace || workspace_bytes < need)
+                return fail(CRI_ERR_INVALID_ARGUMENT, fn,
+                            "workspace of at least " + std::to_string(need) +
+                                " bytes needed (cri_matmul_workspace_bytes)");
+            if (!aligned(workspace, 16) || !aligned(C, 16) || N % 4 != 0)
+                return fail(CRI_ERR_ALIGNMENT, fn, "workspace and C must be 16-byte aligned and N a multiple of 4");
             ws = static_cast<float*>(workspace);
             ws_floats = static_cast<long>(workspace_bytes / 4);
         }

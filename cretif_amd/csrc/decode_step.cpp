@@ -460,14 +460,22 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
         cur = 1 - cur;
     } else {
         // hidden += res; normed = RMSNorm(hidden)  (ref:src/model.cu:963-967 for the residual form)
-        rmsnorm_residual(h, res, L.attn_norm.data_as<float>(), h, normed_.data_as<float>(), M, D, eps, s);
+        prompt_norm(h, res, L.attn_norm.data_as<float>(), M, s, "attention RMSNorm");
         const float* n = normed_.data_as<float>();
+        float* w = split_ws_.data_as<float>();
+        const long wn = split_ws_.numel();
+        // K splits of the prompt GEMMs store their partial sums in split_ws_ instead of adding them
+        // with atomics: the fused projection's are added by RoPE, the others' by a reduction launch
         if (L.qkv_fused) {
-            matmul_dispatch(n, L.qkv, q, M, QD + 2 * KVD, D, L.qkv_fmt, s);
+            check_cri(cri::detail::matmul_split_ws(cri_id(L.qkv_fmt), n, L.qkv.data(), q, M, QD + 2 * KVD, D, w, wn, s,
+                                                   &qkv_sums),
+                      "q/k/v projection");
         } else {
-            matmul_dispatch(n, L.q, q, M, QD, D, L.q_fmt, s);
-            matmul_dispatch(n, L.k, k, M, KVD, D, L.k_fmt, s);
-            matmul_dispatch(n, L.v, v, M, KVD, D, L.v_fmt, s);
+            check_cri(cri::detail::matmul_split_ws(cri_id(L.q_fmt), n, L.q.data(), q, M, QD, D, w, wn, s), "q projection");
+            check_cri(cri::detail::matmul_split_ws(cri_id(L.k_fmt), n, L.k.data(), k, M, KVD, D, w, wn, s),
+                      "k projection");
+            check_cri(cri::detail::matmul_split_ws(cri_id(L.v_fmt), n, L.v.data(), v, M, KVD, D, w, wn, s),
+                      "v projection");
         }
     }
     if (!roped)
@@ -502,17 +510,38 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
                                                                pos, 1, nchunks, scale, attn_ws_.data_as<float>(), s),
                      "attention");
     }
-    // (2..16 tokens: its partial sums are left for the FFN's RMSNorm row kernel)
+    // (2..16 tokens, and a prompt's K split: its partial sums are left for the FFN's RMSNorm row kernel)
     cri::SplitSums o_sums;
     check_cri(cri::detail::matmul_split_ws(cri_id(L.o_fmt), ctx_.data_as<float>(), L.o.data(),
                                            attn_out_.data_as<float>(), M, D, QD, split_ws_.data_as<float>(),
-                                           split_ws_.numel(), s, split_flow(M) ? &o_sums : nullptr),
+                                           split_ws_.numel(), s,
+                                           split_flow(M) || prompt_defers(M) ? &o_sums : nullptr),
               "o projection");
     res = attn_out_.data_as<float>();
     res_splits_ = 0;
     res_part_ = o_sums.part;
     res_part_stride_ = o_sums.stride;
     res_part_count_ = o_sums.S;
+}
+
+bool DecodeStep::prompt_defers(int M) const {
+    return M > kFusedMaxBatch && cfg_.dim % 4 == 0 && cfg_.dim <= 4096;
+}
+
+// a prompt's RMSNorm(hidden + residual) into normed_, hidden updated in place; the residual is the
+// pending partial sums of a K-split projection when there are any (the row kernel adds them in
+// split order), else res
+void DecodeStep::prompt_norm(float* h, const float* res, const float* w, int M, hipStream_t s, const char* what) {
+    const int D = cfg_.dim;
+    if (res_part_count_ > 0) {
+        check_status(cri::detail::launch_split_norm(h, residual_sums(res_part_, res_part_stride_, res_part_count_,
+                                                                     nullptr, D),
+                                                    w, h, normed_.data_as<float>(), M, D, cfg_.rms_norm_eps, s),
+                     what);
+        res_part_count_ = 0;
+    } else {
+        rmsnorm_residual(h, res, w, h, normed_.data_as<float>(), M, D, cfg_.rms_norm_eps, s);
+    }
 }
 
 bool DecodeStep::split_flow(int M) const {
@@ -553,6 +582,7 @@ void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res,
     // of the SwiGLU activations instead of all of them) and leaves the partial sums for the next
     // RMSNorm prologue to add up (false: not taken, C is computed whole).
     bool split_down = false;
+    cri::SplitSums down_sums;  // a prompt's down projection: its K split's partial sums (S = 0: ffn_out written)
     auto down_split = [&](const float* gate, const float* up, int ld) {
         if (M != 1 || !next_takes_split(li)) return false;
         const cri::ActIn act{gate, up, nullptr, nullptr, ld, 0.0f};
@@ -632,7 +662,7 @@ void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res,
         }
         cur = 1 - cur;
     } else {
-        rmsnorm_residual(h, res, L.ffn_norm.data_as<float>(), h, normed_.data_as<float>(), M, D, eps, s);
+        prompt_norm(h, res, L.ffn_norm.data_as<float>(), M, s, "FFN RMSNorm");
         const float* n = normed_.data_as<float>();
         float* gate = ff;
         float* up = ff + static_cast<long>(MB) * F;
@@ -646,7 +676,11 @@ void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res,
             matmul_dispatch(n, L.up, up, M, F, D, L.up_fmt, s);
         }
         silu_mul(gate, up, act_.data_as<float>(), static_cast<long long>(M) * F, s);  // ref:src/model.cu:996-997
-        matmul_dispatch(act_.data_as<float>(), L.down, ffn_out, M, D, F, L.down_fmt, s);
+        // a K split's partial sums are left for the next RMSNorm row kernel (the next layer's or the final one)
+        check_cri(cri::detail::matmul_split_ws(cri_id(L.down_fmt), act_.data_as<float>(), L.down.data(), ffn_out, M, D,
+                                               F, split_ws_.data_as<float>(), split_ws_.numel(), s,
+                                               prompt_defers(M) ? &down_sums : nullptr),
+                  "down projection");
     }
     if (split_down) {
         res = res_parts_.data_as<float>();
@@ -654,7 +688,9 @@ void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res,
     } else {
         res = ffn_out;
     }
-    res_part_count_ = 0;
+    res_part_ = down_sums.part;
+    res_part_stride_ = down_sums.stride;
+    res_part_count_ = down_sums.S;
 }
 
 void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next_ids, hipStream_t s, float* taps,
@@ -673,7 +709,7 @@ void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next
     auto tap = [&](int i) {
         if (!taps) return;
         const cri::SplitSums r = res_splits_ ? residual_sums(res_parts_.data_as<float>(), D, res_splits_, nullptr, D)
-                                             : residual_sums(nullptr, 0, 0, res, D);
+                                             : residual_sums(res_part_, res_part_stride_, res_part_count_, res, D);
         check_status(cri::detail::launch_hidden_tap(hid_[cur].data_as<float>(), r,
                                                     taps + static_cast<long>(i) * M * D, M, D, s),
                      "layer tap");
@@ -705,6 +741,17 @@ void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next
                 matmul_transposed_b(n, W.data_as<float>(), logits, 1, V, D, s);
             else
                 matmul_dispatch(n, W, logits, 1, V, D, wf, s);
+        } else if (res_part_count_ > 0) {  // a prompt's pending partial sums: the row kernel on the last row
+            check_status(cri::detail::launch_split_norm(h + last, residual_sums(res_part_ + last, res_part_stride_,
+                                                                                res_part_count_, nullptr, D),
+                                                        out_norm_.data_as<float>(), hid_[1 - cur].data_as<float>() + last,
+                                                        normed_.data_as<float>(), 1, D, eps, s),
+                         "final RMSNorm");
+            res_part_count_ = 0;
+            if (wf == WeightFormat::FP32)
+                matmul_transposed_b(normed_.data_as<float>(), W.data_as<float>(), logits, 1, V, D, s);
+            else
+                matmul_dispatch(normed_.data_as<float>(), W, logits, 1, V, D, wf, s);
         } else if (wf != WeightFormat::FP32) {  // a plain residual: RMSNorm inside the LM head's prologue
             matmul_dispatch_rmsnorm(h + last, res ? res + last : nullptr, out_norm_.data_as<float>(),
                                     hid_[1 - cur].data_as<float>() + last, W, logits, 1, V, D, wf, eps, s);
@@ -741,7 +788,7 @@ void DecodeStep::enqueue(const int32_t* ids, int M, float* logits, int32_t* next
         matmul_dispatch_rmsnorm(h, res, out_norm_.data_as<float>(), hid_[1 - cur].data_as<float>(), W, logits, M, V,
                                 D, wf, eps, s);
     } else {
-        rmsnorm_residual(h, res, out_norm_.data_as<float>(), h, normed_.data_as<float>(), M, D, eps, s);
+        prompt_norm(h, res, out_norm_.data_as<float>(), M, s, "final RMSNorm");
         if (wf == WeightFormat::FP32)  // tied FP32 table (ref:src/model.cu:1027-1029)
             matmul_transposed_b(normed_.data_as<float>(), W.data_as<float>(), logits, M, V, D, s);
         else

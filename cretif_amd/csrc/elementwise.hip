@@ -94,9 +94,9 @@ __global__ __launch_bounds__(256) void rmsnorm_residual_vec_kernel(const float* 
 // [g n / G, (g + 1) n / G) of the row (G = gridDim.x parts, more workgroups reading the partial
 // sums) and writes their sum of v^2 to row_ss[16 g + row], for consumers that apply the factor
 // to their fp32 outputs (SplitSums.ssq).  Without it G = 1.  Parts of up to 4096 floats,
-// 16-byte aligned.
-__global__ __launch_bounds__(256) void split_norm_kernel(const float* __restrict__ h, const SplitSums r,
-                                                         const float* __restrict__ weight, float* __restrict__ output,
+// 16-byte aligned.  output may be h (each thread reads its elements before writing them).
+__global__ __launch_bounds__(256) void split_norm_kernel(const float* h, const SplitSums r,
+                                                         const float* __restrict__ weight, float* output,
                                                          float* __restrict__ normed, int n, float eps,
                                                          float* __restrict__ row_ss) {
     __shared__ float part[4];
@@ -176,8 +176,9 @@ int launch_split_norm(const float* h, const SplitSums& r, const float* weight, f
                       int n, float eps, hipStream_t stream, float* row_ss) {
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     const int parts = row_ss ? kNormParts : 1;
-    if (rows < 1 || rows > 16 || n % (4 * parts) != 0 || n / parts > 4096 || !a16(h) || !a16(weight) || !a16(output) ||
-        !a16(normed))
+    // row_ss holds 16 rows; without it any number of rows (a prompt's)
+    if (rows < 1 || rows > (row_ss ? 16 : 65535) || n % (4 * parts) != 0 || n / parts > 4096 || !a16(h) || !a16(weight) ||
+        !a16(output) || !a16(normed))
         return kDeclined;
     if (r.S && (r.S > dev::kSplitMaxS || r.N % 4 != 0 || r.stride % 4 != 0 || !a16(r.part))) return kDeclined;
     hipLaunchKernelGGL(dev::split_norm_kernel, dim3(parts, rows), dim3(256), 0, stream, h, r, weight, output, normed, n,

@@ -167,7 +167,20 @@ int launch_mfma_gemm(int fmt, const float* A, const void* B, float* C, int M, in
 
 // multi-token GEMM with weights decoded straight into MFMA operands, Q4_K, Q6_K and Q8_0 (prefill.hip)
 bool prefill_supported(int fmt, int M, int N, int K, const void* A, const void* B);
-int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream);
+// A K split over workgroups (few tiles) adds into a zero-filled C with fp32 atomics, or, given a
+// workspace of at least kPrefillSplitFloats floats (16-byte aligned, N % 4 == 0), stores its
+// partial sums there: left for the consumer with defer (defer->S > 0; defer_S: the count it
+// takes, 0 any), else added up into C (16-byte aligned) in split order by a second launch.
+int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream,
+                   float* ws = nullptr, long ws_floats = 0, SplitSums* defer = nullptr, int defer_S = 0);
+// K splits of the prefill GEMM are chosen so that tiles x splits < 512; so at most this many
+// partial-sum floats (512 tiles of 64 x 256); splits past 16 take the atomics
+constexpr long kPrefillSplitFloats = 512L * 64 * 256;
+// floats of partial sums launch_prefill stores in a workspace for this shape (0: no K split)
+long prefill_workspace_floats(int M, int N, int K);
+// C = the S partial sums of p added in split order (times p's RMSNorm row factor); M N % 4 == 0,
+// C and p.part 16-byte aligned, p.stride % 4 == 0 (mfma_skinny.hip)
+int launch_split_reduce(const SplitSums& p, float* C, int M, hipStream_t stream);
 
 // any-M fused dequant matmul, element-wise decode (generic.hip)
 int launch_generic_matmul(int fmt, const float* A, const void* B, float* C, int M, int N, int K,

@@ -1077,6 +1077,13 @@ static int launch_sk(const ActIn& A, const void* B, float* C, int M, int N, int 
     return 0;
 }
 
+int launch_split_reduce(const SplitSums& p, float* C, int M, hipStream_t stream) {
+    const long mn = static_cast<long>(M) * p.N;
+    hipLaunchKernelGGL(dev::split_reduce_kernel, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, stream,
+                       p, C, M);
+    return 0;
+}
+
 // up to 8 activation rows: hi and lo parts share each MFMA (paired lane rows)
 template <class F, int MODE>
 static int launch_sk_rows(const ActIn& A, const void* B, float* C, int M, int N, int K, int KC, int KS,

@@ -50,6 +50,7 @@
 #include "common.hpp"
 #include "decode.hpp"
 #include "internal.hpp"
+#include "split.hpp"
 
 namespace cri {
 namespace dev {
@@ -573,7 +574,7 @@ constexpr int prefill_lds_bytes() {
 template <class W>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_gemm_kernel(
     const float* __restrict__ A, const uint8_t* __restrict__ B, float* __restrict__ C, int M, int N, int K,
-    long row_bytes, int MT, int NT, int steps_per_split, int remap, int atomic) {
+    long row_bytes, int MT, int NT, int steps_per_split, int remap, int atomic, float* __restrict__ part) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     int* const rowflag = reinterpret_cast<int*>(lds);  // after the k loop
     int bid = blockIdx.x;
@@ -904,6 +905,9 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
     // lane: column n0 + fr, rows m0 + 32 u + 8 g + 4 h + r (accumulator 4 g + r); the stores
     // stream past the caches (the output is not read again by this kernel)
+    // (part: a K split's partial sums, split s at part + s M N, plain stores in place of atomics)
+    float* const out = part ? part + static_cast<long>(ksplit) * M * N : C;
+    const bool add = atomic && !part;
     const int n = n0 + fr;
     const int mrows = M - m0;  // rows of this tile inside C
 #pragma unroll
@@ -912,8 +916,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         for (int i = 0; i < 16; ++i) {
             const int ml = 32 * u + 8 * (i >> 2) + 4 * h + (i & 3);
             if (ml < mrows && n < N && !((flagged >> ml) & 1ull)) {
-                float* cp = C + static_cast<long>(m0 + ml) * N + n;
-                if (atomic)
+                float* cp = out + static_cast<long>(m0 + ml) * N + n;
+                if (add)
                     atomicAdd(cp, acc[u][i]);
                 else
                     __builtin_nontemporal_store(acc[u][i], cp);
@@ -932,8 +936,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         const uint8_t* wp = B + static_cast<long>(nn) * row_bytes;
         float sum = 0.0f;
         for (int k = s_begin * kPKS; k < s_end * kPKS; ++k) sum = __builtin_fmaf(x[k], decode_row_elem(fmt, wp, k), sum);
-        float* cp = C + static_cast<long>(m) * N + nn;
-        if (atomic)
+        float* cp = out + static_cast<long>(m) * N + nn;
+        if (add)
             atomicAdd(cp, sum);
         else
             *cp = sum;
@@ -961,7 +965,7 @@ namespace {
 // The kernels use more than the default 64 KB of LDS; the limit is raised once per kernel and device.
 template <class W>
 int launch_w(dim3 grid, hipStream_t stream, const float* A, const uint8_t* B, float* C, int M, int N, int K, long rb,
-             int MT, int NT, int sps, int remap, int atomic) {
+             int MT, int NT, int sps, int remap, int atomic, float* part) {
     constexpr int kMaxDevices = 64;
     constexpr int kLds = dev::prefill_lds_bytes<W>();
     static std::atomic<bool> ready[kMaxDevices];
@@ -974,36 +978,85 @@ int launch_w(dim3 grid, hipStream_t stream, const float* A, const uint8_t* B, fl
         ready[devid].store(true, std::memory_order_release);
     }
     hipLaunchKernelGGL(dev::prefill_gemm_kernel<W>, grid, dim3(dev::kPThreads), kLds, stream, A, B, C, M, N, K, rb,
-                       MT, NT, sps, remap, atomic);
+                       MT, NT, sps, remap, atomic, part);
     return 0;  // the launch's own status is read by the caller
 }
 
 }  // namespace
 
-int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream) {
-    const int MT = (M + dev::kPTM - 1) / dev::kPTM;
-    const int NT = (N + dev::kPTN - 1) / dev::kPTN;
-    const long tiles = static_cast<long>(MT) * NT;
+// k steps per split and the number of splits: the k range is split over workgroups (whole
+// groups of four steps each) while the tiles alone fill fewer than 256 CUs
+static int prefill_steps_per_split(int M, int N, int K, int* splits) {
+    const long tiles = static_cast<long>((M + dev::kPTM - 1) / dev::kPTM) * ((N + dev::kPTN - 1) / dev::kPTN);
     const int nsteps = K / dev::kPKS;
     int ks = 1;
     while (tiles * ks < 256 && nsteps >= 16 * ks) ks *= 2;
     int sps = (nsteps + ks - 1) / ks;
     sps = (sps + 3) / 4 * 4;  // groups of four steps: splits start on one
-    ks = (nsteps + sps - 1) / sps;
+    *splits = (nsteps + sps - 1) / sps;
+    return sps;
+}
+
+long prefill_workspace_floats(int M, int N, int K) {
+    if (M < 1 || N < 1 || K < 4 * dev::kPKS || K % (4 * dev::kPKS) != 0) return 0;
+    int ks = 1;
+    prefill_steps_per_split(M, N, K, &ks);
+    return ks > 1 && ks <= dev::kSplitMaxS ? static_cast<long>(ks) * M * N : 0;
+}
+
+int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream, float* ws,
+                   long ws_floats, SplitSums* defer, int defer_S) {
+    if (defer) defer->S = 0;
+    const int MT = (M + dev::kPTM - 1) / dev::kPTM;
+    const int NT = (N + dev::kPTN - 1) / dev::kPTN;
+    const long tiles = static_cast<long>(MT) * NT;
+    int ks = 1;
+    const int sps = prefill_steps_per_split(M, N, K, &ks);
     const long grid = tiles * ks;
     if (grid > 0x7FFFFFFFL) return kDeclined;
     const int remap = grid % 8 == 0 ? 1 : 0;
     const int atomic = ks > 1 ? 1 : 0;
-    if (atomic) launch_fill_zero(C, static_cast<long>(M) * N, stream);
+    // A K split goes, when a workspace holds its partial sums, to plain stores there (split s at
+    // ws + s M N), added up in split order by the consumer (defer) or by the reduction kernel:
+    // deterministic, and no zero fill; without one, fp32 atomics into a zero-filled C, whose
+    // order (and so the last bits) varies.  The atomics are dear: at 512 x 2048 x 8192 Q4_K the
+    // kernel storing in their place took 35.3 against 43.0 us (same box), and with the workspace
+    // and the reduction launch the product takes 37.3 against 41.1 us.
+    const long mn = static_cast<long>(M) * N;
+    float* part = nullptr;
+    if (atomic && ws && ks <= dev::kSplitMaxS && ks * mn <= ws_floats && N % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(ws) & 15u) == 0 && (defer ? defer_S == 0 || defer_S == ks
+                                                              : (reinterpret_cast<uintptr_t>(C) & 15u) == 0))
+        part = ws;
+    if (atomic && !part) launch_fill_zero(C, mn, stream);
     const long rb = row_bytes(fmt, K);
     const dim3 g(static_cast<unsigned>(grid));
     const uint8_t* Bb = static_cast<const uint8_t*>(B);
-    if (fmt == kFmtQ4_K) return launch_w<dev::PQ4K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
-    if (fmt == kFmtQ6_K) return launch_w<dev::PQ6K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
-    if (fmt == kFmtQ4_0) return launch_w<dev::PQ4_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
-    if (fmt == kFmtQ5_0) return launch_w<dev::PQ5_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
-    if (fmt == kFmtF16) return launch_w<dev::PF16>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
-    return launch_w<dev::PQ8_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic);
+    int rc;
+    if (fmt == kFmtQ4_K)
+        rc = launch_w<dev::PQ4K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic, part);
+    else if (fmt == kFmtQ6_K)
+        rc = launch_w<dev::PQ6K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic, part);
+    else if (fmt == kFmtQ4_0)
+        rc = launch_w<dev::PQ4_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic, part);
+    else if (fmt == kFmtQ5_0)
+        rc = launch_w<dev::PQ5_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic, part);
+    else if (fmt == kFmtF16)
+        rc = launch_w<dev::PF16>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic, part);
+    else
+        rc = launch_w<dev::PQ8_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, atomic, part);
+    if (rc != 0 || !part) return rc;
+    SplitSums sums;
+    sums.part = part;
+    sums.stride = mn;
+    sums.S = ks;
+    sums.N = N;
+    sums.K = K;
+    if (defer)
+        *defer = sums;  // the consumer adds them up
+    else
+        launch_split_reduce(sums, C, M, stream);
+    return 0;
 }
 
 }  // namespace detail

@@ -166,15 +166,20 @@ private:
     bool capturing_ = false;  // enqueue() is recording a graph: shapes independent of the position
     Tensor res_parts_;    // the down projection's K-split partial sums at one token
     int res_splits_ = 0;  // > 0: the pending residual is that many partial sums in res_parts_
-    // 2..16 tokens: the pending residual as the unreduced partial sums of the o projection
-    // (res_part_count_ partial sums res_part_stride_ floats apart from res_part_; 0: the plain
-    // residual pointer); the FFN's RMSNorm row kernel adds them to the hidden state and
-    // normalizes, and gate/up take plain activations
+    // 2..16 tokens: the pending residual as the unreduced partial sums of the o projection, and
+    // for a prompt those of a K-split o or down projection (res_part_count_ partial sums
+    // res_part_stride_ floats apart from res_part_; 0: the plain residual pointer); the next
+    // RMSNorm row kernel adds them to the hidden state and normalizes, and the projections after
+    // it take plain activations
     Tensor norm_ss_;  // the row kernel's per-row sums of squares, [16 splits][16 rows], splits 1.. zero
     const float* res_part_ = nullptr;
     long res_part_stride_ = 0;
     int res_part_count_ = 0;
     bool split_flow(int M) const;
+    // a prompt (above 16 tokens) leaves the o and down projections' K-split partial sums for the
+    // RMSNorm row kernel that follows them (dim % 4 == 0, dim <= 4096)
+    bool prompt_defers(int M) const;
+    void prompt_norm(float* h, const float* res, const float* w, int M, hipStream_t s, const char* what);
     int pos_host_ = 0;
     hipGraph_t graph_ = nullptr;
     hipGraphExec_t graph_exec_ = nullptr;

@@ -634,6 +634,35 @@ def test_matmul_ws_same_bits_every_call(orc, fmt, M, N, K):
     assert normwise_rel_err(outs[0], orc.matmul_quant(fmt, A, Bq, N, K)) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0", "fp16"])
+@pytest.mark.parametrize("M,N,K,splits", [(96, 2048, 2048, 4), (64, 512, 8192, 16), (17, 300, 4096, 8)])
+def test_matmul_ws_prefill_split(orc, fmt, M, N, K, splits):
+    # above 16 rows with few output tiles the prefill GEMM splits K over workgroups: with a
+    # workspace the partial sums are stored there and added in split order (the same bits on
+    # every call), without one they go to C with atomics; both within the prefill bar of the oracle
+    A = quant.randn(M * K, seed=M + N + K).reshape(M, K)
+    Bq = weights(fmt, N, K, seed=N + K + 1)
+    need = cri.matmul_workspace_bytes(fmt, M, N, K)
+    assert need == splits * M * N * 4
+    ws = torch.full((need // 4,), float("nan"), dtype=torch.float32, device="cuda")
+    dA, dB = dev(A), dev(Bq)
+    outs = []
+    for _ in range(3):
+        C = torch.full((M, N), float("nan"), device="cuda")
+        cri.matmul_ws(fmt, dA, dB, C, M, N, K, ws)
+        outs.append(host(C))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    ref = orc.matmul_quant(fmt, A, Bq, N, K)
+    err = normwise_rel_err(outs[0], ref)
+    C = torch.full((M, N), float("nan"), device="cuda")
+    cri.matmul(fmt, dA, dB, C, M, N, K)
+    err_atomic = normwise_rel_err(host(C), ref)
+    print("prefill split %s %dx%dx%d: workspace %.2e, atomics %.2e" % (fmt, M, N, K, err, err_atomic))
+    assert err <= PREFILL_TOL and err_atomic <= PREFILL_TOL
+    # the two differ only in the order the partial sums are added (a few fp32 roundings)
+    assert normwise_rel_err(outs[0], host(C)) <= 1e-5
+
+
 def test_matmul_ws_errors_and_other_row_counts(orc):
     fmt, N, K = "q4_k", 512, 2048
     A = quant.randn(16 * K, seed=3).reshape(16, K)
@@ -652,9 +681,13 @@ def test_matmul_ws_errors_and_other_row_counts(orc):
         cri.matmul_ws(fmt, dev(A), dev(Bq), C, 16, N - 2, K, ws)
     with pytest.raises(cri.CretifError):
         cri.matmul_ws(9, dev(A), dev(Bq), C, 16, N, K, ws)
-    # one row and prefill-sized batches use no workspace (null is fine) and match cri_matmul
-    assert cri.matmul_workspace_bytes(fmt, 1, N, K) == 0 and cri.matmul_workspace_bytes(fmt, 17, N, K) == 0
-    for M in (1, 17):
+    # one row, and a prefill-sized batch whose tiles fill the GPU unsplit, use no workspace (null
+    # is fine) and match cri_matmul; a prefill-sized batch with few tiles splits K and needs one
+    assert cri.matmul_workspace_bytes(fmt, 1, N, K) == 0 and cri.matmul_workspace_bytes(fmt, 512, 8192, K) == 0
+    assert cri.matmul_workspace_bytes(fmt, 17, N, K) == 4 * 17 * N * 4
+    with pytest.raises(cri.CretifError):
+        cri.matmul_ws(fmt, dev(A), dev(Bq), torch.empty(17, N, device="cuda"), 17, N, K, None)
+    for M in (1,):
         Am = quant.randn(M * K, seed=M).reshape(M, K)
         C1 = torch.empty(M, N, device="cuda")
         cri.matmul_ws(fmt, dev(Am), dev(Bq), C1, M, N, K, None)
