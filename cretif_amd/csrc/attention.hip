@@ -432,7 +432,8 @@ constexpr int kXcds = 8;
 
 __global__ __launch_bounds__(64 * kMrWaves) void decode_attn_mrow_kernel(
     const float* __restrict__ Q, const float* __restrict__ Kc, const float* __restrict__ Vc, float* __restrict__ ws,
-    int G, int n_kv, int M, const int* __restrict__ kv_dev, int kv0, float qscale, int nchunks, long ldq) {
+    int G, int n_kv, int M, const int* __restrict__ kv_dev, int kv0, float qscale, int nchunks, long ldq,
+    float* __restrict__ out, long ldo) {
     __shared__ __attribute__((aligned(16))) float acc_s[kMrWaves][32 * kMrAld];
     __shared__ float mx_s[kMrWaves][32];
     __shared__ float l_s[kMrWaves][32];
@@ -590,6 +591,12 @@ __global__ __launch_bounds__(64 * kMrWaves) void decode_attn_mrow_kernel(
         r1 += f * *reinterpret_cast<const f32x4*>(src + 4);
     }
     const int m = qq / G, g = qq - m * G;
+    if (out) {  // one chunk: the merged output itself, as the combine kernel would divide it
+        float* o = out + m * ldo + static_cast<long>(kvh * G + g) * kMrD + d0;
+        *reinterpret_cast<f32x4*>(o) = f32x4{r0.x / L, r0.y / L, r0.z / L, r0.w / L};
+        *reinterpret_cast<f32x4*>(o + 4) = f32x4{r1.x / L, r1.y / L, r1.z / L, r1.w / L};
+        return;
+    }
     float* rec = ws + ((static_cast<long>(m) * H + kvh * G + g) * nchunks + c) * (kMrD + 4);
     *reinterpret_cast<f32x4*>(rec + 4 + d0) = r0;
     *reinterpret_cast<f32x4*>(rec + 8 + d0) = r1;
@@ -786,9 +793,12 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
         const long nqh = (static_cast<long>(rows) * G + 31) / 32;
         const long wgs = static_cast<long>(n_kv_heads) * nchunks * nqh;
         if (wgs > 0x7FFFFFFFL) return kDeclined;
+        // one chunk (a prompt's many query groups fill the GPU alone): the kernel writes the output
+        const bool direct = nchunks == 1 && ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
         hipLaunchKernelGGL(dev::decode_attn_mrow_kernel, dim3(static_cast<unsigned>(wgs)), dim3(64 * dev::kMrWaves), 0,
-                           stream, Q, K, V, ws, G, n_kv_heads, rows, kv_dev, kv0, qscale, nchunks, ldq);
-        launch_combine(ws, out, n_heads, rows, D, nchunks, ldo, stream);
+                           stream, Q, K, V, ws, G, n_kv_heads, rows, kv_dev, kv0, qscale, nchunks, ldq,
+                           direct ? out : nullptr, ldo);
+        if (!direct) launch_combine(ws, out, n_heads, rows, D, nchunks, ldo, stream);
         return 0;
     }
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(rows));
@@ -802,11 +812,20 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
     return 0;
 }
 
+bool decode_attention_rows_mrow(int rows, int head_dim) { return use_mrow(rows, head_dim); }
+
 int decode_attention_rows_chunks(int n_heads, int n_kv_heads, int head_dim, int max_kv_len, int rows) {
     if (use_mrow(rows, head_dim)) {
         const int tiles = (max_kv_len + dev::kSplitTile - 1) / dev::kSplitTile;
         const int per_wg = (tiles + dev::kMrWaves - 1) / dev::kMrWaves;
-        return per_wg < 1 ? 1 : (per_wg < kMrowMaxChunks ? per_wg : kMrowMaxChunks);
+        int n = per_wg < 1 ? 1 : (per_wg < kMrowMaxChunks ? per_wg : kMrowMaxChunks);
+        // many query groups (a prompt: rows x heads / 32 of them per KV head) already fill the GPU:
+        // fewer, longer chunks (about 512 workgroups in all), down to one, whose workgroups write
+        // the output without records or a combine launch
+        const long groups = static_cast<long>(n_kv_heads) * ((static_cast<long>(rows) * (n_heads / n_kv_heads) + 31) / 32);
+        const long cap = (512 + groups - 1) / groups;
+        if (cap < n) n = static_cast<int>(cap);
+        return n;
     }
     return split_chunks(n_heads, n_kv_heads, head_dim, max_kv_len, 1, -1);
 }

@@ -174,9 +174,11 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     ff_ = Tensor::empty({MB, 2 * static_cast<int64_t>(c.intermediate_size)});
     act_ = Tensor::empty({MB, static_cast<int64_t>(c.intermediate_size)});
     ffn_out_ = Tensor::empty({MB, static_cast<int64_t>(c.dim)});
-    // records for the larger of the one-row and the multi-row chunk counts
-    // (the split attention serves batches of up to kFusedMaxBatch rows; larger ones take the prompt flow)
-    const int64_t arows = std::min<int64_t>(MB, kFusedMaxBatch);
+    // records for the larger of the one-row and the multi-row chunk counts (the split attention
+    // serves batches of up to kFusedMaxBatch rows, and prompts too where the multi-row kernel
+    // takes them: head_dim 64)
+    prompt_mrow_ = MB > kFusedMaxBatch && cri::detail::decode_attention_rows_mrow(static_cast<int>(MB), c.head_dim);
+    const int64_t arows = prompt_mrow_ ? MB : std::min<int64_t>(MB, kFusedMaxBatch);
     const int ch1 = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, 1);
     const int chm = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len,
                                                               static_cast<int>(arows));
@@ -192,7 +194,7 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     argmax_count_ = Tensor::zeros({MB});
     res_parts_ = Tensor::empty({static_cast<int64_t>(cri::kResMaxSplits) * c.dim});
     norm_ss_ = Tensor::zeros({256});
-    if (MB > kFusedMaxBatch) {
+    if (MB > kFusedMaxBatch && !prompt_mrow_) {
         const int64_t rows = std::min<int64_t>(MB, kPromptRows), T4 = round4(c.max_seq_len);
         gqa_q_ = Tensor::empty({c.n_heads * rows * c.head_dim});
         gqa_o_ = Tensor::empty({c.n_heads * rows * c.head_dim});
@@ -485,7 +487,7 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
                      "rope/append");
     // row m attends to positions [0, pos + m] (ref:src/attention.cu:60-75; one token: :410-511)
     const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
-    if (M > kFusedMaxBatch) {
+    if (M > kFusedMaxBatch && !prompt_mrow_) {
         // a prompt: Q K^T and P V through batched_matmul_gqa around a causal softmax, in row blocks
         // (ref:src/attention.cu:809-871); the products span the cache positions the block can see,
         // rounded up to a multiple of 4 -- the whole cache when recording a graph, which is then
@@ -503,6 +505,8 @@ void DecodeStep::attn_block(Layer& L, int li, int M, int& cur, const float*& res
                          "prompt attention");
         }
     } else {
+        // chunks for the whole cache (the chunk length follows the position in the kernel, so a
+        // graph is valid at any position and computes what the eager step does)
         const int nchunks = cri::detail::decode_attention_rows_chunks(cfg_.n_heads, cfg_.n_kv_heads, cfg_.head_dim,
                                                                       cfg_.max_seq_len, M);
         check_status(cri::detail::launch_decode_attention_rows(q, ldq, k_cache(li), v_cache(li), ctx_.data_as<float>(),

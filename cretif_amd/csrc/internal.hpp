@@ -241,6 +241,8 @@ int launch_decode_attention_split(const float* Q, const float* K, const float* V
 // per wave of a four-wave workgroup, up to 16 chunks); ws holds rows * n_heads * nchunks records
 // of head_dim + 4 floats
 int decode_attention_rows_chunks(int n_heads, int n_kv_heads, int head_dim, int max_kv_len, int rows);
+// true where `rows` query rows take the multi-row (matrix-core) kernel
+bool decode_attention_rows_mrow(int rows, int head_dim);
 int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const float* V, float* out, long ldo,
                                  int rows, int n_heads, int n_kv_heads, int head_dim, const int* kv_dev, int kv0,
                                  int nchunks, float scale, float* ws, hipStream_t stream);

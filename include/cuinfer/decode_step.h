@@ -164,6 +164,9 @@ private:
     // kPromptRows, on Q / K^T / V / scores / output workspaces (allocated when max_batch > 16)
     Tensor gqa_q_, gqa_k_, gqa_v_, gqa_s_, gqa_o_;
     bool capturing_ = false;  // enqueue() is recording a graph: shapes independent of the position
+    // prompts (above 16 tokens) through the multi-row split attention (head_dim 64) instead of
+    // batched_matmul_gqa around a materialized causal softmax
+    bool prompt_mrow_ = false;
     Tensor res_parts_;    // the down projection's K-split partial sums at one token
     int res_splits_ = 0;  // > 0: the pending residual is that many partial sums in res_parts_
     // 2..16 tokens: the pending residual as the unreduced partial sums of the o projection, and
