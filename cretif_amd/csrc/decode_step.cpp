@@ -670,14 +670,22 @@ void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res,
         const float* n = normed_.data_as<float>();
         float* gate = ff;
         float* up = ff + static_cast<long>(MB) * F;
+        // (a K split, at short prompts, goes through split_ws_ and a reduction launch: the same bits
+        // on every call)
+        float* w = split_ws_.data_as<float>();
+        const long wn = split_ws_.numel();
         if (L.gu_fused) {
             // the stacked matrix read as its two halves ([0, F) gate, [F, 2F) up)
             const Tensor g = L.gu.view(2, 0, F), u = L.gu.view(2, F, 2 * F);
-            matmul_dispatch(n, g, gate, M, F, D, L.gu_fmt, s);
-            matmul_dispatch(n, u, up, M, F, D, L.gu_fmt, s);
+            check_cri(cri::detail::matmul_split_ws(cri_id(L.gu_fmt), n, g.data(), gate, M, F, D, w, wn, s),
+                      "gate projection");
+            check_cri(cri::detail::matmul_split_ws(cri_id(L.gu_fmt), n, u.data(), up, M, F, D, w, wn, s),
+                      "up projection");
         } else {
-            matmul_dispatch(n, L.gate, gate, M, F, D, L.gate_fmt, s);
-            matmul_dispatch(n, L.up, up, M, F, D, L.up_fmt, s);
+            check_cri(cri::detail::matmul_split_ws(cri_id(L.gate_fmt), n, L.gate.data(), gate, M, F, D, w, wn, s),
+                      "gate projection");
+            check_cri(cri::detail::matmul_split_ws(cri_id(L.up_fmt), n, L.up.data(), up, M, F, D, w, wn, s),
+                      "up projection");
         }
         silu_mul(gate, up, act_.data_as<float>(), static_cast<long long>(M) * F, s);  // ref:src/model.cu:996-997
         // a K split's partial sums are left for the next RMSNorm row kernel (the next layer's or the final one)
