@@ -674,7 +674,14 @@ void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res,
         // on every call)
         float* w = split_ws_.data_as<float>();
         const long wn = split_ws_.numel();
-        if (L.gu_fused) {
+        // the stacked gate/up matrix: both products and SiLU(gate) * up in one launch where the
+        // tiles fill the GPU unsplit (ref:src/model.cu:986-997 computes the same in three steps)
+        const int fused_rc = L.gu_fused ? cri::detail::launch_prefill_swiglu(cri_id(L.gu_fmt), n, L.gu.data(),
+                                                                             act_.data_as<float>(), M, F, D, s)
+                                        : cri::detail::kDeclined;
+        if (fused_rc != cri::detail::kDeclined) {
+            check_status(fused_rc, "gate/up projection with SiLU * up");
+        } else if (L.gu_fused) {
             // the stacked matrix read as its two halves ([0, F) gate, [F, 2F) up)
             const Tensor g = L.gu.view(2, 0, F), u = L.gu.view(2, F, 2 * F);
             check_cri(cri::detail::matmul_split_ws(cri_id(L.gu_fmt), n, g.data(), gate, M, F, D, w, wn, s),
@@ -687,7 +694,8 @@ void DecodeStep::ffn_block(Layer& L, int li, int M, int& cur, const float*& res,
             check_cri(cri::detail::matmul_split_ws(cri_id(L.up_fmt), n, L.up.data(), up, M, F, D, w, wn, s),
                       "up projection");
         }
-        silu_mul(gate, up, act_.data_as<float>(), static_cast<long long>(M) * F, s);  // ref:src/model.cu:996-997
+        if (fused_rc == cri::detail::kDeclined)
+            silu_mul(gate, up, act_.data_as<float>(), static_cast<long long>(M) * F, s);  // ref:src/model.cu:996-997
         // a K split's partial sums are left for the next RMSNorm row kernel (the next layer's or the final one)
         check_cri(cri::detail::matmul_split_ws(cri_id(L.down_fmt), act_.data_as<float>(), L.down.data(), ffn_out, M, D,
                                                F, split_ws_.data_as<float>(), split_ws_.numel(), s,

@@ -176,6 +176,10 @@ int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int 
 // K splits of the prefill GEMM are chosen so that tiles x splits < 512; so at most this many
 // partial-sum floats (512 tiles of 64 x 256); splits past 16 take the atomics
 constexpr long kPrefillSplitFloats = 512L * 64 * 256;
+// C[M, F] = SiLU(A gate^T) * (A up^T) for a stacked gate/up matrix B of 2F rows (gate first), the
+// product and the elementwise step in one launch (the SiLU * up of the separate kernel, bit for
+// bit); kDeclined where the tiles would need a K split (short prompts) or the kernel does not apply
+int launch_prefill_swiglu(int fmt, const float* A, const void* B, float* C, int M, int F, int K, hipStream_t stream);
 // floats of partial sums launch_prefill stores in a workspace for this shape (0: no K split)
 long prefill_workspace_floats(int M, int N, int K);
 // C = the S partial sums of p added in split order (times p's RMSNorm row factor); M N % 4 == 0,

@@ -51,6 +51,7 @@
 #include "decode.hpp"
 #include "internal.hpp"
 #include "split.hpp"
+#include "act.hpp"
 
 namespace cri {
 namespace dev {
@@ -574,7 +575,8 @@ constexpr int prefill_lds_bytes() {
 template <class W>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_gemm_kernel(
     const float* __restrict__ A, const uint8_t* __restrict__ B, float* __restrict__ C, int M, int N, int K,
-    long row_bytes, int MT, int NT, int steps_per_split, int remap, int atomic, float* __restrict__ part) {
+    long row_bytes, int MT, int NT, int steps_per_split, int remap, int atomic, float* __restrict__ part, int swiglu) {
+    static_assert(prefill_lds_bytes<W>() >= 256 + kPTM * kPTN * 4, "the swiglu epilogue's C tile fits in LDS");
     extern __shared__ __attribute__((aligned(16))) char lds[];
     int* const rowflag = reinterpret_cast<int*>(lds);  // after the k loop
     int bid = blockIdx.x;
@@ -594,7 +596,12 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, fr = lane & 31;
-    const int m0 = mt * kPTM, n0 = nt * kPTN + 32 * wave;
+    // swiglu: B holds N = 2F rows, gate [0, F) then up [F, 2F), and C = SiLU(A gate^T) * (A up^T)
+    // is [M, F]; the tile's kPTN / 2 output columns are gate rows (waves 0-3) and the same up rows
+    // (waves 4-7), met in LDS after the k loop
+    const int F = N >> 1;
+    const int m0 = mt * kPTM;
+    const int n0 = swiglu ? (wave >> 2) * F + nt * (kPTN / 2) + 32 * (wave & 3) : nt * kPTN + 32 * wave;
 
     // activation staging: 16 lanes cover one row's 64 columns (256 contiguous bytes per load
     // instruction and row); thread -> columns 4 ap .. 4 ap + 3 of rows ar0 and ar0 + 32
@@ -910,24 +917,60 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const bool add = atomic && !part;
     const int n = n0 + fr;
     const int mrows = M - m0;  // rows of this tile inside C
+    if (swiglu) {
+        // the 64 x 256 tile through LDS (above the flags; every operand read is done), then
+        // thread -> output column nt * 128 + (tid & 127) of rows tid >> 7, + 4, ...:
+        // SiLU(gate) * up with the bits of the separate elementwise kernel
+        float* const ct = reinterpret_cast<float*>(lds + 256);
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int ml = 32 * u + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (ml < mrows && n < N && !((flagged >> ml) & 1ull)) {
-                float* cp = out + static_cast<long>(m0 + ml) * N + n;
-                if (add)
-                    atomicAdd(cp, acc[u][i]);
-                else
-                    __builtin_nontemporal_store(acc[u][i], cp);
+            for (int i = 0; i < 16; ++i) ct[(32 * u + 8 * (i >> 2) + 4 * h + (i & 3)) * kPTN + 32 * wave + fr] = acc[u][i];
+        __syncthreads();
+        const int j = tid & (kPTN / 2 - 1), col = nt * (kPTN / 2) + j;
+        for (int ml = tid / (kPTN / 2); ml < kPTM; ml += kPThreads / (kPTN / 2))
+            if (ml < mrows && col < F && !((flagged >> ml) & 1ull))
+                __builtin_nontemporal_store(silu_f(ct[ml * kPTN + j]) * ct[ml * kPTN + kPTN / 2 + j],
+                                            C + static_cast<long>(m0 + ml) * F + col);
+    } else {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int ml = 32 * u + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (ml < mrows && n < N && !((flagged >> ml) & 1ull)) {
+                    float* cp = out + static_cast<long>(m0 + ml) * N + n;
+                    if (add)
+                        atomicAdd(cp, acc[u][i]);
+                    else
+                        __builtin_nontemporal_store(acc[u][i], cp);
+                }
             }
-        }
+    }
 
     // fp32 path for flagged rows: thread -> column nt * 256 + (tid & 255) of the flagged rows
     // of parity tid >> 8, the reference's per-element decode and a sequential fp32 sum over
     // this workgroup's k range
     const int fmt = W::kFmt;
+    if (swiglu) {
+        // thread -> output column nt * 128 + (tid & 127) of the flagged rows of class tid >> 7 (mod
+        // 4): the gate and up sums over the whole k range (no split), then SiLU(gate) * up
+        for (unsigned long long rest = flagged & (0x1111111111111111ull << (tid >> 7)); rest != 0; rest &= rest - 1) {
+            const int ml = __builtin_ctzll(rest);
+            const int m = m0 + ml, col = nt * (kPTN / 2) + (tid & (kPTN / 2 - 1));
+            if (m >= M || col >= F) continue;
+            const float* x = A + static_cast<long>(m) * K;
+            const uint8_t* gp = B + static_cast<long>(col) * row_bytes;
+            const uint8_t* up = B + static_cast<long>(F + col) * row_bytes;
+            float g = 0.0f, v = 0.0f;
+            for (int k = 0; k < K; ++k) {
+                g = __builtin_fmaf(x[k], decode_row_elem(fmt, gp, k), g);
+                v = __builtin_fmaf(x[k], decode_row_elem(fmt, up, k), v);
+            }
+            C[static_cast<long>(m) * F + col] = silu_f(g) * v;
+        }
+        return;
+    }
     for (unsigned long long rest = flagged & (0x5555555555555555ull << (tid >> 8)); rest != 0; rest &= rest - 1) {
         const int ml = __builtin_ctzll(rest);
         const int m = m0 + ml, nn = nt * kPTN + (tid & 255);
@@ -965,7 +1008,7 @@ namespace {
 // The kernels use more than the default 64 KB of LDS; the limit is raised once per kernel and device.
 template <class W>
 int launch_w(dim3 grid, hipStream_t stream, const float* A, const uint8_t* B, float* C, int M, int N, int K, long rb,
-             int MT, int NT, int sps, int remap, int atomic, float* part) {
+             int MT, int NT, int sps, int remap, int atomic, float* part, int swiglu = 0) {
     constexpr int kMaxDevices = 64;
     constexpr int kLds = dev::prefill_lds_bytes<W>();
     static std::atomic<bool> ready[kMaxDevices];
@@ -978,7 +1021,7 @@ int launch_w(dim3 grid, hipStream_t stream, const float* A, const uint8_t* B, fl
         ready[devid].store(true, std::memory_order_release);
     }
     hipLaunchKernelGGL(dev::prefill_gemm_kernel<W>, grid, dim3(dev::kPThreads), kLds, stream, A, B, C, M, N, K, rb,
-                       MT, NT, sps, remap, atomic, part);
+                       MT, NT, sps, remap, atomic, part, swiglu);
     return 0;  // the launch's own status is read by the caller
 }
 
@@ -1002,6 +1045,29 @@ long prefill_workspace_floats(int M, int N, int K) {
     int ks = 1;
     prefill_steps_per_split(M, N, K, &ks);
     return ks > 1 && ks <= dev::kSplitMaxS ? static_cast<long>(ks) * M * N : 0;
+}
+
+int launch_prefill_swiglu(int fmt, const float* A, const void* B, float* C, int M, int F, int K, hipStream_t stream) {
+    if (F < 1 || !prefill_supported(fmt, M, 2 * F, K, A, B)) return kDeclined;
+    const int MT = (M + dev::kPTM - 1) / dev::kPTM;
+    const int NT = (F + dev::kPTN / 2 - 1) / (dev::kPTN / 2);
+    const long tiles = static_cast<long>(MT) * NT;
+    // whole k range per workgroup: the epilogue needs finished sums
+    int ks = 1;
+    prefill_steps_per_split(M, 2 * F, K, &ks);
+    if (ks > 1 || tiles > 0x7FFFFFFFL) return kDeclined;
+    const int sps = K / dev::kPKS;
+    const int remap = tiles % 8 == 0 ? 1 : 0;
+    const long rb = row_bytes(fmt, K);
+    const dim3 g(static_cast<unsigned>(tiles));
+    const uint8_t* Bb = static_cast<const uint8_t*>(B);
+    const int N = 2 * F;
+    if (fmt == kFmtQ4_K) return launch_w<dev::PQ4K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, 0, nullptr, 1);
+    if (fmt == kFmtQ6_K) return launch_w<dev::PQ6K>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, 0, nullptr, 1);
+    if (fmt == kFmtQ4_0) return launch_w<dev::PQ4_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, 0, nullptr, 1);
+    if (fmt == kFmtQ5_0) return launch_w<dev::PQ5_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, 0, nullptr, 1);
+    if (fmt == kFmtF16) return launch_w<dev::PF16>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, 0, nullptr, 1);
+    return launch_w<dev::PQ8_0>(g, stream, A, Bb, C, M, N, K, rb, MT, NT, sps, remap, 0, nullptr, 1);
 }
 
 int launch_prefill(int fmt, const float* A, const void* B, float* C, int M, int N, int K, hipStream_t stream, float* ws,

@@ -562,3 +562,27 @@ def test_prompt_row_blocks_nan_cache_and_replay(orc, head_dim):
         dec.replay(stream=s)
     s.synchronize()
     assert normwise_rel_err(b.cpu().numpy(), eager) <= 1e-5
+
+
+def test_prompt_swiglu_flagged_rows(orc):
+    # a prompt's stacked gate/up matrix runs as one launch with SiLU(gate) * up in its epilogue; rows
+    # whose activations leave fp16's range (an FFN norm weight of 1e5 makes every row's reach ~1e5)
+    # are recomputed there in fp32, both sums and then SiLU * up, as the separate products and the
+    # elementwise kernel would; the logits against the oracle at the prefill bar
+    m = make_model(2, dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1024, vocab=900, seed=91,
+                   fmts={n: "fp16" for n in ("q", "k", "v", "o", "gate", "up", "down")}, tok="q8_0", lm="fp16",
+                   big_tables=False)
+    m["layers"][0]["ffn_norm"] = (m["layers"][0]["ffn_norm"] * 1e5).astype(np.float32)
+    M, pos, max_seq = 64, 5, 256
+    dec = make_decoder(m, max_seq=max_seq, max_batch=M)
+    kc, vc = random_cache(m, max_seq, 92)
+    load_cache(dec, kc, vc)
+    ids = torch.from_numpy(np.random.default_rng(93).integers(0, m["vocab"], M).astype(np.int32)).cuda()
+    a = torch.empty(M, m["vocab"], device="cuda")
+    dec.set_position(pos)
+    dec.forward(ids, M, a)
+    got = a.cpu().numpy()
+    ref, _ = orc.decode_step(m, list(ids.cpu().numpy()), pos, [k.copy() for k in kc], [v.copy() for v in vc])
+    err = normwise_rel_err(got, ref)
+    print("prompt M=%d, FFN activations ~1e5: normwise err %.2e" % (M, err))
+    assert np.isfinite(got).all() and err <= PREFILL_TOL
