@@ -1032,8 +1032,18 @@ int launch_w(dim3 grid, hipStream_t stream, const float* A, const uint8_t* B, fl
 static int prefill_steps_per_split(int M, int N, int K, int* splits) {
     const long tiles = static_cast<long>((M + dev::kPTM - 1) / dev::kPTM) * ((N + dev::kPTN - 1) / dev::kPTN);
     const int nsteps = K / dev::kPKS;
+    int kmax = 1;
+    while (tiles * kmax < 256 && nsteps >= 16 * kmax) kmax *= 2;
+    // one workgroup per CU: of the splits up to kmax, the one with the fewest groups of four steps
+    // in sequence on a CU (rounds of 256 workgroups x groups per split), the fewer splits on a tie
+    // (512 x 3072 x 2048: two splits in one round rather than four in two)
+    const long groups = (nsteps + 3) / 4;
     int ks = 1;
-    while (tiles * ks < 256 && nsteps >= 16 * ks) ks *= 2;
+    long best = groups;
+    for (int k = 2; k <= kmax; k *= 2) {
+        const long cost = (tiles * k + 255) / 256 * ((groups + k - 1) / k);
+        if (cost < best) best = cost, ks = k;
+    }
     int sps = (nsteps + ks - 1) / ks;
     sps = (sps + 3) / 4 * 4;  // groups of four steps: splits start on one
     *splits = (nsteps + sps - 1) / sps;
