@@ -564,6 +564,27 @@ def test_prompt_row_blocks_nan_cache_and_replay(orc, head_dim):
     assert normwise_rel_err(b.cpu().numpy(), eager) <= 1e-5
 
 
+@pytest.mark.parametrize("ffn", [1056, 1024])
+def test_prompt_swiglu_partial_tile(orc, ffn):
+    # the fused gate/up + SiLU * up launch covers 128 output columns per tile: an FFN width that is
+    # not a multiple of 128 (1056: the last tile holds 32 columns) and one that is, against the oracle
+    m = make_model(2, dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=ffn, vocab=700, seed=95 + ffn,
+                   fmts={n: "fp16" for n in ("q", "k", "v", "o", "gate", "up", "down")}, tok="q8_0", lm="fp16",
+                   big_tables=False)
+    M, pos, max_seq = 80, 9, 256
+    dec = make_decoder(m, max_seq=max_seq, max_batch=M)
+    kc, vc = random_cache(m, max_seq, 96)
+    load_cache(dec, kc, vc)
+    ids = torch.from_numpy(np.random.default_rng(97).integers(0, m["vocab"], M).astype(np.int32)).cuda()
+    a = torch.empty(M, m["vocab"], device="cuda")
+    dec.set_position(pos)
+    dec.forward(ids, M, a)
+    ref, _ = orc.decode_step(m, list(ids.cpu().numpy()), pos, [k.copy() for k in kc], [v.copy() for v in vc])
+    err = normwise_rel_err(a.cpu().numpy(), ref)
+    print("prompt M=%d ffn=%d: normwise err %.2e" % (M, ffn, err))
+    assert err <= PREFILL_TOL
+
+
 def test_prompt_swiglu_flagged_rows(orc):
     # a prompt's stacked gate/up matrix runs as one launch with SiLU(gate) * up in its epilogue; rows
     # whose activations leave fp16's range (an FFN norm weight of 1e5 makes every row's reach ~1e5)

@@ -661,6 +661,12 @@ def test_matmul_ws_prefill_split(orc, fmt, M, N, K, splits):
     assert err <= PREFILL_TOL and err_atomic <= PREFILL_TOL
     # the two differ only in the order the partial sums are added (a few fp32 roundings)
     assert normwise_rel_err(outs[0], host(C)) <= 1e-5
+    # where the workspace is used, C must be 16-byte aligned and N a multiple of 4
+    wide = torch.empty(M, N + 4, device="cuda")
+    with pytest.raises(cri.CretifError):
+        cri.matmul_ws(fmt, dA, dB, wide.view(-1)[1:1 + M * N], M, N, K, ws)
+    with pytest.raises(cri.CretifError):  # too small
+        cri.matmul_ws(fmt, dA, dB, C, M, N, K, ws, need - 16)
 
 
 def test_matmul_ws_errors_and_other_row_counts(orc):
