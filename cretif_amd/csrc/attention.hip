@@ -534,21 +534,25 @@ __global__ __launch_bounds__(64 * kMrWaves) void decode_attn_mrow_kernel(
             o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(T.v1[s], p[s], o1, 0, 0, 0);
         }
     };
-    // the wave's tiles: the next one's loads are in flight while the current one is computed
+    // the wave's tiles: the next one's loads are in flight while the current one is computed.
+    // They end where the workgroup's last query row stops seeing positions: a prompt's early rows
+    // see few, and a tile no query sees would add exact zeros (a causal prompt's query groups
+    // skip about half the tiles of the chunk)
+    const int te = min(t1, Tb + min(nq - 1, qh * 32 + 31) / G);
     constexpr int kStep = kMrWaves * kSplitTile;
     int tb = t0 + w * kSplitTile;
-    if (tb < t1) {
+    if (tb < te) {
         Tile T0, T1;
         load_tile(T0, tb);
         while (true) {
-            if (tb + kStep >= t1) {
+            if (tb + kStep >= te) {
                 run_tile(T0, tb);
                 break;
             }
             load_tile(T1, tb + kStep);
             run_tile(T0, tb);
             tb += kStep;
-            if (tb + kStep >= t1) {
+            if (tb + kStep >= te) {
                 run_tile(T1, tb);
                 break;
             }
