@@ -179,10 +179,14 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
     // takes them: head_dim 64)
     prompt_mrow_ = MB > kFusedMaxBatch && cri::detail::decode_attention_rows_mrow(static_cast<int>(MB), c.head_dim);
     const int64_t arows = prompt_mrow_ ? MB : std::min<int64_t>(MB, kFusedMaxBatch);
-    const int ch1 = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, 1);
-    const int chm = cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len,
-                                                              static_cast<int>(arows));
-    attn_ws_ = Tensor::empty({arows * c.n_heads * std::max(ch1, chm) * (c.head_dim + 4)});
+    // the most records any batch size up to arows writes (its rows x heads x chunks; the chunk count
+    // falls as the rows grow)
+    int64_t recs = 0;
+    for (int64_t r = 1; r <= arows; ++r)
+        recs = std::max<int64_t>(recs, r * c.n_heads *
+                                           cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim,
+                                                                                     c.max_seq_len, static_cast<int>(r)));
+    attn_ws_ = Tensor::empty({recs * (c.head_dim + 4)});
     // partial sums of the decode-batch matmuls whose K is split over workgroups
     split_ws_ = Tensor::empty({cri::detail::skinny_workspace_floats(MB, c.dim)});
     // the q/k/v and gate/up projections' partial sums, left for RoPE and the down projection's
