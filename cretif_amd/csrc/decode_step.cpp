@@ -187,12 +187,15 @@ DecodeStep::DecodeStep(const DecodeStepConfig& c) : cfg_(c) {
                                            cri::detail::decode_attention_rows_chunks(c.n_heads, c.n_kv_heads, c.head_dim,
                                                                                      c.max_seq_len, static_cast<int>(r)));
     attn_ws_ = Tensor::empty({recs * (c.head_dim + 4)});
-    // partial sums of the decode-batch matmuls whose K is split over workgroups
-    split_ws_ = Tensor::empty({cri::detail::skinny_workspace_floats(MB, c.dim)});
-    // the q/k/v and gate/up projections' partial sums, left for RoPE and the down projection's
+    // partial sums of the decode-batch matmuls (up to kFusedMaxBatch rows) and of a prompt's
+    // prefill GEMMs whose K is split over workgroups
+    const int64_t brows = std::min<int64_t>(MB, kFusedMaxBatch);
+    split_ws_ = Tensor::empty({std::max<int64_t>(cri::detail::skinny_workspace_floats(static_cast<int>(brows), c.dim),
+                                                 MB > kFusedMaxBatch ? cri::detail::kPrefillSplitFloats : 0)});
+    // the decode batch's q/k/v and gate/up partial sums, left for RoPE and the down projection's
     // prologue to add up (a second workspace: the down projection splits into split_ws_ while
     // it reads these)
-    defer_ws_ = Tensor::empty({cri::detail::skinny_workspace_floats(MB, c.dim)});
+    defer_ws_ = Tensor::empty({cri::detail::skinny_workspace_floats(static_cast<int>(brows), c.dim)});
     // zeroed once; the argmax kernel that counts in them leaves them zero again
     argmax_part_ = Tensor::empty({MB * cri::detail::argmax_slices(c.vocab_size) * 2});
     argmax_count_ = Tensor::zeros({MB});
