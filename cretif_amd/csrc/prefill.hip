@@ -36,7 +36,10 @@
 //   * the eight m blocks that share a weight block are consecutive workgroups
 //     on one XCD (each XCD has its own L2), so the weights come from HBM once;
 //     when the tiles cannot fill 256 CUs the k range is split over workgroups
-//     that add into a zeroed C with fp32 atomics.
+//     that add into a zeroed C with fp32 atomics, or, given a workspace, store
+//     their partial sums there for a fixed-order reduction;
+//   * a stacked gate/up matrix can take a SiLU(gate) * up epilogue: a tile's
+//     128 output columns are 128 gate rows and the matching 128 up rows.
 // Activations outside fp16's comfortable range would lose the 1e-3 bound (a
 // value >= 65504 becomes inf; a row whose largest magnitude is below 2^-10
 // keeps only subnormal precision), so each thread tracks the largest
