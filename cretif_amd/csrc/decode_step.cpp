@@ -2,9 +2,10 @@
 //
 // The layer loop of TransformerModel::forward's quantized path
 // (ref:src/model.cu:831-1039) over buffers allocated once, with every
-// projection going through matmul_dispatch (or its fused-prologue forms for
-// batches of up to 16 tokens) and the position kept in device memory so that
-// one captured graph serves every following token.
+// projection going through matmul_dispatch (its fused-prologue forms for
+// batches of up to 16 tokens; for a prompt, K splits through the step's
+// workspace and a SiLU * up epilogue on the gate/up GEMM) and the position kept
+// in device memory so that one captured graph serves every following token.
 #include "../../include/cuinfer/decode_step.h"
 
 #include <hip/hip_runtime_api.h>
@@ -27,8 +28,9 @@ namespace {
 
 // Batches up to this many tokens take the fused RMSNorm / SwiGLU prologues.
 constexpr int kFusedMaxBatch = 16;
-// Larger batches (a prompt) run attention through batched_matmul_gqa in row blocks of
-// cri::detail::kPromptRows rows (the scores workspace holds n_heads x that x max_seq_len floats).
+// Larger batches (a prompt) run attention on the multi-row split kernel at head_dim 64, otherwise
+// through batched_matmul_gqa in row blocks of cri::detail::kPromptRows rows (the scores workspace
+// holds n_heads x that x max_seq_len floats).
 using cri::detail::kPromptRows;
 
 int round4(int n) { return (n + 3) / 4 * 4; }
