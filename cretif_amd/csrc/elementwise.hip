@@ -108,17 +108,7 @@ __global__ __launch_bounds__(256) void split_norm_kernel(const float* h, const S
         const int o = 4 * (threadIdx.x + 256 * j), i = c0 + o;
         if (o < cw) {
             v[j] = *reinterpret_cast<const f32x4*>(h + row * n + i);
-            if (r.S) {
-                const float* src = r.part + row * r.N + i;
-                f32x4 p[kSplitMaxS];
-#pragma unroll
-                for (int s = 0; s < kSplitMaxS; ++s) p[s] = *reinterpret_cast<const f32x4*>(src + min(s, r.S - 1) * r.stride);
-                f32x4 t = p[0];
-#pragma unroll
-                for (int s = 1; s < kSplitMaxS; ++s)
-                    if (s < r.S) t += p[s];
-                v[j] += t;
-            }
+            if (r.S) v[j] += split_sum4_any(r.part + row * r.N + i, r.stride, r.S);
             w[j] = *reinterpret_cast<const f32x4*>(weight + i);
         }
     }

@@ -40,5 +40,59 @@ __device__ __forceinline__ float split_sum(const SplitSums& p, long off) {
     return t;
 }
 
+// split_sum with the split count known at compile time (S <= kSplitMaxS): the same additions in
+// the same order, S loads instead of kSplitMaxS
+template <int S>
+__device__ __forceinline__ float split_sum_n(const SplitSums& p, long off) {
+    float v[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) v[s] = p.part[s * p.stride + off];
+    float t = v[0];
+#pragma unroll
+    for (int s = 1; s < S; ++s) t += v[s];
+    return t;
+}
+
+// the same for four consecutive elements (16-byte loads: part, stride and off multiples of 4)
+template <int S>
+__device__ __forceinline__ f32x4 split_sum4_n(const float* part, long stride) {
+    f32x4 v[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) v[s] = *reinterpret_cast<const f32x4*>(part + s * stride);
+    f32x4 t = v[0];
+#pragma unroll
+    for (int s = 1; s < S; ++s) t += v[s];
+    return t;
+}
+__device__ __forceinline__ f32x4 split_sum4_any(const float* part, long stride, int S) {
+    switch (S) {
+        case 1: return split_sum4_n<1>(part, stride);
+        case 2: return split_sum4_n<2>(part, stride);
+        case 4: return split_sum4_n<4>(part, stride);
+        case 8: return split_sum4_n<8>(part, stride);
+        default: {
+            f32x4 v[kSplitMaxS];
+#pragma unroll
+            for (int s = 0; s < kSplitMaxS; ++s) v[s] = *reinterpret_cast<const f32x4*>(part + min(s, S - 1) * stride);
+            f32x4 t = v[0];
+#pragma unroll
+            for (int s = 1; s < kSplitMaxS; ++s)
+                if (s < S) t += v[s];
+            return t;
+        }
+    }
+}
+
+// split_sum dispatched on the common split counts
+__device__ __forceinline__ float split_sum_any(const SplitSums& p, long off) {
+    switch (p.S) {
+        case 1: return split_sum_n<1>(p, off);
+        case 2: return split_sum_n<2>(p, off);
+        case 4: return split_sum_n<4>(p, off);
+        case 8: return split_sum_n<8>(p, off);
+        default: return split_sum(p, off);
+    }
+}
+
 }  // namespace dev
 }  // namespace cri

@@ -53,8 +53,8 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q,
         if (qkv.S) {
             const long e = static_cast<long>(m) * qkv.N + (isq ? 0 : kcol) + off;
             const float f = split_factor(qkv, m);
-            x0 = split_sum(qkv, e) * f;
-            x1 = split_sum(qkv, e + 1) * f;
+            x0 = split_sum_any(qkv, e) * f;
+            x1 = split_sum_any(qkv, e + 1) * f;
         } else {
             const float* src = isq ? q + m * ldq + off : k + m * ldk + off;
             x0 = src[0];
@@ -71,8 +71,8 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q,
         if (qkv.S) {
             const long o = static_cast<long>(m) * qkv.N + vcol + e;
             const float f = split_factor(qkv, m);
-            vrow[e] = split_sum(qkv, o) * f;
-            if (e + 1 < kvd) vrow[e + 1] = split_sum(qkv, o + 1) * f;
+            vrow[e] = split_sum_any(qkv, o) * f;
+            if (e + 1 < kvd) vrow[e + 1] = split_sum_any(qkv, o + 1) * f;
         } else {
             vrow[e] = v[m * ldv + e];
             if (e + 1 < kvd) vrow[e + 1] = v[m * ldv + e + 1];
