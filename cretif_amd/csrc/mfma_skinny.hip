@@ -731,20 +731,13 @@ __device__ __forceinline__ float sum_splits(const float* p) {
 // C = the S partial sums of a workspace K split added in split order, times the RMSNorm row
 // factor of all S sums of squares (split.hpp's steps, which the consumers that read the
 // partial sums directly repeat).  Four consecutive outputs per thread (N % 4 == 0, C 16-byte
-// aligned: the launcher checks); every load is unconditional (splits past S read split S - 1,
-// unused), so all of a thread's loads are in flight together.
+// aligned: the launcher checks); all of a thread's loads are in flight together (exactly S of
+// them for the common counts, sixteen clamped ones otherwise).
 __global__ __launch_bounds__(256) void split_reduce_kernel(const SplitSums p, float* __restrict__ C, int M) {
     const long i4 = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
     if (4 * i4 >= static_cast<long>(M) * p.N) return;
-    const float* src = p.part + 4 * i4;
-    f32x4 v[kSplitMaxS];
-#pragma unroll
-    for (int s = 0; s < kSplitMaxS; ++s) v[s] = *reinterpret_cast<const f32x4*>(src + min(s, p.S - 1) * p.stride);
+    const f32x4 t = split_sum4_any(p.part + 4 * i4, p.stride, p.S);
     const float fac = split_factor(p, static_cast<int>(4 * i4 / p.N));
-    f32x4 t = v[0];
-#pragma unroll
-    for (int s = 1; s < kSplitMaxS; ++s)
-        if (s < p.S) t += v[s];
     *reinterpret_cast<f32x4*>(C + 4 * i4) = t * fac;
 }
 
