@@ -430,6 +430,7 @@ constexpr int kMrWaves = 4;
 constexpr int kMrAld = kMrD + 4;  // LDS row stride of a wave's accumulators (floats)
 constexpr int kXcds = 8;
 
+template <bool PAIR>
 __global__ __launch_bounds__(64 * kMrWaves) void decode_attn_mrow_kernel(
     const float* __restrict__ Q, const float* __restrict__ Kc, const float* __restrict__ Vc, float* __restrict__ ws,
     int G, int n_kv, int M, const int* __restrict__ kv_dev, int kv0, float qscale, int nchunks, long ldq,
@@ -442,13 +443,20 @@ __global__ __launch_bounds__(64 * kMrWaves) void decode_attn_mrow_kernel(
     const int nq = M * G, nqh = (nq + 31) / 32;
     const int nb = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
     const int wi = nb % kXcds == 0 ? (b % kXcds) * (nb / kXcds) + b / kXcds : b;
-    const int qh = wi % nqh, c = (wi / nqh) % nchunks, kvh = wi / (nqh * nchunks);
+    // PAIR (one chunk, direct output): workgroup p of a KV head takes query groups nqh - 1 - p,
+    // then p -- a causal prompt's longest and shortest, so every workgroup does about the same
+    // number of tiles
+    const int npair = (nqh + 1) / 2;
+    const int qh_a = PAIR ? nqh - 1 - wi % npair : wi % nqh;
+    const int qh_b = PAIR && wi % npair != nqh - 1 - wi % npair ? wi % npair : -1;
+    const int c = PAIR ? 0 : (wi / nqh) % nchunks, kvh = PAIR ? wi / npair : wi / (nqh * nchunks);
     const int H = G * n_kv, kvd = n_kv * kMrD;
     const int Tb = (kv_dev ? *kv_dev : 0) + kv0;  // row m attends to positions [0, Tb + m)
     const int Tmax = Tb + M - 1;
     const int Tc = kSplitTile * ((((Tmax + kSplitTile - 1) / kSplitTile) + nchunks - 1) / nchunks);
     const int t0 = c * Tc, t1 = min(Tmax, t0 + Tc);
 
+    auto run_group = [&](const int qh) {
     // the lane's query (column i of S^T and O^T): row qm, head qg; positions below lim are visible
     const int q = qh * 32 + i;
     const bool qok = q < nq;
@@ -607,6 +615,14 @@ __global__ __launch_bounds__(64 * kMrWaves) void decode_attn_mrow_kernel(
     if (d0 == 0) {
         rec[0] = Mx;
         rec[1] = L;
+    }
+    };
+    run_group(qh_a);
+    if constexpr (PAIR) {
+        if (qh_b >= 0) {
+            __syncthreads();  // the first group's merge has read the LDS accumulators
+            run_group(qh_b);
+        }
     }
 }
 
@@ -799,9 +815,16 @@ int launch_decode_attention_rows(const float* Q, long ldq, const float* K, const
         if (wgs > 0x7FFFFFFFL) return kDeclined;
         // one chunk (a prompt's many query groups fill the GPU alone): the kernel writes the output
         const bool direct = nchunks == 1 && ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
-        hipLaunchKernelGGL(dev::decode_attn_mrow_kernel, dim3(static_cast<unsigned>(wgs)), dim3(64 * dev::kMrWaves), 0,
-                           stream, Q, K, V, ws, G, n_kv_heads, rows, kv_dev, kv0, qscale, nchunks, ldq,
-                           direct ? out : nullptr, ldo);
+        // one chunk: query groups in pairs, the longest with the shortest (half the workgroups)
+        const long pwgs = static_cast<long>(n_kv_heads) * ((nqh + 1) / 2);
+        if (direct)
+            hipLaunchKernelGGL(dev::decode_attn_mrow_kernel<true>, dim3(static_cast<unsigned>(pwgs)),
+                               dim3(64 * dev::kMrWaves), 0, stream, Q, K, V, ws, G, n_kv_heads, rows, kv_dev, kv0,
+                               qscale, nchunks, ldq, out, ldo);
+        else
+            hipLaunchKernelGGL(dev::decode_attn_mrow_kernel<false>, dim3(static_cast<unsigned>(wgs)),
+                               dim3(64 * dev::kMrWaves), 0, stream, Q, K, V, ws, G, n_kv_heads, rows, kv_dev, kv0,
+                               qscale, nchunks, ldq, nullptr, ldo);
         if (!direct) launch_combine(ws, out, n_heads, rows, D, nchunks, ldo, stream);
         return 0;
     }
